@@ -1,0 +1,158 @@
+/*
+ * k2t_hip.h -- C ABI of the MI355X (gfx950) kernels for kronos-2t's quantized
+ * decode hot path.
+ *
+ * The reference's per-projection "backend trait" is the LinearBackend enum and
+ * its stripe-range leaf kernels (src/model/real_llm.rs:525-544, 711-892;
+ * src/kernels/simd_lut.rs).  Each entry point below names the reference item
+ * it replaces.  A Rust host binds this header with a plain `extern "C"` block
+ * (see INTEGRATION.md); nothing here uses C++ or torch types.
+ *
+ * Conventions (mirroring include/kronos_ffi.h and src/ffi/mobile_ffi.rs:101-168):
+ *   - every function returns int32_t: 0 = ok, < 0 = error code (K2T_E_*);
+ *     k2t_last_error() returns a thread-local message for the last failure;
+ *   - no C++ exception crosses the ABI; HIP errors map to K2T_E_HIP;
+ *   - *_destroy(NULL) is a no-op;
+ *   - pointers named d_* are device pointers; everything else is host memory;
+ *   - calls are asynchronous on the context's stream (k2t_ctx_set_stream);
+ *     the caller synchronizes (k2t_ctx_sync) before reading results;
+ *   - a context owns scratch used by split-K GEMVs: use one context per
+ *     stream; two calls that overlap on one context race.
+ *
+ * Data layouts are the reference's, unchanged:
+ *   - bit-plane matrices: Nibble4SdotMatrix pair/tail streams
+ *     (simd_lut.rs:3264-3400): per stripe pair and 64-column chunk a record of
+ *     1024 + 256*hp + 64 bytes; odd last stripe in 512 + 128*hp + 32-byte records;
+ *   - NF matrices: NfSdotMatrix pair/tail streams (simd_lut.rs:4796-5023):
+ *     per pair and scale group 64 B of BF16 scales then sgc * 2 * 512 B (NF4);
+ *   - activations: Int8ChunkActivation (simd_lut.rs:2921-2937): int8 q[K],
+ *     f32 scales[K/64], i32 sums[K/64] per token, tokens back to back;
+ *   - int8 Hadamard KV cache: QuantizedKvCache (real_llm.rs:1209-1412):
+ *     slot = (layer*n_kv + kvh)*cap + pos, q8 at slot*hd, one f32 scale per slot.
+ */
+#ifndef K2T_HIP_H
+#define K2T_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define K2T_OK 0
+#define K2T_E_ARG (-1)     /* bad argument: NULL, shape, alignment, range */
+#define K2T_E_HIP (-2)     /* HIP runtime error */
+#define K2T_E_NOMEM (-3)   /* device allocation failed */
+#define K2T_E_STATE (-4)   /* wrong object state / unsupported format */
+#define K2T_E_INTERNAL (-5)
+
+typedef struct k2t_ctx k2t_ctx;
+typedef struct k2t_mat k2t_mat;
+
+/* Library version string ("k2t-hip <semver> gfx950"). */
+const char *k2t_version(void);
+
+/* Thread-local message of the last failing call on this thread
+ * (replaces kronos_last_error, mobile_ffi.rs:159-168). Never NULL. */
+const char *k2t_last_error(void);
+
+/* Number of visible HIP devices (0 when no GPU / no driver). Never fails. */
+int32_t k2t_device_count(void);
+
+/* ---- context ---------------------------------------------------------- */
+
+/* Creates a context on `device` (its own scratch, default stream 0).
+ * Replaces the per-engine SpinThreadPool + activation scratch
+ * (thread_pool.rs:96-175, real_llm.rs:3610-3653). */
+int32_t k2t_ctx_create(int32_t device, k2t_ctx **out);
+void k2t_ctx_destroy(k2t_ctx *ctx);
+/* Sets the hipStream_t (passed as void*) used by later calls; NULL = default stream. */
+int32_t k2t_ctx_set_stream(k2t_ctx *ctx, void *hip_stream);
+/* Blocks until all work queued on the context's stream is done. */
+int32_t k2t_ctx_sync(k2t_ctx *ctx);
+/* Split-K policy for k2t_gemv: 0 = automatic, 1 = never split (bit-exact fp32
+ * epilogue order of simd_lut.rs:4030-4059), n > 1 = at most n K-segments. */
+int32_t k2t_ctx_set_splitk(k2t_ctx *ctx, int32_t max_segments);
+
+/* ---- device memory helpers (tests, benches, non-torch callers) ---------- */
+int32_t k2t_malloc(k2t_ctx *ctx, size_t bytes, void **d_out);
+int32_t k2t_free(k2t_ctx *ctx, void *d_ptr);
+int32_t k2t_memcpy_h2d(k2t_ctx *ctx, void *d_dst, const void *src, size_t bytes);
+int32_t k2t_memcpy_d2h(k2t_ctx *ctx, void *dst, const void *d_src, size_t bytes);
+
+/* ---- matrices ----------------------------------------------------------- */
+
+/* Uploads a Nibble4SdotMatrix (simd_lut.rs:3264-3277) as produced by
+ * from_bipolar_with_perm (3297-3400): hi_planes = planes - 4 (0, 1 or 2).
+ * pair_len must equal (stripes/2)*(cols/64)*(1024+256*hi_planes+64) and
+ * tail_len (stripes&1)*(cols/64)*(512+128*hi_planes+32).  Bytes are copied. */
+int32_t k2t_mat_upload_nibble4(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t hi_planes,
+                               const uint8_t *pair, size_t pair_len, const uint8_t *tail,
+                               size_t tail_len, k2t_mat **out);
+
+/* Uploads an NfSdotMatrix (simd_lut.rs:4796-4842) with `bits` = 4 and
+ * scale_group_chunks = sgc (1..8).  Lengths follow pair_total_bytes /
+ * tail_total_bytes (simd_lut.rs:4834-4842).  codebook = the matrix's i8[16]. */
+int32_t k2t_mat_upload_nf(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t bits, int32_t sgc,
+                          const int8_t *codebook16, const uint8_t *pair, size_t pair_len,
+                          const uint8_t *tail, size_t tail_len, k2t_mat **out);
+
+/* Same as the uploads, but the streams already live in device memory; the
+ * matrix borrows them (caller keeps them alive; destroy does not free them). */
+int32_t k2t_mat_wrap_nibble4(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t hi_planes,
+                             const void *d_pair, size_t pair_len, const void *d_tail,
+                             size_t tail_len, k2t_mat **out);
+int32_t k2t_mat_wrap_nf(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t bits, int32_t sgc,
+                        const int8_t *codebook16, const void *d_pair, size_t pair_len,
+                        const void *d_tail, size_t tail_len, k2t_mat **out);
+void k2t_mat_destroy(k2t_mat *m);
+/* rows, cols, stripes and streamed bytes (pair + tail + codebook). */
+int32_t k2t_mat_info(const k2t_mat *m, int32_t *rows, int32_t *cols, int32_t *stripes,
+                     uint64_t *bytes);
+
+/* ---- activations --------------------------------------------------------- */
+
+/* Int8ChunkActivation::populate_fwht / populate_rmsnorm_fwht
+ * (simd_lut.rs:2954-3196): per token t and chunk c of d_x[t*K ..],
+ * optional (x*inv_rms[t])*w, signed FWHT-64 with the chunk's sign masks,
+ * int8 round-half-even, scale = max/127, i32 sum.  d_norm_w and d_inv_rms may
+ * both be NULL (plain FWHT); if d_norm_w is set, d_inv_rms must be too. */
+int32_t k2t_act_quant(k2t_ctx *ctx, const float *d_x, const float *d_norm_w,
+                      const float *d_inv_rms, int32_t K, int32_t ntok, int8_t *d_q,
+                      float *d_scales, int32_t *d_sums);
+
+/* RMSNorm + FWHT + int8 with inv_rms = 1/sqrt(mean(x^2) + eps) computed on the
+ * device (real_llm.rs:6929 + simd_lut.rs:2970).  The sum of squares is a tree
+ * reduction, so inv_rms may differ from the CPU's in the last ulp. */
+int32_t k2t_act_quant_rmsnorm(k2t_ctx *ctx, const float *d_x, const float *d_norm_w, float eps,
+                              int32_t K, int32_t ntok, int8_t *d_q, float *d_scales,
+                              int32_t *d_sums);
+
+/* ---- GEMV / multi-token tile -------------------------------------------- */
+
+/* nibble4_sdot_stripe_range_raw (simd_lut.rs:3536-3582) and
+ * nf_sdot_stripe_range_raw (5687-5713) for stripes [s0, s1) (s1 = -1: all),
+ * and for ntok > 1 their batch variants nibble4_sdot_batch_stripe_range /
+ * nf_sdot_batch_stripe_range (4101, 6689): token t reads d_xq + t*K,
+ * d_xs + t*K/64, d_xsum + t*K/64 and writes d_out[t*out_stride + row].
+ * Weights are read once per 4 tokens.  d_xsum is required for bit-plane
+ * matrices and ignored for NF ones.  Per-(row, chunk) integer dots are exact;
+ * with split-K disabled the fp32 result is bit-identical to the reference's
+ * in-order fmaf epilogue. */
+int32_t k2t_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq, const float *d_xs,
+                 const int32_t *d_xsum, int32_t ntok, int32_t s0, int32_t s1, float *d_out,
+                 size_t out_stride);
+
+/* Debug/parity: writes the exact integer dot of every (row, chunk) for one
+ * token into d_dots[row * (K/64) + chunk] (Σ q·xq for bit-plane, Σ cb[idx]·xq
+ * for NF).  No reference counterpart (the NEON kernel keeps them in registers,
+ * simd_lut.rs:4030-4059); used to prove bit-exact integer accumulation. */
+int32_t k2t_gemv_chunk_dots(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq,
+                            const int32_t *d_xsum, int32_t *d_dots);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* K2T_HIP_H */

@@ -1,0 +1,84 @@
+// Activation rotation + int8 chunk quantization for gfx950.
+//
+// Replaces Int8ChunkActivation::populate_fwht / populate_rmsnorm_fwht /
+// populate_chunk_fwht_raw (simd_lut.rs:2954-3196).  One wavefront per 64-column chunk,
+// lane i holds element i: optional (x*inv_rms)*w, sign flip with the chunk's SplitMix64
+// mask, x0.125, six butterfly stages through lane exchanges in the reference's order,
+// wave max, 127/max, round-half-even, wave sum.  Every float operation is the
+// reference's, so q / scales / sums are bit-identical given the same inputs.
+#include <float.h>
+
+#include "k2t_device.h"
+#include "k2t_internal.h"
+
+namespace k2t {
+
+__global__ __launch_bounds__(256) void act_quant_kernel(const float *__restrict__ x,
+                                                        const float *__restrict__ w,
+                                                        const float *__restrict__ inv_rms, int K,
+                                                        int total_chunks, int8_t *__restrict__ q,
+                                                        float *__restrict__ scales,
+                                                        int32_t *__restrict__ sums) {
+    const uint32_t lane = threadIdx.x & 63;
+    const int gc = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (gc >= total_chunks) return;
+    const int nc = K / 64;
+    const int tok = gc / nc, c = gc - tok * nc;
+    float v = x[(size_t)gc * 64 + lane];
+    if (w) v = (v * inv_rms[tok]) * w[(size_t)c * 64 + lane];
+    v = flip_sign(v, hadamard_sign_bit((uint64_t)c, lane)) * 0.125f;
+    v = wave_butterflies64(v, lane);
+    const float mx = wave_max_f(fabsf(v));
+    if (mx <= FLT_EPSILON) {
+        q[(size_t)gc * 64 + lane] = 0;
+        if (lane == 0) {
+            scales[gc] = 0.0f;
+            sums[gc] = 0;
+        }
+        return;
+    }
+    const float inv = 127.0f / mx;
+    const int qi = (int)rintf(v * inv);
+    const int s = wave_sum_i(qi);
+    q[(size_t)gc * 64 + lane] = (int8_t)qi;
+    if (lane == 0) {
+        scales[gc] = mx / 127.0f;
+        sums[gc] = s;
+    }
+}
+
+// inv_rms[t] = 1 / sqrt(sum(x^2)/K + eps) per token (real_llm.rs:6929), one block per token.
+__global__ __launch_bounds__(256) void inv_rms_kernel(const float *__restrict__ x, float eps, int K,
+                                                      float *__restrict__ out) {
+    __shared__ float part[4];
+    const float *xt = x + (size_t)blockIdx.x * K;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < K; i += 256) {
+        const float v = xt[i];
+        s = fmaf(v, v, s);
+    }
+    s = wave_sum_f(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+        out[blockIdx.x] = 1.0f / sqrtf(tot / (float)K + eps);
+    }
+}
+
+void launch_act_quant(k2t_ctx *ctx, const float *x, const float *w, const float *inv_rms, int K,
+                      int ntok, int8_t *q, float *scales, int32_t *sums) {
+    const int total = (K / 64) * ntok;
+    if (total <= 0) return;
+    hipLaunchKernelGGL(act_quant_kernel, dim3((total + 3) / 4), dim3(256), 0, ctx->stream, x, w,
+                       inv_rms, K, total, q, scales, sums);
+    hip_check(hipGetLastError(), "act_quant launch");
+}
+
+void launch_inv_rms(k2t_ctx *ctx, const float *x, float eps, int K, int ntok, float *inv_rms) {
+    if (ntok <= 0) return;
+    hipLaunchKernelGGL(inv_rms_kernel, dim3(ntok), dim3(256), 0, ctx->stream, x, eps, K, inv_rms);
+    hip_check(hipGetLastError(), "inv_rms launch");
+}
+
+}  // namespace k2t

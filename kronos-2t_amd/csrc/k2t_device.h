@@ -1,0 +1,80 @@
+// Device helpers shared by the gfx950 kernels: Hadamard sign masks, wave-level
+// butterflies and reductions (DPP), BF16 decode and byte-table lookups.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace k2t {
+
+constexpr int kWave = 64;
+
+// Sign of element `i` of Hadamard block `block` (hadamard.rs:29-44): SplitMix64 state
+// seed + block*0xBF58.. advanced i+1 times, finalized, low bit.  Each lane computes its
+// own element, so no table is needed.
+__device__ __forceinline__ uint32_t hadamard_sign_bit(uint64_t block, uint32_t i) {
+    uint64_t z = 0x9E3779B97F4A7C15ull + block * 0xBF58476D1CE4E5B9ull +
+                 (uint64_t)(i + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (uint32_t)(z & 1);
+}
+
+// DPP lane moves inside one 16-lane row.
+__device__ __forceinline__ int dpp_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int dpp_ror8(int v) { return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false); }
+__device__ __forceinline__ int dpp_ror4(int v) { return __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false); }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
+
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+
+// In-register signed FWHT-64 over one wave (lane i holds element i): butterflies with
+// stride h = 1..32 exactly as hadamard.rs:83-97 (lower lane a+b, upper lane a-b).
+__device__ __forceinline__ float wave_butterflies64(float v, uint32_t lane) {
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+        float p = __shfl_xor(v, h, kWave);
+        v = (lane & h) ? (p - v) : (v + p);
+    }
+    return v;
+}
+
+__device__ __forceinline__ float flip_sign(float v, uint32_t neg) {
+    return __uint_as_float(__float_as_uint(v) ^ (neg << 31));
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// 16-entry signed-byte table lookup of four 4-bit indices, one per byte.
+// `s` holds the low 3 bits of each index, `m` is 0xFF in bytes whose index has bit 3.
+// cb0..cb3 = table bytes 0-3, 4-7, 8-11, 12-15.
+__device__ __forceinline__ uint32_t lut16(uint32_t s, uint32_t m, uint32_t cb0, uint32_t cb1,
+                                          uint32_t cb2, uint32_t cb3) {
+    uint32_t lo = __builtin_amdgcn_perm(cb1, cb0, s);
+    uint32_t hi = __builtin_amdgcn_perm(cb3, cb2, s);
+    return (hi & m) | (lo & ~m);
+}
+
+// Byte mask 0xFF where bit 7 of the byte is set (v_perm selectors >= 13 give 0xFF,
+// selector 0 picks byte 0 of the zero pool).
+__device__ __forceinline__ uint32_t bit7_mask(uint32_t v) {
+    return __builtin_amdgcn_perm(0u, 0u, v & 0x80808080u);
+}
+
+}  // namespace k2t

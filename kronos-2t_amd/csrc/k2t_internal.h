@@ -1,0 +1,65 @@
+// Host-side objects behind the C ABI (include/k2t_hip.h) and the kernel launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+
+struct k2t_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int max_segments = 0;  // split-K policy: 0 auto, 1 off, n cap
+    int num_cus = 256;
+    // split-K scratch: fp32 partial rows + per-row-block arrival counters.
+    float *partial = nullptr;
+    size_t partial_cap = 0;  // floats
+    uint32_t *counters = nullptr;
+    size_t counter_cap = 0;  // entries, always left at zero between calls
+    float *rms_scratch = nullptr;
+    size_t rms_cap = 0;
+};
+
+enum k2t_fmt : int32_t { K2T_FMT_NIBBLE4 = 1, K2T_FMT_NF = 2 };
+
+struct k2t_mat {
+    k2t_ctx *ctx = nullptr;
+    int device = 0;
+    int32_t fmt = 0;
+    int32_t rows = 0, cols = 0;
+    int32_t nc = 0, stripes = 0, pairs = 0, has_tail = 0;
+    int32_t hp = 0;           // bit-plane: hi planes (0..2)
+    int32_t bits = 0, sgc = 1;  // NF
+    uint32_t cb[4] = {0, 0, 0, 0};  // NF codebook bytes 0-15
+    const uint8_t *pair = nullptr, *tail = nullptr;
+    size_t pair_len = 0, tail_len = 0;
+    bool owns = false;
+};
+
+namespace k2t {
+
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+void hip_check(hipError_t e, const char *what);
+
+// Grows the context's split-K scratch (synchronous allocation; counters zeroed).
+void ensure_scratch(k2t_ctx *ctx, size_t partial_floats, size_t counters);
+
+struct GemvPlan {
+    int rb_lo, rb_hi;  // row-block range (pairs, then the tail stripe)
+    int nseg, cps;     // K segments and chunks per segment
+};
+GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1);
+
+void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
+                 const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
+                 int32_t *dots);
+
+void launch_act_quant(k2t_ctx *ctx, const float *x, const float *w, const float *inv_rms, int K,
+                      int ntok, int8_t *q, float *scales, int32_t *sums);
+void launch_inv_rms(k2t_ctx *ctx, const float *x, float eps, int K, int ntok, float *inv_rms);
+
+}  // namespace k2t

@@ -1,0 +1,200 @@
+"""Python binding of the C ABI in include/k2t_hip.h (libk2t_hip.so, built in-tree).
+
+This is the host-side mirror used by tests and bench.py: a thin ctypes layer with
+the same entry points, argument meaning and error behaviour as the C ABI (each
+negative status raises K2TError carrying k2t_last_error()).  Device buffers are
+torch tensors on the ROCm device -- torch is only plumbing for memory and
+streams here; every kernel that runs is in libk2t_hip.so.
+
+Loading fails loudly when the shared library is missing: there is no CPU
+fallback in the product path.
+"""
+import atexit
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libk2t_hip.so")
+_lib = None
+_shutting_down = False
+
+
+def _mark_shutdown():
+    global _shutting_down
+    _shutting_down = True
+
+
+atexit.register(_mark_shutdown)
+
+VP = C.c_void_p
+I32 = C.c_int32
+SZ = C.c_size_t
+
+
+class K2TError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"k2t error {code}: {msg}")
+        self.code = code
+
+
+# Every exported symbol of include/k2t_hip.h with (restype, argtypes).
+SIGNATURES = {
+    "k2t_version": (C.c_char_p, []),
+    "k2t_last_error": (C.c_char_p, []),
+    "k2t_device_count": (I32, []),
+    "k2t_ctx_create": (I32, [I32, C.POINTER(VP)]),
+    "k2t_ctx_destroy": (None, [VP]),
+    "k2t_ctx_set_stream": (I32, [VP, VP]),
+    "k2t_ctx_sync": (I32, [VP]),
+    "k2t_ctx_set_splitk": (I32, [VP, I32]),
+    "k2t_malloc": (I32, [VP, SZ, C.POINTER(VP)]),
+    "k2t_free": (I32, [VP, VP]),
+    "k2t_memcpy_h2d": (I32, [VP, VP, VP, SZ]),
+    "k2t_memcpy_d2h": (I32, [VP, VP, VP, SZ]),
+    "k2t_mat_upload_nibble4": (I32, [VP, I32, I32, I32, VP, SZ, VP, SZ, C.POINTER(VP)]),
+    "k2t_mat_upload_nf": (I32, [VP, I32, I32, I32, I32, VP, VP, SZ, VP, SZ, C.POINTER(VP)]),
+    "k2t_mat_wrap_nibble4": (I32, [VP, I32, I32, I32, VP, SZ, VP, SZ, C.POINTER(VP)]),
+    "k2t_mat_wrap_nf": (I32, [VP, I32, I32, I32, I32, VP, VP, SZ, VP, SZ, C.POINTER(VP)]),
+    "k2t_mat_destroy": (None, [VP]),
+    "k2t_mat_info": (I32, [VP, C.POINTER(I32), C.POINTER(I32), C.POINTER(I32), C.POINTER(C.c_uint64)]),
+    "k2t_act_quant": (I32, [VP, VP, VP, VP, I32, I32, VP, VP, VP]),
+    "k2t_act_quant_rmsnorm": (I32, [VP, VP, VP, C.c_float, I32, I32, VP, VP, VP]),
+    "k2t_gemv": (I32, [VP, VP, VP, VP, VP, I32, I32, I32, VP, SZ]),
+    "k2t_gemv_chunk_dots": (I32, [VP, VP, VP, VP, VP]),
+}
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() (no CPU fallback exists)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        raise K2TError(rc, lib().k2t_last_error().decode())
+    return rc
+
+
+def _p(t):
+    """Device pointer of a torch tensor (or None / int passthrough)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _host(a):
+    import numpy as np
+    a = np.ascontiguousarray(a)
+    return a.ctypes.data_as(VP) if a.size else None, a
+
+
+class Ctx:
+    """k2t_ctx: one per device stream."""
+
+    def __init__(self, device=0, stream=None):
+        h = VP()
+        check(lib().k2t_ctx_create(device, C.byref(h)))
+        self.h = h
+        self.device = device
+        if stream is not None:
+            self.set_stream(stream)
+
+    def set_stream(self, stream):
+        check(lib().k2t_ctx_set_stream(self.h, VP(stream.cuda_stream if hasattr(stream, "cuda_stream") else stream)))
+
+    def set_splitk(self, n):
+        check(lib().k2t_ctx_set_splitk(self.h, int(n)))
+
+    def sync(self):
+        check(lib().k2t_ctx_sync(self.h))
+
+    def close(self):
+        if self.h and not _shutting_down:
+            lib().k2t_ctx_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- matrices
+    def upload_nibble4(self, rows, cols, hi_planes, pair, tail):
+        pp, pa = _host(pair)
+        tp, ta = _host(tail)
+        h = VP()
+        check(lib().k2t_mat_upload_nibble4(self.h, rows, cols, hi_planes, pp, pa.nbytes, tp, ta.nbytes, C.byref(h)))
+        return Mat(self, h, rows, cols)
+
+    def upload_nf(self, rows, cols, bits, sgc, codebook, pair, tail):
+        cp, ca = _host(codebook)
+        pp, pa = _host(pair)
+        tp, ta = _host(tail)
+        h = VP()
+        check(lib().k2t_mat_upload_nf(self.h, rows, cols, bits, sgc, cp, pp, pa.nbytes, tp, ta.nbytes, C.byref(h)))
+        return Mat(self, h, rows, cols)
+
+    def wrap_nibble4(self, rows, cols, hi_planes, d_pair, pair_len, d_tail, tail_len):
+        h = VP()
+        check(lib().k2t_mat_wrap_nibble4(self.h, rows, cols, hi_planes, _p(d_pair), pair_len, _p(d_tail),
+                                         tail_len, C.byref(h)))
+        return Mat(self, h, rows, cols, keep=(d_pair, d_tail))
+
+    def wrap_nf(self, rows, cols, bits, sgc, codebook, d_pair, pair_len, d_tail, tail_len):
+        cp, ca = _host(codebook)
+        h = VP()
+        check(lib().k2t_mat_wrap_nf(self.h, rows, cols, bits, sgc, cp, _p(d_pair), pair_len, _p(d_tail),
+                                    tail_len, C.byref(h)))
+        return Mat(self, h, rows, cols, keep=(d_pair, d_tail))
+
+    # -- activations
+    def act_quant(self, x, q, scales, sums, K, ntok, norm_w=None, inv_rms=None):
+        check(lib().k2t_act_quant(self.h, _p(x), _p(norm_w), _p(inv_rms), K, ntok, _p(q), _p(scales), _p(sums)))
+
+    def act_quant_rmsnorm(self, x, norm_w, eps, q, scales, sums, K, ntok):
+        check(lib().k2t_act_quant_rmsnorm(self.h, _p(x), _p(norm_w), float(eps), K, ntok, _p(q), _p(scales),
+                                          _p(sums)))
+
+    # -- GEMV
+    def gemv(self, m, xq, xs, xsum, out, ntok=1, s0=0, s1=-1, out_stride=0):
+        check(lib().k2t_gemv(self.h, m.h, _p(xq), _p(xs), _p(xsum), ntok, s0, s1, _p(out), out_stride))
+
+    def gemv_chunk_dots(self, m, xq, xsum, dots):
+        check(lib().k2t_gemv_chunk_dots(self.h, m.h, _p(xq), _p(xsum), _p(dots)))
+
+
+class Mat:
+    def __init__(self, ctx, h, rows, cols, keep=None):
+        self.ctx = ctx
+        self.h = h
+        self.rows = rows
+        self.cols = cols
+        self._keep = keep
+
+    def info(self):
+        r, c, s, b = I32(), I32(), I32(), C.c_uint64()
+        check(lib().k2t_mat_info(self.h, C.byref(r), C.byref(c), C.byref(s), C.byref(b)))
+        return r.value, c.value, s.value, b.value
+
+    def close(self):
+        if self.h and not _shutting_down:
+            lib().k2t_mat_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
