@@ -151,6 +151,36 @@ int32_t k2t_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq, const float
 int32_t k2t_gemv_chunk_dots(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq,
                             const int32_t *d_xsum, int32_t *d_dots);
 
+/* ---- offline weight compiler (host memory, multi-threaded) ------------- */
+
+/* Byte lengths of the pair / tail streams: fmt 1 = bit planes (planes 4..6),
+ * fmt 2 = NF (bits 4, sgc 1..8).  Nibble4SdotMatrix::pair_rec_bytes /
+ * NfSdotMatrix::pair_total_bytes (simd_lut.rs:3281-3288, 4834-4842). */
+int32_t k2t_stream_sizes(int32_t fmt, int32_t rows, int32_t cols, int32_t planes_or_bits, int32_t sgc,
+                         size_t *pair_len, size_t *tail_len);
+
+/* compile_hadamard_gptq_bipolar without a Hessian (compiler.rs:912-1107: per-row
+ * FWHT-64, 12-ratio RTN search, BF16 scale per row and chunk) followed by
+ * Nibble4SdotMatrix::from_bipolar_with_perm (simd_lut.rs:3297-3400), written
+ * directly into the caller's pair/tail buffers.  W is row-major [rows][cols] f32.
+ * threads <= 0 uses every hardware thread. */
+int32_t k2t_compile_bipolar(const float *W, int32_t rows, int32_t cols, int32_t planes,
+                            int32_t interleave_gate_up, int32_t threads, uint8_t *pair, size_t pair_len,
+                            uint8_t *tail, size_t tail_len);
+
+/* compile_hadamard_gptq_nf without a Hessian for NF4 (compiler.rs:1404-1866:
+ * fitted Lloyd-Max codebook, 11-ratio RTN + least-squares BF16 refit) followed by
+ * NfSdotMatrix::from_indices (simd_lut.rs:4850-5023) and, if requested,
+ * to_gate_up_interleaved (5500-5523).  Writes the codebook and mu_top (nullable). */
+int32_t k2t_compile_nf(const float *W, int32_t rows, int32_t cols, int32_t bits, int32_t sgc,
+                       int32_t interleave_gate_up, int32_t threads, int8_t *codebook16, float *mu_top,
+                       uint8_t *pair, size_t pair_len, uint8_t *tail, size_t tail_len);
+
+/* Seeded N(0, std) samples (SplitMix64 counter + Box-Muller) for synthetic
+ * random-init weights; deterministic for a given (seed, n) at any thread count.
+ * No reference counterpart (the reference loads checkpoints). */
+int32_t k2t_synth_normal(uint64_t seed, float stddev, float *out, size_t n, int32_t threads);
+
 #ifdef __cplusplus
 }
 #endif

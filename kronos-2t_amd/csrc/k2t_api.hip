@@ -51,27 +51,17 @@ static void device_alloc(void **p, size_t bytes) {
     }
 }
 
-void ensure_scratch(k2t_ctx *ctx, size_t partial_floats, size_t counters) {
+void ensure_scratch(k2t_ctx *ctx, size_t floats) {
     hip_check(hipSetDevice(ctx->device), "hipSetDevice");
-    if (partial_floats > ctx->partial_cap) {
-        // Queued kernels may still read the old buffer.
-        hip_check(hipStreamSynchronize(ctx->stream), "scratch sync");
-        if (ctx->partial) hip_check(hipFree(ctx->partial), "hipFree");
-        ctx->partial = nullptr;
-        size_t cap = std::max(partial_floats, (size_t)1 << 20);
-        device_alloc((void **)&ctx->partial, cap * sizeof(float));
-        ctx->partial_cap = cap;
-    }
-    if (counters > ctx->counter_cap) {
-        hip_check(hipStreamSynchronize(ctx->stream), "scratch sync");
-        if (ctx->counters) hip_check(hipFree(ctx->counters), "hipFree");
-        ctx->counters = nullptr;
-        size_t cap = std::max(counters, (size_t)4096);
-        device_alloc((void **)&ctx->counters, cap * sizeof(uint32_t));
-        // Kernels return every counter to zero after use; this is the only clear.
-        hip_check(hipMemset(ctx->counters, 0, cap * sizeof(uint32_t)), "hipMemset");
-        ctx->counter_cap = cap;
-    }
+    if (floats <= ctx->scratch_cap) return;
+    // Queued kernels may still use the old buffer.
+    hip_check(hipStreamSynchronize(ctx->stream), "scratch sync");
+    if (ctx->scratch) hip_check(hipFree(ctx->scratch), "hipFree");
+    ctx->scratch = nullptr;
+    ctx->scratch_cap = 0;
+    const size_t cap = std::max(floats, (size_t)1 << 16);
+    device_alloc((void **)&ctx->scratch, cap * sizeof(float));
+    ctx->scratch_cap = cap;
 }
 
 static size_t nibble4_pair_len(int rows, int cols, int hp) {
@@ -232,8 +222,7 @@ void k2t_ctx_destroy(k2t_ctx *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->partial) (void)hipFree(ctx->partial);
-    if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->rms_scratch) (void)hipFree(ctx->rms_scratch);
     delete ctx;
 }
@@ -419,12 +408,12 @@ int32_t k2t_gemv_chunk_dots(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq, 
         // The scales are irrelevant to the integer dots; a scratch row of ones keeps the
         // fp32 epilogue well defined.  The float output goes to the split-K scratch.
         const size_t nc = (size_t)m->nc;
-        ensure_scratch(ctx, nc + (size_t)m->stripes * 16, 1);
-        float *ones = ctx->partial;
+        ensure_scratch(ctx, nc + (size_t)m->stripes * 16);
+        float *ones = ctx->scratch;
         std::vector<float> h(nc, 1.0f);
         hip_check(hipMemcpyAsync(ones, h.data(), nc * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
                   "h2d");
-        launch_gemv(ctx, m, d_xq, ones, d_xsum, 1, 0, m->stripes, ctx->partial + nc, (size_t)m->rows, d_dots);
+        launch_gemv(ctx, m, d_xq, ones, d_xsum, 1, 0, m->stripes, ctx->scratch + nc, (size_t)m->rows, d_dots);
         hip_check(hipStreamSynchronize(ctx->stream), "sync");
     });
 }

@@ -1,0 +1,489 @@
+// Offline weight compiler (host, multi-threaded): Hadamard RTN quantization straight
+// into the device layouts.
+//
+//   bit planes : compile_hadamard_gptq_bipolar with no Hessian (compiler.rs:912-1107),
+//                then the Nibble4SdotMatrix layout of from_bipolar_with_perm
+//                (simd_lut.rs:3297-3400), optionally gate_up-interleaved;
+//   NF4        : fit_empirical_nf_codebook (compiler.rs:1404-1526), RTN + least-squares
+//                BF16 refit (compiler.rs:1628-1866), NfSdotMatrix::from_indices
+//                (simd_lut.rs:4850-5023) and to_gate_up_interleaved (5500-5523).
+//
+// Work is split over destination stripes; each worker quantizes the 16 source rows of
+// its stripe and writes its disjoint records, so the bytes equal the reference's
+// two-step (quantize, then pack/repack) output.  Every float expression keeps the
+// reference's operation order (the file is built with fp contraction off).
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cfloat>
+#include <cstdint>
+#include <thread>
+#include <vector>
+
+#include "../../include/k2t_hip.h"
+#include "k2t_internal.h"
+
+namespace k2t {
+namespace host {
+
+static uint64_t sign_bits(uint64_t block) {
+    uint64_t st = 0x9E3779B97F4A7C15ULL + block * 0xBF58476D1CE4E5B9ULL, bits = 0;
+    for (int i = 0; i < 64; i++) {
+        st += 0x9E3779B97F4A7C15ULL;
+        uint64_t z = st;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+        z ^= z >> 31;
+        bits |= (z & 1ULL) << i;
+    }
+    return bits;
+}
+
+struct SignTable {
+    std::vector<uint64_t> m;
+    explicit SignTable(size_t blocks) : m(blocks) {
+        for (size_t b = 0; b < blocks; b++) m[b] = sign_bits(b);
+    }
+};
+
+// hadamard.rs:70-99 on a full row (block index = chunk index).
+static void fwht_row(float *x, size_t n, const SignTable &st) {
+    for (size_t b = 0; b < n / 64; b++) {
+        float *v = x + 64 * b;
+        const uint64_t m = st.m[b];
+        for (int i = 0; i < 64; i++) {
+            uint32_t u;
+            memcpy(&u, &v[i], 4);
+            u ^= (uint32_t)((m >> i) & 1ULL) << 31;
+            float f;
+            memcpy(&f, &u, 4);
+            v[i] = f * 0.125f;
+        }
+        for (int h = 1; h < 64; h <<= 1)
+            for (int i = 0; i < 64; i += 2 * h)
+                for (int j = i; j < i + h; j++) {
+                    const float a = v[j], c = v[j + h];
+                    v[j] = a + c;
+                    v[j + h] = a - c;
+                }
+    }
+}
+
+static uint16_t to_bf16(float v) {
+    uint32_t bits;
+    memcpy(&bits, &v, 4);
+    if ((bits & 0x7F800000u) == 0x7F800000u && (bits & 0x007FFFFFu)) return (uint16_t)((bits >> 16) | 0x40u);
+    return (uint16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+}
+static float from_bf16(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+template <typename F>
+static void parallel_for(size_t n, int threads, F &&fn) {
+    if (threads <= 0) threads = (int)std::max(1u, std::thread::hardware_concurrency());
+    threads = (int)std::min<size_t>((size_t)threads, std::max<size_t>(n, 1));
+    if (threads <= 1) {
+        for (size_t i = 0; i < n; i++) fn(i);
+        return;
+    }
+    std::vector<std::thread> pool;
+    const size_t per = (n + threads - 1) / threads;
+    for (int t = 0; t < threads; t++) {
+        const size_t b = t * per, e = std::min(n, b + per);
+        if (b >= e) break;
+        pool.emplace_back([&, b, e] {
+            for (size_t i = b; i < e; i++) fn(i);
+        });
+    }
+    for (auto &th : pool) th.join();
+}
+
+// Source row of destination row `r` under the [gate64(ic), up64(ic)] interleave.
+static size_t source_row(size_t r, size_t rows, bool interleave) {
+    if (!interleave) return r;
+    const size_t blk = r / 64, off = r % 64, inter_dim = rows / 2;
+    return (blk / 2) * 64 + off + ((blk & 1) ? inter_dim : 0);
+}
+
+// ---------------------------------------------------------------- bit planes
+
+// compiler.rs:1038-1084 for one 64-column chunk: returns the BF16 scale, writes u codes.
+static uint16_t bipolar_chunk(const float *sub, int planes, uint8_t *u) {
+    static const float ratios[12] = {0.62f, 0.67f, 0.72f, 0.77f, 0.82f, 0.87f,
+                                     0.92f, 0.97f, 1.02f, 1.07f, 1.12f, 1.18f};
+    const int max_odd = (1 << planes) - 1;
+    const float max_u_f = (float)max_odd, half_off = 0.5f * max_u_f;
+    float max_abs = 0.0f;
+    for (int i = 0; i < 64; i++) max_abs = fmaxf(max_abs, fabsf(sub[i]));
+    memset(u, 0, 64);
+    if (max_abs <= 1e-12f) return 0;
+    float best_loss = INFINITY;
+    uint16_t best = 0;
+    uint8_t cand[64];
+    for (int k = 0; k < 12; k++) {
+        const uint16_t d = to_bf16((max_abs * ratios[k]) / max_u_f);
+        const float delta = from_bf16(d);
+        if (delta <= 0.0f) continue;
+        const float inv2 = 0.5f / delta;
+        float loss = 0.0f;
+        for (int j = 0; j < 64; j++) {
+            const float wj = sub[j];
+            float t = roundf(wj * inv2 + half_off);
+            t = t < 0.0f ? 0.0f : (t > max_u_f ? max_u_f : t);
+            const int ui = (int)t;
+            cand[j] = (uint8_t)ui;
+            const float diff = wj - (float)(2 * ui - max_odd) * delta;
+            loss += diff * diff;
+        }
+        if (loss < best_loss) {
+            best_loss = loss;
+            best = d;
+            memcpy(u, cand, 64);
+        }
+    }
+    return best;
+}
+
+static void compile_bipolar(const float *W, size_t rows, size_t cols, int planes, bool interleave,
+                            int threads, uint8_t *pair, uint8_t *tail) {
+    const int hp = planes - 4;
+    const size_t nc = cols / 64, stripes = (rows + 15) / 16, np = stripes / 2;
+    const size_t prec = 1024 + 256 * (size_t)hp + 64, trec = 512 + 128 * (size_t)hp + 32;
+    SignTable st(nc);
+    memset(pair, 0, np * nc * prec);
+    if (stripes & 1) memset(tail, 0, nc * trec);
+    parallel_for(stripes, threads, [&](size_t s) {
+        std::vector<float> row(cols);
+        std::vector<uint8_t> codes(cols);
+        const bool in_pair = s < np * 2;
+        const size_t p = s / 2, side = s & 1;
+        for (size_t lane = 0; lane < 16; lane++) {
+            const size_t r = s * 16 + lane;
+            if (r >= rows) break;
+            memcpy(row.data(), W + source_row(r, rows, interleave) * cols, cols * sizeof(float));
+            fwht_row(row.data(), cols, st);
+            const size_t g = lane / 4, j = lane % 4;
+            for (size_t c = 0; c < nc; c++) {
+                const uint16_t sc = bipolar_chunk(row.data() + c * 64, planes, codes.data() + c * 64);
+                uint8_t *rec;
+                size_t doff, hoff, soff;
+                if (in_pair) {
+                    rec = pair + (p * nc + c) * prec;
+                    doff = side * 512;
+                    hoff = 1024 + side * 128 * hp;
+                    soff = 1024 + 256 * hp + side * 32;
+                } else {
+                    rec = tail + c * trec;
+                    doff = 0;
+                    hoff = 512;
+                    soff = 512 + 128 * hp;
+                }
+                rec[soff + lane * 2] = (uint8_t)sc;
+                rec[soff + lane * 2 + 1] = (uint8_t)(sc >> 8);
+                for (size_t k = 0; k < 4; k++)
+                    for (size_t w = 0; w < 16; w++) {
+                        const uint8_t uv = codes[c * 64 + k * 16 + w];
+                        const size_t half = w / 8, sub = w / 4, t = w % 4;
+                        const uint8_t lo = uv & 0x0F;
+                        rec[doff + k * 128 + g * 32 + half * 16 + j * 4 + t] |= (w % 8) < 4 ? lo : (uint8_t)(lo << 4);
+                        if (hp == 1) {
+                            const int bit = (k & 1) == 0 ? 4 + (int)sub : (int)sub;
+                            rec[hoff + (k / 2) * 64 + g * 16 + j * 4 + t] |= (uint8_t)(((uv >> 4) & 1) << bit);
+                        } else if (hp == 2) {
+                            static const int sh[4] = {4, 6, 2, 0};
+                            rec[hoff + k * 64 + g * 16 + j * 4 + t] |= (uint8_t)(((uv >> 4) & 3) << sh[sub]);
+                        }
+                    }
+            }
+        }
+    });
+}
+
+// ---------------------------------------------------------------- NF4
+
+static float fit_nf4_codebook(const float *W, size_t rows, size_t cols, size_t sgc, int8_t *cb,
+                              const SignTable &st) {
+    const int HIST = 2000;
+    const float BIN_W = 5.0f / 2000.0f;
+    const size_t nc = cols / 64, nsg = (nc + sgc - 1) / sgc;
+    const size_t step = std::max<size_t>(rows / 512, 1);
+    std::vector<uint64_t> hist(HIST, 0);
+    uint64_t total = 0;
+    std::vector<float> row(cols);
+    for (size_t r = 0; r < rows; r += step) {
+        memcpy(row.data(), W + r * cols, cols * sizeof(float));
+        fwht_row(row.data(), cols, st);
+        for (size_t sg = 0; sg < nsg; sg++) {
+            const size_t cs = sg * sgc * 64, ce = std::min(cols, (sg + 1) * sgc * 64);
+            float ss = 0.0f;
+            for (size_t i = cs; i < ce; i++) ss += row[i] * row[i];
+            const float rms = sqrtf(ss / (float)(ce - cs));
+            if (rms <= 1e-12f) continue;
+            const float inv = 1.0f / rms;
+            for (size_t i = cs; i < ce; i++) {
+                const float q = (fabsf(row[i]) * inv) / BIN_W;
+                const size_t bin = q >= (float)HIST ? (size_t)HIST - 1 : (size_t)q;
+                hist[std::min(bin, (size_t)HIST - 1)]++;
+                total++;
+            }
+        }
+    }
+    static const int8_t NF4_DEFAULT[16] = {-127, -96, -75, -58, -44, -31, -18, -6,
+                                           6,    18,  31,  44,  58,  75,  96,  127};
+    if (total < 256) {
+        memcpy(cb, NF4_DEFAULT, 16);
+        return 2.7326f;
+    }
+    const int half = 8;
+    double mu[8] = {0.1284, 0.3881, 0.6568, 0.9424, 1.2562, 1.6180, 2.0690, 2.7326};
+    for (int it = 0; it < 24; it++) {
+        size_t bounds[9];
+        bounds[0] = 0;
+        bounds[half] = HIST;
+        for (int m = 0; m < half - 1; m++) {
+            const double rb = round(0.5 * (mu[m] + mu[m + 1]) / (double)BIN_W);
+            size_t b = rb <= 0.0 ? 0 : (size_t)rb;
+            bounds[m + 1] = std::min<size_t>(std::max(b, bounds[m]), HIST);
+        }
+        for (int m = 0; m < half; m++) {
+            double ws = 0.0;
+            uint64_t cs = 0;
+            for (size_t b = bounds[m]; b < bounds[m + 1]; b++)
+                if (hist[b]) {
+                    ws += (double)hist[b] * (((double)b + 0.5) * (double)BIN_W);
+                    cs += hist[b];
+                }
+            if (cs) mu[m] = ws / (double)cs;
+        }
+        for (int m = 1; m < half; m++)
+            if (mu[m] <= mu[m - 1] + 1e-4) mu[m] = mu[m - 1] + 0.05;
+    }
+    const double top = std::max(mu[half - 1], 0.5);
+    int q[8];
+    for (int m = 0; m < half; m++) q[m] = std::min(127, std::max(1, (int)round(127.0 * mu[m] / top)));
+    q[half - 1] = 127;
+    for (int m = half - 2; m >= 0; m--)
+        if (q[m] >= q[m + 1]) q[m] = std::max(q[m + 1] - 1, 1);
+    for (int m = 1; m < half; m++)
+        if (q[m] <= q[m - 1]) q[m] = std::min(q[m - 1] + 1, 127);
+    for (int m = 0; m < half; m++) {
+        cb[half - 1 - m] = (int8_t)(-q[m]);
+        cb[half + m] = (int8_t)q[m];
+    }
+    return (float)top;
+}
+
+static inline size_t nf4_nearest(float w, float inv_delta, const float *th) {
+    const float aw = fabsf(w) * inv_delta;
+    size_t mag;
+    if (aw < th[3]) mag = aw < th[1] ? (size_t)(aw >= th[0]) : 2 + (size_t)(aw >= th[2]);
+    else mag = aw < th[5] ? 4 + (size_t)(aw >= th[4]) : 6 + (size_t)(aw >= th[6]);
+    return w >= 0.0f ? 8 + mag : 7 - mag;
+}
+
+// One scale group of one row: returns the BF16 scale and writes indices.
+static uint16_t nf4_group(const float *sub, size_t glen, const float *cbf, const float *th, float mu_top,
+                          uint8_t *best, uint8_t *cand) {
+    static const float ratios[11] = {0.74f, 0.80f, 0.86f, 0.91f, 0.96f, 1.00f,
+                                     1.04f, 1.09f, 1.15f, 1.22f, 1.30f};
+    float ss = 0.0f;
+    for (size_t j = 0; j < glen; j++) ss += sub[j] * sub[j];
+    const float rms = sqrtf(ss / (float)glen);
+    if (rms <= 1e-12f) {
+        memset(best, 7, glen);
+        return 0;
+    }
+    const float base = rms * (mu_top / 127.0f);
+    float best_loss = INFINITY;
+    uint16_t bestd = 0;
+    memset(best, 0, glen);
+    auto eval = [&](uint16_t d) {
+        const float delta = from_bf16(d);
+        if (delta <= 0.0f) return;
+        const float inv = 1.0f / delta;
+        float loss = 0.0f;
+        for (size_t j = 0; j < glen; j++) {
+            const size_t k = nf4_nearest(sub[j], inv, th);
+            cand[j] = (uint8_t)k;
+            const float diff = sub[j] - cbf[k] * delta;
+            loss += diff * diff;
+        }
+        if (loss < best_loss) {
+            best_loss = loss;
+            bestd = d;
+            memcpy(best, cand, glen);
+        }
+    };
+    for (int e = 0; e < 11; e++) eval(to_bf16(base * ratios[e]));
+    float wc = 0.0f, cc = 0.0f;
+    for (size_t j = 0; j < glen; j++) {
+        const float cv = cbf[best[j]];
+        wc += sub[j] * cv;
+        cc += cv * cv;
+    }
+    if (cc > 1e-12f && wc > 0.0f) {
+        const uint16_t ls = to_bf16(wc / cc);
+        if (ls != bestd) eval(ls);
+    }
+    return bestd;
+}
+
+static void compile_nf4(const float *W, size_t rows, size_t cols, size_t sgc, bool interleave, int threads,
+                        int8_t *cb, float *mu_out, uint8_t *pair, uint8_t *tail) {
+    const size_t nc = cols / 64, nsg = (nc + sgc - 1) / sgc, stripes = (rows + 15) / 16, np = stripes / 2;
+    const size_t ptot = nsg * 64 + nc * 1024, ttot = nsg * 32 + nc * 512;
+    SignTable st(nc);
+    const float mu_top = fit_nf4_codebook(W, rows, cols, sgc, cb, st);
+    if (mu_out) *mu_out = mu_top;
+    float cbf[16], th[7];
+    for (int k = 0; k < 16; k++) cbf[k] = (float)cb[k];
+    for (int m = 0; m < 7; m++) th[m] = 0.5f * (cbf[8 + m] + cbf[9 + m]);
+    memset(pair, 0, np * ptot);
+    if (stripes & 1) memset(tail, 0, ttot);
+    parallel_for(stripes, threads, [&](size_t s) {
+        std::vector<float> row(cols);
+        std::vector<uint8_t> idx(16 * cols, 0), best(sgc * 64), cand(sgc * 64);
+        std::vector<uint16_t> scales(16 * nsg, 0);
+        for (size_t lane = 0; lane < 16; lane++) {
+            const size_t r = s * 16 + lane;
+            if (r >= rows) break;
+            memcpy(row.data(), W + source_row(r, rows, interleave) * cols, cols * sizeof(float));
+            fwht_row(row.data(), cols, st);
+            for (size_t sg = 0; sg < nsg; sg++) {
+                const size_t c0 = sg * sgc, c1 = std::min(nc, c0 + sgc), glen = (c1 - c0) * 64;
+                scales[lane * nsg + sg] =
+                    nf4_group(row.data() + c0 * 64, glen, cbf, th, mu_top, best.data(), cand.data());
+                memcpy(idx.data() + lane * cols + c0 * 64, best.data(), glen);
+            }
+        }
+        // Pack (simd_lut.rs:4874-4923): rows past `rows` keep index 0.
+        const bool in_pair = s < np * 2;
+        const size_t side = s & 1;
+        for (size_t sg = 0; sg < nsg; sg++) {
+            const size_t c0 = sg * sgc, c1 = std::min(nc, c0 + sgc);
+            uint8_t *gb = in_pair ? pair + (s / 2) * ptot + sg * 64 + c0 * 1024 : tail + sg * 32 + c0 * 512;
+            uint8_t *sp = gb + (in_pair ? side * 32 : 0);
+            for (size_t lane = 0; lane < 16; lane++) {
+                sp[lane * 2] = (uint8_t)scales[lane * nsg + sg];
+                sp[lane * 2 + 1] = (uint8_t)(scales[lane * nsg + sg] >> 8);
+            }
+            for (size_t c = c0; c < c1; c++) {
+                uint8_t *dst = in_pair ? gb + (in_pair ? 64 : 32) + (c - c0) * 1024 + side * 512
+                                       : gb + 32 + (c - c0) * 512;
+                for (size_t k = 0; k < 4; k++)
+                    for (size_t g = 0; g < 4; g++)
+                        for (size_t j = 0; j < 4; j++) {
+                            const size_t lane = g * 4 + j;
+                            const uint8_t *ir = idx.data() + lane * cols + c * 64 + k * 16;
+                            const bool live = s * 16 + lane < rows;
+                            for (size_t t = 0; t < 4; t++) {
+                                const uint8_t lo0 = live ? ir[t] & 15 : 0, hi0 = live ? ir[4 + t] & 15 : 0;
+                                const uint8_t lo1 = live ? ir[8 + t] & 15 : 0, hi1 = live ? ir[12 + t] & 15 : 0;
+                                dst[k * 128 + g * 32 + j * 4 + t] = (uint8_t)(lo0 | (hi0 << 4));
+                                dst[k * 128 + g * 32 + 16 + j * 4 + t] = (uint8_t)(lo1 | (hi1 << 4));
+                            }
+                        }
+            }
+        }
+    });
+}
+
+// Counter-based N(0, std): SplitMix64 of (seed, pair index) -> two uniforms -> Box-Muller.
+static void synth_normal(uint64_t seed, float stdv, float *out, size_t n, int threads) {
+    const size_t pairs = (n + 1) / 2, blk = 1 << 16;
+    parallel_for((pairs + blk - 1) / blk, threads, [&](size_t b) {
+        const size_t p0 = b * blk, p1 = std::min(pairs, p0 + blk);
+        for (size_t p = p0; p < p1; p++) {
+            uint64_t z = seed * 0xD1B54A32D192ED03ULL + p * 0x9E3779B97F4A7C15ULL;
+            uint64_t h[2];
+            for (int k = 0; k < 2; k++) {
+                z += 0x9E3779B97F4A7C15ULL;
+                uint64_t x = z;
+                x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ULL;
+                x = (x ^ (x >> 27)) * 0x94D049BB133111EBULL;
+                h[k] = x ^ (x >> 31);
+            }
+            const double u1 = ((double)(h[0] >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+            const double u2 = (double)(h[1] >> 11) * (1.0 / 9007199254740992.0);
+            const double rad = sqrt(-2.0 * log(u1)) * (double)stdv;
+            out[2 * p] = (float)(rad * cos(6.283185307179586 * u2));
+            if (2 * p + 1 < n) out[2 * p + 1] = (float)(rad * sin(6.283185307179586 * u2));
+        }
+    });
+}
+
+}  // namespace host
+}  // namespace k2t
+
+using namespace k2t;
+
+extern "C" {
+
+int32_t k2t_stream_sizes(int32_t fmt, int32_t rows, int32_t cols, int32_t planes_or_bits, int32_t sgc,
+                         size_t *pair_len, size_t *tail_len) {
+    if (!pair_len || !tail_len || rows <= 0 || cols <= 0 || cols % 64) return K2T_E_ARG;
+    const size_t stripes = (size_t)(rows + 15) / 16, nc = (size_t)cols / 64;
+    if (fmt == 1) {
+        if (planes_or_bits < 4 || planes_or_bits > 6) return K2T_E_ARG;
+        const size_t hp = (size_t)planes_or_bits - 4;
+        *pair_len = (stripes / 2) * nc * (1024 + 256 * hp + 64);
+        *tail_len = (stripes & 1) * nc * (512 + 128 * hp + 32);
+        return K2T_OK;
+    }
+    if (fmt == 2) {
+        if (planes_or_bits != 4 || sgc < 1 || sgc > 8) return K2T_E_ARG;
+        const size_t nsg = (nc + sgc - 1) / sgc;
+        *pair_len = (stripes / 2) * (nsg * 64 + nc * 1024);
+        *tail_len = (stripes & 1) * (nsg * 32 + nc * 512);
+        return K2T_OK;
+    }
+    return K2T_E_ARG;
+}
+
+int32_t k2t_compile_bipolar(const float *W, int32_t rows, int32_t cols, int32_t planes,
+                            int32_t interleave_gate_up, int32_t threads, uint8_t *pair, size_t pair_len,
+                            uint8_t *tail, size_t tail_len) {
+    size_t pl = 0, tl = 0;
+    if (!W || k2t_stream_sizes(1, rows, cols, planes, 1, &pl, &tl) != K2T_OK) return K2T_E_ARG;
+    if (pl != pair_len || tl != tail_len || (pl && !pair) || (tl && !tail)) return K2T_E_ARG;
+    if (interleave_gate_up && rows % 128) return K2T_E_ARG;
+    try {
+        host::compile_bipolar(W, (size_t)rows, (size_t)cols, planes, interleave_gate_up != 0, threads, pair, tail);
+    } catch (...) {
+        return K2T_E_INTERNAL;
+    }
+    return K2T_OK;
+}
+
+int32_t k2t_compile_nf(const float *W, int32_t rows, int32_t cols, int32_t bits, int32_t sgc,
+                       int32_t interleave_gate_up, int32_t threads, int8_t *codebook16, float *mu_top,
+                       uint8_t *pair, size_t pair_len, uint8_t *tail, size_t tail_len) {
+    size_t pl = 0, tl = 0;
+    if (!W || !codebook16 || k2t_stream_sizes(2, rows, cols, bits, sgc, &pl, &tl) != K2T_OK) return K2T_E_ARG;
+    if (pl != pair_len || tl != tail_len || (pl && !pair) || (tl && !tail)) return K2T_E_ARG;
+    if (interleave_gate_up && rows % 128) return K2T_E_ARG;
+    try {
+        host::compile_nf4(W, (size_t)rows, (size_t)cols, (size_t)sgc, interleave_gate_up != 0, threads, codebook16,
+                          mu_top, pair, tail);
+    } catch (...) {
+        return K2T_E_INTERNAL;
+    }
+    return K2T_OK;
+}
+
+int32_t k2t_synth_normal(uint64_t seed, float stdv, float *out, size_t n, int32_t threads) {
+    if (!out && n) return K2T_E_ARG;
+    try {
+        host::synth_normal(seed, stdv, out, n, threads);
+    } catch (...) {
+        return K2T_E_INTERNAL;
+    }
+    return K2T_OK;
+}
+
+}  // extern "C"

@@ -8,6 +8,14 @@ namespace k2t {
 
 constexpr int kWave = 64;
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 128-bit streaming load (nontemporal: weight bytes are read once per pass).
+__device__ __forceinline__ uint4 load_stream16(const void *p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Sign of element `i` of Hadamard block `block` (hadamard.rs:29-44): SplitMix64 state
 // seed + block*0xBF58.. advanced i+1 times, finalized, low bit.  Each lane computes its
 // own element, so no table is needed.

@@ -11,11 +11,9 @@ struct k2t_ctx {
     hipStream_t stream = nullptr;
     int max_segments = 0;  // split-K policy: 0 auto, 1 off, n cap
     int num_cus = 256;
-    // split-K scratch: fp32 partial rows + per-row-block arrival counters.
-    float *partial = nullptr;
-    size_t partial_cap = 0;  // floats
-    uint32_t *counters = nullptr;
-    size_t counter_cap = 0;  // entries, always left at zero between calls
+    // small device scratch (debug entry points): grown on demand
+    float *scratch = nullptr;
+    size_t scratch_cap = 0;  // floats
     float *rms_scratch = nullptr;
     size_t rms_cap = 0;
 };
@@ -45,12 +43,12 @@ struct Error : std::runtime_error {
 
 void hip_check(hipError_t e, const char *what);
 
-// Grows the context's split-K scratch (synchronous allocation; counters zeroed).
-void ensure_scratch(k2t_ctx *ctx, size_t partial_floats, size_t counters);
+// Grows the context's scratch buffer (synchronous allocation).
+void ensure_scratch(k2t_ctx *ctx, size_t floats);
 
 struct GemvPlan {
-    int rb_lo, rb_hi;  // row-block range (pairs, then the tail stripe)
-    int nseg, cps;     // K segments and chunks per segment
+    int s_lo, nstripes;  // stripe range
+    int nseg, cps;       // K segments (waves per workgroup) and chunks per segment
 };
 GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1);
 

@@ -61,6 +61,10 @@ SIGNATURES = {
     "k2t_act_quant_rmsnorm": (I32, [VP, VP, VP, C.c_float, I32, I32, VP, VP, VP]),
     "k2t_gemv": (I32, [VP, VP, VP, VP, VP, I32, I32, I32, VP, SZ]),
     "k2t_gemv_chunk_dots": (I32, [VP, VP, VP, VP, VP]),
+    "k2t_stream_sizes": (I32, [I32, I32, I32, I32, I32, C.POINTER(SZ), C.POINTER(SZ)]),
+    "k2t_compile_bipolar": (I32, [VP, I32, I32, I32, I32, I32, VP, SZ, VP, SZ]),
+    "k2t_compile_nf": (I32, [VP, I32, I32, I32, I32, I32, I32, VP, VP, VP, SZ, VP, SZ]),
+    "k2t_synth_normal": (I32, [C.c_uint64, C.c_float, VP, SZ, I32]),
 }
 
 
@@ -198,3 +202,47 @@ class Mat:
             self.close()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------------------- offline compiler
+def stream_sizes(fmt, rows, cols, planes_or_bits, sgc=1):
+    pl, tl = SZ(), SZ()
+    check(lib().k2t_stream_sizes(fmt, rows, cols, planes_or_bits, sgc, C.byref(pl), C.byref(tl)))
+    return pl.value, tl.value
+
+
+def compile_bipolar(W, planes, interleave_gate_up=False, threads=0):
+    """Host RTN bit-plane compile -> (pair, tail) numpy uint8 streams."""
+    import numpy as np
+    W = np.ascontiguousarray(W, np.float32)
+    rows, cols = W.shape
+    pl, tl = stream_sizes(1, rows, cols, planes)
+    pair = np.empty(pl, np.uint8)
+    tail = np.empty(tl, np.uint8)
+    check(lib().k2t_compile_bipolar(W.ctypes.data_as(VP), rows, cols, planes, int(interleave_gate_up), threads,
+                                    pair.ctypes.data_as(VP) if pl else None, pl,
+                                    tail.ctypes.data_as(VP) if tl else None, tl))
+    return pair, tail
+
+
+def compile_nf4(W, sgc=2, interleave_gate_up=False, threads=0):
+    """Host RTN NF4 compile -> (codebook int8[16], mu_top, pair, tail)."""
+    import numpy as np
+    W = np.ascontiguousarray(W, np.float32)
+    rows, cols = W.shape
+    pl, tl = stream_sizes(2, rows, cols, 4, sgc)
+    pair = np.empty(pl, np.uint8)
+    tail = np.empty(tl, np.uint8)
+    cb = np.zeros(16, np.int8)
+    mu = C.c_float()
+    check(lib().k2t_compile_nf(W.ctypes.data_as(VP), rows, cols, 4, sgc, int(interleave_gate_up), threads,
+                               cb.ctypes.data_as(VP), C.byref(mu), pair.ctypes.data_as(VP) if pl else None, pl,
+                               tail.ctypes.data_as(VP) if tl else None, tl))
+    return cb, mu.value, pair, tail
+
+
+def synth_normal(seed, n, std=1.0, threads=0):
+    import numpy as np
+    out = np.empty(n, np.float32)
+    check(lib().k2t_synth_normal(seed, std, out.ctypes.data_as(VP) if n else None, n, threads))
+    return out

@@ -1,9 +1,11 @@
 """GPU parity of the activation quantizer and the GEMV / 4-token tile (C ABI -> HIP).
 
 Bar: int8 q / scales / sums and every per-(row, chunk) integer dot bit-exact against
-the oracle; fp32 GEMV outputs bit-exact with split-K off (same fmaf order as the
-reference's NEON epilogue) and within the reference's own batch tolerance
-1e-4 * (1 + |y|) (simd_lut.rs:8936) with split-K on.
+the oracle; fp32 GEMV outputs bit-exact (same fmaf order as the reference's NEON
+epilogue) both with split-K off and with the automatic K split (per-chunk terms staged
+in LDS).  Only the ordered-partial-sum fallback, used when a 4-token tile's terms do
+not fit in LDS, is held to the reference's batch tolerance 1e-4 * (1 + |y|)
+(simd_lut.rs:8936).
 """
 import numpy as np
 import pytest
@@ -85,7 +87,7 @@ def test_nibble4_gemv_exact(gpu_ctx, hp, rows, cols):
         gpu_ctx.set_splitk(0)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), "fp32 epilogue not bit-exact"
     out2 = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
-    assert np.all(np.abs(out2 - ref) <= 1e-4 * (1 + np.abs(ref)))
+    assert np.array_equal(out2.view(np.uint32), ref.view(np.uint32)), "split-K result not bit-exact"
 
 
 def test_nibble4_config1_quantized(gpu_ctx):
@@ -131,7 +133,7 @@ def test_nf4_gemv_exact(gpu_ctx, sgc, rows, cols):
         gpu_ctx.set_splitk(0)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
     out2 = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
-    assert np.all(np.abs(out2 - ref) <= 1e-4 * (1 + np.abs(ref)))
+    assert np.array_equal(out2.view(np.uint32), ref.view(np.uint32)), "split-K result not bit-exact"
 
 
 def test_nf4_quantized_model_matrix(gpu_ctx):
@@ -143,7 +145,7 @@ def test_nf4_quantized_model_matrix(gpu_ctx):
     m = gpu_ctx.upload_nf(rows, cols, 4, 2, cb, pair, tail)
     out = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows)[0]
     ref = O.nf_gemv(pair, tail, rows, cols, 4, 2, cb, xq, xs)
-    assert np.all(np.abs(out - ref) <= 1e-4 * (1 + np.abs(ref)))
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("fmt", ["b5", "nf4"])
@@ -168,7 +170,7 @@ def test_batch_matches_single(gpu_ctx, fmt):
     finally:
         gpu_ctx.set_splitk(0)
     batch2 = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows, ntok=ntok)
-    assert np.all(np.abs(batch2 - batch) <= 1e-4 * (1 + np.abs(batch)))
+    assert np.array_equal(batch2.view(np.uint32), batch.view(np.uint32))
 
 
 def test_stripe_subrange(gpu_ctx):
@@ -183,7 +185,7 @@ def test_stripe_subrange(gpu_ctx):
         out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, s0=s0, s1=s1)[0]
         lo, hi = s0 * 16, min(s1 * 16, rows)
         assert np.all(np.isnan(out[:lo])) and np.all(np.isnan(out[hi:]))
-        assert np.all(np.abs(out[lo:hi] - ref[lo:hi]) <= 1e-4 * (1 + np.abs(ref[lo:hi])))
+        assert np.array_equal(out[lo:hi].view(np.uint32), ref[lo:hi].view(np.uint32))
 
 
 @pytest.mark.parametrize("rows,cols,hp", [(14336, 4096, 2), (4096, 14336, 2)])
@@ -199,4 +201,18 @@ def test_large_b6_dots_and_outputs(gpu_ctx, rows, cols, hp):
     gpu_ctx.gemv_chunk_dots(m, _t(xq[0]), _t(xsum[0]), d)
     assert np.array_equal(d.cpu().numpy(), dots)
     out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
-    assert np.all(np.abs(out - ref) <= 1e-4 * (1 + np.abs(ref)))
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_batch4_large_k_partial_sum_fallback(gpu_ctx):
+    """4 tokens x K=14336: per-chunk terms exceed LDS, ordered partial sums are used."""
+    rng = np.random.default_rng(21)
+    rows, cols, ntok = 256, 14336, 4
+    _, _, pair, tail = random_nf_streams(rng, rows, cols, 2)
+    cb = np.array([-127, -96, -75, -58, -44, -31, -18, -6, 6, 18, 31, 44, 58, 75, 96, 127], np.int8)
+    m = gpu_ctx.upload_nf(rows, cols, 4, 2, cb, pair, tail)
+    xq, xs, xsum = acts(rng, cols, ntok)
+    out = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows, ntok=ntok)
+    for t in range(ntok):
+        ref = O.nf_gemv(pair, tail, rows, cols, 4, 2, cb, xq[t], xs[t])
+        assert np.all(np.abs(out[t] - ref) <= 1e-4 * (1 + np.abs(ref)))
