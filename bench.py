@@ -101,19 +101,20 @@ def _busy_wait(torch, stream, seconds):
 
 
 def time_case(ctx, torch, case, steps, warmup):
+    """Mean device time per GEMV: `steps` back-to-back launches between two events on
+    the kernels' stream, enqueued behind a spin so the host never starves the queue."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         case.launch(ctx)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     _busy_wait(torch, stream, 2e-3 + steps * 60e-6)
-    for a, b in ev:
-        a.record(stream)
+    a.record(stream)
+    for _ in range(steps):
         case.launch(ctx)
-        b.record(stream)
+    b.record(stream)
     torch.cuda.synchronize()
-    per = np.array([a.elapsed_time(b) for a, b in ev]) * 1e-3  # seconds
-    return float(np.mean(per)), float(np.median(per))
+    return a.elapsed_time(b) * 1e-3 / steps
 
 
 def cpu_baseline(case, seconds=10.0):
@@ -171,6 +172,8 @@ def main():
     ctx.set_stream(torch.cuda.current_stream())
     if os.environ.get("K2T_SPLITK"):
         ctx.set_splitk(int(os.environ["K2T_SPLITK"]))
+    if os.environ.get("K2T_EXACT"):
+        ctx.set_exact(int(os.environ["K2T_EXACT"]))
 
     specs = [("nf4g128_14336x4096", "nf4", 14336, 4096), ("nf4g128_4096x14336", "nf4", 4096, 14336),
              ("b6_14336x4096", "b6", 14336, 4096), ("b6_4096x14336", "b6", 4096, 14336)]
@@ -186,11 +189,10 @@ def main():
     total_t = 0.0
     total_b = 0
     for case in cases:
-        mean_s, med_s = time_case(ctx, torch, case, args.steps, args.warmup)
+        mean_s = time_case(ctx, torch, case, args.steps, args.warmup)
         gbs = case.bytes / mean_s / 1e9
-        results[case.name] = {"us": round(mean_s * 1e6, 3), "us_median": round(med_s * 1e6, 3),
-                              "GB_s": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                              "bytes": case.bytes}
+        results[case.name] = {"us": round(mean_s * 1e6, 3), "GB_s": round(gbs, 1),
+                              "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 2), "bytes": case.bytes}
         total_t += mean_s
         total_b += case.bytes
         print(f"# {case.name}: {mean_s * 1e6:.2f} us  {gbs:.1f} GB/s  {100 * gbs / HBM_PEAK_GBS:.1f}% of peak",

@@ -71,9 +71,14 @@ void k2t_ctx_destroy(k2t_ctx *ctx);
 int32_t k2t_ctx_set_stream(k2t_ctx *ctx, void *hip_stream);
 /* Blocks until all work queued on the context's stream is done. */
 int32_t k2t_ctx_sync(k2t_ctx *ctx);
-/* Split-K policy for k2t_gemv: 0 = automatic, 1 = never split (bit-exact fp32
- * epilogue order of simd_lut.rs:4030-4059), n > 1 = at most n K-segments. */
+/* Cap on the K segments (waves per workgroup) k2t_gemv may use: 0 = automatic. */
 int32_t k2t_ctx_set_splitk(k2t_ctx *ctx, int32_t max_segments);
+/* fp32 epilogue of k2t_gemv.  exact = 1 replays the reference's per-row fmaf chain
+ * in chunk order (simd_lut.rs:4030-4059, 6334-6335) and is bit-identical to it;
+ * exact = 0 (default) sums per-segment chains in a fixed order: deterministic and
+ * within a few ulp of the reference, and faster for long K.  Integer per-(row, chunk)
+ * dots are exact in both modes. */
+int32_t k2t_ctx_set_exact(k2t_ctx *ctx, int32_t exact);
 
 /* ---- device memory helpers (tests, benches, non-torch callers) ---------- */
 int32_t k2t_malloc(k2t_ctx *ctx, size_t bytes, void **d_out);

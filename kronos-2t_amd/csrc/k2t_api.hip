@@ -93,7 +93,7 @@ static void fill_common(k2t_mat *m, int rows, int cols) {
 static void check_shape(int rows, int cols) {
     arg_check(rows > 0 && cols > 0, "rows and cols must be positive");
     arg_check(cols % 64 == 0, "cols must be a multiple of 64");
-    arg_check(cols <= (1 << 24) && rows <= (1 << 26), "matrix too large");
+    arg_check(cols <= 32768 && rows <= (1 << 26), "matrix too large (cols <= 32768, rows <= 2^26)");
 }
 
 static void upload_streams(k2t_mat *m, const uint8_t *pair, size_t pl, const uint8_t *tail,
@@ -247,6 +247,13 @@ int32_t k2t_ctx_set_splitk(k2t_ctx *ctx, int32_t max_segments) {
         arg_check(ctx != nullptr, "ctx is NULL");
         arg_check(max_segments >= 0 && max_segments <= 4096, "max_segments out of range");
         ctx->max_segments = max_segments;
+    });
+}
+
+int32_t k2t_ctx_set_exact(k2t_ctx *ctx, int32_t exact) {
+    return guarded([&] {
+        arg_check(ctx != nullptr, "ctx is NULL");
+        ctx->exact = exact ? 1 : 0;
     });
 }
 

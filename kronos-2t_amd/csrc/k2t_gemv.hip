@@ -6,10 +6,10 @@
 //   NF4        nf_sdot_stripe_range_raw / nf_sdot_decode_neon     (simd_lut.rs:5687-6364)
 //              nf_sdot_batch_stripe_range                         (simd_lut.rs:6689-7034)
 //
-// Work unit = one workgroup per 16-row stripe; its waves split K into segments (as many
-// as needed to put ~8 streaming waves on every CU).  Per step a wave reads the stripe's
-// 512 nibble bytes of two chunks with one 128-bit load per lane (plus hi-plane bytes /
-// BF16 scales), decodes codes (u, or codebook values through a v_perm byte table) and
+// Work unit = one workgroup per stripe pair (32 rows; the odd last stripe alone); its
+// waves split K into segments (as many as needed to put ~8 streaming waves on every CU).
+// Per chunk a wave reads the pair's contiguous record -- 1024 nibble bytes with one
+// 128-bit load per lane, plus hi-plane bytes / BF16 scales -- decodes codes (u, or codebook values through a v_perm byte table) and
 // accumulates them against int8 activations with v_dot4_i32_i8.  Two DPP steps leave
 // every lane with the exact i32 dot of 2 rows for its chunk.
 //
@@ -19,6 +19,8 @@
 // row replays the chain after a barrier.  Either way the result is bit-identical to
 // the reference.  No global scratch, atomics or device-scope fences are used.
 #include <float.h>
+
+#include <stdlib.h>
 
 #include <algorithm>
 
@@ -38,275 +40,327 @@ struct GemvParams {
     size_t out_stride;
     size_t ptot;  // NF: bytes per pair stream
     int rows, K, nc, np;
-    int s_lo, nstripes;  // stripes [s_lo, s_lo + nstripes)
-    int nseg, cps;       // K segments per stripe (= waves per workgroup), chunks per segment
+    int s0, s1;      // stripes written: [s0, s1)
+    int rb_lo;       // first row block (pair index; np = the tail stripe)
+    int nseg, cps;   // K segments per row block (= waves per workgroup), chunks per segment
     int sgc;
     int tok_base;
-    int lds_terms;  // 1: per-chunk terms in LDS (exact chain), 0: ordered partial sums
+    int lds_terms;  // per-chunk terms staged in LDS (always 1 in this build)
+    int stripe_mode;  // 1: a workgroup owns one stripe (16 rows), 0: a stripe pair (32 rows)
+    int exact;        // 1: replay the reference's fmaf chain from LDS-staged terms
+    int dbg;
     uint32_t cb0, cb1, cb2, cb3;
 };
 
-// Sum over the 8 lanes of a 16-lane row that share a 4-row group (lane bits 0, 2, 3),
-// transposing so that a lane with half=h keeps rows 2h and 2h+1 of its group.
-__device__ __forceinline__ void reduce_rows(int a0, int a1, int a2, int a3, uint32_t half,
-                                            int &r0, int &r1) {
-    int s0 = half ? a0 : a2, s1 = half ? a1 : a3;
-    int k0 = half ? a2 : a0, k1 = half ? a3 : a1;
-    k0 += dpp_xor1(s0);
-    k1 += dpp_xor1(s1);
-    k0 += dpp_ror8(k0);
-    k1 += dpp_ror8(k1);
-    k0 += dpp_ror4(k0);
-    k1 += dpp_ror4(k1);
-    r0 = k0;
-    r1 = k1;
-}
-
-// Registers of one fetched stripe-chunk record for one lane.
-template <int NT>
+// Registers of one fetched chunk for one lane: its 64 nibble bytes (rows 4g..4g+3,
+// the lane's 8-column half of each of the four 16-column blocks), hi-plane bytes, the
+// BF16 scales of its two output rows and the matching activation bytes.
+template <int HP, int NT>
 struct Frag {
-    uint4 w;
-    uint4 h;
+    uint4 w[4];
+    uint4 h[HP == 0 ? 1 : (HP == 1 ? 2 : 4)];
     uint32_t ws;
-    uint2 x[NT];
+    uint2 x[NT][4];
+    float sx[NT];
+    int sum[NT];
 };
 
-// One workgroup = one 16-row stripe; its nseg waves take consecutive K segments.
-// A wave steps over chunk pairs: lanes 0-31 decode chunk c, lanes 32-63 chunk c+1.
-// Lane bits: 0 = half (8-column half of a 16-column block), 1 = g bit 0, 2-3 = k
-// (16-column block), 4 = g bit 1, 5 = chunk parity.  A lane's 16 bytes are rows
-// 4g..4g+3 x 8 columns; each quad of lanes reads 64 contiguous bytes and the row
-// reduction stays inside a 16-lane DPP row.
+// One workgroup = one row block (a stripe pair, or the odd tail stripe).  Lane bits:
+// 0 = half (8-column half of a 16-column block), 1-2 = g (4-row group), 3 = stripe of the
+// pair, 4-5 = q.  Each 16-lane group q of each wave owns one K sub-segment, so a row
+// block's K range is split into 4 * nseg sub-segments.  Per chunk a lane loads the four
+// 16-byte pieces of its (side, g, half) -- one per 16-column block k -- so a load
+// instruction reads two 128-byte runs per group, and the lane accumulates all 32 of its
+// columns for 4 rows with v_dot4_i32_i8.  One DPP step over `half` completes the exact
+// i32 dot of each (row, chunk).  The fp32 terms float(dot)*sx and ws are staged in LDS
+// and one thread per row replays the reference's fmaf chain in chunk order.
 // FMT 0: bit-plane Nibble4 with HP hi planes; FMT 1: NF4 codebook stripes.
 template <int FMT, int HP, int NT, bool DOTS>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
-    constexpr int U = NT == 1 ? 4 : 2;  // chunk pairs fetched before use
+    constexpr int U = NT == 1 ? 2 : 1;  // chunks fetched ahead per lane
+    constexpr int NH = HP == 0 ? 1 : (HP == 1 ? 2 : 4);
     extern __shared__ float lds[];
     const uint32_t lane = threadIdx.x & 63;
-    const int seg = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int s = P.s_lo + (int)blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int tok0 = P.tok_base + (int)blockIdx.y * NT;
-    const bool is_tail = s >= 2 * P.np;
     const uint32_t half = lane & 1u;
-    const uint32_t g = ((lane >> 1) & 1u) | (((lane >> 4) & 1u) << 1);
-    const uint32_t k = (lane >> 2) & 3u;
-    const uint32_t par = lane >> 5;
-    const uint32_t piece = k * 8u + g * 2u + half;
-    const uint32_t sc_lane = (4u * g + 2u * half) * 2u;
-    const uint32_t side = (uint32_t)(s & 1);
-    const int c0 = seg * P.cps;
-    const int c1 = min(P.nc, c0 + P.cps);
+    const uint32_t g = (lane >> 1) & 3u;
+    // Pair mode: lane bit 3 = stripe of the pair, bits 4-5 = sub-segment (4 per wave).
+    // Stripe mode: bits 3-5 = sub-segment (8 per wave); the workgroup owns one stripe.
+    const bool smode = P.stripe_mode != 0;
+    const int rb = P.rb_lo + (int)blockIdx.x;  // pair index, or stripe index in stripe mode
+    const bool is_tail = smode ? rb >= 2 * P.np : rb >= P.np;
+    const uint32_t lane_side = smode ? 0u : (lane >> 3) & 1u;
+    const uint32_t side = smode ? (uint32_t)(rb & 1) : (is_tail ? 0u : lane_side);
+    const int pidx = smode ? (rb >> 1) : rb;  // pair whose records hold these rows
+    // The wave owns chunks [wave*cps, (wave+1)*cps); its lane groups take them round-robin
+    // (chunk granules of sgc for NF), so one load instruction covers consecutive records.
+    const int G = smode ? 8 : 4;
+    const int q = smode ? (int)(lane >> 3) : (int)(lane >> 4);
+    const int cw0 = wave * P.cps;
+    const int cw1 = min(P.nc, cw0 + P.cps);
     constexpr int MAX_ODD = (1 << (4 + HP)) - 1;
-    constexpr size_t PREC = 1024 + 256 * HP + 64;
-    constexpr size_t TREC = 512 + 128 * HP + 32;
-    const int row0 = s * 16 + (int)(4u * g + 2u * half);
+    constexpr uint32_t PREC = 1024 + 256 * HP + 64;
+    constexpr uint32_t TREC = 512 + 128 * HP + 32;
+    const int RB = smode ? 16 : 32;  // rows per workgroup
+    const uint32_t rloc = (smode ? 0u : side * 16u) + 4u * g + 2u * half;  // first of this lane's 2 rows
+    const int stripe = smode ? rb : (is_tail ? 2 * P.np : 2 * rb + (int)side);
+    const int row0 = stripe * 16 + (int)(4u * g + 2u * half);
+    const bool live = !(is_tail && lane_side);
 
-    float f[NT][2];
+    // Byte offsets inside one record (per lane), and the record stride / base.
+    uint32_t nib_off, hi_off = 0, sc_off;
+    if constexpr (FMT == 0) {
+        nib_off = (is_tail ? 0u : side * 512u) + g * 32u + half * 16u;
+        hi_off = (is_tail ? 512u : 1024u + side * 128u * HP) + g * 16u;
+        sc_off = (is_tail ? 512u + 128u * HP : 1024u + 256u * HP + side * 32u);
+    } else {
+        nib_off = (is_tail ? 32u : 64u + side * 512u) + g * 32u + half * 16u;
+        sc_off = is_tail ? 0u : side * 32u;
+    }
+    sc_off += (4u * g + 2u * half) * 2u;
+    const uint8_t *mbase = is_tail ? P.tail : P.pair + (size_t)pidx * (FMT == 0 ? (size_t)P.nc * PREC : P.ptot);
+
+    auto fetch = [&](Frag<HP, NT> &fr, int c) {
+        const uint8_t *rec, *scp;
+        if constexpr (FMT == 0) {
+            rec = mbase + (size_t)c * (is_tail ? TREC : PREC);
+            scp = rec;
+        } else {
+            const int sg = c / P.sgc, cst = sg * P.sgc, sb = c - cst;
+            const uint8_t *gb = mbase + (is_tail ? (size_t)sg * 32 + (size_t)cst * 512
+                                                 : (size_t)sg * 64 + (size_t)cst * 1024);
+            rec = gb + (size_t)sb * (is_tail ? 512 : 1024);
+            scp = gb;
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) fr.w[kk] = load_stream16(rec + nib_off + kk * 128);
+
+        if constexpr (FMT == 0 && HP == 2) {
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) fr.h[kk] = load_stream16(rec + hi_off + kk * 64);
+        } else if constexpr (FMT == 0 && HP == 1) {
+            fr.h[0] = load_stream16(rec + hi_off);
+            fr.h[1] = load_stream16(rec + hi_off + 64);
+        }
+        fr.ws = *reinterpret_cast<const uint32_t *>(scp + sc_off);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+                fr.x[t][kk] = (P.dbg & 4) ? make_uint2(lane, kk)
+                                          : *reinterpret_cast<const uint2 *>(P.xq + (size_t)(tok0 + t) * P.K + c * 64 +
+                                                                             kk * 16 + half * 8);
+            fr.sx[t] = (P.dbg & 4) ? 1.0f : P.xs[(size_t)(tok0 + t) * P.nc + c];
+            if constexpr (FMT == 0) fr.sum[t] = (P.dbg & 4) ? 0 : P.xsum[(size_t)(tok0 + t) * P.nc + c];
+        }
+    };
+
+    float2 *terms = reinterpret_cast<float2 *>(lds);  // [NT][nc][RB] (a = float(dot)*sx, ws)
+
+    float f[NT][2];  // fast epilogue: this lane group's partial chains
 #pragma unroll
     for (int t = 0; t < NT; t++) f[t][0] = f[t][1] = 0.0f;
 
-    const int8_t *xbase = P.xq + (size_t)tok0 * P.K + k * 16 + half * 8;
-
-    auto fetch = [&](Frag<NT> &fr, int c) {
-        const uint8_t *nib, *scp, *hib = nullptr;
-        if constexpr (FMT == 0) {
-            if (is_tail) {
-                const uint8_t *base = P.tail + (size_t)c * TREC;
-                nib = base;
-                hib = base + 512;
-                scp = base + 512 + 128 * HP;
-            } else {
-                const uint8_t *base = P.pair + ((size_t)(s >> 1) * P.nc + c) * PREC;
-                nib = base + side * 512u;
-                hib = base + 1024u + side * 128u * HP;
-                scp = base + 1024u + 256u * HP + side * 32u;
-            }
-            nib += piece * 16u;
-            hib += (HP == 2 ? k * 64u : (k >> 1) * 64u) + g * 16u;
-        } else {
-            const int sg = c / P.sgc, cst = sg * P.sgc, sub = c - cst;
-            if (is_tail) {
-                const uint8_t *gb = P.tail + (size_t)sg * 32 + (size_t)cst * 512;
-                nib = gb + 32 + (size_t)sub * 512;
-                scp = gb;
-            } else {
-                const uint8_t *gb = P.pair + (size_t)(s >> 1) * P.ptot + (size_t)sg * 64 + (size_t)cst * 1024;
-                nib = gb + 64 + (size_t)sub * 1024 + side * 512u;
-                scp = gb + side * 32u;
-            }
-            nib += piece * 16u;
+    auto process = [&](const Frag<HP, NT> &fr, int c) {
+        if (P.dbg & 2) {
+            uint32_t z = 0;
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) z ^= fr.w[kk].x ^ fr.w[kk].y ^ fr.w[kk].z ^ fr.w[kk].w;
+#pragma unroll
+            for (int kk = 0; kk < NH; kk++) z ^= fr.h[kk].x ^ fr.h[kk].w;
+            if (z == 0x9e3779b9u) terms[rloc] = make_float2(1.0f, (float)fr.ws);
+            return;
         }
-        fr.w = load_stream16(nib);
-        if constexpr (FMT == 0 && HP > 0) fr.h = load_stream16(hib);
-        fr.ws = *reinterpret_cast<const uint32_t *>(scp + sc_lane);
+        int acc[NT][4];
 #pragma unroll
-        for (int t = 0; t < NT; t++) fr.x[t] = *reinterpret_cast<const uint2 *>(xbase + (size_t)t * P.K + c * 64);
-    };
-
-    // Decodes one record and returns the exact integer dots of rows row0, row0+1.
-    auto dots_of = [&](const Frag<NT> &fr, int c, int (&r)[NT][2]) {
-        uint32_t lo[4], hi[4];
-        const uint32_t wd[4] = {fr.w.x, fr.w.y, fr.w.z, fr.w.w};
-        const uint32_t hd[4] = {fr.h.x, fr.h.y, fr.h.z, fr.h.w};
+        for (int t = 0; t < NT; t++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t d = wd[j];
-            if constexpr (FMT == 0) {
-                uint32_t l = d & 0x0F0F0F0Fu;
-                uint32_t h = (d >> 4) & 0x0F0F0F0Fu;
-                if constexpr (HP == 2) {
-                    // 2-bit hi codes at shifts {4,6} (half 0) / {2,0} (half 1), simd_lut.rs:3376-3384;
-                    // the rotations keep bits inside each byte once masked with 0x30.
-                    const uint32_t hb = hd[j];
-                    l |= __builtin_rotateright32(hb, half ? 30u : 0u) & 0x30303030u;
-                    h |= __builtin_rotateright32(hb, half ? 28u : 2u) & 0x30303030u;
-                } else if constexpr (HP == 1) {
-                    // 1-bit hi code at bit (k even ? 4+sub : sub), sub = 2*half + nibble (3366-3375).
-                    const uint32_t hb = hd[j];
-                    const uint32_t e = ((k & 1u) ? 28u : 0u) + 2u * half;
-                    l |= __builtin_rotateright32(hb, e) & 0x10101010u;
-                    h |= __builtin_rotateright32(hb, (e + 1u) & 31u) & 0x10101010u;
+            for (int j = 0; j < 4; j++) acc[t][j] = 0;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const uint32_t wd[4] = {fr.w[kk].x, fr.w[kk].y, fr.w[kk].z, fr.w[kk].w};
+            uint4 hv = make_uint4(0, 0, 0, 0);
+            if constexpr (HP == 2) hv = fr.h[kk];
+            if constexpr (HP == 1) hv = fr.h[kk >> 1];
+            const uint32_t hd[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t d = wd[j];
+                uint32_t lo, hi;
+                if constexpr (FMT == 0) {
+                    lo = d & 0x0F0F0F0Fu;
+                    hi = (d >> 4) & 0x0F0F0F0Fu;
+                    if constexpr (HP == 2) {
+                        // 2-bit hi codes at shifts {4,6} (half 0) / {2,0} (half 1), simd_lut.rs:3376-3384;
+                        // the rotations keep bits inside each byte once masked with 0x30.
+                        lo |= __builtin_rotateright32(hd[j], half ? 30u : 0u) & 0x30303030u;
+                        hi |= __builtin_rotateright32(hd[j], half ? 28u : 2u) & 0x30303030u;
+                    } else if constexpr (HP == 1) {
+                        // 1-bit hi code at bit (k even ? 4+sub : sub), sub = 2*half + nibble (3366-3375).
+                        const uint32_t e = ((kk & 1) ? 28u : 0u) + 2u * half;
+                        lo |= __builtin_rotateright32(hd[j], e) & 0x10101010u;
+                        hi |= __builtin_rotateright32(hd[j], (e + 1u) & 31u) & 0x10101010u;
+                    }
+                } else {
+                    lo = lut16(d & 0x07070707u, bit7_mask(d << 4), P.cb0, P.cb1, P.cb2, P.cb3);
+                    hi = lut16((d >> 4) & 0x07070707u, bit7_mask(d), P.cb0, P.cb1, P.cb2, P.cb3);
                 }
-                lo[j] = l;
-                hi[j] = h;
-            } else {
-                lo[j] = lut16(d & 0x07070707u, bit7_mask(d << 4), P.cb0, P.cb1, P.cb2, P.cb3);
-                hi[j] = lut16((d >> 4) & 0x07070707u, bit7_mask(d), P.cb0, P.cb1, P.cb2, P.cb3);
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+                    acc[t][j] = __builtin_amdgcn_sdot4((int)lo, (int)fr.x[t][kk].x,
+                                                       __builtin_amdgcn_sdot4((int)hi, (int)fr.x[t][kk].y, acc[t][j],
+                                                                              false),
+                                                       false);
             }
         }
+        const float ws0 = bf16_lo(fr.ws), ws1 = bf16_hi(fr.ws);
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            int a[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                a[j] = __builtin_amdgcn_sdot4((int)lo[j], (int)fr.x[t].x,
-                                              __builtin_amdgcn_sdot4((int)hi[j], (int)fr.x[t].y, 0, false), false);
-            reduce_rows(a[0], a[1], a[2], a[3], half, r[t][0], r[t][1]);
+            // Complete the 64-column dots: add the other half's columns (lane ^ 1).
+            int a0 = acc[t][0] + dpp_xor1(acc[t][0]);
+            int a1 = acc[t][1] + dpp_xor1(acc[t][1]);
+            int a2 = acc[t][2] + dpp_xor1(acc[t][2]);
+            int a3 = acc[t][3] + dpp_xor1(acc[t][3]);
+            int r0 = half ? a2 : a0, r1 = half ? a3 : a1;  // this lane's rows 2*half, 2*half+1
             if constexpr (FMT == 0) {
-                const int off = MAX_ODD * P.xsum[(size_t)(tok0 + t) * P.nc + c];
-                r[t][0] = 2 * r[t][0] - off;
-                r[t][1] = 2 * r[t][1] - off;
+                const int off = MAX_ODD * fr.sum[t];
+                r0 = 2 * r0 - off;
+                r1 = 2 * r1 - off;
+            }
+            if constexpr (DOTS) {
+                if (live && t == 0) {
+                    if (row0 < P.rows) P.dots[(size_t)row0 * P.nc + c] = r0;
+                    if (row0 + 1 < P.rows) P.dots[(size_t)(row0 + 1) * P.nc + c] = r1;
+                }
+            }
+            const float sx = fr.sx[t];
+            if (P.dbg & 8) { if (r0 == 0x7fffffff) terms[0] = make_float2(sx, ws0); continue; }
+            // The reference skips chunks whose activation scale is 0; fma(-0, +0, f) == f for
+            // every f (signed zeros included), so such chunks stage an exactly neutral term.
+            if (P.exact) {
+                float4 *tp = reinterpret_cast<float4 *>(terms + ((size_t)t * P.nc + c) * RB + rloc);
+                *tp = sx != 0.0f ? make_float4((float)r0 * sx, ws0, (float)r1 * sx, ws1)
+                                 : make_float4(-0.0f, 0.0f, -0.0f, 0.0f);
+            } else {
+                const float n0 = fmaf((float)r0 * sx, ws0, f[t][0]);
+                const float n1 = fmaf((float)r1 * sx, ws1, f[t][1]);
+                f[t][0] = sx != 0.0f ? n0 : f[t][0];
+                f[t][1] = sx != 0.0f ? n1 : f[t][1];
             }
         }
     };
 
-    float2 *terms = reinterpret_cast<float2 *>(lds);  // [NT][nc][16] (a = float(dot)*sx, ws)
-
-    for (int cb = c0; cb < c1; cb += 2 * U) {
-        Frag<NT> fr[U];
+    // Chunk of iteration i for this lane group: granules of `gr` chunks dealt round-robin.
+    const int gr = FMT == 1 ? P.sgc : 1;
+    auto chunk_of = [&](int i) { return cw0 + ((i / gr) * G + q) * gr + (i % gr); };
+    const int iters = ((cw1 - cw0 + G * gr - 1) / (G * gr)) * gr;  // wave-uniform
+    for (int ib = 0; ib < iters; ib += U) {
+        Frag<HP, NT> fr[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int c = cb + 2 * u + (int)par;
-            if (c < c1) fetch(fr[u], c);
-            else fr[u] = Frag<NT>{};
+            const int c = chunk_of(ib + u);
+            if (ib + u < iters && c < cw1) fetch(fr[u], c);
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int ce = cb + 2 * u;  // even chunk of this pair (wave-uniform)
-            if (ce >= c1) break;
-            const int c = ce + (int)par;
-            const bool has_odd = ce + 1 < c1;
-            int r[NT][2];
-            dots_of(fr[u], c < c1 ? c : ce, r);
-            const float ws0 = bf16_lo(fr[u].ws), ws1 = bf16_hi(fr[u].ws);
-            if constexpr (DOTS) {
-                if (k == 0 && (par == 0 || has_odd)) {
-                    if (row0 < P.rows) P.dots[(size_t)row0 * P.nc + c] = r[0][0];
-                    if (row0 + 1 < P.rows) P.dots[(size_t)(row0 + 1) * P.nc + c] = r[0][1];
-                }
-            }
-            if (P.nseg > 1 && P.lds_terms) {
-                // Exact path for split K: every (row, chunk) term goes to LDS, one lane per
-                // row replays the reference's fmaf chain afterwards.
-                if (k == 0 && (par == 0 || has_odd)) {
-#pragma unroll
-                    for (int t = 0; t < NT; t++) {
-                        const float sx = P.xs[(size_t)(tok0 + t) * P.nc + c];
-                        float2 *tp = terms + ((size_t)t * P.nc + c) * 16 + (4u * g + 2u * half);
-                        tp[0] = make_float2((float)r[t][0] * sx, ws0);
-                        tp[1] = make_float2((float)r[t][1] * sx, ws1);
-                    }
-                }
-                continue;
-            }
-            // In-register chain: the odd chunk's dots move to the even lanes.
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const int o0 = __shfl_xor(r[t][0], 32, kWave);
-                const int o1 = __shfl_xor(r[t][1], 32, kWave);
-                const float ow0 = __shfl_xor(ws0, 32, kWave), ow1 = __shfl_xor(ws1, 32, kWave);
-                const float sxe = P.xs[(size_t)(tok0 + t) * P.nc + ce];
-                if (sxe != 0.0f) {
-                    f[t][0] = fmaf((float)r[t][0] * sxe, ws0, f[t][0]);
-                    f[t][1] = fmaf((float)r[t][1] * sxe, ws1, f[t][1]);
-                }
-                if (has_odd) {
-                    const float sxo = P.xs[(size_t)(tok0 + t) * P.nc + ce + 1];
-                    if (sxo != 0.0f) {
-                        f[t][0] = fmaf((float)o0 * sxo, ow0, f[t][0]);
-                        f[t][1] = fmaf((float)o1 * sxo, ow1, f[t][1]);
-                    }
-                }
-            }
+            const int c = chunk_of(ib + u);
+            if (ib + u < iters && c < cw1) process(fr[u], c);
         }
     }
 
-    if (P.nseg == 1) {
-        if (k == 0 && par == 0) {
+    if (!P.exact) {
+        // Fast epilogue: add the lane groups' partial chains (fixed butterfly order, so the
+        // result is deterministic), then the waves' partials in wave order.
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                float v = f[t][i];
+                if (smode) v += __int_as_float(dpp_ror8(__float_as_int(v)));  // lane ^ 8
+                v += __shfl_xor(v, 16, kWave);
+                v += __shfl_xor(v, 32, kWave);
+                f[t][i] = v;
+            }
+        float *part = lds;  // [nseg][NT][RB]
+        if (smode ? lane < 8 : lane < 16) {
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                float *o = P.out + (size_t)(tok0 + t) * P.out_stride;
-                if (row0 < P.rows) o[row0] = f[t][0];
-                if (row0 + 1 < P.rows) o[row0 + 1] = f[t][1];
+                part[((size_t)wave * NT + t) * RB + rloc] = f[t][0];
+                part[((size_t)wave * NT + t) * RB + rloc + 1] = f[t][1];
             }
+        }
+        __syncthreads();
+        const int nrows_blk = (is_tail && !smode) ? 16 : RB;
+        const int first_stripe = smode ? rb : (is_tail ? 2 * P.np : 2 * rb);
+        for (int idx = (int)threadIdx.x; idx < NT * RB; idx += (int)blockDim.x) {
+            const int t = idx / RB, rl = idx % RB;
+            if (rl >= nrows_blk) continue;
+            const int st = first_stripe + rl / 16;
+            const int row = st * 16 + rl % 16;
+            if (row >= P.rows || st < P.s0 || st >= P.s1) continue;
+            float acc = part[(size_t)t * RB + rl];
+            for (int w = 1; w < P.nseg; w++) acc += part[((size_t)w * NT + t) * RB + rl];
+            P.out[(size_t)(tok0 + t) * P.out_stride + row] = acc;
         }
         return;
     }
-    if (!P.lds_terms) {
-        // Ordered partial sums (used when the per-chunk terms do not fit in LDS).
-        if (k == 0 && par == 0) {
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                lds[((size_t)seg * NT + t) * 16 + 4u * g + 2u * half] = f[t][0];
-                lds[((size_t)seg * NT + t) * 16 + 4u * g + 2u * half + 1] = f[t][1];
-            }
-        }
-    }
     __syncthreads();
-    if (seg != 0 || (int)lane >= 16 * NT) return;
-    const int t = (int)lane / 16, rl = (int)lane % 16;
-    const int row = s * 16 + rl;
-    float acc = 0.0f;
-    if (P.lds_terms) {
-        const float *xs = P.xs + (size_t)(tok0 + t) * P.nc;
-        const float2 *tp = terms + (size_t)t * P.nc * 16 + rl;
-        for (int c = 0; c < P.nc; c++) {
-            const float2 v = tp[(size_t)c * 16];
-            if (xs[c] != 0.0f) acc = fmaf(v.x, v.y, acc);
+    if (P.dbg & 1) return;
+    const int nrows_blk = (is_tail && !smode) ? 16 : RB;
+    const int first_stripe = smode ? rb : (is_tail ? 2 * P.np : 2 * rb);
+    // One thread per (token, row of the block) replays the chain; LDS reads are batched
+    // 16 chunks at a time so their latency overlaps.
+    for (int idx = (int)threadIdx.x; idx < NT * RB; idx += (int)blockDim.x) {
+        const int t = idx / RB, rl = idx % RB;
+        if (rl >= nrows_blk) continue;
+        const int st = first_stripe + rl / 16;
+        const int row = st * 16 + rl % 16;
+        if (row >= P.rows || st < P.s0 || st >= P.s1) continue;
+        const float2 *tp = terms + (size_t)t * P.nc * RB + rl;
+        float acc = 0.0f;
+        int c = 0;
+        for (; c + 16 <= P.nc; c += 16) {
+            float2 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = tp[(size_t)(c + u) * RB];
+#pragma unroll
+            for (int u = 0; u < 16; u++) acc = fmaf(v[u].x, v[u].y, acc);
         }
-    } else {
-        acc = lds[(size_t)t * 16 + rl];
-        for (int sg = 1; sg < P.nseg; sg++) acc += lds[((size_t)sg * NT + t) * 16 + rl];
+        for (; c < P.nc; c++) {
+            const float2 v = tp[(size_t)c * RB];
+            acc = fmaf(v.x, v.y, acc);
+        }
+        P.out[(size_t)(tok0 + t) * P.out_stride + row] = acc;
     }
-    if (row < P.rows) P.out[(size_t)(tok0 + t) * P.out_stride + row] = acc;
 }
 
 GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1) {
     GemvPlan p;
-    p.s_lo = s0;
-    p.nstripes = s1 - s0;
-    const int step = m->fmt == K2T_FMT_NF ? std::max(m->sgc, 2) : 2;  // even, scale-group aligned
-    const int nunits = (m->nc + step - 1) / step;
-    int nseg = 1;
-    if (ctx->max_segments != 1 && p.nstripes > 0) {
-        const int target = ctx->num_cus * 8;  // waves that keep every CU streaming
-        nseg = (target + p.nstripes - 1) / p.nstripes;
-        const int cap = ctx->max_segments > 1 ? std::min(ctx->max_segments, 16) : 16;
-        nseg = std::max(1, std::min({nseg, cap, nunits}));
+    const int npairs = std::min(m->pairs + m->has_tail, (s1 + 1) / 2) - s0 / 2;
+    // Fewer pair blocks than CUs: give each stripe its own workgroup so every CU streams.
+    p.stripe_mode = npairs < ctx->num_cus ? 1 : 0;
+    if (p.stripe_mode) {
+        p.rb_lo = s0;
+        p.rb_hi = s1;
+    } else {
+        p.rb_lo = s0 / 2;
+        p.rb_hi = s0 / 2 + npairs;
     }
-    const int ups = (nunits + nseg - 1) / nseg;
-    p.cps = ups * step;
-    p.nseg = (m->nc + p.cps - 1) / p.cps;
+    const int nrb = std::max(p.rb_hi - p.rb_lo, 1);
+    const int G = p.stripe_mode ? 8 : 4;  // lane groups per wave
+    const int step = m->fmt == K2T_FMT_NF ? m->sgc : 1;  // keep NF scale groups whole
+    // Short-lived waves that each fetch all their records in one batch stream best
+    // (~14 waves per CU, <= 2 records per lane group).  Shrink the per-wave chunk count
+    // when the matrix has too few row blocks to reach that many waves.
+    const int target = ctx->num_cus * 14;
+    int cps = 2 * G;
+    while (cps > step && (long)nrb * ((m->nc + cps - 1) / cps) < target) cps -= step;
+    cps = std::max({cps, step, (m->nc + 15) / 16});  // at most 16 waves per workgroup
+    if (ctx->max_segments > 0) cps = std::max(cps, (m->nc + ctx->max_segments - 1) / ctx->max_segments);
+    cps = (cps + step - 1) / step * step;
+    p.cps = cps;
+    p.nseg = (m->nc + cps - 1) / cps;
     return p;
 }
 
@@ -336,7 +390,7 @@ void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *
     if (dots) ctx->max_segments = 1;
     GemvPlan plan = plan_gemv(ctx, m, s0, s1);
     ctx->max_segments = saved;
-    if (plan.nstripes <= 0 || ntok <= 0) return;
+    if (plan.rb_hi <= plan.rb_lo || ntok <= 0) return;
     GemvParams P{};
     P.pair = m->pair;
     P.tail = m->tail;
@@ -351,8 +405,10 @@ void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *
     P.K = m->cols;
     P.nc = m->nc;
     P.np = m->pairs;
-    P.s_lo = plan.s_lo;
-    P.nstripes = plan.nstripes;
+    P.s0 = s0;
+    P.s1 = s1;
+    P.rb_lo = plan.rb_lo;
+    P.stripe_mode = plan.stripe_mode;
     P.nseg = plan.nseg;
     P.cps = plan.cps;
     P.sgc = m->sgc;
@@ -360,27 +416,34 @@ void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *
     P.cb1 = m->cb[1];
     P.cb2 = m->cb[2];
     P.cb3 = m->cb[3];
-    const int groups4 = ntok / 4, rem = ntok % 4;
+    // Tokens per weight pass: 4, fewer when the staged terms would not fit in 64 KB of LDS.
+    const size_t per_tok = ctx->exact ? (size_t)m->nc * (plan.stripe_mode ? 16 : 32) * sizeof(float2)
+                                      : (size_t)plan.nseg * 32 * sizeof(float);
+    const int G = (int)std::max<size_t>(1, std::min<size_t>(4, (64 * 1024) / per_tok));
+    const int groups = ntok / G, rem = ntok % G;
     const dim3 block(64 * plan.nseg);
-    auto lds_for = [&](int nt, GemvParams &Q) -> size_t {
-        if (plan.nseg == 1) return 0;
-        const size_t exact = (size_t)nt * m->nc * 16 * sizeof(float2);
-        Q.lds_terms = exact <= 64 * 1024 ? 1 : 0;
-        return Q.lds_terms ? exact : (size_t)plan.nseg * nt * 16 * sizeof(float);
-    };
-    if (groups4 > 0) {
+    P.lds_terms = 1;
+    P.exact = ctx->exact;
+    {
+        static int dbg = -1;
+        if (dbg < 0) {
+            const char *e = getenv("K2T_GEMV_DEBUG");
+            dbg = e ? atoi(e) : 0;
+        }
+        P.dbg = dbg;
+    }
+    if (groups > 0) {
         GemvParams Q = P;
         Q.tok_base = 0;
-        const size_t lds = lds_for(4, Q);
-        launch_fmt<false>(m, 4, dim3(plan.nstripes, groups4), block, lds, ctx->stream, Q);
+        if (dots && G == 1) launch_fmt<true>(m, 1, dim3(plan.rb_hi - plan.rb_lo, groups), block, per_tok, ctx->stream, Q);
+        else launch_fmt<false>(m, G, dim3(plan.rb_hi - plan.rb_lo, groups), block, (size_t)G * per_tok, ctx->stream, Q);
         hip_check(hipGetLastError(), "gemv launch");
     }
     if (rem > 0) {
         GemvParams Q = P;
-        Q.tok_base = groups4 * 4;
-        const size_t lds = lds_for(rem, Q);
-        if (dots) launch_fmt<true>(m, rem, dim3(plan.nstripes, 1), block, lds, ctx->stream, Q);
-        else launch_fmt<false>(m, rem, dim3(plan.nstripes, 1), block, lds, ctx->stream, Q);
+        Q.tok_base = groups * G;
+        if (dots) launch_fmt<true>(m, rem, dim3(plan.rb_hi - plan.rb_lo, 1), block, rem * per_tok, ctx->stream, Q);
+        else launch_fmt<false>(m, rem, dim3(plan.rb_hi - plan.rb_lo, 1), block, rem * per_tok, ctx->stream, Q);
         hip_check(hipGetLastError(), "gemv launch");
     }
 }

@@ -9,7 +9,8 @@
 struct k2t_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
-    int max_segments = 0;  // split-K policy: 0 auto, 1 off, n cap
+    int max_segments = 0;  // cap on waves (K segments) per GEMV workgroup; 0 = automatic
+    int exact = 0;         // 1: bit-exact fmaf-chain epilogue
     int num_cus = 256;
     // small device scratch (debug entry points): grown on demand
     float *scratch = nullptr;
@@ -47,8 +48,9 @@ void hip_check(hipError_t e, const char *what);
 void ensure_scratch(k2t_ctx *ctx, size_t floats);
 
 struct GemvPlan {
-    int s_lo, nstripes;  // stripe range
-    int nseg, cps;       // K segments (waves per workgroup) and chunks per segment
+    int stripe_mode;   // 1: one workgroup per stripe, 0: per stripe pair
+    int rb_lo, rb_hi;  // row blocks: pairs (then the odd tail stripe), or stripes
+    int nseg, cps;     // waves per workgroup (K segments) and chunks per wave
 };
 GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1);
 

@@ -47,6 +47,7 @@ SIGNATURES = {
     "k2t_ctx_set_stream": (I32, [VP, VP]),
     "k2t_ctx_sync": (I32, [VP]),
     "k2t_ctx_set_splitk": (I32, [VP, I32]),
+    "k2t_ctx_set_exact": (I32, [VP, I32]),
     "k2t_malloc": (I32, [VP, SZ, C.POINTER(VP)]),
     "k2t_free": (I32, [VP, VP]),
     "k2t_memcpy_h2d": (I32, [VP, VP, VP, SZ]),
@@ -119,6 +120,9 @@ class Ctx:
 
     def set_splitk(self, n):
         check(lib().k2t_ctx_set_splitk(self.h, int(n)))
+
+    def set_exact(self, on):
+        check(lib().k2t_ctx_set_exact(self.h, int(bool(on))))
 
     def sync(self):
         check(lib().k2t_ctx_sync(self.h))

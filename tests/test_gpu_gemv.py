@@ -2,10 +2,10 @@
 
 Bar: int8 q / scales / sums and every per-(row, chunk) integer dot bit-exact against
 the oracle; fp32 GEMV outputs bit-exact (same fmaf order as the reference's NEON
-epilogue) both with split-K off and with the automatic K split (per-chunk terms staged
-in LDS).  Only the ordered-partial-sum fallback, used when a 4-token tile's terms do
-not fit in LDS, is held to the reference's batch tolerance 1e-4 * (1 + |y|)
-(simd_lut.rs:8936).
+epilogue) in exact mode for every K split, because the per-chunk terms are staged in
+LDS and the chain is replayed in chunk order; the default fast epilogue within
+1e-5 * (1 + |y|) (the reference's own batch tolerance is 1e-4 * (1 + |y|),
+simd_lut.rs:8936).
 """
 import numpy as np
 import pytest
@@ -21,12 +21,21 @@ def _t(a, dtype=None):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-def _run_gemv(ctx, m, xq, xs, xsum, rows, ntok=1, s0=0, s1=-1):
+def _run_gemv(ctx, m, xq, xs, xsum, rows, ntok=1, s0=0, s1=-1, exact=True):
     import torch
     out = torch.full((ntok, rows), float("nan"), dtype=torch.float32, device="cuda")
-    ctx.gemv(m, _t(xq), _t(xs), _t(xsum), out, ntok=ntok, s0=s0, s1=s1, out_stride=rows)
-    ctx.sync()
+    ctx.set_exact(exact)
+    try:
+        ctx.gemv(m, _t(xq), _t(xs), _t(xsum), out, ntok=ntok, s0=s0, s1=s1, out_stride=rows)
+        ctx.sync()
+    finally:
+        ctx.set_exact(False)
     return out.cpu().numpy()
+
+
+def _close(out, ref, tol=1e-5):
+    """Fast epilogue: per-segment chains summed in a fixed order (a few ulp)."""
+    return np.all(np.abs(out - ref) <= tol * (1 + np.abs(ref)))
 
 
 @pytest.mark.parametrize("K,ntok,norm", [(576, 1, False), (2048, 1, True), (14336, 2, True), (8192, 3, False)])
@@ -80,14 +89,15 @@ def test_nibble4_gemv_exact(gpu_ctx, hp, rows, cols):
     d = torch.zeros((rows, cols // 64), dtype=torch.int32, device="cuda")
     gpu_ctx.gemv_chunk_dots(m, _t(xq[0]), _t(xsum[0]), d)
     assert np.array_equal(d.cpu().numpy(), dots), "integer chunk dots differ"
+    out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), "exact epilogue not bit-exact"
     gpu_ctx.set_splitk(1)
     try:
-        out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
+        out1 = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
     finally:
         gpu_ctx.set_splitk(0)
-    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), "fp32 epilogue not bit-exact"
-    out2 = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
-    assert np.array_equal(out2.view(np.uint32), ref.view(np.uint32)), "split-K result not bit-exact"
+    assert np.array_equal(out1.view(np.uint32), ref.view(np.uint32)), "single-segment result not bit-exact"
+    assert _close(_run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, exact=False)[0], ref)
 
 
 def test_nibble4_config1_quantized(gpu_ctx):
@@ -98,13 +108,10 @@ def test_nibble4_config1_quantized(gpu_ctx):
     x = activation(rng, cols, n_outliers=4, outlier_scale=20.0)
     xq, xs, xsum = O.populate_fwht(x)
     m = gpu_ctx.upload_nibble4(rows, cols, 0, pair, tail)
-    gpu_ctx.set_splitk(1)
-    try:
-        out = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows)[0]
-    finally:
-        gpu_ctx.set_splitk(0)
+    out = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows)[0]
     ref = O.nibble4_gemv(pair, tail, rows, cols, 0, xq, xs, xsum)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    assert _close(_run_gemv(gpu_ctx, m, xq, xs, xsum, rows, exact=False)[0], ref)
     # and the quantized product approximates the fp32 one (W x)
     y = W.astype(np.float64) @ x.astype(np.float64)
     cos = float(np.dot(out, y) / (np.linalg.norm(out) * np.linalg.norm(y)))
@@ -126,14 +133,9 @@ def test_nf4_gemv_exact(gpu_ctx, sgc, rows, cols):
     d = torch.zeros((rows, cols // 64), dtype=torch.int32, device="cuda")
     gpu_ctx.gemv_chunk_dots(m, _t(xq[0]), None, d)
     assert np.array_equal(d.cpu().numpy(), dots)
-    gpu_ctx.set_splitk(1)
-    try:
-        out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
-    finally:
-        gpu_ctx.set_splitk(0)
+    out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
-    out2 = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
-    assert np.array_equal(out2.view(np.uint32), ref.view(np.uint32)), "split-K result not bit-exact"
+    assert _close(_run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, exact=False)[0], ref)
 
 
 def test_nf4_quantized_model_matrix(gpu_ctx):
@@ -146,6 +148,7 @@ def test_nf4_quantized_model_matrix(gpu_ctx):
     out = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows)[0]
     ref = O.nf_gemv(pair, tail, rows, cols, 4, 2, cb, xq, xs)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    assert _close(_run_gemv(gpu_ctx, m, xq, xs, xsum, rows, exact=False)[0], ref)
 
 
 @pytest.mark.parametrize("fmt", ["b5", "nf4"])
@@ -161,16 +164,16 @@ def test_batch_matches_single(gpu_ctx, fmt):
         cb = np.array([-127, -96, -75, -58, -44, -31, -18, -6, 6, 18, 31, 44, 58, 75, 96, 127], np.int8)
         m = gpu_ctx.upload_nf(rows, cols, 4, 2, cb, pair, tail)
     xq, xs, xsum = acts(rng, cols, ntok)
-    gpu_ctx.set_splitk(1)
-    try:
-        batch = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows, ntok=ntok)
-        for t in range(ntok):
-            one = _run_gemv(gpu_ctx, m, xq[t], xs[t], xsum[t], rows)[0]
-            assert np.array_equal(batch[t].view(np.uint32), one.view(np.uint32)), f"token {t}"
-    finally:
-        gpu_ctx.set_splitk(0)
-    batch2 = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows, ntok=ntok)
-    assert np.array_equal(batch2.view(np.uint32), batch.view(np.uint32))
+    batch = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows, ntok=ntok)
+    for t in range(ntok):
+        one = _run_gemv(gpu_ctx, m, xq[t], xs[t], xsum[t], rows)[0]
+        assert np.array_equal(batch[t].view(np.uint32), one.view(np.uint32)), f"token {t}"
+    # fast epilogue: batch == per token bit for bit (same segment plan), and near exact
+    fb = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows, ntok=ntok, exact=False)
+    for t in range(ntok):
+        one = _run_gemv(gpu_ctx, m, xq[t], xs[t], xsum[t], rows, exact=False)[0]
+        assert np.array_equal(fb[t].view(np.uint32), one.view(np.uint32)), f"token {t}"
+    assert _close(fb, batch)
 
 
 def test_stripe_subrange(gpu_ctx):
@@ -182,10 +185,14 @@ def test_stripe_subrange(gpu_ctx):
     xq, xs, xsum = acts(rng, cols, 1)
     ref = O.nibble4_gemv(pair, tail, rows, cols, hp, xq[0], xs[0], xsum[0])
     for s0, s1 in [(1, 12), (3, 13), (0, 1), (12, 13), (5, 6)]:
-        out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, s0=s0, s1=s1)[0]
-        lo, hi = s0 * 16, min(s1 * 16, rows)
-        assert np.all(np.isnan(out[:lo])) and np.all(np.isnan(out[hi:]))
-        assert np.array_equal(out[lo:hi].view(np.uint32), ref[lo:hi].view(np.uint32))
+        for exact in (True, False):
+            out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, s0=s0, s1=s1, exact=exact)[0]
+            lo, hi = s0 * 16, min(s1 * 16, rows)
+            assert np.all(np.isnan(out[:lo])) and np.all(np.isnan(out[hi:]))
+            if exact:
+                assert np.array_equal(out[lo:hi].view(np.uint32), ref[lo:hi].view(np.uint32))
+            else:
+                assert _close(out[lo:hi], ref[lo:hi])
 
 
 @pytest.mark.parametrize("rows,cols,hp", [(14336, 4096, 2), (4096, 14336, 2)])
@@ -202,10 +209,12 @@ def test_large_b6_dots_and_outputs(gpu_ctx, rows, cols, hp):
     assert np.array_equal(d.cpu().numpy(), dots)
     out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    assert _close(_run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, exact=False)[0], ref)
 
 
-def test_batch4_large_k_partial_sum_fallback(gpu_ctx):
-    """4 tokens x K=14336: per-chunk terms exceed LDS, ordered partial sums are used."""
+def test_batch4_large_k(gpu_ctx):
+    """4 tokens x K=14336: the kernel takes fewer tokens per weight pass so the staged
+    per-chunk terms fit in LDS; results stay bit-exact."""
     rng = np.random.default_rng(21)
     rows, cols, ntok = 256, 14336, 4
     _, _, pair, tail = random_nf_streams(rng, rows, cols, 2)
@@ -213,6 +222,8 @@ def test_batch4_large_k_partial_sum_fallback(gpu_ctx):
     m = gpu_ctx.upload_nf(rows, cols, 4, 2, cb, pair, tail)
     xq, xs, xsum = acts(rng, cols, ntok)
     out = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows, ntok=ntok)
+    fast = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows, ntok=ntok, exact=False)
     for t in range(ntok):
         ref = O.nf_gemv(pair, tail, rows, cols, 4, 2, cb, xq[t], xs[t])
-        assert np.all(np.abs(out[t] - ref) <= 1e-4 * (1 + np.abs(ref)))
+        assert np.array_equal(out[t].view(np.uint32), ref.view(np.uint32))
+        assert _close(fast[t], ref)
