@@ -186,6 +186,53 @@ int32_t k2t_compile_nf(const float *W, int32_t rows, int32_t cols, int32_t bits,
  * No reference counterpart (the reference loads checkpoints). */
 int32_t k2t_synth_normal(uint64_t seed, float stddev, float *out, size_t n, int32_t threads);
 
+/* ---- decode engine ------------------------------------------------------ */
+
+/* Llama-family decoder shape (LlamaConfig, real_llm.rs:100-403).  q_dim must equal
+ * hidden (the megakernel shape, real_llm.rs:6412-6452); head_dim 64 or 128. */
+typedef struct k2t_model_config {
+    int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate, vocab, max_seq;
+    float rms_eps;
+    float rope_theta; /* effective theta (real_llm.rs:415-422) */
+} k2t_model_config;
+
+typedef struct k2t_model k2t_model;
+
+/* Allocates the int8 Hadamard KV cache (QuantizedKvCache, real_llm.rs:1209-1412, full
+ * max_seq capacity), the RoPE table (real_llm.rs:9212-9232) and workspaces for up to
+ * max_batch tokens per forward pass. */
+int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_batch, k2t_model **out);
+void k2t_model_destroy(k2t_model *m);
+/* Layer weights (borrowed matrices of the same context; gate_up must be row-interleaved
+ * into [gate64(ic), up64(ic)] blocks as after repack_sdot, real_llm.rs:3657-3702) and
+ * RMSNorm weights / optional qkv bias (host arrays, copied). */
+int32_t k2t_model_set_layer(k2t_model *m, int32_t layer, const k2t_mat *qkv, const k2t_mat *o,
+                            const k2t_mat *gate_up, const k2t_mat *down, const float *in_norm,
+                            const float *post_norm, const float *qkv_bias);
+/* Tied quantized lm_head (also the embedding table, embed_token_into real_llm.rs:8063-8097)
+ * and the final norm. */
+int32_t k2t_model_set_head(k2t_model *m, const k2t_mat *lm_head, const float *final_norm);
+/* 1 (default): capture the decode step once and replay it as a HIP graph. */
+int32_t k2t_model_set_graph(k2t_model *m, int32_t enable);
+/* GEMV epilogue of this model's steps (see k2t_ctx_set_exact); default 1 = exact. */
+int32_t k2t_model_set_exact(k2t_model *m, int32_t exact);
+/* reset_context: position back to 0. */
+int32_t k2t_model_reset(k2t_model *m);
+int32_t k2t_model_position(const k2t_model *m, int32_t *pos);
+/* forward_token (real_llm.rs:6455, megakernel 6794-7403): one decode step; logits of
+ * `token` are copied to logits_host (vocab floats) when it is not NULL. */
+int32_t k2t_model_decode(k2t_model *m, int32_t token, float *logits_host);
+/* forward_prompt (real_llm.rs:7407-7446): the prompt in batches of max_batch tokens,
+ * GEMVs reading each weight record once per 4 tokens; logits of the last token. */
+int32_t k2t_model_prefill(k2t_model *m, const int32_t *tokens, int32_t n, float *logits_host);
+/* generate_greedy's decode loop (real_llm.rs:7895-7907): feeds first_token, then
+ * n_steps decode steps whose next token is the argmax of the logits, chosen on the
+ * device.  tokens_out (nullable) receives the n_steps argmax tokens. */
+int32_t k2t_model_generate(k2t_model *m, int32_t first_token, int32_t n_steps, int32_t *tokens_out);
+/* Device pointer of the last logits (valid after a step; read after k2t_model_sync). */
+int32_t k2t_model_logits(k2t_model *m, const float **d_logits);
+int32_t k2t_model_sync(k2t_model *m);
+
 #ifdef __cplusplus
 }
 #endif

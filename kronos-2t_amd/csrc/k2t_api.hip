@@ -15,6 +15,8 @@ namespace k2t {
 
 static thread_local std::string g_last_error;
 
+void set_last_error(const std::string &msg) { g_last_error = msg; }
+
 void hip_check(hipError_t e, const char *what) {
     if (e != hipSuccess) throw Error(K2T_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }

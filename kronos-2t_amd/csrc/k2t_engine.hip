@@ -1,0 +1,490 @@
+// Decode engine: the GPU counterpart of RealLlamaEngine's SDOT paths
+// (forward_token_sdot_megakernel real_llm.rs:6794-7403, forward_prompt 7407-7446,
+// generate_greedy 7880-7915).  The host only enqueues kernels; the token position
+// and the greedy token live in device memory, so a decode step is captured once into
+// a HIP graph and replayed.
+#include <float.h>
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../include/k2t_hip.h"
+#include "k2t_internal.h"
+
+namespace k2t {
+void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float eps, int K, int ntok, int8_t *q,
+                        float *s, int32_t *sums);
+void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *rope, const int *pos_dev, int nq,
+                     int nkv, int hd, int ntok, int layer, int cap, int8_t *kq, int8_t *vq, float *ks, float *vs);
+void launch_attention(hipStream_t st, const float *q, int q_stride, const int8_t *kq, const int8_t *vq, const float *ks,
+                      const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd, int cap, float attn_scale,
+                      int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum);
+int attn_max_splits(int max_seq);
+void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums);
+void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok, float *out);
+void launch_advance_pos(hipStream_t st, int *pos, int n);
+void launch_argmax(hipStream_t st, const float *x, int n, int *out_idx);
+void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum, int ntok,
+                    float *out, size_t out_stride, bool accumulate);
+
+// Greedy pick (argmax_scalar, real_llm.rs:9914-9924): largest value, lowest index on ties,
+// NaN never wins.  One workgroup.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ x, int n, int *__restrict__ out) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        if (v > best) {  // strided scan keeps the lowest index among equals per thread
+            best = v;
+            idx = i;
+        }
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(best, m, 64);
+        const int oi = __shfl_xor(idx, m, 64);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = best;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv[0];
+        int bix = bi[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+            if (bv[w] > b || (bv[w] == b && bi[w] < bix)) {
+                b = bv[w];
+                bix = bi[w];
+            }
+        out[0] = bix == 0x7fffffff ? 0 : bix;
+    }
+}
+
+void launch_argmax(hipStream_t st, const float *x, int n, int *out_idx) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, x, n, out_idx);
+    hip_check(hipGetLastError(), "argmax launch");
+}
+
+}  // namespace k2t
+
+using namespace k2t;
+
+struct k2t_model {
+    k2t_ctx *ctx = nullptr;
+    k2t_model_config cfg{};
+    hipStream_t stream = nullptr;
+    struct Layer {
+        const k2t_mat *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
+        float *in_norm = nullptr, *post_norm = nullptr, *bias = nullptr;
+    };
+    std::vector<Layer> layers;
+    const k2t_mat *head = nullptr;
+    float *final_norm = nullptr;
+    float *rope = nullptr;  // [max_seq][hd] = cos | sin halves
+    int8_t *kq = nullptr, *vq = nullptr;
+    float *ks = nullptr, *vs = nullptr;
+    int *pos_dev = nullptr;  // [0] position, [1..] tokens
+    int *tokens = nullptr;
+    int max_batch = 0;
+    float *hidden = nullptr, *qkv = nullptr, *gu = nullptr, *logits = nullptr, *attn_part = nullptr;
+    int8_t *xq = nullptr;
+    float *xs = nullptr;
+    int32_t *xsum = nullptr;
+    int pos = 0;
+    bool use_graph = true;
+    int exact = 1;  // GEMV epilogue mode used by this model's steps
+    hipGraphExec_t graph = nullptr;
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+void *dalloc(k2t_model *m, size_t bytes) {
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        throw Error(K2T_E_NOMEM, std::string("hipMalloc failed: ") + hipGetErrorString(e));
+    }
+    m->allocs.push_back(p);
+    return p;
+}
+
+void arg(bool ok, const char *msg) {
+    if (!ok) throw Error(K2T_E_ARG, msg);
+}
+
+template <typename F>
+int32_t mguard(F &&fn) {
+    try {
+        fn();
+        return K2T_OK;
+    } catch (const Error &e) {
+        set_last_error(e.what());
+        return e.code;
+    } catch (const std::exception &e) {
+        set_last_error(e.what());
+        return K2T_E_INTERNAL;
+    } catch (...) {
+        set_last_error("unknown error");
+        return K2T_E_INTERNAL;
+    }
+}
+
+// real_llm.rs:9212-9232 build_rope_table: inv_freq in f64 -> f32, angle pos*freq in f32.
+std::vector<float> rope_table(int hd, float theta, int max_seq) {
+    const int half = hd / 2;
+    std::vector<float> inv(half), t((size_t)max_seq * hd);
+    for (int i = 0; i < half; i++) inv[i] = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)hd));
+    for (int p = 0; p < max_seq; p++)
+        for (int i = 0; i < half; i++) {
+            const float a = (float)p * inv[i];
+            t[(size_t)p * hd + i] = cosf(a);
+            t[(size_t)p * hd + half + i] = sinf(a);
+        }
+    return t;
+}
+
+void ensure_batch(k2t_model *m, int n) {
+    if (n <= m->max_batch) return;
+    throw Error(K2T_E_ARG, "token batch larger than the model's max batch");
+}
+
+// One forward pass over `ntok` tokens already in m->tokens, positions pos..pos+ntok-1.
+// Logits (of the last token) go to m->logits; the device position advances by ntok.
+void forward(k2t_model *m, int ntok, bool with_logits) {
+    const k2t_model_config &c = m->cfg;
+    hipStream_t st = m->stream;
+    k2t_ctx *ctx = m->ctx;
+    const int hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, d = c.hidden, inter = c.intermediate;
+    const float attn_scale = 1.0f / sqrtf((float)hd);
+    const int nsplit = attn_max_splits(c.max_seq);
+    launch_embed(st, m->head, m->tokens, ntok, m->hidden);
+    for (int l = 0; l < c.n_layers; l++) {
+        const auto &L = m->layers[l];
+        launch_rmsnorm_act(st, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
+        launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false);
+        launch_qkv_post(st, m->qkv, L.bias, m->rope, m->pos_dev, nq, nkv, hd, ntok, l, c.max_seq, m->kq, m->vq, m->ks,
+                        m->vs);
+        launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, m->pos_dev, l, nq, nkv, hd,
+                         c.max_seq, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum);
+        launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
+        launch_rmsnorm_act(st, m->hidden, L.post_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
+        launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false);
+        launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum);
+        launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
+    }
+    if (with_logits) {
+        const float *last = m->hidden + (size_t)(ntok - 1) * d;
+        launch_rmsnorm_act(st, last, m->final_norm, c.rms_eps, d, 1, m->xq, m->xs, m->xsum);
+        launch_gemv_ex(ctx, m->head, m->xq, m->xs, m->xsum, 1, m->logits, c.vocab, false);
+    }
+    launch_advance_pos(st, m->pos_dev, ntok);
+}
+
+void check_ready(k2t_model *m) {
+    for (size_t l = 0; l < m->layers.size(); l++)
+        arg(m->layers[l].qkv && m->layers[l].o && m->layers[l].gu && m->layers[l].down, "a layer is not set");
+    arg(m->head != nullptr, "lm_head is not set");
+}
+
+// The model's GEMVs run on its own stream with its epilogue mode; the context's settings
+// are restored afterwards.
+struct StreamSwap {
+    k2t_ctx *ctx;
+    hipStream_t saved;
+    int saved_exact;
+    StreamSwap(k2t_model *m) : ctx(m->ctx), saved(m->ctx->stream), saved_exact(m->ctx->exact) {
+        ctx->stream = m->stream;
+        ctx->exact = m->exact;
+    }
+    ~StreamSwap() {
+        ctx->stream = saved;
+        ctx->exact = saved_exact;
+    }
+};
+
+void decode_step(k2t_model *m) {
+    StreamSwap sw(m);
+    if (!m->use_graph) {
+        forward(m, 1, true);
+        return;
+    }
+    if (!m->graph) {
+        hipGraph_t g = nullptr;
+        hip_check(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal), "begin capture");
+        try {
+            forward(m, 1, true);
+        } catch (...) {
+            (void)hipStreamEndCapture(m->stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        hip_check(hipStreamEndCapture(m->stream, &g), "end capture");
+        hipError_t e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        hip_check(e, "graph instantiate");
+    }
+    hip_check(hipGraphLaunch(m->graph, m->stream), "graph launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_batch, k2t_model **out) {
+    return mguard([&] {
+        arg(ctx && cfg && out, "NULL argument");
+        *out = nullptr;
+        const k2t_model_config &c = *cfg;
+        arg(c.n_layers > 0 && c.hidden > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.intermediate > 0 && c.vocab > 0,
+            "non-positive model dimension");
+        arg(c.head_dim == 64 || c.head_dim == 128, "head_dim must be 64 or 128 (Hadamard KV cache)");
+        arg(c.n_heads % c.n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
+        arg(c.n_heads * c.head_dim == c.hidden, "q_dim must equal hidden (megakernel shape)");
+        arg(c.hidden % 64 == 0 && c.intermediate % 64 == 0, "hidden and intermediate must be multiples of 64");
+        arg(c.max_seq > 0 && c.max_seq <= 1 << 20, "max_seq out of range");
+        arg(max_batch >= 1 && max_batch <= 4096, "max_batch out of range");
+        hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+        k2t_model *m = new k2t_model();
+        try {
+            m->ctx = ctx;
+            m->cfg = c;
+            m->max_batch = max_batch;
+            m->layers.resize(c.n_layers);
+            hip_check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "stream create");
+            const size_t slots = (size_t)c.n_layers * c.n_kv_heads * c.max_seq;
+            m->kq = (int8_t *)dalloc(m, slots * c.head_dim);
+            m->vq = (int8_t *)dalloc(m, slots * c.head_dim);
+            m->ks = (float *)dalloc(m, slots * sizeof(float));
+            m->vs = (float *)dalloc(m, slots * sizeof(float));
+            auto rt = rope_table(c.head_dim, c.rope_theta, c.max_seq);
+            m->rope = (float *)dalloc(m, rt.size() * sizeof(float));
+            hip_check(hipMemcpy(m->rope, rt.data(), rt.size() * sizeof(float), hipMemcpyHostToDevice), "rope upload");
+            m->pos_dev = (int *)dalloc(m, (size_t)(max_batch + 1) * sizeof(int));
+            m->tokens = m->pos_dev + 1;
+            hip_check(hipMemset(m->pos_dev, 0, (size_t)(max_batch + 1) * sizeof(int)), "pos clear");
+            const size_t qkv_w = (size_t)(c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
+            const size_t kmax = std::max(c.hidden, c.intermediate);
+            m->hidden = (float *)dalloc(m, (size_t)max_batch * c.hidden * sizeof(float));
+            m->qkv = (float *)dalloc(m, (size_t)max_batch * qkv_w * sizeof(float));
+            m->gu = (float *)dalloc(m, (size_t)max_batch * 2 * c.intermediate * sizeof(float));
+            m->logits = (float *)dalloc(m, (size_t)c.vocab * sizeof(float));
+            m->attn_part = (float *)dalloc(
+                m, (size_t)max_batch * c.n_heads * attn_max_splits(c.max_seq) * (2 + c.head_dim) * sizeof(float));
+            m->xq = (int8_t *)dalloc(m, (size_t)max_batch * kmax);
+            m->xs = (float *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(float));
+            m->xsum = (int32_t *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(int32_t));
+        } catch (...) {
+            k2t_model_destroy(m);
+            throw;
+        }
+        *out = m;
+    });
+}
+
+void k2t_model_destroy(k2t_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->ctx ? m->ctx->device : 0);
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    for (void *p : m->allocs) (void)hipFree(p);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+int32_t k2t_model_set_layer(k2t_model *m, int32_t layer, const k2t_mat *qkv, const k2t_mat *o,
+                            const k2t_mat *gate_up, const k2t_mat *down, const float *in_norm,
+                            const float *post_norm, const float *qkv_bias) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        arg(layer >= 0 && layer < m->cfg.n_layers, "layer out of range");
+        arg(qkv && o && gate_up && down && in_norm && post_norm, "NULL argument");
+        const k2t_model_config &c = m->cfg;
+        const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
+        arg(qkv->rows == qkv_rows && qkv->cols == c.hidden, "qkv shape mismatch");
+        arg(o->rows == c.hidden && o->cols == c.n_heads * c.head_dim, "o_proj shape mismatch");
+        arg(gate_up->rows == 2 * c.intermediate && gate_up->cols == c.hidden, "gate_up shape mismatch");
+        arg(down->rows == c.hidden && down->cols == c.intermediate, "down_proj shape mismatch");
+        for (const k2t_mat *x : {qkv, o, gate_up, down}) arg(x->ctx == m->ctx, "matrix of another context");
+        auto &L = m->layers[layer];
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        if (!L.in_norm) L.in_norm = (float *)dalloc(m, c.hidden * sizeof(float));
+        if (!L.post_norm) L.post_norm = (float *)dalloc(m, c.hidden * sizeof(float));
+        hip_check(hipMemcpy(L.in_norm, in_norm, c.hidden * sizeof(float), hipMemcpyHostToDevice), "norm upload");
+        hip_check(hipMemcpy(L.post_norm, post_norm, c.hidden * sizeof(float), hipMemcpyHostToDevice), "norm upload");
+        if (qkv_bias) {
+            if (!L.bias) L.bias = (float *)dalloc(m, (size_t)qkv_rows * sizeof(float));
+            hip_check(hipMemcpy(L.bias, qkv_bias, (size_t)qkv_rows * sizeof(float), hipMemcpyHostToDevice),
+                      "bias upload");
+        } else {
+            L.bias = nullptr;
+        }
+        L.qkv = qkv;
+        L.o = o;
+        L.gu = gate_up;
+        L.down = down;
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+    });
+}
+
+int32_t k2t_model_set_head(k2t_model *m, const k2t_mat *lm_head, const float *final_norm) {
+    return mguard([&] {
+        arg(m && lm_head && final_norm, "NULL argument");
+        arg(lm_head->rows == m->cfg.vocab && lm_head->cols == m->cfg.hidden, "lm_head shape mismatch");
+        arg(lm_head->ctx == m->ctx, "matrix of another context");
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        if (!m->final_norm) m->final_norm = (float *)dalloc(m, m->cfg.hidden * sizeof(float));
+        hip_check(hipMemcpy(m->final_norm, final_norm, m->cfg.hidden * sizeof(float), hipMemcpyHostToDevice),
+                  "norm upload");
+        m->head = lm_head;
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+    });
+}
+
+int32_t k2t_model_set_graph(k2t_model *m, int32_t enable) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        m->use_graph = enable != 0;
+    });
+}
+
+int32_t k2t_model_set_exact(k2t_model *m, int32_t exact) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        m->exact = exact ? 1 : 0;
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+    });
+}
+
+int32_t k2t_model_reset(k2t_model *m) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        hip_check(hipStreamSynchronize(m->stream), "sync");
+        hip_check(hipMemset(m->pos_dev, 0, sizeof(int)), "pos reset");
+        m->pos = 0;
+    });
+}
+
+int32_t k2t_model_position(const k2t_model *m, int32_t *pos) {
+    return mguard([&] {
+        arg(m && pos, "NULL argument");
+        *pos = m->pos;
+    });
+}
+
+int32_t k2t_model_decode(k2t_model *m, int32_t token, float *logits_host) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        check_ready(m);
+        arg(token >= 0 && token < m->cfg.vocab, "token out of range");
+        arg(m->pos < m->cfg.max_seq, "context full (max_seq reached)");
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        hip_check(hipMemcpyAsync(m->tokens, &token, sizeof(int), hipMemcpyHostToDevice, m->stream), "token upload");
+        decode_step(m);
+        m->pos += 1;
+        if (logits_host) {
+            hip_check(hipMemcpyAsync(logits_host, m->logits, (size_t)m->cfg.vocab * sizeof(float),
+                                     hipMemcpyDeviceToHost, m->stream),
+                      "logits download");
+            hip_check(hipStreamSynchronize(m->stream), "sync");
+        }
+    });
+}
+
+int32_t k2t_model_prefill(k2t_model *m, const int32_t *tokens, int32_t n, float *logits_host) {
+    return mguard([&] {
+        arg(m && tokens, "NULL argument");
+        check_ready(m);
+        arg(n >= 1, "empty prompt");
+        arg(m->pos + n <= m->cfg.max_seq, "prompt exceeds max_seq");
+        for (int i = 0; i < n; i++) arg(tokens[i] >= 0 && tokens[i] < m->cfg.vocab, "token out of range");
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        StreamSwap sw(m);
+        for (int i0 = 0; i0 < n; i0 += m->max_batch) {
+            const int nb = std::min(m->max_batch, n - i0);
+            hip_check(hipMemcpyAsync(m->tokens, tokens + i0, nb * sizeof(int), hipMemcpyHostToDevice, m->stream),
+                      "token upload");
+            forward(m, nb, i0 + nb == n);
+            // the token buffer is reused by the next chunk: wait for this one
+            hip_check(hipStreamSynchronize(m->stream), "sync");
+        }
+        m->pos += n;
+        if (logits_host) {
+            hip_check(hipMemcpyAsync(logits_host, m->logits, (size_t)m->cfg.vocab * sizeof(float),
+                                     hipMemcpyDeviceToHost, m->stream),
+                      "logits download");
+            hip_check(hipStreamSynchronize(m->stream), "sync");
+        }
+    });
+}
+
+int32_t k2t_model_generate(k2t_model *m, int32_t first_token, int32_t n_steps, int32_t *tokens_out) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        check_ready(m);
+        arg(n_steps >= 0, "n_steps < 0");
+        arg(first_token >= 0 && first_token < m->cfg.vocab, "token out of range");
+        arg(m->pos + n_steps <= m->cfg.max_seq, "generation exceeds max_seq");
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        hip_check(hipMemcpyAsync(m->tokens, &first_token, sizeof(int), hipMemcpyHostToDevice, m->stream),
+                  "token upload");
+        std::vector<int> host;
+        int *dev_out = nullptr;
+        if (tokens_out && n_steps > 0) dev_out = (int *)dalloc(m, (size_t)n_steps * sizeof(int));
+        for (int i = 0; i < n_steps; i++) {
+            decode_step(m);
+            // greedy: the next input token is argmax of these logits, written on the device
+            launch_argmax(m->stream, m->logits, m->cfg.vocab, m->tokens);
+            if (dev_out)
+                hip_check(hipMemcpyAsync(dev_out + i, m->tokens, sizeof(int), hipMemcpyDeviceToDevice, m->stream),
+                          "token copy");
+        }
+        m->pos += n_steps;
+        if (dev_out) {
+            hip_check(hipMemcpyAsync(tokens_out, dev_out, (size_t)n_steps * sizeof(int), hipMemcpyDeviceToHost,
+                                     m->stream),
+                      "tokens download");
+        }
+        hip_check(hipStreamSynchronize(m->stream), "sync");
+        if (dev_out) {
+            (void)hipFree(dev_out);
+            m->allocs.pop_back();
+        }
+    });
+}
+
+int32_t k2t_model_logits(k2t_model *m, const float **d_logits) {
+    return mguard([&] {
+        arg(m && d_logits, "NULL argument");
+        *d_logits = m->logits;
+    });
+}
+
+int32_t k2t_model_sync(k2t_model *m) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        hip_check(hipStreamSynchronize(m->stream), "sync");
+    });
+}
+
+}  // extern "C"

@@ -48,6 +48,7 @@ struct GemvParams {
     int lds_terms;  // per-chunk terms staged in LDS (always 1 in this build)
     int stripe_mode;  // 1: a workgroup owns one stripe (16 rows), 0: a stripe pair (32 rows)
     int exact;        // 1: replay the reference's fmaf chain from LDS-staged terms
+    int accum;        // 1: out = out + result (residual add, real_llm.rs:7185-7188)
     int dbg;
     uint32_t cb0, cb1, cb2, cb3;
 };
@@ -301,7 +302,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             if (row >= P.rows || st < P.s0 || st >= P.s1) continue;
             float acc = part[(size_t)t * RB + rl];
             for (int w = 1; w < P.nseg; w++) acc += part[((size_t)w * NT + t) * RB + rl];
-            P.out[(size_t)(tok0 + t) * P.out_stride + row] = acc;
+            float *o = P.out + (size_t)(tok0 + t) * P.out_stride + row;
+            *o = P.accum ? *o + acc : acc;
         }
         return;
     }
@@ -331,7 +333,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             const float2 v = tp[(size_t)c * RB];
             acc = fmaf(v.x, v.y, acc);
         }
-        P.out[(size_t)(tok0 + t) * P.out_stride + row] = acc;
+        float *o = P.out + (size_t)(tok0 + t) * P.out_stride + row;
+        *o = P.accum ? *o + acc : acc;
     }
 }
 
@@ -383,9 +386,24 @@ static void launch_fmt(const k2t_mat *m, int nt, dim3 grid, dim3 block, size_t l
     else launch_nt<0, 2, DOTS>(nt, grid, block, lds, st, P);
 }
 
+static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
+                             const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
+                             int32_t *dots, bool accum);
+
 void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                  const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
                  int32_t *dots) {
+    launch_gemv_impl(ctx, m, xq, xs, xsum, ntok, s0, s1, out, out_stride, dots, false);
+}
+
+void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum, int ntok,
+                    float *out, size_t out_stride, bool accumulate) {
+    launch_gemv_impl(ctx, m, xq, xs, xsum, ntok, 0, m->stripes, out, out_stride, nullptr, accumulate);
+}
+
+static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
+                             const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
+                             int32_t *dots, bool accum) {
     const int saved = ctx->max_segments;
     if (dots) ctx->max_segments = 1;
     GemvPlan plan = plan_gemv(ctx, m, s0, s1);
@@ -424,6 +442,7 @@ void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *
     const dim3 block(64 * plan.nseg);
     P.lds_terms = 1;
     P.exact = ctx->exact;
+    P.accum = accum ? 1 : 0;
     {
         static int dbg = -1;
         if (dbg < 0) {

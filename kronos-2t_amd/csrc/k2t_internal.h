@@ -43,6 +43,7 @@ struct Error : std::runtime_error {
 };
 
 void hip_check(hipError_t e, const char *what);
+void set_last_error(const std::string &msg);
 
 // Grows the context's scratch buffer (synchronous allocation).
 void ensure_scratch(k2t_ctx *ctx, size_t floats);

@@ -1,0 +1,395 @@
+// Decode-step device glue around the GEMVs (gfx950): fused RMSNorm + FWHT + int8,
+// RoPE + Hadamard int8 KV store, flash-decoding q8 attention with a fused
+// IFWHT -> FWHT -> int8 epilogue for o_proj, SwiGLU + FWHT + int8, tied-embedding row
+// decode.  Reference: the decode megakernel real_llm.rs:6794-7403 and its helpers.
+//
+// Every wave-level FWHT uses the butterfly order of hadamard.rs:83-97, so where the
+// reference's inputs are reproduced exactly, rotations and int8 codes are bit-exact.
+// Sums (inv_rms, softmax denominators, attention accumulations) are tree/parallel
+// reductions: those match the reference to fp32 rounding.
+#include <float.h>
+#include <math.h>
+
+#include "k2t_device.h"
+#include "k2t_internal.h"
+
+namespace k2t {
+
+// Quantizes the 64 values held one per lane (already rotated) to int8 with one scale
+// (simd_lut.rs:3097-3128 / 3172-3195).
+__device__ __forceinline__ void quant_chunk_store(float v, uint32_t lane, int8_t *q, float *scale,
+                                                  int32_t *sum) {
+    const float mx = wave_max_f(fabsf(v));
+    if (mx <= FLT_EPSILON) {
+        q[lane] = 0;
+        if (lane == 0) {
+            *scale = 0.0f;
+            *sum = 0;
+        }
+        return;
+    }
+    const float inv = 127.0f / mx;
+    const int qi = (int)rintf(v * inv);
+    const int s = wave_sum_i(qi);
+    q[lane] = (int8_t)qi;
+    if (lane == 0) {
+        *scale = mx / 127.0f;
+        *sum = s;
+    }
+}
+
+__device__ __forceinline__ float fwht_lane(float v, uint64_t block, uint32_t lane) {
+    v = flip_sign(v, hadamard_sign_bit(block, lane)) * 0.125f;
+    return wave_butterflies64(v, lane);
+}
+
+// hadamard.rs:193-228 on one block held one element per lane.
+__device__ __forceinline__ float ifwht_lane(float v, uint64_t block, uint32_t lane) {
+    v = wave_butterflies64(v, lane);
+    return flip_sign(v * 0.125f, hadamard_sign_bit(block, lane));
+}
+
+// ---------------------------------------------------------------- RMSNorm + FWHT + int8
+// One workgroup per token: inv_rms = 1/sqrt(mean(x^2) + eps) (real_llm.rs:6929), then
+// populate_rmsnorm_fwht (simd_lut.rs:2970-2997) chunk by chunk, one wave per chunk.
+__global__ __launch_bounds__(256) void rmsnorm_act_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                          float eps, int K, int8_t *__restrict__ q,
+                                                          float *__restrict__ scales, int32_t *__restrict__ sums) {
+    __shared__ float part[4];
+    __shared__ float inv_s;
+    const int tok = blockIdx.x;
+    const float *xt = x + (size_t)tok * K;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < K; i += 256) ss = fmaf(xt[i], xt[i], ss);
+    ss = wave_sum_f(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    if (threadIdx.x == 0) inv_s = 1.0f / sqrtf(((part[0] + part[1]) + (part[2] + part[3])) / (float)K + eps);
+    __syncthreads();
+    const float inv_rms = inv_s;
+    const uint32_t lane = threadIdx.x & 63;
+    const int nc = K / 64;
+    for (int c = threadIdx.x >> 6; c < nc; c += 4) {
+        const float v = (xt[c * 64 + lane] * inv_rms) * w[c * 64 + lane];
+        const float r = fwht_lane(v, (uint64_t)c, lane);
+        const size_t gc = (size_t)tok * nc + c;
+        quant_chunk_store(r, lane, q + gc * 64, scales + gc, sums + gc);
+    }
+}
+
+void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float eps, int K, int ntok, int8_t *q,
+                        float *s, int32_t *sums) {
+    hipLaunchKernelGGL(rmsnorm_act_kernel, dim3(ntok), dim3(256), 0, st, x, w, eps, K, q, s, sums);
+    hip_check(hipGetLastError(), "rmsnorm_act launch");
+}
+
+// ---------------------------------------------------------------- qkv post-processing
+// One wave per (token, head) of the fused qkv output [q heads | k heads | v heads]:
+// optional bias, RoPE on q and k (real_llm.rs:9328-9361, half-split), then k and v go
+// through store_hadamard_q8_head (real_llm.rs:8282-8365) into the cache slot of `pos`.
+// Positions are read from `pos_dev` (+ token index) so a captured graph can replay.
+__global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, const float *__restrict__ bias,
+                                                      const float *__restrict__ rope, const int *__restrict__ pos_dev,
+                                                      int nq, int nkv, int hd, int row_stride, int layer, int cap,
+                                                      int8_t *__restrict__ kq, int8_t *__restrict__ vq,
+                                                      float *__restrict__ ks, float *__restrict__ vs) {
+    const uint32_t lane = threadIdx.x;
+    const int head = blockIdx.x, tok = blockIdx.y;
+    const int pos = pos_dev[0] + tok;
+    float *h = qkv + (size_t)tok * row_stride + (size_t)head * hd;
+    const int nb = hd / 64;  // 1 or 2 blocks; lane holds element lane (+64)
+    float v0 = h[lane], v1 = nb > 1 ? h[64 + lane] : 0.0f;
+    if (bias) {
+        v0 = v0 + bias[head * hd + lane];
+        if (nb > 1) v1 = v1 + bias[head * hd + 64 + lane];
+    }
+    if (head < nq + nkv) {
+        const float *row = rope + (size_t)pos * hd;
+        if (nb == 1) {  // pairs (i, i+32) live in lanes lane and lane^32
+            const float other = __shfl_xor(v0, 32, kWave);
+            const uint32_t i = lane & 31u;
+            const float c = row[i], s = row[32 + i];
+            v0 = lane < 32 ? v0 * c - other * s : v0 * c + other * s;
+        } else {  // pairs (i, i+64): element lane and 64+lane of this lane
+            const float c = row[lane], s = row[64 + lane];
+            const float x0 = v0, x1 = v1;
+            v0 = x0 * c - x1 * s;
+            v1 = x1 * c + x0 * s;
+        }
+    }
+    if (head < nq) {
+        h[lane] = v0;
+        if (nb > 1) h[64 + lane] = v1;
+        return;
+    }
+    const bool is_k = head < nq + nkv;
+    const int kvh = is_k ? head - nq : head - nq - nkv;
+    const size_t slot = ((size_t)layer * nkv + kvh) * cap + pos;
+    const float r0 = fwht_lane(v0, 0, lane);
+    const float r1 = nb > 1 ? fwht_lane(v1, 1, lane) : 0.0f;
+    const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
+    int8_t *dst = (is_k ? kq : vq) + slot * hd;
+    float *sdst = (is_k ? ks : vs) + slot;
+    if (mx <= FLT_EPSILON) {
+        dst[lane] = 0;
+        if (nb > 1) dst[64 + lane] = 0;
+        if (lane == 0) *sdst = 0.0f;
+        return;
+    }
+    const float inv = 127.0f / mx;
+    dst[lane] = (int8_t)(int)rintf(r0 * inv);
+    if (nb > 1) dst[64 + lane] = (int8_t)(int)rintf(r1 * inv);
+    if (lane == 0) *sdst = mx / 127.0f;
+}
+
+void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *rope, const int *pos_dev, int nq,
+                     int nkv, int hd, int ntok, int layer, int cap, int8_t *kq, int8_t *vq, float *ks, float *vs) {
+    hipLaunchKernelGGL(qkv_post_kernel, dim3(nq + 2 * nkv, ntok), dim3(64), 0, st, qkv, bias, rope, pos_dev, nq, nkv,
+                       hd, (nq + 2 * nkv) * hd, layer, cap, kq, vq, ks, vs);
+    hip_check(hipGetLastError(), "qkv_post launch");
+}
+
+// ---------------------------------------------------------------- attention
+// Flash-decoding over the int8 Hadamard KV cache (causal_gqa_group_q8, real_llm.rs:8471-8594):
+// the query head is rotated and quantized like a KV head, s_t = float(q.k_t)*ks_t*(qs*scale),
+// softmax, o = sum_t p_t*vs_t*v_t in the rotated domain.  Grid (q head, split, token); each
+// workgroup writes (max, sum, o[hd]) for its KV range; attn_merge_kernel combines them.
+constexpr int kAttnSplitLen = 256;
+
+__global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restrict__ q, int q_stride,
+                                                           const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
+                                                           const float *__restrict__ ks, const float *__restrict__ vs,
+                                                           const int *__restrict__ pos_dev, int layer, int nq, int nkv,
+                                                           int hd, int cap, float attn_scale, int nsplit,
+                                                           float *__restrict__ part) {
+    __shared__ __align__(16) int8_t qi[128];
+    __shared__ float qas_s;
+    __shared__ float sc[kAttnSplitLen];
+    __shared__ float red[8];
+    __shared__ float opart[4][128];
+    const int head = blockIdx.x, split = blockIdx.y, tok = blockIdx.z;
+    const int seq = pos_dev[0] + tok + 1;
+    const int t0 = split * kAttnSplitLen, t1 = min(seq, t0 + kAttnSplitLen);
+    float *pp = part + ((size_t)(tok * nq + head) * nsplit + split) * (2 + hd);
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (t0 >= t1) {
+        if (tid == 0) {
+            pp[0] = -INFINITY;
+            pp[1] = 0.0f;
+        }
+        if (tid < (uint32_t)hd) pp[2 + tid] = 0.0f;
+        return;
+    }
+    const int kvh = head / (nq / nkv);
+    const float *qh = q + (size_t)tok * q_stride + (size_t)head * hd;
+    const int nb = hd / 64;
+    if (wv == 0) {
+        const float r0 = fwht_lane(qh[lane], 0, lane);
+        const float r1 = nb > 1 ? fwht_lane(qh[64 + lane], 1, lane) : 0.0f;
+        const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
+        float qs = 0.0f;
+        if (mx <= FLT_EPSILON) {
+            qi[lane] = 0;
+            if (nb > 1) qi[64 + lane] = 0;
+        } else {
+            const float inv = 127.0f / mx;
+            qi[lane] = (int8_t)(int)rintf(r0 * inv);
+            if (nb > 1) qi[64 + lane] = (int8_t)(int)rintf(r1 * inv);
+            qs = mx / 127.0f;
+        }
+        if (lane == 0) qas_s = qs * attn_scale;
+    }
+    __syncthreads();
+    const size_t base = ((size_t)layer * nkv + kvh) * cap;
+    const float qas = qas_s;
+    // scores: one thread per position
+    float smax = -INFINITY;
+    {
+        const int t = t0 + (int)tid;
+        if (t < t1) {
+            const uint4 *kr = reinterpret_cast<const uint4 *>(kq + (base + t) * hd);
+            const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
+            int dot = 0;
+            for (int i = 0; i < hd / 16; i++) {
+                const uint4 a = kr[i], b = qr[i];
+                dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
+            }
+            const float s = ((float)dot * ks[base + t]) * qas;
+            sc[tid] = s;
+            smax = s;
+        }
+    }
+    smax = wave_max_f(smax);
+    if (lane == 0) red[wv] = smax;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float psum = 0.0f;
+    if (t0 + (int)tid < t1) {
+        const float p = expf(sc[tid] - m);
+        sc[tid] = p * vs[base + t0 + tid];  // p_t * vs_t
+        psum = p;
+    }
+    psum = wave_sum_f(psum);
+    __syncthreads();
+    if (lane == 0) red[4 + wv] = psum;
+    // o partial: thread (wave wv, column d) accumulates positions wv, wv+4, ...
+    const int n = t1 - t0;
+    for (int d = lane; d < hd; d += 64) {
+        float acc = 0.0f;
+        for (int i = wv; i < n; i += 4) acc = fmaf(sc[i], (float)vq[(base + t0 + i) * hd + d], acc);
+        opart[wv][d] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        pp[0] = m;
+        pp[1] = (red[4] + red[5]) + (red[6] + red[7]);
+    }
+    if (tid < (uint32_t)hd) pp[2 + tid] = (opart[0][tid] + opart[1][tid]) + (opart[2][tid] + opart[3][tid]);
+}
+
+// Combines the splits of one (token, q head), applies ifwht64 (real_llm.rs:8588-8592), and
+// optionally re-rotates each 64-block with its o_proj chunk index and quantizes it
+// (populate_chunk_fwht_raw(None), real_llm.rs:7060-7084) -> the o_proj activation.
+__global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ part, int nq, int hd, int nsplit,
+                                                        const int *__restrict__ pos_dev, float *__restrict__ out_f,
+                                                        int8_t *__restrict__ aq, float *__restrict__ as,
+                                                        int32_t *__restrict__ asum) {
+    const uint32_t lane = threadIdx.x;
+    const int head = blockIdx.x, tok = blockIdx.y;
+    const int seq = pos_dev[0] + tok + 1;
+    const int ns = min(nsplit, (seq + kAttnSplitLen - 1) / kAttnSplitLen);
+    const float *pp = part + (size_t)(tok * nq + head) * nsplit * (2 + hd);
+    float M = -INFINITY;
+    for (int s = 0; s < ns; s++) M = fmaxf(M, pp[(size_t)s * (2 + hd)]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    const int nb = hd / 64;
+    for (int s = 0; s < ns; s++) {
+        const float *ps = pp + (size_t)s * (2 + hd);
+        const float e = expf(ps[0] - M);
+        L = fmaf(ps[1], e, L);
+        o0 = fmaf(ps[2 + lane], e, o0);
+        if (nb > 1) o1 = fmaf(ps[2 + 64 + lane], e, o1);
+    }
+    const float inv = 1.0f / L;
+    o0 = ifwht_lane(o0 * inv, 0, lane);
+    if (nb > 1) o1 = ifwht_lane(o1 * inv, 1, lane);
+    const size_t hbase = (size_t)tok * nq * hd + (size_t)head * hd;
+    if (out_f) {
+        out_f[hbase + lane] = o0;
+        if (nb > 1) out_f[hbase + 64 + lane] = o1;
+    }
+    if (aq) {
+        const int nc_tok = nq * nb;  // o_proj input chunks per token
+        const size_t c0 = (size_t)head * nb;
+        const size_t g0 = (size_t)tok * nc_tok + c0;
+        quant_chunk_store(fwht_lane(o0, c0, lane), lane, aq + g0 * 64, as + g0, asum + g0);
+        if (nb > 1) quant_chunk_store(fwht_lane(o1, c0 + 1, lane), lane, aq + (g0 + 1) * 64, as + g0 + 1, asum + g0 + 1);
+    }
+}
+
+int attn_max_splits(int max_seq) { return (max_seq + kAttnSplitLen - 1) / kAttnSplitLen; }
+
+void launch_attention(hipStream_t st, const float *q, int q_stride, const int8_t *kq, const int8_t *vq, const float *ks,
+                      const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd, int cap, float attn_scale,
+                      int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum) {
+    hipLaunchKernelGGL(attn_partial_kernel, dim3(nq, nsplit, ntok), dim3(256), 0, st, q, q_stride, kq, vq, ks, vs,
+                       pos_dev, layer, nq, nkv, hd, cap, attn_scale, nsplit, part);
+    hip_check(hipGetLastError(), "attn_partial launch");
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(nq, ntok), dim3(64), 0, st, part, nq, hd, nsplit, pos_dev, out_f, aq, as,
+                       asum);
+    hip_check(hipGetLastError(), "attn_merge launch");
+}
+
+// ---------------------------------------------------------------- SwiGLU + FWHT + int8
+// Interleaved gate_up output: block ic = [gate64(ic), up64(ic)] (simd_lut.rs:3310-3325).
+// swiglu_activate_scalar (real_llm.rs:9801-9805), then populate_chunk_fwht_raw with chunk ic.
+__global__ __launch_bounds__(64) void swiglu_act_kernel(const float *__restrict__ gu, int inter, int8_t *__restrict__ q,
+                                                        float *__restrict__ s, int32_t *__restrict__ sums) {
+    const uint32_t lane = threadIdx.x;
+    const int ic = blockIdx.x, tok = blockIdx.y;
+    const int nci = inter / 64;
+    const float *b = gu + (size_t)tok * 2 * inter + (size_t)ic * 128;
+    const float g = b[lane], u = b[64 + lane];
+    const float v = (g / (1.0f + expf(-g))) * u;
+    const size_t gc = (size_t)tok * nci + ic;
+    quant_chunk_store(fwht_lane(v, (uint64_t)ic, lane), lane, q + gc * 64, s + gc, sums + gc);
+}
+
+void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums) {
+    hipLaunchKernelGGL(swiglu_act_kernel, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums);
+    hip_check(hipGetLastError(), "swiglu_act launch");
+}
+
+// ---------------------------------------------------------------- tied embedding
+// embed_token_into (real_llm.rs:8063-8097): row `token` of the quantized lm_head,
+// dequantized in the rotated domain (simd_lut.rs:3439-3480 / 5558-5634), then ifwht64.
+// One wave per 64-column chunk; tokens come from a device array.
+__global__ __launch_bounds__(64) void embed_kernel(const uint8_t *__restrict__ pair, const uint8_t *__restrict__ tail,
+                                                   int fmt, int hp, int sgc, size_t ptot, int nc, int np,
+                                                   uint32_t cb0, uint32_t cb1, uint32_t cb2, uint32_t cb3,
+                                                   const int *__restrict__ tokens, float *__restrict__ out) {
+    const uint32_t lane = threadIdx.x;
+    const int c = blockIdx.x, tok_i = blockIdx.y;
+    const int r = tokens[tok_i];
+    const int stripe = r / 16, rl = r % 16, g = rl / 4, j = rl % 4;
+    const int k = lane / 16, w = lane % 16, half = w / 8, sub = w / 4, t = w % 4;
+    const bool in_pair = stripe < 2 * np;
+    const int side = stripe & 1;
+    float val;
+    if (fmt == K2T_FMT_NIBBLE4) {
+        const size_t prec = 1024 + 256 * (size_t)hp + 64, trec = 512 + 128 * (size_t)hp + 32;
+        const uint8_t *base = in_pair ? pair + ((size_t)(stripe / 2) * nc + c) * prec : tail + (size_t)c * trec;
+        const uint8_t *d = base + (in_pair ? side * 512 : 0);
+        const uint8_t *h = base + (in_pair ? 1024 + side * 128 * hp : 512);
+        const uint8_t *sp = base + (in_pair ? 1024 + 256 * hp + side * 32 : 512 + 128 * hp);
+        const uint8_t byte = d[k * 128 + g * 32 + half * 16 + j * 4 + t];
+        int u = (w % 8) < 4 ? (byte & 0x0F) : (byte >> 4);
+        if (hp == 1) {
+            const uint8_t hb = h[(k / 2) * 64 + g * 16 + j * 4 + t];
+            const int bit = (k & 1) == 0 ? 4 + sub : sub;
+            u |= ((hb >> bit) & 1) << 4;
+        } else if (hp == 2) {
+            const int shifts[4] = {4, 6, 2, 0};
+            const uint8_t hb = h[k * 64 + g * 16 + j * 4 + t];
+            u |= ((hb >> shifts[sub]) & 3) << 4;
+        }
+        const float delta = __uint_as_float((uint32_t)(sp[rl * 2] | (sp[rl * 2 + 1] << 8)) << 16);
+        val = (float)(2 * u - ((1 << (4 + hp)) - 1)) * delta;
+    } else {
+        const int sg = c / sgc, cst = sg * sgc, sb = c - cst;
+        const uint8_t *gb = in_pair ? pair + (size_t)(stripe / 2) * ptot + (size_t)sg * 64 + (size_t)cst * 1024
+                                    : tail + (size_t)sg * 32 + (size_t)cst * 512;
+        const uint8_t *sp = gb + (in_pair ? side * 32 : 0);
+        const uint8_t *d = gb + (in_pair ? 64 + (size_t)sb * 1024 + side * 512 : 32 + (size_t)sb * 512);
+        const int sub4 = w / 4;
+        const uint8_t byte = d[k * 128 + g * 32 + (sub4 / 2) * 16 + j * 4 + t];
+        const int idx = (sub4 & 1) == 0 ? (byte & 0x0F) : (byte >> 4);
+        const uint32_t cbw = idx < 4 ? cb0 : idx < 8 ? cb1 : idx < 12 ? cb2 : cb3;
+        const int cv = (int)(int8_t)((cbw >> (8 * (idx & 3))) & 0xFF);
+        const float delta = __uint_as_float((uint32_t)(sp[rl * 2] | (sp[rl * 2 + 1] << 8)) << 16);
+        val = (float)cv * delta;
+    }
+    out[(size_t)tok_i * nc * 64 + (size_t)c * 64 + lane] = ifwht_lane(val, (uint64_t)c, lane);
+}
+
+void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok, float *out) {
+    const size_t ptot = m->fmt == K2T_FMT_NF ? (m->pairs ? m->pair_len / m->pairs : 0) : 0;
+    hipLaunchKernelGGL(embed_kernel, dim3(m->nc, ntok), dim3(64), 0, st, m->pair, m->tail, m->fmt, m->hp, m->sgc, ptot,
+                       m->nc, m->pairs, m->cb[0], m->cb[1], m->cb[2], m->cb[3], tokens, out);
+    hip_check(hipGetLastError(), "embed launch");
+}
+
+// Advances the device position counter after a step (keeps graph replays argument-free).
+__global__ void advance_pos_kernel(int *pos, int n) {
+    if (threadIdx.x == 0) pos[0] += n;
+}
+
+void launch_advance_pos(hipStream_t st, int *pos, int n) {
+    hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(64), 0, st, pos, n);
+    hip_check(hipGetLastError(), "advance_pos launch");
+}
+
+}  // namespace k2t

@@ -66,7 +66,27 @@ SIGNATURES = {
     "k2t_compile_bipolar": (I32, [VP, I32, I32, I32, I32, I32, VP, SZ, VP, SZ]),
     "k2t_compile_nf": (I32, [VP, I32, I32, I32, I32, I32, I32, VP, VP, VP, SZ, VP, SZ]),
     "k2t_synth_normal": (I32, [C.c_uint64, C.c_float, VP, SZ, I32]),
+    "k2t_model_create": (I32, [VP, VP, I32, C.POINTER(VP)]),
+    "k2t_model_destroy": (None, [VP]),
+    "k2t_model_set_layer": (I32, [VP, I32, VP, VP, VP, VP, VP, VP, VP]),
+    "k2t_model_set_head": (I32, [VP, VP, VP]),
+    "k2t_model_set_graph": (I32, [VP, I32]),
+    "k2t_model_set_exact": (I32, [VP, I32]),
+    "k2t_model_reset": (I32, [VP]),
+    "k2t_model_position": (I32, [VP, C.POINTER(I32)]),
+    "k2t_model_decode": (I32, [VP, I32, VP]),
+    "k2t_model_prefill": (I32, [VP, VP, I32, VP]),
+    "k2t_model_generate": (I32, [VP, I32, I32, VP]),
+    "k2t_model_logits": (I32, [VP, C.POINTER(VP)]),
+    "k2t_model_sync": (I32, [VP]),
 }
+
+
+class ModelConfig(C.Structure):
+    """k2t_model_config (LlamaConfig subset)."""
+    _fields_ = [("n_layers", I32), ("hidden", I32), ("n_heads", I32), ("n_kv_heads", I32), ("head_dim", I32),
+                ("intermediate", I32), ("vocab", I32), ("max_seq", I32), ("rms_eps", C.c_float),
+                ("rope_theta", C.c_float)]
 
 
 def lib():
@@ -250,3 +270,81 @@ def synth_normal(seed, n, std=1.0, threads=0):
     out = np.empty(n, np.float32)
     check(lib().k2t_synth_normal(seed, std, out.ctypes.data_as(VP) if n else None, n, threads))
     return out
+
+
+class Model:
+    """k2t_model: device-resident decoder (forward_token / forward_prompt / greedy loop)."""
+
+    def __init__(self, ctx, cfg: dict, max_batch=4):
+        import numpy as np  # noqa: F401
+        self.ctx = ctx
+        self.cfg = dict(cfg)
+        c = ModelConfig(**{k: cfg[k] for k, _ in ModelConfig._fields_})
+        h = VP()
+        check(lib().k2t_model_create(ctx.h, C.byref(c), max_batch, C.byref(h)))
+        self.h = h
+        self._keep = []
+
+    def set_layer(self, layer, qkv, o, gate_up, down, in_norm, post_norm, qkv_bias=None):
+        import numpy as np
+        inn = np.ascontiguousarray(in_norm, np.float32)
+        pn = np.ascontiguousarray(post_norm, np.float32)
+        b = None if qkv_bias is None else np.ascontiguousarray(qkv_bias, np.float32)
+        check(lib().k2t_model_set_layer(self.h, layer, qkv.h, o.h, gate_up.h, down.h, inn.ctypes.data_as(VP),
+                                        pn.ctypes.data_as(VP), None if b is None else b.ctypes.data_as(VP)))
+        self._keep.append((qkv, o, gate_up, down))
+
+    def set_head(self, head, final_norm):
+        import numpy as np
+        fn = np.ascontiguousarray(final_norm, np.float32)
+        check(lib().k2t_model_set_head(self.h, head.h, fn.ctypes.data_as(VP)))
+        self._keep.append(head)
+
+    def set_graph(self, on):
+        check(lib().k2t_model_set_graph(self.h, int(bool(on))))
+
+    def set_exact(self, on):
+        check(lib().k2t_model_set_exact(self.h, int(bool(on))))
+
+    def reset(self):
+        check(lib().k2t_model_reset(self.h))
+
+    def position(self):
+        p = I32()
+        check(lib().k2t_model_position(self.h, C.byref(p)))
+        return p.value
+
+    def decode(self, token, want_logits=True):
+        import numpy as np
+        out = np.empty(self.cfg["vocab"], np.float32) if want_logits else None
+        check(lib().k2t_model_decode(self.h, int(token), None if out is None else out.ctypes.data_as(VP)))
+        return out
+
+    def prefill(self, tokens, want_logits=True):
+        import numpy as np
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(self.cfg["vocab"], np.float32) if want_logits else None
+        check(lib().k2t_model_prefill(self.h, t.ctypes.data_as(VP), t.size,
+                                      None if out is None else out.ctypes.data_as(VP)))
+        return out
+
+    def generate(self, first_token, n_steps, want_tokens=True):
+        import numpy as np
+        out = np.empty(max(n_steps, 1), np.int32) if want_tokens else None
+        check(lib().k2t_model_generate(self.h, int(first_token), int(n_steps),
+                                       None if out is None else out.ctypes.data_as(VP)))
+        return None if out is None else out[:n_steps]
+
+    def sync(self):
+        check(lib().k2t_model_sync(self.h))
+
+    def close(self):
+        if self.h and not _shutting_down:
+            lib().k2t_model_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

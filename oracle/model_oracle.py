@@ -1,0 +1,141 @@
+"""CPU restatement of the decode megakernel (forward_token_sdot_megakernel,
+real_llm.rs:6794-7403) built from the C oracle's primitives.
+
+TEST INFRASTRUCTURE ONLY (imported by tests/ and the smoke check, never by the
+product).  Per layer, in the reference's order:
+  1. inv_rms + RMSNorm*w + FWHT + int8 (6929-6950), qkv GEMV (6957-6977), bias, RoPE on q
+     and k heads, Hadamard int8 store of k and v (6990-7021);
+  2. q8 attention per query head (causal_gqa_group_q8, 8471-8594) -> ifwht -> FWHT with
+     chunk index qh*cph+sub -> int8 (7060-7084);
+  3. o_proj GEMV, hidden += proj (7163-7189);
+  4. post-attention norm -> interleaved gate_up GEMV -> SwiGLU -> FWHT (chunk ic) -> int8
+     (7207-7296);
+  5. down GEMV, hidden += (7308-7333);
+then final norm -> lm_head GEMV (7338-7391).  The embedding is the tied quantized
+head's row, dequantized and inverse-rotated (embed_token_into, 8063-8097).
+"""
+import numpy as np
+
+import oracle as O
+
+
+class Matrix:
+    """A quantized matrix in the reference's stream layout."""
+
+    def __init__(self, fmt, rows, cols, pair, tail, hp=0, cb=None, sgc=2):
+        self.fmt, self.rows, self.cols, self.pair, self.tail = fmt, rows, cols, pair, tail
+        self.hp, self.cb, self.sgc = hp, cb, sgc
+
+    def gemv(self, xq, xs, xsum):
+        if self.fmt == "n4":
+            return O.nibble4_gemv(self.pair, self.tail, self.rows, self.cols, self.hp, xq, xs, xsum)
+        return O.nf_gemv(self.pair, self.tail, self.rows, self.cols, 4, self.sgc, self.cb, xq, xs)
+
+    def row_rotated(self, r):
+        if self.fmt == "n4":
+            return O.nibble4_dequant_row(self.pair, self.tail, self.rows, self.cols, self.hp, r)
+        return O.nf_dequant_row(self.pair, self.tail, self.rows, self.cols, 4, self.sgc, self.cb, r)
+
+
+def quantize_matrix(W, fmt, planes=4, sgc=2, interleave_gate_up=False):
+    """Oracle quantizers: Hadamard RTN bit planes (compiler.rs:992-1107 + repack) or NF4."""
+    rows, cols = W.shape
+    if fmt == "n4":
+        u, sc = O.bipolar_rtn(W, planes)
+        pair, tail = O.nibble4_repack(O.pack_interleaved(u, planes), sc, rows, cols, planes, interleave_gate_up)
+        return Matrix("n4", rows, cols, pair, tail, hp=planes - 4)
+    cb, mu = O.nf_fit_codebook(W, 4, sgc)
+    idx, sc = O.nf_rtn(W, 4, sgc, cb, mu)
+    if interleave_gate_up:
+        inter = rows // 2
+        perm = [(b // 2) * 64 + o + (inter if b % 2 else 0) for b in range(rows // 64) for o in range(64)]
+        nsg = (cols // 64 + sgc - 1) // sgc
+        s3 = np.stack([sc.reshape(-1, nsg, 16)[r // 16, :, r % 16] for r in range(rows)])[perm]
+        idx = idx[perm]
+        sc = np.stack([s3[s * 16:(s + 1) * 16].T for s in range(rows // 16)]).ravel()
+    pair, tail = O.nf_from_indices(idx, sc, rows, cols, 4, sgc)
+    return Matrix("nf4", rows, cols, pair, tail, cb=cb, sgc=sgc)
+
+
+class OracleModel:
+    def __init__(self, cfg, layers, head, final_norm):
+        self.cfg = cfg
+        self.layers = layers  # dicts: qkv, o, gu, down (Matrix), in_norm, post_norm, bias
+        self.head = head
+        self.final_norm = final_norm
+        L, nkv, hd, cap = cfg["n_layers"], cfg["n_kv_heads"], cfg["head_dim"], cfg["max_seq"]
+        self.kq = np.zeros((L, nkv, cap, hd), np.int8)
+        self.vq = np.zeros((L, nkv, cap, hd), np.int8)
+        self.ks = np.zeros((L, nkv, cap), np.float32)
+        self.vs = np.zeros((L, nkv, cap), np.float32)
+        self.pos = 0
+
+    def embed(self, token):
+        return O.ifwht64(self.head.row_rotated(token))
+
+    def forward_token(self, token):
+        c = self.cfg
+        d, nq, nkv, hd, inter, eps = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["intermediate"], \
+            c["rms_eps"]
+        pos = self.pos
+        rope = O.rope_row(hd, float(np.float32(c["rope_theta"])), pos)
+        scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+        hidden = self.embed(token).astype(np.float32)
+        for li, L in enumerate(self.layers):
+            xq, xs, xsum = O.populate_fwht(hidden, L["in_norm"], O.inv_rms(hidden, eps))
+            qkv = L["qkv"].gemv(xq, xs, xsum).reshape(-1, hd)
+            if L.get("bias") is not None:
+                qkv = (qkv + L["bias"].reshape(-1, hd)).astype(np.float32)
+            for h in range(nq + nkv):
+                qkv[h] = O.rope_apply(qkv[h], rope)
+            for kvh in range(nkv):
+                self.kq[li, kvh, pos], self.ks[li, kvh, pos] = O.kv_quant_head(qkv[nq + kvh])
+                self.vq[li, kvh, pos], self.vs[li, kvh, pos] = O.kv_quant_head(qkv[nq + nkv + kvh])
+            group = nq // nkv
+            outs = []
+            for qh in range(nq):
+                kvh = qh // group
+                outs.append(O.attn_q8_head(qkv[qh], self.kq[li, kvh, :pos + 1], self.ks[li, kvh, :pos + 1],
+                                           self.vq[li, kvh, :pos + 1], self.vs[li, kvh, :pos + 1], scale))
+            aq, as_, asum = O.populate_fwht(np.concatenate(outs))
+            hidden = (hidden + L["o"].gemv(aq, as_, asum)).astype(np.float32)
+            xq, xs, xsum = O.populate_fwht(hidden, L["post_norm"], O.inv_rms(hidden, eps))
+            gu = L["gu"].gemv(xq, xs, xsum).reshape(-1, 128)
+            sw = np.concatenate([O.swiglu(gu[ic, :64], gu[ic, 64:]) for ic in range(inter // 64)])
+            iq, is_, isum = O.populate_fwht(sw)
+            hidden = (hidden + L["down"].gemv(iq, is_, isum)).astype(np.float32)
+        xq, xs, xsum = O.populate_fwht(hidden, self.final_norm, O.inv_rms(hidden, eps))
+        self.pos += 1
+        return self.head.gemv(xq, xs, xsum)
+
+
+def random_model(cfg, seed, fmt="nf4", planes=None):
+    """Random-init weights ~N(0, 0.02), norms 1 + 0.1*N(0,1); quantized by the oracle.
+    `planes` maps projection -> bit planes for fmt "n4" (p55454 = qkv5/o5/gu4/down5/head4)."""
+    rng = np.random.default_rng(seed)
+    d, nq, nkv, hd, inter, V = cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], \
+        cfg["intermediate"], cfg["vocab"]
+    planes = planes or {"qkv": 4, "o": 4, "gu": 4, "down": 4, "head": 4}
+
+    def q(W, name, gu=False):
+        if fmt == "n4":
+            return quantize_matrix(W, "n4", planes=planes[name], interleave_gate_up=gu)
+        return quantize_matrix(W, "nf4", sgc=2, interleave_gate_up=gu)
+
+    def w(r, c_):
+        return (rng.standard_normal((r, c_)) * 0.02).astype(np.float32)
+
+    layers = []
+    for _ in range(cfg["n_layers"]):
+        layers.append({
+            "qkv": q(w((nq + 2 * nkv) * hd, d), "qkv"),
+            "o": q(w(d, nq * hd), "o"),
+            "gu": q(w(2 * inter, d), "gu", gu=True),
+            "down": q(w(d, inter), "down"),
+            "in_norm": (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+            "post_norm": (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+            "bias": None,
+        })
+    head = q(w(V, d), "head")
+    final_norm = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    return layers, head, final_norm

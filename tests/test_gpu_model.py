@@ -1,0 +1,124 @@
+"""End-to-end decode parity: the GPU engine (C ABI k2t_model_*) against the oracle's
+restatement of the decode megakernel (oracle/model_oracle.py) on small random-init
+models, plus engine invariants (prefill == token-by-token, graph == eager, greedy).
+
+Bar: logits of every step with cosine > 0.99995 against the oracle -- the reference's own
+threshold between two paths of the same model (batched prefill vs token-by-token,
+real_llm.rs:10466-10473) -- (0.9999 with the fast GEMV epilogue) and
+max |diff| <= 2e-2 * max|logit|.  Integer GEMV and
+attention dots are exact (test_gpu_gemv.py), but inv_rms (tree vs sequential sum), expf
+and the attention accumulation order differ in the last ulp and can move an int8 code by
+one; the reference itself has two such orders (NEON vs portable, real_llm.rs:903-962).
+"""
+import numpy as np
+import pytest
+
+from model_oracle import OracleModel, random_model
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, intermediate=512, vocab=520,
+            max_seq=40, rms_eps=1e-5, rope_theta=10000.0)
+TINY128 = dict(n_layers=2, hidden=256, n_heads=2, n_kv_heads=1, head_dim=128, intermediate=384, vocab=300,
+               max_seq=300, rms_eps=1e-5, rope_theta=100000.0)
+P55454 = {"qkv": 5, "o": 5, "gu": 4, "down": 5, "head": 4}
+
+
+def _upload(ctx, m):
+    if m.fmt == "n4":
+        return ctx.upload_nibble4(m.rows, m.cols, m.hp, m.pair, m.tail)
+    return ctx.upload_nf(m.rows, m.cols, 4, m.sgc, m.cb, m.pair, m.tail)
+
+
+def _gpu_model(ctx, cfg, layers, head, final_norm, max_batch=8):
+    import k2t
+    gm = k2t.Model(ctx, cfg, max_batch=max_batch)
+    mats = []
+    for i, L in enumerate(layers):
+        q, o, gu, dn = (_upload(ctx, L[k]) for k in ("qkv", "o", "gu", "down"))
+        mats += [q, o, gu, dn]
+        gm.set_layer(i, q, o, gu, dn, L["in_norm"], L["post_norm"], L.get("bias"))
+    hm = _upload(ctx, head)
+    gm.set_head(hm, final_norm)
+    return gm, mats + [hm]
+
+
+def _close(a, b, cos_min=0.99995):
+    cos = float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
+    rel = float(np.abs(a - b).max() / np.abs(b).max())
+    return rel <= 2e-2 and cos > cos_min, (rel, cos)
+
+
+@pytest.mark.parametrize("exact", [True, False])
+@pytest.mark.parametrize("name,cfg,fmt,planes", [("nf4_hd64", TINY, "nf4", None),
+                                                ("p55454_hd64", TINY, "n4", P55454),
+                                                ("b6_hd128", TINY128, "n4", {k: 6 for k in P55454})])
+def test_decode_matches_oracle(gpu_ctx, name, cfg, fmt, planes, exact):
+    layers, head, fn = random_model(cfg, seed=len(name), fmt=fmt, planes=planes)
+    ref = OracleModel(cfg, layers, head, fn)
+    gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
+    gm.set_exact(exact)  # fast epilogue: per-segment sums, a few ulp per GEMV output
+    rng = np.random.default_rng(9)
+    toks = rng.integers(0, cfg["vocab"], 8)
+    for i, t in enumerate(toks):
+        a = gm.decode(int(t))
+        b = ref.forward_token(int(t))
+        ok, info = _close(a, b, 0.99995 if exact else 0.9999)
+        assert ok, f"{name} step {i}: max rel diff, cos = {info}"
+    assert gm.position() == len(toks)
+
+
+def test_long_context_splits(gpu_ctx):
+    """hd 128 with > 256 positions: the attention is split over KV ranges and merged."""
+    cfg = dict(TINY128, n_layers=1)
+    layers, head, fn = random_model(cfg, seed=3, fmt="nf4")
+    ref = OracleModel(cfg, layers, head, fn)
+    gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
+    rng = np.random.default_rng(4)
+    toks = rng.integers(0, cfg["vocab"], 270)
+    gm.prefill(toks[:-1], want_logits=False)
+    for t in toks[:-1]:
+        ref.forward_token(int(t))
+    a = gm.decode(int(toks[-1]))
+    b = ref.forward_token(int(toks[-1]))
+    ok, info = _close(a, b)
+    assert ok, info
+
+
+def test_prefill_equals_token_by_token_and_graph_equals_eager(gpu_ctx):
+    layers, head, fn = random_model(TINY, seed=5, fmt="nf4")
+    gm, _ = _gpu_model(gpu_ctx, TINY, layers, head, fn, max_batch=4)
+    toks = np.arange(11) * 37 % TINY["vocab"]
+    pre = gm.prefill(toks)  # 3 batches of <= 4 tokens (4-token GEMV tiles)
+    gm.reset()
+    gm.set_graph(False)
+    for t in toks:
+        eager = gm.decode(int(t))
+    gm.reset()
+    gm.set_graph(True)
+    for t in toks:
+        graph = gm.decode(int(t))
+    assert np.array_equal(pre.view(np.uint32), eager.view(np.uint32))
+    assert np.array_equal(graph.view(np.uint32), eager.view(np.uint32))
+
+
+def test_greedy_generate_matches_oracle_argmax(gpu_ctx):
+    layers, head, fn = random_model(TINY, seed=6, fmt="nf4")
+    ref = OracleModel(TINY, layers, head, fn)
+    gm, _ = _gpu_model(gpu_ctx, TINY, layers, head, fn)
+    out = gm.generate(17, 6)
+    tok, seq = 17, []
+    for _ in range(6):
+        logits = ref.forward_token(tok)
+        tok = int(np.argmax(logits))
+        seq.append(tok)
+    assert list(out) == seq
+
+
+def test_model_argument_errors(gpu_ctx):
+    import k2t
+    with pytest.raises(k2t.K2TError):
+        k2t.Model(gpu_ctx, dict(TINY, head_dim=96, hidden=384))
+    gm = k2t.Model(gpu_ctx, TINY)
+    with pytest.raises(k2t.K2TError):
+        gm.decode(1)  # layers not set
