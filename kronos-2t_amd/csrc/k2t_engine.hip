@@ -36,9 +36,23 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
     __shared__ int bi[16];
     float best = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    // Each thread scans its indices in increasing order (keeps the lowest index among
+    // equals), eight loads in flight.
+    int i = threadIdx.x;
+    for (; i + 7 * (int)blockDim.x < n; i += 8 * blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = x[i + u * blockDim.x];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (v[u] > best) {
+                best = v[u];
+                idx = i + u * blockDim.x;
+            }
+    }
+    for (; i < n; i += blockDim.x) {
         const float v = x[i];
-        if (v > best) {  // strided scan keeps the lowest index among equals per thread
+        if (v > best) {
             best = v;
             idx = i;
         }

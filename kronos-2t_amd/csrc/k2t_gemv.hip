@@ -356,10 +356,14 @@ GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1) {
     // Short-lived waves that each fetch all their records in one batch stream best
     // (~14 waves per CU, <= 2 records per lane group).  Shrink the per-wave chunk count
     // when the matrix has too few row blocks to reach that many waves.
+    // A wave's lane groups take `gr`-chunk granules round-robin; one full round keeps
+    // every lane busy.  Waves fetch at most two rounds in one batch: short-lived waves
+    // that issue all their loads up front stream best (~14 waves per CU).  Small matrices
+    // keep one full round per wave rather than many mostly idle waves.
     const int target = ctx->num_cus * 14;
-    int cps = 2 * G;
-    while (cps > step && (long)nrb * ((m->nc + cps - 1) / cps) < target) cps -= step;
-    cps = std::max({cps, step, (m->nc + 15) / 16});  // at most 16 waves per workgroup
+    const int round = G * step;
+    int cps = (long)nrb * ((m->nc + 2 * round - 1) / (2 * round)) >= target ? 2 * round : round;
+    cps = std::max(cps, (m->nc + 15) / 16);  // at most 16 waves per workgroup
     if (ctx->max_segments > 0) cps = std::max(cps, (m->nc + ctx->max_segments - 1) / ctx->max_segments);
     cps = (cps + step - 1) / step * step;
     p.cps = cps;

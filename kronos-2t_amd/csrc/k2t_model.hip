@@ -50,36 +50,49 @@ __device__ __forceinline__ float ifwht_lane(float v, uint64_t block, uint32_t la
 }
 
 // ---------------------------------------------------------------- RMSNorm + FWHT + int8
-// One workgroup per token: inv_rms = 1/sqrt(mean(x^2) + eps) (real_llm.rs:6929), then
-// populate_rmsnorm_fwht (simd_lut.rs:2970-2997) chunk by chunk, one wave per chunk.
-__global__ __launch_bounds__(256) void rmsnorm_act_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                          float eps, int K, int8_t *__restrict__ q,
-                                                          float *__restrict__ scales, int32_t *__restrict__ sums) {
-    __shared__ float part[4];
-    __shared__ float inv_s;
-    const int tok = blockIdx.x;
+// One wave per (chunk, token): every wave recomputes inv_rms = 1/sqrt(mean(x^2) + eps)
+// (real_llm.rs:6929) from the whole row (L2-resident, a few KB) in a fixed order, then
+// runs populate_rmsnorm_fwht (simd_lut.rs:2970-2997) on its own chunk.
+__global__ __launch_bounds__(64) void rmsnorm_act_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                         float eps, int K, int8_t *__restrict__ q,
+                                                         float *__restrict__ scales, int32_t *__restrict__ sums) {
+    const uint32_t lane = threadIdx.x;
+    const int c = blockIdx.x, tok = blockIdx.y;
     const float *xt = x + (size_t)tok * K;
+    // K is a multiple of 64: lane reads float4s at 4*lane + 256*i, four loads in flight.
+    const float4 *x4 = reinterpret_cast<const float4 *>(xt);
+    const int n4 = K / 4;
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < K; i += 256) ss = fmaf(xt[i], xt[i], ss);
-    ss = wave_sum_f(ss);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    if (threadIdx.x == 0) inv_s = 1.0f / sqrtf(((part[0] + part[1]) + (part[2] + part[3])) / (float)K + eps);
-    __syncthreads();
-    const float inv_rms = inv_s;
-    const uint32_t lane = threadIdx.x & 63;
-    const int nc = K / 64;
-    for (int c = threadIdx.x >> 6; c < nc; c += 4) {
-        const float v = (xt[c * 64 + lane] * inv_rms) * w[c * 64 + lane];
-        const float r = fwht_lane(v, (uint64_t)c, lane);
-        const size_t gc = (size_t)tok * nc + c;
-        quant_chunk_store(r, lane, q + gc * 64, scales + gc, sums + gc);
+    int i = (int)lane;
+    for (; i + 192 < n4; i += 256) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = x4[i + 64 * u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            ss = fmaf(v[u].x, v[u].x, ss);
+            ss = fmaf(v[u].y, v[u].y, ss);
+            ss = fmaf(v[u].z, v[u].z, ss);
+            ss = fmaf(v[u].w, v[u].w, ss);
+        }
     }
+    for (; i < n4; i += 64) {
+        const float4 v = x4[i];
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
+    ss = wave_sum_f(ss);
+    const float inv_rms = 1.0f / sqrtf(ss / (float)K + eps);
+    const float v = (xt[c * 64 + lane] * inv_rms) * w[c * 64 + lane];
+    const size_t gc = (size_t)tok * (K / 64) + c;
+    quant_chunk_store(fwht_lane(v, (uint64_t)c, lane), lane, q + gc * 64, scales + gc, sums + gc);
 }
 
 void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float eps, int K, int ntok, int8_t *q,
                         float *s, int32_t *sums) {
-    hipLaunchKernelGGL(rmsnorm_act_kernel, dim3(ntok), dim3(256), 0, st, x, w, eps, K, q, s, sums);
+    hipLaunchKernelGGL(rmsnorm_act_kernel, dim3(K / 64, ntok), dim3(64), 0, st, x, w, eps, K, q, s, sums);
     hip_check(hipGetLastError(), "rmsnorm_act launch");
 }
 
@@ -166,7 +179,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     __shared__ float qas_s;
     __shared__ float sc[kAttnSplitLen];
     __shared__ float red[8];
-    __shared__ float opart[4][128];
+    __shared__ float opart[16][64];  // [position subset][column], 16*64 == 8*128
     const int head = blockIdx.x, split = blockIdx.y, tok = blockIdx.z;
     const int seq = pos_dev[0] + tok + 1;
     const int t0 = split * kAttnSplitLen, t1 = min(seq, t0 + kAttnSplitLen);
@@ -235,19 +248,54 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     psum = wave_sum_f(psum);
     __syncthreads();
     if (lane == 0) red[4 + wv] = psum;
-    // o partial: thread (wave wv, column d) accumulates positions wv, wv+4, ...
+    // o partial: thread = (position subset ps, 4-column group cg); a dword of V per
+    // position, loads batched 4 deep; the position subsets are added in a fixed order.
     const int n = t1 - t0;
-    for (int d = lane; d < hd; d += 64) {
-        float acc = 0.0f;
-        for (int i = wv; i < n; i += 4) acc = fmaf(sc[i], (float)vq[(base + t0 + i) * hd + d], acc);
-        opart[wv][d] = acc;
+    const int ncg = hd / 4;           // 16 or 32 column groups
+    const int nps = 256 / ncg;        // 16 or 8 position subsets
+    const int cg = (int)tid % ncg, ps = (int)tid / ncg;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    const int8_t *vbase = vq + (base + t0) * hd + cg * 4;
+    int i = ps;
+    for (; i + 3 * nps < n; i += 4 * nps) {
+        int vv[4];
+        float ww[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            vv[u] = *reinterpret_cast<const int *>(vbase + (size_t)(i + u * nps) * hd);
+            ww[u] = sc[i + u * nps];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            a0 = fmaf(ww[u], (float)(int8_t)(vv[u] & 0xFF), a0);
+            a1 = fmaf(ww[u], (float)(int8_t)((vv[u] >> 8) & 0xFF), a1);
+            a2 = fmaf(ww[u], (float)(int8_t)((vv[u] >> 16) & 0xFF), a2);
+            a3 = fmaf(ww[u], (float)(int8_t)((vv[u] >> 24) & 0xFF), a3);
+        }
     }
+    for (; i < n; i += nps) {
+        const int v = *reinterpret_cast<const int *>(vbase + (size_t)i * hd);
+        const float wt = sc[i];
+        a0 = fmaf(wt, (float)(int8_t)(v & 0xFF), a0);
+        a1 = fmaf(wt, (float)(int8_t)((v >> 8) & 0xFF), a1);
+        a2 = fmaf(wt, (float)(int8_t)((v >> 16) & 0xFF), a2);
+        a3 = fmaf(wt, (float)(int8_t)((v >> 24) & 0xFF), a3);
+    }
+    float *op = &opart[0][0];  // [nps][hd]
+    op[ps * hd + cg * 4 + 0] = a0;
+    op[ps * hd + cg * 4 + 1] = a1;
+    op[ps * hd + cg * 4 + 2] = a2;
+    op[ps * hd + cg * 4 + 3] = a3;
     __syncthreads();
     if (tid == 0) {
         pp[0] = m;
         pp[1] = (red[4] + red[5]) + (red[6] + red[7]);
     }
-    if (tid < (uint32_t)hd) pp[2 + tid] = (opart[0][tid] + opart[1][tid]) + (opart[2][tid] + opart[3][tid]);
+    if (tid < (uint32_t)hd) {
+        float acc = op[tid];
+        for (int k = 1; k < nps; k++) acc += op[k * hd + tid];
+        pp[2 + tid] = acc;
+    }
 }
 
 // Combines the splits of one (token, q head), applies ifwht64 (real_llm.rs:8588-8592), and

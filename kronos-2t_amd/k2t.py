@@ -348,3 +348,65 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------------------- synthetic models
+SMOLLM2_135M = dict(n_layers=30, hidden=576, n_heads=9, n_kv_heads=3, head_dim=64, intermediate=1536, vocab=49152,
+                    rms_eps=1e-5, rope_theta=100000.0)
+SMOLLM2_1_7B = dict(n_layers=24, hidden=2048, n_heads=32, n_kv_heads=32, head_dim=64, intermediate=8192,
+                    vocab=49152, rms_eps=1e-5, rope_theta=130000.0)
+# parse_mode "p55454" (chat.rs:278-281): qkv 5, o 5, gate_up 4, down 5, head 4 planes
+P55454 = {"qkv": 5, "o": 5, "gu": 4, "down": 5, "head": 4}
+
+
+class HostMatrix:
+    """Compiled streams of one matrix kept on the host (for CPU baselines)."""
+
+    def __init__(self, fmt, rows, cols, pair, tail, hp=0, cb=None, sgc=2):
+        self.fmt, self.rows, self.cols, self.pair, self.tail, self.hp, self.cb, self.sgc = \
+            fmt, rows, cols, pair, tail, hp, cb, sgc
+
+
+def build_random_model(ctx, cfg, max_seq, fmt="nf4", planes=None, seed=1, max_batch=4, keep_host=False,
+                       threads=0, log=None):
+    """Random-init weights ~N(0, 0.02) (norms 1.0) compiled with the host RTN compiler
+    (Hadamard + NF4 g128, or bit planes per projection) and uploaded: the synthetic
+    stand-in for a .k2tb model.  Returns (Model, [k2t Mat], [HostMatrix] or None)."""
+    import numpy as np
+    full = dict(cfg, max_seq=max_seq)
+    model = Model(ctx, full, max_batch=max_batch)
+    d, nq, nkv, hd, inter, V = cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], \
+        cfg["intermediate"], cfg["vocab"]
+    planes = planes or P55454
+    mats, host = [], [] if keep_host else None
+    counter = [seed * 1000003]
+
+    def make(rows, cols, name, gu=False):
+        counter[0] += 1
+        W = synth_normal(counter[0], rows * cols, 0.02, threads).reshape(rows, cols)
+        if fmt == "nf4":
+            cb, mu, pair, tail = compile_nf4(W, 2, gu, threads)
+            m = ctx.upload_nf(rows, cols, 4, 2, cb, pair, tail)
+            hm = HostMatrix("nf4", rows, cols, pair, tail, cb=cb, sgc=2)
+        else:
+            p = planes[name]
+            pair, tail = compile_bipolar(W, p, gu, threads)
+            m = ctx.upload_nibble4(rows, cols, p - 4, pair, tail)
+            hm = HostMatrix("n4", rows, cols, pair, tail, hp=p - 4)
+        mats.append(m)
+        if host is not None:
+            host.append(hm)
+        return m
+
+    ones = np.ones(d, np.float32)
+    for layer in range(cfg["n_layers"]):
+        q = make((nq + 2 * nkv) * hd, d, "qkv")
+        o = make(d, nq * hd, "o")
+        gu = make(2 * inter, d, "gu", gu=True)
+        dn = make(d, inter, "down")
+        model.set_layer(layer, q, o, gu, dn, ones, ones)
+        if log:
+            log(f"layer {layer} compiled")
+    head = make(V, d, "head")
+    model.set_head(head, ones)
+    return model, mats, host

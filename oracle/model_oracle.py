@@ -31,6 +31,29 @@ class Matrix:
             return O.nibble4_gemv(self.pair, self.tail, self.rows, self.cols, self.hp, xq, xs, xsum)
         return O.nf_gemv(self.pair, self.tail, self.rows, self.cols, 4, self.sgc, self.cb, xq, xs)
 
+    def gemv_portable(self, xq, xs, threads=1):
+        """Portable path (simd_lut.rs:3558-3581 / 5719-5748), stripe ranges over host threads
+        like the reference's pool (real_llm.rs:829-836)."""
+        import threading
+        stripes = (self.rows + 15) // 16
+        out = np.zeros(self.rows, np.float32)
+        per = max(2, ((stripes + threads - 1) // threads + 1) & ~1)
+
+        def work(s0, s1):
+            if self.fmt == "n4":
+                o = O.nibble4_gemv_portable(self.pair, self.tail, self.rows, self.cols, self.hp, xq, xs, s0, s1)
+            else:
+                o = O.nf_gemv_portable(self.pair, self.tail, self.rows, self.cols, 4, self.sgc, self.cb, xq, xs,
+                                       s0, s1)
+            out[s0 * 16:min(s1 * 16, self.rows)] = o[s0 * 16:min(s1 * 16, self.rows)]
+
+        ths = [threading.Thread(target=work, args=(a, min(stripes, a + per))) for a in range(0, stripes, per)]
+        for t in ths:
+            t.start()
+        for t in ths:
+            t.join()
+        return out
+
     def row_rotated(self, r):
         if self.fmt == "n4":
             return O.nibble4_dequant_row(self.pair, self.tail, self.rows, self.cols, self.hp, r)
@@ -58,7 +81,11 @@ def quantize_matrix(W, fmt, planes=4, sgc=2, interleave_gate_up=False):
 
 
 class OracleModel:
-    def __init__(self, cfg, layers, head, final_norm):
+    """`gemv_threads` > 0 switches every projection to the threaded portable path (the
+    timed CPU baseline); 0 keeps the NEON-semantics integer path (the parity oracle)."""
+
+    def __init__(self, cfg, layers, head, final_norm, gemv_threads=0):
+        self.gemv_threads = gemv_threads
         self.cfg = cfg
         self.layers = layers  # dicts: qkv, o, gu, down (Matrix), in_norm, post_norm, bias
         self.head = head
@@ -69,6 +96,11 @@ class OracleModel:
         self.ks = np.zeros((L, nkv, cap), np.float32)
         self.vs = np.zeros((L, nkv, cap), np.float32)
         self.pos = 0
+
+    def _gemv(self, m, xq, xs, xsum):
+        if self.gemv_threads:
+            return m.gemv_portable(xq, xs, self.gemv_threads)
+        return m.gemv(xq, xs, xsum)
 
     def embed(self, token):
         return O.ifwht64(self.head.row_rotated(token))
@@ -83,7 +115,7 @@ class OracleModel:
         hidden = self.embed(token).astype(np.float32)
         for li, L in enumerate(self.layers):
             xq, xs, xsum = O.populate_fwht(hidden, L["in_norm"], O.inv_rms(hidden, eps))
-            qkv = L["qkv"].gemv(xq, xs, xsum).reshape(-1, hd)
+            qkv = self._gemv(L["qkv"], xq, xs, xsum).reshape(-1, hd)
             if L.get("bias") is not None:
                 qkv = (qkv + L["bias"].reshape(-1, hd)).astype(np.float32)
             for h in range(nq + nkv):
@@ -98,15 +130,15 @@ class OracleModel:
                 outs.append(O.attn_q8_head(qkv[qh], self.kq[li, kvh, :pos + 1], self.ks[li, kvh, :pos + 1],
                                            self.vq[li, kvh, :pos + 1], self.vs[li, kvh, :pos + 1], scale))
             aq, as_, asum = O.populate_fwht(np.concatenate(outs))
-            hidden = (hidden + L["o"].gemv(aq, as_, asum)).astype(np.float32)
+            hidden = (hidden + self._gemv(L["o"], aq, as_, asum)).astype(np.float32)
             xq, xs, xsum = O.populate_fwht(hidden, L["post_norm"], O.inv_rms(hidden, eps))
-            gu = L["gu"].gemv(xq, xs, xsum).reshape(-1, 128)
+            gu = self._gemv(L["gu"], xq, xs, xsum).reshape(-1, 128)
             sw = np.concatenate([O.swiglu(gu[ic, :64], gu[ic, 64:]) for ic in range(inter // 64)])
             iq, is_, isum = O.populate_fwht(sw)
-            hidden = (hidden + L["down"].gemv(iq, is_, isum)).astype(np.float32)
+            hidden = (hidden + self._gemv(L["down"], iq, is_, isum)).astype(np.float32)
         xq, xs, xsum = O.populate_fwht(hidden, self.final_norm, O.inv_rms(hidden, eps))
         self.pos += 1
-        return self.head.gemv(xq, xs, xsum)
+        return self._gemv(self.head, xq, xs, xsum)
 
 
 def random_model(cfg, seed, fmt="nf4", planes=None):
