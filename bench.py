@@ -15,7 +15,6 @@ import argparse
 import json
 import os
 import sys
-import threading
 import time
 
 import numpy as np
@@ -35,6 +34,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list of GEMV case names to run (profiling)")
     ap.add_argument("--decode-only", action="store_true", help="skip the GEMV sweep and the 135M run (profiling)")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="also run 3 plain device copies of MB MiB (HBM counter calibration)")
     return ap.parse_args()
 
 
@@ -119,49 +120,6 @@ def time_case(ctx, torch, case, steps, warmup):
     return a.elapsed_time(b) * 1e-3 / steps
 
 
-def cpu_baseline(case, seconds=10.0):
-    """Reference portable path restated in C (oracle nf_gemv_portable / nibble4 portable):
-    dequantize each row, fp32 dot per chunk.  Stripe ranges split over host threads."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
-    rows, cols = case.rows, case.cols
-    q = case.q[0].cpu().numpy()
-    s = case.s[0].cpu().numpy()
-    stripes = (rows + 15) // 16
-    threads = min(16, os.cpu_count() or 1)
-    out = np.zeros(rows, np.float32)
-
-    def work(s0, s1):
-        o = np.zeros(rows, np.float32)
-        if case.fmt == "b6":
-            o = O.nibble4_gemv_portable(case.pair_host, case.tail_host, rows, cols, 2, q, s, s0, s1)
-        else:
-            o = O.nf_gemv_portable(case.pair_host, case.tail_host, rows, cols, 4, 2, case.cb, q, s, s0, s1)
-        out[s0 * 16:min(s1 * 16, rows)] = o[s0 * 16:min(s1 * 16, rows)]
-
-    def one_pass():
-        per = (stripes + threads - 1) // threads
-        per += per & 1
-        ths = [threading.Thread(target=work, args=(a, min(stripes, a + per))) for a in range(0, stripes, per)]
-        for t in ths:
-            t.start()
-        for t in ths:
-            t.join()
-
-    t0 = time.perf_counter()
-    one_pass()
-    first = time.perf_counter() - t0
-    reps = max(1, int(seconds / max(first, 1e-3)))
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        one_pass()
-    dt = (time.perf_counter() - t0) / reps
-    return {"value": round(case.bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{case.name} full matrix x{reps} passes, portable dequantize+fp32-dot path "
-                      f"(simd_lut.rs:5719-5748), {threads} host threads over stripe ranges",
-            "ms_per_gemv": round(dt * 1e3, 3)}
-
-
 def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log):
     import k2t
     t0 = time.perf_counter()
@@ -194,7 +152,30 @@ def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log):
     return model, mats, host, res
 
 
-def cpu_decode_baseline(cfg, host, ntok=2):
+def load_traffic(kernel_case):
+    """HBM bytes per launch of the roofline kernel, from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a
+    plain copy of known size).  None when no summary for this case is committed."""
+    path = os.path.join(ROOT, "profiles", f"gemv_{kernel_case}_hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for ln in open(path):
+        if ln.startswith("traffic_bytes_per_launch:"):
+            return int(float(ln.split(":", 1)[1]))
+    return None
+
+
+def copy_probe(torch, mib):
+    """Three plain device-to-device copies of `mib` MiB (a kernel of known HBM traffic:
+    mib MiB read + mib MiB written) for scaling the PMC byte counters."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def cpu_decode_baseline(cfg, host, seconds=10.0, max_tokens=32):
     """The reference's portable CPU decode (dequantize + fp32 dot GEMVs over stripe ranges,
     real_llm.rs:829-836 / simd_lut.rs:5719-5748; scalar q8 attention) restated in the
     oracle, on this machine's host cores, for `ntok` tokens from an empty context."""
@@ -207,12 +188,14 @@ def cpu_decode_baseline(cfg, host, ntok=2):
     for i in range(cfg["n_layers"]):
         q, o, gu, dn = conv[4 * i:4 * i + 4]
         layers.append({"qkv": q, "o": o, "gu": gu, "down": dn, "in_norm": ones, "post_norm": ones, "bias": None})
-    om = OracleModel(dict(cfg, max_seq=ntok + 1), layers, conv[-1], ones, gemv_threads=threads)
+    om = OracleModel(dict(cfg, max_seq=max_tokens + 1), layers, conv[-1], ones, gemv_threads=threads)
     om.forward_token(1)  # warm
     om.pos = 0
     t0 = time.perf_counter()
-    for t in range(ntok):
-        om.forward_token(3 + t)
+    ntok = 0
+    while ntok < max_tokens and (ntok < 2 or time.perf_counter() - t0 < seconds):
+        om.forward_token(3 + ntok)
+        ntok += 1
     dt = (time.perf_counter() - t0) / ntok
     return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{ntok} decode tokens of the 1.7B nf4g128 model from an empty context on the portable "
@@ -259,6 +242,8 @@ def main():
                 dom = key
             del case
     line = {"metric": "quant GEMV HBM GB/s (% peak) + decode tok/s, 1.7B-shape nf4g128, 1 MI355X"}
+    if args.copy_probe:
+        copy_probe(torch, args.copy_probe)
     if args.only:
         line.update({"config": {"cases": results}})
         print(json.dumps(line))
@@ -298,7 +283,7 @@ def main():
                                "ffn 8192, vocab 49152), 256-token prefill in 4-token tiles then greedy decode",
                    "decode_1_7b_nf4g128": r17, "decode_135m_p55454_ctx512": r135, "gemv_sweep": results},
         "roofline": {"bound": "hbm", "kernel": f"gemv_kernel ({dom})", "achieved": dr["GB_s"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(dr["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(dr["GB_s"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom),
                      "algorithmic_bytes_per_launch": dr["bytes"], "avg_launch_us": dr["us"]},
         "cpu_baseline": cpu,
     })

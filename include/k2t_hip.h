@@ -6,7 +6,7 @@
  * its stripe-range leaf kernels (src/model/real_llm.rs:525-544, 711-892;
  * src/kernels/simd_lut.rs).  Each entry point below names the reference item
  * it replaces.  A Rust host binds this header with a plain `extern "C"` block
- * (see INTEGRATION.md); nothing here uses C++ or torch types.
+ * declaring the same signatures; nothing here uses C++ or torch types.
  *
  * Conventions (mirroring include/kronos_ffi.h and src/ffi/mobile_ffi.rs:101-168):
  *   - every function returns int32_t: 0 = ok, < 0 = error code (K2T_E_*);

@@ -49,7 +49,6 @@ struct GemvParams {
     int stripe_mode;  // 1: a workgroup owns one stripe (16 rows), 0: a stripe pair (32 rows)
     int exact;        // 1: replay the reference's fmaf chain from LDS-staged terms
     int accum;        // 1: out = out + result (residual add, real_llm.rs:7185-7188)
-    int dbg;
     uint32_t cb0, cb1, cb2, cb3;
 };
 
@@ -149,11 +148,10 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         for (int t = 0; t < NT; t++) {
 #pragma unroll
             for (int kk = 0; kk < 4; kk++)
-                fr.x[t][kk] = (P.dbg & 4) ? make_uint2(lane, kk)
-                                          : *reinterpret_cast<const uint2 *>(P.xq + (size_t)(tok0 + t) * P.K + c * 64 +
-                                                                             kk * 16 + half * 8);
-            fr.sx[t] = (P.dbg & 4) ? 1.0f : P.xs[(size_t)(tok0 + t) * P.nc + c];
-            if constexpr (FMT == 0) fr.sum[t] = (P.dbg & 4) ? 0 : P.xsum[(size_t)(tok0 + t) * P.nc + c];
+                fr.x[t][kk] = *reinterpret_cast<const uint2 *>(P.xq + (size_t)(tok0 + t) * P.K + c * 64 + kk * 16 +
+                                                               half * 8);
+            fr.sx[t] = P.xs[(size_t)(tok0 + t) * P.nc + c];
+            if constexpr (FMT == 0) fr.sum[t] = P.xsum[(size_t)(tok0 + t) * P.nc + c];
         }
     };
 
@@ -164,15 +162,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     for (int t = 0; t < NT; t++) f[t][0] = f[t][1] = 0.0f;
 
     auto process = [&](const Frag<HP, NT> &fr, int c) {
-        if (P.dbg & 2) {
-            uint32_t z = 0;
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) z ^= fr.w[kk].x ^ fr.w[kk].y ^ fr.w[kk].z ^ fr.w[kk].w;
-#pragma unroll
-            for (int kk = 0; kk < NH; kk++) z ^= fr.h[kk].x ^ fr.h[kk].w;
-            if (z == 0x9e3779b9u) terms[rloc] = make_float2(1.0f, (float)fr.ws);
-            return;
-        }
         int acc[NT][4];
 #pragma unroll
         for (int t = 0; t < NT; t++)
@@ -236,7 +225,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
                 }
             }
             const float sx = fr.sx[t];
-            if (P.dbg & 8) { if (r0 == 0x7fffffff) terms[0] = make_float2(sx, ws0); continue; }
             // The reference skips chunks whose activation scale is 0; fma(-0, +0, f) == f for
             // every f (signed zeros included), so such chunks stage an exactly neutral term.
             if (P.exact) {
@@ -308,7 +296,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         return;
     }
     __syncthreads();
-    if (P.dbg & 1) return;
     const int nrows_blk = (is_tail && !smode) ? 16 : RB;
     const int first_stripe = smode ? rb : (is_tail ? 2 * P.np : 2 * rb);
     // One thread per (token, row of the block) replays the chain; LDS reads are batched
@@ -447,14 +434,6 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
     P.lds_terms = 1;
     P.exact = ctx->exact;
     P.accum = accum ? 1 : 0;
-    {
-        static int dbg = -1;
-        if (dbg < 0) {
-            const char *e = getenv("K2T_GEMV_DEBUG");
-            dbg = e ? atoi(e) : 0;
-        }
-        P.dbg = dbg;
-    }
     if (groups > 0) {
         GemvParams Q = P;
         Q.tok_base = 0;
