@@ -85,4 +85,10 @@ __device__ __forceinline__ uint32_t bit7_mask(uint32_t v) {
     return __builtin_amdgcn_perm(0u, 0u, v & 0x80808080u);
 }
 
+// Byte mask 0xFF where bit 3 of the byte is set: selector 8 returns the sign of byte 1
+// of the second operand (0x80 -> 0xFF), selector 0 its byte 0 (0x00).
+__device__ __forceinline__ uint32_t bit3_mask(uint32_t v) {
+    return __builtin_amdgcn_perm(0u, 0x8000u, v & 0x08080808u);
+}
+
 }  // namespace k2t

@@ -77,7 +77,6 @@ struct Frag {
 // FMT 0: bit-plane Nibble4 with HP hi planes; FMT 1: NF4 codebook stripes.
 template <int FMT, int HP, int NT, bool DOTS>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
-    constexpr int U = NT == 1 ? 2 : 1;  // chunks fetched ahead per lane
     constexpr int NH = HP == 0 ? 1 : (HP == 1 ? 2 : 4);
     extern __shared__ float lds[];
     const uint32_t lane = threadIdx.x & 63;
@@ -193,7 +192,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
                         hi |= __builtin_rotateright32(hd[j], (e + 1u) & 31u) & 0x10101010u;
                     }
                 } else {
-                    lo = lut16(d & 0x07070707u, bit7_mask(d << 4), P.cb0, P.cb1, P.cb2, P.cb3);
+                    lo = lut16(d & 0x07070707u, bit3_mask(d), P.cb0, P.cb1, P.cb2, P.cb3);
                     hi = lut16((d >> 4) & 0x07070707u, bit7_mask(d), P.cb0, P.cb1, P.cb2, P.cb3);
                 }
 #pragma unroll
@@ -240,21 +239,27 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         }
     };
 
-    // Chunk of iteration i for this lane group: granules of `gr` chunks dealt round-robin.
-    const int gr = FMT == 1 ? P.sgc : 1;
-    auto chunk_of = [&](int i) { return cw0 + ((i / gr) * G + q) * gr + (i % gr); };
-    const int iters = ((cw1 - cw0 + G * gr - 1) / (G * gr)) * gr;  // wave-uniform
-    for (int ib = 0; ib < iters; ib += U) {
-        Frag<HP, NT> fr[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int c = chunk_of(ib + u);
-            if (ib + u < iters && c < cw1) fetch(fr[u], c);
+    // Chunk of iteration i for this lane group: chunks dealt round-robin over the groups.
+    auto chunk_of = [&](int i) { return cw0 + i * G + q; };
+    const int iters = (cw1 - cw0 + G - 1) / G;  // wave-uniform
+    auto valid = [&](int i) { return i < iters && chunk_of(i) < cw1; };
+    if constexpr (NT == 1) {
+        // Two fragments in flight: chunk i+1 is fetched before chunk i is processed.
+        Frag<HP, NT> fa, fb;
+        if (valid(0)) fetch(fa, chunk_of(0));
+        for (int i = 0; i < iters; i += 2) {
+            if (valid(i + 1)) fetch(fb, chunk_of(i + 1));
+            if (valid(i)) process(fa, chunk_of(i));
+            if (valid(i + 2)) fetch(fa, chunk_of(i + 2));
+            if (valid(i + 1)) process(fb, chunk_of(i + 1));
         }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int c = chunk_of(ib + u);
-            if (ib + u < iters && c < cw1) process(fr[u], c);
+    } else {
+        // Multi-token tiles hold NT activation slices per fragment: one in flight.
+        for (int i = 0; i < iters; i++) {
+            if (!valid(i)) continue;
+            Frag<HP, NT> fa;
+            fetch(fa, chunk_of(i));
+            process(fa, chunk_of(i));
         }
     }
 
@@ -339,20 +344,14 @@ GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1) {
     }
     const int nrb = std::max(p.rb_hi - p.rb_lo, 1);
     const int G = p.stripe_mode ? 8 : 4;  // lane groups per wave
-    const int step = m->fmt == K2T_FMT_NF ? m->sgc : 1;  // keep NF scale groups whole
-    // Short-lived waves that each fetch all their records in one batch stream best
-    // (~14 waves per CU, <= 2 records per lane group).  Shrink the per-wave chunk count
-    // when the matrix has too few row blocks to reach that many waves.
-    // A wave's lane groups take `gr`-chunk granules round-robin; one full round keeps
-    // every lane busy.  Waves fetch at most two rounds in one batch: short-lived waves
-    // that issue all their loads up front stream best (~14 waves per CU).  Small matrices
-    // keep one full round per wave rather than many mostly idle waves.
+    // A wave's lane groups take chunks round-robin; one full round keeps every lane busy.
+    // Short-lived waves of at most two rounds stream best (~14 waves per CU).  Small
+    // matrices keep one full round per wave rather than many mostly idle waves.
     const int target = ctx->num_cus * 14;
-    const int round = G * step;
+    const int round = G;
     int cps = (long)nrb * ((m->nc + 2 * round - 1) / (2 * round)) >= target ? 2 * round : round;
     cps = std::max(cps, (m->nc + 15) / 16);  // at most 16 waves per workgroup
     if (ctx->max_segments > 0) cps = std::max(cps, (m->nc + ctx->max_segments - 1) / ctx->max_segments);
-    cps = (cps + step - 1) / step * step;
     p.cps = cps;
     p.nseg = (m->nc + cps - 1) / cps;
     return p;
