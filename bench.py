@@ -126,6 +126,8 @@ def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log):
     model, mats, host = k2t.build_random_model(ctx, cfg, max_seq=prefill + warmup + steps + 8, fmt=fmt,
                                                seed=7, max_batch=256, keep_host=True, threads=0)
     t_build = time.perf_counter() - t0
+    if os.environ.get("K2T_MODEL_EXACT"):
+        model.set_exact(int(os.environ["K2T_MODEL_EXACT"]))
     wbytes = sum(m.info()[3] for m in mats)
     rng = np.random.default_rng(SEED)
     toks = rng.integers(0, cfg["vocab"], prefill).astype(np.int32)

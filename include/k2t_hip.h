@@ -214,8 +214,16 @@ int32_t k2t_model_set_layer(k2t_model *m, int32_t layer, const k2t_mat *qkv, con
 int32_t k2t_model_set_head(k2t_model *m, const k2t_mat *lm_head, const float *final_norm);
 /* 1 (default): capture the decode step once and replay it as a HIP graph. */
 int32_t k2t_model_set_graph(k2t_model *m, int32_t enable);
-/* GEMV epilogue of this model's steps (see k2t_ctx_set_exact); default 1 = exact. */
+/* GEMV epilogue of this model's steps (see k2t_ctx_set_exact); default 0 = fast.
+ * exact = 1 also disables the persistent decode kernel (it sums per-segment chains). */
 int32_t k2t_model_set_exact(k2t_model *m, int32_t exact);
+/* 1: a decode step runs as one persistent kernel (one workgroup per CU) whose
+ * phases hand vectors over through {payload, epoch} words instead of kernel boundaries:
+ * the shape of forward_token_sdot_megakernel (real_llm.rs:6794-7403).  0 (default): one
+ * kernel per operation.  Used only where the device and model shape allow it (see
+ * k2t_model_persistent_active). */
+int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable);
+int32_t k2t_model_persistent_active(const k2t_model *m, int32_t *active);
 /* reset_context: position back to 0. */
 int32_t k2t_model_reset(k2t_model *m);
 int32_t k2t_model_position(const k2t_model *m, int32_t *pos);

@@ -216,6 +216,15 @@ int32_t k2t_ctx_create(int32_t device, k2t_ctx **out) {
         int cus = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
             c->num_cus = cus;
+        uint64_t masks[kSignBlocks];
+        for (int b = 0; b < kSignBlocks; b++) masks[b] = hadamard_sign_mask_host((uint64_t)b);
+        hipError_t e = hipMalloc(&c->signs, sizeof(masks));
+        if (e == hipSuccess) e = hipMemcpy(c->signs, masks, sizeof(masks), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            if (c->signs) (void)hipFree(c->signs);
+            delete c;
+            hip_check(e, "sign table");
+        }
         *out = c;
     });
 }
@@ -226,6 +235,7 @@ void k2t_ctx_destroy(k2t_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->rms_scratch) (void)hipFree(ctx->rms_scratch);
+    if (ctx->signs) (void)hipFree(ctx->signs);
     delete ctx;
 }
 

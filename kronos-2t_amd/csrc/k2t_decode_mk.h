@@ -1,0 +1,42 @@
+// Host/device interface of the persistent single-launch decode kernel (k2t_decode_mk.hip).
+#pragma once
+#include "../../include/k2t_hip.h"
+#include "k2t_gemv_core.h"
+#include "k2t_internal.h"
+
+namespace k2t {
+
+struct MkLayer {
+    MatDev qkv, o, gu, down;
+    const float *in_norm, *post_norm, *bias;
+};
+
+struct MkParams {
+    const MkLayer *layers;
+    int L;
+    MatDev head;
+    const float *final_norm;
+    int d, nq, nkv, hd, inter, vocab, max_seq, kmax;
+    float eps, attn_scale;
+    const float *rope;
+    const int *pos_dev;
+    const int *tokens;
+    const uint32_t *step_dev;
+    int8_t *kq, *vq;
+    float *ks, *vs;
+    // hand-off vectors as {payload, epoch} words
+    unsigned long long *HA, *HB, *QKV, *OACT, *GACT;
+    float *logits;
+    int *err;
+    uint32_t spin_limit;
+    unsigned long long *trace;  // optional: [wg][layer*6 + phase][3] timestamps (profiling)
+};
+
+// pair_mode_nseg4: gate_up layout (4 wave groups = one [gate64, up64] block of 4 pairs).
+MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4);
+size_t decode_mk_lds_bytes(const k2t_model_config &c);
+bool decode_mk_supported(const k2t_model_config &c, int num_cus);
+void launch_decode_mk(hipStream_t st, const MkParams &P, int num_cus, size_t lds);
+void launch_advance_step(hipStream_t st, int *pos, uint32_t *step, int n);
+
+}  // namespace k2t

@@ -1,0 +1,589 @@
+// Persistent single-launch decode step for gfx950: the reference's decode megakernel
+// (forward_token_sdot_megakernel, real_llm.rs:6794-7403) as one HIP kernel of one
+// workgroup per CU.
+//
+// The reference runs its phases on a thread pool with a barrier between them.  On
+// MI355X a grid barrier is the expensive part (device-scope fences write back the L2 of
+// every XCD), so the phases here are linked by data instead: every vector handed from one
+// phase to the next is stored as 64-bit words {32-bit payload, 32-bit epoch}, written and
+// read with agent-scope atomics (coherent across XCDs, no fence needed because payload
+// and flag travel in one word).  A consumer polls exactly the words it needs until their
+// epoch matches the current (step, layer, phase); a workgroup with no task in a phase
+// goes on to the next one and starts streaming its weights early.  Every poll is bounded:
+// on timeout the kernel raises an error flag and all workgroups exit.
+//
+// Phases per layer (real_llm.rs:6929-7333):
+//   1 qkv   : RMSNorm + FWHT + int8 of hidden (built per workgroup in LDS), qkv GEMV
+//   2 attn  : per q head: bias, RoPE, int8 Hadamard K/V of this position (stored by the
+//             first q head of each KV group), q8 attention over the cache, IFWHT, FWHT
+//             with the o_proj chunk index, int8 -> o activation chunks
+//   3 o     : o_proj GEMV, hidden_mid = hidden + o
+//   4 gu    : RMSNorm + FWHT + int8 of hidden_mid, gate_up GEMV of one [gate64, up64]
+//             block per task, SwiGLU + FWHT (chunk ic) + int8 -> down activation chunks
+//   5 down  : down GEMV, hidden = hidden_mid + down
+// then the final norm and lm_head GEMV (logits); argmax and the position advance run as
+// ordinary kernels after it.
+#include <float.h>
+#include <math.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "../../include/k2t_hip.h"
+#include "k2t_decode_mk.h"
+#include "k2t_gemv_core.h"
+#include "k2t_internal.h"
+
+namespace k2t {
+
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kActWords = 18;  // per 64-element activation chunk: 16 code words, scale, sum
+
+__device__ __forceinline__ void ll_store(unsigned long long *p, uint32_t v, uint32_t epoch) {
+    __hip_atomic_store(p, ((unsigned long long)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long ll_load(const unsigned long long *p) {
+    return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls one word until its epoch matches; false on timeout or when another workgroup
+// has raised the error flag.
+__device__ bool ll_wait(const MkParams &P, const unsigned long long *p, uint32_t epoch, uint32_t &v) {
+    for (uint32_t spins = 0;; spins++) {
+        const unsigned long long w = ll_load(p);
+        if ((uint32_t)(w >> 32) == epoch) {
+            v = (uint32_t)w;
+            return true;
+        }
+        if ((spins & 31u) == 31u) {
+            if (__hip_atomic_load(P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return false;
+            if (spins > P.spin_limit) {
+                __hip_atomic_store(P.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return false;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+}
+
+struct Lds {
+    float *hbuf;     // [d] fp32 vector being normalised
+    int8_t *xl;      // [kmax] int8 activation of the current GEMV
+    float *xsl;      // [kmax/64]
+    int32_t *xsuml;  // [kmax/64]
+    float *part;     // [16][32] wave partials
+    float *vec;      // [128] gate_up block / attention vectors
+    float *att;      // attention scratch: q, k, v f32 [3*hd], int8 q/k/v [3*hd], opart, scores
+    int *flag;       // [4] workgroup flags
+};
+
+__host__ __device__ constexpr size_t pad16(size_t b) { return (b + 15) / 16 * 16; }
+
+__device__ Lds carve(const MkParams &P, float *base) {
+    Lds L;
+    char *p = reinterpret_cast<char *>(base);
+    L.hbuf = reinterpret_cast<float *>(p);
+    p += pad16((size_t)P.d * 4);
+    L.xl = reinterpret_cast<int8_t *>(p);
+    p += pad16((size_t)P.kmax);
+    L.xsl = reinterpret_cast<float *>(p);
+    p += pad16((size_t)(P.kmax / 64) * 4);
+    L.xsuml = reinterpret_cast<int32_t *>(p);
+    p += pad16((size_t)(P.kmax / 64) * 4);
+    L.part = reinterpret_cast<float *>(p);
+    p += kWaves * 32 * 4;
+    L.vec = reinterpret_cast<float *>(p);
+    p += 128 * 4;
+    L.flag = reinterpret_cast<int *>(p);
+    p += 16;
+    L.att = reinterpret_cast<float *>(p);
+    return L;
+}
+
+// Waits for an fp32 vector of n LL words and copies it to LDS.  Returns false (for the
+// whole workgroup) on error.
+__device__ bool load_vec(const MkParams &P, const Lds &S, const unsigned long long *src, int n, uint32_t epoch,
+                         float *dst) {
+    bool ok = true;
+    for (int i = (int)threadIdx.x; i < n; i += kThreads) {
+        uint32_t v = 0;
+        if (!ll_wait(P, src + i, epoch, v)) {
+            ok = false;
+            break;
+        }
+        dst[i] = __uint_as_float(v);
+    }
+    if (threadIdx.x == 0) S.flag[0] = 0;
+    __syncthreads();
+    if (!ok) S.flag[0] = 1;
+    __syncthreads();
+    return S.flag[0] == 0;
+}
+
+// Waits for nch int8 activation chunks (kActWords LL words each) and unpacks them into
+// the LDS activation (codes, scales, sums).
+__device__ bool load_act(const MkParams &P, const Lds &S, const unsigned long long *src, int nch, uint32_t epoch) {
+    bool ok = true;
+    for (int i = (int)threadIdx.x; i < nch * kActWords; i += kThreads) {
+        uint32_t v = 0;
+        if (!ll_wait(P, src + i, epoch, v)) {
+            ok = false;
+            break;
+        }
+        const int c = i / kActWords, w = i % kActWords;
+        if (w < 16) reinterpret_cast<uint32_t *>(S.xl + c * 64)[w] = v;
+        else if (w == 16) S.xsl[c] = __uint_as_float(v);
+        else S.xsuml[c] = (int32_t)v;
+    }
+    if (threadIdx.x == 0) S.flag[0] = 0;
+    __syncthreads();
+    if (!ok) S.flag[0] = 1;
+    __syncthreads();
+    return S.flag[0] == 0;
+}
+
+// Quantizes the 64 rotated values held one per lane and stores the chunk as kActWords
+// LL words (simd_lut.rs:3097-3128 arithmetic, as quant_chunk_store).
+__device__ void store_act_chunk(float v, uint32_t lane, unsigned long long *dst, uint32_t epoch) {
+    const float mx = wave_max_f(fabsf(v));
+    int qi = 0;
+    float scale = 0.0f;
+    if (mx > FLT_EPSILON) {
+        const float inv = 127.0f / mx;
+        qi = (int)rintf(v * inv);
+        scale = mx / 127.0f;
+    }
+    const int s = wave_sum_i(qi);
+    // pack four lanes' codes per word: lane 4w + b -> byte b of word w
+    const uint32_t byte = (uint32_t)qi & 0xFFu;
+    uint32_t word = byte << (8 * (lane & 3u));
+    word |= __shfl_xor(word, 1, kWave);
+    word |= __shfl_xor(word, 2, kWave);
+    if ((lane & 3u) == 0) ll_store(dst + lane / 4, word, epoch);
+    if (lane == 0) {
+        ll_store(dst + 16, __float_as_uint(scale), epoch);
+        ll_store(dst + 17, (uint32_t)s, epoch);
+    }
+}
+
+// RMSNorm + FWHT + int8 of S.hbuf[0..d) into the LDS activation: wave 0 computes inv_rms
+// in row_sumsq_wave order (bit-identical to rmsnorm_act_kernel), then one wave per chunk.
+__device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, uint32_t lane, int wave) {
+    if (wave == 0) {
+        const float ss = row_sumsq_wave(S.hbuf, P.d, lane);
+        if (lane == 0) S.vec[0] = 1.0f / sqrtf(ss / (float)P.d + P.eps);
+    }
+    __syncthreads();
+    const float inv_rms = S.vec[0];
+    for (int c = wave; c < P.d / 64; c += kWaves) {
+        const float v = (S.hbuf[c * 64 + lane] * inv_rms) * w[c * 64 + lane];
+        quant_chunk_store(fwht_lane(v, (uint64_t)c, lane), lane, S.xl + c * 64, S.xsl + c, S.xsuml + c);
+    }
+    __syncthreads();
+}
+
+// One round of matrix M's row blocks for this wave (dispatch over the weight formats).
+__device__ __forceinline__ void gemv_wave_any(const MatDev &M, int rb, bool active, int wseg, uint32_t lane,
+                                              const Lds &S, float *part) {
+    if (M.fmt == 1) gemv_wave<1, 0>(M, rb, active, wseg, lane, S.xl, S.xsl, S.xsuml, part);
+    else if (M.hp == 0) gemv_wave<0, 0>(M, rb, active, wseg, lane, S.xl, S.xsl, S.xsuml, part);
+    else if (M.hp == 1) gemv_wave<0, 1>(M, rb, active, wseg, lane, S.xl, S.xsl, S.xsuml, part);
+    else gemv_wave<0, 2>(M, rb, active, wseg, lane, S.xl, S.xsl, S.xsuml, part);
+}
+
+// Row r of the tied lm_head, dequantized in the rotated domain and inverse-rotated
+// (embed_token_into, real_llm.rs:8063-8097), chunk c, element `lane`.
+__device__ float embed_value(const MatDev &M, int r, int c, uint32_t lane) {
+    const int stripe = r / 16, rl = r % 16, g = rl / 4, j = rl % 4;
+    const int k = lane / 16, w = lane % 16, half = w / 8, sub = w / 4, t = w % 4;
+    const bool in_pair = stripe < 2 * M.np;
+    const int side = stripe & 1;
+    float val;
+    if (M.fmt == 0) {
+        const int hp = M.hp;
+        const size_t prec = 1024 + 256 * (size_t)hp + 64, trec = 512 + 128 * (size_t)hp + 32;
+        const uint8_t *base = in_pair ? M.pair + ((size_t)(stripe / 2) * M.nc + c) * prec : M.tail + (size_t)c * trec;
+        const uint8_t *d = base + (in_pair ? side * 512 : 0);
+        const uint8_t *h = base + (in_pair ? 1024 + side * 128 * hp : 512);
+        const uint8_t *sp = base + (in_pair ? 1024 + 256 * hp + side * 32 : 512 + 128 * hp);
+        const uint8_t byte = d[k * 128 + g * 32 + half * 16 + j * 4 + t];
+        int u = (w % 8) < 4 ? (byte & 0x0F) : (byte >> 4);
+        if (hp == 1) {
+            const uint8_t hb = h[(k / 2) * 64 + g * 16 + j * 4 + t];
+            const int bit = (k & 1) == 0 ? 4 + sub : sub;
+            u |= ((hb >> bit) & 1) << 4;
+        } else if (hp == 2) {
+            const int sh = sub == 0 ? 4 : sub == 1 ? 6 : sub == 2 ? 2 : 0;
+            const uint8_t hb = h[k * 64 + g * 16 + j * 4 + t];
+            u |= ((hb >> sh) & 3) << 4;
+        }
+        const float delta = __uint_as_float((uint32_t)(sp[rl * 2] | (sp[rl * 2 + 1] << 8)) << 16);
+        val = (float)(2 * u - ((1 << (4 + hp)) - 1)) * delta;
+    } else {
+        const int sg = c / M.sgc, cst = sg * M.sgc, sb = c - cst;
+        const uint8_t *gb = in_pair ? M.pair + (size_t)(stripe / 2) * M.ptot + (size_t)sg * 64 + (size_t)cst * 1024
+                                    : M.tail + (size_t)sg * 32 + (size_t)cst * 512;
+        const uint8_t *sp = gb + (in_pair ? side * 32 : 0);
+        const uint8_t *d = gb + (in_pair ? 64 + (size_t)sb * 1024 + side * 512 : 32 + (size_t)sb * 512);
+        const int sub4 = w / 4;
+        const uint8_t byte = d[k * 128 + g * 32 + (sub4 / 2) * 16 + j * 4 + t];
+        const int idx = (sub4 & 1) == 0 ? (byte & 0x0F) : (byte >> 4);
+        const uint32_t cbw = idx < 4 ? M.cb0 : idx < 8 ? M.cb1 : idx < 12 ? M.cb2 : M.cb3;
+        const int cv = (int)(int8_t)((cbw >> (8 * (idx & 3))) & 0xFF);
+        const float delta = __uint_as_float((uint32_t)(sp[rl * 2] | (sp[rl * 2 + 1] << 8)) << 16);
+        val = (float)cv * delta;
+    }
+    return ifwht_lane(val, (uint64_t)c, lane);
+}
+
+// Rotates one head (hd = 64 or 128, one or two blocks held as v0/v1 per lane) and
+// quantizes it with one scale (store_hadamard_q8_head, real_llm.rs:8282-8365).
+__device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t lane, int8_t *dst) {
+    const float r0 = fwht_lane(v0, 0, lane);
+    const float r1 = nb > 1 ? fwht_lane(v1, 1, lane) : 0.0f;
+    const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
+    if (mx <= FLT_EPSILON) {
+        dst[lane] = 0;
+        if (nb > 1) dst[64 + lane] = 0;
+        return 0.0f;
+    }
+    const float inv = 127.0f / mx;
+    dst[lane] = (int8_t)(int)rintf(r0 * inv);
+    if (nb > 1) dst[64 + lane] = (int8_t)(int)rintf(r1 * inv);
+    return mx / 127.0f;
+}
+
+// Attention of q head h for the current position (causal_gqa_group_q8,
+// real_llm.rs:8471-8594), ending with the o_proj activation chunks of this head.
+__device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &S, int layer, int h, int pos,
+                               uint32_t ep_in, uint32_t ep_out, uint32_t lane, int wave) {
+    const int hd = P.hd, nb = hd / 64, nq = P.nq, nkv = P.nkv;
+    const int group = nq / nkv, kvh = h / group;
+    float *qf = S.att, *kf = qf + hd, *vf = kf + hd;
+    int8_t *qi = reinterpret_cast<int8_t *>(vf + hd);
+    int8_t *kn = qi + 128, *vn = kn + 128;
+    float *scal = reinterpret_cast<float *>(vn + 128);  // qas, ks_new, vs_new, m, 1/L
+    float *red = scal + 8;                              // [32]
+    float *opart = red + 32;                            // [16 waves][hd]
+    float *sc = opart + kThreads * 4;                   // [max_seq]
+    // 1. this position's q, k, v (+ bias)
+    bool ok = true;
+    const int t = (int)threadIdx.x;
+    if (t < 3 * hd) {
+        const int part = t / hd, i = t % hd;
+        const int row = part == 0 ? h * hd + i : part == 1 ? (nq + kvh) * hd + i : (nq + nkv + kvh) * hd + i;
+        uint32_t v = 0;
+        ok = ll_wait(P, P.QKV + row, ep_in, v);
+        float f = __uint_as_float(v);
+        if (Ly.bias) f = f + Ly.bias[row];
+        qf[t] = f;  // qf, kf, vf are contiguous
+    }
+    if (t == 0) S.flag[0] = 0;
+    __syncthreads();
+    if (!ok) S.flag[0] = 1;
+    __syncthreads();
+    if (S.flag[0]) return false;
+    // 2. RoPE (real_llm.rs:9328-9361) on q and k, int8 Hadamard q / k / v
+    const size_t slot = ((size_t)layer * nkv + kvh) * P.max_seq + pos;
+    if (wave == 0) {
+        const float *rrow = P.rope + (size_t)pos * hd;
+        float q0 = qf[lane], q1 = nb > 1 ? qf[64 + lane] : 0.0f;
+        float k0 = kf[lane], k1 = nb > 1 ? kf[64 + lane] : 0.0f;
+        if (nb == 1) {
+            const uint32_t i = lane & 31u;
+            const float c = rrow[i], s = rrow[32 + i];
+            const float qo = __shfl_xor(q0, 32, kWave), ko = __shfl_xor(k0, 32, kWave);
+            q0 = lane < 32 ? q0 * c - qo * s : q0 * c + qo * s;
+            k0 = lane < 32 ? k0 * c - ko * s : k0 * c + ko * s;
+        } else {
+            const float c = rrow[lane], s = rrow[64 + lane];
+            const float a0 = q0, a1 = q1, b0 = k0, b1 = k1;
+            q0 = a0 * c - a1 * s;
+            q1 = a1 * c + a0 * s;
+            k0 = b0 * c - b1 * s;
+            k1 = b1 * c + b0 * s;
+        }
+        const float qs = quant_head(q0, q1, nb, lane, qi);
+        const float ksn = quant_head(k0, k1, nb, lane, kn);
+        const float vsn = quant_head(vf[lane], nb > 1 ? vf[64 + lane] : 0.0f, nb, lane, vn);
+        if (lane == 0) {
+            scal[0] = qs * P.attn_scale;
+            scal[1] = ksn;
+            scal[2] = vsn;
+        }
+        if (h % group == 0) {  // the first q head of the group stores this position's K/V
+            P.kq[slot * hd + lane] = kn[lane];
+            P.vq[slot * hd + lane] = vn[lane];
+            if (nb > 1) {
+                P.kq[slot * hd + 64 + lane] = kn[64 + lane];
+                P.vq[slot * hd + 64 + lane] = vn[64 + lane];
+            }
+            if (lane == 0) {
+                P.ks[slot] = ksn;
+                P.vs[slot] = vsn;
+            }
+        }
+    }
+    __syncthreads();
+    // 3. scores s_t = float(q8 . k8_t) * ks_t * (qs * scale), t <= pos
+    const int seq = pos + 1;
+    const size_t base = ((size_t)layer * nkv + kvh) * P.max_seq;
+    const float qas = scal[0];
+    float smax = -INFINITY;
+    for (int tt = t; tt < seq; tt += kThreads) {
+        const uint4 *kr = tt == pos ? reinterpret_cast<const uint4 *>(kn)
+                                    : reinterpret_cast<const uint4 *>(P.kq + (base + tt) * hd);
+        const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
+        int dot = 0;
+        for (int i = 0; i < hd / 16; i++) {
+            const uint4 a = kr[i], b = qr[i];
+            dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
+            dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
+            dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
+            dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
+        }
+        const float kscale = tt == pos ? scal[1] : P.ks[base + tt];
+        const float s = ((float)dot * kscale) * qas;
+        sc[tt] = s;
+        smax = fmaxf(smax, s);
+    }
+    smax = wave_max_f(smax);
+    if (lane == 0) red[wave] = smax;
+    __syncthreads();
+    float m = red[0];
+    for (int w2 = 1; w2 < kWaves; w2++) m = fmaxf(m, red[w2]);
+    __syncthreads();
+    float psum = 0.0f;
+    for (int tt = t; tt < seq; tt += kThreads) {
+        const float p = expf(sc[tt] - m);
+        sc[tt] = p * (tt == pos ? scal[2] : P.vs[base + tt]);  // p_t * vs_t
+        psum += p;
+    }
+    psum = wave_sum_f(psum);
+    if (lane == 0) red[16 + wave] = psum;
+    __syncthreads();
+    // 4. o = sum_t p_t vs_t v_t: thread = (position subset, 4-column group); the subsets
+    //    of one wave are added with lane shuffles, then the 16 waves' sums in wave order.
+    const int ncg = hd / 4, nps = kThreads / ncg;
+    const int cg = t % ncg, ps = t / ncg;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    for (int tt = ps; tt < seq; tt += nps) {
+        const int v = tt == pos ? *reinterpret_cast<const int *>(vn + cg * 4)
+                                : *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4);
+        const float wt = sc[tt];
+        a0 = fmaf(wt, (float)(int8_t)(v & 0xFF), a0);
+        a1 = fmaf(wt, (float)(int8_t)((v >> 8) & 0xFF), a1);
+        a2 = fmaf(wt, (float)(int8_t)((v >> 16) & 0xFF), a2);
+        a3 = fmaf(wt, (float)(int8_t)((v >> 24) & 0xFF), a3);
+    }
+    for (int m2 = ncg; m2 < 64; m2 <<= 1) {  // lanes l and l ^ m2 hold the same columns
+        a0 += __shfl_xor(a0, m2, kWave);
+        a1 += __shfl_xor(a1, m2, kWave);
+        a2 += __shfl_xor(a2, m2, kWave);
+        a3 += __shfl_xor(a3, m2, kWave);
+    }
+    if ((int)lane < ncg) {
+        opart[wave * hd + cg * 4 + 0] = a0;
+        opart[wave * hd + cg * 4 + 1] = a1;
+        opart[wave * hd + cg * 4 + 2] = a2;
+        opart[wave * hd + cg * 4 + 3] = a3;
+    }
+    __syncthreads();
+    if (t < hd) {
+        float acc = opart[t];
+        for (int w2 = 1; w2 < kWaves; w2++) acc += opart[w2 * hd + t];
+        float L = red[16];
+        for (int w2 = 1; w2 < kWaves; w2++) L += red[16 + w2];
+        qf[t] = acc * (1.0f / L);  // reuse qf for o
+    }
+    __syncthreads();
+    // 5. ifwht64 per block, then FWHT with the o_proj chunk index + int8 (real_llm.rs:7060-7084)
+    if (wave < nb) {
+        const float o = ifwht_lane(qf[wave * 64 + lane], (uint64_t)wave, lane);
+        const int c = h * nb + wave;
+        store_act_chunk(fwht_lane(o, (uint64_t)c, lane), lane, P.OACT + (size_t)c * kActWords, ep_out);
+    }
+    return true;
+}
+
+#define MK_TR(l, ph, k)                                                                             \
+    if (P.trace && threadIdx.x == 0)                                                                \
+        P.trace[(((size_t)blockIdx.x * (P.L + 1) + (l)) * 6 + (ph)) * 3 + (k)] = wall_clock64();
+
+// Phase kinds of the step's schedule: per layer kQkv, kAttn, kO, kGu, kDown; then kHead.
+enum PhaseKind { kQkv = 0, kAttn = 1, kO = 2, kGu = 3, kDown = 4, kHead = 5 };
+
+__global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
+    extern __shared__ float lds_raw[];
+    const Lds S = carve(P, lds_raw);
+    const uint32_t lane = threadIdx.x & 63u;
+    const int wave = (int)(threadIdx.x >> 6);
+    const int t = (int)threadIdx.x;
+    const uint32_t step = *P.step_dev;
+    const int pos = *P.pos_dev;
+    const uint32_t nph = 2u + 5u * (uint32_t)P.L;
+    auto E = [&](int ph) { return step * nph + (uint32_t)ph + 1u; };
+    const int d = P.d;
+    MK_TR(P.L, 5, 0)
+
+    // phase 0: embedding -> HA (one wave per 64-element chunk)
+    {
+        const int token = P.tokens[0];
+        for (int c = (int)blockIdx.x * kWaves + wave; c < d / 64; c += (int)gridDim.x * kWaves)
+            ll_store(P.HA + c * 64 + lane, __float_as_uint(embed_value(P.head, token, c, lane)), E(0));
+    }
+    // phases 1 .. 5L+1: a single GEMV body serves every matrix
+    for (int ph = 1; ph < (int)nph; ph++) {
+        const int l = (ph - 1) / 5;
+        const int kind = ph == (int)nph - 1 ? kHead : (ph - 1) % 5;
+        if (kind == kAttn) {
+            if ((int)blockIdx.x < P.nq) MK_TR(l, 1, 0)
+            for (int h = (int)blockIdx.x; h < P.nq; h += (int)gridDim.x)
+                if (!attention_head(P, P.layers[l], S, l, h, pos, E(ph - 1), E(ph), lane, wave)) return;
+            if ((int)blockIdx.x < P.nq) MK_TR(l, 1, 2)
+            continue;
+        }
+        const MkLayer &Ly = P.layers[kind == kHead ? 0 : l];
+        const MatDev &M = kind == kQkv ? Ly.qkv : kind == kO ? Ly.o : kind == kGu ? Ly.gu : kind == kDown ? Ly.down : P.head;
+        const int nblocks = M.smode ? M.stripes : M.np + (M.stripes & 1);
+        const int groups = kWaves / M.nseg;
+        if ((int)blockIdx.x * groups >= nblocks) continue;  // no task here: go on to the next phase
+        const int tr_ph = kind == kHead ? 0 : kind;
+        const int tr_l = kind == kHead ? P.L : l;
+        MK_TR(tr_l, tr_ph, 0)
+        // ---- input activation -> LDS
+        if (kind == kO || kind == kDown) {
+            if (!load_act(P, S, kind == kO ? P.OACT : P.GACT, kind == kO ? P.nq * P.hd / 64 : P.inter / 64, E(ph - 1)))
+                return;
+            MK_TR(tr_l, tr_ph, 1)
+        } else {
+            // qkv / head read HA (written one phase earlier: embedding or down); gate_up reads HB (o)
+            if (!load_vec(P, S, kind == kGu ? P.HB : P.HA, d, E(ph - 1), S.hbuf)) return;
+            MK_TR(tr_l, tr_ph, 1)
+            build_norm_act(P, S, kind == kQkv ? Ly.in_norm : kind == kGu ? Ly.post_norm : P.final_norm, lane, wave);
+        }
+        // ---- GEMV rounds
+        const int grp = wave / M.nseg, wseg = wave % M.nseg;
+        const int RB = M.smode ? 16 : 32;
+        bool ok = true;
+        for (int base = (int)blockIdx.x * groups; base < nblocks; base += (int)gridDim.x * groups) {
+            const int rb = base + grp;
+            gemv_wave_any(M, rb, rb < nblocks, wseg, lane, S, S.part + wave * 32);
+            __syncthreads();
+            if (t < groups * RB) {
+                const int g2 = t / RB, rl = t % RB, rb2 = base + g2;
+                if (rb2 < nblocks) {
+                    const bool tail = !M.smode && rb2 >= M.np;
+                    const int first_stripe = M.smode ? rb2 : (tail ? 2 * M.np : 2 * rb2);
+                    const int row = first_stripe * 16 + rl;
+                    if (rl < (tail ? 16 : RB) && row < M.rows) {
+                        const float *gp = S.part + (g2 * M.nseg) * 32;
+                        float acc = gp[rl];
+                        for (int w2 = 1; w2 < M.nseg; w2++) acc += gp[w2 * 32 + rl];
+                        if (kind == kHead) {
+                            P.logits[row] = acc;
+                        } else if (kind == kQkv) {
+                            ll_store(P.QKV + row, __float_as_uint(acc), E(ph));
+                        } else if (kind == kGu) {
+                            S.vec[t] = acc;  // the 4 groups = the 4 pairs of block ic
+                        } else {
+                            // residual: HB = HA + o (HA from phase ph-3), HA = HB + down (HB from ph-2)
+                            const unsigned long long *res = kind == kO ? P.HA : P.HB;
+                            const uint32_t er = kind == kO ? E(ph - 3) : E(ph - 2);
+                            uint32_t hv = 0;
+                            if (ok && !ll_wait(P, res + row, er, hv)) ok = false;
+                            ll_store((kind == kO ? P.HB : P.HA) + row, __float_as_uint(__uint_as_float(hv) + acc), E(ph));
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            if (kind == kGu) {
+                if (wave == 0) {
+                    const int ic = base / 4;
+                    const float g = S.vec[lane], u = S.vec[64 + lane];
+                    const float v = (g / (1.0f + expf(-g))) * u;  // real_llm.rs:9801-9805
+                    store_act_chunk(fwht_lane(v, (uint64_t)ic, lane), lane, P.GACT + (size_t)ic * kActWords, E(ph));
+                }
+                __syncthreads();
+            }
+        }
+        if (!ok) return;
+        MK_TR(tr_l, tr_ph, 2)
+    }
+}
+
+__global__ void advance_step_kernel(int *pos, uint32_t *step, int n) {
+    if (threadIdx.x == 0) {
+        pos[0] += n;
+        step[0] += 1u;
+    }
+}
+
+}  // namespace
+
+MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4) {
+    MatDev d{};
+    d.pair = m->pair;
+    d.tail = m->tail;
+    d.ptot = m->fmt == K2T_FMT_NF ? (m->pairs ? m->pair_len / m->pairs : 0) : 0;
+    d.rows = m->rows;
+    d.nc = m->nc;
+    d.np = m->pairs;
+    d.stripes = m->stripes;
+    d.fmt = m->fmt == K2T_FMT_NF ? 1 : 0;
+    d.hp = m->hp;
+    d.sgc = m->sgc;
+    d.cb0 = m->cb[0];
+    d.cb1 = m->cb[1];
+    d.cb2 = m->cb[2];
+    d.cb3 = m->cb[3];
+    if (pair_mode_nseg4) {  // 4 wave groups: the 4 pairs of one [gate64, up64] block
+        d.smode = 0;
+        d.nseg = kWaves / 4;
+    } else {
+        // Stripe mode with one round of the 8 lane groups per wave where K allows.
+        d.smode = 1;
+        const int want = (m->nc + 7) / 8;
+        int nseg = 1;
+        while (nseg < want && nseg < kWaves) nseg *= 2;
+        d.nseg = nseg;
+    }
+    d.cps = (m->nc + d.nseg - 1) / d.nseg;
+    return d;
+}
+
+size_t decode_mk_lds_bytes(const k2t_model_config &c) {
+    const size_t kmax = std::max(c.hidden, c.intermediate);
+    const size_t hd = c.head_dim;
+    size_t b = pad16((size_t)c.hidden * 4) + pad16(kmax) + 2 * pad16((kmax / 64) * 4) + kWaves * 32 * 4 + 128 * 4 + 16;
+    b += (3 * hd) * 4 + 3 * 128 + 8 * 4 + 32 * 4 + (size_t)kThreads * 4 * 4 + (size_t)c.max_seq * 4;
+    return (b + 255) / 256 * 256;
+}
+
+bool decode_mk_supported(const k2t_model_config &c, int num_cus) {
+    if (decode_mk_lds_bytes(c) > 64 * 1024) return false;
+    if (c.hidden > 8192 || c.intermediate > 32768) return false;
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_mk_kernel, kThreads, decode_mk_lds_bytes(c)) !=
+            hipSuccess ||
+        nb < 1)
+        return false;
+    return num_cus > 0;
+}
+
+void launch_decode_mk(hipStream_t st, const MkParams &P, int num_cus, size_t lds) {
+    hipLaunchKernelGGL(decode_mk_kernel, dim3(num_cus), dim3(kThreads), lds, st, P);
+    hip_check(hipGetLastError(), "decode megakernel launch");
+}
+
+void launch_advance_step(hipStream_t st, int *pos, uint32_t *step, int n) {
+    hipLaunchKernelGGL(advance_step_kernel, dim3(1), dim3(64), 0, st, pos, step, n);
+    hip_check(hipGetLastError(), "advance launch");
+}
+
+}  // namespace k2t

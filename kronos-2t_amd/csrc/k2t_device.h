@@ -1,6 +1,7 @@
 // Device helpers shared by the gfx950 kernels: Hadamard sign masks, wave-level
 // butterflies and reductions (DPP), BF16 decode and byte-table lookups.
 #pragma once
+#include <float.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -35,6 +36,20 @@ __device__ __forceinline__ int dpp_ror4(int v) { return __builtin_amdgcn_mov_dpp
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
 
+// Exchange with lane ^ 1, ^ 2 (DPP quad permutes) and ^ 4 (ds_swizzle bit mode).
+__device__ __forceinline__ float xchg1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float xchg2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float xchg4(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));
+}
+__device__ __forceinline__ int xchg1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int xchg2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ int xchg4(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x101F); }
+
 __device__ __forceinline__ float wave_max_f(float v) {
 #pragma unroll
     for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
@@ -49,6 +64,36 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
     for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
     return v;
+}
+
+// Sum of squares of a K-float row (K a multiple of 64) by one wave, in a fixed order:
+// lane l takes float4 l, l+64, ... four loads in flight, fmaf per component, then a
+// butterfly sum.  Every kernel that needs inv_rms uses this, so all agree bit for bit.
+__device__ __forceinline__ float row_sumsq_wave(const float *xt, int K, uint32_t lane) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(xt);
+    const int n4 = K / 4;
+    float ss = 0.0f;
+    int i = (int)lane;
+    for (; i + 192 < n4; i += 256) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = x4[i + 64 * u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            ss = fmaf(v[u].x, v[u].x, ss);
+            ss = fmaf(v[u].y, v[u].y, ss);
+            ss = fmaf(v[u].z, v[u].z, ss);
+            ss = fmaf(v[u].w, v[u].w, ss);
+        }
+    }
+    for (; i < n4; i += 64) {
+        const float4 v = x4[i];
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
+    return wave_sum_f(ss);
 }
 
 // In-register signed FWHT-64 over one wave (lane i holds element i): butterflies with
@@ -89,6 +134,40 @@ __device__ __forceinline__ uint32_t bit7_mask(uint32_t v) {
 // of the second operand (0x80 -> 0xFF), selector 0 its byte 0 (0x00).
 __device__ __forceinline__ uint32_t bit3_mask(uint32_t v) {
     return __builtin_amdgcn_perm(0u, 0x8000u, v & 0x08080808u);
+}
+
+// Quantizes the 64 values held one per lane (already rotated) to int8 with one scale
+// (simd_lut.rs:3097-3128 / 3172-3195).
+__device__ __forceinline__ void quant_chunk_store(float v, uint32_t lane, int8_t *q, float *scale,
+                                                  int32_t *sum) {
+    const float mx = wave_max_f(fabsf(v));
+    if (mx <= FLT_EPSILON) {
+        q[lane] = 0;
+        if (lane == 0) {
+            *scale = 0.0f;
+            *sum = 0;
+        }
+        return;
+    }
+    const float inv = 127.0f / mx;
+    const int qi = (int)rintf(v * inv);
+    const int s = wave_sum_i(qi);
+    q[lane] = (int8_t)qi;
+    if (lane == 0) {
+        *scale = mx / 127.0f;
+        *sum = s;
+    }
+}
+
+__device__ __forceinline__ float fwht_lane(float v, uint64_t block, uint32_t lane) {
+    v = flip_sign(v, hadamard_sign_bit(block, lane)) * 0.125f;
+    return wave_butterflies64(v, lane);
+}
+
+// hadamard.rs:193-228 on one block held one element per lane.
+__device__ __forceinline__ float ifwht_lane(float v, uint64_t block, uint32_t lane) {
+    v = wave_butterflies64(v, lane);
+    return flip_sign(v * 0.125f, hadamard_sign_bit(block, lane));
 }
 
 }  // namespace k2t

@@ -5,12 +5,15 @@
 // a HIP graph and replayed.
 #include <float.h>
 #include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
 #include <vector>
 
 #include "../../include/k2t_hip.h"
+#include "k2t_decode_mk.h"
 #include "k2t_internal.h"
 
 namespace k2t {
@@ -114,9 +117,17 @@ struct k2t_model {
     int32_t *xsum = nullptr;
     int pos = 0;
     bool use_graph = true;
-    int exact = 1;  // GEMV epilogue mode used by this model's steps
+    int exact = 0;  // GEMV epilogue mode used by this model's steps
     hipGraphExec_t graph = nullptr;
     std::vector<void *> allocs;
+    // persistent single-launch decode step (fast epilogue only; opt-in)
+    bool persistent = false;
+    bool mk_ok = false;
+    size_t mk_lds = 0;
+    uint32_t *step_dev = nullptr;
+    int *err_dev = nullptr;
+    unsigned long long *ll_ha = nullptr, *ll_hb = nullptr, *ll_qkv = nullptr, *ll_oact = nullptr, *ll_gact = nullptr;
+    MkLayer *mk_layers = nullptr;
 };
 
 namespace {
@@ -182,24 +193,46 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
     const float attn_scale = 1.0f / sqrtf((float)hd);
     const int nsplit = attn_max_splits(c.max_seq);
     launch_embed(st, m->head, m->tokens, ntok, m->hidden);
+    // One token: the RMSNorm / SwiGLU + FWHT + int8 activations are built inside the GEMVs
+    // (each wave for its own chunks); batches use the standalone kernels.  Same codes.
+    const bool fused = ntok == 1;
+    static int skip = getenv("K2T_SKIP") ? atoi(getenv("K2T_SKIP")) : 0;  // TEMP timing probe
     for (int l = 0; l < c.n_layers; l++) {
         const auto &L = m->layers[l];
-        launch_rmsnorm_act(st, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
-        launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false);
+        if (fused && skip) {
+            if (!(skip & 1)) launch_gemv_fused(ctx, L.qkv, K2T_XS_RMSNORM, m->hidden, L.in_norm, c.rms_eps, m->qkv, false);
+            if (!(skip & 2)) launch_qkv_post(st, m->qkv, L.bias, m->rope, m->pos_dev, nq, nkv, hd, ntok, l, c.max_seq, m->kq, m->vq, m->ks, m->vs);
+            if (!(skip & 4)) launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, m->pos_dev, l, nq, nkv, hd,
+                         c.max_seq, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum);
+            if (!(skip & 8)) launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
+            if (!(skip & 16)) launch_gemv_fused(ctx, L.gu, K2T_XS_RMSNORM, m->hidden, L.post_norm, c.rms_eps, m->gu, false);
+            if (!(skip & 32)) launch_gemv_fused(ctx, L.down, K2T_XS_SWIGLU, m->gu, nullptr, 0.0f, m->hidden, true);
+            continue;
+        }
+        if (fused) {
+            launch_gemv_fused(ctx, L.qkv, K2T_XS_RMSNORM, m->hidden, L.in_norm, c.rms_eps, m->qkv, false);
+        } else {
+            launch_rmsnorm_act(st, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
+            launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false);
+        }
         launch_qkv_post(st, m->qkv, L.bias, m->rope, m->pos_dev, nq, nkv, hd, ntok, l, c.max_seq, m->kq, m->vq, m->ks,
                         m->vs);
         launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, m->pos_dev, l, nq, nkv, hd,
                          c.max_seq, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum);
         launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
-        launch_rmsnorm_act(st, m->hidden, L.post_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
-        launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false);
-        launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum);
-        launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
+        if (fused) {
+            launch_gemv_fused(ctx, L.gu, K2T_XS_RMSNORM, m->hidden, L.post_norm, c.rms_eps, m->gu, false);
+            launch_gemv_fused(ctx, L.down, K2T_XS_SWIGLU, m->gu, nullptr, 0.0f, m->hidden, true);
+        } else {
+            launch_rmsnorm_act(st, m->hidden, L.post_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
+            launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false);
+            launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum);
+            launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
+        }
     }
     if (with_logits) {
         const float *last = m->hidden + (size_t)(ntok - 1) * d;
-        launch_rmsnorm_act(st, last, m->final_norm, c.rms_eps, d, 1, m->xq, m->xs, m->xsum);
-        launch_gemv_ex(ctx, m->head, m->xq, m->xs, m->xsum, 1, m->logits, c.vocab, false);
+        launch_gemv_fused(ctx, m->head, K2T_XS_RMSNORM, last, m->final_norm, c.rms_eps, m->logits, false);
     }
     launch_advance_pos(st, m->pos_dev, ntok);
 }
@@ -226,17 +259,110 @@ struct StreamSwap {
     }
 };
 
+bool use_persistent(const k2t_model *m) { return m->persistent && m->mk_ok && !m->exact; }
+
+// Uploads the layer table of the persistent kernel (matrix views and launch shapes).
+void upload_mk_layers(k2t_model *m) {
+    std::vector<MkLayer> h(m->layers.size());
+    for (size_t l = 0; l < m->layers.size(); l++) {
+        const auto &L = m->layers[l];
+        h[l].qkv = mat_dev(L.qkv, false);
+        h[l].o = mat_dev(L.o, false);
+        h[l].gu = mat_dev(L.gu, true);
+        h[l].down = mat_dev(L.down, false);
+        h[l].in_norm = L.in_norm;
+        h[l].post_norm = L.post_norm;
+        h[l].bias = L.bias;
+    }
+    hip_check(hipMemcpy(m->mk_layers, h.data(), h.size() * sizeof(MkLayer), hipMemcpyHostToDevice), "layer table");
+}
+
+// One decode step as a single persistent kernel, then the position / step advance.
+void forward_mk(k2t_model *m) {
+    const k2t_model_config &c = m->cfg;
+    MkParams P{};
+    P.layers = m->mk_layers;
+    P.L = c.n_layers;
+    P.head = mat_dev(m->head, false);
+    P.final_norm = m->final_norm;
+    P.d = c.hidden;
+    P.nq = c.n_heads;
+    P.nkv = c.n_kv_heads;
+    P.hd = c.head_dim;
+    P.inter = c.intermediate;
+    P.vocab = c.vocab;
+    P.max_seq = c.max_seq;
+    P.kmax = std::max(c.hidden, c.intermediate);
+    P.eps = c.rms_eps;
+    P.attn_scale = 1.0f / sqrtf((float)c.head_dim);
+    P.rope = m->rope;
+    P.pos_dev = m->pos_dev;
+    P.tokens = m->tokens;
+    P.step_dev = m->step_dev;
+    P.kq = m->kq;
+    P.vq = m->vq;
+    P.ks = m->ks;
+    P.vs = m->vs;
+    P.HA = m->ll_ha;
+    P.HB = m->ll_hb;
+    P.QKV = m->ll_qkv;
+    P.OACT = m->ll_oact;
+    P.GACT = m->ll_gact;
+    P.logits = m->logits;
+    P.err = m->err_dev;
+    P.spin_limit = 1u << 22;
+    static unsigned long long *trace = nullptr;  // TEMP profiling: K2T_MK_TRACE=1
+    if (getenv("K2T_MK_TRACE") && !m->use_graph) {
+        const size_t n = (size_t)m->ctx->num_cus * (c.n_layers + 1) * 6 * 3;
+        if (!trace) hip_check(hipMalloc(&trace, n * 8), "trace");
+        hip_check(hipMemset(trace, 0, n * 8), "trace clear");
+        P.trace = trace;
+    }
+    launch_decode_mk(m->stream, P, m->ctx->num_cus, m->mk_lds);
+    if (P.trace) {
+        const size_t n = (size_t)m->ctx->num_cus * (c.n_layers + 1) * 6 * 3;
+        std::vector<unsigned long long> h(n);
+        hip_check(hipStreamSynchronize(m->stream), "sync");
+        hip_check(hipMemcpy(h.data(), trace, n * 8, hipMemcpyDeviceToHost), "trace copy");
+        FILE *f = fopen(getenv("K2T_MK_TRACE"), "wb");
+        if (f) {
+            fwrite(h.data(), 8, n, f);
+            fclose(f);
+        }
+    }
+    launch_advance_step(m->stream, m->pos_dev, m->step_dev, 1);
+}
+
+// Raises the persistent kernel's dependency-timeout flag as an error (after a sync).
+void check_mk_error(k2t_model *m) {
+    if (!m->err_dev) return;
+    int e = 0;
+    hip_check(hipMemcpy(&e, m->err_dev, sizeof(int), hipMemcpyDeviceToHost), "error flag");
+    if (e) {
+        (void)hipMemset(m->err_dev, 0, sizeof(int));
+        throw Error(K2T_E_INTERNAL, "persistent decode kernel: dependency wait timed out");
+    }
+}
+
 void decode_step(k2t_model *m) {
     StreamSwap sw(m);
+    const bool pk = use_persistent(m);
     if (!m->use_graph) {
-        forward(m, 1, true);
+        if (pk) {
+            upload_mk_layers(m);
+            forward_mk(m);
+        } else {
+            forward(m, 1, true);
+        }
         return;
     }
     if (!m->graph) {
+        if (pk) upload_mk_layers(m);
         hipGraph_t g = nullptr;
         hip_check(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal), "begin capture");
         try {
-            forward(m, 1, true);
+            if (pk) forward_mk(m);
+            else forward(m, 1, true);
         } catch (...) {
             (void)hipStreamEndCapture(m->stream, &g);
             if (g) (void)hipGraphDestroy(g);
@@ -297,6 +423,22 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             m->xq = (int8_t *)dalloc(m, (size_t)max_batch * kmax);
             m->xs = (float *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(float));
             m->xsum = (int32_t *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(int32_t));
+            // persistent decode kernel state
+            m->mk_ok = decode_mk_supported(c, ctx->num_cus);
+            m->mk_lds = decode_mk_lds_bytes(c);
+            m->step_dev = (uint32_t *)dalloc(m, 16);
+            m->err_dev = (int *)m->step_dev + 1;
+            const uint32_t one[4] = {1u, 0u, 0u, 0u};
+            hip_check(hipMemcpy(m->step_dev, one, sizeof(one), hipMemcpyHostToDevice), "step init");
+            const size_t words = 2 * (size_t)c.hidden + qkv_w + (size_t)(c.n_heads * c.head_dim / 64) * 18 +
+                                 (size_t)(c.intermediate / 64) * 18;
+            m->ll_ha = (unsigned long long *)dalloc(m, words * 8);
+            hip_check(hipMemset(m->ll_ha, 0, words * 8), "hand-off clear");
+            m->ll_hb = m->ll_ha + c.hidden;
+            m->ll_qkv = m->ll_hb + c.hidden;
+            m->ll_oact = m->ll_qkv + qkv_w;
+            m->ll_gact = m->ll_oact + (size_t)(c.n_heads * c.head_dim / 64) * 18;
+            m->mk_layers = (MkLayer *)dalloc(m, (size_t)c.n_layers * sizeof(MkLayer));
         } catch (...) {
             k2t_model_destroy(m);
             throw;
@@ -420,6 +562,7 @@ int32_t k2t_model_decode(k2t_model *m, int32_t token, float *logits_host) {
                                      hipMemcpyDeviceToHost, m->stream),
                       "logits download");
             hip_check(hipStreamSynchronize(m->stream), "sync");
+            check_mk_error(m);
         }
     });
 }
@@ -483,6 +626,7 @@ int32_t k2t_model_generate(k2t_model *m, int32_t first_token, int32_t n_steps, i
             (void)hipFree(dev_out);
             m->allocs.pop_back();
         }
+        check_mk_error(m);
     });
 }
 
@@ -498,6 +642,25 @@ int32_t k2t_model_sync(k2t_model *m) {
         arg(m != nullptr, "model is NULL");
         hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
         hip_check(hipStreamSynchronize(m->stream), "sync");
+        check_mk_error(m);
+    });
+}
+
+int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        m->persistent = enable != 0;
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+    });
+}
+
+int32_t k2t_model_persistent_active(const k2t_model *m, int32_t *active) {
+    return mguard([&] {
+        arg(m && active, "NULL argument");
+        *active = use_persistent(m) ? 1 : 0;
     });
 }
 

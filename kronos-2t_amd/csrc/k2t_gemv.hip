@@ -25,6 +25,7 @@
 #include <algorithm>
 
 #include "k2t_device.h"
+#include "../../include/k2t_hip.h"
 #include "k2t_internal.h"
 
 namespace k2t {
@@ -50,6 +51,182 @@ struct GemvParams {
     int exact;        // 1: replay the reference's fmaf chain from LDS-staged terms
     int accum;        // 1: out = out + result (residual add, real_llm.rs:7185-7188)
     uint32_t cb0, cb1, cb2, cb3;
+    // Fused activation builder (XS != 0): fp32 source row, RMSNorm weights, eps, the
+    // Hadamard sign masks and the byte offset of the activation region in LDS.
+    const float *xsrc;
+    const float *xnorm;
+    const uint64_t *signs;
+    float eps;
+    int xoff;
+};
+
+// Builds the int8 activation chunks [c0, c1) of one token in LDS (xl[c*64 + e],
+// xsl[c], xsuml[c]) from an fp32 source:
+//   XS 1: v = (x*inv_rms)*w, inv_rms = 1/sqrt(mean(x^2)+eps) computed once per workgroup
+//         (populate_rmsnorm_fwht, simd_lut.rs:2970-2997; inv_rms as real_llm.rs:6929)
+//   XS 2: v = silu(gate)*up of the interleaved gate_up block c  (real_llm.rs:9801-9805,
+//         populate_chunk_fwht_raw with chunk index c, 7207-7296)
+// then the signed FWHT-64 of chunk c and int8 quantization (simd_lut.rs:3097-3128).
+// Eight lanes per chunk, eight consecutive elements per lane: butterflies h = 1, 2, 4
+// run in registers and h = 8, 16, 32 across lanes (^1, ^2, ^4).  Each butterfly adds or
+// subtracts the same operands as hadamard.rs:83-97, so the codes, scales and sums equal
+// those of the one-element-per-lane kernels (rmsnorm_act / swiglu_act).
+// Source registers of one 8-element slice: XS 1 = x (a) and w (b); XS 2 = gate (a), up (b).
+struct XSlice {
+    float4 a0, a1, b0, b1;
+};
+
+template <int XS>
+__device__ __forceinline__ void load_slice(const GemvParams &P, const float *src, int c, uint32_t s, XSlice &r) {
+    if constexpr (XS == 1) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(src + c * 64 + s * 8);
+        const float4 *w4 = reinterpret_cast<const float4 *>(P.xnorm + c * 64 + s * 8);
+        r.a0 = x4[0];
+        r.a1 = x4[1];
+        r.b0 = w4[0];
+        r.b1 = w4[1];
+    } else {
+        const float4 *g4 = reinterpret_cast<const float4 *>(src + (size_t)c * 128 + s * 8);
+        r.a0 = g4[0];
+        r.a1 = g4[1];
+        r.b0 = g4[16];
+        r.b1 = g4[17];
+    }
+}
+
+// Turns one loaded slice into its int8 codes (as described above) and stores them in LDS.
+template <int XS>
+__device__ __forceinline__ void finish_slice(const GemvParams &P, const XSlice &r, int c, bool act, uint32_t s,
+                                             float inv_rms, int8_t *xl, float *xsl, int32_t *xsuml) {
+    float v[8];
+    const float a[8] = {r.a0.x, r.a0.y, r.a0.z, r.a0.w, r.a1.x, r.a1.y, r.a1.z, r.a1.w};
+    const float b[8] = {r.b0.x, r.b0.y, r.b0.z, r.b0.w, r.b1.x, r.b1.y, r.b1.z, r.b1.w};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if constexpr (XS == 1) v[j] = (a[j] * inv_rms) * b[j];
+        else v[j] = (a[j] / (1.0f + expf(-a[j]))) * b[j];
+    }
+    const uint32_t sb = (uint32_t)(P.signs[c] >> (8u * s)) & 0xFFu;
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = flip_sign(v[j], (sb >> j) & 1u) * 0.125f;
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (!(j & h)) {
+                const float x0 = v[j], x1 = v[j | h];
+                v[j] = x0 + x1;
+                v[j | h] = x0 - x1;
+            }
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+        const bool upper = (s & (uint32_t)m) != 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float p = m == 1 ? xchg1(v[j]) : m == 2 ? xchg2(v[j]) : xchg4(v[j]);
+            v[j] = upper ? p - v[j] : v[j] + p;
+        }
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
+    mx = fmaxf(mx, xchg1(mx));
+    mx = fmaxf(mx, xchg2(mx));
+    mx = fmaxf(mx, xchg4(mx));
+    uint32_t lo = 0, hi = 0;
+    int sum = 0;
+    if (mx > FLT_EPSILON) {
+        const float inv = 127.0f / mx;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int qi = (int)rintf(v[j] * inv);
+            sum += qi;
+            if (j < 4) lo |= ((uint32_t)qi & 0xFFu) << (8 * j);
+            else hi |= ((uint32_t)qi & 0xFFu) << (8 * (j - 4));
+        }
+    }
+    sum += xchg1(sum);
+    sum += xchg2(sum);
+    sum += xchg4(sum);
+    if (act) {
+        *reinterpret_cast<uint2 *>(xl + c * 64 + s * 8) = make_uint2(lo, hi);
+        if (s == 0) {
+            xsl[c] = mx > FLT_EPSILON ? mx / 127.0f : 0.0f;
+            xsuml[c] = sum;
+        }
+    }
+}
+
+// Builds the int8 activation chunks [c0, c1) of one token in LDS in two steps, so that
+// the source loads are issued before the first weight loads (loads complete in order):
+//   begin(): loads the first 8 chunk slices and, for XS 1, the first kSqPre float4 of
+//            every lane's share of the row for sum(x^2);
+//   finish(): inv_rms, then codes of every chunk (later slices load after the weights).
+constexpr int kSqPre = 8;
+template <int XS>
+struct XBuilder {
+    const GemvParams &P;
+    const float *src;
+    int c0, c1;
+    uint32_t lane, slot, s;
+    XSlice first;
+    float4 sq[XS == 1 ? kSqPre : 1];
+
+    __device__ XBuilder(const GemvParams &P_, int tok, int c0_, int c1_, uint32_t lane_)
+        : P(P_), src(P_.xsrc + (size_t)tok * (XS == 2 ? 2 * P_.K : P_.K)), c0(c0_), c1(c1_), lane(lane_),
+          slot(lane_ >> 3), s(lane_ & 7u) {}
+
+    __device__ void begin() {
+        const int u = (int)slot;
+        load_slice<XS>(P, src, c0 + (u < c1 - c0 ? u : 0), s, first);
+        if constexpr (XS == 1) {
+            const float4 *x4 = reinterpret_cast<const float4 *>(src);
+            const int n4 = P.K / 4;
+#pragma unroll
+            for (int j = 0; j < kSqPre; j++) {
+                const int i = (int)lane + 64 * j;
+                sq[j] = i < n4 ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+    }
+
+    __device__ void finish(int8_t *xl, float *xsl, int32_t *xsuml) {
+        float inv_rms = 1.0f;
+        if constexpr (XS == 1) {
+            // Same fmaf order as row_sumsq_wave: lane l adds float4 l, l+64, ... ascending.
+            const float4 *x4 = reinterpret_cast<const float4 *>(src);
+            const int n4 = P.K / 4;
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kSqPre; j++) {
+                if ((int)lane + 64 * j < n4) {
+                    ss = fmaf(sq[j].x, sq[j].x, ss);
+                    ss = fmaf(sq[j].y, sq[j].y, ss);
+                    ss = fmaf(sq[j].z, sq[j].z, ss);
+                    ss = fmaf(sq[j].w, sq[j].w, ss);
+                }
+            }
+            for (int i = (int)lane + 64 * kSqPre; i < n4; i += 64) {
+                const float4 v = x4[i];
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+            ss = wave_sum_f(ss);
+            inv_rms = 1.0f / sqrtf(ss / (float)P.K + P.eps);
+        }
+        const int n = c1 - c0;
+        finish_slice<XS>(P, first, c0 + ((int)slot < n ? (int)slot : 0), (int)slot < n, s, inv_rms, xl, xsl, xsuml);
+        for (int base = 8; base < n; base += 8) {
+            const int u = base + (int)slot;
+            const bool act = u < n;
+            const int c = c0 + (act ? u : 0);
+            XSlice r;
+            load_slice<XS>(P, src, c, s, r);
+            finish_slice<XS>(P, r, c, act, s, inv_rms, xl, xsl, xsuml);
+        }
+    }
 };
 
 // Registers of one fetched chunk for one lane: its 64 nibble bytes (rows 4g..4g+3,
@@ -75,7 +252,21 @@ struct Frag {
 // i32 dot of each (row, chunk).  The fp32 terms float(dot)*sx and ws are staged in LDS
 // and one thread per row replays the reference's fmaf chain in chunk order.
 // FMT 0: bit-plane Nibble4 with HP hi planes; FMT 1: NF4 codebook stripes.
-template <int FMT, int HP, int NT, bool DOTS>
+#ifdef K2T_GEMV_TS
+__device__ unsigned long long k2t_gemv_ts[1 << 20];
+#define K2T_TS(k)                                                                                   \
+    if (lane == 0) {                                                                                \
+        k2t_gemv_ts[((size_t)blockIdx.x * P.nseg + wave) * 6 + (k)] = wall_clock64();              \
+        if ((k) == 0)                                                                               \
+            k2t_gemv_ts[((size_t)blockIdx.x * P.nseg + wave) * 6 + 5] =                             \
+                ((unsigned long long)__builtin_amdgcn_s_getreg((15 << 11) | 20) << 32) |           \
+                __builtin_amdgcn_s_getreg((31 << 11) | 4);                                          \
+    }
+#else
+#define K2T_TS(k)
+#endif
+
+template <int FMT, int HP, int NT, bool DOTS, int XS>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     constexpr int NH = HP == 0 ? 1 : (HP == 1 ? 2 : 4);
     extern __shared__ float lds[];
@@ -143,6 +334,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             fr.h[1] = load_stream16(rec + hi_off + 64);
         }
         fr.ws = *reinterpret_cast<const uint32_t *>(scp + sc_off);
+        if constexpr (XS != 0) return;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
 #pragma unroll
@@ -155,12 +347,22 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     };
 
     float2 *terms = reinterpret_cast<float2 *>(lds);  // [NT][nc][RB] (a = float(dot)*sx, ws)
+    // Fused activation (XS != 0, one token): int8 codes, scales and sums per chunk.
+    int8_t *xl = reinterpret_cast<int8_t *>(lds) + P.xoff;
+    float *xsl = reinterpret_cast<float *>(xl + P.K);
+    int32_t *xsuml = reinterpret_cast<int32_t *>(xsl + P.nc);
 
     float f[NT][2];  // fast epilogue: this lane group's partial chains
 #pragma unroll
     for (int t = 0; t < NT; t++) f[t][0] = f[t][1] = 0.0f;
 
-    auto process = [&](const Frag<HP, NT> &fr, int c) {
+    auto process = [&](Frag<HP, NT> &fr, int c) {
+        if constexpr (XS != 0) {  // activation built in LDS by this wave
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) fr.x[0][kk] = *reinterpret_cast<const uint2 *>(xl + c * 64 + kk * 16 + half * 8);
+            fr.sx[0] = xsl[c];
+            if constexpr (FMT == 0) fr.sum[0] = xsuml[c];
+        }
         int acc[NT][4];
 #pragma unroll
         for (int t = 0; t < NT; t++)
@@ -243,15 +445,29 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     auto chunk_of = [&](int i) { return cw0 + i * G + q; };
     const int iters = (cw1 - cw0 + G - 1) / G;  // wave-uniform
     auto valid = [&](int i) { return i < iters && chunk_of(i) < cw1; };
+    K2T_TS(0)
     if constexpr (NT == 1) {
         // Two fragments in flight: chunk i+1 is fetched before chunk i is processed.
         Frag<HP, NT> fa, fb;
-        if (valid(0)) fetch(fa, chunk_of(0));
+        if constexpr (XS != 0) {
+            // Source loads first, then the first weight loads; the wave builds its
+            // activation while the weights are in flight.
+            XBuilder<XS> xb(P, tok0, cw0, cw1, lane);
+            xb.begin();
+            if (valid(0)) fetch(fa, chunk_of(0));
+            if (valid(1)) fetch(fb, chunk_of(1));
+            xb.finish(xl, xsl, xsuml);
+            __builtin_amdgcn_wave_barrier();
+        } else {
+            if (valid(0)) fetch(fa, chunk_of(0));
+        }
+        K2T_TS(1)
         for (int i = 0; i < iters; i += 2) {
-            if (valid(i + 1)) fetch(fb, chunk_of(i + 1));
+            if (XS == 0 && valid(i + 1)) fetch(fb, chunk_of(i + 1));
             if (valid(i)) process(fa, chunk_of(i));
             if (valid(i + 2)) fetch(fa, chunk_of(i + 2));
             if (valid(i + 1)) process(fb, chunk_of(i + 1));
+            if (XS != 0 && valid(i + 3)) fetch(fb, chunk_of(i + 3));
         }
     } else {
         // Multi-token tiles hold NT activation slices per fragment: one in flight.
@@ -263,6 +479,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         }
     }
 
+    K2T_TS(2)
     if (!P.exact) {
         // Fast epilogue: add the lane groups' partial chains (fixed butterfly order, so the
         // result is deterministic), then the waves' partials in wave order.
@@ -285,6 +502,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             }
         }
         __syncthreads();
+        K2T_TS(3)
         const int nrows_blk = (is_tail && !smode) ? 16 : RB;
         const int first_stripe = smode ? rb : (is_tail ? 2 * P.np : 2 * rb);
         for (int idx = (int)threadIdx.x; idx < NT * RB; idx += (int)blockDim.x) {
@@ -298,9 +516,11 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             float *o = P.out + (size_t)(tok0 + t) * P.out_stride + row;
             *o = P.accum ? *o + acc : acc;
         }
+        K2T_TS(4)
         return;
     }
     __syncthreads();
+    K2T_TS(3)
     const int nrows_blk = (is_tail && !smode) ? 16 : RB;
     const int first_stripe = smode ? rb : (is_tail ? 2 * P.np : 2 * rb);
     // One thread per (token, row of the block) replays the chain; LDS reads are batched
@@ -328,6 +548,19 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         float *o = P.out + (size_t)(tok0 + t) * P.out_stride + row;
         *o = P.accum ? *o + acc : acc;
     }
+    K2T_TS(4)
+}
+
+uint64_t hadamard_sign_mask_host(uint64_t block) {
+    uint64_t mask = 0;
+    for (uint64_t i = 0; i < 64; i++) {
+        uint64_t z = 0x9E3779B97F4A7C15ull + block * 0xBF58476D1CE4E5B9ull + (i + 1) * 0x9E3779B97F4A7C15ull;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        mask |= (z & 1) << i;
+    }
+    return mask;
 }
 
 GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1) {
@@ -358,27 +591,36 @@ GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1) {
 }
 
 template <int FMT, int HP, bool DOTS>
-static void launch_nt(int nt, dim3 grid, dim3 block, size_t lds, hipStream_t st, const GemvParams &P) {
+static void launch_nt(int nt, int xs, dim3 grid, dim3 block, size_t lds, hipStream_t st, const GemvParams &P) {
+    if (xs == K2T_XS_RMSNORM) {
+        hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, false, K2T_XS_RMSNORM>), grid, block, lds, st, P);
+        return;
+    }
+    if (xs == K2T_XS_SWIGLU) {
+        hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, false, K2T_XS_SWIGLU>), grid, block, lds, st, P);
+        return;
+    }
     switch (nt) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, DOTS>), grid, block, lds, st, P); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 2, false>), grid, block, lds, st, P); break;
-        case 3: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 3, false>), grid, block, lds, st, P); break;
-        default: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 4, false>), grid, block, lds, st, P); break;
+        case 1: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, DOTS, 0>), grid, block, lds, st, P); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 2, false, 0>), grid, block, lds, st, P); break;
+        case 3: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 3, false, 0>), grid, block, lds, st, P); break;
+        default: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 4, false, 0>), grid, block, lds, st, P); break;
     }
 }
 
 template <bool DOTS>
-static void launch_fmt(const k2t_mat *m, int nt, dim3 grid, dim3 block, size_t lds, hipStream_t st,
+static void launch_fmt(const k2t_mat *m, int nt, int xs, dim3 grid, dim3 block, size_t lds, hipStream_t st,
                        const GemvParams &P) {
-    if (m->fmt == K2T_FMT_NF) launch_nt<1, 0, DOTS>(nt, grid, block, lds, st, P);
-    else if (m->hp == 0) launch_nt<0, 0, DOTS>(nt, grid, block, lds, st, P);
-    else if (m->hp == 1) launch_nt<0, 1, DOTS>(nt, grid, block, lds, st, P);
-    else launch_nt<0, 2, DOTS>(nt, grid, block, lds, st, P);
+    if (m->fmt == K2T_FMT_NF) launch_nt<1, 0, DOTS>(nt, xs, grid, block, lds, st, P);
+    else if (m->hp == 0) launch_nt<0, 0, DOTS>(nt, xs, grid, block, lds, st, P);
+    else if (m->hp == 1) launch_nt<0, 1, DOTS>(nt, xs, grid, block, lds, st, P);
+    else launch_nt<0, 2, DOTS>(nt, xs, grid, block, lds, st, P);
 }
 
 static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                              const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
-                             int32_t *dots, bool accum);
+                             int32_t *dots, bool accum, int xsm = 0, const float *src = nullptr,
+                             const float *w = nullptr, float eps = 0.0f);
 
 void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                  const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
@@ -391,9 +633,15 @@ void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const floa
     launch_gemv_impl(ctx, m, xq, xs, xsum, ntok, 0, m->stripes, out, out_stride, nullptr, accumulate);
 }
 
+void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float *src, const float *w, float eps,
+                       float *out, bool accumulate) {
+    launch_gemv_impl(ctx, m, nullptr, nullptr, nullptr, 1, 0, m->stripes, out, (size_t)m->rows, nullptr, accumulate,
+                     xs_mode, src, w, eps);
+}
+
 static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                              const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
-                             int32_t *dots, bool accum) {
+                             int32_t *dots, bool accum, int xsm, const float *src, const float *w, float eps) {
     const int saved = ctx->max_segments;
     if (dots) ctx->max_segments = 1;
     GemvPlan plan = plan_gemv(ctx, m, s0, s1);
@@ -425,9 +673,19 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
     P.cb2 = m->cb[2];
     P.cb3 = m->cb[3];
     // Tokens per weight pass: 4, fewer when the staged terms would not fit in 64 KB of LDS.
-    const size_t per_tok = ctx->exact ? (size_t)m->nc * (plan.stripe_mode ? 16 : 32) * sizeof(float2)
-                                      : (size_t)plan.nseg * 32 * sizeof(float);
-    const int G = (int)std::max<size_t>(1, std::min<size_t>(4, (64 * 1024) / per_tok));
+    size_t per_tok = ctx->exact ? (size_t)m->nc * (plan.stripe_mode ? 16 : 32) * sizeof(float2)
+                                : (size_t)plan.nseg * 32 * sizeof(float);
+    int G = (int)std::max<size_t>(1, std::min<size_t>(4, (64 * 1024) / per_tok));
+    if (xsm != 0) {  // one token; its int8 activation is built in LDS after the terms
+        if (ntok != 1 || m->cols > kSignBlocks * 64 || !ctx->signs) throw Error(K2T_E_INTERNAL, "fused gemv shape");
+        P.xsrc = src;
+        P.xnorm = w;
+        P.eps = eps;
+        P.signs = ctx->signs;
+        P.xoff = (int)((per_tok + 15) / 16 * 16);
+        per_tok = (size_t)P.xoff + (size_t)m->cols + 8 * (size_t)m->nc;
+        G = 1;
+    }
     const int groups = ntok / G, rem = ntok % G;
     const dim3 block(64 * plan.nseg);
     P.lds_terms = 1;
@@ -436,15 +694,18 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
     if (groups > 0) {
         GemvParams Q = P;
         Q.tok_base = 0;
-        if (dots && G == 1) launch_fmt<true>(m, 1, dim3(plan.rb_hi - plan.rb_lo, groups), block, per_tok, ctx->stream, Q);
-        else launch_fmt<false>(m, G, dim3(plan.rb_hi - plan.rb_lo, groups), block, (size_t)G * per_tok, ctx->stream, Q);
+        if (dots && G == 1)
+            launch_fmt<true>(m, 1, 0, dim3(plan.rb_hi - plan.rb_lo, groups), block, per_tok, ctx->stream, Q);
+        else
+            launch_fmt<false>(m, G, xsm, dim3(plan.rb_hi - plan.rb_lo, groups), block, (size_t)G * per_tok,
+                              ctx->stream, Q);
         hip_check(hipGetLastError(), "gemv launch");
     }
     if (rem > 0) {
         GemvParams Q = P;
         Q.tok_base = groups * G;
-        if (dots) launch_fmt<true>(m, rem, dim3(plan.rb_hi - plan.rb_lo, 1), block, rem * per_tok, ctx->stream, Q);
-        else launch_fmt<false>(m, rem, dim3(plan.rb_hi - plan.rb_lo, 1), block, rem * per_tok, ctx->stream, Q);
+        if (dots) launch_fmt<true>(m, rem, 0, dim3(plan.rb_hi - plan.rb_lo, 1), block, rem * per_tok, ctx->stream, Q);
+        else launch_fmt<false>(m, rem, 0, dim3(plan.rb_hi - plan.rb_lo, 1), block, rem * per_tok, ctx->stream, Q);
         hip_check(hipGetLastError(), "gemv launch");
     }
 }

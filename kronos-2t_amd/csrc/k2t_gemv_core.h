@@ -1,0 +1,203 @@
+// Per-wave building blocks of the quantized GEMV for kernels that own their workgroup
+// layout (the persistent decode kernel): lane geometry inside a row block, the fetch of
+// one chunk record, and the exact integer dots of a lane's two rows.  Layouts are the
+// reference's Nibble4SdotMatrix (simd_lut.rs:3264-3400) and NfSdotMatrix
+// (simd_lut.rs:4796-5023); the arithmetic is that of sdot_decode_neon /
+// nf_sdot_decode_neon (simd_lut.rs:3766-4091, 6074-6364).
+#pragma once
+#include "k2t_device.h"
+
+namespace k2t {
+
+// Device view of one quantized matrix plus its launch shape inside the persistent kernel.
+struct MatDev {
+    const uint8_t *pair, *tail;
+    size_t ptot;  // NF: bytes per pair stream
+    int rows, nc, np, stripes;
+    int fmt, hp, sgc;  // fmt: 0 = bit planes (hp hi planes), 1 = NF4
+    uint32_t cb0, cb1, cb2, cb3;
+    int smode;  // 1: a wave group owns one stripe (16 rows), 0: a stripe pair (32 rows)
+    int nseg;   // waves per row block (K segments), a power of two <= 16
+    int cps;    // chunks per wave
+};
+
+template <int HP>
+struct WFrag {
+    uint4 w[4];
+    uint4 h[HP == 0 ? 1 : (HP == 1 ? 2 : 4)];
+    uint32_t ws;
+};
+
+// Lane geometry for row block `rb` (a pair, the odd tail stripe, or a stripe in stripe
+// mode).  Lane bits: 0 = 8-column half, 1-2 = 4-row group g, 3 = stripe of the pair (pair
+// mode) or a lane-group bit (stripe mode), the rest = lane group (chunks round-robin).
+struct Geo {
+    uint32_t half, g, side, nib_off, hi_off, sc_off, rloc;
+    int q, G, RB, first_stripe, nrows;
+    bool is_tail, live;
+    const uint8_t *mbase;
+};
+
+template <int FMT, int HP>
+__device__ __forceinline__ Geo make_geo(const MatDev &M, int rb, uint32_t lane) {
+    Geo o;
+    const bool smode = M.smode != 0;
+    o.half = lane & 1u;
+    o.g = (lane >> 1) & 3u;
+    o.is_tail = smode ? rb >= 2 * M.np : rb >= M.np;
+    const uint32_t lane_side = smode ? 0u : (lane >> 3) & 1u;
+    o.side = smode ? (uint32_t)(rb & 1) : (o.is_tail ? 0u : lane_side);
+    const int pidx = smode ? (rb >> 1) : rb;
+    o.G = smode ? 8 : 4;
+    o.q = smode ? (int)(lane >> 3) : (int)(lane >> 4);
+    o.RB = smode ? 16 : 32;
+    o.rloc = (smode ? 0u : o.side * 16u) + 4u * o.g + 2u * o.half;
+    o.first_stripe = smode ? rb : (o.is_tail ? 2 * M.np : 2 * rb);
+    o.nrows = (o.is_tail && !smode) ? 16 : o.RB;
+    o.live = !(o.is_tail && lane_side);
+    constexpr uint32_t PREC = 1024 + 256 * HP + 64;
+    if constexpr (FMT == 0) {
+        o.nib_off = (o.is_tail ? 0u : o.side * 512u) + o.g * 32u + o.half * 16u;
+        o.hi_off = (o.is_tail ? 512u : 1024u + o.side * 128u * HP) + o.g * 16u;
+        o.sc_off = (o.is_tail ? 512u + 128u * HP : 1024u + 256u * HP + o.side * 32u);
+    } else {
+        o.nib_off = (o.is_tail ? 32u : 64u + o.side * 512u) + o.g * 32u + o.half * 16u;
+        o.hi_off = 0;
+        o.sc_off = o.is_tail ? 0u : o.side * 32u;
+    }
+    o.sc_off += (4u * o.g + 2u * o.half) * 2u;
+    o.mbase = o.is_tail ? M.tail : M.pair + (size_t)pidx * (FMT == 0 ? (size_t)M.nc * PREC : M.ptot);
+    return o;
+}
+
+template <int FMT, int HP>
+__device__ __forceinline__ void fetch_w(const MatDev &M, const Geo &o, int c, WFrag<HP> &fr) {
+    constexpr uint32_t PREC = 1024 + 256 * HP + 64;
+    constexpr uint32_t TREC = 512 + 128 * HP + 32;
+    const uint8_t *rec, *scp;
+    if constexpr (FMT == 0) {
+        rec = o.mbase + (size_t)c * (o.is_tail ? TREC : PREC);
+        scp = rec;
+    } else {
+        const int sg = c / M.sgc, cst = sg * M.sgc, sb = c - cst;
+        const uint8_t *gb =
+            o.mbase + (o.is_tail ? (size_t)sg * 32 + (size_t)cst * 512 : (size_t)sg * 64 + (size_t)cst * 1024);
+        rec = gb + (size_t)sb * (o.is_tail ? 512 : 1024);
+        scp = gb;
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) fr.w[kk] = load_stream16(rec + o.nib_off + kk * 128);
+    if constexpr (FMT == 0 && HP == 2) {
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) fr.h[kk] = load_stream16(rec + o.hi_off + kk * 64);
+    } else if constexpr (FMT == 0 && HP == 1) {
+        fr.h[0] = load_stream16(rec + o.hi_off);
+        fr.h[1] = load_stream16(rec + o.hi_off + 64);
+    }
+    fr.ws = *reinterpret_cast<const uint32_t *>(scp + o.sc_off);
+}
+
+// Exact i32 dots of this lane's two rows (4g + 2*half, +1) with activation chunk x (the
+// lane's 8-byte slices of the four 16-column blocks) and its code sum (bit planes).
+template <int FMT, int HP>
+__device__ __forceinline__ void chunk_dots(const MatDev &M, const WFrag<HP> &fr, uint32_t half, const uint2 *x,
+                                           int xsum, int &r0, int &r1) {
+    constexpr int MAX_ODD = (1 << (4 + HP)) - 1;
+    int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+        const uint32_t wd[4] = {fr.w[kk].x, fr.w[kk].y, fr.w[kk].z, fr.w[kk].w};
+        uint4 hv = make_uint4(0, 0, 0, 0);
+        if constexpr (HP == 2) hv = fr.h[kk];
+        if constexpr (HP == 1) hv = fr.h[kk >> 1];
+        const uint32_t hd[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t d = wd[j];
+            uint32_t lo, hi;
+            if constexpr (FMT == 0) {
+                lo = d & 0x0F0F0F0Fu;
+                hi = (d >> 4) & 0x0F0F0F0Fu;
+                if constexpr (HP == 2) {
+                    lo |= __builtin_rotateright32(hd[j], half ? 30u : 0u) & 0x30303030u;
+                    hi |= __builtin_rotateright32(hd[j], half ? 28u : 2u) & 0x30303030u;
+                } else if constexpr (HP == 1) {
+                    const uint32_t e = ((kk & 1) ? 28u : 0u) + 2u * half;
+                    lo |= __builtin_rotateright32(hd[j], e) & 0x10101010u;
+                    hi |= __builtin_rotateright32(hd[j], (e + 1u) & 31u) & 0x10101010u;
+                }
+            } else {
+                lo = lut16(d & 0x07070707u, bit3_mask(d), M.cb0, M.cb1, M.cb2, M.cb3);
+                hi = lut16((d >> 4) & 0x07070707u, bit7_mask(d), M.cb0, M.cb1, M.cb2, M.cb3);
+            }
+            acc[j] = __builtin_amdgcn_sdot4((int)lo, (int)x[kk].x,
+                                            __builtin_amdgcn_sdot4((int)hi, (int)x[kk].y, acc[j], false), false);
+        }
+    }
+    const int a0 = acc[0] + dpp_xor1(acc[0]);
+    const int a1 = acc[1] + dpp_xor1(acc[1]);
+    const int a2 = acc[2] + dpp_xor1(acc[2]);
+    const int a3 = acc[3] + dpp_xor1(acc[3]);
+    r0 = half ? a2 : a0;
+    r1 = half ? a3 : a1;
+    if constexpr (FMT == 0) {
+        r0 = 2 * r0 - MAX_ODD * xsum;
+        r1 = 2 * r1 - MAX_ODD * xsum;
+    }
+}
+
+// One wave's share (K segment `wseg`) of row block `rb` against the activation held in
+// LDS (xl codes, xsl scales, xsuml code sums).  The fast epilogue: per-lane-group
+// partial fmaf chains, summed across lane groups in a fixed butterfly order; lanes
+// holding a row's partial write it to part[rloc], part[rloc + 1] (part = this wave's
+// 32-float slot).  Every lane of the wave must call this (cross-lane steps).
+template <int FMT, int HP>
+__device__ void gemv_wave(const MatDev &M, int rb, bool active, int wseg, uint32_t lane, const int8_t *xl,
+                          const float *xsl, const int32_t *xsuml, float *part) {
+    float f0 = 0.0f, f1 = 0.0f;
+    Geo o{};
+    if (active) o = make_geo<FMT, HP>(M, rb, lane);
+    const int G = M.smode ? 8 : 4;
+    const int q = M.smode ? (int)(lane >> 3) : (int)(lane >> 4);
+    const int cw0 = wseg * M.cps, cw1 = active ? min(M.nc, cw0 + M.cps) : cw0;
+    const int iters = cw1 > cw0 ? (cw1 - cw0 + G - 1) / G : 0;
+    const uint32_t half = lane & 1u;
+    auto chunk_of = [&](int i) { return cw0 + i * G + q; };
+    auto valid = [&](int i) { return i < iters && chunk_of(i) < cw1; };
+    auto process = [&](const WFrag<HP> &fr, int c) {
+        uint2 x[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) x[kk] = *reinterpret_cast<const uint2 *>(xl + c * 64 + kk * 16 + half * 8);
+        const float sx = xsl[c];
+        const int xsum = FMT == 0 ? xsuml[c] : 0;
+        int r0, r1;
+        chunk_dots<FMT, HP>(M, fr, half, x, xsum, r0, r1);
+        const float n0 = fmaf((float)r0 * sx, bf16_lo(fr.ws), f0);
+        const float n1 = fmaf((float)r1 * sx, bf16_hi(fr.ws), f1);
+        f0 = sx != 0.0f ? n0 : f0;
+        f1 = sx != 0.0f ? n1 : f1;
+    };
+    WFrag<HP> fa, fb;
+    if (valid(0)) fetch_w<FMT, HP>(M, o, chunk_of(0), fa);
+    for (int i = 0; i < iters; i += 2) {
+        if (valid(i + 1)) fetch_w<FMT, HP>(M, o, chunk_of(i + 1), fb);
+        if (valid(i)) process(fa, chunk_of(i));
+        if (valid(i + 2)) fetch_w<FMT, HP>(M, o, chunk_of(i + 2), fa);
+        if (valid(i + 1)) process(fb, chunk_of(i + 1));
+    }
+    if (M.smode) {
+        f0 += __int_as_float(dpp_ror8(__float_as_int(f0)));
+        f1 += __int_as_float(dpp_ror8(__float_as_int(f1)));
+    }
+    f0 += __shfl_xor(f0, 16, kWave);
+    f0 += __shfl_xor(f0, 32, kWave);
+    f1 += __shfl_xor(f1, 16, kWave);
+    f1 += __shfl_xor(f1, 32, kWave);
+    const uint32_t rloc = (M.smode ? 0u : ((lane >> 3) & 1u) * 16u) + 4u * ((lane >> 1) & 3u) + 2u * half;
+    if (M.smode ? lane < 8 : lane < 16) {
+        part[rloc] = f0;
+        part[rloc + 1] = f1;
+    }
+}
+
+}  // namespace k2t

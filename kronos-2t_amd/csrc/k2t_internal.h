@@ -17,7 +17,11 @@ struct k2t_ctx {
     size_t scratch_cap = 0;  // floats
     float *rms_scratch = nullptr;
     size_t rms_cap = 0;
+    // Hadamard sign masks of 64-blocks 0..kSignBlocks-1 (bit i = sign of element i),
+    // uploaded at creation for the GEMV's fused activation builder.
+    uint64_t *signs = nullptr;
 };
+constexpr int kSignBlocks = 512;  // K <= 32768
 
 enum k2t_fmt : int32_t { K2T_FMT_NIBBLE4 = 1, K2T_FMT_NF = 2 };
 
@@ -58,6 +62,15 @@ GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1);
 void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                  const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
                  int32_t *dots);
+
+// GEMV whose int8 activation is built by each wave from an fp32 source (one token):
+//   K2T_XS_RMSNORM: src = hidden[K], w = norm weights -> RMSNorm + FWHT + int8
+//   K2T_XS_SWIGLU : src = interleaved gate_up[2K]      -> SwiGLU + FWHT + int8
+// Codes equal those of rmsnorm_act / swiglu_act followed by launch_gemv.
+enum { K2T_XS_GLOBAL = 0, K2T_XS_RMSNORM = 1, K2T_XS_SWIGLU = 2 };
+void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float *src, const float *w, float eps,
+                       float *out, bool accumulate);
+uint64_t hadamard_sign_mask_host(uint64_t block);
 
 void launch_act_quant(k2t_ctx *ctx, const float *x, const float *w, const float *inv_rms, int K,
                       int ntok, int8_t *q, float *scales, int32_t *sums);

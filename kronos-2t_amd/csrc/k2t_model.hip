@@ -15,40 +15,6 @@
 
 namespace k2t {
 
-// Quantizes the 64 values held one per lane (already rotated) to int8 with one scale
-// (simd_lut.rs:3097-3128 / 3172-3195).
-__device__ __forceinline__ void quant_chunk_store(float v, uint32_t lane, int8_t *q, float *scale,
-                                                  int32_t *sum) {
-    const float mx = wave_max_f(fabsf(v));
-    if (mx <= FLT_EPSILON) {
-        q[lane] = 0;
-        if (lane == 0) {
-            *scale = 0.0f;
-            *sum = 0;
-        }
-        return;
-    }
-    const float inv = 127.0f / mx;
-    const int qi = (int)rintf(v * inv);
-    const int s = wave_sum_i(qi);
-    q[lane] = (int8_t)qi;
-    if (lane == 0) {
-        *scale = mx / 127.0f;
-        *sum = s;
-    }
-}
-
-__device__ __forceinline__ float fwht_lane(float v, uint64_t block, uint32_t lane) {
-    v = flip_sign(v, hadamard_sign_bit(block, lane)) * 0.125f;
-    return wave_butterflies64(v, lane);
-}
-
-// hadamard.rs:193-228 on one block held one element per lane.
-__device__ __forceinline__ float ifwht_lane(float v, uint64_t block, uint32_t lane) {
-    v = wave_butterflies64(v, lane);
-    return flip_sign(v * 0.125f, hadamard_sign_bit(block, lane));
-}
-
 // ---------------------------------------------------------------- RMSNorm + FWHT + int8
 // One wave per (chunk, token): every wave recomputes inv_rms = 1/sqrt(mean(x^2) + eps)
 // (real_llm.rs:6929) from the whole row (L2-resident, a few KB) in a fixed order, then
@@ -59,31 +25,7 @@ __global__ __launch_bounds__(64) void rmsnorm_act_kernel(const float *__restrict
     const uint32_t lane = threadIdx.x;
     const int c = blockIdx.x, tok = blockIdx.y;
     const float *xt = x + (size_t)tok * K;
-    // K is a multiple of 64: lane reads float4s at 4*lane + 256*i, four loads in flight.
-    const float4 *x4 = reinterpret_cast<const float4 *>(xt);
-    const int n4 = K / 4;
-    float ss = 0.0f;
-    int i = (int)lane;
-    for (; i + 192 < n4; i += 256) {
-        float4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = x4[i + 64 * u];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            ss = fmaf(v[u].x, v[u].x, ss);
-            ss = fmaf(v[u].y, v[u].y, ss);
-            ss = fmaf(v[u].z, v[u].z, ss);
-            ss = fmaf(v[u].w, v[u].w, ss);
-        }
-    }
-    for (; i < n4; i += 64) {
-        const float4 v = x4[i];
-        ss = fmaf(v.x, v.x, ss);
-        ss = fmaf(v.y, v.y, ss);
-        ss = fmaf(v.z, v.z, ss);
-        ss = fmaf(v.w, v.w, ss);
-    }
-    ss = wave_sum_f(ss);
+    const float ss = row_sumsq_wave(xt, K, lane);
     const float inv_rms = 1.0f / sqrtf(ss / (float)K + eps);
     const float v = (xt[c * 64 + lane] * inv_rms) * w[c * 64 + lane];
     const size_t gc = (size_t)tok * (K / 64) + c;

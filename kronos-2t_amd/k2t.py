@@ -72,6 +72,8 @@ SIGNATURES = {
     "k2t_model_set_head": (I32, [VP, VP, VP]),
     "k2t_model_set_graph": (I32, [VP, I32]),
     "k2t_model_set_exact": (I32, [VP, I32]),
+    "k2t_model_set_persistent": (I32, [VP, I32]),
+    "k2t_model_persistent_active": (I32, [VP, C.POINTER(I32)]),
     "k2t_model_reset": (I32, [VP]),
     "k2t_model_position": (I32, [VP, C.POINTER(I32)]),
     "k2t_model_decode": (I32, [VP, I32, VP]),
@@ -305,6 +307,14 @@ class Model:
 
     def set_exact(self, on):
         check(lib().k2t_model_set_exact(self.h, int(bool(on))))
+
+    def set_persistent(self, on):
+        check(lib().k2t_model_set_persistent(self.h, int(bool(on))))
+
+    def persistent_active(self):
+        v = I32()
+        check(lib().k2t_model_persistent_active(self.h, C.byref(v)))
+        return bool(v.value)
 
     def reset(self):
         check(lib().k2t_model_reset(self.h))

@@ -59,6 +59,9 @@ def test_decode_matches_oracle(gpu_ctx, name, cfg, fmt, planes, exact):
     ref = OracleModel(cfg, layers, head, fn)
     gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
     gm.set_exact(exact)  # fast epilogue: per-segment sums, a few ulp per GEMV output
+    # exact = False also runs the persistent single-launch decode kernel
+    gm.set_persistent(True)
+    assert gm.persistent_active() == (not exact)
     rng = np.random.default_rng(9)
     toks = rng.integers(0, cfg["vocab"], 8)
     for i, t in enumerate(toks):
@@ -87,10 +90,14 @@ def test_long_context_splits(gpu_ctx):
 
 
 def test_prefill_equals_token_by_token_and_graph_equals_eager(gpu_ctx):
+    """Batched prefill and token-by-token decode on the one-kernel-per-operation path run
+    the same arithmetic (bit-exact); the persistent kernel sums attention and GEMV
+    partials in its own fixed order (close, and graph replay == eager bit-exact)."""
     layers, head, fn = random_model(TINY, seed=5, fmt="nf4")
     gm, _ = _gpu_model(gpu_ctx, TINY, layers, head, fn, max_batch=4)
     toks = np.arange(11) * 37 % TINY["vocab"]
     pre = gm.prefill(toks)  # 3 batches of <= 4 tokens (4-token GEMV tiles)
+    gm.set_persistent(False)
     gm.reset()
     gm.set_graph(False)
     for t in toks:
@@ -101,12 +108,44 @@ def test_prefill_equals_token_by_token_and_graph_equals_eager(gpu_ctx):
         graph = gm.decode(int(t))
     assert np.array_equal(pre.view(np.uint32), eager.view(np.uint32))
     assert np.array_equal(graph.view(np.uint32), eager.view(np.uint32))
+    gm.set_persistent(True)
+    assert gm.persistent_active()
+    gm.reset()
+    gm.set_graph(False)
+    for t in toks:
+        pk_eager = gm.decode(int(t))
+    gm.reset()
+    gm.set_graph(True)
+    for t in toks:
+        pk_graph = gm.decode(int(t))
+    assert np.array_equal(pk_graph.view(np.uint32), pk_eager.view(np.uint32))
+    ok, info = _close(pk_eager, eager, 0.99999)
+    assert ok, info
 
 
-def test_greedy_generate_matches_oracle_argmax(gpu_ctx):
+def test_persistent_decode_long_run_matches_per_op(gpu_ctx):
+    """40 decode steps of a 3-layer b5 GQA model (hd 64) on the persistent kernel track the
+    per-operation path step by step (same quantized inputs, different summation order)."""
+    cfg = dict(TINY, n_layers=3, max_seq=48)
+    layers, head, fn = random_model(cfg, seed=11, fmt="n4", planes={k: 5 for k in P55454})
+    a, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
+    b, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
+    a.set_persistent(True)
+    b.set_persistent(False)
+    assert a.persistent_active() and not b.persistent_active()
+    rng = np.random.default_rng(12)
+    for i, t in enumerate(rng.integers(0, cfg["vocab"], 40)):
+        x, y = a.decode(int(t)), b.decode(int(t))
+        ok, info = _close(x, y, 0.9999)
+        assert ok, (i, info)
+
+
+@pytest.mark.parametrize("persistent", [False, True])
+def test_greedy_generate_matches_oracle_argmax(gpu_ctx, persistent):
     layers, head, fn = random_model(TINY, seed=6, fmt="nf4")
     ref = OracleModel(TINY, layers, head, fn)
     gm, _ = _gpu_model(gpu_ctx, TINY, layers, head, fn)
+    gm.set_persistent(persistent)
     out = gm.generate(17, 6)
     tok, seq = 17, []
     for _ in range(6):
