@@ -128,6 +128,8 @@ def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log):
     t_build = time.perf_counter() - t0
     if os.environ.get("K2T_MODEL_EXACT"):
         model.set_exact(int(os.environ["K2T_MODEL_EXACT"]))
+    if os.environ.get("K2T_PERSISTENT"):
+        model.set_persistent(int(os.environ["K2T_PERSISTENT"]))
     wbytes = sum(m.info()[3] for m in mats)
     rng = np.random.default_rng(SEED)
     toks = rng.integers(0, cfg["vocab"], prefill).astype(np.int32)

@@ -27,6 +27,7 @@ struct MkParams {
     // hand-off vectors as {payload, epoch} words
     unsigned long long *HA, *HB, *QKV, *OACT, *GACT;
     float *logits;
+    const uint64_t *signs;  // Hadamard sign masks of 64-blocks (bit i = element i)
     int *err;
     uint32_t spin_limit;
     unsigned long long *trace;  // optional: [wg][layer*6 + phase][3] timestamps (profiling)
@@ -36,7 +37,10 @@ struct MkParams {
 MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4);
 size_t decode_mk_lds_bytes(const k2t_model_config &c);
 bool decode_mk_supported(const k2t_model_config &c, int num_cus);
-void launch_decode_mk(hipStream_t st, const MkParams &P, int num_cus, size_t lds);
+// Accumulates the common weight format of the model's matrices (fmt < 0: first call);
+// false when a matrix differs (the persistent kernel needs one format).
+bool decode_mk_format(const MatDev &m, int &fmt, int &hp);
+void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds);
 void launch_advance_step(hipStream_t st, int *pos, uint32_t *step, int n);
 
 }  // namespace k2t

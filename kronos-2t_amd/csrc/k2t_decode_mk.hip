@@ -104,40 +104,37 @@ __device__ Lds carve(const MkParams &P, float *base) {
     return L;
 }
 
-// Waits for an fp32 vector of n LL words and copies it to LDS.  Returns false (for the
-// whole workgroup) on error.
-__device__ bool load_vec(const MkParams &P, const Lds &S, const unsigned long long *src, int n, uint32_t epoch,
-                         float *dst) {
+// Waits for n LL words; kPoll loads per thread are issued before any is checked, then
+// stragglers are polled one by one.  Payloads go to dst (fp32 vector, act == false) or
+// are unpacked into the LDS activation (codes, scales, sums; act == true).  Returns
+// false (for the whole workgroup) on error.
+constexpr int kPoll = 8;
+__device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, const unsigned long long *src, int n,
+                                           uint32_t epoch, bool act, float *dst) {
     bool ok = true;
-    for (int i = (int)threadIdx.x; i < n; i += kThreads) {
-        uint32_t v = 0;
-        if (!ll_wait(P, src + i, epoch, v)) {
-            ok = false;
-            break;
+    for (int i0 = (int)threadIdx.x; i0 < n; i0 += kThreads * kPoll) {
+        unsigned long long w[kPoll];
+#pragma unroll
+        for (int k = 0; k < kPoll; k++) {
+            const int i = i0 + k * kThreads;
+            w[k] = i < n ? ll_load(src + i) : 0ull;
         }
-        dst[i] = __uint_as_float(v);
-    }
-    if (threadIdx.x == 0) S.flag[0] = 0;
-    __syncthreads();
-    if (!ok) S.flag[0] = 1;
-    __syncthreads();
-    return S.flag[0] == 0;
-}
-
-// Waits for nch int8 activation chunks (kActWords LL words each) and unpacks them into
-// the LDS activation (codes, scales, sums).
-__device__ bool load_act(const MkParams &P, const Lds &S, const unsigned long long *src, int nch, uint32_t epoch) {
-    bool ok = true;
-    for (int i = (int)threadIdx.x; i < nch * kActWords; i += kThreads) {
-        uint32_t v = 0;
-        if (!ll_wait(P, src + i, epoch, v)) {
-            ok = false;
-            break;
+#pragma unroll
+        for (int k = 0; k < kPoll; k++) {
+            const int i = i0 + k * kThreads;
+            if (i < n && ok) {
+                uint32_t v = (uint32_t)w[k];
+                if ((uint32_t)(w[k] >> 32) != epoch && !ll_wait(P, src + i, epoch, v)) ok = false;
+                if (!act) {
+                    dst[i] = __uint_as_float(v);
+                } else {
+                    const int c = i / kActWords, wd = i % kActWords;
+                    if (wd < 16) reinterpret_cast<uint32_t *>(S.xl + c * 64)[wd] = v;
+                    else if (wd == 16) S.xsl[c] = __uint_as_float(v);
+                    else S.xsuml[c] = (int32_t)v;
+                }
+            }
         }
-        const int c = i / kActWords, w = i % kActWords;
-        if (w < 16) reinterpret_cast<uint32_t *>(S.xl + c * 64)[w] = v;
-        else if (w == 16) S.xsl[c] = __uint_as_float(v);
-        else S.xsuml[c] = (int32_t)v;
     }
     if (threadIdx.x == 0) S.flag[0] = 0;
     __syncthreads();
@@ -171,7 +168,8 @@ __device__ void store_act_chunk(float v, uint32_t lane, unsigned long long *dst,
 }
 
 // RMSNorm + FWHT + int8 of S.hbuf[0..d) into the LDS activation: wave 0 computes inv_rms
-// in row_sumsq_wave order (bit-identical to rmsnorm_act_kernel), then one wave per chunk.
+// in row_sumsq_wave order (bit-identical to rmsnorm_act_kernel); then eight lanes per
+// chunk, every chunk of the vector at once (rotate_quant_slice8).
 __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, uint32_t lane, int wave) {
     if (wave == 0) {
         const float ss = row_sumsq_wave(S.hbuf, P.d, lane);
@@ -179,20 +177,38 @@ __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, 
     }
     __syncthreads();
     const float inv_rms = S.vec[0];
-    for (int c = wave; c < P.d / 64; c += kWaves) {
-        const float v = (S.hbuf[c * 64 + lane] * inv_rms) * w[c * 64 + lane];
-        quant_chunk_store(fwht_lane(v, (uint64_t)c, lane), lane, S.xl + c * 64, S.xsl + c, S.xsuml + c);
+    const uint32_t s8 = lane & 7u;
+    const int nc = P.d / 64;
+    for (int c0 = wave * 8; c0 < nc; c0 += kWaves * 8) {
+        const int c = c0 + (int)(lane >> 3);
+        const bool act = c < nc;
+        const int cc = act ? c : 0;
+        const float4 *x4 = reinterpret_cast<const float4 *>(S.hbuf + cc * 64 + s8 * 8);
+        const float4 *w4 = reinterpret_cast<const float4 *>(w + cc * 64 + s8 * 8);
+        const float4 xa = x4[0], xb = x4[1], wa = w4[0], wb = w4[1];
+        float v[8] = {(xa.x * inv_rms) * wa.x, (xa.y * inv_rms) * wa.y, (xa.z * inv_rms) * wa.z,
+                      (xa.w * inv_rms) * wa.w, (xb.x * inv_rms) * wb.x, (xb.y * inv_rms) * wb.y,
+                      (xb.z * inv_rms) * wb.z, (xb.w * inv_rms) * wb.w};
+        rotate_quant_slice8(v, P.signs[cc], s8, cc, act, S.xl, S.xsl, S.xsuml);
     }
     __syncthreads();
 }
 
-// One round of matrix M's row blocks for this wave (dispatch over the weight formats).
-__device__ __forceinline__ void gemv_wave_any(const MatDev &M, int rb, bool active, int wseg, uint32_t lane,
-                                              const Lds &S, float *part) {
-    if (M.fmt == 1) gemv_wave<1, 0>(M, rb, active, wseg, lane, S.xl, S.xsl, S.xsuml, part);
-    else if (M.hp == 0) gemv_wave<0, 0>(M, rb, active, wseg, lane, S.xl, S.xsl, S.xsuml, part);
-    else if (M.hp == 1) gemv_wave<0, 1>(M, rb, active, wseg, lane, S.xl, S.xsl, S.xsuml, part);
-    else gemv_wave<0, 2>(M, rb, active, wseg, lane, S.xl, S.xsl, S.xsuml, part);
+// Phase kinds of the step's schedule: per layer kQkv, kAttn, kO, kGu, kDown; then kHead.
+enum PhaseKind { kQkv = 0, kAttn = 1, kO = 2, kGu = 3, kDown = 4, kHead = 5 };
+
+// Waits for a GEMV phase's input and builds its int8 activation in LDS: the o_proj /
+// down_proj activation chunks as produced, or RMSNorm + FWHT + int8 of the hidden vector
+// (HA after the embedding or a down phase, HB after an o phase).
+__device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, const MkLayer &Ly, int kind,
+                                              uint32_t epoch, uint32_t lane, int wave) {
+    if (kind == kO || kind == kDown) {
+        const int nch = kind == kO ? P.nq * P.hd / 64 : P.inter / 64;
+        return load_words(P, S, kind == kO ? P.OACT : P.GACT, nch * kActWords, epoch, true, nullptr);
+    }
+    if (!load_words(P, S, kind == kGu ? P.HB : P.HA, P.d, epoch, false, S.hbuf)) return false;
+    build_norm_act(P, S, kind == kQkv ? Ly.in_norm : kind == kGu ? Ly.post_norm : P.final_norm, lane, wave);
+    return true;
 }
 
 // Row r of the tied lm_head, dequantized in the rotated domain and inverse-rotated
@@ -270,9 +286,32 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     float *red = scal + 8;                              // [32]
     float *opart = red + 32;                            // [16 waves][hd]
     float *sc = opart + kThreads * 4;                   // [max_seq]
+    const int t = (int)threadIdx.x;
+    const int seq = pos + 1;
+    const size_t base = ((size_t)layer * nkv + kvh) * P.max_seq;
+    const int ncg = hd / 4, nps = kThreads / ncg;
+    const int cg = t % ncg, ps = t / ncg;
+    // 0. past positions' K rows, scales and V slices do not depend on this step: request
+    //    this thread's first ones before waiting for q / k / v.
+    constexpr int kVPre = 8;
+    uint4 kpre[8];
+    float kspre = 0.0f, vspre = 0.0f;
+    if (t < pos) {
+        const uint4 *kr = reinterpret_cast<const uint4 *>(P.kq + (base + t) * hd);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (i < hd / 16) kpre[i] = kr[i];
+        kspre = P.ks[base + t];
+        vspre = P.vs[base + t];
+    }
+    int vpre[kVPre];
+#pragma unroll
+    for (int i = 0; i < kVPre; i++) {
+        const int tt = ps + i * nps;
+        vpre[i] = tt < pos ? *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4) : 0;
+    }
     // 1. this position's q, k, v (+ bias)
     bool ok = true;
-    const int t = (int)threadIdx.x;
     if (t < 3 * hd) {
         const int part = t / hd, i = t % hd;
         const int row = part == 0 ? h * hd + i : part == 1 ? (nq + kvh) * hd + i : (nq + nkv + kvh) * hd + i;
@@ -289,64 +328,70 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     if (S.flag[0]) return false;
     // 2. RoPE (real_llm.rs:9328-9361) on q and k, int8 Hadamard q / k / v
     const size_t slot = ((size_t)layer * nkv + kvh) * P.max_seq + pos;
-    if (wave == 0) {
+    // waves 0, 1, 2 handle q, k, v concurrently
+    if (wave < 2) {
         const float *rrow = P.rope + (size_t)pos * hd;
-        float q0 = qf[lane], q1 = nb > 1 ? qf[64 + lane] : 0.0f;
-        float k0 = kf[lane], k1 = nb > 1 ? kf[64 + lane] : 0.0f;
+        const float *src = wave == 0 ? qf : kf;
+        float x0 = src[lane], x1 = nb > 1 ? src[64 + lane] : 0.0f;
         if (nb == 1) {
             const uint32_t i = lane & 31u;
-            const float c = rrow[i], s = rrow[32 + i];
-            const float qo = __shfl_xor(q0, 32, kWave), ko = __shfl_xor(k0, 32, kWave);
-            q0 = lane < 32 ? q0 * c - qo * s : q0 * c + qo * s;
-            k0 = lane < 32 ? k0 * c - ko * s : k0 * c + ko * s;
+            const float c = rrow[i], sn = rrow[32 + i];
+            const float xo = __shfl_xor(x0, 32, kWave);
+            x0 = lane < 32 ? x0 * c - xo * sn : x0 * c + xo * sn;
         } else {
-            const float c = rrow[lane], s = rrow[64 + lane];
-            const float a0 = q0, a1 = q1, b0 = k0, b1 = k1;
-            q0 = a0 * c - a1 * s;
-            q1 = a1 * c + a0 * s;
-            k0 = b0 * c - b1 * s;
-            k1 = b1 * c + b0 * s;
+            const float c = rrow[lane], sn = rrow[64 + lane];
+            const float a0 = x0, a1 = x1;
+            x0 = a0 * c - a1 * sn;
+            x1 = a1 * c + a0 * sn;
         }
-        const float qs = quant_head(q0, q1, nb, lane, qi);
-        const float ksn = quant_head(k0, k1, nb, lane, kn);
-        const float vsn = quant_head(vf[lane], nb > 1 ? vf[64 + lane] : 0.0f, nb, lane, vn);
-        if (lane == 0) {
-            scal[0] = qs * P.attn_scale;
-            scal[1] = ksn;
-            scal[2] = vsn;
-        }
-        if (h % group == 0) {  // the first q head of the group stores this position's K/V
+        int8_t *dst = wave == 0 ? qi : kn;
+        const float sc8 = quant_head(x0, x1, nb, lane, dst);
+        if (lane == 0) scal[wave] = wave == 0 ? sc8 * P.attn_scale : sc8;
+        if (wave == 1 && h % group == 0) {  // the first q head of the group stores this position's K
             P.kq[slot * hd + lane] = kn[lane];
+            if (nb > 1) P.kq[slot * hd + 64 + lane] = kn[64 + lane];
+            if (lane == 0) P.ks[slot] = sc8;
+        }
+    } else if (wave == 2) {
+        const float vsn = quant_head(vf[lane], nb > 1 ? vf[64 + lane] : 0.0f, nb, lane, vn);
+        if (lane == 0) scal[2] = vsn;
+        if (h % group == 0) {
             P.vq[slot * hd + lane] = vn[lane];
-            if (nb > 1) {
-                P.kq[slot * hd + 64 + lane] = kn[64 + lane];
-                P.vq[slot * hd + 64 + lane] = vn[64 + lane];
-            }
-            if (lane == 0) {
-                P.ks[slot] = ksn;
-                P.vs[slot] = vsn;
-            }
+            if (nb > 1) P.vq[slot * hd + 64 + lane] = vn[64 + lane];
+            if (lane == 0) P.vs[slot] = vsn;
         }
     }
     __syncthreads();
     // 3. scores s_t = float(q8 . k8_t) * ks_t * (qs * scale), t <= pos
-    const int seq = pos + 1;
-    const size_t base = ((size_t)layer * nkv + kvh) * P.max_seq;
     const float qas = scal[0];
     float smax = -INFINITY;
     for (int tt = t; tt < seq; tt += kThreads) {
-        const uint4 *kr = tt == pos ? reinterpret_cast<const uint4 *>(kn)
-                                    : reinterpret_cast<const uint4 *>(P.kq + (base + tt) * hd);
         const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
         int dot = 0;
-        for (int i = 0; i < hd / 16; i++) {
-            const uint4 a = kr[i], b = qr[i];
-            dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
-            dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
-            dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
-            dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
+        float kscale;
+        if (tt == t && tt < pos) {  // prefetched
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (i >= hd / 16) break;
+                const uint4 a = kpre[i], b = qr[i];
+                dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
+            }
+            kscale = kspre;
+        } else {
+            const uint4 *kr = tt == pos ? reinterpret_cast<const uint4 *>(kn)
+                                        : reinterpret_cast<const uint4 *>(P.kq + (base + tt) * hd);
+            for (int i = 0; i < hd / 16; i++) {
+                const uint4 a = kr[i], b = qr[i];
+                dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
+            }
+            kscale = tt == pos ? scal[1] : P.ks[base + tt];
         }
-        const float kscale = tt == pos ? scal[1] : P.ks[base + tt];
         const float s = ((float)dot * kscale) * qas;
         sc[tt] = s;
         smax = fmaxf(smax, s);
@@ -360,25 +405,31 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     float psum = 0.0f;
     for (int tt = t; tt < seq; tt += kThreads) {
         const float p = expf(sc[tt] - m);
-        sc[tt] = p * (tt == pos ? scal[2] : P.vs[base + tt]);  // p_t * vs_t
+        const float vsc = tt == pos ? scal[2] : (tt == t ? vspre : P.vs[base + tt]);
+        sc[tt] = p * vsc;  // p_t * vs_t
         psum += p;
     }
     psum = wave_sum_f(psum);
     if (lane == 0) red[16 + wave] = psum;
     __syncthreads();
     // 4. o = sum_t p_t vs_t v_t: thread = (position subset, 4-column group); the subsets
-    //    of one wave are added with lane shuffles, then the 16 waves' sums in wave order.
-    const int ncg = hd / 4, nps = kThreads / ncg;
-    const int cg = t % ncg, ps = t / ncg;
+    //    of one wave are added with lane shuffles, then the waves' sums in wave order.
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    for (int tt = ps; tt < seq; tt += nps) {
-        const int v = tt == pos ? *reinterpret_cast<const int *>(vn + cg * 4)
-                                : *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4);
-        const float wt = sc[tt];
+    auto vacc = [&](int v, float wt) {
         a0 = fmaf(wt, (float)(int8_t)(v & 0xFF), a0);
         a1 = fmaf(wt, (float)(int8_t)((v >> 8) & 0xFF), a1);
         a2 = fmaf(wt, (float)(int8_t)((v >> 16) & 0xFF), a2);
         a3 = fmaf(wt, (float)(int8_t)((v >> 24) & 0xFF), a3);
+    };
+#pragma unroll
+    for (int i = 0; i < kVPre; i++) {  // prefetched slices, positions in ascending order
+        const int tt = ps + i * nps;
+        if (tt < seq) vacc(tt == pos ? *reinterpret_cast<const int *>(vn + cg * 4) : vpre[i], sc[tt]);
+    }
+    for (int tt = ps + kVPre * nps; tt < seq; tt += nps) {
+        const int v = tt == pos ? *reinterpret_cast<const int *>(vn + cg * 4)
+                                : *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4);
+        vacc(v, sc[tt]);
     }
     for (int m2 = ncg; m2 < 64; m2 <<= 1) {  // lanes l and l ^ m2 hold the same columns
         a0 += __shfl_xor(a0, m2, kWave);
@@ -414,9 +465,9 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     if (P.trace && threadIdx.x == 0)                                                                \
         P.trace[(((size_t)blockIdx.x * (P.L + 1) + (l)) * 6 + (ph)) * 3 + (k)] = wall_clock64();
 
-// Phase kinds of the step's schedule: per layer kQkv, kAttn, kO, kGu, kDown; then kHead.
-enum PhaseKind { kQkv = 0, kAttn = 1, kO = 2, kGu = 3, kDown = 4, kHead = 5 };
-
+// FMT/HP: the one weight format every projection and the head use (mixed-format models
+// run the one-kernel-per-operation path).
+template <int FMT, int HP>
 __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
     extern __shared__ float lds_raw[];
     const Lds S = carve(P, lds_raw);
@@ -440,39 +491,48 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
     for (int ph = 1; ph < (int)nph; ph++) {
         const int l = (ph - 1) / 5;
         const int kind = ph == (int)nph - 1 ? kHead : (ph - 1) % 5;
+        // Each phase kind starts its task list at a different workgroup, so that the
+        // workgroups of consecutive phases are mostly disjoint: a workgroup done with one
+        // phase (or idle in it) is already streaming its next phase's weights.
+        const int nwg = (int)gridDim.x;
+        const int off = (kind == kAttn ? 0 : kind == kO ? 32 : kind == kGu ? 96 : kind == kDown ? 224 : 96) % nwg;
+        const int vb = ((int)blockIdx.x + nwg - off) % nwg;  // this workgroup's rank in the phase
         if (kind == kAttn) {
-            if ((int)blockIdx.x < P.nq) MK_TR(l, 1, 0)
-            for (int h = (int)blockIdx.x; h < P.nq; h += (int)gridDim.x)
+            if (vb < P.nq) MK_TR(l, 1, 0)
+            for (int h = vb; h < P.nq; h += nwg)
                 if (!attention_head(P, P.layers[l], S, l, h, pos, E(ph - 1), E(ph), lane, wave)) return;
-            if ((int)blockIdx.x < P.nq) MK_TR(l, 1, 2)
+            if (vb < P.nq) MK_TR(l, 1, 2)
             continue;
         }
         const MkLayer &Ly = P.layers[kind == kHead ? 0 : l];
         const MatDev &M = kind == kQkv ? Ly.qkv : kind == kO ? Ly.o : kind == kGu ? Ly.gu : kind == kDown ? Ly.down : P.head;
         const int nblocks = M.smode ? M.stripes : M.np + (M.stripes & 1);
         const int groups = kWaves / M.nseg;
-        if ((int)blockIdx.x * groups >= nblocks) continue;  // no task here: go on to the next phase
+        if (vb * groups >= nblocks) continue;  // no task here: go on to the next phase
         const int tr_ph = kind == kHead ? 0 : kind;
         const int tr_l = kind == kHead ? P.L : l;
         MK_TR(tr_l, tr_ph, 0)
-        // ---- input activation -> LDS
-        if (kind == kO || kind == kDown) {
-            if (!load_act(P, S, kind == kO ? P.OACT : P.GACT, kind == kO ? P.nq * P.hd / 64 : P.inter / 64, E(ph - 1)))
-                return;
-            MK_TR(tr_l, tr_ph, 1)
-        } else {
-            // qkv / head read HA (written one phase earlier: embedding or down); gate_up reads HB (o)
-            if (!load_vec(P, S, kind == kGu ? P.HB : P.HA, d, E(ph - 1), S.hbuf)) return;
-            MK_TR(tr_l, tr_ph, 1)
-            build_norm_act(P, S, kind == kQkv ? Ly.in_norm : kind == kGu ? Ly.post_norm : P.final_norm, lane, wave);
-        }
         // ---- GEMV rounds
         const int grp = wave / M.nseg, wseg = wave % M.nseg;
         const int RB = M.smode ? 16 : 32;
         bool ok = true;
-        for (int base = (int)blockIdx.x * groups; base < nblocks; base += (int)gridDim.x * groups) {
+        for (int base = vb * groups; base < nblocks; base += nwg * groups) {
             const int rb = base + grp;
-            gemv_wave_any(M, rb, rb < nblocks, wseg, lane, S, S.part + wave * 32);
+            const bool first = base == vb * groups;
+            // The first round requests its first weight fragments, then waits for the
+            // phase input (the weights stream in meanwhile), then computes.
+#define MK_ROUND(F, H)                                                                               \
+    {                                                                                                \
+        GemvWave<F, H> gw(M, rb, rb < nblocks, wseg, lane);                                          \
+        gw.start();                                                                                  \
+        if (first) {                                                                                 \
+            if (!mk_load_input(P, S, Ly, kind, E(ph - 1), lane, wave)) return;                        \
+            MK_TR(tr_l, tr_ph, 1)                                                                    \
+        }                                                                                            \
+        gw.finish(S.xl, S.xsl, S.xsuml, S.part + wave * 32);                                         \
+    }
+            MK_ROUND(FMT, HP)
+#undef MK_ROUND
             __syncthreads();
             if (t < groups * RB) {
                 const int g2 = t / RB, rl = t % RB, rb2 = base + g2;
@@ -565,19 +625,34 @@ size_t decode_mk_lds_bytes(const k2t_model_config &c) {
     return (b + 255) / 256 * 256;
 }
 
+template <int FMT, int HP>
+static bool occupancy_ok(size_t lds) {
+    int nb = 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_mk_kernel<FMT, HP>, kThreads, lds) == hipSuccess &&
+           nb >= 1;
+}
+
 bool decode_mk_supported(const k2t_model_config &c, int num_cus) {
     if (decode_mk_lds_bytes(c) > 64 * 1024) return false;
     if (c.hidden > 8192 || c.intermediate > 32768) return false;
-    int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_mk_kernel, kThreads, decode_mk_lds_bytes(c)) !=
-            hipSuccess ||
-        nb < 1)
-        return false;
-    return num_cus > 0;
+    const size_t lds = decode_mk_lds_bytes(c);
+    return num_cus > 0 && occupancy_ok<1, 0>(lds) && occupancy_ok<0, 0>(lds);
 }
 
-void launch_decode_mk(hipStream_t st, const MkParams &P, int num_cus, size_t lds) {
-    hipLaunchKernelGGL(decode_mk_kernel, dim3(num_cus), dim3(kThreads), lds, st, P);
+bool decode_mk_format(const MatDev &m, int &fmt, int &hp) {
+    if (m.fmt == 0 && m.hp != 0) return false;  // b5 / b6 fragments exceed the register budget
+    if (fmt < 0) {
+        fmt = m.fmt;
+        hp = m.hp;
+        return true;
+    }
+    return m.fmt == fmt && (m.fmt == 1 || m.hp == hp);
+}
+
+void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds) {
+    if (fmt == 1) hipLaunchKernelGGL((decode_mk_kernel<1, 0>), dim3(num_cus), dim3(kThreads), lds, st, P);
+    else if (hp == 0) hipLaunchKernelGGL((decode_mk_kernel<0, 0>), dim3(num_cus), dim3(kThreads), lds, st, P);
+    else throw Error(K2T_E_INTERNAL, "persistent decode kernel: unsupported weight format");
     hip_check(hipGetLastError(), "decode megakernel launch");
 }
 

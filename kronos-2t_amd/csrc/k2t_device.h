@@ -170,4 +170,64 @@ __device__ __forceinline__ float ifwht_lane(float v, uint64_t block, uint32_t la
     return flip_sign(v * 0.125f, hadamard_sign_bit(block, lane));
 }
 
+// Signed FWHT-64 + int8 quantization of one 64-element chunk held as eight consecutive
+// elements per lane by eight lanes (lane bits 0-2 = s, element s*8 + j): sign flip with
+// the chunk's mask bits, x0.125, butterflies h = 1, 2, 4 in registers and h = 8, 16, 32
+// across lanes (^1, ^2, ^4), then max, int8 round-half-even, scale = max/127 and the code
+// sum.  Each butterfly adds or subtracts the same operands as hadamard.rs:83-97, so the
+// result equals fwht_lane + quant_chunk_store.  All 64 lanes must call it; `act` only
+// gates the stores (codes at xl[c*64 + s*8], scale xsl[c], sum xsuml[c]).
+__device__ __forceinline__ void rotate_quant_slice8(float *v, uint64_t sign_mask, uint32_t s, int c, bool act,
+                                                    int8_t *xl, float *xsl, int32_t *xsuml) {
+    const uint32_t sb = (uint32_t)(sign_mask >> (8u * s)) & 0xFFu;
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = flip_sign(v[j], (sb >> j) & 1u) * 0.125f;
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (!(j & h)) {
+                const float x0 = v[j], x1 = v[j | h];
+                v[j] = x0 + x1;
+                v[j | h] = x0 - x1;
+            }
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+        const bool upper = (s & (uint32_t)m) != 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float p = m == 1 ? xchg1(v[j]) : m == 2 ? xchg2(v[j]) : xchg4(v[j]);
+            v[j] = upper ? p - v[j] : v[j] + p;
+        }
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
+    mx = fmaxf(mx, xchg1(mx));
+    mx = fmaxf(mx, xchg2(mx));
+    mx = fmaxf(mx, xchg4(mx));
+    uint32_t lo = 0, hi = 0;
+    int sum = 0;
+    if (mx > FLT_EPSILON) {
+        const float inv = 127.0f / mx;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int qi = (int)rintf(v[j] * inv);
+            sum += qi;
+            if (j < 4) lo |= ((uint32_t)qi & 0xFFu) << (8 * j);
+            else hi |= ((uint32_t)qi & 0xFFu) << (8 * (j - 4));
+        }
+    }
+    sum += xchg1(sum);
+    sum += xchg2(sum);
+    sum += xchg4(sum);
+    if (act) {
+        *reinterpret_cast<uint2 *>(xl + c * 64 + s * 8) = make_uint2(lo, hi);
+        if (s == 0) {
+            xsl[c] = mx > FLT_EPSILON ? mx / 127.0f : 0.0f;
+            xsuml[c] = sum;
+        }
+    }
+}
+
 }  // namespace k2t

@@ -259,7 +259,23 @@ struct StreamSwap {
     }
 };
 
-bool use_persistent(const k2t_model *m) { return m->persistent && m->mk_ok && !m->exact; }
+// The persistent kernel needs the fast epilogue and one weight format for every matrix.
+bool mk_format(const k2t_model *m, int &fmt, int &hp) {
+    fmt = -1;
+    hp = 0;
+    if (!m->head) return false;
+    for (const auto &L : m->layers) {
+        if (!L.qkv || !L.o || !L.gu || !L.down) return false;
+        for (const k2t_mat *x : {L.qkv, L.o, L.gu, L.down})
+            if (!decode_mk_format(mat_dev(x, false), fmt, hp)) return false;
+    }
+    return decode_mk_format(mat_dev(m->head, false), fmt, hp);
+}
+
+bool use_persistent(const k2t_model *m) {
+    int fmt, hp;
+    return m->persistent && m->mk_ok && !m->exact && mk_format(m, fmt, hp);
+}
 
 // Uploads the layer table of the persistent kernel (matrix views and launch shapes).
 void upload_mk_layers(k2t_model *m) {
@@ -309,6 +325,7 @@ void forward_mk(k2t_model *m) {
     P.OACT = m->ll_oact;
     P.GACT = m->ll_gact;
     P.logits = m->logits;
+    P.signs = m->ctx->signs;
     P.err = m->err_dev;
     P.spin_limit = 1u << 22;
     static unsigned long long *trace = nullptr;  // TEMP profiling: K2T_MK_TRACE=1
@@ -318,7 +335,9 @@ void forward_mk(k2t_model *m) {
         hip_check(hipMemset(trace, 0, n * 8), "trace clear");
         P.trace = trace;
     }
-    launch_decode_mk(m->stream, P, m->ctx->num_cus, m->mk_lds);
+    int fmt = 1, hp = 0;
+    mk_format(m, fmt, hp);
+    launch_decode_mk(m->stream, P, fmt, hp, m->ctx->num_cus, m->mk_lds);
     if (P.trace) {
         const size_t n = (size_t)m->ctx->num_cus * (c.n_layers + 1) * 6 * 3;
         std::vector<unsigned long long> h(n);

@@ -106,55 +106,7 @@ __device__ __forceinline__ void finish_slice(const GemvParams &P, const XSlice &
         if constexpr (XS == 1) v[j] = (a[j] * inv_rms) * b[j];
         else v[j] = (a[j] / (1.0f + expf(-a[j]))) * b[j];
     }
-    const uint32_t sb = (uint32_t)(P.signs[c] >> (8u * s)) & 0xFFu;
-#pragma unroll
-    for (int j = 0; j < 8; j++) v[j] = flip_sign(v[j], (sb >> j) & 1u) * 0.125f;
-#pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (!(j & h)) {
-                const float x0 = v[j], x1 = v[j | h];
-                v[j] = x0 + x1;
-                v[j | h] = x0 - x1;
-            }
-#pragma unroll
-    for (int m = 1; m < 8; m <<= 1) {
-        const bool upper = (s & (uint32_t)m) != 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float p = m == 1 ? xchg1(v[j]) : m == 2 ? xchg2(v[j]) : xchg4(v[j]);
-            v[j] = upper ? p - v[j] : v[j] + p;
-        }
-    }
-    float mx = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
-    mx = fmaxf(mx, xchg1(mx));
-    mx = fmaxf(mx, xchg2(mx));
-    mx = fmaxf(mx, xchg4(mx));
-    uint32_t lo = 0, hi = 0;
-    int sum = 0;
-    if (mx > FLT_EPSILON) {
-        const float inv = 127.0f / mx;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int qi = (int)rintf(v[j] * inv);
-            sum += qi;
-            if (j < 4) lo |= ((uint32_t)qi & 0xFFu) << (8 * j);
-            else hi |= ((uint32_t)qi & 0xFFu) << (8 * (j - 4));
-        }
-    }
-    sum += xchg1(sum);
-    sum += xchg2(sum);
-    sum += xchg4(sum);
-    if (act) {
-        *reinterpret_cast<uint2 *>(xl + c * 64 + s * 8) = make_uint2(lo, hi);
-        if (s == 0) {
-            xsl[c] = mx > FLT_EPSILON ? mx / 127.0f : 0.0f;
-            xsuml[c] = sum;
-        }
-    }
+    rotate_quant_slice8(v, P.signs[c], s, c, act, xl, xsl, xsuml);
 }
 
 // Builds the int8 activation chunks [c0, c1) of one token in LDS in two steps, so that

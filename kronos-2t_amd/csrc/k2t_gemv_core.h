@@ -147,24 +147,62 @@ __device__ __forceinline__ void chunk_dots(const MatDev &M, const WFrag<HP> &fr,
 }
 
 // One wave's share (K segment `wseg`) of row block `rb` against the activation held in
-// LDS (xl codes, xsl scales, xsuml code sums).  The fast epilogue: per-lane-group
-// partial fmaf chains, summed across lane groups in a fixed butterfly order; lanes
-// holding a row's partial write it to part[rloc], part[rloc + 1] (part = this wave's
-// 32-float slot).  Every lane of the wave must call this (cross-lane steps).
+// LDS (xl codes, xsl scales, xsuml code sums), in two steps so that a caller can wait for
+// its activation while the first weights are in flight: start() requests the first two
+// chunk fragments; finish() runs the loop.  The fast epilogue: per-lane-group partial
+// fmaf chains, summed across lane groups in a fixed butterfly order; lanes holding a
+// row's partial write it to part[rloc], part[rloc + 1] (part = this wave's 32-float
+// slot).  Every lane of the wave must take part (cross-lane steps).
 template <int FMT, int HP>
-__device__ void gemv_wave(const MatDev &M, int rb, bool active, int wseg, uint32_t lane, const int8_t *xl,
-                          const float *xsl, const int32_t *xsuml, float *part) {
-    float f0 = 0.0f, f1 = 0.0f;
-    Geo o{};
-    if (active) o = make_geo<FMT, HP>(M, rb, lane);
-    const int G = M.smode ? 8 : 4;
-    const int q = M.smode ? (int)(lane >> 3) : (int)(lane >> 4);
-    const int cw0 = wseg * M.cps, cw1 = active ? min(M.nc, cw0 + M.cps) : cw0;
-    const int iters = cw1 > cw0 ? (cw1 - cw0 + G - 1) / G : 0;
-    const uint32_t half = lane & 1u;
-    auto chunk_of = [&](int i) { return cw0 + i * G + q; };
-    auto valid = [&](int i) { return i < iters && chunk_of(i) < cw1; };
-    auto process = [&](const WFrag<HP> &fr, int c) {
+struct GemvWave {
+    const MatDev &M;
+    Geo o;
+    int cw0, cw1, iters, G, q;
+    uint32_t lane, half;
+    WFrag<HP> fa, fb;
+
+    __device__ __forceinline__ GemvWave(const MatDev &M_, int rb, bool active, int wseg, uint32_t lane_)
+        : M(M_), o{}, lane(lane_), half(lane_ & 1u) {
+        if (active) o = make_geo<FMT, HP>(M, rb, lane);
+        G = M.smode ? 8 : 4;
+        q = M.smode ? (int)(lane >> 3) : (int)(lane >> 4);
+        cw0 = wseg * M.cps;
+        cw1 = active ? min(M.nc, cw0 + M.cps) : cw0;
+        iters = cw1 > cw0 ? (cw1 - cw0 + G - 1) / G : 0;
+    }
+    __device__ __forceinline__ int chunk_of(int i) const { return cw0 + i * G + q; }
+    __device__ __forceinline__ bool valid(int i) const { return i < iters && chunk_of(i) < cw1; }
+
+    __device__ __forceinline__ void start() {
+        if (valid(0)) fetch_w<FMT, HP>(M, o, chunk_of(0), fa);
+        if (valid(1)) fetch_w<FMT, HP>(M, o, chunk_of(1), fb);
+    }
+
+    __device__ __forceinline__ void finish(const int8_t *xl, const float *xsl, const int32_t *xsuml, float *part) {
+        float f0 = 0.0f, f1 = 0.0f;
+        for (int i = 0; i < iters; i += 2) {
+            if (valid(i)) process(fa, chunk_of(i), xl, xsl, xsuml, f0, f1);
+            if (valid(i + 2)) fetch_w<FMT, HP>(M, o, chunk_of(i + 2), fa);
+            if (valid(i + 1)) process(fb, chunk_of(i + 1), xl, xsl, xsuml, f0, f1);
+            if (valid(i + 3)) fetch_w<FMT, HP>(M, o, chunk_of(i + 3), fb);
+        }
+        if (M.smode) {
+            f0 += __int_as_float(dpp_ror8(__float_as_int(f0)));
+            f1 += __int_as_float(dpp_ror8(__float_as_int(f1)));
+        }
+        f0 += __shfl_xor(f0, 16, kWave);
+        f0 += __shfl_xor(f0, 32, kWave);
+        f1 += __shfl_xor(f1, 16, kWave);
+        f1 += __shfl_xor(f1, 32, kWave);
+        const uint32_t rloc = (M.smode ? 0u : ((lane >> 3) & 1u) * 16u) + 4u * ((lane >> 1) & 3u) + 2u * half;
+        if (M.smode ? lane < 8 : lane < 16) {
+            part[rloc] = f0;
+            part[rloc + 1] = f1;
+        }
+    }
+
+    __device__ __forceinline__ void process(const WFrag<HP> &fr, int c, const int8_t *xl, const float *xsl,
+                                            const int32_t *xsuml, float &f0, float &f1) const {
         uint2 x[4];
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) x[kk] = *reinterpret_cast<const uint2 *>(xl + c * 64 + kk * 16 + half * 8);
@@ -176,28 +214,7 @@ __device__ void gemv_wave(const MatDev &M, int rb, bool active, int wseg, uint32
         const float n1 = fmaf((float)r1 * sx, bf16_hi(fr.ws), f1);
         f0 = sx != 0.0f ? n0 : f0;
         f1 = sx != 0.0f ? n1 : f1;
-    };
-    WFrag<HP> fa, fb;
-    if (valid(0)) fetch_w<FMT, HP>(M, o, chunk_of(0), fa);
-    for (int i = 0; i < iters; i += 2) {
-        if (valid(i + 1)) fetch_w<FMT, HP>(M, o, chunk_of(i + 1), fb);
-        if (valid(i)) process(fa, chunk_of(i));
-        if (valid(i + 2)) fetch_w<FMT, HP>(M, o, chunk_of(i + 2), fa);
-        if (valid(i + 1)) process(fb, chunk_of(i + 1));
     }
-    if (M.smode) {
-        f0 += __int_as_float(dpp_ror8(__float_as_int(f0)));
-        f1 += __int_as_float(dpp_ror8(__float_as_int(f1)));
-    }
-    f0 += __shfl_xor(f0, 16, kWave);
-    f0 += __shfl_xor(f0, 32, kWave);
-    f1 += __shfl_xor(f1, 16, kWave);
-    f1 += __shfl_xor(f1, 32, kWave);
-    const uint32_t rloc = (M.smode ? 0u : ((lane >> 3) & 1u) * 16u) + 4u * ((lane >> 1) & 3u) + 2u * half;
-    if (M.smode ? lane < 8 : lane < 16) {
-        part[rloc] = f0;
-        part[rloc + 1] = f1;
-    }
-}
+};
 
 }  // namespace k2t

@@ -59,9 +59,10 @@ def test_decode_matches_oracle(gpu_ctx, name, cfg, fmt, planes, exact):
     ref = OracleModel(cfg, layers, head, fn)
     gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
     gm.set_exact(exact)  # fast epilogue: per-segment sums, a few ulp per GEMV output
-    # exact = False also runs the persistent single-launch decode kernel
+    # exact = False also runs the persistent single-launch decode kernel where every matrix
+    # has one format other than b6 (p55454 mixes b5 and b4)
     gm.set_persistent(True)
-    assert gm.persistent_active() == (not exact)
+    assert gm.persistent_active() == (not exact and name == "nf4_hd64")
     rng = np.random.default_rng(9)
     toks = rng.integers(0, cfg["vocab"], 8)
     for i, t in enumerate(toks):
@@ -124,10 +125,10 @@ def test_prefill_equals_token_by_token_and_graph_equals_eager(gpu_ctx):
 
 
 def test_persistent_decode_long_run_matches_per_op(gpu_ctx):
-    """40 decode steps of a 3-layer b5 GQA model (hd 64) on the persistent kernel track the
+    """40 decode steps of a 3-layer b4 GQA model (hd 64) on the persistent kernel track the
     per-operation path step by step (same quantized inputs, different summation order)."""
     cfg = dict(TINY, n_layers=3, max_seq=48)
-    layers, head, fn = random_model(cfg, seed=11, fmt="n4", planes={k: 5 for k in P55454})
+    layers, head, fn = random_model(cfg, seed=11, fmt="n4", planes={k: 4 for k in P55454})
     a, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
     b, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
     a.set_persistent(True)
