@@ -217,11 +217,12 @@ int32_t k2t_model_set_graph(k2t_model *m, int32_t enable);
 /* GEMV epilogue of this model's steps (see k2t_ctx_set_exact); default 0 = fast.
  * exact = 1 also disables the persistent decode kernel (it sums per-segment chains). */
 int32_t k2t_model_set_exact(k2t_model *m, int32_t exact);
-/* 1: a decode step runs as one persistent kernel (one workgroup per CU) whose
+/* 1 (default): a decode step runs as one persistent kernel (one workgroup per CU) whose
  * phases hand vectors over through {payload, epoch} words instead of kernel boundaries:
- * the shape of forward_token_sdot_megakernel (real_llm.rs:6794-7403).  0 (default): one
- * kernel per operation.  Used only where the device and model shape allow it (see
- * k2t_model_persistent_active). */
+ * the shape of forward_token_sdot_megakernel (real_llm.rs:6794-7403).  0: one kernel per
+ * operation.  Used only with the fast epilogue, when every matrix is NF4 or every matrix
+ * has 4 bit planes, and the device and model shape allow it (see
+ * k2t_model_persistent_active); otherwise the per-operation path runs. */
 int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable);
 int32_t k2t_model_persistent_active(const k2t_model *m, int32_t *active);
 /* reset_context: position back to 0. */

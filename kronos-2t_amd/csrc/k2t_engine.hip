@@ -120,8 +120,8 @@ struct k2t_model {
     int exact = 0;  // GEMV epilogue mode used by this model's steps
     hipGraphExec_t graph = nullptr;
     std::vector<void *> allocs;
-    // persistent single-launch decode step (fast epilogue only; opt-in)
-    bool persistent = false;
+    // persistent single-launch decode step (fast epilogue, NF4 or 4-plane weights)
+    bool persistent = true;
     bool mk_ok = false;
     size_t mk_lds = 0;
     uint32_t *step_dev = nullptr;
