@@ -96,8 +96,9 @@ int32_t k2t_mat_upload_nibble4(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t
                                const uint8_t *pair, size_t pair_len, const uint8_t *tail,
                                size_t tail_len, k2t_mat **out);
 
-/* Uploads an NfSdotMatrix (simd_lut.rs:4796-4842) with `bits` = 4 and
- * scale_group_chunks = sgc (1..8).  Lengths follow pair_total_bytes /
+/* Uploads an NfSdotMatrix (simd_lut.rs:4796-4842) with `bits` = 4 (NF4, 512-byte
+ * stripe-chunks) or 3 (NF3, 384-byte stripe-chunks of 48-byte triplet blocks,
+ * simd_lut.rs:4932-4960) and scale_group_chunks = sgc (1..8).  Lengths follow pair_total_bytes /
  * tail_total_bytes (simd_lut.rs:4834-4842).  codebook = the matrix's i8[16]. */
 int32_t k2t_mat_upload_nf(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t bits, int32_t sgc,
                           const int8_t *codebook16, const uint8_t *pair, size_t pair_len,
@@ -159,7 +160,7 @@ int32_t k2t_gemv_chunk_dots(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq,
 /* ---- offline weight compiler (host memory, multi-threaded) ------------- */
 
 /* Byte lengths of the pair / tail streams: fmt 1 = bit planes (planes 4..6),
- * fmt 2 = NF (bits 4, sgc 1..8).  Nibble4SdotMatrix::pair_rec_bytes /
+ * fmt 2 = NF (bits 3 or 4, sgc 1..8).  Nibble4SdotMatrix::pair_rec_bytes /
  * NfSdotMatrix::pair_total_bytes (simd_lut.rs:3281-3288, 4834-4842). */
 int32_t k2t_stream_sizes(int32_t fmt, int32_t rows, int32_t cols, int32_t planes_or_bits, int32_t sgc,
                          size_t *pair_len, size_t *tail_len);
@@ -176,7 +177,8 @@ int32_t k2t_compile_bipolar(const float *W, int32_t rows, int32_t cols, int32_t 
 /* compile_hadamard_gptq_nf without a Hessian for NF4 (compiler.rs:1404-1866:
  * fitted Lloyd-Max codebook, 11-ratio RTN + least-squares BF16 refit) followed by
  * NfSdotMatrix::from_indices (simd_lut.rs:4850-5023) and, if requested,
- * to_gate_up_interleaved (5500-5523).  Writes the codebook and mu_top (nullable). */
+ * to_gate_up_interleaved (5500-5523).  Writes the codebook and mu_top (nullable).
+ * bits must be 4. */
 int32_t k2t_compile_nf(const float *W, int32_t rows, int32_t cols, int32_t bits, int32_t sgc,
                        int32_t interleave_gate_up, int32_t threads, int8_t *codebook16, float *mu_top,
                        uint8_t *pair, size_t pair_len, uint8_t *tail, size_t tail_len);

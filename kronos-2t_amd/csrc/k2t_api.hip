@@ -74,13 +74,16 @@ static size_t nibble4_tail_len(int rows, int cols, int hp) {
     size_t stripes = (size_t)(rows + 15) / 16;
     return (stripes & 1) * (size_t)(cols / 64) * (512 + 128 * (size_t)hp + 32);
 }
-static size_t nf_pair_len(int rows, int cols, int sgc) {
+// Bytes per stripe-chunk: NF4 512 (nibbles), NF3 384 (48-byte triplet blocks),
+// NfSdotMatrix::chunk_bytes (simd_lut.rs:4826-4833).
+static size_t nf_chunk_bytes(int bits) { return bits == 3 ? 384 : 512; }
+static size_t nf_pair_len(int rows, int cols, int bits, int sgc) {
     size_t stripes = (size_t)(rows + 15) / 16, nc = (size_t)cols / 64, nsg = (nc + sgc - 1) / sgc;
-    return (stripes / 2) * (nsg * 64 + nc * 2 * 512);
+    return (stripes / 2) * (nsg * 64 + nc * 2 * nf_chunk_bytes(bits));
 }
-static size_t nf_tail_len(int rows, int cols, int sgc) {
+static size_t nf_tail_len(int rows, int cols, int bits, int sgc) {
     size_t stripes = (size_t)(rows + 15) / 16, nc = (size_t)cols / 64, nsg = (nc + sgc - 1) / sgc;
-    return (stripes & 1) * (nsg * 32 + nc * 512);
+    return (stripes & 1) * (nsg * 32 + nc * nf_chunk_bytes(bits));
 }
 
 static void fill_common(k2t_mat *m, int rows, int cols) {
@@ -158,11 +161,11 @@ static k2t_mat *make_nf(k2t_ctx *ctx, int rows, int cols, int bits, int sgc, con
                         const void *pair, size_t pl, const void *tail, size_t tl, bool device_src) {
     arg_check(ctx != nullptr, "ctx is NULL");
     check_shape(rows, cols);
-    arg_check(bits == 4, "only NF4 (bits = 4) codebook stripes are supported by this build");
+    arg_check(bits == 3 || bits == 4, "NF codebook stripes must have 3 or 4 bits");
     arg_check(sgc >= 1 && sgc <= 8, "scale_group_chunks must be in 1..8");
     arg_check(cb != nullptr, "codebook is NULL");
-    arg_check(pl == nf_pair_len(rows, cols, sgc), "pair stream length does not match the NF layout");
-    arg_check(tl == nf_tail_len(rows, cols, sgc), "tail stream length does not match the NF layout");
+    arg_check(pl == nf_pair_len(rows, cols, bits, sgc), "pair stream length does not match the NF layout");
+    arg_check(tl == nf_tail_len(rows, cols, bits, sgc), "tail stream length does not match the NF layout");
     k2t_mat *m = new k2t_mat();
     m->ctx = ctx;
     m->device = ctx->device;

@@ -436,10 +436,10 @@ int32_t k2t_stream_sizes(int32_t fmt, int32_t rows, int32_t cols, int32_t planes
         return K2T_OK;
     }
     if (fmt == 2) {
-        if (planes_or_bits != 4 || sgc < 1 || sgc > 8) return K2T_E_ARG;
-        const size_t nsg = (nc + sgc - 1) / sgc;
-        *pair_len = (stripes / 2) * (nsg * 64 + nc * 1024);
-        *tail_len = (stripes & 1) * (nsg * 32 + nc * 512);
+        if ((planes_or_bits != 3 && planes_or_bits != 4) || sgc < 1 || sgc > 8) return K2T_E_ARG;
+        const size_t nsg = (nc + sgc - 1) / sgc, cb = planes_or_bits == 3 ? 384 : 512;
+        *pair_len = (stripes / 2) * (nsg * 64 + nc * 2 * cb);
+        *tail_len = (stripes & 1) * (nsg * 32 + nc * cb);
         return K2T_OK;
     }
     return K2T_E_ARG;
@@ -464,6 +464,7 @@ int32_t k2t_compile_nf(const float *W, int32_t rows, int32_t cols, int32_t bits,
                        int32_t interleave_gate_up, int32_t threads, int8_t *codebook16, float *mu_top,
                        uint8_t *pair, size_t pair_len, uint8_t *tail, size_t tail_len) {
     size_t pl = 0, tl = 0;
+    if (bits != 4) return K2T_E_ARG;  // this compiler packs NF4 only
     if (!W || !codebook16 || k2t_stream_sizes(2, rows, cols, bits, sgc, &pl, &tl) != K2T_OK) return K2T_E_ARG;
     if (pl != pair_len || tl != tail_len || (pl && !pair) || (tl && !tail)) return K2T_E_ARG;
     if (interleave_gate_up && rows % 128) return K2T_E_ARG;

@@ -595,7 +595,7 @@ MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4) {
     d.nc = m->nc;
     d.np = m->pairs;
     d.stripes = m->stripes;
-    d.fmt = m->fmt == K2T_FMT_NF ? 1 : 0;
+    d.fmt = m->fmt == K2T_FMT_NF ? (m->bits == 3 ? 2 : 1) : 0;  // 2: NF3 (per-operation path only)
     d.hp = m->hp;
     d.sgc = m->sgc;
     d.cb0 = m->cb[0];
@@ -641,6 +641,7 @@ bool decode_mk_supported(const k2t_model_config &c, int num_cus) {
 
 bool decode_mk_format(const MatDev &m, int &fmt, int &hp) {
     if (m.fmt == 0 && m.hp != 0) return false;  // b5 / b6 fragments exceed the register budget
+    if (m.fmt == 2) return false;                 // NF3 runs on the per-operation path
     if (fmt < 0) {
         fmt = m.fmt;
         hp = m.hp;

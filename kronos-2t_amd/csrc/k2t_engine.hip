@@ -518,6 +518,7 @@ int32_t k2t_model_set_head(k2t_model *m, const k2t_mat *lm_head, const float *fi
     return mguard([&] {
         arg(m && lm_head && final_norm, "NULL argument");
         arg(lm_head->rows == m->cfg.vocab && lm_head->cols == m->cfg.hidden, "lm_head shape mismatch");
+        arg(lm_head->fmt != K2T_FMT_NF || lm_head->bits == 4, "the tied lm_head must be NF4 or bit planes");
         arg(lm_head->ctx == m->ctx, "matrix of another context");
         hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
         if (!m->final_norm) m->final_norm = (float *)dalloc(m, m->cfg.hidden * sizeof(float));

@@ -203,7 +203,9 @@ struct Frag {
 // columns for 4 rows with v_dot4_i32_i8.  One DPP step over `half` completes the exact
 // i32 dot of each (row, chunk).  The fp32 terms float(dot)*sx and ws are staged in LDS
 // and one thread per row replays the reference's fmaf chain in chunk order.
-// FMT 0: bit-plane Nibble4 with HP hi planes; FMT 1: NF4 codebook stripes.
+// FMT 0: bit-plane Nibble4 with HP hi planes; FMT 1: NF4 codebook stripes; FMT 2: NF3
+// codebook stripes (384-byte stripe-chunks of 48-byte triplet blocks; lane bit 0 then
+// picks the 32-column half of the chunk instead of an 8-column half of each block).
 #ifdef K2T_GEMV_TS
 __device__ unsigned long long k2t_gemv_ts[1 << 20];
 #define K2T_TS(k)                                                                                   \
@@ -256,8 +258,11 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         nib_off = (is_tail ? 0u : side * 512u) + g * 32u + half * 16u;
         hi_off = (is_tail ? 512u : 1024u + side * 128u * HP) + g * 16u;
         sc_off = (is_tail ? 512u + 128u * HP : 1024u + 256u * HP + side * 32u);
-    } else {
+    } else if constexpr (FMT == 1) {
         nib_off = (is_tail ? 32u : 64u + side * 512u) + g * 32u + half * 16u;
+        sc_off = is_tail ? 0u : side * 32u;
+    } else {
+        nib_off = (is_tail ? 32u : 64u + side * 384u) + half * 192u + g * 48u;
         sc_off = is_tail ? 0u : side * 32u;
     }
     sc_off += (4u * g + 2u * half) * 2u;
@@ -269,14 +274,20 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             rec = mbase + (size_t)c * (is_tail ? TREC : PREC);
             scp = rec;
         } else {
+            constexpr size_t CB = FMT == 1 ? 512 : 384;  // bytes per stripe-chunk
             const int sg = c / P.sgc, cst = sg * P.sgc, sb = c - cst;
-            const uint8_t *gb = mbase + (is_tail ? (size_t)sg * 32 + (size_t)cst * 512
-                                                 : (size_t)sg * 64 + (size_t)cst * 1024);
-            rec = gb + (size_t)sb * (is_tail ? 512 : 1024);
+            const uint8_t *gb = mbase + (is_tail ? (size_t)sg * 32 + (size_t)cst * CB
+                                                 : (size_t)sg * 64 + (size_t)cst * 2 * CB);
+            rec = gb + (size_t)sb * (is_tail ? CB : 2 * CB);
             scp = gb;
         }
+        if constexpr (FMT == 2) {
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) fr.w[kk] = load_stream16(rec + nib_off + kk * 128);
+            for (int kk = 0; kk < 3; kk++) fr.w[kk] = load_stream16(rec + nib_off + kk * 16);
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) fr.w[kk] = load_stream16(rec + nib_off + kk * 128);
+        }
 
         if constexpr (FMT == 0 && HP == 2) {
 #pragma unroll
@@ -291,8 +302,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         for (int t = 0; t < NT; t++) {
 #pragma unroll
             for (int kk = 0; kk < 4; kk++)
-                fr.x[t][kk] = *reinterpret_cast<const uint2 *>(P.xq + (size_t)(tok0 + t) * P.K + c * 64 + kk * 16 +
-                                                               half * 8);
+                fr.x[t][kk] = *reinterpret_cast<const uint2 *>(P.xq + (size_t)(tok0 + t) * P.K + c * 64 +
+                                                               (FMT == 2 ? half * 32 + kk * 8 : kk * 16 + half * 8));
             fr.sx[t] = P.xs[(size_t)(tok0 + t) * P.nc + c];
             if constexpr (FMT == 0) fr.sum[t] = P.xsum[(size_t)(tok0 + t) * P.nc + c];
         }
@@ -311,7 +322,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     auto process = [&](Frag<HP, NT> &fr, int c) {
         if constexpr (XS != 0) {  // activation built in LDS by this wave
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) fr.x[0][kk] = *reinterpret_cast<const uint2 *>(xl + c * 64 + kk * 16 + half * 8);
+            for (int kk = 0; kk < 4; kk++)
+                fr.x[0][kk] = *reinterpret_cast<const uint2 *>(xl + c * 64 +
+                                                              (FMT == 2 ? half * 32 + kk * 8 : kk * 16 + half * 8));
             fr.sx[0] = xsl[c];
             if constexpr (FMT == 0) fr.sum[0] = xsuml[c];
         }
@@ -320,8 +333,40 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         for (int t = 0; t < NT; t++)
 #pragma unroll
             for (int j = 0; j < 4; j++) acc[t][j] = 0;
+        if constexpr (FMT == 2) {
+            // NF3 triplets (simd_lut.rs:4932-4960): bytes (v0, v1, v2) of row j, column
+            // group t hold the 3-bit codes of columns k0*16 + 4q + t (q = 0..3, codes 0-3)
+            // and k1*16 + 4q + t (codes 4-7), k0 = 2*half, k1 = k0 + 1.  Four columns per
+            // dword; one v_perm reads the 8-entry codebook.
+            const uint32_t p0[4] = {fr.w[0].x, fr.w[0].y, fr.w[0].z, fr.w[0].w};
+            const uint32_t p1[4] = {fr.w[1].x, fr.w[1].y, fr.w[1].z, fr.w[1].w};
+            const uint32_t p2[4] = {fr.w[2].x, fr.w[2].y, fr.w[2].z, fr.w[2].w};
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
+            for (int j = 0; j < 4; j++) {
+                const uint32_t v0 = p0[j], v1 = p1[j], v2 = p2[j];
+                const uint32_t id[8] = {v0 & 0x07070707u,
+                                        (v0 >> 3) & 0x07070707u,
+                                        ((v0 >> 6) & 0x03030303u) | ((v2 >> 4) & 0x04040404u),
+                                        v1 & 0x07070707u,
+                                        (v1 >> 3) & 0x07070707u,
+                                        ((v1 >> 6) & 0x03030303u) | ((v2 >> 5) & 0x04040404u),
+                                        v2 & 0x07070707u,
+                                        (v2 >> 3) & 0x07070707u};
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const uint32_t xw[8] = {fr.x[t][0].x, fr.x[t][0].y, fr.x[t][1].x, fr.x[t][1].y,
+                                            fr.x[t][2].x, fr.x[t][2].y, fr.x[t][3].x, fr.x[t][3].y};
+                    int a = acc[t][j];
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+                        a = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(P.cb1, P.cb0, id[u]), (int)xw[u], a,
+                                                   false);
+                    acc[t][j] = a;
+                }
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < (FMT == 2 ? 0 : 4); kk++) {
             const uint32_t wd[4] = {fr.w[kk].x, fr.w[kk].y, fr.w[kk].z, fr.w[kk].w};
             uint4 hv = make_uint4(0, 0, 0, 0);
             if constexpr (HP == 2) hv = fr.h[kk];
@@ -563,7 +608,8 @@ static void launch_nt(int nt, int xs, dim3 grid, dim3 block, size_t lds, hipStre
 template <bool DOTS>
 static void launch_fmt(const k2t_mat *m, int nt, int xs, dim3 grid, dim3 block, size_t lds, hipStream_t st,
                        const GemvParams &P) {
-    if (m->fmt == K2T_FMT_NF) launch_nt<1, 0, DOTS>(nt, xs, grid, block, lds, st, P);
+    if (m->fmt == K2T_FMT_NF && m->bits == 3) launch_nt<2, 0, DOTS>(nt, xs, grid, block, lds, st, P);
+    else if (m->fmt == K2T_FMT_NF) launch_nt<1, 0, DOTS>(nt, xs, grid, block, lds, st, P);
     else if (m->hp == 0) launch_nt<0, 0, DOTS>(nt, xs, grid, block, lds, st, P);
     else if (m->hp == 1) launch_nt<0, 1, DOTS>(nt, xs, grid, block, lds, st, P);
     else launch_nt<0, 2, DOTS>(nt, xs, grid, block, lds, st, P);

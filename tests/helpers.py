@@ -49,11 +49,11 @@ def quantized_nibble4(rng, rows, cols, planes, std=0.02, interleave=False):
     return W, u, sc, pair, tail
 
 
-def random_nf_streams(rng, rows, cols, sgc):
-    idx = rng.integers(0, 16, (rows, cols), dtype=np.uint8)
+def random_nf_streams(rng, rows, cols, sgc, bits=4):
+    idx = rng.integers(0, 1 << bits, (rows, cols), dtype=np.uint8)
     nsg = (cols // 64 + sgc - 1) // sgc
     sc = random_bf16_scales(rng, ((rows + 15) // 16) * nsg * 16)
-    pair, tail = O.nf_from_indices(idx, sc, rows, cols, 4, sgc)
+    pair, tail = O.nf_from_indices(idx, sc, rows, cols, bits, sgc)
     return idx, sc, pair, tail
 
 

@@ -138,6 +138,52 @@ def test_nf4_gemv_exact(gpu_ctx, sgc, rows, cols):
     assert _close(_run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, exact=False)[0], ref)
 
 
+@pytest.mark.parametrize("sgc", [1, 2])
+@pytest.mark.parametrize("rows,cols", [(1536, 2048), (40, 256), (2048, 768)])
+def test_nf3_gemv_exact(gpu_ctx, sgc, rows, cols):
+    """NF3 stripes (simd_lut.rs:4932-4960, 6074-6364 with BITS = 3): 8-entry codebook,
+    48-byte triplet blocks.  Integer dots and the exact epilogue bit-exact."""
+    import torch
+    rng = np.random.default_rng(rows + cols + sgc + 3)
+    idx, sc, pair, tail = random_nf_streams(rng, rows, cols, sgc, bits=3)
+    cb = np.zeros(16, np.int8)
+    cb[:8] = np.sort(rng.choice(np.arange(-127, 128), 8, replace=False)).astype(np.int8)
+    m = gpu_ctx.upload_nf(rows, cols, 3, sgc, cb, pair, tail)
+    xq, xs, xsum = acts(rng, cols, 1, n_outliers=3, zero_chunk=1)
+    ref, dots = O.nf_gemv(pair, tail, rows, cols, 3, sgc, cb, xq[0], xs[0], want_dots=True)
+    d = torch.zeros((rows, cols // 64), dtype=torch.int32, device="cuda")
+    gpu_ctx.gemv_chunk_dots(m, _t(xq[0]), None, d)
+    assert np.array_equal(d.cpu().numpy(), dots)
+    out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    assert _close(_run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, exact=False)[0], ref)
+
+
+def test_nf3_expert_slice_pair_range_and_batch(gpu_ctx):
+    """nf_sdot_pair_stream_range_slices (simd_lut.rs:6372-6540): an expert's NF3 g128
+    gate_up slice (rows % 32 == 0, no tail) run over a pair sub-range writes exactly those
+    rows; 4-token tiles equal the per-token results."""
+    rng = np.random.default_rng(21)
+    rows, cols, sgc = 1536, 2048, 2
+    W = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    cb, mu = O.nf_fit_codebook(W, 3, sgc)
+    idx, sc = O.nf_rtn(W, 3, sgc, cb, mu)
+    pair, tail = O.nf_from_indices(idx, sc, rows, cols, 3, sgc)
+    assert tail.size == 0
+    m = gpu_ctx.upload_nf(rows, cols, 3, sgc, cb, pair, tail)
+    xq, xs, xsum = acts(rng, cols, 4, outlier_frac=0.001, outlier_scale=30.0)
+    p0, p1 = 7, 30  # pair range -> stripes [14, 60)
+    out = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, s0=2 * p0, s1=2 * p1)[0]
+    ref = O.nf_gemv(pair, tail, rows, cols, 3, sgc, cb, xq[0], xs[0], s0=2 * p0, s1=2 * p1)
+    lo, hi = 32 * p0, 32 * p1
+    assert np.array_equal(out[lo:hi].view(np.uint32), ref[lo:hi].view(np.uint32))
+    assert np.isnan(out[:lo]).all() and np.isnan(out[hi:]).all()
+    batch = _run_gemv(gpu_ctx, m, xq, xs, xsum, rows, ntok=4)
+    for t in range(4):
+        single = O.nf_gemv(pair, tail, rows, cols, 3, sgc, cb, xq[t], xs[t])
+        assert np.array_equal(batch[t].view(np.uint32), single.view(np.uint32)), t
+
+
 def test_nf4_quantized_model_matrix(gpu_ctx):
     rng = np.random.default_rng(3)
     rows, cols = 2048, 2048
