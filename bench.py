@@ -56,7 +56,8 @@ class GemvCase:
             pair, tail = k2t.compile_bipolar(W, 6)
             self.cb = None
         else:
-            cb, mu, pair, tail = k2t.compile_nf4(W, 2)
+            self.bits = 3 if fmt == "nf3" else 4
+            cb, mu, pair, tail = k2t.compile_nf4(W, 2, bits=self.bits)
             self.cb = cb
         del W
         self.stream_bytes = pair.size + tail.size + (16 if self.cb is not None else 0)
@@ -71,8 +72,8 @@ class GemvCase:
             if fmt == "b6":
                 self.mats.append(ctx.wrap_nibble4(rows, cols, 2, p, pair.size, t if tail.size else None, tail.size))
             else:
-                self.mats.append(ctx.wrap_nf(rows, cols, 4, 2, self.cb, p, pair.size, t if tail.size else None,
-                                             tail.size))
+                self.mats.append(ctx.wrap_nf(rows, cols, self.bits, 2, self.cb, p, pair.size,
+                                             t if tail.size else None, tail.size))
         self.pair_host, self.tail_host = pair, tail
         rng = np.random.default_rng(SEED + cols)
         x = rng.standard_normal((ntok, cols)).astype(np.float32)
@@ -227,7 +228,8 @@ def main():
 
     # ---- config 4: GEMV sweep
     specs = [("nf4g128_14336x4096", "nf4", 14336, 4096), ("nf4g128_4096x14336", "nf4", 4096, 14336),
-             ("b6_14336x4096", "b6", 14336, 4096), ("b6_4096x14336", "b6", 4096, 14336)]
+             ("b6_14336x4096", "b6", 14336, 4096), ("b6_4096x14336", "b6", 4096, 14336),
+             ("nf3g128_14336x4096", "nf3", 14336, 4096), ("nf3g128_4096x14336", "nf3", 4096, 14336)]
     only = [s for s in args.only.split(",") if s]
     results = {}
     dom = None

@@ -174,11 +174,11 @@ int32_t k2t_compile_bipolar(const float *W, int32_t rows, int32_t cols, int32_t 
                             int32_t interleave_gate_up, int32_t threads, uint8_t *pair, size_t pair_len,
                             uint8_t *tail, size_t tail_len);
 
-/* compile_hadamard_gptq_nf without a Hessian for NF4 (compiler.rs:1404-1866:
+/* compile_hadamard_gptq_nf without a Hessian for NF4 / NF3 (compiler.rs:1404-1866:
  * fitted Lloyd-Max codebook, 11-ratio RTN + least-squares BF16 refit) followed by
  * NfSdotMatrix::from_indices (simd_lut.rs:4850-5023) and, if requested,
  * to_gate_up_interleaved (5500-5523).  Writes the codebook and mu_top (nullable).
- * bits must be 4. */
+ * bits = 3 or 4. */
 int32_t k2t_compile_nf(const float *W, int32_t rows, int32_t cols, int32_t bits, int32_t sgc,
                        int32_t interleave_gate_up, int32_t threads, int8_t *codebook16, float *mu_top,
                        uint8_t *pair, size_t pair_len, uint8_t *tail, size_t tail_len);

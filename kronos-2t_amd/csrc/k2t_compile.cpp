@@ -206,8 +206,8 @@ static void compile_bipolar(const float *W, size_t rows, size_t cols, int planes
 
 // ---------------------------------------------------------------- NF4
 
-static float fit_nf4_codebook(const float *W, size_t rows, size_t cols, size_t sgc, int8_t *cb,
-                              const SignTable &st) {
+static float fit_nf_codebook(const float *W, size_t rows, size_t cols, int bits, size_t sgc, int8_t *cb,
+                             const SignTable &st) {
     const int HIST = 2000;
     const float BIN_W = 5.0f / 2000.0f;
     const size_t nc = cols / 64, nsg = (nc + sgc - 1) / sgc;
@@ -235,12 +235,18 @@ static float fit_nf4_codebook(const float *W, size_t rows, size_t cols, size_t s
     }
     static const int8_t NF4_DEFAULT[16] = {-127, -96, -75, -58, -44, -31, -18, -6,
                                            6,    18,  31,  44,  58,  75,  96,  127};
+    static const int8_t NF3_DEFAULT[16] = {-127, -79, -45, -14, 14, 45, 79, 127, 0, 0, 0, 0, 0, 0, 0, 0};
     if (total < 256) {
-        memcpy(cb, NF4_DEFAULT, 16);
-        return 2.7326f;
+        memcpy(cb, bits == 3 ? NF3_DEFAULT : NF4_DEFAULT, 16);
+        return bits == 3 ? 2.1520f : 2.7326f;
     }
-    const int half = 8;
+    // Lloyd-Max start points of the positive half (compiler.rs:1404-1526)
+    const int half = 1 << (bits - 1);
     double mu[8] = {0.1284, 0.3881, 0.6568, 0.9424, 1.2562, 1.6180, 2.0690, 2.7326};
+    if (bits == 3) {
+        const double mu3[4] = {0.2451, 0.7560, 1.3439, 2.1520};
+        for (int m = 0; m < 4; m++) mu[m] = mu3[m];
+    }
     for (int it = 0; it < 24; it++) {
         size_t bounds[9];
         bounds[0] = 0;
@@ -271,6 +277,7 @@ static float fit_nf4_codebook(const float *W, size_t rows, size_t cols, size_t s
         if (q[m] >= q[m + 1]) q[m] = std::max(q[m + 1] - 1, 1);
     for (int m = 1; m < half; m++)
         if (q[m] <= q[m - 1]) q[m] = std::min(q[m - 1] + 1, 127);
+    memset(cb, 0, 16);
     for (int m = 0; m < half; m++) {
         cb[half - 1 - m] = (int8_t)(-q[m]);
         cb[half + m] = (int8_t)q[m];
@@ -278,24 +285,32 @@ static float fit_nf4_codebook(const float *W, size_t rows, size_t cols, size_t s
     return (float)top;
 }
 
-static inline size_t nf4_nearest(float w, float inv_delta, const float *th) {
+// compiler.rs:1660-1699 quant_nearest: decision tree over the midpoints of the positive half.
+template <int BITS>
+static inline size_t nf_nearest(float w, float inv_delta, const float *th) {
+    constexpr size_t half = (size_t)1 << (BITS - 1);
     const float aw = fabsf(w) * inv_delta;
     size_t mag;
-    if (aw < th[3]) mag = aw < th[1] ? (size_t)(aw >= th[0]) : 2 + (size_t)(aw >= th[2]);
-    else mag = aw < th[5] ? 4 + (size_t)(aw >= th[4]) : 6 + (size_t)(aw >= th[6]);
-    return w >= 0.0f ? 8 + mag : 7 - mag;
+    if constexpr (BITS == 4) {
+        if (aw < th[3]) mag = aw < th[1] ? (size_t)(aw >= th[0]) : 2 + (size_t)(aw >= th[2]);
+        else mag = aw < th[5] ? 4 + (size_t)(aw >= th[4]) : 6 + (size_t)(aw >= th[6]);
+    } else {
+        mag = aw < th[1] ? (size_t)(aw >= th[0]) : 2 + (size_t)(aw >= th[2]);
+    }
+    return w >= 0.0f ? half + mag : half - 1 - mag;
 }
 
 // One scale group of one row: returns the BF16 scale and writes indices.
-static uint16_t nf4_group(const float *sub, size_t glen, const float *cbf, const float *th, float mu_top,
-                          uint8_t *best, uint8_t *cand) {
+template <int BITS>
+static uint16_t nf_group(const float *sub, size_t glen, const float *cbf, const float *th, float mu_top,
+                         uint8_t *best, uint8_t *cand) {
     static const float ratios[11] = {0.74f, 0.80f, 0.86f, 0.91f, 0.96f, 1.00f,
                                      1.04f, 1.09f, 1.15f, 1.22f, 1.30f};
     float ss = 0.0f;
     for (size_t j = 0; j < glen; j++) ss += sub[j] * sub[j];
     const float rms = sqrtf(ss / (float)glen);
     if (rms <= 1e-12f) {
-        memset(best, 7, glen);
+        memset(best, (1 << (BITS - 1)) - 1, glen);
         return 0;
     }
     const float base = rms * (mu_top / 127.0f);
@@ -308,7 +323,7 @@ static uint16_t nf4_group(const float *sub, size_t glen, const float *cbf, const
         const float inv = 1.0f / delta;
         float loss = 0.0f;
         for (size_t j = 0; j < glen; j++) {
-            const size_t k = nf4_nearest(sub[j], inv, th);
+            const size_t k = nf_nearest<BITS>(sub[j], inv, th);
             cand[j] = (uint8_t)k;
             const float diff = sub[j] - cbf[k] * delta;
             loss += diff * diff;
@@ -333,16 +348,45 @@ static uint16_t nf4_group(const float *sub, size_t glen, const float *cbf, const
     return bestd;
 }
 
-static void compile_nf4(const float *W, size_t rows, size_t cols, size_t sgc, bool interleave, int threads,
-                        int8_t *cb, float *mu_out, uint8_t *pair, uint8_t *tail) {
+// NF3 stripe-chunk (simd_lut.rs:4932-4960): for each column pair-block kp (16-column
+// blocks 2kp, 2kp+1), row group g and (row j, column t) three bytes at
+// kp*192 + g*48 + {0, 16, 32} + j*4 + t pack the eight 3-bit codes of columns
+// 16*k + 4*quad + t (k in {2kp, 2kp+1}, quad 0..3): v0 = i0 | i1<<3 | (i2&3)<<6,
+// v1 = i3 | i4<<3 | (i5&3)<<6, v2 = i6 | i7<<3 | (i2>>2)<<6 | (i5>>2)<<7.
+static void pack_nf3_chunk(const uint8_t *idx, size_t cols, size_t c, size_t s, size_t rows, uint8_t *dst) {
+    for (size_t kp = 0; kp < 2; kp++)
+        for (size_t g = 0; g < 4; g++)
+            for (size_t j = 0; j < 4; j++) {
+                const size_t lane = g * 4 + j;
+                const bool live = s * 16 + lane < rows;
+                const uint8_t *ir = idx + lane * cols + c * 64;
+                for (size_t t = 0; t < 4; t++) {
+                    uint8_t i[8];
+                    for (size_t u = 0; u < 8; u++) {
+                        const size_t k = 2 * kp + u / 4, quad = u % 4;
+                        i[u] = live ? ir[k * 16 + quad * 4 + t] & 7 : 0;
+                    }
+                    uint8_t *blk = dst + kp * 192 + g * 48 + j * 4 + t;
+                    blk[0] = (uint8_t)(i[0] | (i[1] << 3) | ((i[2] & 3) << 6));
+                    blk[16] = (uint8_t)(i[3] | (i[4] << 3) | ((i[5] & 3) << 6));
+                    blk[32] = (uint8_t)(i[6] | (i[7] << 3) | (((i[2] >> 2) & 1) << 6) | (((i[5] >> 2) & 1) << 7));
+                }
+            }
+}
+
+template <int BITS>
+static void compile_nf(const float *W, size_t rows, size_t cols, size_t sgc, bool interleave, int threads,
+                       int8_t *cb, float *mu_out, uint8_t *pair, uint8_t *tail) {
+    constexpr size_t CB = BITS == 3 ? 384 : 512;  // bytes per stripe-chunk
+    constexpr int half = 1 << (BITS - 1);
     const size_t nc = cols / 64, nsg = (nc + sgc - 1) / sgc, stripes = (rows + 15) / 16, np = stripes / 2;
-    const size_t ptot = nsg * 64 + nc * 1024, ttot = nsg * 32 + nc * 512;
+    const size_t ptot = nsg * 64 + nc * 2 * CB, ttot = nsg * 32 + nc * CB;
     SignTable st(nc);
-    const float mu_top = fit_nf4_codebook(W, rows, cols, sgc, cb, st);
+    const float mu_top = fit_nf_codebook(W, rows, cols, BITS, sgc, cb, st);
     if (mu_out) *mu_out = mu_top;
     float cbf[16], th[7];
     for (int k = 0; k < 16; k++) cbf[k] = (float)cb[k];
-    for (int m = 0; m < 7; m++) th[m] = 0.5f * (cbf[8 + m] + cbf[9 + m]);
+    for (int m = 0; m + 1 < half; m++) th[m] = 0.5f * (cbf[half + m] + cbf[half + m + 1]);
     memset(pair, 0, np * ptot);
     if (stripes & 1) memset(tail, 0, ttot);
     parallel_for(stripes, threads, [&](size_t s) {
@@ -357,7 +401,7 @@ static void compile_nf4(const float *W, size_t rows, size_t cols, size_t sgc, bo
             for (size_t sg = 0; sg < nsg; sg++) {
                 const size_t c0 = sg * sgc, c1 = std::min(nc, c0 + sgc), glen = (c1 - c0) * 64;
                 scales[lane * nsg + sg] =
-                    nf4_group(row.data() + c0 * 64, glen, cbf, th, mu_top, best.data(), cand.data());
+                    nf_group<BITS>(row.data() + c0 * 64, glen, cbf, th, mu_top, best.data(), cand.data());
                 memcpy(idx.data() + lane * cols + c0 * 64, best.data(), glen);
             }
         }
@@ -366,15 +410,18 @@ static void compile_nf4(const float *W, size_t rows, size_t cols, size_t sgc, bo
         const size_t side = s & 1;
         for (size_t sg = 0; sg < nsg; sg++) {
             const size_t c0 = sg * sgc, c1 = std::min(nc, c0 + sgc);
-            uint8_t *gb = in_pair ? pair + (s / 2) * ptot + sg * 64 + c0 * 1024 : tail + sg * 32 + c0 * 512;
+            uint8_t *gb = in_pair ? pair + (s / 2) * ptot + sg * 64 + c0 * 2 * CB : tail + sg * 32 + c0 * CB;
             uint8_t *sp = gb + (in_pair ? side * 32 : 0);
             for (size_t lane = 0; lane < 16; lane++) {
                 sp[lane * 2] = (uint8_t)scales[lane * nsg + sg];
                 sp[lane * 2 + 1] = (uint8_t)(scales[lane * nsg + sg] >> 8);
             }
             for (size_t c = c0; c < c1; c++) {
-                uint8_t *dst = in_pair ? gb + (in_pair ? 64 : 32) + (c - c0) * 1024 + side * 512
-                                       : gb + 32 + (c - c0) * 512;
+                uint8_t *dst = in_pair ? gb + 64 + (c - c0) * 2 * CB + side * CB : gb + 32 + (c - c0) * CB;
+                if constexpr (BITS == 3) {
+                    pack_nf3_chunk(idx.data(), cols, c, s, rows, dst);
+                    continue;
+                }
                 for (size_t k = 0; k < 4; k++)
                     for (size_t g = 0; g < 4; g++)
                         for (size_t j = 0; j < 4; j++) {
@@ -464,13 +511,16 @@ int32_t k2t_compile_nf(const float *W, int32_t rows, int32_t cols, int32_t bits,
                        int32_t interleave_gate_up, int32_t threads, int8_t *codebook16, float *mu_top,
                        uint8_t *pair, size_t pair_len, uint8_t *tail, size_t tail_len) {
     size_t pl = 0, tl = 0;
-    if (bits != 4) return K2T_E_ARG;  // this compiler packs NF4 only
     if (!W || !codebook16 || k2t_stream_sizes(2, rows, cols, bits, sgc, &pl, &tl) != K2T_OK) return K2T_E_ARG;
     if (pl != pair_len || tl != tail_len || (pl && !pair) || (tl && !tail)) return K2T_E_ARG;
     if (interleave_gate_up && rows % 128) return K2T_E_ARG;
     try {
-        host::compile_nf4(W, (size_t)rows, (size_t)cols, (size_t)sgc, interleave_gate_up != 0, threads, codebook16,
-                          mu_top, pair, tail);
+        if (bits == 3)
+            host::compile_nf<3>(W, (size_t)rows, (size_t)cols, (size_t)sgc, interleave_gate_up != 0, threads,
+                                codebook16, mu_top, pair, tail);
+        else
+            host::compile_nf<4>(W, (size_t)rows, (size_t)cols, (size_t)sgc, interleave_gate_up != 0, threads,
+                                codebook16, mu_top, pair, tail);
     } catch (...) {
         return K2T_E_INTERNAL;
     }

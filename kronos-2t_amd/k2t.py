@@ -251,17 +251,17 @@ def compile_bipolar(W, planes, interleave_gate_up=False, threads=0):
     return pair, tail
 
 
-def compile_nf4(W, sgc=2, interleave_gate_up=False, threads=0):
-    """Host RTN NF4 compile -> (codebook int8[16], mu_top, pair, tail)."""
+def compile_nf4(W, sgc=2, interleave_gate_up=False, threads=0, bits=4):
+    """Host RTN NF4 (bits=4) / NF3 (bits=3) compile -> (codebook int8[16], mu_top, pair, tail)."""
     import numpy as np
     W = np.ascontiguousarray(W, np.float32)
     rows, cols = W.shape
-    pl, tl = stream_sizes(2, rows, cols, 4, sgc)
+    pl, tl = stream_sizes(2, rows, cols, bits, sgc)
     pair = np.empty(pl, np.uint8)
     tail = np.empty(tl, np.uint8)
     cb = np.zeros(16, np.int8)
     mu = C.c_float()
-    check(lib().k2t_compile_nf(W.ctypes.data_as(VP), rows, cols, 4, sgc, int(interleave_gate_up), threads,
+    check(lib().k2t_compile_nf(W.ctypes.data_as(VP), rows, cols, bits, sgc, int(interleave_gate_up), threads,
                                cb.ctypes.data_as(VP), C.byref(mu), pair.ctypes.data_as(VP) if pl else None, pl,
                                tail.ctypes.data_as(VP) if tl else None, tl))
     return cb, mu.value, pair, tail
