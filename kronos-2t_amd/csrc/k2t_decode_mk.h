@@ -30,7 +30,6 @@ struct MkParams {
     const uint64_t *signs;  // Hadamard sign masks of 64-blocks (bit i = element i)
     int *err;
     uint32_t spin_limit;
-    unsigned long long *trace;  // optional: [wg][layer*6 + phase][3] timestamps (profiling)
 };
 
 // pair_mode_nseg4: gate_up layout (4 wave groups = one [gate64, up64] block of 4 pairs).

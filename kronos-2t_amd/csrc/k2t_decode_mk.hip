@@ -461,10 +461,6 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     return true;
 }
 
-#define MK_TR(l, ph, k)                                                                             \
-    if (P.trace && threadIdx.x == 0)                                                                \
-        P.trace[(((size_t)blockIdx.x * (P.L + 1) + (l)) * 6 + (ph)) * 3 + (k)] = wall_clock64();
-
 // FMT/HP: the one weight format every projection and the head use (mixed-format models
 // run the one-kernel-per-operation path).
 template <int FMT, int HP>
@@ -479,7 +475,6 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
     const uint32_t nph = 2u + 5u * (uint32_t)P.L;
     auto E = [&](int ph) { return step * nph + (uint32_t)ph + 1u; };
     const int d = P.d;
-    MK_TR(P.L, 5, 0)
 
     // phase 0: embedding -> HA (one wave per 64-element chunk)
     {
@@ -498,10 +493,8 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
         const int off = (kind == kAttn ? 0 : kind == kO ? 32 : kind == kGu ? 96 : kind == kDown ? 224 : 96) % nwg;
         const int vb = ((int)blockIdx.x + nwg - off) % nwg;  // this workgroup's rank in the phase
         if (kind == kAttn) {
-            if (vb < P.nq) MK_TR(l, 1, 0)
             for (int h = vb; h < P.nq; h += nwg)
                 if (!attention_head(P, P.layers[l], S, l, h, pos, E(ph - 1), E(ph), lane, wave)) return;
-            if (vb < P.nq) MK_TR(l, 1, 2)
             continue;
         }
         const MkLayer &Ly = P.layers[kind == kHead ? 0 : l];
@@ -509,9 +502,6 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
         const int nblocks = M.smode ? M.stripes : M.np + (M.stripes & 1);
         const int groups = kWaves / M.nseg;
         if (vb * groups >= nblocks) continue;  // no task here: go on to the next phase
-        const int tr_ph = kind == kHead ? 0 : kind;
-        const int tr_l = kind == kHead ? P.L : l;
-        MK_TR(tr_l, tr_ph, 0)
         // ---- GEMV rounds
         const int grp = wave / M.nseg, wseg = wave % M.nseg;
         const int RB = M.smode ? 16 : 32;
@@ -527,7 +517,6 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
         gw.start();                                                                                  \
         if (first) {                                                                                 \
             if (!mk_load_input(P, S, Ly, kind, E(ph - 1), lane, wave)) return;                        \
-            MK_TR(tr_l, tr_ph, 1)                                                                    \
         }                                                                                            \
         gw.finish(S.xl, S.xsl, S.xsuml, S.part + wave * 32);                                         \
     }
@@ -573,7 +562,6 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
             }
         }
         if (!ok) return;
-        MK_TR(tr_l, tr_ph, 2)
     }
 }
 

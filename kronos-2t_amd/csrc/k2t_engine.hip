@@ -196,19 +196,8 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
     // One token: the RMSNorm / SwiGLU + FWHT + int8 activations are built inside the GEMVs
     // (each wave for its own chunks); batches use the standalone kernels.  Same codes.
     const bool fused = ntok == 1;
-    static int skip = getenv("K2T_SKIP") ? atoi(getenv("K2T_SKIP")) : 0;  // TEMP timing probe
     for (int l = 0; l < c.n_layers; l++) {
         const auto &L = m->layers[l];
-        if (fused && skip) {
-            if (!(skip & 1)) launch_gemv_fused(ctx, L.qkv, K2T_XS_RMSNORM, m->hidden, L.in_norm, c.rms_eps, m->qkv, false);
-            if (!(skip & 2)) launch_qkv_post(st, m->qkv, L.bias, m->rope, m->pos_dev, nq, nkv, hd, ntok, l, c.max_seq, m->kq, m->vq, m->ks, m->vs);
-            if (!(skip & 4)) launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, m->pos_dev, l, nq, nkv, hd,
-                         c.max_seq, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum);
-            if (!(skip & 8)) launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
-            if (!(skip & 16)) launch_gemv_fused(ctx, L.gu, K2T_XS_RMSNORM, m->hidden, L.post_norm, c.rms_eps, m->gu, false);
-            if (!(skip & 32)) launch_gemv_fused(ctx, L.down, K2T_XS_SWIGLU, m->gu, nullptr, 0.0f, m->hidden, true);
-            continue;
-        }
         if (fused) {
             launch_gemv_fused(ctx, L.qkv, K2T_XS_RMSNORM, m->hidden, L.in_norm, c.rms_eps, m->qkv, false);
         } else {
@@ -328,27 +317,9 @@ void forward_mk(k2t_model *m) {
     P.signs = m->ctx->signs;
     P.err = m->err_dev;
     P.spin_limit = 1u << 22;
-    static unsigned long long *trace = nullptr;  // TEMP profiling: K2T_MK_TRACE=1
-    if (getenv("K2T_MK_TRACE") && !m->use_graph) {
-        const size_t n = (size_t)m->ctx->num_cus * (c.n_layers + 1) * 6 * 3;
-        if (!trace) hip_check(hipMalloc(&trace, n * 8), "trace");
-        hip_check(hipMemset(trace, 0, n * 8), "trace clear");
-        P.trace = trace;
-    }
     int fmt = 1, hp = 0;
     mk_format(m, fmt, hp);
     launch_decode_mk(m->stream, P, fmt, hp, m->ctx->num_cus, m->mk_lds);
-    if (P.trace) {
-        const size_t n = (size_t)m->ctx->num_cus * (c.n_layers + 1) * 6 * 3;
-        std::vector<unsigned long long> h(n);
-        hip_check(hipStreamSynchronize(m->stream), "sync");
-        hip_check(hipMemcpy(h.data(), trace, n * 8, hipMemcpyDeviceToHost), "trace copy");
-        FILE *f = fopen(getenv("K2T_MK_TRACE"), "wb");
-        if (f) {
-            fwrite(h.data(), 8, n, f);
-            fclose(f);
-        }
-    }
     launch_advance_step(m->stream, m->pos_dev, m->step_dev, 1);
 }
 

@@ -206,19 +206,6 @@ struct Frag {
 // FMT 0: bit-plane Nibble4 with HP hi planes; FMT 1: NF4 codebook stripes; FMT 2: NF3
 // codebook stripes (384-byte stripe-chunks of 48-byte triplet blocks; lane bit 0 then
 // picks the 32-column half of the chunk instead of an 8-column half of each block).
-#ifdef K2T_GEMV_TS
-__device__ unsigned long long k2t_gemv_ts[1 << 20];
-#define K2T_TS(k)                                                                                   \
-    if (lane == 0) {                                                                                \
-        k2t_gemv_ts[((size_t)blockIdx.x * P.nseg + wave) * 6 + (k)] = wall_clock64();              \
-        if ((k) == 0)                                                                               \
-            k2t_gemv_ts[((size_t)blockIdx.x * P.nseg + wave) * 6 + 5] =                             \
-                ((unsigned long long)__builtin_amdgcn_s_getreg((15 << 11) | 20) << 32) |           \
-                __builtin_amdgcn_s_getreg((31 << 11) | 4);                                          \
-    }
-#else
-#define K2T_TS(k)
-#endif
 
 template <int FMT, int HP, int NT, bool DOTS, int XS>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
@@ -442,7 +429,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     auto chunk_of = [&](int i) { return cw0 + i * G + q; };
     const int iters = (cw1 - cw0 + G - 1) / G;  // wave-uniform
     auto valid = [&](int i) { return i < iters && chunk_of(i) < cw1; };
-    K2T_TS(0)
     if constexpr (NT == 1) {
         // Two fragments in flight: chunk i+1 is fetched before chunk i is processed.
         Frag<HP, NT> fa, fb;
@@ -458,7 +444,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         } else {
             if (valid(0)) fetch(fa, chunk_of(0));
         }
-        K2T_TS(1)
         for (int i = 0; i < iters; i += 2) {
             if (XS == 0 && valid(i + 1)) fetch(fb, chunk_of(i + 1));
             if (valid(i)) process(fa, chunk_of(i));
@@ -476,7 +461,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         }
     }
 
-    K2T_TS(2)
     if (!P.exact) {
         // Fast epilogue: add the lane groups' partial chains (fixed butterfly order, so the
         // result is deterministic), then the waves' partials in wave order.
@@ -499,7 +483,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             }
         }
         __syncthreads();
-        K2T_TS(3)
         const int nrows_blk = (is_tail && !smode) ? 16 : RB;
         const int first_stripe = smode ? rb : (is_tail ? 2 * P.np : 2 * rb);
         for (int idx = (int)threadIdx.x; idx < NT * RB; idx += (int)blockDim.x) {
@@ -513,11 +496,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             float *o = P.out + (size_t)(tok0 + t) * P.out_stride + row;
             *o = P.accum ? *o + acc : acc;
         }
-        K2T_TS(4)
         return;
     }
     __syncthreads();
-    K2T_TS(3)
     const int nrows_blk = (is_tail && !smode) ? 16 : RB;
     const int first_stripe = smode ? rb : (is_tail ? 2 * P.np : 2 * rb);
     // One thread per (token, row of the block) replays the chain; LDS reads are batched
@@ -545,7 +526,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         float *o = P.out + (size_t)(tok0 + t) * P.out_stride + row;
         *o = P.accum ? *o + acc : acc;
     }
-    K2T_TS(4)
 }
 
 uint64_t hadamard_sign_mask_host(uint64_t block) {
