@@ -214,6 +214,17 @@ int32_t k2t_model_set_layer(k2t_model *m, int32_t layer, const k2t_mat *qkv, con
 /* Tied quantized lm_head (also the embedding table, embed_token_into real_llm.rs:8063-8097)
  * and the final norm. */
 int32_t k2t_model_set_head(k2t_model *m, const k2t_mat *lm_head, const float *final_norm);
+/* Embedding source, in embed_token_into's precedence (real_llm.rs:8063-8097):
+ *   K2T_EMBED_TIED (default): row `token` of the quantized lm_head, dequantized in the
+ *                   rotated domain and inverse-rotated (the lm_head must be NF4 or bit planes);
+ *   K2T_EMBED_F32 / K2T_EMBED_BF16: untied rows [vocab][hidden] (host array, copied);
+ *   K2T_EMBED_NF4:  an NF4 matrix [vocab][hidden] of the same context (borrowed),
+ *                   read like the tied head (embed_nf4, real_llm.rs:8086-8090). */
+#define K2T_EMBED_TIED 0
+#define K2T_EMBED_F32 1
+#define K2T_EMBED_BF16 2
+#define K2T_EMBED_NF4 3
+int32_t k2t_model_set_embedding(k2t_model *m, int32_t kind, const void *rows, const k2t_mat *nf4);
 /* 1 (default): capture the decode step once and replay it as a HIP graph. */
 int32_t k2t_model_set_graph(k2t_model *m, int32_t enable);
 /* GEMV epilogue of this model's steps (see k2t_ctx_set_exact); default 0 = fast.
@@ -243,6 +254,48 @@ int32_t k2t_model_generate(k2t_model *m, int32_t first_token, int32_t n_steps, i
 /* Device pointer of the last logits (valid after a step; read after k2t_model_sync). */
 int32_t k2t_model_logits(k2t_model *m, const float **d_logits);
 int32_t k2t_model_sync(k2t_model *m);
+
+/* ---- .k2tb compiled models ------------------------------------------------ */
+
+/* A memory-mapped .k2tb file: the cache of RealLlamaEngine::save_bipolar
+ * (real_llm.rs:3705-3895), versions 1-4 and 6, as read by load_bipolar
+ * (real_llm.rs:3902-4190).  Every read is bounds-checked: a truncated or corrupt file
+ * returns K2T_E_ARG; matrices this path cannot run (VQ2, Q2C, NF2/NF5, 2-3 bit planes)
+ * and K2TKRONOS5 MoE cores return K2T_E_STATE. */
+typedef struct k2t_k2tb k2t_k2tb;
+typedef struct k2t_k2tb_matrix_info {
+    int32_t tag;            /* cache tag: 0 FusedBipolar, 2 NfSdot */
+    int32_t fmt;            /* stream format after repack: 1 Nibble4 (bit planes), 2 NF */
+    int32_t rows, cols;
+    int32_t planes_or_bits; /* bit planes (4..6) or NF bits (3, 4) */
+    int32_t sgc;            /* NF scale-group chunks */
+    int8_t codebook[16];    /* NF codebook */
+    size_t pair_len, tail_len; /* repacked stream sizes */
+} k2t_k2tb_matrix_info;
+
+int32_t k2t_k2tb_open(const char *path, k2t_k2tb **out);
+void k2t_k2tb_close(k2t_k2tb *f);
+/* Version (1..6), layer count, the six mode words (RealWeightMode, real_llm.rs:3790-3848). */
+int32_t k2t_k2tb_header(const k2t_k2tb *f, int32_t *version, int32_t *n_layers, uint64_t *mode_words6);
+/* One matrix in the layout the GEMV streams (repack_sdot, real_llm.rs:3657-3702):
+ * bit-plane bodies become Nibble4SdotMatrix records (from_bipolar_with_perm,
+ * simd_lut.rs:3297-3400), NF streams are copied; interleave_gate_up = 1 reorders rows
+ * into [gate64(ic), up64(ic)] blocks (simd_lut.rs:5500-5523 for NF).
+ * layer >= 0: which 0 qkv, 1 o, 2 gate_up, 3 down; layer = -1: which 4 lm_head,
+ * 5 NF4 embedding.  pair = tail = NULL fills `info` only (size query). */
+int32_t k2t_k2tb_matrix(const k2t_k2tb *f, int32_t layer, int32_t which, int32_t interleave_gate_up,
+                        k2t_k2tb_matrix_info *info, uint8_t *pair, size_t pair_cap, uint8_t *tail,
+                        size_t tail_cap);
+/* Vectors: layer >= 0: which 0 input_norm, 1 post_attn_norm, 2 qkv_bias, 3 q_norm,
+ * 4 k_norm (f32); layer = -1: 0 final_norm, 1 f32 embedding rows (f32), 2 bf16
+ * embedding rows (uint16).  *count = elements (0 when absent); out = NULL queries. */
+int32_t k2t_k2tb_vector(const k2t_k2tb *f, int32_t layer, int32_t which, size_t *count, void *out, size_t cap);
+/* load_bipolar + repack_sdot (real_llm.rs:3902-4190, 3657-3702) onto the context's
+ * device: creates the model for `cfg` (LlamaConfig from config.json, whose layer count
+ * must match the file), uploads every matrix (owned by the model) and sets the layers,
+ * head and embedding. */
+int32_t k2t_model_load_k2tb(k2t_ctx *ctx, const k2t_model_config *cfg, const char *path, int32_t max_batch,
+                            k2t_model **out);
 
 #ifdef __cplusplus
 }

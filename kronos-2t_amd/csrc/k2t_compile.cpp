@@ -23,6 +23,7 @@
 
 #include "../../include/k2t_hip.h"
 #include "k2t_internal.h"
+#include "k2t_pack.h"
 
 namespace k2t {
 namespace host {
@@ -83,32 +84,7 @@ static float from_bf16(uint16_t b) {
     return f;
 }
 
-template <typename F>
-static void parallel_for(size_t n, int threads, F &&fn) {
-    if (threads <= 0) threads = (int)std::max(1u, std::thread::hardware_concurrency());
-    threads = (int)std::min<size_t>((size_t)threads, std::max<size_t>(n, 1));
-    if (threads <= 1) {
-        for (size_t i = 0; i < n; i++) fn(i);
-        return;
-    }
-    std::vector<std::thread> pool;
-    const size_t per = (n + threads - 1) / threads;
-    for (int t = 0; t < threads; t++) {
-        const size_t b = t * per, e = std::min(n, b + per);
-        if (b >= e) break;
-        pool.emplace_back([&, b, e] {
-            for (size_t i = b; i < e; i++) fn(i);
-        });
-    }
-    for (auto &th : pool) th.join();
-}
-
-// Source row of destination row `r` under the [gate64(ic), up64(ic)] interleave.
-static size_t source_row(size_t r, size_t rows, bool interleave) {
-    if (!interleave) return r;
-    const size_t blk = r / 64, off = r % 64, inter_dim = rows / 2;
-    return (blk / 2) * 64 + off + ((blk & 1) ? inter_dim : 0);
-}
+static size_t source_row(size_t r, size_t rows, bool interleave) { return gate_up_source_row(r, rows, interleave); }
 
 // ---------------------------------------------------------------- bit planes
 
@@ -167,38 +143,11 @@ static void compile_bipolar(const float *W, size_t rows, size_t cols, int planes
             if (r >= rows) break;
             memcpy(row.data(), W + source_row(r, rows, interleave) * cols, cols * sizeof(float));
             fwht_row(row.data(), cols, st);
-            const size_t g = lane / 4, j = lane % 4;
+            const N4RecOffsets off = n4_offsets(in_pair, side, hp);
             for (size_t c = 0; c < nc; c++) {
                 const uint16_t sc = bipolar_chunk(row.data() + c * 64, planes, codes.data() + c * 64);
-                uint8_t *rec;
-                size_t doff, hoff, soff;
-                if (in_pair) {
-                    rec = pair + (p * nc + c) * prec;
-                    doff = side * 512;
-                    hoff = 1024 + side * 128 * hp;
-                    soff = 1024 + 256 * hp + side * 32;
-                } else {
-                    rec = tail + c * trec;
-                    doff = 0;
-                    hoff = 512;
-                    soff = 512 + 128 * hp;
-                }
-                rec[soff + lane * 2] = (uint8_t)sc;
-                rec[soff + lane * 2 + 1] = (uint8_t)(sc >> 8);
-                for (size_t k = 0; k < 4; k++)
-                    for (size_t w = 0; w < 16; w++) {
-                        const uint8_t uv = codes[c * 64 + k * 16 + w];
-                        const size_t half = w / 8, sub = w / 4, t = w % 4;
-                        const uint8_t lo = uv & 0x0F;
-                        rec[doff + k * 128 + g * 32 + half * 16 + j * 4 + t] |= (w % 8) < 4 ? lo : (uint8_t)(lo << 4);
-                        if (hp == 1) {
-                            const int bit = (k & 1) == 0 ? 4 + (int)sub : (int)sub;
-                            rec[hoff + (k / 2) * 64 + g * 16 + j * 4 + t] |= (uint8_t)(((uv >> 4) & 1) << bit);
-                        } else if (hp == 2) {
-                            static const int sh[4] = {4, 6, 2, 0};
-                            rec[hoff + k * 64 + g * 16 + j * 4 + t] |= (uint8_t)(((uv >> 4) & 3) << sh[sub]);
-                        }
-                    }
+                uint8_t *rec = in_pair ? pair + (p * nc + c) * prec : tail + c * trec;
+                n4_place_chunk(rec, off, hp, lane, codes.data() + c * 64, sc);
             }
         }
     });

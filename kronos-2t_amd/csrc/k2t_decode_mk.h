@@ -15,6 +15,9 @@ struct MkParams {
     const MkLayer *layers;
     int L;
     MatDev head;
+    MatDev embed;        // NF4 / bit-plane embedding table (ekind 0 tied, 3 NF4)
+    const void *erows;   // f32 (ekind 1) or bf16 (ekind 2) embedding rows
+    int ekind;
     const float *final_norm;
     int d, nq, nkv, hd, inter, vocab, max_seq, kmax;
     float eps, attn_scale;

@@ -480,7 +480,17 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
     {
         const int token = P.tokens[0];
         for (int c = (int)blockIdx.x * kWaves + wave; c < d / 64; c += (int)gridDim.x * kWaves)
-            ll_store(P.HA + c * 64 + lane, __float_as_uint(embed_value(P.head, token, c, lane)), E(0));
+        {
+            float v;
+            if (P.ekind == K2T_EMBED_F32) {
+                v = ((const float *)P.erows)[(size_t)token * d + c * 64 + lane];
+            } else if (P.ekind == K2T_EMBED_BF16) {
+                v = __uint_as_float((uint32_t)((const uint16_t *)P.erows)[(size_t)token * d + c * 64 + lane] << 16);
+            } else {
+                v = embed_value(P.embed, token, c, lane);
+            }
+            ll_store(P.HA + c * 64 + lane, __float_as_uint(v), E(0));
+        }
     }
     // phases 1 .. 5L+1: a single GEMV body serves every matrix
     for (int ph = 1; ph < (int)nph; ph++) {

@@ -27,6 +27,7 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, const int8_t
 int attn_max_splits(int max_seq);
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums);
 void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok, float *out);
+void launch_embed_rows(hipStream_t st, const void *rows, bool bf16, const int *tokens, int ntok, int d, float *out);
 void launch_advance_pos(hipStream_t st, int *pos, int n);
 void launch_argmax(hipStream_t st, const float *x, int n, int *out_idx);
 void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum, int ntok,
@@ -105,6 +106,11 @@ struct k2t_model {
     std::vector<Layer> layers;
     const k2t_mat *head = nullptr;
     float *final_norm = nullptr;
+    // embedding source (embed_token_into's precedence, real_llm.rs:8063-8097)
+    int embed_kind = K2T_EMBED_TIED;
+    void *embed_rows = nullptr;          // f32 / bf16 rows [vocab][hidden] (device)
+    const k2t_mat *embed_mat = nullptr;  // NF4 embedding matrix
+    std::vector<k2t_mat *> owned;        // matrices the model destroys (k2tb loader)
     float *rope = nullptr;  // [max_seq][hd] = cos | sin halves
     int8_t *kq = nullptr, *vq = nullptr;
     float *ks = nullptr, *vs = nullptr;
@@ -192,7 +198,10 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
     const int hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, d = c.hidden, inter = c.intermediate;
     const float attn_scale = 1.0f / sqrtf((float)hd);
     const int nsplit = attn_max_splits(c.max_seq);
-    launch_embed(st, m->head, m->tokens, ntok, m->hidden);
+    if (m->embed_kind == K2T_EMBED_F32 || m->embed_kind == K2T_EMBED_BF16)
+        launch_embed_rows(st, m->embed_rows, m->embed_kind == K2T_EMBED_BF16, m->tokens, ntok, c.hidden, m->hidden);
+    else
+        launch_embed(st, m->embed_kind == K2T_EMBED_NF4 ? m->embed_mat : m->head, m->tokens, ntok, m->hidden);
     // One token: the RMSNorm / SwiGLU + FWHT + int8 activations are built inside the GEMVs
     // (each wave for its own chunks); batches use the standalone kernels.  Same codes.
     const bool fused = ntok == 1;
@@ -289,6 +298,9 @@ void forward_mk(k2t_model *m) {
     P.layers = m->mk_layers;
     P.L = c.n_layers;
     P.head = mat_dev(m->head, false);
+    P.embed = mat_dev(m->embed_kind == K2T_EMBED_NF4 ? m->embed_mat : m->head, false);
+    P.erows = m->embed_rows;
+    P.ekind = m->embed_kind;
     P.final_norm = m->final_norm;
     P.d = c.hidden;
     P.nq = c.n_heads;
@@ -368,6 +380,10 @@ void decode_step(k2t_model *m) {
 
 }  // namespace
 
+namespace k2t {
+void model_adopt(k2t_model *m, k2t_mat *mat) { m->owned.push_back(mat); }
+}  // namespace k2t
+
 extern "C" {
 
 int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_batch, k2t_model **out) {
@@ -443,6 +459,7 @@ void k2t_model_destroy(k2t_model *m) {
     if (m->stream) (void)hipStreamSynchronize(m->stream);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
     for (void *p : m->allocs) (void)hipFree(p);
+    for (k2t_mat *x : m->owned) k2t_mat_destroy(x);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
 }
@@ -489,13 +506,45 @@ int32_t k2t_model_set_head(k2t_model *m, const k2t_mat *lm_head, const float *fi
     return mguard([&] {
         arg(m && lm_head && final_norm, "NULL argument");
         arg(lm_head->rows == m->cfg.vocab && lm_head->cols == m->cfg.hidden, "lm_head shape mismatch");
-        arg(lm_head->fmt != K2T_FMT_NF || lm_head->bits == 4, "the tied lm_head must be NF4 or bit planes");
+        arg(m->embed_kind != K2T_EMBED_TIED || lm_head->fmt != K2T_FMT_NF || lm_head->bits == 4,
+            "a tied lm_head (the embedding table) must be NF4 or bit planes");
         arg(lm_head->ctx == m->ctx, "matrix of another context");
         hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
         if (!m->final_norm) m->final_norm = (float *)dalloc(m, m->cfg.hidden * sizeof(float));
         hip_check(hipMemcpy(m->final_norm, final_norm, m->cfg.hidden * sizeof(float), hipMemcpyHostToDevice),
                   "norm upload");
         m->head = lm_head;
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+    });
+}
+
+int32_t k2t_model_set_embedding(k2t_model *m, int32_t kind, const void *rows, const k2t_mat *nf4) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        const k2t_model_config &c = m->cfg;
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        if (kind == K2T_EMBED_TIED) {
+            arg(!m->head || m->head->fmt != K2T_FMT_NF || m->head->bits == 4,
+                "a tied lm_head (the embedding table) must be NF4 or bit planes");
+        } else if (kind == K2T_EMBED_F32 || kind == K2T_EMBED_BF16) {
+            arg(rows != nullptr, "embedding rows are NULL");
+            const size_t bytes = (size_t)c.vocab * c.hidden * (kind == K2T_EMBED_F32 ? 4 : 2);
+            void *d = dalloc(m, bytes);
+            hip_check(hipMemcpy(d, rows, bytes, hipMemcpyHostToDevice), "embedding upload");
+            m->embed_rows = d;
+        } else if (kind == K2T_EMBED_NF4) {
+            arg(nf4 != nullptr, "embedding matrix is NULL");
+            arg(nf4->ctx == m->ctx, "matrix of another context");
+            arg(nf4->fmt == K2T_FMT_NF && nf4->bits == 4, "the embedding matrix must be NF4");
+            arg(nf4->rows == c.vocab && nf4->cols == c.hidden, "embedding matrix shape mismatch");
+            m->embed_mat = nf4;
+        } else {
+            arg(false, "unknown embedding kind");
+        }
+        m->embed_kind = kind;
         if (m->graph) {
             (void)hipGraphExecDestroy(m->graph);
             m->graph = nullptr;

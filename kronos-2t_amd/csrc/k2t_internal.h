@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/k2t_hip.h"
+
 #include <stdexcept>
 #include <string>
 
@@ -71,6 +73,9 @@ enum { K2T_XS_GLOBAL = 0, K2T_XS_RMSNORM = 1, K2T_XS_SWIGLU = 2 };
 void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float *src, const float *w, float eps,
                        float *out, bool accumulate);
 uint64_t hadamard_sign_mask_host(uint64_t block);
+
+// The model takes ownership of `mat` (destroyed with the model).
+void model_adopt(k2t_model *m, k2t_mat *mat);
 
 void launch_act_quant(k2t_ctx *ctx, const float *x, const float *w, const float *inv_rms, int K,
                       int ntok, int8_t *q, float *scales, int32_t *sums);

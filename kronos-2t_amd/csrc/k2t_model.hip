@@ -372,6 +372,24 @@ void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok,
     hip_check(hipGetLastError(), "embed launch");
 }
 
+// Untied embedding rows (embed_token_into, real_llm.rs:8073-8085): f32 rows are copied,
+// bf16 rows widened; one thread per element.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const void *__restrict__ rows, int bf16,
+                                                         const int *__restrict__ tokens, int d,
+                                                         float *__restrict__ out) {
+    const int i = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+    if (i >= d) return;
+    const size_t src = (size_t)tokens[t] * d + i;
+    out[(size_t)t * d + i] = bf16 ? __uint_as_float((uint32_t)((const uint16_t *)rows)[src] << 16)
+                                  : ((const float *)rows)[src];
+}
+
+void launch_embed_rows(hipStream_t st, const void *rows, bool bf16, const int *tokens, int ntok, int d, float *out) {
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((d + 255) / 256, ntok), dim3(256), 0, st, rows, bf16 ? 1 : 0, tokens,
+                       d, out);
+    hip_check(hipGetLastError(), "embed_rows launch");
+}
+
 // Advances the device position counter after a step (keeps graph replays argument-free).
 __global__ void advance_pos_kernel(int *pos, int n) {
     if (threadIdx.x == 0) pos[0] += n;

@@ -81,7 +81,16 @@ SIGNATURES = {
     "k2t_model_generate": (I32, [VP, I32, I32, VP]),
     "k2t_model_logits": (I32, [VP, C.POINTER(VP)]),
     "k2t_model_sync": (I32, [VP]),
+    "k2t_model_set_embedding": (I32, [VP, I32, VP, VP]),
+    "k2t_k2tb_open": (I32, [C.c_char_p, C.POINTER(VP)]),
+    "k2t_k2tb_close": (None, [VP]),
+    "k2t_k2tb_header": (I32, [VP, C.POINTER(I32), C.POINTER(I32), VP]),
+    "k2t_k2tb_matrix": (I32, [VP, I32, I32, I32, VP, VP, SZ, VP, SZ]),
+    "k2t_k2tb_vector": (I32, [VP, I32, I32, C.POINTER(SZ), VP, SZ]),
+    "k2t_model_load_k2tb": (I32, [VP, VP, C.c_char_p, I32, C.POINTER(VP)]),
 }
+
+EMBED_TIED, EMBED_F32, EMBED_BF16, EMBED_NF4 = 0, 1, 2, 3
 
 
 class ModelConfig(C.Structure):
@@ -89,6 +98,12 @@ class ModelConfig(C.Structure):
     _fields_ = [("n_layers", I32), ("hidden", I32), ("n_heads", I32), ("n_kv_heads", I32), ("head_dim", I32),
                 ("intermediate", I32), ("vocab", I32), ("max_seq", I32), ("rms_eps", C.c_float),
                 ("rope_theta", C.c_float)]
+
+
+class K2tbMatrixInfo(C.Structure):
+    """k2t_k2tb_matrix_info."""
+    _fields_ = [("tag", I32), ("fmt", I32), ("rows", I32), ("cols", I32), ("planes_or_bits", I32), ("sgc", I32),
+                ("codebook", C.c_int8 * 16), ("pair_len", SZ), ("tail_len", SZ)]
 
 
 def lib():
@@ -302,6 +317,34 @@ class Model:
         check(lib().k2t_model_set_head(self.h, head.h, fn.ctypes.data_as(VP)))
         self._keep.append(head)
 
+    def set_embedding(self, kind, rows=None, nf4=None):
+        """k2t_model_set_embedding: EMBED_TIED, EMBED_F32 / EMBED_BF16 (host rows
+        [vocab][hidden], float32 / uint16) or EMBED_NF4 (a Mat of the same context)."""
+        import numpy as np
+        r = None
+        if kind == EMBED_F32:
+            r = np.ascontiguousarray(rows, np.float32)
+        elif kind == EMBED_BF16:
+            r = np.ascontiguousarray(rows, np.uint16)
+        check(lib().k2t_model_set_embedding(self.h, int(kind), None if r is None else r.ctypes.data_as(VP),
+                                            None if nf4 is None else nf4.h))
+        if nf4 is not None:
+            self._keep.append(nf4)
+
+    @classmethod
+    def load_k2tb(cls, ctx, cfg: dict, path, max_batch=4):
+        """k2t_model_load_k2tb: a compiled .k2tb model (load_bipolar + repack_sdot)
+        for the config `cfg` (see load_llama_config), uploaded to the context's device."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        self.cfg = dict(cfg)
+        c = ModelConfig(**{k: cfg[k] for k, _ in ModelConfig._fields_})
+        h = VP()
+        check(lib().k2t_model_load_k2tb(ctx.h, C.byref(c), os.fsencode(path), max_batch, C.byref(h)))
+        self.h = h
+        self._keep = []
+        return self
+
     def set_graph(self, on):
         check(lib().k2t_model_set_graph(self.h, int(bool(on))))
 
@@ -358,6 +401,98 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------------------- .k2tb files
+class K2tb:
+    """A memory-mapped .k2tb file (k2t_k2tb_*): header, vectors and matrices repacked
+    into the GEMV layouts on the host.  Needs no GPU."""
+
+    def __init__(self, path):
+        h = VP()
+        check(lib().k2t_k2tb_open(os.fsencode(path), C.byref(h)))
+        self.h = h
+
+    def header(self):
+        import numpy as np
+        v, n = I32(), I32()
+        mw = np.zeros(6, np.uint64)
+        check(lib().k2t_k2tb_header(self.h, C.byref(v), C.byref(n), mw.ctypes.data_as(VP)))
+        return v.value, n.value, [int(x) for x in mw]
+
+    def matrix(self, layer, which, interleave_gate_up=False):
+        """(info, pair bytes, tail bytes); layer -1 with which 4 = lm_head, 5 = NF4 embedding."""
+        import numpy as np
+        info = K2tbMatrixInfo()
+        check(lib().k2t_k2tb_matrix(self.h, layer, which, int(interleave_gate_up), C.byref(info), None, 0, None, 0))
+        pair = np.empty(info.pair_len, np.uint8)
+        tail = np.empty(max(info.tail_len, 1), np.uint8)
+        check(lib().k2t_k2tb_matrix(self.h, layer, which, int(interleave_gate_up), C.byref(info),
+                                    pair.ctypes.data_as(VP), pair.size, tail.ctypes.data_as(VP), tail.size))
+        return info, pair, tail[:info.tail_len]
+
+    def vector(self, layer, which):
+        import numpy as np
+        n = SZ()
+        check(lib().k2t_k2tb_vector(self.h, layer, which, C.byref(n), None, 0))
+        dt = np.uint16 if (layer < 0 and which == 2) else np.float32
+        out = np.empty(max(n.value, 1), dt)
+        check(lib().k2t_k2tb_vector(self.h, layer, which, C.byref(n), out.ctypes.data_as(VP), out.size))
+        return out[:n.value]
+
+    def close(self):
+        if self.h and not _shutting_down:
+            lib().k2t_k2tb_close(self.h)
+        self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def load_llama_config(model_dir, max_seq):
+    """The k2t_model_config fields of LlamaConfig::from_config_json (real_llm.rs:125-410)
+    read from `model_dir`/config.json, with the reference's defaults for missing keys.
+    rope_theta is the effective base (NTK-alpha stretch, real_llm.rs:415-422).  Raises
+    ValueError for shapes this path does not run (MoE, per-layer sliding masks)."""
+    import json
+    with open(os.path.join(model_dir, "config.json")) as f:
+        j = json.load(f)
+
+    def opt_pos(k):  # parse_opt_usize: null or 0 -> None
+        v = j.get(k)
+        return int(v) if v else None
+
+    hidden = int(j.get("hidden_size", 576))
+    n_heads = int(j.get("num_attention_heads", 9))
+    head_dim = opt_pos("head_dim") or hidden // n_heads
+    theta = float(j.get("rope_theta", 100000.0))
+    rs = j.get("rope_scaling")
+    if isinstance(rs, dict):
+        alpha = float(rs.get("alpha", 0.0) or 0.0)
+        kind = rs.get("type", rs.get("rope_type"))
+        if kind == "dynamic" and alpha > 1.0:
+            d = float(head_dim)
+            # effective_rope_theta: f32 theta widened, alpha stored as f32
+            a32 = float(C.c_float(alpha).value)
+            theta = float(C.c_float(theta).value) * a32 ** (d / (d - 2.0))
+    n_experts = opt_pos("num_experts") or opt_pos("num_local_experts") or 0
+    if n_experts > 1:
+        raise ValueError("sparse-MoE configs are not supported by this loader")
+    inter = int(j.get("intermediate_size", 1536))
+    return dict(n_layers=int(j.get("num_hidden_layers", 30)), hidden=hidden, n_heads=n_heads,
+                n_kv_heads=int(j.get("num_key_value_heads", 3)), head_dim=head_dim, intermediate=inter,
+                vocab=int(j.get("vocab_size", 49152)), max_seq=int(max_seq),
+                rms_eps=float(j.get("rms_norm_eps", 1e-5)), rope_theta=theta,
+                tie_word_embeddings=bool(j.get("tie_word_embeddings", True)))
 
 
 # ---------------------------------------------------------------------------- synthetic models

@@ -12,7 +12,8 @@ product).  Per layer, in the reference's order:
      (7207-7296);
   5. down GEMV, hidden += (7308-7333);
 then final norm -> lm_head GEMV (7338-7391).  The embedding is the tied quantized
-head's row, dequantized and inverse-rotated (embed_token_into, 8063-8097).
+head's row, dequantized and inverse-rotated (embed_token_into, 8063-8097), unless an
+untied embedding function is given (f32 / bf16 rows, NF4 matrix: 8073-8090).
 """
 import numpy as np
 
@@ -84,8 +85,9 @@ class OracleModel:
     """`gemv_threads` > 0 switches every projection to the threaded portable path (the
     timed CPU baseline); 0 keeps the NEON-semantics integer path (the parity oracle)."""
 
-    def __init__(self, cfg, layers, head, final_norm, gemv_threads=0):
+    def __init__(self, cfg, layers, head, final_norm, gemv_threads=0, embed=None):
         self.gemv_threads = gemv_threads
+        self.embed_fn = embed  # untied embedding: token -> f32[hidden] (embed_token_into)
         self.cfg = cfg
         self.layers = layers  # dicts: qkv, o, gu, down (Matrix), in_norm, post_norm, bias
         self.head = head
@@ -103,6 +105,8 @@ class OracleModel:
         return m.gemv(xq, xs, xsum)
 
     def embed(self, token):
+        if self.embed_fn is not None:
+            return self.embed_fn(token)
         return O.ifwht64(self.head.row_rotated(token))
 
     def forward_token(self, token):
