@@ -49,6 +49,7 @@ extern "C" {
 
 typedef struct k2t_ctx k2t_ctx;
 typedef struct k2t_mat k2t_mat;
+typedef struct k2t_experts k2t_experts; /* sparse-MoE expert bank (.k2tm shard in HBM) */
 
 /* Library version string ("k2t-hip <semver> gfx950"). */
 const char *k2t_version(void);
@@ -190,8 +191,11 @@ int32_t k2t_synth_normal(uint64_t seed, float stddev, float *out, size_t n, int3
 
 /* ---- decode engine ------------------------------------------------------ */
 
-/* Llama-family decoder shape (LlamaConfig, real_llm.rs:100-403).  q_dim must equal
- * hidden (the megakernel shape, real_llm.rs:6412-6452); head_dim 64 or 128. */
+/* Llama-family decoder shape (LlamaConfig, real_llm.rs:100-403); head_dim 64 or 128.
+ * q_dim = n_heads * head_dim may differ from hidden (the generic decode path,
+ * real_llm.rs:6485-6792); the persistent decode kernel needs q_dim == hidden (the
+ * megakernel shape, real_llm.rs:6412-6452).  For MoE models `intermediate` is the dense
+ * size (any positive multiple of 64 when every layer is MoE). */
 typedef struct k2t_model_config {
     int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate, vocab, max_seq;
     float rms_eps;
@@ -225,6 +229,21 @@ int32_t k2t_model_set_head(k2t_model *m, const k2t_mat *lm_head, const float *fi
 #define K2T_EMBED_BF16 2
 #define K2T_EMBED_NF4 3
 int32_t k2t_model_set_embedding(k2t_model *m, int32_t kind, const void *rows, const k2t_mat *nf4);
+/* Per-head q / k RMSNorm weights [head_dim] (Qwen3 q_norm / k_norm; apply_qk_norm_rope,
+ * real_llm.rs:8139-8178, applied before RoPE); NULL clears. */
+int32_t k2t_model_set_qk_norm(k2t_model *m, int32_t layer, const float *q_norm, const float *k_norm);
+/* Makes `layer` a sparse-MoE layer (set its attention first with k2t_model_set_layer and
+ * gate_up = down = NULL): layer `shard_layer` of the expert bank (borrowed), an fp32
+ * router [E][hidden] (+ bias [E] or NULL; host arrays, copied), top_k experts per
+ * token, norm_topk_prob and scoring as in route_sorted (sparse_moe.rs:86-182).  The
+ * feed-forward is forward_layer_single (sparse_moe.rs:961-1084) per token. */
+int32_t k2t_model_set_moe(k2t_model *m, int32_t layer, const k2t_experts *bank, int32_t shard_layer,
+                          const float *router_w, const float *router_bias, int32_t top_k, int32_t norm_topk_prob,
+                          int32_t scoring);
+/* Benchmark support (no reference counterpart): fills cache positions [0, n_pos) of every
+ * layer with seeded pseudo-random int8 K/V and positive scales and sets the position to
+ * n_pos, so a decode step runs at that context without a prefill. */
+int32_t k2t_model_kv_synthetic(k2t_model *m, int32_t n_pos, uint64_t seed);
 /* 1 (default): capture the decode step once and replay it as a HIP graph. */
 int32_t k2t_model_set_graph(k2t_model *m, int32_t enable);
 /* GEMV epilogue of this model's steps (see k2t_ctx_set_exact); default 0 = fast.
@@ -254,6 +273,49 @@ int32_t k2t_model_generate(k2t_model *m, int32_t first_token, int32_t n_steps, i
 /* Device pointer of the last logits (valid after a step; read after k2t_model_sync). */
 int32_t k2t_model_logits(k2t_model *m, const float **d_logits);
 int32_t k2t_model_sync(k2t_model *m);
+
+/* ---- sparse-MoE experts (.k2tm shards) ------------------------------------- */
+
+/* K2tmShardHeader (moe_800b.rs:792-854): page 0 of a .k2tm shard ("K2TM800B_V1\0", then
+ * seven u64 words at byte 16).  Records follow at 16384 + (layer*E + e)*aligned bytes. */
+typedef struct k2t_k2tm_header {
+    int64_t num_layers, experts_per_layer, d_model, d_ff_expert, scale_group_chunks, aligned_expert_bytes, bits;
+} k2t_k2tm_header;
+/* nf_expert_byte_layout (moe_800b.rs:1332-1375): offsets inside one expert record. */
+typedef struct k2t_k2tm_layout {
+    int64_t gu_codebook_off, dn_codebook_off, gu_pair_off, gu_pair_bytes, dn_pair_off, dn_pair_bytes,
+        aligned_expert_bytes;
+} k2t_k2tm_layout;
+
+/* Router scoring (MoeRouterScoring, sparse_moe.rs:86-182). */
+#define K2T_MOE_SOFTMAX 0      /* softmax over all experts, top-k, optional renormalization */
+#define K2T_MOE_TOPK_SOFTMAX 1 /* top-k logits, softmax over them (gpt-oss) */
+#define K2T_MOE_SIGMOID 2      /* sigmoid scores, top-k, optional renormalization */
+#define K2T_MOE_MAX_TOPK 16
+
+/* Decodes and validates a header page (len >= 16384); experts must be NF3 or NF4 and
+ * aligned_expert_bytes must equal the layout of the declared shape. */
+int32_t k2t_k2tm_read_header(const uint8_t *page, size_t len, k2t_k2tm_header *out);
+int32_t k2t_k2tm_expert_layout(int64_t d_model, int64_t d_ff, int32_t bits, int32_t sgc, k2t_k2tm_layout *out);
+/* A whole shard (header page + every record) copied into HBM (MoeExpertBackend::ZeroCopyMmap,
+ * sparse_moe.rs:1025-1045, with HBM in place of the mapping: no paging). */
+int32_t k2t_experts_upload(k2t_ctx *ctx, const uint8_t *k2tm, size_t len, k2t_experts **out);
+/* A shard already in device memory (borrowed; 256-byte aligned), described by its host
+ * header page. */
+int32_t k2t_experts_wrap(k2t_ctx *ctx, const uint8_t *d_k2tm, size_t len, const uint8_t *header_page,
+                         k2t_experts **out);
+void k2t_experts_destroy(k2t_experts *b);
+int32_t k2t_experts_info(const k2t_experts *b, k2t_k2tm_header *out);
+/* One token through one MoE layer (forward_layer_single, sparse_moe.rs:961-1084, plus the
+ * residual add of real_llm.rs:6711-6714):
+ *   x_norm = RMSNorm(hidden) * post_norm; routes = route_sorted(router, x_norm);
+ *   hidden += sum over routes of w * down(SwiGLU(gate_up(x_norm)))
+ * router_w: device f32 [E][d_model] (bias [E] or NULL).  route ids / weights (device,
+ * top_k each, nullable) receive the routing.  Uses the context's scratch. */
+int32_t k2t_moe_ffn(k2t_ctx *ctx, const k2t_experts *bank, int32_t shard_layer, const float *d_router_w,
+                    const float *d_router_bias, int32_t top_k, int32_t norm_topk_prob, int32_t scoring,
+                    float *d_hidden, const float *d_post_norm, float eps, int32_t *d_route_ids,
+                    float *d_route_weights);
 
 /* ---- .k2tb compiled models ------------------------------------------------ */
 

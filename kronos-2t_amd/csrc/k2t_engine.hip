@@ -15,11 +15,13 @@
 #include "../../include/k2t_hip.h"
 #include "k2t_decode_mk.h"
 #include "k2t_internal.h"
+#include "k2t_moe.h"
 
 namespace k2t {
 void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float eps, int K, int ntok, int8_t *q,
                         float *s, int32_t *sums);
-void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *rope, const int *pos_dev, int nq,
+void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
+                     const float *rope, const int *pos_dev, int nq,
                      int nkv, int hd, int ntok, int layer, int cap, int8_t *kq, int8_t *vq, float *ks, float *vs);
 void launch_attention(hipStream_t st, const float *q, int q_stride, const int8_t *kq, const int8_t *vq, const float *ks,
                       const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd, int cap, float attn_scale,
@@ -27,6 +29,8 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, const int8_t
 int attn_max_splits(int max_seq);
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums);
 void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok, float *out);
+void launch_kv_synthetic(hipStream_t st, int8_t *kq, int8_t *vq, float *ks, float *vs, int layers_kv, int cap,
+                         int n_pos, int hd, uint64_t seed);
 void launch_embed_rows(hipStream_t st, const void *rows, bool bf16, const int *tokens, int ntok, int d, float *out);
 void launch_advance_pos(hipStream_t st, int *pos, int n);
 void launch_argmax(hipStream_t st, const float *x, int n, int *out_idx);
@@ -102,6 +106,9 @@ struct k2t_model {
     struct Layer {
         const k2t_mat *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
         float *in_norm = nullptr, *post_norm = nullptr, *bias = nullptr;
+        float *q_norm = nullptr, *k_norm = nullptr;  // per-head RMSNorm weights [hd] (Qwen3)
+        bool has_moe = false;
+        MoeLayer moe{};  // sparse-MoE feed-forward in place of gate_up / down
     };
     std::vector<Layer> layers;
     const k2t_mat *head = nullptr;
@@ -111,6 +118,8 @@ struct k2t_model {
     void *embed_rows = nullptr;          // f32 / bf16 rows [vocab][hidden] (device)
     const k2t_mat *embed_mat = nullptr;  // NF4 embedding matrix
     std::vector<k2t_mat *> owned;        // matrices the model destroys (k2tb loader)
+    float *moe_ws = nullptr;             // MoE workspace (largest layer's need)
+    size_t moe_ws_floats = 0;
     float *rope = nullptr;  // [max_seq][hd] = cos | sin halves
     int8_t *kq = nullptr, *vq = nullptr;
     float *ks = nullptr, *vs = nullptr;
@@ -213,12 +222,16 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
             launch_rmsnorm_act(st, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
             launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false);
         }
-        launch_qkv_post(st, m->qkv, L.bias, m->rope, m->pos_dev, nq, nkv, hd, ntok, l, c.max_seq, m->kq, m->vq, m->ks,
-                        m->vs);
+        launch_qkv_post(st, m->qkv, L.bias, L.q_norm, L.k_norm, c.rms_eps, m->rope, m->pos_dev, nq, nkv, hd, ntok, l,
+                        c.max_seq, m->kq, m->vq, m->ks, m->vs);
         launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, m->pos_dev, l, nq, nkv, hd,
                          c.max_seq, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum);
         launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
-        if (fused) {
+        if (L.has_moe) {
+            // one token at a time: each token has its own routes (forward_layer_single)
+            const MoeWork ws = moe_work_carve(m->moe_ws, L.moe.bank, L.moe.top_k);
+            for (int t = 0; t < ntok; t++) launch_moe_ffn(ctx, L.moe, m->hidden + (size_t)t * d, L.post_norm, c.rms_eps, ws);
+        } else if (fused) {
             launch_gemv_fused(ctx, L.gu, K2T_XS_RMSNORM, m->hidden, L.post_norm, c.rms_eps, m->gu, false);
             launch_gemv_fused(ctx, L.down, K2T_XS_SWIGLU, m->gu, nullptr, 0.0f, m->hidden, true);
         } else {
@@ -237,7 +250,8 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
 
 void check_ready(k2t_model *m) {
     for (size_t l = 0; l < m->layers.size(); l++)
-        arg(m->layers[l].qkv && m->layers[l].o && m->layers[l].gu && m->layers[l].down, "a layer is not set");
+        arg(m->layers[l].qkv && m->layers[l].o && ((m->layers[l].gu && m->layers[l].down) || m->layers[l].has_moe),
+            "a layer is not set");
     arg(m->head != nullptr, "lm_head is not set");
 }
 
@@ -272,6 +286,8 @@ bool mk_format(const k2t_model *m, int &fmt, int &hp) {
 
 bool use_persistent(const k2t_model *m) {
     int fmt, hp;
+    for (const auto &L : m->layers)
+        if (L.has_moe || L.q_norm || L.k_norm) return false;  // these run on the per-operation path
     return m->persistent && m->mk_ok && !m->exact && mk_format(m, fmt, hp);
 }
 
@@ -395,7 +411,7 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             "non-positive model dimension");
         arg(c.head_dim == 64 || c.head_dim == 128, "head_dim must be 64 or 128 (Hadamard KV cache)");
         arg(c.n_heads % c.n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
-        arg(c.n_heads * c.head_dim == c.hidden, "q_dim must equal hidden (megakernel shape)");
+        arg(c.n_heads * c.head_dim <= 32768, "q_dim too large");
         arg(c.hidden % 64 == 0 && c.intermediate % 64 == 0, "hidden and intermediate must be multiples of 64");
         arg(c.max_seq > 0 && c.max_seq <= 1 << 20, "max_seq out of range");
         arg(max_batch >= 1 && max_batch <= 4096, "max_batch out of range");
@@ -419,7 +435,7 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             m->tokens = m->pos_dev + 1;
             hip_check(hipMemset(m->pos_dev, 0, (size_t)(max_batch + 1) * sizeof(int)), "pos clear");
             const size_t qkv_w = (size_t)(c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
-            const size_t kmax = std::max(c.hidden, c.intermediate);
+            const size_t kmax = std::max({c.hidden, c.intermediate, c.n_heads * c.head_dim});
             m->hidden = (float *)dalloc(m, (size_t)max_batch * c.hidden * sizeof(float));
             m->qkv = (float *)dalloc(m, (size_t)max_batch * qkv_w * sizeof(float));
             m->gu = (float *)dalloc(m, (size_t)max_batch * 2 * c.intermediate * sizeof(float));
@@ -430,7 +446,8 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             m->xs = (float *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(float));
             m->xsum = (int32_t *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(int32_t));
             // persistent decode kernel state
-            m->mk_ok = decode_mk_supported(c, ctx->num_cus);
+            // the persistent kernel's phases assume the megakernel shape q_dim == hidden
+            m->mk_ok = decode_mk_supported(c, ctx->num_cus) && c.n_heads * c.head_dim == c.hidden;
             m->mk_lds = decode_mk_lds_bytes(c);
             m->step_dev = (uint32_t *)dalloc(m, 16);
             m->err_dev = (int *)m->step_dev + 1;
@@ -470,14 +487,18 @@ int32_t k2t_model_set_layer(k2t_model *m, int32_t layer, const k2t_mat *qkv, con
     return mguard([&] {
         arg(m != nullptr, "model is NULL");
         arg(layer >= 0 && layer < m->cfg.n_layers, "layer out of range");
-        arg(qkv && o && gate_up && down && in_norm && post_norm, "NULL argument");
+        arg(qkv && o && in_norm && post_norm, "NULL argument");
+        arg((gate_up == nullptr) == (down == nullptr), "gate_up and down must both be set, or both NULL (MoE layer)");
         const k2t_model_config &c = m->cfg;
         const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
         arg(qkv->rows == qkv_rows && qkv->cols == c.hidden, "qkv shape mismatch");
         arg(o->rows == c.hidden && o->cols == c.n_heads * c.head_dim, "o_proj shape mismatch");
-        arg(gate_up->rows == 2 * c.intermediate && gate_up->cols == c.hidden, "gate_up shape mismatch");
-        arg(down->rows == c.hidden && down->cols == c.intermediate, "down_proj shape mismatch");
-        for (const k2t_mat *x : {qkv, o, gate_up, down}) arg(x->ctx == m->ctx, "matrix of another context");
+        if (gate_up) {
+            arg(gate_up->rows == 2 * c.intermediate && gate_up->cols == c.hidden, "gate_up shape mismatch");
+            arg(down->rows == c.hidden && down->cols == c.intermediate, "down_proj shape mismatch");
+            arg(gate_up->ctx == m->ctx && down->ctx == m->ctx, "matrix of another context");
+        }
+        for (const k2t_mat *x : {qkv, o}) arg(x->ctx == m->ctx, "matrix of another context");
         auto &L = m->layers[layer];
         hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
         if (!L.in_norm) L.in_norm = (float *)dalloc(m, c.hidden * sizeof(float));
@@ -495,6 +516,7 @@ int32_t k2t_model_set_layer(k2t_model *m, int32_t layer, const k2t_mat *qkv, con
         L.o = o;
         L.gu = gate_up;
         L.down = down;
+        if (gate_up) L.has_moe = false;
         if (m->graph) {
             (void)hipGraphExecDestroy(m->graph);
             m->graph = nullptr;
@@ -514,6 +536,65 @@ int32_t k2t_model_set_head(k2t_model *m, const k2t_mat *lm_head, const float *fi
         hip_check(hipMemcpy(m->final_norm, final_norm, m->cfg.hidden * sizeof(float), hipMemcpyHostToDevice),
                   "norm upload");
         m->head = lm_head;
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+    });
+}
+
+int32_t k2t_model_set_qk_norm(k2t_model *m, int32_t layer, const float *q_norm, const float *k_norm) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        arg(layer >= 0 && layer < m->cfg.n_layers, "layer out of range");
+        auto &L = m->layers[layer];
+        const size_t hd = (size_t)m->cfg.head_dim;
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        auto put = [&](float *&dst, const float *src) {
+            if (!src) {
+                dst = nullptr;
+                return;
+            }
+            if (!dst) dst = (float *)dalloc(m, hd * sizeof(float));
+            hip_check(hipMemcpy(dst, src, hd * sizeof(float), hipMemcpyHostToDevice), "qk norm upload");
+        };
+        put(L.q_norm, q_norm);
+        put(L.k_norm, k_norm);
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+    });
+}
+
+int32_t k2t_model_set_moe(k2t_model *m, int32_t layer, const k2t_experts *bank, int32_t shard_layer,
+                          const float *router_w, const float *router_bias, int32_t top_k, int32_t norm_topk_prob,
+                          int32_t scoring) {
+    return mguard([&] {
+        arg(m && router_w, "NULL argument");
+        arg(layer >= 0 && layer < m->cfg.n_layers, "layer out of range");
+        check_moe_args(bank, shard_layer, top_k, scoring);
+        arg(bank->ctx == m->ctx, "expert bank of another context");
+        arg(bank->hdr.d_model == m->cfg.hidden, "expert d_model does not match the model's hidden size");
+        auto &L = m->layers[layer];
+        arg(L.qkv != nullptr, "set the layer's attention first (k2t_model_set_layer with NULL gate_up / down)");
+        arg(L.gu == nullptr, "the layer has a dense feed-forward");
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        const size_t E = (size_t)bank->hdr.experts_per_layer, d = (size_t)m->cfg.hidden;
+        float *rw = (float *)dalloc(m, E * d * sizeof(float));
+        hip_check(hipMemcpy(rw, router_w, E * d * sizeof(float), hipMemcpyHostToDevice), "router upload");
+        float *rb = nullptr;
+        if (router_bias) {
+            rb = (float *)dalloc(m, E * sizeof(float));
+            hip_check(hipMemcpy(rb, router_bias, E * sizeof(float), hipMemcpyHostToDevice), "router upload");
+        }
+        const size_t need = moe_work_floats(bank, top_k);
+        if (need > m->moe_ws_floats) {
+            m->moe_ws = (float *)dalloc(m, need * sizeof(float));
+            m->moe_ws_floats = need;
+        }
+        L.moe = MoeLayer{bank, shard_layer, rw, rb, top_k, norm_topk_prob ? 1 : 0, scoring};
+        L.has_moe = true;
         if (m->graph) {
             (void)hipGraphExecDestroy(m->graph);
             m->graph = nullptr;
@@ -567,6 +648,21 @@ int32_t k2t_model_set_exact(k2t_model *m, int32_t exact) {
             (void)hipGraphExecDestroy(m->graph);
             m->graph = nullptr;
         }
+    });
+}
+
+int32_t k2t_model_kv_synthetic(k2t_model *m, int32_t n_pos, uint64_t seed) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        arg(n_pos >= 0 && n_pos < m->cfg.max_seq, "n_pos must be in [0, max_seq)");
+        const k2t_model_config &c = m->cfg;
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        hip_check(hipStreamSynchronize(m->stream), "sync");
+        launch_kv_synthetic(m->stream, m->kq, m->vq, m->ks, m->vs, c.n_layers * c.n_kv_heads, c.max_seq, n_pos,
+                            c.head_dim, seed);
+        hip_check(hipMemcpyAsync(m->pos_dev, &n_pos, sizeof(int), hipMemcpyHostToDevice, m->stream), "pos set");
+        hip_check(hipStreamSynchronize(m->stream), "sync");
+        m->pos = n_pos;
     });
 }
 

@@ -58,7 +58,26 @@ struct GemvParams {
     const uint64_t *signs;
     float eps;
     int xoff;
+    // Grouped mode (sparse-MoE experts): workgroup slot z = blockIdx.z streams the matrix of
+    // expert route[z] inside the .k2tm bank: record = bank + route[z] * bank_stride, matrix
+    // pairs at record + mat_off, 16-byte codebook at record + cb_off.  Output and fp32
+    // activation source advance by slot_out / slot_src floats per slot.  gu_split = 1
+    // writes rows [0, rows/2) (gate) and [rows/2, rows) (up) in [gate64, up64] blocks.
+    const int *route;
+    const uint8_t *bank;
+    size_t bank_stride;
+    uint32_t mat_off, cb_off;
+    size_t slot_out, slot_src;
+    int gu_split;
 };
+
+// Output index of row r: the [gate64(ic), up64(ic)] interleave of a split gate/up matrix.
+__device__ __forceinline__ int gu_out_row(int r, int rows, int split) {
+    if (!split) return r;
+    const int inter = rows >> 1;
+    const int u = r >= inter ? 1 : 0, rr = r - u * inter;
+    return (rr >> 6) * 128 + u * 64 + (rr & 63);
+}
 
 // Builds the int8 activation chunks [c0, c1) of one token in LDS (xl[c*64 + e],
 // xsl[c], xsuml[c]) from an fp32 source:
@@ -124,8 +143,8 @@ struct XBuilder {
     XSlice first;
     float4 sq[XS == 1 ? kSqPre : 1];
 
-    __device__ XBuilder(const GemvParams &P_, int tok, int c0_, int c1_, uint32_t lane_)
-        : P(P_), src(P_.xsrc + (size_t)tok * (XS == 2 ? 2 * P_.K : P_.K)), c0(c0_), c1(c1_), lane(lane_),
+    __device__ XBuilder(const GemvParams &P_, const float *xsrc, int tok, int c0_, int c1_, uint32_t lane_)
+        : P(P_), src(xsrc + (size_t)tok * (XS == 2 ? 2 * P_.K : P_.K)), c0(c0_), c1(c1_), lane(lane_),
           slot(lane_ >> 3), s(lane_ & 7u) {}
 
     __device__ void begin() {
@@ -253,7 +272,25 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         sc_off = is_tail ? 0u : side * 32u;
     }
     sc_off += (4u * g + 2u * half) * 2u;
-    const uint8_t *mbase = is_tail ? P.tail : P.pair + (size_t)pidx * (FMT == 0 ? (size_t)P.nc * PREC : P.ptot);
+    // Matrix, codebook, output and activation source of this workgroup (grouped mode: of
+    // the expert routed to slot blockIdx.z; expert matrices have no tail stripe).
+    const uint8_t *pair_p = P.pair;
+    uint32_t cb0 = P.cb0, cb1 = P.cb1, cb2 = P.cb2, cb3 = P.cb3;
+    float *out_p = P.out;
+    const float *xsrc_p = P.xsrc;
+    if (P.route) {
+        const int z = (int)blockIdx.z;
+        const uint8_t *rec = P.bank + (size_t)P.route[z] * P.bank_stride;
+        pair_p = rec + P.mat_off;
+        const uint4 cbw = *reinterpret_cast<const uint4 *>(rec + P.cb_off);
+        cb0 = cbw.x;
+        cb1 = cbw.y;
+        cb2 = cbw.z;
+        cb3 = cbw.w;
+        out_p += (size_t)z * P.slot_out;
+        xsrc_p += (size_t)z * P.slot_src;
+    }
+    const uint8_t *mbase = is_tail ? P.tail : pair_p + (size_t)pidx * (FMT == 0 ? (size_t)P.nc * PREC : P.ptot);
 
     auto fetch = [&](Frag<HP, NT> &fr, int c) {
         const uint8_t *rec, *scp;
@@ -346,7 +383,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
                     int a = acc[t][j];
 #pragma unroll
                     for (int u = 0; u < 8; u++)
-                        a = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(P.cb1, P.cb0, id[u]), (int)xw[u], a,
+                        a = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(cb1, cb0, id[u]), (int)xw[u], a,
                                                    false);
                     acc[t][j] = a;
                 }
@@ -378,8 +415,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
                         hi |= __builtin_rotateright32(hd[j], (e + 1u) & 31u) & 0x10101010u;
                     }
                 } else {
-                    lo = lut16(d & 0x07070707u, bit3_mask(d), P.cb0, P.cb1, P.cb2, P.cb3);
-                    hi = lut16((d >> 4) & 0x07070707u, bit7_mask(d), P.cb0, P.cb1, P.cb2, P.cb3);
+                    lo = lut16(d & 0x07070707u, bit3_mask(d), cb0, cb1, cb2, cb3);
+                    hi = lut16((d >> 4) & 0x07070707u, bit7_mask(d), cb0, cb1, cb2, cb3);
                 }
 #pragma unroll
                 for (int t = 0; t < NT; t++)
@@ -435,7 +472,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         if constexpr (XS != 0) {
             // Source loads first, then the first weight loads; the wave builds its
             // activation while the weights are in flight.
-            XBuilder<XS> xb(P, tok0, cw0, cw1, lane);
+            XBuilder<XS> xb(P, xsrc_p, tok0, cw0, cw1, lane);
             xb.begin();
             if (valid(0)) fetch(fa, chunk_of(0));
             if (valid(1)) fetch(fb, chunk_of(1));
@@ -493,7 +530,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             if (row >= P.rows || st < P.s0 || st >= P.s1) continue;
             float acc = part[(size_t)t * RB + rl];
             for (int w = 1; w < P.nseg; w++) acc += part[((size_t)w * NT + t) * RB + rl];
-            float *o = P.out + (size_t)(tok0 + t) * P.out_stride + row;
+            float *o = out_p + (size_t)(tok0 + t) * P.out_stride + gu_out_row(row, P.rows, P.gu_split);
             *o = P.accum ? *o + acc : acc;
         }
         return;
@@ -523,7 +560,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             const float2 v = tp[(size_t)c * RB];
             acc = fmaf(v.x, v.y, acc);
         }
-        float *o = P.out + (size_t)(tok0 + t) * P.out_stride + row;
+        float *o = out_p + (size_t)(tok0 + t) * P.out_stride + gu_out_row(row, P.rows, P.gu_split);
         *o = P.accum ? *o + acc : acc;
     }
 }
@@ -598,7 +635,7 @@ static void launch_fmt(const k2t_mat *m, int nt, int xs, dim3 grid, dim3 block, 
 static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                              const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
                              int32_t *dots, bool accum, int xsm = 0, const float *src = nullptr,
-                             const float *w = nullptr, float eps = 0.0f);
+                             const float *w = nullptr, float eps = 0.0f, const GemvGroup *grp = nullptr);
 
 void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                  const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
@@ -617,9 +654,18 @@ void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float 
                      xs_mode, src, w, eps);
 }
 
+void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, int xs_mode, const float *src,
+                         const float *w, float eps, float *out) {
+    if (g.nslots <= 0) return;
+    if (geom->has_tail) throw Error(K2T_E_INTERNAL, "grouped gemv: expert matrices have no tail stripe");
+    launch_gemv_impl(ctx, geom, nullptr, nullptr, nullptr, 1, 0, geom->stripes, out, (size_t)geom->rows, nullptr,
+                     false, xs_mode, src, w, eps, &g);
+}
+
 static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                              const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
-                             int32_t *dots, bool accum, int xsm, const float *src, const float *w, float eps) {
+                             int32_t *dots, bool accum, int xsm, const float *src, const float *w, float eps,
+                             const GemvGroup *grp) {
     const int saved = ctx->max_segments;
     if (dots) ctx->max_segments = 1;
     GemvPlan plan = plan_gemv(ctx, m, s0, s1);
@@ -663,6 +709,23 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
         P.xoff = (int)((per_tok + 15) / 16 * 16);
         per_tok = (size_t)P.xoff + (size_t)m->cols + 8 * (size_t)m->nc;
         G = 1;
+    }
+    if (grp) {
+        if (xsm == 0) throw Error(K2T_E_INTERNAL, "grouped gemv needs a fused activation source");
+        P.route = grp->route;
+        P.bank = grp->bank;
+        P.bank_stride = grp->stride;
+        P.mat_off = grp->mat_off;
+        P.cb_off = grp->cb_off;
+        P.slot_out = grp->slot_out;
+        P.slot_src = grp->slot_src;
+        P.gu_split = grp->gu_split;
+        const dim3 block(64 * plan.nseg);
+        P.lds_terms = 1;
+        P.exact = ctx->exact;
+        launch_fmt<false>(m, 1, xsm, dim3(plan.rb_hi - plan.rb_lo, 1, grp->nslots), block, per_tok, ctx->stream, P);
+        hip_check(hipGetLastError(), "grouped gemv launch");
+        return;
     }
     const int groups = ntok / G, rem = ntok % G;
     const dim3 block(64 * plan.nseg);

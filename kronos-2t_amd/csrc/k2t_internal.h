@@ -74,6 +74,22 @@ void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float 
                        float *out, bool accumulate);
 uint64_t hadamard_sign_mask_host(uint64_t block);
 
+// Grouped GEMV over sparse-MoE experts of one .k2tm bank (see GemvParams::route): slot z
+// streams the matrix of expert route[z]; `geom` gives the matrix shape and format (its
+// pair pointer is unused).  One token; the activation is built by the fused builder from
+// src + z * slot_src.
+struct GemvGroup {
+    const int *route;
+    int nslots;
+    const uint8_t *bank;
+    size_t stride;
+    uint32_t mat_off, cb_off;
+    size_t slot_out, slot_src;
+    int gu_split;
+};
+void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, int xs_mode, const float *src,
+                         const float *w, float eps, float *out);
+
 // The model takes ownership of `mat` (destroyed with the model).
 void model_adopt(k2t_model *m, k2t_mat *mat);
 

@@ -44,10 +44,12 @@ void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float ep
 // through store_hadamard_q8_head (real_llm.rs:8282-8365) into the cache slot of `pos`.
 // Positions are read from `pos_dev` (+ token index) so a captured graph can replay.
 __global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, const float *__restrict__ bias,
-                                                      const float *__restrict__ rope, const int *__restrict__ pos_dev,
-                                                      int nq, int nkv, int hd, int row_stride, int layer, int cap,
-                                                      int8_t *__restrict__ kq, int8_t *__restrict__ vq,
-                                                      float *__restrict__ ks, float *__restrict__ vs) {
+                                                      const float *__restrict__ qn, const float *__restrict__ kn,
+                                                      float eps, const float *__restrict__ rope,
+                                                      const int *__restrict__ pos_dev, int nq, int nkv, int hd,
+                                                      int row_stride, int layer, int cap, int8_t *__restrict__ kq,
+                                                      int8_t *__restrict__ vq, float *__restrict__ ks,
+                                                      float *__restrict__ vs) {
     const uint32_t lane = threadIdx.x;
     const int head = blockIdx.x, tok = blockIdx.y;
     const int pos = pos_dev[0] + tok;
@@ -57,6 +59,17 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, c
     if (bias) {
         v0 = v0 + bias[head * hd + lane];
         if (nb > 1) v1 = v1 + bias[head * hd + 64 + lane];
+    }
+    // Per-head RMSNorm of q and k before RoPE (apply_qk_norm_rope / apply_per_head_rms_norm,
+    // real_llm.rs:8139-8178): inv_rms = 1/sqrt(sum(v^2) * (1/hd) + eps), v = (v*inv_rms)*w.
+    const float *hn = head < nq ? qn : (head < nq + nkv ? kn : nullptr);
+    if (hn) {
+        float ss = v0 * v0;
+        if (nb > 1) ss = fmaf(v1, v1, ss);
+        ss = wave_sum_f(ss);
+        const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)hd) + eps);
+        v0 = (v0 * inv_rms) * hn[lane];
+        if (nb > 1) v1 = (v1 * inv_rms) * hn[64 + lane];
     }
     if (head < nq + nkv) {
         const float *row = rope + (size_t)pos * hd;
@@ -97,10 +110,11 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, c
     if (lane == 0) *sdst = mx / 127.0f;
 }
 
-void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *rope, const int *pos_dev, int nq,
-                     int nkv, int hd, int ntok, int layer, int cap, int8_t *kq, int8_t *vq, float *ks, float *vs) {
-    hipLaunchKernelGGL(qkv_post_kernel, dim3(nq + 2 * nkv, ntok), dim3(64), 0, st, qkv, bias, rope, pos_dev, nq, nkv,
-                       hd, (nq + 2 * nkv) * hd, layer, cap, kq, vq, ks, vs);
+void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
+                     const float *rope, const int *pos_dev, int nq, int nkv, int hd, int ntok, int layer, int cap,
+                     int8_t *kq, int8_t *vq, float *ks, float *vs) {
+    hipLaunchKernelGGL(qkv_post_kernel, dim3(nq + 2 * nkv, ntok), dim3(64), 0, st, qkv, bias, qn, kn, eps, rope,
+                       pos_dev, nq, nkv, hd, (nq + 2 * nkv) * hd, layer, cap, kq, vq, ks, vs);
     hip_check(hipGetLastError(), "qkv_post launch");
 }
 
@@ -388,6 +402,43 @@ void launch_embed_rows(hipStream_t st, const void *rows, bool bf16, const int *t
     hipLaunchKernelGGL(embed_rows_kernel, dim3((d + 255) / 256, ntok), dim3(256), 0, st, rows, bf16 ? 1 : 0, tokens,
                        d, out);
     hip_check(hipGetLastError(), "embed_rows launch");
+}
+
+// Benchmark support: seeded pseudo-random int8 K/V codes and positive scales for cache
+// positions [0, n_pos) of every layer and KV head (a counter-based SplitMix64 hash per
+// element, so the fill is reproducible and needs no state).
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void kv_synthetic_kernel(int8_t *__restrict__ kq, int8_t *__restrict__ vq,
+                                                           float *__restrict__ ks, float *__restrict__ vs,
+                                                           int layers_kv, int cap, int n_pos, int hd, uint64_t seed) {
+    const size_t slot_lin = blockIdx.x;  // (layer*nkv + kvh) * n_pos + pos
+    const int lk = (int)(slot_lin / (size_t)n_pos), pos = (int)(slot_lin % (size_t)n_pos);
+    if (lk >= layers_kv) return;
+    const size_t slot = (size_t)lk * cap + pos;
+    const uint64_t base = seed * 0x9E3779B97F4A7C15ull + slot_lin * 0x100000001B3ull;
+    for (int i = (int)threadIdx.x; i < hd; i += (int)blockDim.x) {
+        const uint64_t h = mix64(base + (uint64_t)i);
+        kq[slot * hd + i] = (int8_t)((int)(h & 0xFF) - 128 == -128 ? -127 : (int)(h & 0xFF) - 128);
+        vq[slot * hd + i] = (int8_t)((int)((h >> 8) & 0xFF) - 128 == -128 ? -127 : (int)((h >> 8) & 0xFF) - 128);
+    }
+    if (threadIdx.x == 0) {
+        const uint64_t h = mix64(base ^ 0xD1B54A32D192ED03ull);
+        ks[slot] = 0.005f + 0.045f * (float)(h & 0xFFFF) / 65535.0f;
+        vs[slot] = 0.005f + 0.045f * (float)((h >> 16) & 0xFFFF) / 65535.0f;
+    }
+}
+
+void launch_kv_synthetic(hipStream_t st, int8_t *kq, int8_t *vq, float *ks, float *vs, int layers_kv, int cap,
+                         int n_pos, int hd, uint64_t seed) {
+    if (n_pos <= 0) return;
+    hipLaunchKernelGGL(kv_synthetic_kernel, dim3((unsigned)((size_t)layers_kv * n_pos)), dim3(128), 0, st, kq, vq, ks,
+                       vs, layers_kv, cap, n_pos, hd, seed);
+    hip_check(hipGetLastError(), "kv_synthetic launch");
 }
 
 // Advances the device position counter after a step (keeps graph replays argument-free).

@@ -1,0 +1,457 @@
+// Sparse-MoE feed-forward for one token (SparseMoeRuntime::forward_layer_single,
+// sparse_moe.rs:961-1084) over NF3 / NF4 expert records of a .k2tm shard held in HBM.
+//
+// Every expert of every layer stays resident (a 30B-A3B shard is ~11 GB of the 288 GB),
+// so there is no paging.  Per token and MoE layer:
+//   1. moe_router_kernel   x_norm = RMSNorm(hidden) * post_norm, logits = W_router x_norm
+//                          (+ bias), one wave per expert;
+//   2. moe_select_kernel   softmax / topk-softmax / sigmoid, top-k, renormalize, sort by
+//                          expert id (route_sorted, sparse_moe.rs:86-182), one wave;
+//   3. grouped gate_up GEMV: slot z streams expert route[z]'s gate_up pairs with the int8
+//      activation of x_norm built in LDS (populate_fwht of x_norm); rows are written in
+//      [gate64, up64] blocks;
+//   4. grouped down GEMV: SwiGLU + FWHT (chunk c) + int8 of slot z's gate_up, built in
+//      LDS, times expert route[z]'s down pairs;
+//   5. moe_combine_kernel  proj = sum_z w_z * out_z in route order, hidden += proj.
+#include <float.h>
+#include <math.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/k2t_hip.h"
+#include "k2t_device.h"
+#include "k2t_internal.h"
+#include "k2t_moe.h"
+
+namespace k2t {
+
+// ---------------------------------------------------------------- .k2tm layout
+// K2tmShardHeader (moe_800b.rs:792-854) and nf_expert_byte_layout (moe_800b.rs:1311-1375).
+constexpr size_t kK2tmPage = 16384;
+static const char kK2tmMagic[12] = {'K', '2', 'T', 'M', '8', '0', '0', 'B', '_', 'V', '1', '\0'};
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+ExpertLayout expert_layout(size_t d_model, size_t d_ff, int bits, size_t sgc) {
+    ExpertLayout L{};
+    const size_t chunk_b = bits == 3 ? 384 : 512;
+    sgc = sgc < 1 ? 1 : sgc;
+    L.gu_rows = 2 * d_ff;
+    L.dn_rows = d_model;
+    const size_t gu_chunks = d_model / 64, gu_sg = (gu_chunks + sgc - 1) / sgc;
+    const size_t dn_chunks = d_ff / 64, dn_sg = (dn_chunks + sgc - 1) / sgc;
+    L.gu_pair_bytes = (L.gu_rows / 32) * (gu_sg * 64 + gu_chunks * 2 * chunk_b);
+    L.dn_pair_bytes = (L.dn_rows / 32) * (dn_sg * 64 + dn_chunks * 2 * chunk_b);
+    L.gu_cb_off = 0;
+    L.dn_cb_off = 16;
+    L.gu_pair_off = 64;
+    L.dn_pair_off = align_up(L.gu_pair_off + L.gu_pair_bytes, 64);
+    L.aligned_bytes = align_up(L.dn_pair_off + L.dn_pair_bytes, kK2tmPage);
+    return L;
+}
+
+static void decode_header(const uint8_t *page, size_t len, k2t_k2tm_header *h) {
+    if (!page || len < kK2tmPage) throw Error(K2T_E_ARG, "k2tm header shorter than 16384 bytes");
+    if (memcmp(page, kK2tmMagic, 12) != 0) throw Error(K2T_E_ARG, "bad k2tm header magic");
+    uint64_t w[7];
+    memcpy(w, page + 16, sizeof(w));
+    h->num_layers = (int64_t)w[0];
+    h->experts_per_layer = (int64_t)w[1];
+    h->d_model = (int64_t)w[2];
+    h->d_ff_expert = (int64_t)w[3];
+    h->scale_group_chunks = (int64_t)w[4];
+    h->aligned_expert_bytes = (int64_t)w[5];
+    h->bits = (int64_t)w[6];
+    const auto bad = [](const char *m) { throw Error(K2T_E_ARG, std::string("k2tm header: ") + m); };
+    if (h->num_layers <= 0 || h->num_layers > 4096) bad("layer count out of range");
+    if (h->experts_per_layer < 2 || h->experts_per_layer > 1024) bad("experts per layer out of range");
+    if (h->d_model <= 0 || h->d_model % 64 || h->d_model > 32768) bad("d_model must be a positive multiple of 64");
+    if (h->d_ff_expert <= 0 || h->d_ff_expert % 64 || h->d_ff_expert > 32768)
+        bad("d_ff_expert must be a positive multiple of 64");
+    if (h->scale_group_chunks < 0 || h->scale_group_chunks > 8) bad("scale_group_chunks out of range");
+    if (h->bits != 3 && h->bits != 4)
+        throw Error(K2T_E_STATE, "k2tm experts with " + std::to_string(h->bits) + " bits: the HIP GEMV takes NF3 and NF4");
+    const ExpertLayout L = expert_layout((size_t)h->d_model, (size_t)h->d_ff_expert, (int)h->bits,
+                                         (size_t)h->scale_group_chunks);
+    if ((size_t)h->aligned_expert_bytes != L.aligned_bytes) bad("aligned_expert_bytes does not match the NF layout");
+}
+
+static size_t total_bytes(const k2t_k2tm_header &h) {
+    return kK2tmPage + (size_t)h.num_layers * (size_t)h.experts_per_layer * (size_t)h.aligned_expert_bytes;
+}
+
+static void fill_geom(k2t_mat &m, int rows, int cols, int bits, int sgc, size_t pair_bytes) {
+    m = k2t_mat{};
+    m.fmt = K2T_FMT_NF;
+    m.rows = rows;
+    m.cols = cols;
+    m.nc = cols / 64;
+    m.stripes = rows / 16;
+    m.pairs = rows / 32;
+    m.has_tail = 0;
+    m.bits = bits;
+    m.sgc = sgc < 1 ? 1 : sgc;
+    m.pair_len = pair_bytes;
+}
+
+static k2t_experts *make_bank(k2t_ctx *ctx, const k2t_k2tm_header &h) {
+    k2t_experts *b = new k2t_experts();
+    b->ctx = ctx;
+    b->hdr = h;
+    b->lay = expert_layout((size_t)h.d_model, (size_t)h.d_ff_expert, (int)h.bits, (size_t)h.scale_group_chunks);
+    b->len = total_bytes(h);
+    fill_geom(b->gu, (int)b->lay.gu_rows, (int)h.d_model, (int)h.bits, (int)h.scale_group_chunks, b->lay.gu_pair_bytes);
+    fill_geom(b->dn, (int)b->lay.dn_rows, (int)h.d_ff_expert, (int)h.bits, (int)h.scale_group_chunks,
+              b->lay.dn_pair_bytes);
+    b->gu.ctx = b->dn.ctx = ctx;
+    return b;
+}
+
+// ---------------------------------------------------------------- kernels
+// Router logits: each wave owns one expert row; x_norm = (x * inv_rms) * w is formed on
+// the fly (rms_norm, real_llm.rs:9858-9898; the sum of squares in the order of the GEMV's
+// fused builder, so x_norm matches the expert activations' source), dot as in
+// dot_f32_moe (sparse_moe.rs:1644-1655) with a tree reduction.
+__global__ __launch_bounds__(256) void moe_router_kernel(const float *__restrict__ x, const float *__restrict__ nw,
+                                                         float eps, int d, const float *__restrict__ W,
+                                                         const float *__restrict__ bias, int E,
+                                                         float *__restrict__ logits) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const int e = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (e >= E) return;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const float4 *w4 = reinterpret_cast<const float4 *>(nw);
+    const float4 *r4 = reinterpret_cast<const float4 *>(W + (size_t)e * d);
+    const int n4 = d / 4;
+    float ss = 0.0f;
+    for (int i = (int)lane; i < n4; i += 64) {
+        const float4 v = x4[i];
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
+    ss = wave_sum_f(ss);
+    const float inv_rms = 1.0f / sqrtf(ss / (float)d + eps);
+    float acc = 0.0f;
+    for (int i = (int)lane; i < n4; i += 64) {
+        const float4 v = x4[i], w = w4[i], r = r4[i];
+        acc = fmaf((v.x * inv_rms) * w.x, r.x, acc);
+        acc = fmaf((v.y * inv_rms) * w.y, r.y, acc);
+        acc = fmaf((v.z * inv_rms) * w.z, r.z, acc);
+        acc = fmaf((v.w * inv_rms) * w.w, r.w, acc);
+    }
+    acc = wave_sum_f(acc);
+    if (lane == 0) logits[e] = bias ? acc + bias[e] : acc;
+}
+
+// Largest (value, lowest index on ties) over the wave; returns the lane's view of it.
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(v, m, kWave);
+        const int oi = __shfl_xor(i, m, kWave);
+        if (ov > v || (ov == v && oi < i)) {
+            v = ov;
+            i = oi;
+        }
+    }
+}
+
+// route_sorted (sparse_moe.rs:86-182) for E <= 256 experts on one wave.  Top-k picks the
+// largest score with the lowest id among equals, the order select_topk_by_score's strict
+// comparisons give; the top-k sums run in selection order like the reference's loops.
+__global__ __launch_bounds__(64) void moe_select_kernel(const float *__restrict__ logits, int E, int k, int norm_topk,
+                                                        int scoring, int *__restrict__ ids, float *__restrict__ wts) {
+    const int lane = (int)threadIdx.x;
+    float sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = lane + 64 * j;
+        sc[j] = e < E ? logits[e] : -INFINITY;
+        if (sc[j] != sc[j]) sc[j] = -INFINITY;  // NaN never wins a comparison: rank it last
+    }
+    if (scoring == K2T_MOE_SOFTMAX) {
+        float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        m = wave_max_f(m);
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            sc[j] = lane + 64 * j < E ? expf(sc[j] - m) : 0.0f;
+            s += sc[j];
+        }
+        s = wave_sum_f(s);
+        const float inv_all = s > 0.0f ? 1.0f / s : 1.0f / (float)E;
+#pragma unroll
+        for (int j = 0; j < 4; j++) sc[j] = lane + 64 * j < E ? sc[j] * inv_all : -INFINITY;
+    } else if (scoring == K2T_MOE_SIGMOID) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            sc[j] = lane + 64 * j < E && sc[j] == sc[j] ? 1.0f / (1.0f + expf(-sc[j])) : -INFINITY;
+    }
+    int sel_id[K2T_MOE_MAX_TOPK];
+    float sel_w[K2T_MOE_MAX_TOPK];
+    for (int r = 0; r < k; r++) {
+        float bv = sc[0];
+        int bi = lane;
+#pragma unroll
+        for (int j = 1; j < 4; j++)
+            if (sc[j] > bv) {
+                bv = sc[j];
+                bi = lane + 64 * j;
+            }
+        wave_argmax(bv, bi);
+        bi = min(bi, E - 1);  // every id indexes a record of the bank, whatever the scores
+        sel_id[r] = bi;
+        sel_w[r] = bv;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (lane + 64 * j == bi) sc[j] = -INFINITY;
+    }
+    if (lane != 0) return;
+    if (scoring == K2T_MOE_TOPK_SOFTMAX) {
+        const float mz = sel_w[0];
+        float s = 0.0f;
+        for (int r = 0; r < k; r++) {
+            sel_w[r] = expf(sel_w[r] - mz);
+            s += sel_w[r];
+        }
+        const float inv = s > 0.0f ? 1.0f / s : 1.0f / (float)k;
+        for (int r = 0; r < k; r++) sel_w[r] *= inv;
+    } else if (norm_topk) {
+        float s = 0.0f;
+        for (int r = 0; r < k; r++) s += sel_w[r];
+        if (s > 0.0f) {
+            const float inv = 1.0f / s;
+            for (int r = 0; r < k; r++) sel_w[r] *= inv;
+        }
+    }
+    // insertion sort by ascending expert id (sparse_moe.rs:170-179)
+    for (int i = 1; i < k; i++) {
+        const int ci = sel_id[i];
+        const float cw = sel_w[i];
+        int j = i;
+        while (j > 0 && sel_id[j - 1] > ci) {
+            sel_id[j] = sel_id[j - 1];
+            sel_w[j] = sel_w[j - 1];
+            j--;
+        }
+        sel_id[j] = ci;
+        sel_w[j] = cw;
+    }
+    for (int r = 0; r < k; r++) {
+        ids[r] = sel_id[r];
+        wts[r] = sel_w[r];
+    }
+}
+
+// out.fill(0); out += w_z * expert_z in route order; hidden += out
+// (sparse_moe.rs:1001-1003, 1041-1043; real_llm.rs:6714).
+__global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ hidden, const float *__restrict__ eo,
+                                                          const float *__restrict__ wts, int k, int d) {
+    const int r = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (r >= d) return;
+    float p = 0.0f;
+    for (int z = 0; z < k; z++) p = p + wts[z] * eo[(size_t)z * d + r];
+    hidden[r] = hidden[r] + p;
+}
+
+void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float *post_norm, float eps,
+                    const MoeWork &ws) {
+    const k2t_experts *b = L.bank;
+    const int d = (int)b->hdr.d_model, dff = (int)b->hdr.d_ff_expert, E = (int)b->hdr.experts_per_layer;
+    hipStream_t st = ctx->stream;
+    hipLaunchKernelGGL(moe_router_kernel, dim3((E + 3) / 4), dim3(256), 0, st, hidden, post_norm, eps, d, L.router_w,
+                       L.router_b, E, ws.logits);
+    hip_check(hipGetLastError(), "moe router launch");
+    hipLaunchKernelGGL(moe_select_kernel, dim3(1), dim3(64), 0, st, ws.logits, E, L.top_k, L.norm_topk, L.scoring,
+                       ws.ids, ws.wts);
+    hip_check(hipGetLastError(), "moe select launch");
+    const uint8_t *layer_base = b->d_bytes + kK2tmPage + (size_t)L.shard_layer * E * b->lay.aligned_bytes;
+    GemvGroup g{};
+    g.route = ws.ids;
+    g.nslots = L.top_k;
+    g.bank = layer_base;
+    g.stride = b->lay.aligned_bytes;
+    g.mat_off = (uint32_t)b->lay.gu_pair_off;
+    g.cb_off = (uint32_t)b->lay.gu_cb_off;
+    g.slot_out = (size_t)2 * dff;
+    g.slot_src = 0;
+    g.gu_split = 1;
+    launch_gemv_grouped(ctx, &b->gu, g, K2T_XS_RMSNORM, hidden, post_norm, eps, ws.gu);
+    g.mat_off = (uint32_t)b->lay.dn_pair_off;
+    g.cb_off = (uint32_t)b->lay.dn_cb_off;
+    g.slot_out = (size_t)d;
+    g.slot_src = (size_t)2 * dff;
+    g.gu_split = 0;
+    launch_gemv_grouped(ctx, &b->dn, g, K2T_XS_SWIGLU, ws.gu, nullptr, 0.0f, ws.eo);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((d + 255) / 256), dim3(256), 0, st, hidden, ws.eo, ws.wts, L.top_k,
+                       d);
+    hip_check(hipGetLastError(), "moe combine launch");
+}
+
+size_t moe_work_floats(const k2t_experts *b, int top_k) {
+    const size_t d = (size_t)b->hdr.d_model, dff = (size_t)b->hdr.d_ff_expert, E = (size_t)b->hdr.experts_per_layer;
+    return E + 2 * (size_t)top_k + (size_t)top_k * 2 * dff + (size_t)top_k * d + 64;
+}
+
+MoeWork moe_work_carve(float *base, const k2t_experts *b, int top_k) {
+    const size_t d = (size_t)b->hdr.d_model, dff = (size_t)b->hdr.d_ff_expert, E = (size_t)b->hdr.experts_per_layer;
+    MoeWork w;
+    float *p = base;
+    w.gu = p;  // 16-byte aligned first
+    p += (size_t)top_k * 2 * dff;
+    w.eo = p;
+    p += (size_t)top_k * d;
+    w.logits = p;
+    p += E;
+    w.wts = p;
+    p += top_k;
+    w.ids = reinterpret_cast<int *>(p);
+    return w;
+}
+
+void check_moe_args(const k2t_experts *bank, int shard_layer, int top_k, int scoring) {
+    if (!bank) throw Error(K2T_E_ARG, "expert bank is NULL");
+    if (shard_layer < 0 || shard_layer >= bank->hdr.num_layers) throw Error(K2T_E_ARG, "shard layer out of range");
+    if (top_k < 1 || top_k > K2T_MOE_MAX_TOPK || top_k > bank->hdr.experts_per_layer)
+        throw Error(K2T_E_ARG, "top_k out of range");
+    if (bank->hdr.experts_per_layer > 256) throw Error(K2T_E_ARG, "at most 256 experts per layer");
+    if (scoring != K2T_MOE_SOFTMAX && scoring != K2T_MOE_TOPK_SOFTMAX && scoring != K2T_MOE_SIGMOID)
+        throw Error(K2T_E_ARG, "unknown router scoring");
+    if ((size_t)bank->hdr.d_model > (size_t)kSignBlocks * 64 || (size_t)bank->hdr.d_ff_expert > (size_t)kSignBlocks * 64)
+        throw Error(K2T_E_ARG, "expert dimensions exceed the Hadamard sign table");
+}
+
+}  // namespace k2t
+
+using namespace k2t;
+
+namespace {
+template <typename F>
+int32_t mguard(F &&fn) {
+    try {
+        fn();
+        return K2T_OK;
+    } catch (const Error &e) {
+        set_last_error(e.what());
+        return e.code;
+    } catch (const std::exception &e) {
+        set_last_error(e.what());
+        return K2T_E_INTERNAL;
+    } catch (...) {
+        set_last_error("unknown error");
+        return K2T_E_INTERNAL;
+    }
+}
+}  // namespace
+
+extern "C" {
+
+int32_t k2t_k2tm_read_header(const uint8_t *page, size_t len, k2t_k2tm_header *out) {
+    return mguard([&] {
+        if (!out) throw Error(K2T_E_ARG, "NULL argument");
+        decode_header(page, len, out);
+    });
+}
+
+int32_t k2t_k2tm_expert_layout(int64_t d_model, int64_t d_ff, int32_t bits, int32_t sgc, k2t_k2tm_layout *out) {
+    return mguard([&] {
+        if (!out) throw Error(K2T_E_ARG, "NULL argument");
+        if (d_model <= 0 || d_model % 64 || d_ff <= 0 || d_ff % 64 || (bits != 3 && bits != 4) || sgc < 0 || sgc > 8)
+            throw Error(K2T_E_ARG, "bad expert layout parameters");
+        const ExpertLayout L = expert_layout((size_t)d_model, (size_t)d_ff, bits, (size_t)sgc);
+        out->gu_codebook_off = L.gu_cb_off;
+        out->dn_codebook_off = L.dn_cb_off;
+        out->gu_pair_off = L.gu_pair_off;
+        out->gu_pair_bytes = L.gu_pair_bytes;
+        out->dn_pair_off = L.dn_pair_off;
+        out->dn_pair_bytes = L.dn_pair_bytes;
+        out->aligned_expert_bytes = L.aligned_bytes;
+    });
+}
+
+int32_t k2t_experts_upload(k2t_ctx *ctx, const uint8_t *k2tm, size_t len, k2t_experts **out) {
+    return mguard([&] {
+        if (!ctx || !k2tm || !out) throw Error(K2T_E_ARG, "NULL argument");
+        *out = nullptr;
+        k2t_k2tm_header h;
+        decode_header(k2tm, len, &h);
+        if (len < total_bytes(h)) throw Error(K2T_E_ARG, "k2tm shard shorter than its header declares");
+        k2t_experts *b = make_bank(ctx, h);
+        hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+        void *d = nullptr;
+        const hipError_t e = hipMalloc(&d, b->len);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            delete b;
+            throw Error(K2T_E_NOMEM, std::string("hipMalloc failed: ") + hipGetErrorString(e));
+        }
+        b->d_bytes = (uint8_t *)d;
+        b->owns = true;
+        const hipError_t c = hipMemcpy(d, k2tm, b->len, hipMemcpyHostToDevice);
+        if (c != hipSuccess) {
+            k2t_experts_destroy(b);
+            hip_check(c, "k2tm upload");
+        }
+        *out = b;
+    });
+}
+
+int32_t k2t_experts_wrap(k2t_ctx *ctx, const uint8_t *d_k2tm, size_t len, const uint8_t *header_page,
+                         k2t_experts **out) {
+    return mguard([&] {
+        if (!ctx || !d_k2tm || !out) throw Error(K2T_E_ARG, "NULL argument");
+        *out = nullptr;
+        k2t_k2tm_header h;
+        decode_header(header_page, kK2tmPage, &h);
+        if (len < total_bytes(h)) throw Error(K2T_E_ARG, "device shard shorter than its header declares");
+        if ((uintptr_t)d_k2tm % 256) throw Error(K2T_E_ARG, "device shard must be 256-byte aligned");
+        k2t_experts *b = make_bank(ctx, h);
+        b->d_bytes = const_cast<uint8_t *>(d_k2tm);
+        b->owns = false;
+        *out = b;
+    });
+}
+
+void k2t_experts_destroy(k2t_experts *b) {
+    if (!b) return;
+    if (b->owns && b->d_bytes) {
+        (void)hipSetDevice(b->ctx->device);
+        (void)hipFree(b->d_bytes);
+    }
+    delete b;
+}
+
+int32_t k2t_experts_info(const k2t_experts *b, k2t_k2tm_header *out) {
+    return mguard([&] {
+        if (!b || !out) throw Error(K2T_E_ARG, "NULL argument");
+        *out = b->hdr;
+    });
+}
+
+int32_t k2t_moe_ffn(k2t_ctx *ctx, const k2t_experts *bank, int32_t shard_layer, const float *d_router_w,
+                    const float *d_router_bias, int32_t top_k, int32_t norm_topk_prob, int32_t scoring,
+                    float *d_hidden, const float *d_post_norm, float eps, int32_t *d_route_ids,
+                    float *d_route_weights) {
+    return mguard([&] {
+        if (!ctx || !d_router_w || !d_hidden || !d_post_norm) throw Error(K2T_E_ARG, "NULL argument");
+        check_moe_args(bank, shard_layer, top_k, scoring);
+        if (bank->ctx != ctx) throw Error(K2T_E_ARG, "expert bank of another context");
+        MoeLayer L{bank, shard_layer, d_router_w, d_router_bias, top_k, norm_topk_prob ? 1 : 0, scoring};
+        ensure_scratch(ctx, moe_work_floats(bank, top_k));
+        const MoeWork ws = moe_work_carve(ctx->scratch, bank, top_k);
+        launch_moe_ffn(ctx, L, d_hidden, d_post_norm, eps, ws);
+        if (d_route_ids)
+            hip_check(hipMemcpyAsync(d_route_ids, ws.ids, (size_t)top_k * sizeof(int), hipMemcpyDeviceToDevice,
+                                     ctx->stream),
+                      "route copy");
+        if (d_route_weights)
+            hip_check(hipMemcpyAsync(d_route_weights, ws.wts, (size_t)top_k * sizeof(float), hipMemcpyDeviceToDevice,
+                                     ctx->stream),
+                      "route copy");
+    });
+}
+
+}  // extern "C"

@@ -88,7 +88,19 @@ SIGNATURES = {
     "k2t_k2tb_matrix": (I32, [VP, I32, I32, I32, VP, VP, SZ, VP, SZ]),
     "k2t_k2tb_vector": (I32, [VP, I32, I32, C.POINTER(SZ), VP, SZ]),
     "k2t_model_load_k2tb": (I32, [VP, VP, C.c_char_p, I32, C.POINTER(VP)]),
+    "k2t_k2tm_read_header": (I32, [VP, SZ, VP]),
+    "k2t_k2tm_expert_layout": (I32, [C.c_int64, C.c_int64, I32, I32, VP]),
+    "k2t_experts_upload": (I32, [VP, VP, SZ, C.POINTER(VP)]),
+    "k2t_experts_wrap": (I32, [VP, VP, SZ, VP, C.POINTER(VP)]),
+    "k2t_experts_destroy": (None, [VP]),
+    "k2t_experts_info": (I32, [VP, VP]),
+    "k2t_moe_ffn": (I32, [VP, VP, I32, VP, VP, I32, I32, I32, VP, VP, C.c_float, VP, VP]),
+    "k2t_model_set_qk_norm": (I32, [VP, I32, VP, VP]),
+    "k2t_model_set_moe": (I32, [VP, I32, VP, I32, VP, VP, I32, I32, I32]),
+    "k2t_model_kv_synthetic": (I32, [VP, I32, C.c_uint64]),
 }
+
+MOE_SOFTMAX, MOE_TOPK_SOFTMAX, MOE_SIGMOID = 0, 1, 2
 
 EMBED_TIED, EMBED_F32, EMBED_BF16, EMBED_NF4 = 0, 1, 2, 3
 
@@ -98,6 +110,32 @@ class ModelConfig(C.Structure):
     _fields_ = [("n_layers", I32), ("hidden", I32), ("n_heads", I32), ("n_kv_heads", I32), ("head_dim", I32),
                 ("intermediate", I32), ("vocab", I32), ("max_seq", I32), ("rms_eps", C.c_float),
                 ("rope_theta", C.c_float)]
+
+
+class K2tmHeader(C.Structure):
+    """k2t_k2tm_header (K2tmShardHeader)."""
+    _fields_ = [(n, C.c_int64) for n in ("num_layers", "experts_per_layer", "d_model", "d_ff_expert",
+                                         "scale_group_chunks", "aligned_expert_bytes", "bits")]
+
+
+class K2tmLayout(C.Structure):
+    """k2t_k2tm_layout (NfExpertByteLayout offsets)."""
+    _fields_ = [(n, C.c_int64) for n in ("gu_codebook_off", "dn_codebook_off", "gu_pair_off", "gu_pair_bytes",
+                                         "dn_pair_off", "dn_pair_bytes", "aligned_expert_bytes")]
+
+
+def k2tm_read_header(page):
+    import numpy as np
+    b = np.frombuffer(page, np.uint8) if isinstance(page, (bytes, bytearray)) else np.ascontiguousarray(page, np.uint8)
+    h = K2tmHeader()
+    check(lib().k2t_k2tm_read_header(b.ctypes.data_as(VP), b.size, C.byref(h)))
+    return {n: getattr(h, n) for n, _ in K2tmHeader._fields_}
+
+
+def k2tm_expert_layout(d_model, d_ff, bits, sgc):
+    out = K2tmLayout()
+    check(lib().k2t_k2tm_expert_layout(d_model, d_ff, bits, sgc, C.byref(out)))
+    return {n: getattr(out, n) for n, _ in K2tmLayout._fields_}
 
 
 class K2tbMatrixInfo(C.Structure):
@@ -216,8 +254,56 @@ class Ctx:
     def gemv(self, m, xq, xs, xsum, out, ntok=1, s0=0, s1=-1, out_stride=0):
         check(lib().k2t_gemv(self.h, m.h, _p(xq), _p(xs), _p(xsum), ntok, s0, s1, _p(out), out_stride))
 
+    def moe_ffn(self, bank, shard_layer, router_w, hidden, post_norm, eps, top_k, norm_topk_prob=True,
+                scoring=0, router_bias=None, route_ids=None, route_weights=None):
+        """k2t_moe_ffn: hidden (device f32 [d]) += the MoE feed-forward of one token."""
+        check(lib().k2t_moe_ffn(self.h, bank.h, shard_layer, _p(router_w), _p(router_bias), top_k,
+                                int(bool(norm_topk_prob)), scoring, _p(hidden), _p(post_norm), float(eps),
+                                _p(route_ids), _p(route_weights)))
+
     def gemv_chunk_dots(self, m, xq, xsum, dots):
         check(lib().k2t_gemv_chunk_dots(self.h, m.h, _p(xq), _p(xsum), _p(dots)))
+
+
+class ExpertBank:
+    """k2t_experts: a .k2tm shard in HBM (uploaded from host bytes, or wrapping device memory)."""
+
+    def __init__(self, ctx, h, keep=None):
+        self.ctx, self.h, self._keep = ctx, h, keep
+
+    @classmethod
+    def upload(cls, ctx, k2tm_bytes):
+        import numpy as np
+        b = np.frombuffer(k2tm_bytes, np.uint8) if isinstance(k2tm_bytes, (bytes, bytearray)) else \
+            np.ascontiguousarray(k2tm_bytes, np.uint8)
+        h = VP()
+        check(lib().k2t_experts_upload(ctx.h, b.ctypes.data_as(VP), b.size, C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def wrap(cls, ctx, d_tensor, nbytes, header_page):
+        import numpy as np
+        hp = np.ascontiguousarray(np.frombuffer(header_page, np.uint8) if isinstance(header_page, (bytes, bytearray))
+                                  else header_page, np.uint8)
+        h = VP()
+        check(lib().k2t_experts_wrap(ctx.h, _p(d_tensor), nbytes, hp.ctypes.data_as(VP), C.byref(h)))
+        return cls(ctx, h, keep=d_tensor)
+
+    def info(self):
+        h = K2tmHeader()
+        check(lib().k2t_experts_info(self.h, C.byref(h)))
+        return {n: getattr(h, n) for n, _ in K2tmHeader._fields_}
+
+    def close(self):
+        if self.h and not _shutting_down:
+            lib().k2t_experts_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Mat:
@@ -307,7 +393,8 @@ class Model:
         inn = np.ascontiguousarray(in_norm, np.float32)
         pn = np.ascontiguousarray(post_norm, np.float32)
         b = None if qkv_bias is None else np.ascontiguousarray(qkv_bias, np.float32)
-        check(lib().k2t_model_set_layer(self.h, layer, qkv.h, o.h, gate_up.h, down.h, inn.ctypes.data_as(VP),
+        check(lib().k2t_model_set_layer(self.h, layer, qkv.h, o.h, None if gate_up is None else gate_up.h,
+                                        None if down is None else down.h, inn.ctypes.data_as(VP),
                                         pn.ctypes.data_as(VP), None if b is None else b.ctypes.data_as(VP)))
         self._keep.append((qkv, o, gate_up, down))
 
@@ -316,6 +403,26 @@ class Model:
         fn = np.ascontiguousarray(final_norm, np.float32)
         check(lib().k2t_model_set_head(self.h, head.h, fn.ctypes.data_as(VP)))
         self._keep.append(head)
+
+    def set_qk_norm(self, layer, q_norm=None, k_norm=None):
+        import numpy as np
+        qn = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32)
+        kn = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32)
+        check(lib().k2t_model_set_qk_norm(self.h, layer, None if qn is None else qn.ctypes.data_as(VP),
+                                          None if kn is None else kn.ctypes.data_as(VP)))
+
+    def set_moe(self, layer, bank, shard_layer, router_w, top_k, norm_topk_prob=True, scoring=0,
+                router_bias=None):
+        import numpy as np
+        rw = np.ascontiguousarray(router_w, np.float32)
+        rb = None if router_bias is None else np.ascontiguousarray(router_bias, np.float32)
+        check(lib().k2t_model_set_moe(self.h, layer, bank.h, shard_layer, rw.ctypes.data_as(VP),
+                                      None if rb is None else rb.ctypes.data_as(VP), top_k,
+                                      int(bool(norm_topk_prob)), scoring))
+        self._keep.append(bank)
+
+    def kv_synthetic(self, n_pos, seed=0):
+        check(lib().k2t_model_kv_synthetic(self.h, int(n_pos), int(seed)))
 
     def set_embedding(self, kind, rows=None, nf4=None):
         """k2t_model_set_embedding: EMBED_TIED, EMBED_F32 / EMBED_BF16 (host rows

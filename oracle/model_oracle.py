@@ -117,11 +117,18 @@ class OracleModel:
         rope = O.rope_row(hd, float(np.float32(c["rope_theta"])), pos)
         scale = np.float32(1.0) / np.sqrt(np.float32(hd))
         hidden = self.embed(token).astype(np.float32)
+        self.last_routes = []
         for li, L in enumerate(self.layers):
             xq, xs, xsum = O.populate_fwht(hidden, L["in_norm"], O.inv_rms(hidden, eps))
             qkv = self._gemv(L["qkv"], xq, xs, xsum).reshape(-1, hd)
             if L.get("bias") is not None:
                 qkv = (qkv + L["bias"].reshape(-1, hd)).astype(np.float32)
+            # per-head q / k RMSNorm before RoPE (apply_qk_norm_rope, 8139-8178); hd is a
+            # power of two, so sum*(1/hd) equals the mean or_inv_rms forms
+            for h in range(nq + nkv):
+                wn = L.get("q_norm") if h < nq else L.get("k_norm")
+                if wn is not None:
+                    qkv[h] = ((qkv[h] * np.float32(O.inv_rms(qkv[h], eps))) * wn).astype(np.float32)
             for h in range(nq + nkv):
                 qkv[h] = O.rope_apply(qkv[h], rope)
             for kvh in range(nkv):
@@ -135,6 +142,10 @@ class OracleModel:
                                            self.vq[li, kvh, :pos + 1], self.vs[li, kvh, :pos + 1], scale))
             aq, as_, asum = O.populate_fwht(np.concatenate(outs))
             hidden = (hidden + self._gemv(L["o"], aq, as_, asum)).astype(np.float32)
+            if L.get("moe") is not None:
+                hidden, routes = moe_ffn(hidden, L["post_norm"], eps, L["moe"])
+                self.last_routes.append(routes)
+                continue
             xq, xs, xsum = O.populate_fwht(hidden, L["post_norm"], O.inv_rms(hidden, eps))
             gu = self._gemv(L["gu"], xq, xs, xsum).reshape(-1, 128)
             sw = np.concatenate([O.swiglu(gu[ic, :64], gu[ic, 64:]) for ic in range(inter // 64)])
@@ -143,6 +154,92 @@ class OracleModel:
         xq, xs, xsum = O.populate_fwht(hidden, self.final_norm, O.inv_rms(hidden, eps))
         self.pos += 1
         return self._gemv(self.head, xq, xs, xsum)
+
+
+# ------------------------------------------------------------------ sparse MoE
+SOFTMAX, TOPK_SOFTMAX, SIGMOID = 0, 1, 2
+
+
+def route_sorted(logits, top_k, norm_topk_prob, scoring):
+    """DenseMoeRouter::route_sorted after the logits (sparse_moe.rs:86-182) in float32:
+    scoring, select_topk_by_score (strict '>' insertion, 185-206), renormalization in
+    selection order, then sort by ascending expert id."""
+    z = np.asarray(logits, np.float32).copy()
+    E = z.size
+    k = min(top_k, E)
+    f32 = np.float32
+    if scoring == SOFTMAX:
+        m = z.max()
+        s = f32(0.0)
+        for e in range(E):
+            z[e] = np.exp(f32(z[e] - m), dtype=np.float32)
+            s = f32(s + z[e])
+        inv = f32(1.0) / s if s > 0 else f32(1.0) / f32(E)
+        z = (z * inv).astype(np.float32)
+    elif scoring == SIGMOID:
+        z = (f32(1.0) / (f32(1.0) + np.exp(-z, dtype=np.float32))).astype(np.float32)
+    out = []
+    for e in range(E):
+        v = z[e]
+        if len(out) < k:
+            pos = len(out)
+            while pos > 0 and v > out[pos - 1][1]:
+                pos -= 1
+            out.insert(pos, (e, v))
+        elif v > out[k - 1][1]:
+            pos = k - 1
+            while pos > 0 and v > out[pos - 1][1]:
+                pos -= 1
+            out.insert(pos, (e, v))
+            out.pop()
+    if scoring == TOPK_SOFTMAX:
+        mz = max(w for _, w in out)
+        ws = [np.exp(f32(w - mz), dtype=np.float32) for _, w in out]
+        s = f32(0.0)
+        for w in ws:
+            s = f32(s + w)
+        inv = f32(1.0) / s if s > 0 else f32(1.0) / f32(k)
+        out = [(e, f32(w * inv)) for (e, _), w in zip(out, ws)]
+    elif norm_topk_prob:
+        s = f32(0.0)
+        for _, w in out:
+            s = f32(s + w)
+        if s > 0:
+            inv = f32(1.0) / s
+            out = [(e, f32(w * inv)) for e, w in out]
+    return sorted(out, key=lambda t: t[0])
+
+
+def rms_norm(x, w, eps):
+    """rms_norm (real_llm.rs:9858-9898): (x * inv_rms) * w."""
+    return ((np.asarray(x, np.float32) * np.float32(O.inv_rms(x, eps))) * np.asarray(w, np.float32)).astype(np.float32)
+
+
+def moe_ffn(hidden, post_norm, eps, moe):
+    """forward_layer_single (sparse_moe.rs:961-1084) + the residual add (real_llm.rs:6711-6714).
+    moe: dict(router_w [E][d] f32, router_b [E] or None, top_k, norm_topk_prob, scoring,
+    experts: list of (gu Matrix-like dict, dn dict) with pair/cb/bits/sgc/rows/cols).
+    Returns (new hidden, routes)."""
+    xn = rms_norm(hidden, post_norm, eps)
+    W = np.asarray(moe["router_w"], np.float32)
+    logits = np.array([np.dot(W[e].astype(np.float64), xn.astype(np.float64)) for e in range(W.shape[0])],
+                      np.float32)
+    if moe.get("router_b") is not None:
+        logits = (logits + moe["router_b"]).astype(np.float32)
+    routes = route_sorted(logits, moe["top_k"], moe["norm_topk_prob"], moe["scoring"])
+    aq, as_, _ = O.populate_fwht(xn)
+    out = np.zeros(hidden.size, np.float32)
+    for e, w in routes:
+        gu, dn = moe["experts"][e]
+        g = O.nf_gemv(gu["pair"], np.zeros(0, np.uint8), gu["rows"], gu["cols"], gu["bits"], gu["sgc"], gu["cb"],
+                      aq, as_)
+        dff = gu["rows"] // 2
+        sw = O.swiglu(g[:dff], g[dff:])
+        mq, ms, _ = O.populate_fwht(sw)
+        y = O.nf_gemv(dn["pair"], np.zeros(0, np.uint8), dn["rows"], dn["cols"], dn["bits"], dn["sgc"], dn["cb"],
+                      mq, ms)
+        out = (out + (np.float32(w) * y).astype(np.float32)).astype(np.float32)
+    return (hidden + out).astype(np.float32), routes
 
 
 def random_model(cfg, seed, fmt="nf4", planes=None):

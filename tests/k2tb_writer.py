@@ -97,3 +97,57 @@ def nf_source(W, bits=4, sgc=2):
     idx, sc = O.nf_rtn(W, bits, sgc, cb, mu)
     pair, tail = O.nf_from_indices(idx, sc, rows, cols, bits, sgc)
     return {"kind": "nf", "rows": rows, "cols": cols, "bits": bits, "sgc": sgc, "cb": cb, "pair": pair, "tail": tail}
+
+
+# ------------------------------------------------------------------ .k2tm shards
+K2TM_PAGE = 16384
+K2TM_MAGIC = b"K2TM800B_V1\0"
+
+
+def _align(v, a):
+    return (v + a - 1) // a * a
+
+
+def expert_layout(d_model, d_ff, bits, sgc):
+    """nf_expert_byte_layout (moe_800b.rs:1332-1375)."""
+    chunk_b = 384 if bits == 3 else 512
+    sgc = max(sgc, 1)
+    gu_chunks, dn_chunks = d_model // 64, d_ff // 64
+    gu_pair = (2 * d_ff // 32) * (-(-gu_chunks // sgc) * 64 + gu_chunks * 2 * chunk_b)
+    dn_pair = (d_model // 32) * (-(-dn_chunks // sgc) * 64 + dn_chunks * 2 * chunk_b)
+    dn_off = _align(64 + gu_pair, 64)
+    return dict(gu_cb=0, dn_cb=16, gu_off=64, gu_bytes=gu_pair, dn_off=dn_off, dn_bytes=dn_pair,
+                aligned=_align(dn_off + dn_pair, K2TM_PAGE))
+
+
+def write_k2tm(experts, d_model, d_ff, bits, sgc):
+    """K2tmShardHeader page + pack_nf_expert_record per expert (moe_800b.rs:792-854,
+    1377-1404).  experts[layer][e] = (gu nf_source dict, dn nf_source dict).  Returns bytes."""
+    L = expert_layout(d_model, d_ff, bits, sgc)
+    n_layers, E = len(experts), len(experts[0])
+    buf = bytearray(K2TM_PAGE + n_layers * E * L["aligned"])
+    buf[0:12] = K2TM_MAGIC
+    for i, w in enumerate((n_layers, E, d_model, d_ff, sgc, L["aligned"], bits)):
+        buf[16 + 8 * i:24 + 8 * i] = struct.pack("<Q", w)
+    for li, layer in enumerate(experts):
+        for e, (gu, dn) in enumerate(layer):
+            assert gu["tail"].size == 0 and dn["tail"].size == 0
+            assert gu["pair"].size == L["gu_bytes"] and dn["pair"].size == L["dn_bytes"]
+            base = K2TM_PAGE + (li * E + e) * L["aligned"]
+            buf[base + L["gu_cb"]:base + L["gu_cb"] + 16] = np.asarray(gu["cb"], np.int8).tobytes()
+            buf[base + L["dn_cb"]:base + L["dn_cb"] + 16] = np.asarray(dn["cb"], np.int8).tobytes()
+            buf[base + L["gu_off"]:base + L["gu_off"] + L["gu_bytes"]] = gu["pair"].tobytes()
+            buf[base + L["dn_off"]:base + L["dn_off"] + L["dn_bytes"]] = dn["pair"].tobytes()
+    return bytes(buf)
+
+
+def random_moe_layer(rng, d_model, d_ff, E, bits=3, sgc=2):
+    """One layer's experts: gate_up = [gate; up] rows (2*d_ff x d_model) and down
+    (d_model x d_ff), ~N(0, 0.02), NF-quantized by the oracle; plus an fp32 router."""
+    experts = []
+    for _ in range(E):
+        Wgu = (rng.standard_normal((2 * d_ff, d_model)) * 0.02).astype(np.float32)
+        Wdn = (rng.standard_normal((d_model, d_ff)) * 0.02).astype(np.float32)
+        experts.append((nf_source(Wgu, bits, sgc), nf_source(Wdn, bits, sgc)))
+    router = (rng.standard_normal((E, d_model)) * 0.05).astype(np.float32)
+    return experts, router

@@ -1,0 +1,181 @@
+"""Sparse-MoE feed-forward on the GPU (k2t_moe_ffn, and MoE layers inside the decode
+engine with per-head QK-norm and q_dim != hidden) against the oracle's restatement of
+forward_layer_single (sparse_moe.rs:961-1084) / route_sorted (86-182).
+
+Bar: the routed expert ids equal the oracle's (inputs are drawn so that no two of the
+top-(k+1) router probabilities are within 1e-4 of each other: the router's fp32 dot
+order, like the reference's NEON vs x86 orders, is not a bit-exact contract), the route
+weights within 1e-5, and the layer output within the end-to-end bar (cosine > 0.99999,
+max |diff| <= 1e-3 of max |hidden|).  Integer expert dots are exact (grouped NF GEMV),
+but an int8 code of x_norm or of the SwiGLU output can move by one where inv_rms / expf
+round differently.
+"""
+import numpy as np
+import pytest
+import torch
+
+import k2t
+from k2tb_writer import K2TM_PAGE, random_moe_layer, write_k2tm
+from model_oracle import Matrix, OracleModel, moe_ffn, quantize_matrix
+
+pytestmark = pytest.mark.gpu
+
+
+def _moe_dict(experts, router, top_k, norm, scoring):
+    return dict(router_w=router, router_b=None, top_k=top_k, norm_topk_prob=norm, scoring=scoring,
+                experts=experts)
+
+
+def _well_separated(hidden, post_norm, eps, router, k):
+    from model_oracle import rms_norm
+    z = router.astype(np.float64) @ rms_norm(hidden, post_norm, eps).astype(np.float64)
+    s = np.sort(z)[::-1][:k + 1]
+    return np.min(np.abs(np.diff(s))) > 1e-3
+
+
+@pytest.mark.parametrize("bits,E,k,scoring,norm", [(3, 16, 4, 0, True), (4, 16, 4, 0, False), (3, 64, 8, 1, True),
+                                                    (3, 32, 6, 2, True)])
+def test_moe_ffn_matches_oracle(gpu_ctx, bits, E, k, scoring, norm):
+    print(f"moe_ffn bits={bits} E={E} k={k} scoring={scoring}", flush=True)
+    d, dff = 256, 128
+    rng = np.random.default_rng(100 + E + bits)
+    layers = [random_moe_layer(rng, d, dff, E, bits=bits) for _ in range(2)]
+    blob = write_k2tm([l[0] for l in layers], d, dff, bits, 2)
+    bank = k2t.ExpertBank.upload(gpu_ctx, blob)
+    assert bank.info()["experts_per_layer"] == E
+    post_norm = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    ids = torch.zeros(k, dtype=torch.int32, device="cuda")
+    wts = torch.zeros(k, dtype=torch.float32, device="cuda")
+    checked = 0
+    for trial in range(12):
+        hidden = rng.standard_normal(d).astype(np.float32)
+        layer = trial % 2
+        experts, router = layers[layer]
+        if not _well_separated(hidden, post_norm, 1e-6, router, k):
+            continue
+        want, routes = moe_ffn(hidden, post_norm, 1e-6, _moe_dict(experts, router, k, norm, scoring))
+        dh = torch.from_numpy(hidden).cuda()
+        gpu_ctx.moe_ffn(bank, layer, torch.from_numpy(router).cuda(), dh, torch.from_numpy(post_norm).cuda(), 1e-6,
+                        k, norm, scoring, route_ids=ids, route_weights=wts)
+        gpu_ctx.sync()
+        got_ids = ids.cpu().numpy().tolist()
+        assert got_ids == [e for e, _ in routes], f"trial {trial}: routes {got_ids} vs {routes}"
+        assert np.allclose(wts.cpu().numpy(), [w for _, w in routes], rtol=1e-5, atol=1e-7)
+        got = dh.cpu().numpy()
+        delta_w, delta_g = want - hidden, got - hidden
+        cos = float(np.dot(delta_w, delta_g) / (np.linalg.norm(delta_w) * np.linalg.norm(delta_g)))
+        assert cos > 0.9999, f"trial {trial}: moe output cos {cos}"
+        assert np.abs(got - want).max() <= 1e-3 * np.abs(want).max()
+        checked += 1
+    assert checked >= 6
+    bank.close()
+
+
+def test_moe_ffn_argument_errors(gpu_ctx):
+    rng = np.random.default_rng(5)
+    experts, router = random_moe_layer(rng, 128, 64, 4, bits=3)
+    bank = k2t.ExpertBank.upload(gpu_ctx, write_k2tm([experts], 128, 64, 3, 2))
+    h = torch.zeros(128, device="cuda")
+    r = torch.from_numpy(router).cuda()
+    with pytest.raises(k2t.K2TError):
+        gpu_ctx.moe_ffn(bank, 1, r, h, h, 1e-6, 2)  # shard layer out of range
+    with pytest.raises(k2t.K2TError):
+        gpu_ctx.moe_ffn(bank, 0, r, h, h, 1e-6, 5)  # top_k > experts
+    with pytest.raises(k2t.K2TError):
+        gpu_ctx.moe_ffn(bank, 0, r, h, h, 1e-6, 2, scoring=7)
+    blob = bytearray(write_k2tm([experts], 128, 64, 3, 2))
+    with pytest.raises(k2t.K2TError):
+        k2t.ExpertBank.upload(gpu_ctx, bytes(blob[:-100]))  # truncated shard
+    bank.close()
+
+
+CFG = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=64, vocab=300,
+           max_seq=32, rms_eps=1e-6, rope_theta=1000000.0)
+
+
+def _attn_layer(rng, cfg):
+    d, nq, nkv, hd = cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    w = lambda r, c: (rng.standard_normal((r, c)) * 0.02).astype(np.float32)  # noqa: E731
+    return {"qkv": quantize_matrix(w((nq + 2 * nkv) * hd, d), "nf4"), "o": quantize_matrix(w(d, nq * hd), "nf4"),
+            "in_norm": (1 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+            "post_norm": (1 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+            "q_norm": (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32),
+            "k_norm": (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32), "bias": None}
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_moe_model_decode_matches_oracle(gpu_ctx, graph):
+    """Qwen3-MoE-shaped toy: q_dim (512) != hidden (256), hd 128, QK-norm, every layer
+    sparse (16 NF3 experts, top 4, softmax + renorm), NF4 attention, tied NF4 head."""
+    print(f"moe model decode graph={graph}", flush=True)
+    cfg = CFG
+    rng = np.random.default_rng(77)
+    d, E, k, dff = cfg["hidden"], 16, 4, 128
+    moe_layers = [random_moe_layer(rng, d, dff, E, bits=3) for _ in range(cfg["n_layers"])]
+    blob = write_k2tm([m[0] for m in moe_layers], d, dff, 3, 2)
+    bank = k2t.ExpertBank.upload(gpu_ctx, blob)
+    layers = []
+    for li in range(cfg["n_layers"]):
+        L = _attn_layer(rng, cfg)
+        L["moe"] = _moe_dict(moe_layers[li][0], moe_layers[li][1], k, True, 0)
+        layers.append(L)
+    head = quantize_matrix((rng.standard_normal((cfg["vocab"], d)) * 0.02).astype(np.float32), "nf4")
+    fn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    ref = OracleModel(cfg, layers, head, fn)
+    gm = k2t.Model(gpu_ctx, cfg, max_batch=4)
+    gm.set_graph(graph)
+    mats = []
+    up = lambda m: gpu_ctx.upload_nf(m.rows, m.cols, 4, m.sgc, m.cb, m.pair, m.tail)  # noqa: E731
+    for li, L in enumerate(layers):
+        q, o = up(L["qkv"]), up(L["o"])
+        mats += [q, o]
+        gm.set_layer(li, q, o, None, None, L["in_norm"], L["post_norm"])
+        gm.set_qk_norm(li, L["q_norm"], L["k_norm"])
+        gm.set_moe(li, bank, li, moe_layers[li][1], k, True, 0)
+    hm = up(head)
+    gm.set_head(hm, fn)
+    assert not gm.persistent_active()
+    toks = np.random.default_rng(8).integers(0, cfg["vocab"], 6)
+    for i, t in enumerate(toks):
+        a, b = gm.decode(int(t)), ref.forward_token(int(t))
+        cos = float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
+        rel = float(np.abs(a - b).max() / np.abs(b).max())
+        assert cos > 0.9999 and rel <= 2e-2, f"step {i}: cos {cos} rel {rel}"
+    # prompt path: MoE runs per token inside a batch
+    gm.reset()
+    ref2 = OracleModel(cfg, layers, head, fn)
+    a = gm.prefill(np.array([3, 250, 17], np.int32))
+    for t in (3, 250, 17):
+        b = ref2.forward_token(t)
+    cos = float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
+    assert cos > 0.9999, f"prefill cos {cos}"
+    gm.close()
+    for m in mats + [hm]:
+        m.close()
+    bank.close()
+
+
+def test_kv_synthetic_sets_position(gpu_ctx):
+    cfg = dict(CFG, n_layers=1)
+    rng = np.random.default_rng(3)
+    L = _attn_layer(rng, cfg)
+    layers, head = [L], quantize_matrix((rng.standard_normal((cfg["vocab"], cfg["hidden"])) * 0.02)
+                                        .astype(np.float32), "nf4")
+    experts, router = random_moe_layer(rng, cfg["hidden"], 64, 8, bits=3)
+    bank = k2t.ExpertBank.upload(gpu_ctx, write_k2tm([experts], cfg["hidden"], 64, 3, 2))
+    gm = k2t.Model(gpu_ctx, cfg, max_batch=2)
+    up = lambda m: gpu_ctx.upload_nf(m.rows, m.cols, 4, m.sgc, m.cb, m.pair, m.tail)  # noqa: E731
+    q, o, hm = up(L["qkv"]), up(L["o"]), up(head)
+    gm.set_layer(0, q, o, None, None, L["in_norm"], L["post_norm"])
+    gm.set_moe(0, bank, 0, router, 2)
+    gm.set_head(hm, np.ones(cfg["hidden"], np.float32))
+    gm.kv_synthetic(20, seed=1)
+    assert gm.position() == 20
+    logits = gm.decode(5)
+    assert np.isfinite(logits).all() and gm.position() == 21
+    with pytest.raises(k2t.K2TError):
+        gm.kv_synthetic(cfg["max_seq"])
+    gm.close()
+    for m in (q, o, hm):
+        m.close()
+    bank.close()

@@ -1,0 +1,91 @@
+"""Sparse-MoE host pieces (no GPU): the .k2tm header / expert layout of the C ABI, and
+the oracle's route_sorted.
+
+Pins:
+  - k2t_k2tm_expert_layout equals nf_expert_byte_layout's closed form for the
+    30B-A3B expert (gate_up 1536x2048, down 2048x768, NF3 g128: 1,228,800 + 614,400 pair
+    bytes, counted by hand from the record layout) and the test writer's layout;
+  - header decoding round-trips the writer's page and rejects bad magic / sizes / bits;
+  - route_sorted against brute force: top-k of distinct scores by argsort, softmax
+    weights from the closed form, renormalized weights summing to 1, ties resolved to
+    the lower expert id, output sorted by id, and the three scoring rules.
+"""
+import numpy as np
+import pytest
+
+import k2t
+from k2tb_writer import K2TM_PAGE, expert_layout, random_moe_layer, write_k2tm
+from model_oracle import SIGMOID, SOFTMAX, TOPK_SOFTMAX, route_sorted
+
+
+def test_expert_layout_30b_shape():
+    L = k2t.k2tm_expert_layout(2048, 768, 3, 2)
+    # gate_up: 48 pairs x (16 scale groups x 64 B + 32 chunks x 2 x 384 B)
+    assert L["gu_pair_bytes"] == 48 * (16 * 64 + 32 * 2 * 384) == 1228800
+    # down: 64 pairs x (6 x 64 + 12 x 2 x 384)
+    assert L["dn_pair_bytes"] == 64 * (6 * 64 + 12 * 2 * 384) == 614400
+    assert L["gu_pair_off"] == 64 and L["gu_codebook_off"] == 0 and L["dn_codebook_off"] == 16
+    assert L["dn_pair_off"] == 64 + 1228800
+    assert L["aligned_expert_bytes"] == ((64 + 1228800 + 614400 + 16383) // 16384) * 16384
+    for args in [(256, 128, 3, 2), (256, 128, 4, 2), (512, 192, 4, 1), (2048, 768, 4, 2)]:
+        a, b = k2t.k2tm_expert_layout(*args), expert_layout(*args)
+        assert (a["gu_pair_bytes"], a["dn_pair_off"], a["dn_pair_bytes"], a["aligned_expert_bytes"]) == \
+               (b["gu_bytes"], b["dn_off"], b["dn_bytes"], b["aligned"])
+
+
+def test_k2tm_header_roundtrip_and_errors():
+    rng = np.random.default_rng(3)
+    layers = [random_moe_layer(rng, 128, 64, 4, bits=3)[0] for _ in range(2)]
+    blob = write_k2tm(layers, 128, 64, 3, 2)
+    h = k2t.k2tm_read_header(blob[:K2TM_PAGE])
+    assert (h["num_layers"], h["experts_per_layer"], h["d_model"], h["d_ff_expert"], h["bits"]) == (2, 4, 128, 64, 3)
+    assert len(blob) == K2TM_PAGE + 2 * 4 * h["aligned_expert_bytes"]
+    bad = bytearray(blob[:K2TM_PAGE])
+    bad[0] = ord("X")
+    with pytest.raises(k2t.K2TError):
+        k2t.k2tm_read_header(bytes(bad))
+    with pytest.raises(k2t.K2TError):
+        k2t.k2tm_read_header(blob[:100])
+    bad = bytearray(blob[:K2TM_PAGE])
+    bad[16 + 5 * 8] ^= 0x40  # aligned_expert_bytes
+    with pytest.raises(k2t.K2TError):
+        k2t.k2tm_read_header(bytes(bad))
+    bad = bytearray(blob[:K2TM_PAGE])
+    bad[16 + 6 * 8] = 5  # NF5 experts
+    with pytest.raises(k2t.K2TError) as ei:
+        k2t.k2tm_read_header(bytes(bad))
+    assert ei.value.code == -4
+
+
+def test_route_sorted_against_brute_force():
+    rng = np.random.default_rng(7)
+    for E, k in [(16, 4), (128, 8), (60, 6)]:
+        z = rng.standard_normal(E).astype(np.float32)
+        r = route_sorted(z, k, True, SOFTMAX)
+        top = sorted(np.argsort(-z.astype(np.float64))[:k].tolist())
+        assert [e for e, _ in r] == top
+        p = np.exp(z.astype(np.float64) - z.max())
+        p /= p.sum()
+        want = p[top] / p[top].sum()
+        assert np.allclose([w for _, w in r], want, rtol=1e-5)
+        assert abs(sum(w for _, w in r) - 1.0) < 1e-5
+        # without renormalization: plain softmax probabilities
+        r2 = route_sorted(z, k, False, SOFTMAX)
+        assert np.allclose([w for _, w in r2], p[top], rtol=1e-5)
+        # topk-softmax: softmax over the k largest logits
+        r3 = route_sorted(z, k, True, TOPK_SOFTMAX)
+        q = np.exp(z[top].astype(np.float64) - z[top].max())
+        assert np.allclose([w for _, w in r3], q / q.sum(), rtol=1e-5)
+        # sigmoid scores, renormalized
+        r4 = route_sorted(z, k, True, SIGMOID)
+        s = 1.0 / (1.0 + np.exp(-z[top].astype(np.float64)))
+        assert np.allclose([w for _, w in r4], s / s.sum(), rtol=1e-5)
+
+
+def test_route_sorted_ties_pick_lower_ids():
+    z = np.array([1.0, 3.0, 3.0, 2.0, 3.0, 0.5], np.float32)
+    r = route_sorted(z, 2, True, SOFTMAX)
+    assert [e for e, _ in r] == [1, 2]
+    assert abs(r[0][1] - 0.5) < 1e-7 and abs(r[1][1] - 0.5) < 1e-7
+    r = route_sorted(z, 4, False, TOPK_SOFTMAX)
+    assert [e for e, _ in r] == [1, 2, 3, 4]
