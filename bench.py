@@ -34,6 +34,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="", help="comma list of GEMV case names to run (profiling)")
     ap.add_argument("--decode-only", action="store_true", help="skip the GEMV sweep and the 135M run (profiling)")
+    ap.add_argument("--moe-only", action="store_true", help="run only the config-5 MoE decode (profiling)")
+    ap.add_argument("--no-moe", action="store_true", help="skip the config-5 MoE decode")
+    ap.add_argument("--moe-context", type=int, default=6600)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="also run 3 plain device copies of MB MiB (HBM counter calibration)")
     return ap.parse_args()
@@ -157,6 +160,102 @@ def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log):
     return model, mats, host, res
 
 
+QWEN3_30B_A3B = dict(n_layers=48, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=128, intermediate=768,
+                     vocab=151936, rms_eps=1e-6, rope_theta=1000000.0)
+MOE_EXPERTS, MOE_TOPK, MOE_FF, MOE_POOL = 128, 8, 768, 16
+
+
+def moe_decode_bench(ctx, torch, steps, warmup, context, log):
+    """Config 5: Qwen3-30B-A3B-shaped sparse-MoE decode at `context` tokens.  NF4g128
+    attention (QK-norm, q_dim 4096 != hidden 2048) and lm_head compiled on the host, an
+    untied bf16 embedding, fp32 routers ~N(0, 0.05) from fixed seeds (reproducible
+    routing), and a .k2tm bank of 48 x 128 NF3 g128 experts (gate_up 1536x2048, down
+    2048x768) in HBM: MOE_POOL experts compiled on the host, their records replicated
+    into all 6144 slots (distinct memory, so every routed expert is read from HBM).
+    The KV cache is filled with seeded synthetic int8 K/V up to `context`."""
+    import k2t
+    cfg = dict(QWEN3_30B_A3B, max_seq=context + warmup + steps + 8)
+    d, nq, nkv, hd, V, L = cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["vocab"], \
+        cfg["n_layers"]
+    t0 = time.perf_counter()
+    lay = k2t.k2tm_expert_layout(d, MOE_FF, 3, 2)
+    rec = lay["aligned_expert_bytes"]
+    pool = np.zeros((MOE_POOL, rec), np.uint8)
+    for j in range(MOE_POOL):
+        Wgu = k2t.synth_normal(SEED + 5000 + 2 * j, 2 * MOE_FF * d, 0.02).reshape(2 * MOE_FF, d)
+        Wdn = k2t.synth_normal(SEED + 5001 + 2 * j, d * MOE_FF, 0.02).reshape(d, MOE_FF)
+        cg, _, pg, _ = k2t.compile_nf4(Wgu, 2, bits=3)
+        cd, _, pd, _ = k2t.compile_nf4(Wdn, 2, bits=3)
+        pool[j, lay["gu_codebook_off"]:lay["gu_codebook_off"] + 16] = cg.view(np.uint8)
+        pool[j, lay["dn_codebook_off"]:lay["dn_codebook_off"] + 16] = cd.view(np.uint8)
+        pool[j, lay["gu_pair_off"]:lay["gu_pair_off"] + pg.size] = pg
+        pool[j, lay["dn_pair_off"]:lay["dn_pair_off"] + pd.size] = pd
+    page = np.zeros(16384, np.uint8)
+    page[:12] = np.frombuffer(b"K2TM800B_V1\0", np.uint8)
+    page[16:16 + 56] = np.array([L, MOE_EXPERTS, d, MOE_FF, 2, rec, 3], np.uint64).view(np.uint8)
+    n_rec = L * MOE_EXPERTS
+    bank_t = torch.empty(16384 + n_rec * rec, dtype=torch.uint8, device="cuda")
+    bank_t[:16384].copy_(torch.from_numpy(page))
+    recs = bank_t[16384:].view(n_rec, rec)
+    pool_d = torch.from_numpy(pool).cuda()
+    for j in range(MOE_POOL):
+        sl = recs[j::MOE_POOL]
+        sl.copy_(pool_d[j].unsqueeze(0).expand(sl.shape[0], rec))
+    del pool_d
+    bank = k2t.ExpertBank.wrap(ctx, bank_t, bank_t.numel(), page)
+    model = k2t.Model(ctx, cfg, max_batch=1)
+    mats = []
+    ones_d, ones_hd = np.ones(d, np.float32), np.ones(hd, np.float32)
+
+    def nf4(rows, cols, seed):
+        W = k2t.synth_normal(seed, rows * cols, 0.02).reshape(rows, cols)
+        cb, _, pair, tail = k2t.compile_nf4(W, 2)
+        m = ctx.upload_nf(rows, cols, 4, 2, cb, pair, tail)
+        mats.append(m)
+        return m
+
+    for li in range(L):
+        q = nf4((nq + 2 * nkv) * hd, d, SEED + 100 * li + 1)
+        o = nf4(d, nq * hd, SEED + 100 * li + 2)
+        model.set_layer(li, q, o, None, None, ones_d, ones_d)
+        model.set_qk_norm(li, ones_hd, ones_hd)
+        router = k2t.synth_normal(SEED + 100 * li + 3, MOE_EXPERTS * d, 0.05).reshape(MOE_EXPERTS, d)
+        model.set_moe(li, bank, li, router, MOE_TOPK, True, k2t.MOE_SOFTMAX)
+    head = nf4(V, d, SEED + 99991)
+    emb = (k2t.synth_normal(SEED + 99992, V * d, 0.02).view(np.uint32) >> 16).astype(np.uint16)
+    model.set_embedding(k2t.EMBED_BF16, emb)
+    del emb
+    model.set_head(head, ones_d)
+    t_build = time.perf_counter() - t0
+    model.kv_synthetic(context, seed=SEED)
+    model.generate(1, warmup, want_tokens=False)  # graph capture + warm-up
+    model.sync()
+    t0 = time.perf_counter()
+    model.generate(1, steps, want_tokens=False)
+    t_dec = time.perf_counter() - t0
+    tok_s = steps / t_dec
+    attn_bytes = sum(m.info()[3] for m in mats if m is not head)
+    expert_bytes = MOE_TOPK * (lay["gu_pair_bytes"] + lay["dn_pair_bytes"] + 32)
+    router_bytes = MOE_EXPERTS * d * 4
+    wbytes = attn_bytes + head.info()[3] + L * (expert_bytes + router_bytes)
+    kv_per_tok = L * nkv * 2 * (hd + 4)
+    ctx_mid = context + warmup + steps / 2
+    res = {"decode_tok_s": round(tok_s, 1), "ms_per_token": round(t_dec / steps * 1e3, 4), "decode_steps": steps,
+           "context_at_decode": [context + warmup, context + warmup + steps],
+           "weight_bytes_per_token": int(wbytes), "kv_bytes_per_token_of_context": kv_per_tok,
+           "resident_expert_bytes": int(n_rec * rec),
+           "decode_GB_s": round((wbytes + kv_per_tok * ctx_mid) * tok_s / 1e9, 1), "build_s": round(t_build, 1)}
+    log(f"# 30B-A3B MoE nf3/nf4g128 @ctx {context}: decode {tok_s:.1f} tok/s ({t_dec / steps * 1e3:.3f} ms/token), "
+        f"{wbytes / 1e6:.1f} MB weights/token")
+    model.close()
+    for m in mats:
+        m.close()
+    bank.close()
+    del bank_t
+    torch.cuda.empty_cache()
+    return res
+
+
 def load_traffic(kernel_case):
     """HBM bytes per launch of the roofline kernel, from the committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a
@@ -226,6 +325,12 @@ def main():
     if os.environ.get("K2T_EXACT"):
         ctx.set_exact(int(os.environ["K2T_EXACT"]))
 
+    if args.moe_only:
+        r30 = moe_decode_bench(ctx, torch, args.steps, args.warmup, args.moe_context, log)
+        print(json.dumps({"metric": "decode tok/s, 30B-A3B-shape MoE", "value": r30["decode_tok_s"],
+                          "unit": "tok/s", "config": r30}))
+        return
+
     # ---- config 4: GEMV sweep
     specs = [("nf4g128_14336x4096", "nf4", 14336, 4096), ("nf4g128_4096x14336", "nf4", 4096, 14336),
              ("b6_14336x4096", "b6", 14336, 4096), ("b6_4096x14336", "b6", 4096, 14336),
@@ -270,6 +375,11 @@ def main():
         return
     m135, mats135, _, r135 = decode_bench(ctx, torch, "135M p55454", k2t.SMOLLM2_135M, "n4", 512, 64, 8, log)
     m135.close()
+    for m in mats135:
+        m.close()
+    torch.cuda.empty_cache()
+    # ---- config 5: 30B-A3B-shaped sparse MoE, decode at context 6600
+    r30 = None if args.no_moe else moe_decode_bench(ctx, torch, 32, 4, args.moe_context, log)
 
     dr = results[dom]
     line.update({
@@ -287,7 +397,8 @@ def main():
                 "random token ids; greedy decode",
         "config": {"workload": "config 3: SmolLM2-1.7B-shaped nf4g128 (24 layers, d 2048, 32 heads MHA, hd 64, "
                                "ffn 8192, vocab 49152), 256-token prefill in 4-token tiles then greedy decode",
-                   "decode_1_7b_nf4g128": r17, "decode_135m_p55454_ctx512": r135, "gemv_sweep": results},
+                   "decode_1_7b_nf4g128": r17, "decode_135m_p55454_ctx512": r135,
+                   "decode_30b_a3b_moe_nf3_ctx6600": r30, "gemv_sweep": results},
         "roofline": {"bound": "hbm", "kernel": f"gemv_kernel ({dom})", "achieved": dr["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dr["GB_s"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom),
                      "algorithmic_bytes_per_launch": dr["bytes"], "avg_launch_us": dr["us"]},

@@ -229,7 +229,8 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
         launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
         if (L.has_moe) {
             // one token at a time: each token has its own routes (forward_layer_single)
-            const MoeWork ws = moe_work_carve(m->moe_ws, L.moe.bank, L.moe.top_k);
+            MoeWork ws = moe_work_carve(m->moe_ws, L.moe.bank, L.moe.top_k);
+            ws.err = m->err_dev;  // timeouts surface through the model's error word
             for (int t = 0; t < ntok; t++) launch_moe_ffn(ctx, L.moe, m->hidden + (size_t)t * d, L.post_norm, c.rms_eps, ws);
         } else if (fused) {
             launch_gemv_fused(ctx, L.gu, K2T_XS_RMSNORM, m->hidden, L.post_norm, c.rms_eps, m->gu, false);
@@ -358,7 +359,8 @@ void check_mk_error(k2t_model *m) {
     hip_check(hipMemcpy(&e, m->err_dev, sizeof(int), hipMemcpyDeviceToHost), "error flag");
     if (e) {
         (void)hipMemset(m->err_dev, 0, sizeof(int));
-        throw Error(K2T_E_INTERNAL, "persistent decode kernel: dependency wait timed out");
+        throw Error(K2T_E_INTERNAL, e == 2 ? "MoE route selection: router wait timed out"
+                                           : "persistent decode kernel: dependency wait timed out");
     }
 }
 
@@ -592,6 +594,8 @@ int32_t k2t_model_set_moe(k2t_model *m, int32_t layer, const k2t_experts *bank, 
         if (need > m->moe_ws_floats) {
             m->moe_ws = (float *)dalloc(m, need * sizeof(float));
             m->moe_ws_floats = need;
+            // the route hand-off words and the call counter start at epoch 0
+            hip_check(hipMemset(m->moe_ws, 0, need * sizeof(float)), "moe workspace clear");
         }
         L.moe = MoeLayer{bank, shard_layer, rw, rb, top_k, norm_topk_prob ? 1 : 0, scoring};
         L.has_moe = true;

@@ -136,7 +136,25 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     __shared__ float sc[kAttnSplitLen];
     __shared__ float red[8];
     __shared__ float opart[16][64];  // [position subset][column], 16*64 == 8*128
-    const int head = blockIdx.x, split = blockIdx.y, tok = blockIdx.z;
+    // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs by linear id,
+    // so the q heads that share a KV head and a split get ids congruent mod 8 and run on
+    // one XCD, where the K/V tile is fetched from HBM once and then hit in that XCD's L2.
+    const int tok = blockIdx.z;
+    int head, split;
+    {
+        const int lin = (int)blockIdx.x + (int)blockIdx.y * (int)gridDim.x;  // < nq * nsplit
+        const int grp = nq / nkv, units = nkv * nsplit;                    // (kv head, split) tiles
+        const int xcd = lin & 7, r = lin >> 3;
+        const int nx = (units + 7) >> 3;  // tiles per XCD lane (the last XCDs may hold fewer)
+        const int member = r / nx, ti = xcd + 8 * (r % nx);
+        if ((nq * nsplit) % 8 == 0 && units % 8 == 0 && ti < units && member < grp) {
+            head = (ti / nsplit) * grp + member;
+            split = ti % nsplit;
+        } else {
+            head = (int)blockIdx.x;
+            split = (int)blockIdx.y;
+        }
+    }
     const int seq = pos_dev[0] + tok + 1;
     const int t0 = split * kAttnSplitLen, t1 = min(seq, t0 + kAttnSplitLen);
     float *pp = part + ((size_t)(tok * nq + head) * nsplit + split) * (2 + hd);
@@ -266,16 +284,36 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
     const int seq = pos_dev[0] + tok + 1;
     const int ns = min(nsplit, (seq + kAttnSplitLen - 1) / kAttnSplitLen);
     const float *pp = part + (size_t)(tok * nq + head) * nsplit * (2 + hd);
+    // Split maxima and sums one split per lane (loads in flight together), then the
+    // rescaled sums in split order.
     float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, pp[(size_t)s * (2 + hd)]);
+    for (int s = (int)lane; s < ns; s += 64) M = fmaxf(M, pp[(size_t)s * (2 + hd)]);
+    M = wave_max_f(M);
     float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
     const int nb = hd / 64;
-    for (int s = 0; s < ns; s++) {
-        const float *ps = pp + (size_t)s * (2 + hd);
-        const float e = expf(ps[0] - M);
-        L = fmaf(ps[1], e, L);
-        o0 = fmaf(ps[2 + lane], e, o0);
-        if (nb > 1) o1 = fmaf(ps[2 + 64 + lane], e, o1);
+    for (int s0 = 0; s0 < ns; s0 += 64) {
+        const int s = s0 + (int)lane;
+        const float em = s < ns ? expf(pp[(size_t)s * (2 + hd)] - M) : 0.0f;
+        const float lm = s < ns ? pp[(size_t)s * (2 + hd) + 1] : 0.0f;
+        const int cnt = min(64, ns - s0);
+        for (int j0 = 0; j0 < cnt; j0 += 8) {
+            float v0[8], v1[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float *ps = pp + (size_t)(s0 + j0 + u) * (2 + hd);
+                const bool ok = j0 + u < cnt;
+                v0[u] = ok ? ps[2 + lane] : 0.0f;
+                v1[u] = ok && nb > 1 ? ps[2 + 64 + lane] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (j0 + u >= cnt) break;
+                const float e = __shfl(em, j0 + u, kWave);
+                L = fmaf(__shfl(lm, j0 + u, kWave), e, L);
+                o0 = fmaf(v0[u], e, o0);
+                o1 = fmaf(v1[u], e, o1);
+            }
+        }
     }
     const float inv = 1.0f / L;
     o0 = ifwht_lane(o0 * inv, 0, lane);

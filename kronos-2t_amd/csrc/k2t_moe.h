@@ -39,12 +39,17 @@ struct MoeLayer {
 struct MoeWork {
     float *gu;      // [top_k][2*d_ff] gate_up outputs, [gate64, up64] blocks
     float *eo;      // [top_k][d_model] expert outputs
-    float *logits;  // [E]
-    float *wts;     // [top_k]
-    int *ids;       // [top_k]
+    unsigned long long *words;  // [E] router logits as {epoch, value} words
+    float *wts;                 // [top_k]
+    int *ids;                   // [top_k]
+    uint32_t *ctr;              // route-call counter (epoch source)
+    int *err;                   // raised when the route wait times out
 };
 
+// Workspace size; the words and the counter must start zeroed (model: at allocation;
+// the standalone entry point: launch_moe_clear before each call).
 size_t moe_work_floats(const k2t_experts *b, int top_k);
+void launch_moe_clear(hipStream_t st, const MoeWork &ws, int E);
 MoeWork moe_work_carve(float *base, const k2t_experts *b, int top_k);
 void check_moe_args(const k2t_experts *bank, int shard_layer, int top_k, int scoring);
 

@@ -3,10 +3,10 @@
 //
 // Every expert of every layer stays resident (a 30B-A3B shard is ~11 GB of the 288 GB),
 // so there is no paging.  Per token and MoE layer:
-//   1. moe_router_kernel   x_norm = RMSNorm(hidden) * post_norm, logits = W_router x_norm
-//                          (+ bias), one wave per expert;
-//   2. moe_select_kernel   softmax / topk-softmax / sigmoid, top-k, renormalize, sort by
-//                          expert id (route_sorted, sparse_moe.rs:86-182), one wave;
+//   1. moe_route_kernel    x_norm = RMSNorm(hidden) * post_norm, logits = W_router x_norm
+//                          (+ bias), one wave per expert; then, in the same launch,
+//                          softmax / topk-softmax / sigmoid, top-k, renormalize, sort by
+//                          expert id (route_sorted, sparse_moe.rs:86-182) on one wave;
 //   3. grouped gate_up GEMV: slot z streams expert route[z]'s gate_up pairs with the int8
 //      activation of x_norm built in LDS (populate_fwht of x_norm); rows are written in
 //      [gate64, up64] blocks;
@@ -109,43 +109,6 @@ static k2t_experts *make_bank(k2t_ctx *ctx, const k2t_k2tm_header &h) {
 }
 
 // ---------------------------------------------------------------- kernels
-// Router logits: each wave owns one expert row; x_norm = (x * inv_rms) * w is formed on
-// the fly (rms_norm, real_llm.rs:9858-9898; the sum of squares in the order of the GEMV's
-// fused builder, so x_norm matches the expert activations' source), dot as in
-// dot_f32_moe (sparse_moe.rs:1644-1655) with a tree reduction.
-__global__ __launch_bounds__(256) void moe_router_kernel(const float *__restrict__ x, const float *__restrict__ nw,
-                                                         float eps, int d, const float *__restrict__ W,
-                                                         const float *__restrict__ bias, int E,
-                                                         float *__restrict__ logits) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const int e = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-    if (e >= E) return;
-    const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    const float4 *w4 = reinterpret_cast<const float4 *>(nw);
-    const float4 *r4 = reinterpret_cast<const float4 *>(W + (size_t)e * d);
-    const int n4 = d / 4;
-    float ss = 0.0f;
-    for (int i = (int)lane; i < n4; i += 64) {
-        const float4 v = x4[i];
-        ss = fmaf(v.x, v.x, ss);
-        ss = fmaf(v.y, v.y, ss);
-        ss = fmaf(v.z, v.z, ss);
-        ss = fmaf(v.w, v.w, ss);
-    }
-    ss = wave_sum_f(ss);
-    const float inv_rms = 1.0f / sqrtf(ss / (float)d + eps);
-    float acc = 0.0f;
-    for (int i = (int)lane; i < n4; i += 64) {
-        const float4 v = x4[i], w = w4[i], r = r4[i];
-        acc = fmaf((v.x * inv_rms) * w.x, r.x, acc);
-        acc = fmaf((v.y * inv_rms) * w.y, r.y, acc);
-        acc = fmaf((v.z * inv_rms) * w.z, r.z, acc);
-        acc = fmaf((v.w * inv_rms) * w.w, r.w, acc);
-    }
-    acc = wave_sum_f(acc);
-    if (lane == 0) logits[e] = bias ? acc + bias[e] : acc;
-}
-
 // Largest (value, lowest index on ties) over the wave; returns the lane's view of it.
 __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 #pragma unroll
@@ -162,16 +125,12 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 // route_sorted (sparse_moe.rs:86-182) for E <= 256 experts on one wave.  Top-k picks the
 // largest score with the lowest id among equals, the order select_topk_by_score's strict
 // comparisons give; the top-k sums run in selection order like the reference's loops.
-__global__ __launch_bounds__(64) void moe_select_kernel(const float *__restrict__ logits, int E, int k, int norm_topk,
-                                                        int scoring, int *__restrict__ ids, float *__restrict__ wts) {
-    const int lane = (int)threadIdx.x;
-    float sc[4];
+// sc[j] holds the logit of expert lane + 64 j (-inf past E) on entry.
+__device__ void select_routes(float sc[4], int lane, int E, int k, int norm_topk, int scoring, int *__restrict__ ids,
+                              float *__restrict__ wts) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int e = lane + 64 * j;
-        sc[j] = e < E ? logits[e] : -INFINITY;
+    for (int j = 0; j < 4; j++)
         if (sc[j] != sc[j]) sc[j] = -INFINITY;  // NaN never wins a comparison: rank it last
-    }
     if (scoring == K2T_MOE_SOFTMAX) {
         float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         m = wave_max_f(m);
@@ -190,8 +149,9 @@ __global__ __launch_bounds__(64) void moe_select_kernel(const float *__restrict_
         for (int j = 0; j < 4; j++)
             sc[j] = lane + 64 * j < E && sc[j] == sc[j] ? 1.0f / (1.0f + expf(-sc[j])) : -INFINITY;
     }
-    int sel_id[K2T_MOE_MAX_TOPK];
-    float sel_w[K2T_MOE_MAX_TOPK];
+    // Selection round r leaves its (id, score) in lane r's registers.
+    int my_id = 0;
+    float my_w = 0.0f;
     for (int r = 0; r < k; r++) {
         float bv = sc[0];
         int bi = lane;
@@ -203,47 +163,143 @@ __global__ __launch_bounds__(64) void moe_select_kernel(const float *__restrict_
             }
         wave_argmax(bv, bi);
         bi = min(bi, E - 1);  // every id indexes a record of the bank, whatever the scores
-        sel_id[r] = bi;
-        sel_w[r] = bv;
+        if (lane == r) {
+            my_id = bi;
+            my_w = bv;
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++)
             if (lane + 64 * j == bi) sc[j] = -INFINITY;
     }
-    if (lane != 0) return;
+    // Weight normalization; the sums run over the selections in selection order.
     if (scoring == K2T_MOE_TOPK_SOFTMAX) {
-        const float mz = sel_w[0];
+        const float mz = __shfl(my_w, 0, kWave);
+        const float ex = lane < k ? expf(my_w - mz) : 0.0f;
         float s = 0.0f;
-        for (int r = 0; r < k; r++) {
-            sel_w[r] = expf(sel_w[r] - mz);
-            s += sel_w[r];
-        }
+        for (int r = 0; r < k; r++) s += __shfl(ex, r, kWave);
         const float inv = s > 0.0f ? 1.0f / s : 1.0f / (float)k;
-        for (int r = 0; r < k; r++) sel_w[r] *= inv;
+        my_w = ex * inv;
     } else if (norm_topk) {
         float s = 0.0f;
-        for (int r = 0; r < k; r++) s += sel_w[r];
-        if (s > 0.0f) {
-            const float inv = 1.0f / s;
-            for (int r = 0; r < k; r++) sel_w[r] *= inv;
-        }
+        for (int r = 0; r < k; r++) s += __shfl(my_w, r, kWave);
+        if (s > 0.0f) my_w *= 1.0f / s;
     }
-    // insertion sort by ascending expert id (sparse_moe.rs:170-179)
-    for (int i = 1; i < k; i++) {
-        const int ci = sel_id[i];
-        const float cw = sel_w[i];
-        int j = i;
-        while (j > 0 && sel_id[j - 1] > ci) {
-            sel_id[j] = sel_id[j - 1];
-            sel_w[j] = sel_w[j - 1];
-            j--;
-        }
-        sel_id[j] = ci;
-        sel_w[j] = cw;
-    }
+    // Ascending expert id (sparse_moe.rs:170-179): lane r's rank among the k selections
+    // (ids are distinct, ties in id order are impossible).
+    int rank = 0;
     for (int r = 0; r < k; r++) {
-        ids[r] = sel_id[r];
-        wts[r] = sel_w[r];
+        const int other = __shfl(my_id, r, kWave);
+        rank += (r != lane && other < my_id) ? 1 : 0;
     }
+    if (lane < k) {
+        ids[rank] = my_id;
+        wts[rank] = my_w;
+    }
+}
+
+// Router logits: each wave owns one expert row; x_norm = (x * inv_rms) * w is formed on
+// the fly (rms_norm, real_llm.rs:9858-9898; the sum of squares in the order of the GEMV's
+// fused builder, so x_norm matches the expert activations' source), dot as in
+// dot_f32_moe (sparse_moe.rs:1644-1655) with a tree reduction.
+//
+// The same launch also selects the routes: every logit is published as one 64-bit word
+// {epoch, value} (a single agent-scope atomic store, so the value and its ready mark
+// arrive together, with no fence), and wave 0 of workgroup 0 waits for all E words of
+// this call's epoch, then runs the selection.  The epoch is the call counter *ctr + 1;
+// workgroup 0 advances the counter after its wait, when every workgroup has read it.
+// The wait is bounded: on timeout it raises *err and still writes in-range ids.
+__device__ __forceinline__ void word_store(unsigned long long *p, uint32_t v, uint32_t epoch) {
+    __hip_atomic_store(p, ((unsigned long long)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long word_load(const unsigned long long *p) {
+    return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NJ>  // float4 per lane of each vector: d <= 256 * NJ
+__global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ x, const float *__restrict__ nw,
+                                                        float eps, int d, const float *__restrict__ W,
+                                                        const float *__restrict__ bias, int E, int k, int norm_topk,
+                                                        int scoring, unsigned long long *__restrict__ words,
+                                                        uint32_t *__restrict__ ctr, int *__restrict__ err,
+                                                        uint32_t spin_limit, int *__restrict__ ids,
+                                                        float *__restrict__ wts) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const int wave = (int)(threadIdx.x >> 6);
+    const int e = (int)blockIdx.x * 4 + wave;
+    const uint32_t epoch = *ctr + 1u;
+    if (e < E) {
+    // All loads of the wave first (NJ float4 of each vector per lane).
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const float4 *w4 = reinterpret_cast<const float4 *>(nw);
+    const float4 *r4 = reinterpret_cast<const float4 *>(W + (size_t)e * d);
+    const int n4 = d / 4;
+    float4 xv[NJ], wv[NJ], rv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int i = (int)lane + 64 * j;
+        const bool ok = i < n4;
+        xv[j] = ok ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        wv[j] = ok ? w4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        rv[j] = ok ? r4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        ss = fmaf(xv[j].x, xv[j].x, ss);
+        ss = fmaf(xv[j].y, xv[j].y, ss);
+        ss = fmaf(xv[j].z, xv[j].z, ss);
+        ss = fmaf(xv[j].w, xv[j].w, ss);
+    }
+    ss = wave_sum_f(ss);
+    const float inv_rms = 1.0f / sqrtf(ss / (float)d + eps);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        acc = fmaf((xv[j].x * inv_rms) * wv[j].x, rv[j].x, acc);
+        acc = fmaf((xv[j].y * inv_rms) * wv[j].y, rv[j].y, acc);
+        acc = fmaf((xv[j].z * inv_rms) * wv[j].z, rv[j].z, acc);
+        acc = fmaf((xv[j].w * inv_rms) * wv[j].w, rv[j].w, acc);
+    }
+    acc = wave_sum_f(acc);
+    if (lane == 0) word_store(words + e, __float_as_uint(bias ? acc + bias[e] : acc), epoch);
+    }
+    if (blockIdx.x != 0 || wave != 0) return;
+    float sc[4];
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int ee = (int)lane + 64 * j;
+        sc[j] = -INFINITY;
+        if (ee >= E) continue;
+        unsigned long long w = word_load(words + ee);
+        for (uint32_t spins = 0; ok && (uint32_t)(w >> 32) != epoch; spins++) {
+            if (spins > spin_limit) {
+                ok = false;
+                __hip_atomic_store(err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            w = word_load(words + ee);
+        }
+        if (ok) sc[j] = __uint_as_float((uint32_t)w);
+    }
+    select_routes(sc, (int)lane, E, k, norm_topk, scoring, ids, wts);
+    if (lane == 0) *ctr = epoch;
+}
+
+// Clears the hand-off words and the call counter of a fresh workspace (a kernel, so that a
+// captured graph holds no memset node).
+__global__ void moe_clear_kernel(unsigned long long *words, int E, uint32_t *ctr, int *err) {
+    for (int i = (int)threadIdx.x; i < E; i += (int)blockDim.x) words[i] = 0ull;
+    if (threadIdx.x == 0) {
+        *ctr = 0u;
+        *err = 0;
+    }
+}
+
+void launch_moe_clear(hipStream_t st, const MoeWork &ws, int E) {
+    hipLaunchKernelGGL(moe_clear_kernel, dim3(1), dim3(256), 0, st, ws.words, E, ws.ctr, ws.err);
+    hip_check(hipGetLastError(), "moe clear launch");
 }
 
 // out.fill(0); out += w_z * expert_z in route order; hidden += out
@@ -262,12 +318,19 @@ void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float 
     const k2t_experts *b = L.bank;
     const int d = (int)b->hdr.d_model, dff = (int)b->hdr.d_ff_expert, E = (int)b->hdr.experts_per_layer;
     hipStream_t st = ctx->stream;
-    hipLaunchKernelGGL(moe_router_kernel, dim3((E + 3) / 4), dim3(256), 0, st, hidden, post_norm, eps, d, L.router_w,
-                       L.router_b, E, ws.logits);
-    hip_check(hipGetLastError(), "moe router launch");
-    hipLaunchKernelGGL(moe_select_kernel, dim3(1), dim3(64), 0, st, ws.logits, E, L.top_k, L.norm_topk, L.scoring,
-                       ws.ids, ws.wts);
-    hip_check(hipGetLastError(), "moe select launch");
+    if (d <= 1024)
+        hipLaunchKernelGGL(moe_route_kernel<4>, dim3((E + 3) / 4), dim3(256), 0, st, hidden, post_norm, eps, d,
+                           L.router_w, L.router_b, E, L.top_k, L.norm_topk, L.scoring, ws.words, ws.ctr, ws.err,
+                           1u << 22, ws.ids, ws.wts);
+    else if (d <= 2048)
+        hipLaunchKernelGGL(moe_route_kernel<8>, dim3((E + 3) / 4), dim3(256), 0, st, hidden, post_norm, eps, d,
+                           L.router_w, L.router_b, E, L.top_k, L.norm_topk, L.scoring, ws.words, ws.ctr, ws.err,
+                           1u << 22, ws.ids, ws.wts);
+    else
+        hipLaunchKernelGGL(moe_route_kernel<16>, dim3((E + 3) / 4), dim3(256), 0, st, hidden, post_norm, eps, d,
+                           L.router_w, L.router_b, E, L.top_k, L.norm_topk, L.scoring, ws.words, ws.ctr, ws.err,
+                           1u << 22, ws.ids, ws.wts);
+    hip_check(hipGetLastError(), "moe route launch");
     const uint8_t *layer_base = b->d_bytes + kK2tmPage + (size_t)L.shard_layer * E * b->lay.aligned_bytes;
     GemvGroup g{};
     g.route = ws.ids;
@@ -293,22 +356,25 @@ void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float 
 
 size_t moe_work_floats(const k2t_experts *b, int top_k) {
     const size_t d = (size_t)b->hdr.d_model, dff = (size_t)b->hdr.d_ff_expert, E = (size_t)b->hdr.experts_per_layer;
-    return E + 2 * (size_t)top_k + (size_t)top_k * 2 * dff + (size_t)top_k * d + 64;
+    return (size_t)top_k * 2 * dff + (size_t)top_k * d + 2 * E + 2 * (size_t)top_k + 64;
 }
 
 MoeWork moe_work_carve(float *base, const k2t_experts *b, int top_k) {
     const size_t d = (size_t)b->hdr.d_model, dff = (size_t)b->hdr.d_ff_expert, E = (size_t)b->hdr.experts_per_layer;
     MoeWork w;
-    float *p = base;
-    w.gu = p;  // 16-byte aligned first
+    float *p = base;  // 256-byte aligned; every region below is a multiple of 64 floats
+    w.gu = p;
     p += (size_t)top_k * 2 * dff;
     w.eo = p;
     p += (size_t)top_k * d;
-    w.logits = p;
-    p += E;
+    w.words = reinterpret_cast<unsigned long long *>(p);
+    p += 2 * E;
     w.wts = p;
     p += top_k;
     w.ids = reinterpret_cast<int *>(p);
+    p += top_k;
+    w.ctr = reinterpret_cast<uint32_t *>(p);
+    w.err = reinterpret_cast<int *>(p + 1);
     return w;
 }
 
@@ -320,6 +386,7 @@ void check_moe_args(const k2t_experts *bank, int shard_layer, int top_k, int sco
     if (bank->hdr.experts_per_layer > 256) throw Error(K2T_E_ARG, "at most 256 experts per layer");
     if (scoring != K2T_MOE_SOFTMAX && scoring != K2T_MOE_TOPK_SOFTMAX && scoring != K2T_MOE_SIGMOID)
         throw Error(K2T_E_ARG, "unknown router scoring");
+    if (bank->hdr.d_model > 4096) throw Error(K2T_E_ARG, "MoE router: d_model above 4096");
     if ((size_t)bank->hdr.d_model > (size_t)kSignBlocks * 64 || (size_t)bank->hdr.d_ff_expert > (size_t)kSignBlocks * 64)
         throw Error(K2T_E_ARG, "expert dimensions exceed the Hadamard sign table");
 }
@@ -442,6 +509,7 @@ int32_t k2t_moe_ffn(k2t_ctx *ctx, const k2t_experts *bank, int32_t shard_layer, 
         MoeLayer L{bank, shard_layer, d_router_w, d_router_bias, top_k, norm_topk_prob ? 1 : 0, scoring};
         ensure_scratch(ctx, moe_work_floats(bank, top_k));
         const MoeWork ws = moe_work_carve(ctx->scratch, bank, top_k);
+        launch_moe_clear(ctx->stream, ws, (int)bank->hdr.experts_per_layer);  // the scratch is shared
         launch_moe_ffn(ctx, L, d_hidden, d_post_norm, eps, ws);
         if (d_route_ids)
             hip_check(hipMemcpyAsync(d_route_ids, ws.ids, (size_t)top_k * sizeof(int), hipMemcpyDeviceToDevice,

@@ -90,6 +90,29 @@ def test_long_context_splits(gpu_ctx):
     assert ok, info
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_gqa_long_context_xcd_order(gpu_ctx, hd):
+    """GQA (8 q heads over 2 KV heads) with max_seq 1024: 2 KV heads x 4 splits = 8 (KV head,
+    split) tiles, so the partial-attention workgroups take the XCD-grouped order (the q
+    heads of one KV head on one XCD); 300 positions fill two splits.  Decode logits vs
+    the oracle."""
+    print(f"gqa long context hd={hd}", flush=True)
+    cfg = dict(n_layers=1, hidden=8 * hd, n_heads=8, n_kv_heads=2, head_dim=hd, intermediate=256, vocab=200,
+               max_seq=1024, rms_eps=1e-5, rope_theta=10000.0)
+    layers, head, fn = random_model(cfg, seed=11, fmt="nf4")
+    ref = OracleModel(cfg, layers, head, fn)
+    gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
+    rng = np.random.default_rng(12)
+    toks = rng.integers(0, cfg["vocab"], 300)
+    gm.prefill(toks[:-2], want_logits=False)
+    for t in toks[:-2]:
+        ref.forward_token(int(t))
+    for t in toks[-2:]:
+        a, b = gm.decode(int(t)), ref.forward_token(int(t))
+        ok, info = _close(a, b)
+        assert ok, info
+
+
 def test_prefill_equals_token_by_token_and_graph_equals_eager(gpu_ctx):
     """Batched prefill and token-by-token decode on the one-kernel-per-operation path run
     the same arithmetic (bit-exact); the persistent kernel sums attention and GEMV
