@@ -240,6 +240,15 @@ int32_t k2t_model_set_qk_norm(k2t_model *m, int32_t layer, const float *q_norm, 
 int32_t k2t_model_set_moe(k2t_model *m, int32_t layer, const k2t_experts *bank, int32_t shard_layer,
                           const float *router_w, const float *router_bias, int32_t top_k, int32_t norm_topk_prob,
                           int32_t scoring);
+/* set_kv_sliding_window (real_llm.rs:1764-1790): an O(1) sliding-window + attention-sink
+ * ring for the int8 KV cache (QuantizedKvCache::new_with_opts, real_llm.rs:1235-1257).
+ * window >= 8 with window + 512 < max_seq enables it: sinks = min(sink_tokens, window/2),
+ * ring = window - sinks + 512 slots; attention then covers the sinks and the last
+ * window - sinks positions (active_kv_pos, real_llm.rs:8596-8612).  Any other window
+ * (0 included) restores the full causal cache.  Resets the position to 0. */
+int32_t k2t_model_set_kv_window(k2t_model *m, int32_t window, int32_t sink_tokens);
+/* Active (window, sinks); (0, 0) for the full cache. */
+int32_t k2t_model_kv_window(const k2t_model *m, int32_t *window, int32_t *sink_tokens);
 /* Benchmark support (no reference counterpart): fills cache positions [0, n_pos) of every
  * layer with seeded pseudo-random int8 K/V and positive scales and sets the position to
  * n_pos, so a decode step runs at that context without a prefill. */

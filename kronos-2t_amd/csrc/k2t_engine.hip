@@ -22,9 +22,9 @@ void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float ep
                         float *s, int32_t *sums);
 void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
                      const float *rope, const int *pos_dev, int nq,
-                     int nkv, int hd, int ntok, int layer, int cap, int8_t *kq, int8_t *vq, float *ks, float *vs);
+                     int nkv, int hd, int ntok, int layer, KvRing kr, int8_t *kq, int8_t *vq, float *ks, float *vs);
 void launch_attention(hipStream_t st, const float *q, int q_stride, const int8_t *kq, const int8_t *vq, const float *ks,
-                      const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd, int cap, float attn_scale,
+                      const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr, float attn_scale,
                       int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum);
 int attn_max_splits(int max_seq);
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums);
@@ -118,6 +118,7 @@ struct k2t_model {
     void *embed_rows = nullptr;          // f32 / bf16 rows [vocab][hidden] (device)
     const k2t_mat *embed_mat = nullptr;  // NF4 embedding matrix
     std::vector<k2t_mat *> owned;        // matrices the model destroys (k2tb loader)
+    KvRing ring{};                       // KV slots: cap = max_seq, or a sliding-window ring
     float *moe_ws = nullptr;             // MoE workspace (largest layer's need)
     size_t moe_ws_floats = 0;
     float *rope = nullptr;  // [max_seq][hd] = cos | sin halves
@@ -206,7 +207,7 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
     k2t_ctx *ctx = m->ctx;
     const int hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, d = c.hidden, inter = c.intermediate;
     const float attn_scale = 1.0f / sqrtf((float)hd);
-    const int nsplit = attn_max_splits(c.max_seq);
+    const int nsplit = attn_max_splits(m->ring.window > 0 ? std::min(c.max_seq, m->ring.window) : c.max_seq);
     if (m->embed_kind == K2T_EMBED_F32 || m->embed_kind == K2T_EMBED_BF16)
         launch_embed_rows(st, m->embed_rows, m->embed_kind == K2T_EMBED_BF16, m->tokens, ntok, c.hidden, m->hidden);
     else
@@ -223,9 +224,9 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
             launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false);
         }
         launch_qkv_post(st, m->qkv, L.bias, L.q_norm, L.k_norm, c.rms_eps, m->rope, m->pos_dev, nq, nkv, hd, ntok, l,
-                        c.max_seq, m->kq, m->vq, m->ks, m->vs);
+                        m->ring, m->kq, m->vq, m->ks, m->vs);
         launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, m->pos_dev, l, nq, nkv, hd,
-                         c.max_seq, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum);
+                         m->ring, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum);
         launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
         if (L.has_moe) {
             // one token at a time: each token has its own routes (forward_layer_single)
@@ -287,6 +288,7 @@ bool mk_format(const k2t_model *m, int &fmt, int &hp) {
 
 bool use_persistent(const k2t_model *m) {
     int fmt, hp;
+    if (m->ring.window > 0) return false;  // the sliding-window ring runs on the per-operation path
     for (const auto &L : m->layers)
         if (L.has_moe || L.q_norm || L.k_norm) return false;  // these run on the per-operation path
     return m->persistent && m->mk_ok && !m->exact && mk_format(m, fmt, hp);
@@ -422,6 +424,7 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
         try {
             m->ctx = ctx;
             m->cfg = c;
+            m->ring = KvRing{c.max_seq, 0, 0, 0};
             m->max_batch = max_batch;
             m->layers.resize(c.n_layers);
             hip_check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "stream create");
@@ -655,6 +658,41 @@ int32_t k2t_model_set_exact(k2t_model *m, int32_t exact) {
     });
 }
 
+int32_t k2t_model_set_kv_window(k2t_model *m, int32_t window, int32_t sink_tokens) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        arg(window >= 0 && sink_tokens >= 0, "window and sink_tokens must be >= 0");
+        const k2t_model_config &c = m->cfg;
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        hip_check(hipStreamSynchronize(m->stream), "sync");
+        // QuantizedKvCache::new_with_opts (real_llm.rs:1235-1257): a window of at least 8
+        // that leaves room for the ring's 512-slot batch slack; otherwise the full cache.
+        constexpr int kRingSlack = 512;
+        if (window >= 8 && window + kRingSlack < c.max_seq) {
+            const int s = std::min(sink_tokens, window / 2);
+            const int rl = (window - s) + kRingSlack;
+            m->ring = KvRing{s + rl, window, s, rl};
+        } else {
+            m->ring = KvRing{c.max_seq, 0, 0, 0};
+        }
+        // set_kv_sliding_window starts a new context (real_llm.rs:1764-1790)
+        hip_check(hipMemset(m->pos_dev, 0, sizeof(int)), "pos reset");
+        m->pos = 0;
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+    });
+}
+
+int32_t k2t_model_kv_window(const k2t_model *m, int32_t *window, int32_t *sink_tokens) {
+    return mguard([&] {
+        arg(m && window && sink_tokens, "NULL argument");
+        *window = m->ring.window;
+        *sink_tokens = m->ring.sinks;
+    });
+}
+
 int32_t k2t_model_kv_synthetic(k2t_model *m, int32_t n_pos, uint64_t seed) {
     return mguard([&] {
         arg(m != nullptr, "model is NULL");
@@ -662,8 +700,8 @@ int32_t k2t_model_kv_synthetic(k2t_model *m, int32_t n_pos, uint64_t seed) {
         const k2t_model_config &c = m->cfg;
         hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
         hip_check(hipStreamSynchronize(m->stream), "sync");
-        launch_kv_synthetic(m->stream, m->kq, m->vq, m->ks, m->vs, c.n_layers * c.n_kv_heads, c.max_seq, n_pos,
-                            c.head_dim, seed);
+        launch_kv_synthetic(m->stream, m->kq, m->vq, m->ks, m->vs, c.n_layers * c.n_kv_heads, m->ring.cap,
+                            std::min(n_pos, m->ring.cap), c.head_dim, seed);
         hip_check(hipMemcpyAsync(m->pos_dev, &n_pos, sizeof(int), hipMemcpyHostToDevice, m->stream), "pos set");
         hip_check(hipStreamSynchronize(m->stream), "sync");
         m->pos = n_pos;

@@ -90,6 +90,13 @@ struct GemvGroup {
 void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, int xs_mode, const float *src,
                          const float *w, float eps, float *out);
 
+// KV cache geometry (QuantKvRawPtrs, real_llm.rs:1096-1122): `cap` slots per (layer, KV
+// head); with a sliding window (window > 0), positions below `sinks` keep their own slot
+// and later ones wrap in a ring of `ring` slots.
+struct KvRing {
+    int cap, window, sinks, ring;
+};
+
 // The model takes ownership of `mat` (destroyed with the model).
 void model_adopt(k2t_model *m, k2t_mat *mat);
 

@@ -15,6 +15,20 @@
 
 namespace k2t {
 
+// slot_of_pos (real_llm.rs:1116-1122)
+__device__ __forceinline__ int ring_slot(const KvRing &r, int pos) {
+    return (r.ring == 0 || pos < r.sinks) ? pos : r.sinks + (pos - r.sinks) % r.ring;
+}
+// active_kv_len / active_kv_pos (real_llm.rs:8596-8612): the sinks, then the last
+// window - sinks positions, once the sequence is longer than the window.
+__device__ __forceinline__ int active_len(const KvRing &r, int seq) {
+    return (r.window > 0 && seq > r.window) ? r.window : seq;
+}
+__device__ __forceinline__ int active_pos(const KvRing &r, int idx, int seq) {
+    return (r.window > 0 && seq > r.window && idx >= r.sinks) ? (seq - (r.window - r.sinks)) + (idx - r.sinks) : idx;
+}
+
+
 // ---------------------------------------------------------------- RMSNorm + FWHT + int8
 // One wave per (chunk, token): every wave recomputes inv_rms = 1/sqrt(mean(x^2) + eps)
 // (real_llm.rs:6929) from the whole row (L2-resident, a few KB) in a fixed order, then
@@ -47,7 +61,7 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, c
                                                       const float *__restrict__ qn, const float *__restrict__ kn,
                                                       float eps, const float *__restrict__ rope,
                                                       const int *__restrict__ pos_dev, int nq, int nkv, int hd,
-                                                      int row_stride, int layer, int cap, int8_t *__restrict__ kq,
+                                                      int row_stride, int layer, KvRing kr, int8_t *__restrict__ kq,
                                                       int8_t *__restrict__ vq, float *__restrict__ ks,
                                                       float *__restrict__ vs) {
     const uint32_t lane = threadIdx.x;
@@ -92,7 +106,7 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, c
     }
     const bool is_k = head < nq + nkv;
     const int kvh = is_k ? head - nq : head - nq - nkv;
-    const size_t slot = ((size_t)layer * nkv + kvh) * cap + pos;
+    const size_t slot = ((size_t)layer * nkv + kvh) * kr.cap + ring_slot(kr, pos);
     const float r0 = fwht_lane(v0, 0, lane);
     const float r1 = nb > 1 ? fwht_lane(v1, 1, lane) : 0.0f;
     const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
@@ -111,10 +125,10 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, c
 }
 
 void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
-                     const float *rope, const int *pos_dev, int nq, int nkv, int hd, int ntok, int layer, int cap,
+                     const float *rope, const int *pos_dev, int nq, int nkv, int hd, int ntok, int layer, KvRing kr,
                      int8_t *kq, int8_t *vq, float *ks, float *vs) {
     hipLaunchKernelGGL(qkv_post_kernel, dim3(nq + 2 * nkv, ntok), dim3(64), 0, st, qkv, bias, qn, kn, eps, rope,
-                       pos_dev, nq, nkv, hd, (nq + 2 * nkv) * hd, layer, cap, kq, vq, ks, vs);
+                       pos_dev, nq, nkv, hd, (nq + 2 * nkv) * hd, layer, kr, kq, vq, ks, vs);
     hip_check(hipGetLastError(), "qkv_post launch");
 }
 
@@ -129,7 +143,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
                                                            const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
                                                            const float *__restrict__ ks, const float *__restrict__ vs,
                                                            const int *__restrict__ pos_dev, int layer, int nq, int nkv,
-                                                           int hd, int cap, float attn_scale, int nsplit,
+                                                           int hd, KvRing kr, float attn_scale, int nsplit,
                                                            float *__restrict__ part) {
     __shared__ __align__(16) int8_t qi[128];
     __shared__ float qas_s;
@@ -156,7 +170,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
         }
     }
     const int seq = pos_dev[0] + tok + 1;
-    const int t0 = split * kAttnSplitLen, t1 = min(seq, t0 + kAttnSplitLen);
+    const int act = active_len(kr, seq);  // attended positions: index idx -> slot of active_pos
+    const int t0 = split * kAttnSplitLen, t1 = min(act, t0 + kAttnSplitLen);
     float *pp = part + ((size_t)(tok * nq + head) * nsplit + split) * (2 + hd);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     if (t0 >= t1) {
@@ -187,24 +202,36 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
         if (lane == 0) qas_s = qs * attn_scale;
     }
     __syncthreads();
-    const size_t base = ((size_t)layer * nkv + kvh) * cap;
+    const size_t base = ((size_t)layer * nkv + kvh) * kr.cap;
     const float qas = qas_s;
+    // slot of the idx-th attended position (identity without a sliding window)
+    auto slot_of = [&](int idx) -> size_t { return (size_t)ring_slot(kr, active_pos(kr, idx, seq)); };
     // scores: one thread per position
     float smax = -INFINITY;
+    float vscale = 0.0f;
     {
         const int t = t0 + (int)tid;
         if (t < t1) {
-            const uint4 *kr = reinterpret_cast<const uint4 *>(kq + (base + t) * hd);
+            const size_t sl = base + slot_of(t);
+            const uint4 *krow = reinterpret_cast<const uint4 *>(kq + sl * hd);
             const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
-            int dot = 0;
+            int dot[2] = {0, 0};
             for (int i = 0; i < hd / 16; i++) {
-                const uint4 a = kr[i], b = qr[i];
-                dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
-                dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
-                dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
-                dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
+                const uint4 a = krow[i], b = qr[i];
+                int d = dot[i >> 2];
+                d = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, d, false);
+                d = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, d, false);
+                d = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, d, false);
+                d = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, d, false);
+                dot[i >> 2] = d;
             }
-            const float s = ((float)dot * ks[base + t]) * qas;
+            const float kscale = ks[sl];
+            vscale = vs[sl];
+            float s;
+            if (kr.window > 0 && hd == 128)  // per-64-block terms (causal_gqa_group_q4_or_window, 8823-8868)
+                s = ((float)dot[0] * kscale) * qas + ((float)dot[1] * kscale) * qas;
+            else  // causal_gqa_group_q8 (8471-8594): one dot per head
+                s = ((float)(dot[0] + dot[1]) * kscale) * qas;
             sc[tid] = s;
             smax = s;
         }
@@ -216,7 +243,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     float psum = 0.0f;
     if (t0 + (int)tid < t1) {
         const float p = expf(sc[tid] - m);
-        sc[tid] = p * vs[base + t0 + tid];  // p_t * vs_t
+        sc[tid] = p * vscale;  // p_t * vs_t
         psum = p;
     }
     psum = wave_sum_f(psum);
@@ -229,14 +256,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     const int nps = 256 / ncg;        // 16 or 8 position subsets
     const int cg = (int)tid % ncg, ps = (int)tid / ncg;
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    const int8_t *vbase = vq + (base + t0) * hd + cg * 4;
+    const int8_t *vcol = vq + base * hd + cg * 4;
     int i = ps;
     for (; i + 3 * nps < n; i += 4 * nps) {
         int vv[4];
         float ww[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            vv[u] = *reinterpret_cast<const int *>(vbase + (size_t)(i + u * nps) * hd);
+            vv[u] = *reinterpret_cast<const int *>(vcol + slot_of(t0 + i + u * nps) * hd);
             ww[u] = sc[i + u * nps];
         }
 #pragma unroll
@@ -248,7 +275,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
         }
     }
     for (; i < n; i += nps) {
-        const int v = *reinterpret_cast<const int *>(vbase + (size_t)i * hd);
+        const int v = *reinterpret_cast<const int *>(vcol + slot_of(t0 + i) * hd);
         const float wt = sc[i];
         a0 = fmaf(wt, (float)(int8_t)(v & 0xFF), a0);
         a1 = fmaf(wt, (float)(int8_t)((v >> 8) & 0xFF), a1);
@@ -276,13 +303,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
 // optionally re-rotates each 64-block with its o_proj chunk index and quantizes it
 // (populate_chunk_fwht_raw(None), real_llm.rs:7060-7084) -> the o_proj activation.
 __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ part, int nq, int hd, int nsplit,
-                                                        const int *__restrict__ pos_dev, float *__restrict__ out_f,
+                                                        KvRing kr, const int *__restrict__ pos_dev,
+                                                        float *__restrict__ out_f,
                                                         int8_t *__restrict__ aq, float *__restrict__ as,
                                                         int32_t *__restrict__ asum) {
     const uint32_t lane = threadIdx.x;
     const int head = blockIdx.x, tok = blockIdx.y;
-    const int seq = pos_dev[0] + tok + 1;
-    const int ns = min(nsplit, (seq + kAttnSplitLen - 1) / kAttnSplitLen);
+    const int act = active_len(kr, pos_dev[0] + tok + 1);
+    const int ns = min(nsplit, (act + kAttnSplitLen - 1) / kAttnSplitLen);
     const float *pp = part + (size_t)(tok * nq + head) * nsplit * (2 + hd);
     // Split maxima and sums one split per lane (loads in flight together), then the
     // rescaled sums in split order.
@@ -335,12 +363,12 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
 int attn_max_splits(int max_seq) { return (max_seq + kAttnSplitLen - 1) / kAttnSplitLen; }
 
 void launch_attention(hipStream_t st, const float *q, int q_stride, const int8_t *kq, const int8_t *vq, const float *ks,
-                      const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd, int cap, float attn_scale,
+                      const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr, float attn_scale,
                       int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum) {
     hipLaunchKernelGGL(attn_partial_kernel, dim3(nq, nsplit, ntok), dim3(256), 0, st, q, q_stride, kq, vq, ks, vs,
-                       pos_dev, layer, nq, nkv, hd, cap, attn_scale, nsplit, part);
+                       pos_dev, layer, nq, nkv, hd, kr, attn_scale, nsplit, part);
     hip_check(hipGetLastError(), "attn_partial launch");
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(nq, ntok), dim3(64), 0, st, part, nq, hd, nsplit, pos_dev, out_f, aq, as,
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(nq, ntok), dim3(64), 0, st, part, nq, hd, nsplit, kr, pos_dev, out_f, aq, as,
                        asum);
     hip_check(hipGetLastError(), "attn_merge launch");
 }

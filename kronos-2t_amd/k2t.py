@@ -98,6 +98,8 @@ SIGNATURES = {
     "k2t_model_set_qk_norm": (I32, [VP, I32, VP, VP]),
     "k2t_model_set_moe": (I32, [VP, I32, VP, I32, VP, VP, I32, I32, I32]),
     "k2t_model_kv_synthetic": (I32, [VP, I32, C.c_uint64]),
+    "k2t_model_set_kv_window": (I32, [VP, I32, I32]),
+    "k2t_model_kv_window": (I32, [VP, C.POINTER(I32), C.POINTER(I32)]),
 }
 
 MOE_SOFTMAX, MOE_TOPK_SOFTMAX, MOE_SIGMOID = 0, 1, 2
@@ -420,6 +422,15 @@ class Model:
                                       None if rb is None else rb.ctypes.data_as(VP), top_k,
                                       int(bool(norm_topk_prob)), scoring))
         self._keep.append(bank)
+
+    def set_kv_window(self, window, sink_tokens=4):
+        """k2t_model_set_kv_window (set_kv_sliding_window); window 0 restores the full cache."""
+        check(lib().k2t_model_set_kv_window(self.h, int(window), int(sink_tokens)))
+
+    def kv_window(self):
+        w, s = I32(), I32()
+        check(lib().k2t_model_kv_window(self.h, C.byref(w), C.byref(s)))
+        return w.value, s.value
 
     def kv_synthetic(self, n_pos, seed=0):
         check(lib().k2t_model_kv_synthetic(self.h, int(n_pos), int(seed)))

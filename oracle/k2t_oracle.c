@@ -967,6 +967,43 @@ void or_attn_q8_head(const float *q_head, const int8_t *k_q8, const float *ks, c
     or_ifwht64(out, hd);
 }
 
+/* causal_gqa_group_q4_or_window, int8 branch (real_llm.rs:8794-8937): the sliding-window
+ * path forms each score from per-64-block dots, total += float(dot_g) * ks * qs, and
+ * skips positions whose weight p_norm * vs is zero.  k/v rows are the attended
+ * positions, already gathered in active_kv_pos order. */
+void or_attn_q8_head_window(const float *q_head, const int8_t *k_q8, const float *ks, const int8_t *v_q8,
+                            const float *vs, size_t seq, size_t hd, float attn_scale, float *out,
+                            float *scores) {
+    int8_t qi[128];
+    float q_scale;
+    or_kv_quant_head(q_head, hd, qi, &q_scale);
+    float qas = q_scale * attn_scale;
+    for (size_t t = 0; t < seq; t++) {
+        float total = 0.0f;
+        for (size_t g = 0; g < hd / 64; g++) {
+            int32_t dot = 0;
+            for (size_t i = 0; i < 64; i++) dot += (int32_t)qi[g * 64 + i] * (int32_t)k_q8[t * hd + g * 64 + i];
+            total += (float)dot * ks[t] * qas;
+        }
+        scores[t] = total;
+    }
+    float mx = -INFINITY;
+    for (size_t t = 0; t < seq; t++) mx = fmaxf(mx, scores[t]);
+    float sum = 0.0f;
+    for (size_t t = 0; t < seq; t++) {
+        scores[t] = expf(scores[t] - mx);
+        sum += scores[t];
+    }
+    float inv = 1.0f / sum;
+    for (size_t i = 0; i < hd; i++) out[i] = 0.0f;
+    for (size_t t = 0; t < seq; t++) {
+        float w = (scores[t] * inv) * vs[t];
+        if (w == 0.0f) continue;
+        for (size_t i = 0; i < hd; i++) out[i] += w * (float)v_q8[t * hd + i];
+    }
+    or_ifwht64(out, hd);
+}
+
 /* ------------------------------------------------------------------ */
 /* Small fp32 glue (real_llm.rs)                                         */
 /* ------------------------------------------------------------------ */

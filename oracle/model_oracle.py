@@ -85,7 +85,7 @@ class OracleModel:
     """`gemv_threads` > 0 switches every projection to the threaded portable path (the
     timed CPU baseline); 0 keeps the NEON-semantics integer path (the parity oracle)."""
 
-    def __init__(self, cfg, layers, head, final_norm, gemv_threads=0, embed=None):
+    def __init__(self, cfg, layers, head, final_norm, gemv_threads=0, embed=None, window=0, sinks=0):
         self.gemv_threads = gemv_threads
         self.embed_fn = embed  # untied embedding: token -> f32[hidden] (embed_token_into)
         self.cfg = cfg
@@ -93,6 +93,12 @@ class OracleModel:
         self.head = head
         self.final_norm = final_norm
         L, nkv, hd, cap = cfg["n_layers"], cfg["n_kv_heads"], cfg["head_dim"], cfg["max_seq"]
+        # QuantizedKvCache::new_with_opts (real_llm.rs:1235-1257): sliding-window ring
+        self.window = self.sinks = self.ring = 0
+        if window >= 8 and window + 512 < cap:
+            self.window, self.sinks = window, min(sinks, window // 2)
+            self.ring = (window - self.sinks) + 512
+            cap = self.sinks + self.ring
         self.kq = np.zeros((L, nkv, cap, hd), np.int8)
         self.vq = np.zeros((L, nkv, cap, hd), np.int8)
         self.ks = np.zeros((L, nkv, cap), np.float32)
@@ -103,6 +109,20 @@ class OracleModel:
         if self.gemv_threads:
             return m.gemv_portable(xq, xs, self.gemv_threads)
         return m.gemv(xq, xs, xsum)
+
+    def slot_of_pos(self, pos):
+        """real_llm.rs:1116-1122"""
+        if self.ring == 0 or pos < self.sinks:
+            return pos
+        return self.sinks + (pos - self.sinks) % self.ring
+
+    def active_slots(self, seq):
+        """active_kv_len / active_kv_pos (real_llm.rs:8596-8612) mapped to cache slots."""
+        if self.window > 0 and seq > self.window:
+            pos = list(range(self.sinks)) + list(range(seq - (self.window - self.sinks), seq))
+        else:
+            pos = list(range(seq))
+        return [self.slot_of_pos(p) for p in pos]
 
     def embed(self, token):
         if self.embed_fn is not None:
@@ -131,15 +151,21 @@ class OracleModel:
                     qkv[h] = ((qkv[h] * np.float32(O.inv_rms(qkv[h], eps))) * wn).astype(np.float32)
             for h in range(nq + nkv):
                 qkv[h] = O.rope_apply(qkv[h], rope)
+            sl = self.slot_of_pos(pos)
             for kvh in range(nkv):
-                self.kq[li, kvh, pos], self.ks[li, kvh, pos] = O.kv_quant_head(qkv[nq + kvh])
-                self.vq[li, kvh, pos], self.vs[li, kvh, pos] = O.kv_quant_head(qkv[nq + nkv + kvh])
+                self.kq[li, kvh, sl], self.ks[li, kvh, sl] = O.kv_quant_head(qkv[nq + kvh])
+                self.vq[li, kvh, sl], self.vs[li, kvh, sl] = O.kv_quant_head(qkv[nq + nkv + kvh])
             group = nq // nkv
             outs = []
+            act = self.active_slots(pos + 1)
             for qh in range(nq):
                 kvh = qh // group
-                outs.append(O.attn_q8_head(qkv[qh], self.kq[li, kvh, :pos + 1], self.ks[li, kvh, :pos + 1],
-                                           self.vq[li, kvh, :pos + 1], self.vs[li, kvh, :pos + 1], scale))
+                if self.window:
+                    outs.append(O.attn_q8_head(qkv[qh], self.kq[li, kvh, act], self.ks[li, kvh, act],
+                                               self.vq[li, kvh, act], self.vs[li, kvh, act], scale, window=True))
+                else:
+                    outs.append(O.attn_q8_head(qkv[qh], self.kq[li, kvh, :pos + 1], self.ks[li, kvh, :pos + 1],
+                                               self.vq[li, kvh, :pos + 1], self.vs[li, kvh, :pos + 1], scale))
             aq, as_, asum = O.populate_fwht(np.concatenate(outs))
             hidden = (hidden + self._gemv(L["o"], aq, as_, asum)).astype(np.float32)
             if L.get("moe") is not None:

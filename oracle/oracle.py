@@ -62,6 +62,7 @@ def lib():
             "or_nf_tail_total": (SZ, [SZ, C.c_int, SZ]),
             "or_kv_quant_head": (None, [F32P, SZ, I8P, F32P]),
             "or_attn_q8_head": (None, [F32P, I8P, F32P, I8P, F32P, SZ, SZ, C.c_float, F32P, F32P]),
+            "or_attn_q8_head_window": (None, [F32P, I8P, F32P, I8P, F32P, SZ, SZ, C.c_float, F32P, F32P]),
             "or_rope_row": (None, [SZ, C.c_double, SZ, F32P]),
             "or_rope_apply": (None, [F32P, SZ, F32P]),
             "or_swiglu": (None, [F32P, F32P, F32P, SZ]),
@@ -301,14 +302,16 @@ def kv_quant_head(src):
     return q, float(s[0])
 
 
-def attn_q8_head(q_head, k_q8, ks, v_q8, vs, attn_scale):
-    """real_llm.rs:8471-8594 (portable branches)."""
+def attn_q8_head(q_head, k_q8, ks, v_q8, vs, attn_scale, window=False):
+    """real_llm.rs:8471-8594 (portable branches); window=True: the sliding-window path
+    (8794-8937) over rows already gathered in active_kv_pos order."""
     q_head = _f32(q_head)
     hd = q_head.size
     seq = len(ks)
     out = np.zeros(hd, np.float32)
     sc = np.zeros(max(seq, 1), np.float32)
-    lib().or_attn_q8_head(q_head, np.ascontiguousarray(k_q8, np.int8).reshape(-1), _f32(ks),
+    fn = lib().or_attn_q8_head_window if window else lib().or_attn_q8_head
+    fn(q_head, np.ascontiguousarray(k_q8, np.int8).reshape(-1), _f32(ks),
                           np.ascontiguousarray(v_q8, np.int8).reshape(-1), _f32(vs), seq, hd,
                           float(attn_scale), out, sc)
     return out

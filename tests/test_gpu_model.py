@@ -113,6 +113,31 @@ def test_gqa_long_context_xcd_order(gpu_ctx, hd):
         assert ok, info
 
 
+@pytest.mark.parametrize("hd,n_tok", [(64, 560), (128, 48)])
+def test_sliding_window_ring_matches_oracle(gpu_ctx, hd, n_tok):
+    """Sliding window 16 with 4 sinks (set_kv_sliding_window): attention over the sinks
+    and the last 12 positions, K/V in a 524-slot ring; 560 tokens wrap the ring (hd 64),
+    48 exercise the per-64-block window scores (hd 128).  Prefill and decode vs the oracle."""
+    print(f"sliding window hd={hd} tokens={n_tok}", flush=True)
+    cfg = dict(n_layers=1, hidden=2 * hd, n_heads=2, n_kv_heads=1, head_dim=hd, intermediate=128, vocab=160,
+               max_seq=700, rms_eps=1e-5, rope_theta=10000.0)
+    layers, head, fn = random_model(cfg, seed=21, fmt="nf4")
+    ref = OracleModel(cfg, layers, head, fn, window=16, sinks=4)
+    gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=32)
+    gm.set_kv_window(16, 4)
+    assert gm.kv_window() == (16, 4) and not gm.persistent_active()
+    toks = np.random.default_rng(22).integers(0, cfg["vocab"], n_tok)
+    gm.prefill(toks[:-3], want_logits=False)
+    for t in toks[:-3]:
+        ref.forward_token(int(t))
+    for t in toks[-3:]:
+        a, b = gm.decode(int(t)), ref.forward_token(int(t))
+        ok, info = _close(a, b)
+        assert ok, info
+    gm.set_kv_window(0, 0)
+    assert gm.kv_window() == (0, 0) and gm.position() == 0
+
+
 def test_prefill_equals_token_by_token_and_graph_equals_eager(gpu_ctx):
     """Batched prefill and token-by-token decode on the one-kernel-per-operation path run
     the same arithmetic (bit-exact); the persistent kernel sums attention and GEMV

@@ -83,3 +83,42 @@ def test_embedding_is_inverse_rotated_head_row():
         e = O.ifwht64(head.row_rotated(r))
         cos = float(np.dot(e, Wh[r]) / (np.linalg.norm(e) * np.linalg.norm(Wh[r])))
         assert cos > 0.99
+
+
+def test_sliding_window_slots_and_attention():
+    """Window / sink ring (real_llm.rs:1116-1122, 1235-1257, 8596-8612): the attended
+    positions are the sinks plus the last window - sinks positions; their ring slots are
+    distinct and still hold those positions' data after the ring wraps.  The window
+    attention with per-64-block scores equals the full-head form for hd 64 and stays
+    within fp32 rounding of it for hd 128."""
+    import oracle as O
+    from model_oracle import OracleModel
+    cfg = dict(n_layers=1, hidden=64, n_heads=1, n_kv_heads=1, head_dim=64, intermediate=64, vocab=8, max_seq=1200,
+               rms_eps=1e-5, rope_theta=10000.0)
+    om = OracleModel(cfg, [], None, None, window=16, sinks=4)
+    assert (om.window, om.sinks, om.ring) == (16, 4, 12 + 512)
+    owner = {}
+    for pos in range(1100):  # wraps the 524-slot ring twice
+        owner[om.slot_of_pos(pos)] = pos
+        seq = pos + 1
+        act = om.active_slots(seq)
+        want = list(range(seq)) if seq <= 16 else list(range(4)) + list(range(seq - 12, seq))
+        assert [owner[s] for s in act] == want
+        assert len(set(act)) == len(act)
+    # sinks capped at window / 2; a window without room for the slack disables the ring
+    assert OracleModel(cfg, [], None, None, window=16, sinks=20).sinks == 8
+    assert OracleModel(cfg, [], None, None, window=700, sinks=4).window == 0
+    rng = np.random.default_rng(1)
+    for hd in (64, 128):
+        q = rng.standard_normal(hd).astype(np.float32)
+        n = 37
+        kq = rng.integers(-127, 128, (n, hd)).astype(np.int8)
+        vq = rng.integers(-127, 128, (n, hd)).astype(np.int8)
+        ks = rng.uniform(0.01, 0.03, n).astype(np.float32)
+        vs = rng.uniform(0.01, 0.03, n).astype(np.float32)
+        a = O.attn_q8_head(q, kq, ks, vq, vs, 0.125)
+        b = O.attn_q8_head(q, kq, ks, vq, vs, 0.125, window=True)
+        if hd == 64:
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        else:
+            assert np.allclose(a, b, rtol=1e-5, atol=1e-6)
