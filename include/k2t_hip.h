@@ -247,6 +247,11 @@ int32_t k2t_model_set_moe(k2t_model *m, int32_t layer, const k2t_experts *bank, 
  * window - sinks positions (active_kv_pos, real_llm.rs:8596-8612).  Any other window
  * (0 included) restores the full causal cache.  Resets the position to 0. */
 int32_t k2t_model_set_kv_window(k2t_model *m, int32_t window, int32_t sink_tokens);
+/* set_kv_bits (real_llm.rs:1732-1752): 8 (default) = int8 Hadamard KV with one f32 scale
+ * per head; 4 = NF4-codebook Hadamard KV with a refined BF16 scale per 64-block
+ * (store_hadamard_q4_head_raw, real_llm.rs:8646-8700).  Resets the position to 0. */
+int32_t k2t_model_set_kv_bits(k2t_model *m, int32_t bits);
+int32_t k2t_model_kv_bits(const k2t_model *m, int32_t *bits);
 /* Active (window, sinks); (0, 0) for the full cache. */
 int32_t k2t_model_kv_window(const k2t_model *m, int32_t *window, int32_t *sink_tokens);
 /* Benchmark support (no reference counterpart): fills cache positions [0, n_pos) of every
@@ -282,6 +287,25 @@ int32_t k2t_model_generate(k2t_model *m, int32_t first_token, int32_t n_steps, i
 /* Device pointer of the last logits (valid after a step; read after k2t_model_sync). */
 int32_t k2t_model_logits(k2t_model *m, const float **d_logits);
 int32_t k2t_model_sync(k2t_model *m);
+
+/* ---- KV cache and attention ops ------------------------------------------- */
+
+/* Hadamard KV store of n post-RoPE heads [n][head_dim] into slots 0..n-1:
+ * bits 8: int8 d_q [n][hd] and f32 d_scales [n] (store_hadamard_q8_head*,
+ * real_llm.rs:8282-8365); bits 4: NF4 nibbles d_q [n][hd/2] and BF16 d_scales [n][hd/64]
+ * (store_hadamard_q4_head_raw, real_llm.rs:8646-8700).  The engine's own store is the same code. */
+int32_t k2t_kv_store(k2t_ctx *ctx, int32_t bits, const float *d_heads, int32_t n, int32_t head_dim, void *d_q,
+                     void *d_scales);
+/* Decode attention of one token (causal_gqa_attention_q8, real_llm.rs:8938-8988, and the
+ * window / NF4 path causal_gqa_group_q4_or_window, 8794-8937): queries d_q [n_heads][hd]
+ * (post-RoPE), a KV cache of n_kv_heads x cap slots in k2t_kv_store's layout, `seq`
+ * positions (window > 0: a sink + ring cache of cap slots, ring = cap - sinks, as
+ * k2t_model_set_kv_window lays it out); d_out [n_heads][hd] receives the attention output
+ * after ifwht64.  Synchronizes the context's stream. */
+int32_t k2t_attn_decode(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_heads, int32_t n_kv_heads,
+                        int32_t head_dim, const void *d_kq, const void *d_ks, const void *d_vq, const void *d_vs,
+                        int32_t cap, int32_t seq, int32_t window, int32_t sink_tokens, float attn_scale,
+                        float *d_out);
 
 /* ---- sparse-MoE experts (.k2tm shards) ------------------------------------- */
 

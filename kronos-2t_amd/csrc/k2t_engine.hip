@@ -30,7 +30,8 @@ int attn_max_splits(int max_seq);
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums);
 void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok, float *out);
 void launch_kv_synthetic(hipStream_t st, int8_t *kq, int8_t *vq, float *ks, float *vs, int layers_kv, int cap,
-                         int n_pos, int hd, uint64_t seed);
+                         int n_pos, int hd, int bits, uint64_t seed);
+void launch_kv_store(hipStream_t st, const float *heads, int n, int hd, int bits, int8_t *qbuf, float *sbuf);
 void launch_embed_rows(hipStream_t st, const void *rows, bool bf16, const int *tokens, int ntok, int d, float *out);
 void launch_advance_pos(hipStream_t st, int *pos, int n);
 void launch_argmax(hipStream_t st, const float *x, int n, int *out_idx);
@@ -288,7 +289,8 @@ bool mk_format(const k2t_model *m, int &fmt, int &hp) {
 
 bool use_persistent(const k2t_model *m) {
     int fmt, hp;
-    if (m->ring.window > 0) return false;  // the sliding-window ring runs on the per-operation path
+    // the sliding-window ring and the NF4 KV cache run on the per-operation path
+    if (m->ring.window > 0 || m->ring.bits != 8) return false;
     for (const auto &L : m->layers)
         if (L.has_moe || L.q_norm || L.k_norm) return false;  // these run on the per-operation path
     return m->persistent && m->mk_ok && !m->exact && mk_format(m, fmt, hp);
@@ -424,7 +426,7 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
         try {
             m->ctx = ctx;
             m->cfg = c;
-            m->ring = KvRing{c.max_seq, 0, 0, 0};
+            m->ring = KvRing{c.max_seq, 0, 0, 0, 8};
             m->max_batch = max_batch;
             m->layers.resize(c.n_layers);
             hip_check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "stream create");
@@ -671,9 +673,9 @@ int32_t k2t_model_set_kv_window(k2t_model *m, int32_t window, int32_t sink_token
         if (window >= 8 && window + kRingSlack < c.max_seq) {
             const int s = std::min(sink_tokens, window / 2);
             const int rl = (window - s) + kRingSlack;
-            m->ring = KvRing{s + rl, window, s, rl};
+            m->ring = KvRing{s + rl, window, s, rl, m->ring.bits};
         } else {
-            m->ring = KvRing{c.max_seq, 0, 0, 0};
+            m->ring = KvRing{c.max_seq, 0, 0, 0, m->ring.bits};
         }
         // set_kv_sliding_window starts a new context (real_llm.rs:1764-1790)
         hip_check(hipMemset(m->pos_dev, 0, sizeof(int)), "pos reset");
@@ -682,6 +684,31 @@ int32_t k2t_model_set_kv_window(k2t_model *m, int32_t window, int32_t sink_token
             (void)hipGraphExecDestroy(m->graph);
             m->graph = nullptr;
         }
+    });
+}
+
+int32_t k2t_model_set_kv_bits(k2t_model *m, int32_t bits) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        arg(bits == 4 || bits == 8, "KV bits must be 4 or 8");
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        hip_check(hipStreamSynchronize(m->stream), "sync");
+        // set_kv_bits (real_llm.rs:1732-1752): a new cache, position 0.  The NF4 nibbles
+        // and BF16 block scales fit in the int8 buffers (hd/2 <= hd bytes, hd/64 BF16 <= one f32).
+        m->ring.bits = bits;
+        hip_check(hipMemset(m->pos_dev, 0, sizeof(int)), "pos reset");
+        m->pos = 0;
+        if (m->graph) {
+            (void)hipGraphExecDestroy(m->graph);
+            m->graph = nullptr;
+        }
+    });
+}
+
+int32_t k2t_model_kv_bits(const k2t_model *m, int32_t *bits) {
+    return mguard([&] {
+        arg(m && bits, "NULL argument");
+        *bits = m->ring.bits;
     });
 }
 
@@ -701,7 +728,7 @@ int32_t k2t_model_kv_synthetic(k2t_model *m, int32_t n_pos, uint64_t seed) {
         hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
         hip_check(hipStreamSynchronize(m->stream), "sync");
         launch_kv_synthetic(m->stream, m->kq, m->vq, m->ks, m->vs, c.n_layers * c.n_kv_heads, m->ring.cap,
-                            std::min(n_pos, m->ring.cap), c.head_dim, seed);
+                            std::min(n_pos, m->ring.cap), c.head_dim, m->ring.bits, seed);
         hip_check(hipMemcpyAsync(m->pos_dev, &n_pos, sizeof(int), hipMemcpyHostToDevice, m->stream), "pos set");
         hip_check(hipStreamSynchronize(m->stream), "sync");
         m->pos = n_pos;
@@ -839,6 +866,53 @@ int32_t k2t_model_persistent_active(const k2t_model *m, int32_t *active) {
     return mguard([&] {
         arg(m && active, "NULL argument");
         *active = use_persistent(m) ? 1 : 0;
+    });
+}
+
+int32_t k2t_kv_store(k2t_ctx *ctx, int32_t bits, const float *d_heads, int32_t n, int32_t head_dim, void *d_q,
+                     void *d_scales) {
+    return mguard([&] {
+        arg(ctx && d_heads && d_q && d_scales, "NULL argument");
+        arg(bits == 4 || bits == 8, "KV bits must be 4 or 8");
+        arg(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128");
+        arg(n >= 0 && n <= (1 << 24), "n out of range");
+        if (n == 0) return;
+        hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+        launch_kv_store(ctx->stream, d_heads, n, head_dim, bits, (int8_t *)d_q, (float *)d_scales);
+    });
+}
+
+int32_t k2t_attn_decode(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_heads, int32_t n_kv_heads,
+                        int32_t head_dim, const void *d_kq, const void *d_ks, const void *d_vq, const void *d_vs,
+                        int32_t cap, int32_t seq, int32_t window, int32_t sink_tokens, float attn_scale,
+                        float *d_out) {
+    return mguard([&] {
+        arg(ctx && d_q && d_kq && d_ks && d_vq && d_vs && d_out, "NULL argument");
+        arg(bits == 4 || bits == 8, "KV bits must be 4 or 8");
+        arg(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128");
+        arg(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
+        arg(seq >= 1 && cap >= 1 && seq <= (1 << 24), "seq / cap out of range");
+        KvRing kr{cap, 0, 0, 0, bits};
+        if (window > 0) {
+            arg(window >= 8 && sink_tokens >= 0 && sink_tokens <= window / 2, "window >= 8 and sinks <= window / 2");
+            arg(cap > window, "a windowed cache needs cap > window");
+            kr = KvRing{cap, window, sink_tokens, cap - sink_tokens, bits};
+        } else {
+            arg(seq <= cap, "seq exceeds the cache");
+        }
+        const int act = window > 0 ? std::min(seq, window) : seq;
+        const int nsplit = attn_max_splits(act);
+        hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+        const size_t part = (size_t)n_heads * nsplit * (2 + head_dim);
+        ensure_scratch(ctx, part + 64);
+        float *pp = ctx->scratch;
+        int *pos = reinterpret_cast<int *>(ctx->scratch + part);
+        const int p0 = seq - 1;
+        hip_check(hipMemcpyAsync(pos, &p0, sizeof(int), hipMemcpyHostToDevice, ctx->stream), "pos upload");
+        launch_attention(ctx->stream, d_q, n_heads * head_dim, (const int8_t *)d_kq, (const int8_t *)d_vq,
+                         (const float *)d_ks, (const float *)d_vs, pos, 0, n_heads, n_kv_heads, head_dim, kr,
+                         attn_scale, nsplit, 1, pp, d_out, nullptr, nullptr, nullptr);
+        hip_check(hipStreamSynchronize(ctx->stream), "sync");  // the position lives in host memory above
     });
 }
 

@@ -92,9 +92,11 @@ void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, 
 
 // KV cache geometry (QuantKvRawPtrs, real_llm.rs:1096-1122): `cap` slots per (layer, KV
 // head); with a sliding window (window > 0), positions below `sinks` keep their own slot
-// and later ones wrap in a ring of `ring` slots.
+// and later ones wrap in a ring of `ring` slots.  bits 8: int8 codes [slot][hd] and one
+// f32 scale per slot; bits 4: NF4 nibbles [slot][hd/2] and one BF16 scale per 64-block
+// [slot][hd/64] (stored in the same buffers).
 struct KvRing {
-    int cap, window, sinks, ring;
+    int cap, window, sinks, ring, bits;
 };
 
 // The model takes ownership of `mat` (destroyed with the model).

@@ -28,6 +28,90 @@ __device__ __forceinline__ int active_pos(const KvRing &r, int idx, int seq) {
     return (r.window > 0 && seq > r.window && idx >= r.sinks) ? (seq - (r.window - r.sinks)) + (idx - r.sinks) : idx;
 }
 
+// NF4_DEFAULT_CODEBOOK_I8 (simd_lut.rs:4338-4350) as v_perm table words, bytes 0-15.
+constexpr uint32_t kNf4Cb0 = 0xC6B5A081u;  // -127 -96 -75 -58
+constexpr uint32_t kNf4Cb1 = 0xFAEEE1D4u;  // -44 -31 -18 -6
+constexpr uint32_t kNf4Cb2 = 0x2C1F1206u;  // 6 18 31 44
+constexpr uint32_t kNf4Cb3 = 0x7F604B3Au;  // 58 75 96 127
+
+__device__ __forceinline__ int nf4_cb_value(int i) {
+    const uint32_t w = i < 4 ? kNf4Cb0 : i < 8 ? kNf4Cb1 : i < 12 ? kNf4Cb2 : kNf4Cb3;
+    return (int)(int8_t)((w >> (8 * (i & 3))) & 0xFFu);
+}
+
+// nf4_nearest_idx (real_llm.rs:8614-8644): midpoint thresholds of the default codebook.
+__device__ __forceinline__ int nf4_nearest_idx(float y) {
+    const float a = fabsf(y);
+    int p;
+    if (a < 37.5f) p = a < 12.0f ? 0 : (a < 24.5f ? 1 : 2);
+    else if (a < 85.5f) p = a < 51.0f ? 3 : (a < 66.5f ? 4 : 5);
+    else p = a < 111.5f ? 6 : 7;
+    return y >= 0.0f ? 8 + p : 7 - p;
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float v) {
+    const uint32_t b = __float_as_uint(v);
+    if ((b & 0x7F800000u) == 0x7F800000u && (b & 0x007FFFFFu)) return (uint16_t)((b >> 16) | 0x40u);
+    return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+
+// store_hadamard_q4_head_raw (real_llm.rs:8646-8700) for one rotated 64-block held one
+// element per lane: NF4 codes against 127/max, the least-squares scale num/den summed
+// in element order (as the reference's loop), rounded to BF16, then the final codes.
+// Byte h*16 + i holds element h*32 + i (low nibble) and h*32 + 16 + i (high nibble).
+__device__ __forceinline__ void store_q4_block(float v, uint32_t lane, uint8_t *__restrict__ dst32,
+                                               uint16_t *__restrict__ dst_s) {
+    const float mx = wave_max_f(fabsf(v));
+    if (mx < 1e-30f) {
+        if (lane < 32) dst32[lane] = 0x88;
+        if (lane == 0) *dst_s = 0;
+        return;
+    }
+    const float inv0 = 127.0f / mx;
+    const float c = (float)nf4_cb_value(nf4_nearest_idx(v * inv0));
+    const float vc = v * c, cc = c * c;
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 64; j++) {
+        num += __shfl(vc, j, kWave);
+        den += __shfl(cc, j, kWave);
+    }
+    const float s_ref = (den > 1e-12f && num > 0.0f) ? num / den : mx / 127.0f;
+    const uint16_t sb = f32_to_bf16_rne(s_ref);
+    const float s_fin = __uint_as_float((uint32_t)sb << 16);
+    const float inv_fin = s_fin > 1e-30f ? 1.0f / s_fin : 0.0f;
+    const int idx = nf4_nearest_idx(v * inv_fin);
+    const int hi = __shfl(idx, (int)lane + 16, kWave);
+    if ((lane & 31u) < 16u) dst32[(lane >> 5) * 16 + (lane & 15u)] = (uint8_t)(idx | (hi << 4));
+    if (lane == 0) *dst_s = sb;
+}
+
+// One rotated head (lane holds elements lane and 64 + lane) into KV slot `slot`: int8 with
+// one scale (store_hadamard_q8_head*, real_llm.rs:8282-8365) or NF4 per 64-block.
+__device__ __forceinline__ void kv_store_head(float r0, float r1, int nb, uint32_t lane, int bits, int hd, size_t slot,
+                                              int8_t *__restrict__ qbuf, float *__restrict__ sbuf) {
+    if (bits == 4) {
+        uint8_t *q4 = reinterpret_cast<uint8_t *>(qbuf) + slot * (size_t)(hd / 2);
+        uint16_t *s16 = reinterpret_cast<uint16_t *>(sbuf) + slot * (size_t)nb;
+        store_q4_block(r0, lane, q4, s16);
+        if (nb > 1) store_q4_block(r1, lane, q4 + 32, s16 + 1);
+        return;
+    }
+    const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
+    int8_t *dst = qbuf + slot * hd;
+    float *sdst = sbuf + slot;
+    if (mx <= FLT_EPSILON) {
+        dst[lane] = 0;
+        if (nb > 1) dst[64 + lane] = 0;
+        if (lane == 0) *sdst = 0.0f;
+        return;
+    }
+    const float inv = 127.0f / mx;
+    dst[lane] = (int8_t)(int)rintf(r0 * inv);
+    if (nb > 1) dst[64 + lane] = (int8_t)(int)rintf(r1 * inv);
+    if (lane == 0) *sdst = mx / 127.0f;
+}
+
 
 // ---------------------------------------------------------------- RMSNorm + FWHT + int8
 // One wave per (chunk, token): every wave recomputes inv_rms = 1/sqrt(mean(x^2) + eps)
@@ -109,19 +193,23 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, c
     const size_t slot = ((size_t)layer * nkv + kvh) * kr.cap + ring_slot(kr, pos);
     const float r0 = fwht_lane(v0, 0, lane);
     const float r1 = nb > 1 ? fwht_lane(v1, 1, lane) : 0.0f;
-    const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
-    int8_t *dst = (is_k ? kq : vq) + slot * hd;
-    float *sdst = (is_k ? ks : vs) + slot;
-    if (mx <= FLT_EPSILON) {
-        dst[lane] = 0;
-        if (nb > 1) dst[64 + lane] = 0;
-        if (lane == 0) *sdst = 0.0f;
-        return;
-    }
-    const float inv = 127.0f / mx;
-    dst[lane] = (int8_t)(int)rintf(r0 * inv);
-    if (nb > 1) dst[64 + lane] = (int8_t)(int)rintf(r1 * inv);
-    if (lane == 0) *sdst = mx / 127.0f;
+    kv_store_head(r0, r1, nb, lane, kr.bits, hd, slot, is_k ? kq : vq, is_k ? ks : vs);
+}
+
+// Standalone KV store of n rotated-domain inputs (post-RoPE heads) into slots 0..n-1.
+__global__ __launch_bounds__(64) void kv_store_kernel(const float *__restrict__ heads, int hd, int bits,
+                                                      int8_t *__restrict__ qbuf, float *__restrict__ sbuf) {
+    const uint32_t lane = threadIdx.x;
+    const int nb = hd / 64;
+    const float *h = heads + (size_t)blockIdx.x * hd;
+    const float r0 = fwht_lane(h[lane], 0, lane);
+    const float r1 = nb > 1 ? fwht_lane(h[64 + lane], 1, lane) : 0.0f;
+    kv_store_head(r0, r1, nb, lane, bits, hd, blockIdx.x, qbuf, sbuf);
+}
+
+void launch_kv_store(hipStream_t st, const float *heads, int n, int hd, int bits, int8_t *qbuf, float *sbuf) {
+    hipLaunchKernelGGL(kv_store_kernel, dim3(n), dim3(64), 0, st, heads, hd, bits, qbuf, sbuf);
+    hip_check(hipGetLastError(), "kv_store launch");
 }
 
 void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
@@ -211,7 +299,37 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     float vscale = 0.0f;
     {
         const int t = t0 + (int)tid;
-        if (t < t1) {
+        if (t < t1 && kr.bits == 4) {
+            // NF4 KV (causal_gqa_group_q4_or_window, real_llm.rs:8827-8849): per 64-block
+            // dot of the codebook values with q, total += float(dot) * ks_g * qs
+            const size_t sl = base + slot_of(t);
+            const uint8_t *k4 = reinterpret_cast<const uint8_t *>(kq) + sl * (size_t)(hd / 2);
+            const uint16_t *k16 = reinterpret_cast<const uint16_t *>(ks) + sl * (size_t)nb;
+            float s = 0.0f;
+            for (int g = 0; g < nb; g++) {
+                const uint4 *kp = reinterpret_cast<const uint4 *>(k4 + g * 32);
+                const uint32_t *qw = reinterpret_cast<const uint32_t *>(qi + g * 64);
+                int dot = 0;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint4 a = kp[h];
+                    const uint32_t w4[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t d = w4[j];
+                        const uint32_t lo = lut16(d & 0x07070707u, bit3_mask(d), kNf4Cb0, kNf4Cb1, kNf4Cb2, kNf4Cb3);
+                        const uint32_t hi =
+                            lut16((d >> 4) & 0x07070707u, bit7_mask(d), kNf4Cb0, kNf4Cb1, kNf4Cb2, kNf4Cb3);
+                        dot = __builtin_amdgcn_sdot4((int)lo, (int)qw[h * 8 + j], dot, false);
+                        dot = __builtin_amdgcn_sdot4((int)hi, (int)qw[h * 8 + 4 + j], dot, false);
+                    }
+                }
+                s += ((float)dot * __uint_as_float((uint32_t)k16[g] << 16)) * qas;
+            }
+            vscale = 1.0f;  // the V scales are per 64-block: applied in the V sum
+            sc[tid] = s;
+            smax = s;
+        } else if (t < t1) {
             const size_t sl = base + slot_of(t);
             const uint4 *krow = reinterpret_cast<const uint4 *>(kq + sl * hd);
             const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
@@ -258,7 +376,26 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     const int8_t *vcol = vq + base * hd + cg * 4;
     int i = ps;
-    for (; i + 3 * nps < n; i += 4 * nps) {
+    if (kr.bits == 4) {
+        // NF4 V: this thread's 4 columns are one nibble half of 4 bytes of block g
+        const int c0 = cg * 4, g = c0 >> 6, e0 = c0 & 63, hhalf = (e0 >> 5), i0 = e0 & 31;
+        const uint32_t off = (uint32_t)(g * 32 + hhalf * 16 + (i0 & 15));
+        const bool upper = i0 >= 16;
+        const uint8_t *v4 = reinterpret_cast<const uint8_t *>(vq) + base * (size_t)(hd / 2) + off;
+        const uint16_t *v16 = reinterpret_cast<const uint16_t *>(vs) + base * (size_t)nb + g;
+        for (; i < n; i += nps) {
+            const size_t sl = slot_of(t0 + i);
+            const uint32_t d = *reinterpret_cast<const uint32_t *>(v4 + sl * (size_t)(hd / 2));
+            const uint32_t c = upper ? lut16((d >> 4) & 0x07070707u, bit7_mask(d), kNf4Cb0, kNf4Cb1, kNf4Cb2, kNf4Cb3)
+                                     : lut16(d & 0x07070707u, bit3_mask(d), kNf4Cb0, kNf4Cb1, kNf4Cb2, kNf4Cb3);
+            const float wt = sc[i] * __uint_as_float((uint32_t)v16[sl * (size_t)nb] << 16);
+            a0 = fmaf(wt, (float)(int8_t)(c & 0xFF), a0);
+            a1 = fmaf(wt, (float)(int8_t)((c >> 8) & 0xFF), a1);
+            a2 = fmaf(wt, (float)(int8_t)((c >> 16) & 0xFF), a2);
+            a3 = fmaf(wt, (float)(int8_t)((c >> 24) & 0xFF), a3);
+        }
+    }
+    for (; kr.bits != 4 && i + 3 * nps < n; i += 4 * nps) {
         int vv[4];
         float ww[4];
 #pragma unroll
@@ -274,7 +411,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
             a3 = fmaf(ww[u], (float)(int8_t)((vv[u] >> 24) & 0xFF), a3);
         }
     }
-    for (; i < n; i += nps) {
+    for (; kr.bits != 4 && i < n; i += nps) {
         const int v = *reinterpret_cast<const int *>(vcol + slot_of(t0 + i) * hd);
         const float wt = sc[i];
         a0 = fmaf(wt, (float)(int8_t)(v & 0xFF), a0);
@@ -481,7 +618,8 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
 
 __global__ __launch_bounds__(256) void kv_synthetic_kernel(int8_t *__restrict__ kq, int8_t *__restrict__ vq,
                                                            float *__restrict__ ks, float *__restrict__ vs,
-                                                           int layers_kv, int cap, int n_pos, int hd, uint64_t seed) {
+                                                           int layers_kv, int cap, int n_pos, int hd, int bits,
+                                                           uint64_t seed) {
     const size_t slot_lin = blockIdx.x;  // (layer*nkv + kvh) * n_pos + pos
     const int lk = (int)(slot_lin / (size_t)n_pos), pos = (int)(slot_lin % (size_t)n_pos);
     if (lk >= layers_kv) return;
@@ -494,16 +632,25 @@ __global__ __launch_bounds__(256) void kv_synthetic_kernel(int8_t *__restrict__ 
     }
     if (threadIdx.x == 0) {
         const uint64_t h = mix64(base ^ 0xD1B54A32D192ED03ull);
-        ks[slot] = 0.005f + 0.045f * (float)(h & 0xFFFF) / 65535.0f;
-        vs[slot] = 0.005f + 0.045f * (float)((h >> 16) & 0xFFFF) / 65535.0f;
+        const float a = 0.005f + 0.045f * (float)(h & 0xFFFF) / 65535.0f;
+        const float b = 0.005f + 0.045f * (float)((h >> 16) & 0xFFFF) / 65535.0f;
+        if (bits == 4) {  // BF16 block scales (the codes above are read as nibbles)
+            for (int g = 0; g < hd / 64; g++) {
+                reinterpret_cast<uint16_t *>(ks)[slot * (hd / 64) + g] = (uint16_t)(__float_as_uint(a) >> 16);
+                reinterpret_cast<uint16_t *>(vs)[slot * (hd / 64) + g] = (uint16_t)(__float_as_uint(b) >> 16);
+            }
+        } else {
+            ks[slot] = a;
+            vs[slot] = b;
+        }
     }
 }
 
 void launch_kv_synthetic(hipStream_t st, int8_t *kq, int8_t *vq, float *ks, float *vs, int layers_kv, int cap,
-                         int n_pos, int hd, uint64_t seed) {
+                         int n_pos, int hd, int bits, uint64_t seed) {
     if (n_pos <= 0) return;
     hipLaunchKernelGGL(kv_synthetic_kernel, dim3((unsigned)((size_t)layers_kv * n_pos)), dim3(128), 0, st, kq, vq, ks,
-                       vs, layers_kv, cap, n_pos, hd, seed);
+                       vs, layers_kv, cap, n_pos, hd, bits, seed);
     hip_check(hipGetLastError(), "kv_synthetic launch");
 }
 

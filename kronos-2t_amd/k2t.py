@@ -100,6 +100,10 @@ SIGNATURES = {
     "k2t_model_kv_synthetic": (I32, [VP, I32, C.c_uint64]),
     "k2t_model_set_kv_window": (I32, [VP, I32, I32]),
     "k2t_model_kv_window": (I32, [VP, C.POINTER(I32), C.POINTER(I32)]),
+    "k2t_model_set_kv_bits": (I32, [VP, I32]),
+    "k2t_model_kv_bits": (I32, [VP, C.POINTER(I32)]),
+    "k2t_kv_store": (I32, [VP, I32, VP, I32, I32, VP, VP]),
+    "k2t_attn_decode": (I32, [VP, I32, VP, I32, I32, I32, VP, VP, VP, VP, I32, I32, I32, I32, C.c_float, VP]),
 }
 
 MOE_SOFTMAX, MOE_TOPK_SOFTMAX, MOE_SIGMOID = 0, 1, 2
@@ -255,6 +259,16 @@ class Ctx:
     # -- GEMV
     def gemv(self, m, xq, xs, xsum, out, ntok=1, s0=0, s1=-1, out_stride=0):
         check(lib().k2t_gemv(self.h, m.h, _p(xq), _p(xs), _p(xsum), ntok, s0, s1, _p(out), out_stride))
+
+    def kv_store(self, bits, heads, n, head_dim, q, scales):
+        """k2t_kv_store: n post-RoPE heads -> Hadamard int8 / NF4 KV slots 0..n-1."""
+        check(lib().k2t_kv_store(self.h, bits, _p(heads), n, head_dim, _p(q), _p(scales)))
+
+    def attn_decode(self, bits, q, n_heads, n_kv_heads, head_dim, kq, ks, vq, vs, cap, seq, attn_scale, out,
+                    window=0, sink_tokens=0):
+        """k2t_attn_decode: one token's attention over a KV cache in k2t_kv_store's layout."""
+        check(lib().k2t_attn_decode(self.h, bits, _p(q), n_heads, n_kv_heads, head_dim, _p(kq), _p(ks), _p(vq),
+                                    _p(vs), cap, seq, window, sink_tokens, float(attn_scale), _p(out)))
 
     def moe_ffn(self, bank, shard_layer, router_w, hidden, post_norm, eps, top_k, norm_topk_prob=True,
                 scoring=0, router_bias=None, route_ids=None, route_weights=None):
@@ -426,6 +440,14 @@ class Model:
     def set_kv_window(self, window, sink_tokens=4):
         """k2t_model_set_kv_window (set_kv_sliding_window); window 0 restores the full cache."""
         check(lib().k2t_model_set_kv_window(self.h, int(window), int(sink_tokens)))
+
+    def set_kv_bits(self, bits):
+        check(lib().k2t_model_set_kv_bits(self.h, int(bits)))
+
+    def kv_bits(self):
+        b = I32()
+        check(lib().k2t_model_kv_bits(self.h, C.byref(b)))
+        return b.value
 
     def kv_window(self):
         w, s = I32(), I32()

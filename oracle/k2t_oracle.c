@@ -1034,3 +1034,107 @@ void or_rope_apply(float *head, size_t hd, const float *row) {
 void or_swiglu(const float *g, const float *u, float *out, size_t n) {
     for (size_t i = 0; i < n; i++) out[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
 }
+
+/* ------------------------------------------------------------------ */
+/* NF4 Hadamard KV cache (real_llm.rs:8614-8700, 8794-8937)             */
+/* ------------------------------------------------------------------ */
+
+static const int8_t OR_NF4_CB[16] = {-127, -96, -75, -58, -44, -31, -18, -6, 6, 18, 31, 44, 58, 75, 96, 127};
+
+/* nf4_nearest_idx (real_llm.rs:8614-8644) */
+int or_nf4_nearest_idx(float y) {
+    float a = fabsf(y);
+    int p;
+    if (a < 37.5f) p = a < 12.0f ? 0 : (a < 24.5f ? 1 : 2);
+    else if (a < 85.5f) p = a < 51.0f ? 3 : (a < 66.5f ? 4 : 5);
+    else p = a < 111.5f ? 6 : 7;
+    return y >= 0.0f ? 8 + p : 7 - p;
+}
+
+/* store_hadamard_q4_head_raw (real_llm.rs:8646-8700): q4 [hd/2] bytes, s16 [hd/64]. */
+void or_kv_quant_head_q4(const float *head, size_t hd, uint8_t *q4, uint16_t *s16) {
+    float rot[128];
+    memcpy(rot, head, hd * sizeof(float));
+    or_fwht64(rot, hd);
+    for (size_t g = 0; g < hd / 64; g++) {
+        const float *blk = rot + g * 64;
+        float max_abs = 0.0f;
+        for (int i = 0; i < 64; i++) {
+            float a = fabsf(blk[i]);
+            if (a > max_abs) max_abs = a;
+        }
+        if (max_abs < 1e-30f) {
+            s16[g] = 0;
+            memset(q4 + g * 32, 0x88, 32);
+            continue;
+        }
+        float inv0 = 127.0f / max_abs;
+        float num = 0.0f, den = 0.0f;
+        for (int i = 0; i < 64; i++) {
+            float c = (float)OR_NF4_CB[or_nf4_nearest_idx(blk[i] * inv0)];
+            num += blk[i] * c;
+            den += c * c;
+        }
+        float s_ref = (den > 1e-12f && num > 0.0f) ? num / den : max_abs / 127.0f;
+        uint16_t sb = or_f32_to_bf16(s_ref);
+        float sf = or_bf16_to_f32(sb);
+        float invf = sf > 1e-30f ? 1.0f / sf : 0.0f;
+        s16[g] = sb;
+        for (int h = 0; h < 2; h++)
+            for (int i = 0; i < 16; i++) {
+                int lo = or_nf4_nearest_idx(blk[h * 32 + i] * invf);
+                int hi = or_nf4_nearest_idx(blk[h * 32 + 16 + i] * invf);
+                q4[g * 32 + h * 16 + i] = (uint8_t)(lo | (hi << 4));
+            }
+    }
+}
+
+/* causal_gqa_group_q4_or_window, NF4 branch (real_llm.rs:8827-8849, 8881-8906), over rows
+ * already gathered in attended order: k4/v4 [seq][hd/2], ks16/vs16 [seq][hd/64]. */
+void or_attn_q4_head(const float *q_head, const uint8_t *k4, const uint16_t *ks16, const uint8_t *v4,
+                     const uint16_t *vs16, size_t seq, size_t hd, float attn_scale, float *out, float *scores) {
+    int8_t qi[128];
+    float q_scale;
+    or_kv_quant_head(q_head, hd, qi, &q_scale);
+    const float qs = q_scale * attn_scale;
+    const size_t gph = hd / 64, half = hd / 2;
+    for (size_t t = 0; t < seq; t++) {
+        float total = 0.0f;
+        for (size_t g = 0; g < gph; g++) {
+            int32_t acc = 0;
+            const uint8_t *kp = k4 + t * half + g * 32;
+            for (int h = 0; h < 2; h++)
+                for (int i = 0; i < 16; i++) {
+                    uint8_t b = kp[h * 16 + i];
+                    acc += OR_NF4_CB[b & 0x0F] * qi[g * 64 + h * 32 + i] + OR_NF4_CB[b >> 4] * qi[g * 64 + h * 32 + 16 + i];
+                }
+            total += (float)acc * or_bf16_to_f32(ks16[t * gph + g]) * qs;
+        }
+        scores[t] = total;
+    }
+    float mx = -INFINITY;
+    for (size_t t = 0; t < seq; t++) mx = fmaxf(mx, scores[t]);
+    float sum = 0.0f;
+    for (size_t t = 0; t < seq; t++) {
+        scores[t] = expf(scores[t] - mx);
+        sum += scores[t];
+    }
+    float inv = 1.0f / sum;
+    for (size_t i = 0; i < hd; i++) out[i] = 0.0f;
+    for (size_t t = 0; t < seq; t++) {
+        float p_norm = scores[t] * inv;
+        if (p_norm == 0.0f) continue;
+        for (size_t g = 0; g < gph; g++) {
+            float w = p_norm * or_bf16_to_f32(vs16[t * gph + g]);
+            if (w == 0.0f) continue;
+            const uint8_t *vp = v4 + t * half + g * 32;
+            for (int h = 0; h < 2; h++)
+                for (int i = 0; i < 16; i++) {
+                    uint8_t b = vp[h * 16 + i];
+                    out[g * 64 + h * 32 + i] += w * (float)OR_NF4_CB[b & 0x0F];
+                    out[g * 64 + h * 32 + 16 + i] += w * (float)OR_NF4_CB[b >> 4];
+                }
+        }
+    }
+    or_ifwht64(out, hd);
+}

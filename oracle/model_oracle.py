@@ -85,7 +85,7 @@ class OracleModel:
     """`gemv_threads` > 0 switches every projection to the threaded portable path (the
     timed CPU baseline); 0 keeps the NEON-semantics integer path (the parity oracle)."""
 
-    def __init__(self, cfg, layers, head, final_norm, gemv_threads=0, embed=None, window=0, sinks=0):
+    def __init__(self, cfg, layers, head, final_norm, gemv_threads=0, embed=None, window=0, sinks=0, kv_bits=8):
         self.gemv_threads = gemv_threads
         self.embed_fn = embed  # untied embedding: token -> f32[hidden] (embed_token_into)
         self.cfg = cfg
@@ -99,6 +99,12 @@ class OracleModel:
             self.window, self.sinks = window, min(sinks, window // 2)
             self.ring = (window - self.sinks) + 512
             cap = self.sinks + self.ring
+        self.kv_bits = kv_bits
+        if kv_bits == 4:  # NF4 nibbles + BF16 block scales (QuantizedKvCache bits 4)
+            self.k4 = np.full((L, nkv, cap, hd // 2), 0x88, np.uint8)
+            self.v4 = np.full((L, nkv, cap, hd // 2), 0x88, np.uint8)
+            self.ks16 = np.zeros((L, nkv, cap, hd // 64), np.uint16)
+            self.vs16 = np.zeros((L, nkv, cap, hd // 64), np.uint16)
         self.kq = np.zeros((L, nkv, cap, hd), np.int8)
         self.vq = np.zeros((L, nkv, cap, hd), np.int8)
         self.ks = np.zeros((L, nkv, cap), np.float32)
@@ -153,14 +159,21 @@ class OracleModel:
                 qkv[h] = O.rope_apply(qkv[h], rope)
             sl = self.slot_of_pos(pos)
             for kvh in range(nkv):
-                self.kq[li, kvh, sl], self.ks[li, kvh, sl] = O.kv_quant_head(qkv[nq + kvh])
-                self.vq[li, kvh, sl], self.vs[li, kvh, sl] = O.kv_quant_head(qkv[nq + nkv + kvh])
+                if self.kv_bits == 4:
+                    self.k4[li, kvh, sl], self.ks16[li, kvh, sl] = O.kv_quant_head_q4(qkv[nq + kvh])
+                    self.v4[li, kvh, sl], self.vs16[li, kvh, sl] = O.kv_quant_head_q4(qkv[nq + nkv + kvh])
+                else:
+                    self.kq[li, kvh, sl], self.ks[li, kvh, sl] = O.kv_quant_head(qkv[nq + kvh])
+                    self.vq[li, kvh, sl], self.vs[li, kvh, sl] = O.kv_quant_head(qkv[nq + nkv + kvh])
             group = nq // nkv
             outs = []
             act = self.active_slots(pos + 1)
             for qh in range(nq):
                 kvh = qh // group
-                if self.window:
+                if self.kv_bits == 4:
+                    outs.append(O.attn_q4_head(qkv[qh], self.k4[li, kvh, act], self.ks16[li, kvh, act],
+                                               self.v4[li, kvh, act], self.vs16[li, kvh, act], scale))
+                elif self.window:
                     outs.append(O.attn_q8_head(qkv[qh], self.kq[li, kvh, act], self.ks[li, kvh, act],
                                                self.vq[li, kvh, act], self.vs[li, kvh, act], scale, window=True))
                 else:

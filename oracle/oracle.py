@@ -63,6 +63,9 @@ def lib():
             "or_kv_quant_head": (None, [F32P, SZ, I8P, F32P]),
             "or_attn_q8_head": (None, [F32P, I8P, F32P, I8P, F32P, SZ, SZ, C.c_float, F32P, F32P]),
             "or_attn_q8_head_window": (None, [F32P, I8P, F32P, I8P, F32P, SZ, SZ, C.c_float, F32P, F32P]),
+            "or_nf4_nearest_idx": (C.c_int, [C.c_float]),
+            "or_kv_quant_head_q4": (None, [F32P, SZ, U8P, U16P]),
+            "or_attn_q4_head": (None, [F32P, U8P, U16P, U8P, U16P, SZ, SZ, C.c_float, F32P, F32P]),
             "or_rope_row": (None, [SZ, C.c_double, SZ, F32P]),
             "or_rope_apply": (None, [F32P, SZ, F32P]),
             "or_swiglu": (None, [F32P, F32P, F32P, SZ]),
@@ -314,6 +317,33 @@ def attn_q8_head(q_head, k_q8, ks, v_q8, vs, attn_scale, window=False):
     fn(q_head, np.ascontiguousarray(k_q8, np.int8).reshape(-1), _f32(ks),
                           np.ascontiguousarray(v_q8, np.int8).reshape(-1), _f32(vs), seq, hd,
                           float(attn_scale), out, sc)
+    return out
+
+
+def nf4_nearest_idx(y):
+    return int(lib().or_nf4_nearest_idx(float(y)))
+
+
+def kv_quant_head_q4(src):
+    """store_hadamard_q4_head_raw (real_llm.rs:8646-8700): (nibbles [hd/2], bf16 scales [hd/64])."""
+    src = _f32(src)
+    hd = src.size
+    q4 = np.zeros(hd // 2, np.uint8)
+    s16 = np.zeros(hd // 64, np.uint16)
+    lib().or_kv_quant_head_q4(src, hd, q4, s16)
+    return q4, s16
+
+
+def attn_q4_head(q_head, k4, ks16, v4, vs16, attn_scale):
+    """NF4-KV attention (real_llm.rs:8827-8849, 8881-8906) over rows in attended order."""
+    q_head = _f32(q_head)
+    hd = q_head.size
+    seq = len(k4)
+    out = np.zeros(hd, np.float32)
+    sc = np.zeros(max(seq, 1), np.float32)
+    lib().or_attn_q4_head(q_head, np.ascontiguousarray(k4, np.uint8).reshape(-1),
+                          np.ascontiguousarray(ks16, np.uint16).reshape(-1), np.ascontiguousarray(v4, np.uint8).reshape(-1),
+                          np.ascontiguousarray(vs16, np.uint16).reshape(-1), seq, hd, float(attn_scale), out, sc)
     return out
 
 

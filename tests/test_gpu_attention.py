@@ -1,0 +1,130 @@
+"""KV-cache store and decode attention as standalone ops (k2t_kv_store, k2t_attn_decode;
+the engine runs the same device code) against the oracle, for the int8 and the NF4
+Hadamard caches, with and without the sliding-window ring; plus NF4-KV models end to end.
+
+Bars: the store is integer / byte work and BF16 scales: bit-exact.  Attention fp32
+outputs within 1e-4 relative of max |out| (flash-decoding splits and the merge change the
+summation order of the reference's single pass; exp is `expf` on both sides)."""
+import numpy as np
+import pytest
+import torch
+
+import k2t
+import oracle as O
+from model_oracle import OracleModel, random_model
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("hd", [64, 128])
+def test_kv_store_bit_exact(gpu_ctx, bits, hd):
+    print(f"kv_store bits={bits} hd={hd}", flush=True)
+    rng = np.random.default_rng(hd + bits)
+    n = 37
+    heads = (rng.standard_normal((n, hd)) * rng.uniform(0.01, 4.0, (n, 1))).astype(np.float32)
+    heads[5] = 0.0
+    heads[9, :3] *= 50.0  # outliers
+    dh = torch.from_numpy(heads).cuda()
+    if bits == 8:
+        q = torch.zeros((n, hd), dtype=torch.int8, device="cuda")
+        s = torch.zeros(n, dtype=torch.float32, device="cuda")
+    else:
+        q = torch.zeros((n, hd // 2), dtype=torch.uint8, device="cuda")
+        s = torch.zeros((n, hd // 64), dtype=torch.int16, device="cuda")
+    gpu_ctx.kv_store(bits, dh, n, hd, q, s)
+    gpu_ctx.sync()
+    gq, gs = q.cpu().numpy(), s.cpu().numpy()
+    for t in range(n):
+        if bits == 8:
+            rq, rs = O.kv_quant_head(heads[t])
+            assert np.array_equal(gq[t], rq) and np.float32(gs[t]).view(np.uint32) == np.float32(rs).view(np.uint32), t
+        else:
+            rq, rs = O.kv_quant_head_q4(heads[t])
+            assert np.array_equal(gq[t], rq) and np.array_equal(gs[t].view(np.uint16), rs), t
+
+
+def _cache(rng, bits, n_kv, cap, hd, fill):
+    """A cache of n_kv x cap slots with `fill` random heads stored by the oracle."""
+    if bits == 8:
+        kq = np.zeros((n_kv, cap, hd), np.int8)
+        ks = np.zeros((n_kv, cap), np.float32)
+    else:
+        kq = np.full((n_kv, cap, hd // 2), 0x88, np.uint8)
+        ks = np.zeros((n_kv, cap, hd // 64), np.uint16)
+    vq, vs = kq.copy(), ks.copy()
+    for h in range(n_kv):
+        for t in range(fill):
+            k, v = rng.standard_normal(hd).astype(np.float32), rng.standard_normal(hd).astype(np.float32)
+            f = O.kv_quant_head if bits == 8 else O.kv_quant_head_q4
+            kq[h, t], ks[h, t] = f(k)
+            vq[h, t], vs[h, t] = f(v)
+    return kq, ks, vq, vs
+
+
+@pytest.mark.parametrize("bits,hd,seq,window,sinks", [(8, 64, 300, 0, 0), (8, 128, 70, 0, 0), (4, 64, 300, 0, 0),
+                                                      (4, 128, 70, 0, 0), (8, 128, 90, 24, 4), (4, 64, 90, 24, 4)])
+def test_attn_decode_matches_oracle(gpu_ctx, bits, hd, seq, window, sinks):
+    print(f"attn_decode bits={bits} hd={hd} seq={seq} window={window}", flush=True)
+    rng = np.random.default_rng(seq + hd + bits)
+    nq, nkv = 4, 2
+    cap = seq if window == 0 else 40  # ring = cap - sinks slots
+    kq, ks, vq, vs = _cache(rng, bits, nkv, cap, hd, min(seq, cap))
+    q = rng.standard_normal((nq, hd)).astype(np.float32)
+    scale = 1.0 / np.sqrt(hd)
+    out = torch.zeros((nq, hd), dtype=torch.float32, device="cuda")
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    gpu_ctx.attn_decode(bits, dev(q), nq, nkv, hd, dev(kq), dev(ks.view(np.int16) if bits == 4 else ks), dev(vq),
+                        dev(vs.view(np.int16) if bits == 4 else vs), cap, seq, scale, out, window, sinks)
+    got = out.cpu().numpy()
+    ring = cap - sinks
+    if window and seq > window:
+        pos = list(range(sinks)) + list(range(seq - (window - sinks), seq))
+    else:
+        pos = list(range(seq))
+    slots = [p if (not window or p < sinks) else sinks + (p - sinks) % ring for p in pos]
+    for h in range(nq):
+        kv = h // (nq // nkv)
+        if bits == 8:
+            want = O.attn_q8_head(q[h], kq[kv, slots], ks[kv, slots], vq[kv, slots], vs[kv, slots], scale,
+                                  window=bool(window))
+        else:
+            want = O.attn_q4_head(q[h], kq[kv, slots], ks[kv, slots], vq[kv, slots], vs[kv, slots], scale)
+        assert np.abs(got[h] - want).max() <= 1e-4 * np.abs(want).max(), (h, np.abs(got[h] - want).max())
+
+
+@pytest.mark.parametrize("window", [0, 16])
+def test_nf4_kv_model_matches_oracle(gpu_ctx, window):
+    """set_kv_bits(4): the engine stores and reads the NF4 Hadamard KV cache; decode vs the
+    oracle's NF4 cache (with the sliding-window ring when window > 0)."""
+    print(f"nf4 kv model window={window}", flush=True)
+    cfg = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, intermediate=256, vocab=300,
+               max_seq=600, rms_eps=1e-5, rope_theta=10000.0)
+    layers, head, fn = random_model(cfg, seed=31, fmt="nf4")
+    ref = OracleModel(cfg, layers, head, fn, window=window, sinks=4, kv_bits=4)
+    gm = k2t.Model(gpu_ctx, cfg, max_batch=16)
+    mats = []
+    up = lambda m: gpu_ctx.upload_nf(m.rows, m.cols, 4, m.sgc, m.cb, m.pair, m.tail)  # noqa: E731
+    for i, L in enumerate(layers):
+        qm, om, gu, dn = (up(L[k]) for k in ("qkv", "o", "gu", "down"))
+        mats += [qm, om, gu, dn]
+        gm.set_layer(i, qm, om, gu, dn, L["in_norm"], L["post_norm"])
+    hm = up(head)
+    gm.set_head(hm, fn)
+    gm.set_kv_bits(4)
+    if window:
+        gm.set_kv_window(window, 4)
+    assert gm.kv_bits() == 4 and not gm.persistent_active()  # the window keeps the bit width
+    assert gm.kv_window() == ((window, 4) if window else (0, 0))
+    toks = np.random.default_rng(32).integers(0, cfg["vocab"], 40)
+    gm.prefill(toks[:-3], want_logits=False)
+    for t in toks[:-3]:
+        ref.forward_token(int(t))
+    for t in toks[-3:]:
+        a, b = gm.decode(int(t)), ref.forward_token(int(t))
+        cos = float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
+        rel = float(np.abs(a - b).max() / np.abs(b).max())
+        assert cos > 0.9999 and rel <= 2e-2, (cos, rel)
+    gm.close()
+    for m in mats + [hm]:
+        m.close()

@@ -368,3 +368,80 @@ def test_rope_and_swiglu_closed_forms():
     g = np.array([-2.0, 0.0, 3.0], np.float32)
     u = np.array([1.0, 5.0, 2.0], np.float32)
     np.testing.assert_allclose(O.swiglu(g, u), g / (1 + np.exp(-g)) * u, rtol=1e-6)
+
+
+def test_nf4_kv_store_pins():
+    """store_hadamard_q4_head_raw (real_llm.rs:8646-8700): nearest-codebook thresholds are
+    the midpoints of NF4_DEFAULT_CODEBOOK_I8 (brute force), codes are the nearest entries
+    to v / s for the stored BF16 scale, the refined scale is the least-squares fit of
+    the first-pass codes (closed form in f64, then BF16), zero blocks store 0x88 / 0."""
+    import oracle as O
+    cb = np.array([-127, -96, -75, -58, -44, -31, -18, -6, 6, 18, 31, 44, 58, 75, 96, 127], np.float64)
+    for y in np.linspace(-140, 140, 5601):
+        i = O.nf4_nearest_idx(np.float32(y))
+        d = np.abs(cb - y)
+        assert d[i] <= d.min() + 1e-9, (y, i)
+    rng = np.random.default_rng(4)
+    for hd in (64, 128):
+        for trial in range(20):
+            head = (rng.standard_normal(hd) * rng.uniform(0.01, 3.0)).astype(np.float32)
+            q4, s16 = O.kv_quant_head_q4(head)
+            rot = O.fwht64(head)
+            for g in range(hd // 64):
+                blk = rot[g * 64:(g + 1) * 64].astype(np.float64)
+                mx = np.abs(blk).max()
+                c0 = cb[[O.nf4_nearest_idx(np.float32(v) * np.float32(127.0 / np.float32(mx))) for v in blk]]
+                s_ls = (blk * c0).sum() / (c0 * c0).sum()
+                s = (np.uint32(s16[g]) << 16).view(np.float32)
+                assert abs(float(s) - s_ls) <= 2 ** -7 * s_ls  # one BF16 ulp of the LS scale
+                codes = np.zeros(64, np.int64)
+                for h in range(2):
+                    for i in range(16):
+                        b = q4[g * 32 + h * 16 + i]
+                        codes[h * 32 + i], codes[h * 32 + 16 + i] = b & 15, b >> 4
+                # every code is the nearest codebook entry to v / s
+                err = np.abs(cb[codes] * float(s) - blk)
+                best = np.abs(cb[None, :] * float(s) - blk[:, None]).min(axis=1)
+                assert np.all(err <= best + 1e-6 * max(1.0, float(s) * 127))
+    q4, s16 = O.kv_quant_head_q4(np.zeros(64, np.float32))
+    assert np.all(q4 == 0x88) and s16[0] == 0
+
+
+def test_nf4_kv_attention_against_f64():
+    """The NF4-KV attention restatement against f64 softmax attention on the dequantized
+    K / V (codebook value x BF16 block scale, inverse-rotated) with the unquantized
+    query: a dropped scale, a swapped nibble half or a wrong block index fails."""
+    import oracle as O
+    cb = np.array([-127, -96, -75, -58, -44, -31, -18, -6, 6, 18, 31, 44, 58, 75, 96, 127], np.float64)
+    rng = np.random.default_rng(9)
+
+    def deq(q4, s16, hd):
+        out = np.zeros(hd)
+        for g in range(hd // 64):
+            s = float((np.uint32(s16[g]) << 16).view(np.float32))
+            for h in range(2):
+                for i in range(16):
+                    b = q4[g * 32 + h * 16 + i]
+                    out[g * 64 + h * 32 + i] = cb[b & 15] * s
+                    out[g * 64 + h * 32 + 16 + i] = cb[b >> 4] * s
+        return O.ifwht64(out.astype(np.float32)).astype(np.float64)
+
+    for hd in (64, 128):
+        n = 50
+        K = rng.standard_normal((n, hd)).astype(np.float32)
+        V = rng.standard_normal((n, hd)).astype(np.float32)
+        q = rng.standard_normal(hd).astype(np.float32)
+        k4, ks, v4, vs = [], [], [], []
+        for t in range(n):
+            a, b = O.kv_quant_head_q4(K[t])
+            c, d = O.kv_quant_head_q4(V[t])
+            k4.append(a), ks.append(b), v4.append(c), vs.append(d)
+        scale = 1.0 / np.sqrt(hd)
+        got = O.attn_q4_head(q, np.array(k4), np.array(ks), np.array(v4), np.array(vs), scale)
+        Kd = np.stack([deq(k4[t], ks[t], hd) for t in range(n)])
+        Vd = np.stack([deq(v4[t], vs[t], hd) for t in range(n)])
+        z = Kd @ q.astype(np.float64) * scale
+        p = np.exp(z - z.max())
+        want = (p / p.sum()) @ Vd
+        cos = np.dot(got, want) / (np.linalg.norm(got) * np.linalg.norm(want))
+        assert cos > 0.999, (hd, cos)
