@@ -2,6 +2,7 @@
 // Mirrors the FFI conventions of src/ffi/mobile_ffi.rs:76-168 (i32 status codes, a
 // thread-local last error, catch-all at every entry, destroy(NULL) is a no-op).
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>

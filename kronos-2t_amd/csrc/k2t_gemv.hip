@@ -200,6 +200,49 @@ struct XBuilder {
     }
 };
 
+// XS 3: a ready int8 activation in global memory (one token), staged through LDS.  Each
+// wave copies the codes, scales and sums of its own chunks [c0, c1) once (c1 - c0 <= 32),
+// so the chunk loop issues only weight loads.
+template <int FMT>
+struct XStage {
+    const GemvParams &P;
+    int tok, c0, c1;
+    uint32_t lane;
+    uint4 q[2];
+    float sx;
+    int32_t sm;
+
+    __device__ XStage(const GemvParams &P_, int tok_, int c0_, int c1_, uint32_t lane_)
+        : P(P_), tok(tok_), c0(c0_), c1(c1_), lane(lane_) {}
+
+    __device__ void begin() {
+        const int n = c1 - c0, n_u4 = n * 4;
+        const uint4 *src = reinterpret_cast<const uint4 *>(P.xq + (size_t)tok * P.K + (size_t)c0 * 64);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i = (int)lane + 64 * j;
+            q[j] = i < n_u4 ? src[i] : make_uint4(0, 0, 0, 0);
+        }
+        sx = (int)lane < n ? P.xs[(size_t)tok * P.nc + c0 + lane] : 0.0f;
+        sm = 0;
+        if constexpr (FMT == 0) sm = (int)lane < n ? P.xsum[(size_t)tok * P.nc + c0 + lane] : 0;
+    }
+
+    __device__ void finish(int8_t *xl, float *xsl, int32_t *xsuml) {
+        const int n = c1 - c0, n_u4 = n * 4;
+        uint4 *dst = reinterpret_cast<uint4 *>(xl + (size_t)c0 * 64);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i = (int)lane + 64 * j;
+            if (i < n_u4) dst[i] = q[j];
+        }
+        if ((int)lane < n) {
+            xsl[c0 + lane] = sx;
+            xsuml[c0 + lane] = sm;
+        }
+    }
+};
+
 // Registers of one fetched chunk for one lane: its 64 nibble bytes (rows 4g..4g+3,
 // the lane's 8-column half of each of the four 16-column blocks), hi-plane bytes, the
 // BF16 scales of its two output rows and the matching activation bytes.
@@ -469,7 +512,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     if constexpr (NT == 1) {
         // Two fragments in flight: chunk i+1 is fetched before chunk i is processed.
         Frag<HP, NT> fa, fb;
-        if constexpr (XS != 0) {
+        if constexpr (XS == 3) {
+            XStage<FMT> xb(P, tok0, cw0, cw1, lane);
+            xb.begin();
+            if (valid(0)) fetch(fa, chunk_of(0));
+            if (valid(1)) fetch(fb, chunk_of(1));
+            xb.finish(xl, xsl, xsuml);
+            __builtin_amdgcn_wave_barrier();
+        } else if constexpr (XS != 0) {
             // Source loads first, then the first weight loads; the wave builds its
             // activation while the weights are in flight.
             XBuilder<XS> xb(P, xsrc_p, tok0, cw0, cw1, lane);
@@ -614,6 +664,10 @@ static void launch_nt(int nt, int xs, dim3 grid, dim3 block, size_t lds, hipStre
         hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, false, K2T_XS_SWIGLU>), grid, block, lds, st, P);
         return;
     }
+    if (xs == K2T_XS_STAGED) {
+        hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, false, K2T_XS_STAGED>), grid, block, lds, st, P);
+        return;
+    }
     switch (nt) {
         case 1: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, DOTS, 0>), grid, block, lds, st, P); break;
         case 2: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 2, false, 0>), grid, block, lds, st, P); break;
@@ -700,12 +754,15 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
     size_t per_tok = ctx->exact ? (size_t)m->nc * (plan.stripe_mode ? 16 : 32) * sizeof(float2)
                                 : (size_t)plan.nseg * 32 * sizeof(float);
     int G = (int)std::max<size_t>(1, std::min<size_t>(4, (64 * 1024) / per_tok));
+    // One token from a ready int8 activation: stage it through LDS (XS 3) when each wave's
+    // chunk range fits the staging registers.
+    if (xsm == 0 && ntok == 1 && !dots && !grp && plan.cps <= 32 && ctx->stage_x) xsm = K2T_XS_STAGED;
     if (xsm != 0) {  // one token; its int8 activation is built in LDS after the terms
         if (ntok != 1 || m->cols > kSignBlocks * 64 || !ctx->signs) throw Error(K2T_E_INTERNAL, "fused gemv shape");
         P.xsrc = src;
         P.xnorm = w;
         P.eps = eps;
-        P.signs = ctx->signs;
+        P.signs = ctx->signs;  // (XS 3 reads P.xq / P.xs / P.xsum set above)
         P.xoff = (int)((per_tok + 15) / 16 * 16);
         per_tok = (size_t)P.xoff + (size_t)m->cols + 8 * (size_t)m->nc;
         G = 1;

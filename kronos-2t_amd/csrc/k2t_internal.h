@@ -13,6 +13,7 @@ struct k2t_ctx {
     hipStream_t stream = nullptr;
     int max_segments = 0;  // cap on waves (K segments) per GEMV workgroup; 0 = automatic
     int exact = 0;         // 1: bit-exact fmaf-chain epilogue
+    int stage_x = 1;       // 1: single-token GEMVs stage the int8 activation through LDS
     int num_cus = 256;
     // small device scratch (debug entry points): grown on demand
     float *scratch = nullptr;
@@ -69,7 +70,8 @@ void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *
 //   K2T_XS_RMSNORM: src = hidden[K], w = norm weights -> RMSNorm + FWHT + int8
 //   K2T_XS_SWIGLU : src = interleaved gate_up[2K]      -> SwiGLU + FWHT + int8
 // Codes equal those of rmsnorm_act / swiglu_act followed by launch_gemv.
-enum { K2T_XS_GLOBAL = 0, K2T_XS_RMSNORM = 1, K2T_XS_SWIGLU = 2 };
+//   K2T_XS_STAGED : a ready int8 activation (xq, xs, xsum) staged through LDS per wave
+enum { K2T_XS_GLOBAL = 0, K2T_XS_RMSNORM = 1, K2T_XS_SWIGLU = 2, K2T_XS_STAGED = 3 };
 void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float *src, const float *w, float eps,
                        float *out, bool accumulate);
 uint64_t hadamard_sign_mask_host(uint64_t block);
