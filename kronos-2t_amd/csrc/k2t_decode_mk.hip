@@ -461,6 +461,16 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     return true;
 }
 
+// Stripe-mode task order with both stripes of a pair on one XCD: with one stripe per
+// workgroup, tasks t and t + 8 run on workgroups 8 apart (the same XCD), so the L2 lines
+// shared by the two halves of a record are fetched from HBM once.
+__device__ __forceinline__ int xcd_stripe(const MatDev &M, int t, int nblocks) {
+    // (with two or more stripes per workgroup, consecutive tasks already pair up)
+    if (!M.smode || M.nseg != kWaves || (nblocks & 15) != 0 || t >= nblocks) return t;
+    const int a = t >> 4, s8 = (t >> 3) & 1, j = t & 7;
+    return 2 * (8 * a + j) + s8;
+}
+
 // FMT/HP: the one weight format every projection and the head use (mixed-format models
 // run the one-kernel-per-operation path).
 template <int FMT, int HP>
@@ -517,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
         const int RB = M.smode ? 16 : 32;
         bool ok = true;
         for (int base = vb * groups; base < nblocks; base += nwg * groups) {
-            const int rb = base + grp;
+            const int rb = xcd_stripe(M, base + grp, nblocks);
             const bool first = base == vb * groups;
             // The first round requests its first weight fragments, then waits for the
             // phase input (the weights stream in meanwhile), then computes.
@@ -534,7 +544,7 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
 #undef MK_ROUND
             __syncthreads();
             if (t < groups * RB) {
-                const int g2 = t / RB, rl = t % RB, rb2 = base + g2;
+                const int g2 = t / RB, rl = t % RB, rb2 = xcd_stripe(M, base + g2, nblocks);
                 if (rb2 < nblocks) {
                     const bool tail = !M.smode && rb2 >= M.np;
                     const int first_stripe = M.smode ? rb2 : (tail ? 2 * M.np : 2 * rb2);

@@ -281,7 +281,15 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     // Pair mode: lane bit 3 = stripe of the pair, bits 4-5 = sub-segment (4 per wave).
     // Stripe mode: bits 3-5 = sub-segment (8 per wave); the workgroup owns one stripe.
     const bool smode = P.stripe_mode != 0;
-    const int rb = P.rb_lo + (int)blockIdx.x;  // pair index, or stripe index in stripe mode
+    // Stripe mode: both stripes of a pair run on one XCD (workgroups are dispatched
+    // round-robin over the 8 XCDs by id), so the L2 lines shared by the two halves of a
+    // record are fetched from HBM once.  Ids 16a + 8s + j (j < 8) take stripe 2(8a + j) + s.
+    int rbi = (int)blockIdx.x;
+    if (P.stripe_mode && (gridDim.x & 15u) == 0) {
+        const int a = rbi >> 4, s8 = (rbi >> 3) & 1, j = rbi & 7;
+        rbi = 2 * (8 * a + j) + s8;
+    }
+    const int rb = P.rb_lo + rbi;  // pair index, or stripe index in stripe mode
     const bool is_tail = smode ? rb >= 2 * P.np : rb >= P.np;
     const uint32_t lane_side = smode ? 0u : (lane >> 3) & 1u;
     const uint32_t side = smode ? (uint32_t)(rb & 1) : (is_tail ? 0u : lane_side);
