@@ -781,8 +781,12 @@ int32_t k2t_model_prefill(k2t_model *m, const int32_t *tokens, int32_t n, float 
         for (int i = 0; i < n; i++) arg(tokens[i] >= 0 && tokens[i] < m->cfg.vocab, "token out of range");
         hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
         StreamSwap sw(m);
-        for (int i0 = 0; i0 < n; i0 += m->max_batch) {
-            const int nb = std::min(m->max_batch, n - i0);
+        // A batch stores all its K/V before any of its tokens attends.  With the window ring
+        // that is safe for up to the ring's batch slack (512 slots) of tokens: beyond it a
+        // later token would overwrite a slot an earlier one still reads.
+        const int chunk = m->ring.window > 0 ? std::min(m->max_batch, 512) : m->max_batch;
+        for (int i0 = 0; i0 < n; i0 += chunk) {
+            const int nb = std::min(chunk, n - i0);
             hip_check(hipMemcpyAsync(m->tokens, tokens + i0, nb * sizeof(int), hipMemcpyHostToDevice, m->stream),
                       "token upload");
             forward(m, nb, i0 + nb == n);

@@ -128,3 +128,86 @@ def test_nf4_kv_model_matches_oracle(gpu_ctx, window):
     gm.close()
     for m in mats + [hm]:
         m.close()
+
+
+def _tiny_nf4_model(gpu_ctx, cfg, seed, max_batch):
+    layers, head, fn = random_model(cfg, seed=seed, fmt="nf4")
+    gm = k2t.Model(gpu_ctx, cfg, max_batch=max_batch)
+    mats = []
+    up = lambda m: gpu_ctx.upload_nf(m.rows, m.cols, 4, m.sgc, m.cb, m.pair, m.tail)  # noqa: E731
+    for i, L in enumerate(layers):
+        qm, om, gu, dn = (up(L[k]) for k in ("qkv", "o", "gu", "down"))
+        mats += [qm, om, gu, dn]
+        gm.set_layer(i, qm, om, gu, dn, L["in_norm"], L["post_norm"])
+    hm = up(head)
+    gm.set_head(hm, fn)
+    return gm, mats + [hm]
+
+
+def _mk_bf16(n, seed, scale):
+    """The reference test's weight generator (real_llm.rs:10500-10511): SplitMix64 of
+    i + seed * 0x9E3779B97F4A7C15, top 24 bits -> u in [0, 1), (2u - 1) * scale, BF16."""
+    M = (1 << 64) - 1
+    i = np.arange(n, dtype=np.uint64)
+    z = (i + np.uint64((seed * 0x9E3779B97F4A7C15) & M)) & np.uint64(M)
+    z = ((z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)) & np.uint64(M)
+    z = ((z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)) & np.uint64(M)
+    z = z ^ (z >> np.uint64(31))
+    u = (z >> np.uint64(40)).astype(np.float32) / np.float32(1 << 24)
+    v = ((np.float32(2.0) * u - np.float32(1.0)) * np.float32(scale)).astype(np.float32)
+    b = v.view(np.uint32)
+    b16 = ((b + np.uint32(0x7FFF) + ((b >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    return b16
+
+
+def test_reference_kv_invariants(gpu_ctx):
+    """The reference's own KV test (real_llm.rs:10480-10625) on the GPU engine, with its
+    model: vocab 192, hidden 256, 2 layers, 2 heads / 1 KV head of 128, ffn 512, weights
+    from its generator (uniform, BF16; untied BF16 embedding and lm_head), compiled here
+    with the NF4 g128 RTN compiler (the reference uses GPTQ).  Its bars: Q4-KV vs Q8-KV
+    prefill logits cosine > 0.998; with Q4 KV and a 16-token window with 4 sinks, a
+    640-token batched prefill (past the 528-slot ring) equals token-by-token decode at
+    cosine > 0.9999."""
+    print("reference kv invariants", flush=True)
+    V, h, inter, nl, kvd = 192, 256, 512, 2, 128
+    cfg = dict(n_layers=nl, hidden=h, n_heads=2, n_kv_heads=1, head_dim=128, intermediate=inter, vocab=V,
+               max_seq=1024, rms_eps=1e-5, rope_theta=100000.0)
+    f32 = lambda b16: (b16.astype(np.uint32) << 16).view(np.float32)  # noqa: E731
+    gm = k2t.Model(gpu_ctx, cfg, max_batch=64)
+    mats = []
+
+    def nf4(W, gu=False):
+        cb, _, pair, tail = k2t.compile_nf4(np.ascontiguousarray(W, np.float32), 2, interleave_gate_up=gu)
+        m = gpu_ctx.upload_nf(W.shape[0], W.shape[1], 4, 2, cb, pair, tail)
+        mats.append(m)
+        return m
+
+    for l in range(nl):
+        q = f32(_mk_bf16(h * h, 13 + l, 0.08)).reshape(h, h)
+        k = f32(_mk_bf16(kvd * h, 17 + l, 0.08)).reshape(kvd, h)
+        v = f32(_mk_bf16(kvd * h, 19 + l, 0.08)).reshape(kvd, h)
+        o = f32(_mk_bf16(h * h, 41 + l, 0.08)).reshape(h, h)
+        g = f32(_mk_bf16(inter * h, 43 + l, 0.08)).reshape(inter, h)
+        u = f32(_mk_bf16(inter * h, 47 + l, 0.08)).reshape(inter, h)
+        d = f32(_mk_bf16(h * inter, 53 + l, 0.055)).reshape(h, inter)
+        gm.set_layer(l, nf4(np.concatenate([q, k, v])), nf4(o), nf4(np.concatenate([g, u]), gu=True), nf4(d),
+                     f32(_mk_bf16(h, 7 + l, 1.0)), f32(_mk_bf16(h, 11 + l, 1.0)))
+    gm.set_embedding(k2t.EMBED_BF16, _mk_bf16(V * h, 31, 0.4))
+    gm.set_head(nf4(f32(_mk_bf16(V * h, 61, 0.3)).reshape(V, h)), f32(_mk_bf16(h, 59, 1.0)))
+    cos = lambda a, b: float(np.dot(a.astype(np.float64), b) / (np.linalg.norm(a) * np.linalg.norm(b)))  # noqa: E731
+    prompt = np.array([(i * 11 + 3) % V for i in range(24)], np.int32)
+    gm.set_kv_bits(8)
+    l8 = gm.prefill(prompt)
+    gm.set_kv_bits(4)
+    l4 = gm.prefill(prompt)
+    assert cos(l8, l4) > 0.998, cos(l8, l4)
+    long_seq = np.array([(i * 13 + 5) % V for i in range(640)], np.int32)
+    gm.set_kv_window(16, 4)
+    lb = gm.prefill(long_seq)
+    gm.set_kv_window(16, 4)  # resets the position
+    for t in long_seq:
+        ls = gm.decode(int(t))
+    assert cos(lb, ls) > 0.9999, cos(lb, ls)
+    gm.close()
+    for m in mats:
+        m.close()
