@@ -211,3 +211,47 @@ def test_reference_kv_invariants(gpu_ctx):
     gm.close()
     for m in mats:
         m.close()
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_reference_q8_kv_attention_accuracy(gpu_ctx, hd):
+    """test_hadamard_q8_kv_cache_attention_accuracy (real_llm.rs:10190-10284) with its own
+    inputs: 6 q heads over 2 KV heads, K/V/q from f(i, m) = ((i*m % 101)/101 - 0.5)*1.6 with
+    columns 7 and hd/2 + 7 scaled x12, 37 cached positions; the GPU's Hadamard int8 store
+    + decode attention against fp32 attention on the unquantized K/V at cosine > 0.9998
+    (the reference's bar) for pos 0, 7, 15, 36."""
+    heads, kvh, n_max = 6, 2, 37
+    kv_dim = kvh * hd
+    scale = 1.0 / np.sqrt(np.float32(hd))
+
+    def f(i, m):
+        i = np.asarray(i, np.int64)
+        base = ((i * m % 101).astype(np.float32) / np.float32(101.0) - np.float32(0.5)) * np.float32(1.6)
+        col = i % hd
+        return np.where((col == 7) | (col == hd // 2 + 7), base * np.float32(12.0), base).astype(np.float32)
+
+    k_all = f(np.arange(n_max * kv_dim), 19).reshape(n_max, kvh, hd)
+    v_all = f(np.arange(n_max * kv_dim), 29).reshape(n_max, kvh, hd)
+    # cache layout [kv head][slot]: store each head's 37 rows
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    kq = torch.zeros((kvh, n_max, hd), dtype=torch.int8, device="cuda")
+    vq = torch.zeros((kvh, n_max, hd), dtype=torch.int8, device="cuda")
+    ks = torch.zeros((kvh, n_max), dtype=torch.float32, device="cuda")
+    vs = torch.zeros((kvh, n_max), dtype=torch.float32, device="cuda")
+    for h in range(kvh):
+        gpu_ctx.kv_store(8, dev(k_all[:, h]), n_max, hd, kq[h], ks[h])
+        gpu_ctx.kv_store(8, dev(v_all[:, h]), n_max, hd, vq[h], vs[h])
+    out = torch.zeros((heads, hd), dtype=torch.float32, device="cuda")
+    for pos in (0, 7, 15, 36):
+        q = f(np.arange(heads * hd) + pos * 13, 37).reshape(heads, hd)
+        gpu_ctx.attn_decode(8, dev(q), heads, kvh, hd, kq, ks, vq, vs, n_max, pos + 1, float(scale), out)
+        got = out.cpu().numpy().astype(np.float64).ravel()
+        want = np.zeros((heads, hd))
+        for h in range(heads):
+            g = h // (heads // kvh)
+            K, V = k_all[:pos + 1, g].astype(np.float64), v_all[:pos + 1, g].astype(np.float64)
+            z = K @ q[h].astype(np.float64) * float(scale)
+            p = np.exp(z - z.max())
+            want[h] = (p / p.sum()) @ V
+        cos = float(np.dot(got, want.ravel()) / (np.linalg.norm(got) * np.linalg.norm(want)))
+        assert cos > 0.99980, (hd, pos, cos)
