@@ -23,9 +23,10 @@ void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float ep
 void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
                      const float *rope, const int *pos_dev, int nq,
                      int nkv, int hd, int ntok, int layer, KvRing kr, int8_t *kq, int8_t *vq, float *ks, float *vs);
-void launch_attention(hipStream_t st, const float *q, int q_stride, const int8_t *kq, const int8_t *vq, const float *ks,
-                      const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr, float attn_scale,
-                      int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum);
+void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
+                      const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
+                      float attn_scale, int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as,
+                      int32_t *asum);
 int attn_max_splits(int max_seq);
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums);
 void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok, float *out);
@@ -224,10 +225,17 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
             launch_rmsnorm_act(st, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
             launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false);
         }
-        launch_qkv_post(st, m->qkv, L.bias, L.q_norm, L.k_norm, c.rms_eps, m->rope, m->pos_dev, nq, nkv, hd, ntok, l,
-                        m->ring, m->kq, m->vq, m->ks, m->vs);
-        launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, m->pos_dev, l, nq, nkv, hd,
-                         m->ring, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum);
+        // One token: qkv_post's work runs inside the attention kernel.  A batch stores every
+        // token's K / V first (a later token of the batch attends to them).
+        AttnPost post{};
+        if (ntok == 1) {
+            post = AttnPost{1, L.bias, L.q_norm, L.k_norm, m->rope, c.rms_eps};
+        } else {
+            launch_qkv_post(st, m->qkv, L.bias, L.q_norm, L.k_norm, c.rms_eps, m->rope, m->pos_dev, nq, nkv, hd, ntok,
+                            l, m->ring, m->kq, m->vq, m->ks, m->vs);
+        }
+        launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, post, m->pos_dev, l, nq, nkv,
+                         hd, m->ring, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum);
         launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
         if (L.has_moe) {
             // one token at a time: each token has its own routes (forward_layer_single)
@@ -913,9 +921,10 @@ int32_t k2t_attn_decode(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_
         int *pos = reinterpret_cast<int *>(ctx->scratch + part);
         const int p0 = seq - 1;
         hip_check(hipMemcpyAsync(pos, &p0, sizeof(int), hipMemcpyHostToDevice, ctx->stream), "pos upload");
-        launch_attention(ctx->stream, d_q, n_heads * head_dim, (const int8_t *)d_kq, (const int8_t *)d_vq,
-                         (const float *)d_ks, (const float *)d_vs, pos, 0, n_heads, n_kv_heads, head_dim, kr,
-                         attn_scale, nsplit, 1, pp, d_out, nullptr, nullptr, nullptr);
+        // read-only on the cache (no post stage: the caller's queries are final)
+        launch_attention(ctx->stream, d_q, n_heads * head_dim, (int8_t *)d_kq, (int8_t *)d_vq, (float *)d_ks,
+                         (float *)d_vs, AttnPost{}, pos, 0, n_heads, n_kv_heads, head_dim, kr, attn_scale, nsplit, 1,
+                         pp, d_out, nullptr, nullptr, nullptr);
         hip_check(hipStreamSynchronize(ctx->stream), "sync");  // the position lives in host memory above
     });
 }

@@ -101,6 +101,14 @@ struct KvRing {
     int cap, window, sinks, ring, bits;
 };
 
+// One-token decode attention that also does qkv_post's work (bias, QK-norm, RoPE, K/V
+// store): q is then the raw qkv row.
+struct AttnPost {
+    int on;
+    const float *bias, *qn, *kn, *rope;
+    float eps;
+};
+
 // The model takes ownership of `mat` (destroyed with the model).
 void model_adopt(k2t_model *m, k2t_mat *mat);
 

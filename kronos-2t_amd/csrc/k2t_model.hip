@@ -141,25 +141,21 @@ void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float ep
 // optional bias, RoPE on q and k (real_llm.rs:9328-9361, half-split), then k and v go
 // through store_hadamard_q8_head (real_llm.rs:8282-8365) into the cache slot of `pos`.
 // Positions are read from `pos_dev` (+ token index) so a captured graph can replay.
-__global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, const float *__restrict__ bias,
-                                                      const float *__restrict__ qn, const float *__restrict__ kn,
-                                                      float eps, const float *__restrict__ rope,
-                                                      const int *__restrict__ pos_dev, int nq, int nkv, int hd,
-                                                      int row_stride, int layer, KvRing kr, int8_t *__restrict__ kq,
-                                                      int8_t *__restrict__ vq, float *__restrict__ ks,
-                                                      float *__restrict__ vs) {
-    const uint32_t lane = threadIdx.x;
-    const int head = blockIdx.x, tok = blockIdx.y;
-    const int pos = pos_dev[0] + tok;
-    float *h = qkv + (size_t)tok * row_stride + (size_t)head * hd;
-    const int nb = hd / 64;  // 1 or 2 blocks; lane holds element lane (+64)
-    float v0 = h[lane], v1 = nb > 1 ? h[64 + lane] : 0.0f;
+// Bias, per-head q / k RMSNorm (apply_qk_norm_rope / apply_per_head_rms_norm,
+// real_llm.rs:8139-8178: inv_rms = 1/sqrt(sum(v^2) * (1/hd) + eps), v = (v*inv_rms)*w,
+// before RoPE) and RoPE (q and k heads) of one head of a qkv row; lane holds elements
+// lane and 64 + lane.
+__device__ __forceinline__ void head_post(const float *__restrict__ h, int head, int nq, int nkv, int hd,
+                                          const float *__restrict__ bias, const float *__restrict__ qn,
+                                          const float *__restrict__ kn, float eps, const float *__restrict__ rope,
+                                          int pos, uint32_t lane, float &v0, float &v1) {
+    const int nb = hd / 64;
+    v0 = h[lane];
+    v1 = nb > 1 ? h[64 + lane] : 0.0f;
     if (bias) {
         v0 = v0 + bias[head * hd + lane];
         if (nb > 1) v1 = v1 + bias[head * hd + 64 + lane];
     }
-    // Per-head RMSNorm of q and k before RoPE (apply_qk_norm_rope / apply_per_head_rms_norm,
-    // real_llm.rs:8139-8178): inv_rms = 1/sqrt(sum(v^2) * (1/hd) + eps), v = (v*inv_rms)*w.
     const float *hn = head < nq ? qn : (head < nq + nkv ? kn : nullptr);
     if (hn) {
         float ss = v0 * v0;
@@ -183,6 +179,22 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, c
             v1 = x1 * c + x0 * s;
         }
     }
+}
+
+__global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, const float *__restrict__ bias,
+                                                      const float *__restrict__ qn, const float *__restrict__ kn,
+                                                      float eps, const float *__restrict__ rope,
+                                                      const int *__restrict__ pos_dev, int nq, int nkv, int hd,
+                                                      int row_stride, int layer, KvRing kr, int8_t *__restrict__ kq,
+                                                      int8_t *__restrict__ vq, float *__restrict__ ks,
+                                                      float *__restrict__ vs) {
+    const uint32_t lane = threadIdx.x;
+    const int head = blockIdx.x, tok = blockIdx.y;
+    const int pos = pos_dev[0] + tok;
+    float *h = qkv + (size_t)tok * row_stride + (size_t)head * hd;
+    const int nb = hd / 64;  // 1 or 2 blocks; lane holds element lane (+64)
+    float v0, v1;
+    head_post(h, head, nq, nkv, hd, bias, qn, kn, eps, rope, pos, lane, v0, v1);
     if (head < nq) {
         h[lane] = v0;
         if (nb > 1) h[64 + lane] = v1;
@@ -228,12 +240,14 @@ void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float 
 constexpr int kAttnSplitLen = 256;
 
 __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restrict__ q, int q_stride,
-                                                           const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
-                                                           const float *__restrict__ ks, const float *__restrict__ vs,
+                                                           int8_t *__restrict__ kq, int8_t *__restrict__ vq,
+                                                           float *__restrict__ ks, float *__restrict__ vs,
                                                            const int *__restrict__ pos_dev, int layer, int nq, int nkv,
                                                            int hd, KvRing kr, float attn_scale, int nsplit,
-                                                           float *__restrict__ part) {
+                                                           AttnPost post, float *__restrict__ part) {
     __shared__ __align__(16) int8_t qi[128];
+    __shared__ __align__(16) int8_t kcur[128], vcur[128];  // current position's K / V (post.on)
+    __shared__ float cur_s[4];                              // their scales (f32, or BF16 pairs)
     __shared__ float qas_s;
     __shared__ float sc[kAttnSplitLen];
     __shared__ float red[8];
@@ -273,9 +287,36 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     const int kvh = head / (nq / nkv);
     const float *qh = q + (size_t)tok * q_stride + (size_t)head * hd;
     const int nb = hd / 64;
+    // post.on (one token): q is the raw qkv row; this workgroup applies bias, QK-norm and
+    // RoPE to its q head, and the workgroups whose split holds the current position build
+    // its K / V (qkv_post's arithmetic) in LDS; the first q head of each KV group writes
+    // them to the cache.  No workgroup reads the current position's slot from memory.
+    const int cur = act - 1;
+    const bool covers = post.on && t0 <= cur && cur < t1;
+    if (covers && (wv == 1 || wv == 2)) {
+        const int hh = wv == 1 ? nq + kvh : nq + nkv + kvh;
+        float a0, a1;
+        head_post(q + (size_t)tok * q_stride + (size_t)hh * hd, hh, nq, nkv, hd, post.bias, post.qn, post.kn,
+                  post.eps, post.rope, seq - 1, lane, a0, a1);
+        const float r0 = fwht_lane(a0, 0, lane);
+        const float r1 = nb > 1 ? fwht_lane(a1, 1, lane) : 0.0f;
+        kv_store_head(r0, r1, nb, lane, kr.bits, hd, 0, wv == 1 ? kcur : vcur, wv == 1 ? cur_s : cur_s + 2);
+        if (head % (nq / nkv) == 0) {
+            const size_t slot = ((size_t)layer * nkv + kvh) * kr.cap + ring_slot(kr, seq - 1);
+            kv_store_head(r0, r1, nb, lane, kr.bits, hd, slot, wv == 1 ? kq : vq, wv == 1 ? ks : vs);
+        }
+    }
     if (wv == 0) {
-        const float r0 = fwht_lane(qh[lane], 0, lane);
-        const float r1 = nb > 1 ? fwht_lane(qh[64 + lane], 1, lane) : 0.0f;
+        float qv0, qv1;
+        if (post.on) {
+            head_post(qh, head, nq, nkv, hd, post.bias, post.qn, post.kn, post.eps, post.rope, seq - 1, lane, qv0,
+                      qv1);
+        } else {
+            qv0 = qh[lane];
+            qv1 = nb > 1 ? qh[64 + lane] : 0.0f;
+        }
+        const float r0 = fwht_lane(qv0, 0, lane);
+        const float r1 = nb > 1 ? fwht_lane(qv1, 1, lane) : 0.0f;
         const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
         float qs = 0.0f;
         if (mx <= FLT_EPSILON) {
@@ -302,9 +343,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
         if (t < t1 && kr.bits == 4) {
             // NF4 KV (causal_gqa_group_q4_or_window, real_llm.rs:8827-8849): per 64-block
             // dot of the codebook values with q, total += float(dot) * ks_g * qs
+            const bool here = covers && t == cur;
             const size_t sl = base + slot_of(t);
-            const uint8_t *k4 = reinterpret_cast<const uint8_t *>(kq) + sl * (size_t)(hd / 2);
-            const uint16_t *k16 = reinterpret_cast<const uint16_t *>(ks) + sl * (size_t)nb;
+            const uint8_t *k4 = here ? reinterpret_cast<const uint8_t *>(kcur)
+                                     : reinterpret_cast<const uint8_t *>(kq) + sl * (size_t)(hd / 2);
+            const uint16_t *k16 = here ? reinterpret_cast<const uint16_t *>(cur_s)
+                                       : reinterpret_cast<const uint16_t *>(ks) + sl * (size_t)nb;
             float s = 0.0f;
             for (int g = 0; g < nb; g++) {
                 const uint4 *kp = reinterpret_cast<const uint4 *>(k4 + g * 32);
@@ -330,8 +374,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
             sc[tid] = s;
             smax = s;
         } else if (t < t1) {
+            const bool here = covers && t == cur;
             const size_t sl = base + slot_of(t);
-            const uint4 *krow = reinterpret_cast<const uint4 *>(kq + sl * hd);
+            const uint4 *krow = here ? reinterpret_cast<const uint4 *>(kcur) : reinterpret_cast<const uint4 *>(kq + sl * hd);
             const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
             int dot[2] = {0, 0};
             for (int i = 0; i < hd / 16; i++) {
@@ -343,8 +388,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
                 d = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, d, false);
                 dot[i >> 2] = d;
             }
-            const float kscale = ks[sl];
-            vscale = vs[sl];
+            const float kscale = here ? cur_s[0] : ks[sl];
+            vscale = here ? cur_s[2] : vs[sl];
             float s;
             if (kr.window > 0 && hd == 128)  // per-64-block terms (causal_gqa_group_q4_or_window, 8823-8868)
                 s = ((float)dot[0] * kscale) * qas + ((float)dot[1] * kscale) * qas;
@@ -384,11 +429,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
         const uint8_t *v4 = reinterpret_cast<const uint8_t *>(vq) + base * (size_t)(hd / 2) + off;
         const uint16_t *v16 = reinterpret_cast<const uint16_t *>(vs) + base * (size_t)nb + g;
         for (; i < n; i += nps) {
+            const bool here = covers && t0 + i == cur;
             const size_t sl = slot_of(t0 + i);
-            const uint32_t d = *reinterpret_cast<const uint32_t *>(v4 + sl * (size_t)(hd / 2));
+            const uint32_t d = here ? *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint8_t *>(vcur) + off)
+                                    : *reinterpret_cast<const uint32_t *>(v4 + sl * (size_t)(hd / 2));
             const uint32_t c = upper ? lut16((d >> 4) & 0x07070707u, bit7_mask(d), kNf4Cb0, kNf4Cb1, kNf4Cb2, kNf4Cb3)
                                      : lut16(d & 0x07070707u, bit3_mask(d), kNf4Cb0, kNf4Cb1, kNf4Cb2, kNf4Cb3);
-            const float wt = sc[i] * __uint_as_float((uint32_t)v16[sl * (size_t)nb] << 16);
+            const uint16_t vsb = here ? reinterpret_cast<const uint16_t *>(cur_s + 2)[g] : v16[sl * (size_t)nb];
+            const float wt = sc[i] * __uint_as_float((uint32_t)vsb << 16);
             a0 = fmaf(wt, (float)(int8_t)(c & 0xFF), a0);
             a1 = fmaf(wt, (float)(int8_t)((c >> 8) & 0xFF), a1);
             a2 = fmaf(wt, (float)(int8_t)((c >> 16) & 0xFF), a2);
@@ -400,7 +448,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
         float ww[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            vv[u] = *reinterpret_cast<const int *>(vcol + slot_of(t0 + i + u * nps) * hd);
+            const int idx = t0 + i + u * nps;
+            vv[u] = covers && idx == cur ? *reinterpret_cast<const int *>(vcur + cg * 4)
+                                         : *reinterpret_cast<const int *>(vcol + slot_of(idx) * hd);
             ww[u] = sc[i + u * nps];
         }
 #pragma unroll
@@ -412,7 +462,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
         }
     }
     for (; kr.bits != 4 && i < n; i += nps) {
-        const int v = *reinterpret_cast<const int *>(vcol + slot_of(t0 + i) * hd);
+        const int v = covers && t0 + i == cur ? *reinterpret_cast<const int *>(vcur + cg * 4)
+                                              : *reinterpret_cast<const int *>(vcol + slot_of(t0 + i) * hd);
         const float wt = sc[i];
         a0 = fmaf(wt, (float)(int8_t)(v & 0xFF), a0);
         a1 = fmaf(wt, (float)(int8_t)((v >> 8) & 0xFF), a1);
@@ -499,11 +550,12 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
 
 int attn_max_splits(int max_seq) { return (max_seq + kAttnSplitLen - 1) / kAttnSplitLen; }
 
-void launch_attention(hipStream_t st, const float *q, int q_stride, const int8_t *kq, const int8_t *vq, const float *ks,
-                      const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr, float attn_scale,
+void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
+                      const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
+                      float attn_scale,
                       int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum) {
     hipLaunchKernelGGL(attn_partial_kernel, dim3(nq, nsplit, ntok), dim3(256), 0, st, q, q_stride, kq, vq, ks, vs,
-                       pos_dev, layer, nq, nkv, hd, kr, attn_scale, nsplit, part);
+                       pos_dev, layer, nq, nkv, hd, kr, attn_scale, nsplit, post, part);
     hip_check(hipGetLastError(), "attn_partial launch");
     hipLaunchKernelGGL(attn_merge_kernel, dim3(nq, ntok), dim3(64), 0, st, part, nq, hd, nsplit, kr, pos_dev, out_f, aq, as,
                        asum);
