@@ -36,6 +36,7 @@ def parse():
     ap.add_argument("--decode-only", action="store_true", help="skip the GEMV sweep and the 135M run (profiling)")
     ap.add_argument("--moe-only", action="store_true", help="run only the config-5 MoE decode (profiling)")
     ap.add_argument("--no-moe", action="store_true", help="skip the config-5 MoE decode")
+    ap.add_argument("--small-only", action="store_true", help="run only the config-2 135M decode (profiling)")
     ap.add_argument("--moe-context", type=int, default=6600)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="also run 3 plain device copies of MB MiB (HBM counter calibration)")
@@ -329,6 +330,12 @@ def main():
     if os.environ.get("K2T_EXACT"):
         ctx.set_exact(int(os.environ["K2T_EXACT"]))
 
+    if args.small_only:
+        m135, mats135, _, r135 = decode_bench(ctx, torch, "135M p55454", k2t.SMOLLM2_135M, "n4", 512, args.steps,
+                                              args.warmup, log)
+        print(json.dumps({"metric": "decode tok/s, 135M p55454", "value": r135["decode_tok_s"], "unit": "tok/s",
+                          "config": r135}))
+        return
     if args.moe_only:
         r30 = moe_decode_bench(ctx, torch, args.steps, args.warmup, args.moe_context, log)
         print(json.dumps({"metric": "decode tok/s, 30B-A3B-shape MoE", "value": r30["decode_tok_s"],
