@@ -284,6 +284,30 @@ def copy_probe(torch, mib):
     torch.cuda.synchronize()
 
 
+def copy_ceiling(torch, nbytes, steps=60):
+    """Practical HBM rate of one launch moving this many bytes: device-to-device copies of
+    nbytes/2 read + nbytes/2 written, rotated over enough buffers to miss the 256 MB
+    Infinity Cache, timed back to back like the GEMV cases.  Returns (GB/s, us)."""
+    n = max(1, nbytes // 8)  # float32 elements per source buffer (nbytes/2 bytes)
+    ncopy = max(2, int(np.ceil(320e6 / (4 * n))))
+    src = [torch.ones(n, dtype=torch.float32, device="cuda") for _ in range(ncopy)]
+    dst = [torch.empty_like(src[0]) for _ in range(ncopy)]
+    for i in range(ncopy):
+        dst[i].copy_(src[i])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _busy_wait(torch, stream, 2e-3 + steps * 60e-6)
+    a.record(stream)
+    for i in range(steps):
+        dst[i % ncopy].copy_(src[i % ncopy])
+    b.record(stream)
+    torch.cuda.synchronize()
+    t = a.elapsed_time(b) * 1e-3 / steps
+    del src, dst
+    return 8 * n / t / 1e9, t * 1e6
+
+
 def cpu_decode_baseline(cfg, host, seconds=10.0, max_tokens=32):
     """The reference's portable CPU decode (dequantize + fp32 dot GEMVs over stripe ranges,
     real_llm.rs:829-836 / simd_lut.rs:5719-5748; scalar q8 attention) restated in the
@@ -364,11 +388,17 @@ def main():
             if ntok == 1 and fmt == "nf4" and (dom is None or results[key]["GB_s"] < results[dom]["GB_s"]):
                 dom = key
             del case
+    ceiling = None
+    if dom is not None:
+        cg, cu = copy_ceiling(torch, results[dom]["bytes"])
+        ceiling = {"GB_s": round(cg, 1), "us": round(cu, 3), "frac": round(cg / HBM_PEAK_GBS, 4)}
+        log(f"# copy ceiling at {results[dom]['bytes']} B per launch: {cu:.2f} us  {cg:.1f} GB/s "
+            f"{100 * cg / HBM_PEAK_GBS:.1f}% of peak")
     line = {"metric": "quant GEMV HBM GB/s (% peak) + decode tok/s, 1.7B-shape nf4g128, 1 MI355X"}
     if args.copy_probe:
         copy_probe(torch, args.copy_probe)
     if args.only:
-        line.update({"config": {"cases": results}})
+        line.update({"config": {"cases": results, "copy_ceiling": ceiling}})
         print(json.dumps(line))
         return
     torch.cuda.empty_cache()
@@ -413,7 +443,8 @@ def main():
                    "decode_30b_a3b_moe_nf3_ctx6600": r30, "gemv_sweep": results},
         "roofline": {"bound": "hbm", "kernel": f"gemv_kernel ({dom})", "achieved": dr["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dr["GB_s"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom),
-                     "algorithmic_bytes_per_launch": dr["bytes"], "avg_launch_us": dr["us"]},
+                     "algorithmic_bytes_per_launch": dr["bytes"], "avg_launch_us": dr["us"],
+                     "copy_ceiling_same_bytes": ceiling},
         "cpu_baseline": cpu,
     })
     print(json.dumps(line))
