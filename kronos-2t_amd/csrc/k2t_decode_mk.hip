@@ -104,10 +104,11 @@ __device__ Lds carve(const MkParams &P, float *base) {
     return L;
 }
 
-// Waits for n LL words; kPoll loads per thread are issued before any is checked, then
-// stragglers are polled one by one.  Payloads go to dst (fp32 vector, act == false) or
-// are unpacked into the LDS activation (codes, scales, sums; act == true).  Returns
-// false (for the whole workgroup) on error.
+// Waits for n LL words: each thread issues the loads of its (up to kPoll) words, then
+// re-requests all of its words that are not yet current together, one round trip per
+// poll, until every one holds `epoch` (bounded like ll_wait).  Payloads go to dst (fp32
+// vector, act == false) or are unpacked into the LDS activation (codes, scales, sums;
+// act == true).  Returns false (for the whole workgroup) on error.
 constexpr int kPoll = 8;
 __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, const unsigned long long *src, int n,
                                            uint32_t epoch, bool act, float *dst) {
@@ -119,12 +120,35 @@ __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, cons
             const int i = i0 + k * kThreads;
             w[k] = i < n ? ll_load(src + i) : 0ull;
         }
+        uint32_t pending = 0;
+#pragma unroll
+        for (int k = 0; k < kPoll; k++)
+            if (i0 + k * kThreads < n && (uint32_t)(w[k] >> 32) != epoch) pending |= 1u << k;
+        for (uint32_t spins = 0; pending != 0 && ok; spins++) {
+            if ((spins & 31u) == 31u) {
+                if (__hip_atomic_load(P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                    ok = false;
+                    break;
+                }
+                if (spins > P.spin_limit) {
+                    __hip_atomic_store(P.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+#pragma unroll
+            for (int k = 0; k < kPoll; k++)
+                if (pending & (1u << k)) w[k] = ll_load(src + i0 + k * kThreads);
+#pragma unroll
+            for (int k = 0; k < kPoll; k++)
+                if ((pending & (1u << k)) && (uint32_t)(w[k] >> 32) == epoch) pending &= ~(1u << k);
+        }
 #pragma unroll
         for (int k = 0; k < kPoll; k++) {
             const int i = i0 + k * kThreads;
             if (i < n && ok) {
-                uint32_t v = (uint32_t)w[k];
-                if ((uint32_t)(w[k] >> 32) != epoch && !ll_wait(P, src + i, epoch, v)) ok = false;
+                const uint32_t v = (uint32_t)w[k];
                 if (!act) {
                     dst[i] = __uint_as_float(v);
                 } else {
@@ -310,6 +334,14 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
         const int tt = ps + i * nps;
         vpre[i] = tt < pos ? *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4) : 0;
     }
+    // RoPE row of this position (waves 0 and 1 rotate q and k): requested before the wait
+    float rc = 0.0f, rsn = 0.0f;
+    if (wave < 2) {
+        const float *rrow = P.rope + (size_t)pos * hd;
+        const uint32_t ri = nb == 1 ? (lane & 31u) : lane;
+        rc = rrow[ri];
+        rsn = rrow[(nb == 1 ? 32u : 64u) + ri];
+    }
     // 1. this position's q, k, v (+ bias)
     bool ok = true;
     if (t < 3 * hd) {
@@ -330,16 +362,14 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     const size_t slot = ((size_t)layer * nkv + kvh) * P.max_seq + pos;
     // waves 0, 1, 2 handle q, k, v concurrently
     if (wave < 2) {
-        const float *rrow = P.rope + (size_t)pos * hd;
         const float *src = wave == 0 ? qf : kf;
         float x0 = src[lane], x1 = nb > 1 ? src[64 + lane] : 0.0f;
         if (nb == 1) {
-            const uint32_t i = lane & 31u;
-            const float c = rrow[i], sn = rrow[32 + i];
+            const float c = rc, sn = rsn;
             const float xo = __shfl_xor(x0, 32, kWave);
             x0 = lane < 32 ? x0 * c - xo * sn : x0 * c + xo * sn;
         } else {
-            const float c = rrow[lane], sn = rrow[64 + lane];
+            const float c = rc, sn = rsn;
             const float a0 = x0, a1 = x1;
             x0 = a0 * c - a1 * sn;
             x1 = a1 * c + a0 * sn;
