@@ -9,12 +9,17 @@ namespace k2t {
 struct MkLayer {
     MatDev qkv, o, gu, down;
     const float *in_norm, *post_norm, *bias;
+    // First workgroup of each phase's task list (qkv, attention, o, gate_up, down): the
+    // lists are laid end to end over the grid, so consecutive phases use disjoint
+    // workgroups wherever their task counts allow.
+    int off[5];
 };
 
 struct MkParams {
     const MkLayer *layers;
     int L;
     MatDev head;
+    int head_off;        // first workgroup of the lm_head phase
     MatDev embed;        // NF4 / bit-plane embedding table (ekind 0 tied, 3 NF4)
     const void *erows;   // f32 (ekind 1) or bf16 (ekind 2) embedding rows
     int ekind;
@@ -36,7 +41,11 @@ struct MkParams {
 };
 
 // pair_mode_nseg4: gate_up layout (4 wave groups = one [gate64, up64] block of 4 pairs).
-MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4);
+// max_nseg (> 0) caps the K segments per row block in stripe mode (more rows per
+// workgroup, fewer workgroups for the phase).
+MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg = 0);
+// Workgroup tasks of a GEMV phase of the persistent kernel.
+int mk_phase_tasks(const MatDev &M);
 size_t decode_mk_lds_bytes(const k2t_model_config &c);
 bool decode_mk_supported(const k2t_model_config &c, int num_cus);
 // Accumulates the common weight format of the model's matrices (fmt < 0: first call);

@@ -536,11 +536,12 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
     for (int ph = 1; ph < (int)nph; ph++) {
         const int l = (ph - 1) / 5;
         const int kind = ph == (int)nph - 1 ? kHead : (ph - 1) % 5;
-        // Each phase kind starts its task list at a different workgroup, so that the
-        // workgroups of consecutive phases are mostly disjoint: a workgroup done with one
-        // phase (or idle in it) is already streaming its next phase's weights.
+        // Each phase's task list starts where the previous phase's ended (MkLayer::off): a
+        // workgroup idle in one phase is already streaming its next phase's weights, and
+        // no phase's input polls queue behind weight loads that a workgroup issued on
+        // finishing the previous phase.
         const int nwg = (int)gridDim.x;
-        const int off = (kind == kAttn ? 0 : kind == kO ? 32 : kind == kGu ? 96 : kind == kDown ? 224 : 96) % nwg;
+        const int off = kind == kHead ? P.head_off : P.layers[l].off[kind];
         const int vb = ((int)blockIdx.x + nwg - off) % nwg;  // this workgroup's rank in the phase
         if (kind == kAttn) {
             for (int h = vb; h < P.nq; h += nwg)
@@ -624,7 +625,7 @@ __global__ void advance_step_kernel(int *pos, uint32_t *step, int n) {
 
 }  // namespace
 
-MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4) {
+MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg) {
     MatDev d{};
     d.pair = m->pair;
     d.tail = m->tail;
@@ -647,12 +648,19 @@ MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4) {
         // Stripe mode with one round of the 8 lane groups per wave where K allows.
         d.smode = 1;
         const int want = (m->nc + 7) / 8;
+        const int cap = max_nseg > 0 ? std::min(max_nseg, kWaves) : kWaves;
         int nseg = 1;
-        while (nseg < want && nseg < kWaves) nseg *= 2;
+        while (nseg < want && nseg < cap) nseg *= 2;
         d.nseg = nseg;
     }
     d.cps = (m->nc + d.nseg - 1) / d.nseg;
     return d;
+}
+
+int mk_phase_tasks(const MatDev &M) {
+    const int nblocks = M.smode ? M.stripes : M.np + (M.stripes & 1);
+    const int groups = kWaves / M.nseg;
+    return (nblocks + groups - 1) / groups;
 }
 
 size_t decode_mk_lds_bytes(const k2t_model_config &c) {

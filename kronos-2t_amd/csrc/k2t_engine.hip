@@ -146,6 +146,7 @@ struct k2t_model {
     int *err_dev = nullptr;
     unsigned long long *ll_ha = nullptr, *ll_hb = nullptr, *ll_qkv = nullptr, *ll_oact = nullptr, *ll_gact = nullptr;
     MkLayer *mk_layers = nullptr;
+    int mk_head_off = 0;  // first workgroup of the persistent kernel's lm_head phase
 };
 
 namespace {
@@ -309,14 +310,31 @@ void upload_mk_layers(k2t_model *m) {
     std::vector<MkLayer> h(m->layers.size());
     for (size_t l = 0; l < m->layers.size(); l++) {
         const auto &L = m->layers[l];
-        h[l].qkv = mat_dev(L.qkv, false);
         h[l].o = mat_dev(L.o, false);
         h[l].gu = mat_dev(L.gu, true);
         h[l].down = mat_dev(L.down, false);
+        // qkv follows down: fewer, longer qkv tasks where that lets the two phases use
+        // disjoint workgroups (the phases' task lists are laid end to end).
+        h[l].qkv = mat_dev(L.qkv, false);
+        for (int cap = h[l].qkv.nseg / 2;
+             cap >= 1 && mk_phase_tasks(h[l].qkv) + mk_phase_tasks(h[l].down) > m->ctx->num_cus; cap /= 2)
+            h[l].qkv = mat_dev(L.qkv, false, cap);
         h[l].in_norm = L.in_norm;
         h[l].post_norm = L.post_norm;
         h[l].bias = L.bias;
     }
+    // phase task lists laid end to end over the grid (one workgroup per CU)
+    const int nwg = m->ctx->num_cus;
+    int cursor = 0;
+    for (auto &x : h) {
+        const int tasks[5] = {mk_phase_tasks(x.qkv), m->cfg.n_heads, mk_phase_tasks(x.o), mk_phase_tasks(x.gu),
+                              mk_phase_tasks(x.down)};
+        for (int k = 0; k < 5; k++) {
+            x.off[k] = cursor;
+            cursor = (cursor + tasks[k]) % nwg;
+        }
+    }
+    m->mk_head_off = cursor;
     hip_check(hipMemcpy(m->mk_layers, h.data(), h.size() * sizeof(MkLayer), hipMemcpyHostToDevice), "layer table");
 }
 
@@ -327,6 +345,7 @@ void forward_mk(k2t_model *m) {
     P.layers = m->mk_layers;
     P.L = c.n_layers;
     P.head = mat_dev(m->head, false);
+    P.head_off = m->mk_head_off;
     P.embed = mat_dev(m->embed_kind == K2T_EMBED_NF4 ? m->embed_mat : m->head, false);
     P.erows = m->embed_rows;
     P.ekind = m->embed_kind;
