@@ -268,7 +268,10 @@ int32_t k2t_model_set_exact(k2t_model *m, int32_t exact);
  * the shape of forward_token_sdot_megakernel (real_llm.rs:6794-7403).  0: one kernel per
  * operation.  Used only with the fast epilogue, when every matrix is NF4 or every matrix
  * has 4 bit planes, and the device and model shape allow it (see
- * k2t_model_persistent_active); otherwise the per-operation path runs. */
+ * k2t_model_persistent_active); otherwise the per-operation path runs.  2: as 1, and
+ * also for bit-plane models that mix 4- and 5-plane matrices (p55454), which then run a
+ * 256-thread variant; it is slower than the per-operation path on SmolLM2-135M (one
+ * attention head per workgroup), so 1 leaves such models on the per-operation path. */
 int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable);
 int32_t k2t_model_persistent_active(const k2t_model *m, int32_t *active);
 /* reset_context: position back to 0. */

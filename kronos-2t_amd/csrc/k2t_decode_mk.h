@@ -43,13 +43,18 @@ struct MkParams {
 // pair_mode_nseg4: gate_up layout (4 wave groups = one [gate64, up64] block of 4 pairs).
 // max_nseg (> 0) caps the K segments per row block in stripe mode (more rows per
 // workgroup, fewer workgroups for the phase).
-MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg = 0);
+// nwaves: waves per workgroup of the kernel that will run (decode_mk_threads / 64).
+MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg = 0, int nwaves = 8);
 // Workgroup tasks of a GEMV phase of the persistent kernel.
-int mk_phase_tasks(const MatDev &M);
+int mk_phase_tasks(const MatDev &M, int nwaves = 8);
+// Threads per workgroup of the persistent kernel for the format decode_mk_format chose.
+int decode_mk_threads(int hp);
 size_t decode_mk_lds_bytes(const k2t_model_config &c);
 bool decode_mk_supported(const k2t_model_config &c, int num_cus);
 // Accumulates the common weight format of the model's matrices (fmt < 0: first call);
-// false when a matrix differs (the persistent kernel needs one format).
+// false when a matrix differs (the persistent kernel needs one format family).  Bit-plane
+// models with any 5-plane matrix get hp = kHpMixed: the 256-thread kernel that reads
+// each matrix's plane count (4 or 5).
 bool decode_mk_format(const MatDev &m, int &fmt, int &hp);
 void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds);
 void launch_advance_step(hipStream_t st, int *pos, uint32_t *step, int n);

@@ -38,8 +38,11 @@ namespace k2t {
 
 namespace {
 
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / 64;
+// Threads per workgroup: 512 (8 waves, two per SIMD, 256 VGPRs each) for single-format
+// models; 256 (one wave per SIMD, 512 VGPRs) for the mixed 4/5-plane variant, whose
+// fragments do not fit in 256.  Device helpers take the count as a template parameter.
+constexpr int kMaxThreads = 512;
+constexpr int kMaxWaves = kMaxThreads / 64;
 constexpr int kActWords = 18;  // per 64-element activation chunk: 16 code words, scale, sum
 
 __device__ __forceinline__ void ll_store(unsigned long long *p, uint32_t v, uint32_t epoch) {
@@ -95,7 +98,7 @@ __device__ Lds carve(const MkParams &P, float *base) {
     L.xsuml = reinterpret_cast<int32_t *>(p);
     p += pad16((size_t)(P.kmax / 64) * 4);
     L.part = reinterpret_cast<float *>(p);
-    p += kWaves * 32 * 4;
+    p += kMaxWaves * 32 * 4;
     L.vec = reinterpret_cast<float *>(p);
     p += 128 * 4;
     L.flag = reinterpret_cast<int *>(p);
@@ -110,20 +113,21 @@ __device__ Lds carve(const MkParams &P, float *base) {
 // vector, act == false) or are unpacked into the LDS activation (codes, scales, sums;
 // act == true).  Returns false (for the whole workgroup) on error.
 constexpr int kPoll = 8;
+template <int NTH>
 __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, const unsigned long long *src, int n,
                                            uint32_t epoch, bool act, float *dst) {
     bool ok = true;
-    for (int i0 = (int)threadIdx.x; i0 < n; i0 += kThreads * kPoll) {
+    for (int i0 = (int)threadIdx.x; i0 < n; i0 += NTH * kPoll) {
         unsigned long long w[kPoll];
 #pragma unroll
         for (int k = 0; k < kPoll; k++) {
-            const int i = i0 + k * kThreads;
+            const int i = i0 + k * NTH;
             w[k] = i < n ? ll_load(src + i) : 0ull;
         }
         uint32_t pending = 0;
 #pragma unroll
         for (int k = 0; k < kPoll; k++)
-            if (i0 + k * kThreads < n && (uint32_t)(w[k] >> 32) != epoch) pending |= 1u << k;
+            if (i0 + k * NTH < n && (uint32_t)(w[k] >> 32) != epoch) pending |= 1u << k;
         for (uint32_t spins = 0; pending != 0 && ok; spins++) {
             if ((spins & 31u) == 31u) {
                 if (__hip_atomic_load(P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
@@ -139,14 +143,14 @@ __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, cons
             }
 #pragma unroll
             for (int k = 0; k < kPoll; k++)
-                if (pending & (1u << k)) w[k] = ll_load(src + i0 + k * kThreads);
+                if (pending & (1u << k)) w[k] = ll_load(src + i0 + k * NTH);
 #pragma unroll
             for (int k = 0; k < kPoll; k++)
                 if ((pending & (1u << k)) && (uint32_t)(w[k] >> 32) == epoch) pending &= ~(1u << k);
         }
 #pragma unroll
         for (int k = 0; k < kPoll; k++) {
-            const int i = i0 + k * kThreads;
+            const int i = i0 + k * NTH;
             if (i < n && ok) {
                 const uint32_t v = (uint32_t)w[k];
                 if (!act) {
@@ -194,6 +198,7 @@ __device__ void store_act_chunk(float v, uint32_t lane, unsigned long long *dst,
 // RMSNorm + FWHT + int8 of S.hbuf[0..d) into the LDS activation: wave 0 computes inv_rms
 // in row_sumsq_wave order (bit-identical to rmsnorm_act_kernel); then eight lanes per
 // chunk, every chunk of the vector at once (rotate_quant_slice8).
+template <int NTH>
 __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, uint32_t lane, int wave) {
     if (wave == 0) {
         const float ss = row_sumsq_wave(S.hbuf, P.d, lane);
@@ -203,7 +208,7 @@ __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, 
     const float inv_rms = S.vec[0];
     const uint32_t s8 = lane & 7u;
     const int nc = P.d / 64;
-    for (int c0 = wave * 8; c0 < nc; c0 += kWaves * 8) {
+    for (int c0 = wave * 8; c0 < nc; c0 += NTH / 64 * 8) {
         const int c = c0 + (int)(lane >> 3);
         const bool act = c < nc;
         const int cc = act ? c : 0;
@@ -224,14 +229,15 @@ enum PhaseKind { kQkv = 0, kAttn = 1, kO = 2, kGu = 3, kDown = 4, kHead = 5 };
 // Waits for a GEMV phase's input and builds its int8 activation in LDS: the o_proj /
 // down_proj activation chunks as produced, or RMSNorm + FWHT + int8 of the hidden vector
 // (HA after the embedding or a down phase, HB after an o phase).
+template <int NTH>
 __device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, const MkLayer &Ly, int kind,
                                               uint32_t epoch, uint32_t lane, int wave) {
     if (kind == kO || kind == kDown) {
         const int nch = kind == kO ? P.nq * P.hd / 64 : P.inter / 64;
-        return load_words(P, S, kind == kO ? P.OACT : P.GACT, nch * kActWords, epoch, true, nullptr);
+        return load_words<NTH>(P, S, kind == kO ? P.OACT : P.GACT, nch * kActWords, epoch, true, nullptr);
     }
-    if (!load_words(P, S, kind == kGu ? P.HB : P.HA, P.d, epoch, false, S.hbuf)) return false;
-    build_norm_act(P, S, kind == kQkv ? Ly.in_norm : kind == kGu ? Ly.post_norm : P.final_norm, lane, wave);
+    if (!load_words<NTH>(P, S, kind == kGu ? P.HB : P.HA, P.d, epoch, false, S.hbuf)) return false;
+    build_norm_act<NTH>(P, S, kind == kQkv ? Ly.in_norm : kind == kGu ? Ly.post_norm : P.final_norm, lane, wave);
     return true;
 }
 
@@ -299,6 +305,7 @@ __device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t
 
 // Attention of q head h for the current position (causal_gqa_group_q8,
 // real_llm.rs:8471-8594), ending with the o_proj activation chunks of this head.
+template <int NTH>
 __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &S, int layer, int h, int pos,
                                uint32_t ep_in, uint32_t ep_out, uint32_t lane, int wave) {
     const int hd = P.hd, nb = hd / 64, nq = P.nq, nkv = P.nkv;
@@ -309,11 +316,11 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     float *scal = reinterpret_cast<float *>(vn + 128);  // qas, ks_new, vs_new, m, 1/L
     float *red = scal + 8;                              // [32]
     float *opart = red + 32;                            // [16 waves][hd]
-    float *sc = opart + kThreads * 4;                   // [max_seq]
+    float *sc = opart + kMaxThreads * 4;                // [max_seq]
     const int t = (int)threadIdx.x;
     const int seq = pos + 1;
     const size_t base = ((size_t)layer * nkv + kvh) * P.max_seq;
-    const int ncg = hd / 4, nps = kThreads / ncg;
+    const int ncg = hd / 4, nps = NTH / ncg;
     const int cg = t % ncg, ps = t / ncg;
     // 0. past positions' K rows, scales and V slices do not depend on this step: request
     //    this thread's first ones before waiting for q / k / v.
@@ -395,7 +402,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     // 3. scores s_t = float(q8 . k8_t) * ks_t * (qs * scale), t <= pos
     const float qas = scal[0];
     float smax = -INFINITY;
-    for (int tt = t; tt < seq; tt += kThreads) {
+    for (int tt = t; tt < seq; tt += NTH) {
         const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
         int dot = 0;
         float kscale;
@@ -430,10 +437,10 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     if (lane == 0) red[wave] = smax;
     __syncthreads();
     float m = red[0];
-    for (int w2 = 1; w2 < kWaves; w2++) m = fmaxf(m, red[w2]);
+    for (int w2 = 1; w2 < (NTH / 64); w2++) m = fmaxf(m, red[w2]);
     __syncthreads();
     float psum = 0.0f;
-    for (int tt = t; tt < seq; tt += kThreads) {
+    for (int tt = t; tt < seq; tt += NTH) {
         const float p = expf(sc[tt] - m);
         const float vsc = tt == pos ? scal[2] : (tt == t ? vspre : P.vs[base + tt]);
         sc[tt] = p * vsc;  // p_t * vs_t
@@ -476,9 +483,9 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     __syncthreads();
     if (t < hd) {
         float acc = opart[t];
-        for (int w2 = 1; w2 < kWaves; w2++) acc += opart[w2 * hd + t];
+        for (int w2 = 1; w2 < (NTH / 64); w2++) acc += opart[w2 * hd + t];
         float L = red[16];
-        for (int w2 = 1; w2 < kWaves; w2++) L += red[16 + w2];
+        for (int w2 = 1; w2 < (NTH / 64); w2++) L += red[16 + w2];
         qf[t] = acc * (1.0f / L);  // reuse qf for o
     }
     __syncthreads();
@@ -494,17 +501,20 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
 // Stripe-mode task order with both stripes of a pair on one XCD: with one stripe per
 // workgroup, tasks t and t + 8 run on workgroups 8 apart (the same XCD), so the L2 lines
 // shared by the two halves of a record are fetched from HBM once.
+template <int NW>
 __device__ __forceinline__ int xcd_stripe(const MatDev &M, int t, int nblocks) {
     // (with two or more stripes per workgroup, consecutive tasks already pair up)
-    if (!M.smode || M.nseg != kWaves || (nblocks & 15) != 0 || t >= nblocks) return t;
+    if (!M.smode || M.nseg != NW || (nblocks & 15) != 0 || t >= nblocks) return t;
     const int a = t >> 4, s8 = (t >> 3) & 1, j = t & 7;
     return 2 * (8 * a + j) + s8;
 }
 
 // FMT/HP: the one weight format every projection and the head use (mixed-format models
 // run the one-kernel-per-operation path).
-template <int FMT, int HP>
-__global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
+template <int FMT, int HP, int NTH>
+__global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
+    constexpr int kThreads = NTH;
+    constexpr int kWaves = NTH / 64;
     extern __shared__ float lds_raw[];
     const Lds S = carve(P, lds_raw);
     const uint32_t lane = threadIdx.x & 63u;
@@ -545,7 +555,7 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
         const int vb = ((int)blockIdx.x + nwg - off) % nwg;  // this workgroup's rank in the phase
         if (kind == kAttn) {
             for (int h = vb; h < P.nq; h += nwg)
-                if (!attention_head(P, P.layers[l], S, l, h, pos, E(ph - 1), E(ph), lane, wave)) return;
+                if (!attention_head<NTH>(P, P.layers[l], S, l, h, pos, E(ph - 1), E(ph), lane, wave)) return;
             continue;
         }
         const MkLayer &Ly = P.layers[kind == kHead ? 0 : l];
@@ -558,7 +568,7 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
         const int RB = M.smode ? 16 : 32;
         bool ok = true;
         for (int base = vb * groups; base < nblocks; base += nwg * groups) {
-            const int rb = xcd_stripe(M, base + grp, nblocks);
+            const int rb = xcd_stripe<kWaves>(M, base + grp, nblocks);
             const bool first = base == vb * groups;
             // The first round requests its first weight fragments, then waits for the
             // phase input (the weights stream in meanwhile), then computes.
@@ -567,7 +577,7 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
         GemvWave<F, H> gw(M, rb, rb < nblocks, wseg, lane);                                          \
         gw.start();                                                                                  \
         if (first) {                                                                                 \
-            if (!mk_load_input(P, S, Ly, kind, E(ph - 1), lane, wave)) return;                        \
+            if (!mk_load_input<NTH>(P, S, Ly, kind, E(ph - 1), lane, wave)) return;                        \
         }                                                                                            \
         gw.finish(S.xl, S.xsl, S.xsuml, S.part + wave * 32);                                         \
     }
@@ -575,7 +585,7 @@ __global__ __launch_bounds__(kThreads) void decode_mk_kernel(MkParams P) {
 #undef MK_ROUND
             __syncthreads();
             if (t < groups * RB) {
-                const int g2 = t / RB, rl = t % RB, rb2 = xcd_stripe(M, base + g2, nblocks);
+                const int g2 = t / RB, rl = t % RB, rb2 = xcd_stripe<kWaves>(M, base + g2, nblocks);
                 if (rb2 < nblocks) {
                     const bool tail = !M.smode && rb2 >= M.np;
                     const int first_stripe = M.smode ? rb2 : (tail ? 2 * M.np : 2 * rb2);
@@ -625,7 +635,8 @@ __global__ void advance_step_kernel(int *pos, uint32_t *step, int n) {
 
 }  // namespace
 
-MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg) {
+MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg, int nwaves) {
+    const int kWaves = nwaves;
     MatDev d{};
     d.pair = m->pair;
     d.tail = m->tail;
@@ -657,24 +668,24 @@ MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg) {
     return d;
 }
 
-int mk_phase_tasks(const MatDev &M) {
+int mk_phase_tasks(const MatDev &M, int nwaves) {
     const int nblocks = M.smode ? M.stripes : M.np + (M.stripes & 1);
-    const int groups = kWaves / M.nseg;
+    const int groups = nwaves / M.nseg;
     return (nblocks + groups - 1) / groups;
 }
 
 size_t decode_mk_lds_bytes(const k2t_model_config &c) {
     const size_t kmax = std::max(c.hidden, c.intermediate);
     const size_t hd = c.head_dim;
-    size_t b = pad16((size_t)c.hidden * 4) + pad16(kmax) + 2 * pad16((kmax / 64) * 4) + kWaves * 32 * 4 + 128 * 4 + 16;
-    b += (3 * hd) * 4 + 3 * 128 + 8 * 4 + 32 * 4 + (size_t)kThreads * 4 * 4 + (size_t)c.max_seq * 4;
+    size_t b = pad16((size_t)c.hidden * 4) + pad16(kmax) + 2 * pad16((kmax / 64) * 4) + kMaxWaves * 32 * 4 + 128 * 4 + 16;
+    b += (3 * hd) * 4 + 3 * 128 + 8 * 4 + 32 * 4 + (size_t)kMaxThreads * 4 * 4 + (size_t)c.max_seq * 4;
     return (b + 255) / 256 * 256;
 }
 
-template <int FMT, int HP>
+template <int FMT, int HP, int NTH>
 static bool occupancy_ok(size_t lds) {
     int nb = 0;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_mk_kernel<FMT, HP>, kThreads, lds) == hipSuccess &&
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_mk_kernel<FMT, HP, NTH>, NTH, lds) == hipSuccess &&
            nb >= 1;
 }
 
@@ -682,23 +693,32 @@ bool decode_mk_supported(const k2t_model_config &c, int num_cus) {
     if (decode_mk_lds_bytes(c) > 64 * 1024) return false;
     if (c.hidden > 8192 || c.intermediate > 32768) return false;
     const size_t lds = decode_mk_lds_bytes(c);
-    return num_cus > 0 && occupancy_ok<1, 0>(lds) && occupancy_ok<0, 0>(lds);
+    return num_cus > 0 && occupancy_ok<1, 0, 512>(lds) && occupancy_ok<0, 0, 512>(lds) &&
+           occupancy_ok<0, kHpMixed, 256>(lds);
 }
 
+int decode_mk_threads(int hp) { return hp == kHpMixed ? 256 : 512; }
+
 bool decode_mk_format(const MatDev &m, int &fmt, int &hp) {
-    if (m.fmt == 0 && m.hp != 0) return false;  // b5 / b6 fragments exceed the register budget
-    if (m.fmt == 2) return false;                 // NF3 runs on the per-operation path
+    if (m.fmt == 0 && m.hp > 1) return false;  // b6 fragments exceed the register budget
+    if (m.fmt == 2) return false;               // NF3 runs on the per-operation path
+    // any 5-plane matrix selects the 256-thread kernel that reads each matrix's plane count
+    const int mhp = m.fmt == 0 && m.hp == 1 ? kHpMixed : 0;
     if (fmt < 0) {
         fmt = m.fmt;
-        hp = m.hp;
+        hp = mhp;
         return true;
     }
-    return m.fmt == fmt && (m.fmt == 1 || m.hp == hp);
+    if (m.fmt != fmt) return false;
+    if (mhp == kHpMixed) hp = kHpMixed;
+    return true;
 }
 
 void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds) {
-    if (fmt == 1) hipLaunchKernelGGL((decode_mk_kernel<1, 0>), dim3(num_cus), dim3(kThreads), lds, st, P);
-    else if (hp == 0) hipLaunchKernelGGL((decode_mk_kernel<0, 0>), dim3(num_cus), dim3(kThreads), lds, st, P);
+    if (fmt == 1) hipLaunchKernelGGL((decode_mk_kernel<1, 0, 512>), dim3(num_cus), dim3(512), lds, st, P);
+    else if (hp == 0) hipLaunchKernelGGL((decode_mk_kernel<0, 0, 512>), dim3(num_cus), dim3(512), lds, st, P);
+    else if (hp == kHpMixed)
+        hipLaunchKernelGGL((decode_mk_kernel<0, kHpMixed, 256>), dim3(num_cus), dim3(256), lds, st, P);
     else throw Error(K2T_E_INTERNAL, "persistent decode kernel: unsupported weight format");
     hip_check(hipGetLastError(), "decode megakernel launch");
 }

@@ -139,7 +139,7 @@ struct k2t_model {
     hipGraphExec_t graph = nullptr;
     std::vector<void *> allocs;
     // persistent single-launch decode step (fast epilogue, NF4 or 4-plane weights)
-    bool persistent = true;
+    int persistent = 1;  // 0 off, 1 single-format models, 2 also mixed 4/5-plane models
     bool mk_ok = false;
     size_t mk_lds = 0;
     uint32_t *step_dev = nullptr;
@@ -302,23 +302,27 @@ bool use_persistent(const k2t_model *m) {
     if (m->ring.window > 0 || m->ring.bits != 8) return false;
     for (const auto &L : m->layers)
         if (L.has_moe || L.q_norm || L.k_norm) return false;  // these run on the per-operation path
-    return m->persistent && m->mk_ok && !m->exact && mk_format(m, fmt, hp);
+    return m->persistent && m->mk_ok && !m->exact && mk_format(m, fmt, hp) &&
+           (hp != kHpMixed || m->persistent == 2);
 }
 
 // Uploads the layer table of the persistent kernel (matrix views and launch shapes).
 void upload_mk_layers(k2t_model *m) {
+    int fmt, hp;
+    mk_format(m, fmt, hp);
+    const int nw = decode_mk_threads(hp) / 64;
     std::vector<MkLayer> h(m->layers.size());
     for (size_t l = 0; l < m->layers.size(); l++) {
         const auto &L = m->layers[l];
-        h[l].o = mat_dev(L.o, false);
-        h[l].gu = mat_dev(L.gu, true);
-        h[l].down = mat_dev(L.down, false);
+        h[l].o = mat_dev(L.o, false, 0, nw);
+        h[l].gu = mat_dev(L.gu, true, 0, nw);
+        h[l].down = mat_dev(L.down, false, 0, nw);
         // qkv follows down: fewer, longer qkv tasks where that lets the two phases use
         // disjoint workgroups (the phases' task lists are laid end to end).
-        h[l].qkv = mat_dev(L.qkv, false);
+        h[l].qkv = mat_dev(L.qkv, false, 0, nw);
         for (int cap = h[l].qkv.nseg / 2;
-             cap >= 1 && mk_phase_tasks(h[l].qkv) + mk_phase_tasks(h[l].down) > m->ctx->num_cus; cap /= 2)
-            h[l].qkv = mat_dev(L.qkv, false, cap);
+             cap >= 1 && mk_phase_tasks(h[l].qkv, nw) + mk_phase_tasks(h[l].down, nw) > m->ctx->num_cus; cap /= 2)
+            h[l].qkv = mat_dev(L.qkv, false, cap, nw);
         h[l].in_norm = L.in_norm;
         h[l].post_norm = L.post_norm;
         h[l].bias = L.bias;
@@ -327,8 +331,8 @@ void upload_mk_layers(k2t_model *m) {
     const int nwg = m->ctx->num_cus;
     int cursor = 0;
     for (auto &x : h) {
-        const int tasks[5] = {mk_phase_tasks(x.qkv), m->cfg.n_heads, mk_phase_tasks(x.o), mk_phase_tasks(x.gu),
-                              mk_phase_tasks(x.down)};
+        const int tasks[5] = {mk_phase_tasks(x.qkv, nw), m->cfg.n_heads, mk_phase_tasks(x.o, nw),
+                              mk_phase_tasks(x.gu, nw), mk_phase_tasks(x.down, nw)};
         for (int k = 0; k < 5; k++) {
             x.off[k] = cursor;
             cursor = (cursor + tasks[k]) % nwg;
@@ -344,9 +348,12 @@ void forward_mk(k2t_model *m) {
     MkParams P{};
     P.layers = m->mk_layers;
     P.L = c.n_layers;
-    P.head = mat_dev(m->head, false);
+    int fmt, hp;
+    mk_format(m, fmt, hp);
+    const int nw = decode_mk_threads(hp) / 64;
+    P.head = mat_dev(m->head, false, 0, nw);
     P.head_off = m->mk_head_off;
-    P.embed = mat_dev(m->embed_kind == K2T_EMBED_NF4 ? m->embed_mat : m->head, false);
+    P.embed = mat_dev(m->embed_kind == K2T_EMBED_NF4 ? m->embed_mat : m->head, false, 0, nw);
     P.erows = m->embed_rows;
     P.ekind = m->embed_kind;
     P.final_norm = m->final_norm;
@@ -377,8 +384,6 @@ void forward_mk(k2t_model *m) {
     P.signs = m->ctx->signs;
     P.err = m->err_dev;
     P.spin_limit = 1u << 22;
-    int fmt = 1, hp = 0;
-    mk_format(m, fmt, hp);
     launch_decode_mk(m->stream, P, fmt, hp, m->ctx->num_cus, m->mk_lds);
     launch_advance_step(m->stream, m->pos_dev, m->step_dev, 1);
 }
@@ -885,7 +890,8 @@ int32_t k2t_model_sync(k2t_model *m) {
 int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable) {
     return mguard([&] {
         arg(m != nullptr, "model is NULL");
-        m->persistent = enable != 0;
+        arg(enable >= 0 && enable <= 2, "persistent mode must be 0, 1 or 2");
+        m->persistent = enable;
         if (m->graph) {
             (void)hipGraphExecDestroy(m->graph);
             m->graph = nullptr;

@@ -21,12 +21,24 @@ struct MatDev {
     int cps;    // chunks per wave
 };
 
+// HP: hi planes of the bit-plane format (0, 1, 2), or kHpMixed: 0 or 1 per matrix,
+// read from MatDev::hp at run time (one kernel for models that mix 4- and 5-plane
+// matrices, such as p55454).
+constexpr int kHpMixed = 3;
+
 template <int HP>
 struct WFrag {
     uint4 w[4];
-    uint4 h[HP == 0 ? 1 : (HP == 1 ? 2 : 4)];
+    uint4 h[HP == 0 ? 1 : (HP == 1 || HP == kHpMixed ? 2 : 4)];
     uint32_t ws;
 };
+
+// Hi planes of matrix M under template HP.
+template <int HP>
+__device__ __forceinline__ int hp_of(const MatDev &M) {
+    if constexpr (HP == kHpMixed) return M.hp;
+    else return HP;
+}
 
 // Lane geometry for row block `rb` (a pair, the odd tail stripe, or a stripe in stripe
 // mode).  Lane bits: 0 = 8-column half, 1-2 = 4-row group g, 3 = stripe of the pair (pair
@@ -55,11 +67,12 @@ __device__ __forceinline__ Geo make_geo(const MatDev &M, int rb, uint32_t lane) 
     o.first_stripe = smode ? rb : (o.is_tail ? 2 * M.np : 2 * rb);
     o.nrows = (o.is_tail && !smode) ? 16 : o.RB;
     o.live = !(o.is_tail && lane_side);
-    constexpr uint32_t PREC = 1024 + 256 * HP + 64;
+    const uint32_t hp = (uint32_t)hp_of<HP>(M);
+    const uint32_t PREC = 1024 + 256 * hp + 64;
     if constexpr (FMT == 0) {
         o.nib_off = (o.is_tail ? 0u : o.side * 512u) + o.g * 32u + o.half * 16u;
-        o.hi_off = (o.is_tail ? 512u : 1024u + o.side * 128u * HP) + o.g * 16u;
-        o.sc_off = (o.is_tail ? 512u + 128u * HP : 1024u + 256u * HP + o.side * 32u);
+        o.hi_off = (o.is_tail ? 512u : 1024u + o.side * 128u * hp) + o.g * 16u;
+        o.sc_off = (o.is_tail ? 512u + 128u * hp : 1024u + 256u * hp + o.side * 32u);
     } else {
         o.nib_off = (o.is_tail ? 32u : 64u + o.side * 512u) + o.g * 32u + o.half * 16u;
         o.hi_off = 0;
@@ -72,8 +85,9 @@ __device__ __forceinline__ Geo make_geo(const MatDev &M, int rb, uint32_t lane) 
 
 template <int FMT, int HP>
 __device__ __forceinline__ void fetch_w(const MatDev &M, const Geo &o, int c, WFrag<HP> &fr) {
-    constexpr uint32_t PREC = 1024 + 256 * HP + 64;
-    constexpr uint32_t TREC = 512 + 128 * HP + 32;
+    const uint32_t hp = (uint32_t)hp_of<HP>(M);
+    const uint32_t PREC = 1024 + 256 * hp + 64;
+    const uint32_t TREC = 512 + 128 * hp + 32;
     const uint8_t *rec, *scp;
     if constexpr (FMT == 0) {
         rec = o.mbase + (size_t)c * (o.is_tail ? TREC : PREC);
@@ -93,6 +107,13 @@ __device__ __forceinline__ void fetch_w(const MatDev &M, const Geo &o, int c, WF
     } else if constexpr (FMT == 0 && HP == 1) {
         fr.h[0] = load_stream16(rec + o.hi_off);
         fr.h[1] = load_stream16(rec + o.hi_off + 64);
+    } else if constexpr (FMT == 0 && HP == kHpMixed) {
+        if (hp == 1) {
+            fr.h[0] = load_stream16(rec + o.hi_off);
+            fr.h[1] = load_stream16(rec + o.hi_off + 64);
+        } else {
+            fr.h[0] = fr.h[1] = make_uint4(0, 0, 0, 0);
+        }
     }
     fr.ws = *reinterpret_cast<const uint32_t *>(scp + o.sc_off);
 }
@@ -102,14 +123,14 @@ __device__ __forceinline__ void fetch_w(const MatDev &M, const Geo &o, int c, WF
 template <int FMT, int HP>
 __device__ __forceinline__ void chunk_dots(const MatDev &M, const WFrag<HP> &fr, uint32_t half, const uint2 *x,
                                            int xsum, int &r0, int &r1) {
-    constexpr int MAX_ODD = (1 << (4 + HP)) - 1;
+    const int MAX_ODD = (1 << (4 + hp_of<HP>(M))) - 1;
     int acc[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) {
         const uint32_t wd[4] = {fr.w[kk].x, fr.w[kk].y, fr.w[kk].z, fr.w[kk].w};
         uint4 hv = make_uint4(0, 0, 0, 0);
         if constexpr (HP == 2) hv = fr.h[kk];
-        if constexpr (HP == 1) hv = fr.h[kk >> 1];
+        if constexpr (HP == 1 || HP == kHpMixed) hv = fr.h[kk >> 1];  // zero for a 4-plane matrix
         const uint32_t hd[4] = {hv.x, hv.y, hv.z, hv.w};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -121,7 +142,7 @@ __device__ __forceinline__ void chunk_dots(const MatDev &M, const WFrag<HP> &fr,
                 if constexpr (HP == 2) {
                     lo |= __builtin_rotateright32(hd[j], half ? 30u : 0u) & 0x30303030u;
                     hi |= __builtin_rotateright32(hd[j], half ? 28u : 2u) & 0x30303030u;
-                } else if constexpr (HP == 1) {
+                } else if constexpr (HP == 1 || HP == kHpMixed) {
                     const uint32_t e = ((kk & 1) ? 28u : 0u) + 2u * half;
                     lo |= __builtin_rotateright32(hd[j], e) & 0x10101010u;
                     hi |= __builtin_rotateright32(hd[j], (e + 1u) & 31u) & 0x10101010u;

@@ -492,7 +492,9 @@ class Model:
         check(lib().k2t_model_set_exact(self.h, int(bool(on))))
 
     def set_persistent(self, on):
-        check(lib().k2t_model_set_persistent(self.h, int(bool(on))))
+        """True / 1: the persistent decode kernel where supported; 2: also for mixed 4/5-plane
+        bit-plane models; False / 0: one kernel per operation."""
+        check(lib().k2t_model_set_persistent(self.h, 2 if on == 2 else int(bool(on))))
 
     def persistent_active(self):
         v = I32()

@@ -60,9 +60,10 @@ def test_decode_matches_oracle(gpu_ctx, name, cfg, fmt, planes, exact):
     gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
     gm.set_exact(exact)  # fast epilogue: per-segment sums, a few ulp per GEMV output
     # exact = False also runs the persistent single-launch decode kernel where every matrix
-    # has one format other than b6 (p55454 mixes b5 and b4)
-    gm.set_persistent(True)
-    assert gm.persistent_active() == (not exact and name == "nf4_hd64")
+    # is NF4 or has 4 or 5 bit planes (p55454 mixes b5 and b4: mode 2 runs the 256-thread
+    # variant that reads each matrix's plane count); b6 runs the per-operation path
+    gm.set_persistent(2)
+    assert gm.persistent_active() == (not exact and name in ("nf4_hd64", "p55454_hd64"))
     rng = np.random.default_rng(9)
     toks = rng.integers(0, cfg["vocab"], 8)
     for i, t in enumerate(toks):
