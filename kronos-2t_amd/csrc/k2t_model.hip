@@ -238,20 +238,37 @@ void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float 
 // softmax, o = sum_t p_t*vs_t*v_t in the rotated domain.  Grid (q head, split, token); each
 // workgroup writes (max, sum, o[hd]) for its KV range; attn_merge_kernel combines them.
 constexpr int kAttnSplitLen = 256;
+// Contexts up to kAttnWhole positions run one 1024-thread workgroup per (q head, token)
+// over every position, and that workgroup also writes the o_proj activation (FINAL): no
+// merge kernel.
+constexpr int kAttnWhole = 1024;
 
-__global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restrict__ q, int q_stride,
+// Sum of n (a power of two) values in a fixed pairwise tree.
+__device__ __forceinline__ float tree_sum(const float *v, int n) {
+    float t[16];
+    for (int i = 0; i < n; i++) t[i] = v[i];
+    for (int w = n; w > 1; w >>= 1)
+        for (int i = 0; i < w / 2; i++) t[i] = t[2 * i] + t[2 * i + 1];
+    return t[0];
+}
+
+template <int NTH, bool FINAL>
+__global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restrict__ q, int q_stride,
                                                            int8_t *__restrict__ kq, int8_t *__restrict__ vq,
                                                            float *__restrict__ ks, float *__restrict__ vs,
                                                            const int *__restrict__ pos_dev, int layer, int nq, int nkv,
                                                            int hd, KvRing kr, float attn_scale, int nsplit,
-                                                           AttnPost post, float *__restrict__ part) {
+                                                           AttnPost post, float *__restrict__ part,
+                                                           float *__restrict__ out_f, int8_t *__restrict__ aq,
+                                                           float *__restrict__ as, int32_t *__restrict__ asum) {
+    constexpr int NW = NTH / 64;  // waves
     __shared__ __align__(16) int8_t qi[128];
     __shared__ __align__(16) int8_t kcur[128], vcur[128];  // current position's K / V (post.on)
     __shared__ float cur_s[4];                              // their scales (f32, or BF16 pairs)
     __shared__ float qas_s;
-    __shared__ float sc[kAttnSplitLen];
-    __shared__ float red[8];
-    __shared__ float opart[16][64];  // [position subset][column], 16*64 == 8*128
+    __shared__ float sc[NTH];
+    __shared__ float red[2 * NW];
+    __shared__ float opart[NTH * 4];  // [position subset][column]: (NTH / (hd / 4)) * hd
     // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs by linear id,
     // so the q heads that share a KV head and a split get ids congruent mod 8 and run on
     // one XCD, where the K/V tile is fetched from HBM once and then hit in that XCD's L2.
@@ -273,7 +290,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     }
     const int seq = pos_dev[0] + tok + 1;
     const int act = active_len(kr, seq);  // attended positions: index idx -> slot of active_pos
-    const int t0 = split * kAttnSplitLen, t1 = min(act, t0 + kAttnSplitLen);
+    const int t0 = split * NTH, t1 = min(act, t0 + NTH);
     float *pp = part + ((size_t)(tok * nq + head) * nsplit + split) * (2 + hd);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     if (t0 >= t1) {
@@ -402,7 +419,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     smax = wave_max_f(smax);
     if (lane == 0) red[wv] = smax;
     __syncthreads();
-    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float m = red[0];
+    for (int w = 1; w < NW; w++) m = fmaxf(m, red[w]);
     float psum = 0.0f;
     if (t0 + (int)tid < t1) {
         const float p = expf(sc[tid] - m);
@@ -411,12 +429,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
     }
     psum = wave_sum_f(psum);
     __syncthreads();
-    if (lane == 0) red[4 + wv] = psum;
+    if (lane == 0) red[NW + wv] = psum;
     // o partial: thread = (position subset ps, 4-column group cg); a dword of V per
     // position, loads batched 4 deep; the position subsets are added in a fixed order.
     const int n = t1 - t0;
     const int ncg = hd / 4;           // 16 or 32 column groups
-    const int nps = 256 / ncg;        // 16 or 8 position subsets
+    const int nps = NTH / ncg;        // position subsets (16 or 8 at 256 threads)
     const int cg = (int)tid % ncg, ps = (int)tid / ncg;
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     const int8_t *vcol = vq + base * hd + cg * 4;
@@ -470,15 +488,37 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float *__restri
         a2 = fmaf(wt, (float)(int8_t)((v >> 16) & 0xFF), a2);
         a3 = fmaf(wt, (float)(int8_t)((v >> 24) & 0xFF), a3);
     }
-    float *op = &opart[0][0];  // [nps][hd]
+    float *op = opart;  // [nps][hd]
     op[ps * hd + cg * 4 + 0] = a0;
     op[ps * hd + cg * 4 + 1] = a1;
     op[ps * hd + cg * 4 + 2] = a2;
     op[ps * hd + cg * 4 + 3] = a3;
     __syncthreads();
+    if constexpr (FINAL) {
+        // One span covers every position: attn_merge_kernel's arithmetic for one split
+        // (its weight exp(m - m) is exactly 1), then ifwht64 per block and the FWHT +
+        // int8 of the o_proj chunk (populate_chunk_fwht_raw(None), real_llm.rs:7060-7084).
+        const float inv = 1.0f / tree_sum(red + NW, NW);
+        if (tid < (uint32_t)hd) {
+            float acc = op[tid];
+            for (int k = 1; k < nps; k++) acc += op[k * hd + tid];
+            sc[tid] = acc;  // the scores are no longer needed
+        }
+        __syncthreads();
+        if ((int)wv < nb) {
+            const float o = ifwht_lane(sc[wv * 64 + lane] * inv, (uint64_t)wv, lane);
+            const size_t hbase = (size_t)tok * nq * hd + (size_t)head * hd;
+            if (out_f) out_f[hbase + wv * 64 + lane] = o;
+            if (aq) {
+                const size_t c = (size_t)head * nb + wv, g = (size_t)tok * nq * nb + c;
+                quant_chunk_store(fwht_lane(o, c, lane), lane, aq + g * 64, as + g, asum + g);
+            }
+        }
+        return;
+    }
     if (tid == 0) {
         pp[0] = m;
-        pp[1] = (red[4] + red[5]) + (red[6] + red[7]);
+        pp[1] = tree_sum(red + NW, NW);
     }
     if (tid < (uint32_t)hd) {
         float acc = op[tid];
@@ -548,14 +588,25 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
     }
 }
 
-int attn_max_splits(int max_seq) { return (max_seq + kAttnSplitLen - 1) / kAttnSplitLen; }
+// One split (the whole-context kernel) up to kAttnWhole positions, else 256-position spans.
+int attn_max_splits(int max_seq) {
+    return max_seq <= kAttnWhole ? 1 : (max_seq + kAttnSplitLen - 1) / kAttnSplitLen;
+}
 
 void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale,
                       int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum) {
-    hipLaunchKernelGGL(attn_partial_kernel, dim3(nq, nsplit, ntok), dim3(256), 0, st, q, q_stride, kq, vq, ks, vs,
-                       pos_dev, layer, nq, nkv, hd, kr, attn_scale, nsplit, post, part);
+    if (nsplit == 1) {  // the caller sized the context within kAttnWhole (attn_max_splits)
+        hipLaunchKernelGGL((attn_partial_kernel<kAttnWhole, true>), dim3(nq, 1, ntok), dim3(kAttnWhole), 0, st, q,
+                           q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part, out_f,
+                           aq, as, asum);
+        hip_check(hipGetLastError(), "attention launch");
+        return;
+    }
+    hipLaunchKernelGGL((attn_partial_kernel<kAttnSplitLen, false>), dim3(nq, nsplit, ntok), dim3(kAttnSplitLen), 0, st,
+                       q, q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, nsplit, post, part,
+                       nullptr, nullptr, nullptr, nullptr);
     hip_check(hipGetLastError(), "attn_partial launch");
     hipLaunchKernelGGL(attn_merge_kernel, dim3(nq, ntok), dim3(64), 0, st, part, nq, hd, nsplit, kr, pos_dev, out_f, aq, as,
                        asum);
