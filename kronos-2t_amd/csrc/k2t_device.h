@@ -124,6 +124,46 @@ __device__ __forceinline__ uint32_t lut16(uint32_t s, uint32_t m, uint32_t cb0, 
     return (hi & m) | (lo & ~m);
 }
 
+// A 16-entry signed-byte codebook (cb0..cb3, byte i = entry i) as two 8-byte tables T
+// (from entries 0-7) and U (entries 8-15) such that, per byte, entry n equals
+//   perm(T, n) ^ perm(U, n ^ 8)
+// for the 4-bit index n: perm with a selector 0-7 returns that table byte, with 8-11 the
+// sign of table byte 1, 3, 5, 7 spread over the byte, with 12 zero, with 13-15 0xFF.  So
+// for n < 8 the U lookup returns a fill byte fixed by U's signs, and for n >= 8 the T
+// lookup one fixed by T's signs; T and U hold the entries XOR those fills.  The fills
+// depend on T's and U's own sign bits, an acyclic chain that every codebook satisfies.
+__device__ __forceinline__ void nf4_xor_tables(uint32_t cb0, uint32_t cb1, uint32_t cb2, uint32_t cb3, uint32_t &t0,
+                                               uint32_t &t1, uint32_t &u0, uint32_t &u1) {
+    const uint32_t w[4] = {cb0, cb1, cb2, cb3};
+    auto sgn = [&](int i) { return (w[i >> 2] >> (8 * (i & 3) + 7)) & 1u; };
+    uint32_t eT[8], eU[8];  // fill of the T lookup for entry 8 + j, of the U lookup for entry j
+    eT[4] = eU[4] = 0u;
+    eT[5] = eT[6] = eT[7] = eU[5] = eU[6] = eU[7] = 1u;
+    eT[2] = sgn(5) ^ 1u;  // sign of T[5] = entry 5 ^ fill 1
+    eT[3] = sgn(7) ^ 1u;
+    eU[2] = sgn(13) ^ 1u;
+    eU[3] = sgn(15) ^ 1u;
+    eU[1] = sgn(11) ^ eT[3];
+    eT[1] = sgn(3) ^ eU[3];
+    eU[0] = sgn(9) ^ eT[1];
+    eT[0] = sgn(1) ^ eU[1];
+    uint32_t t[2] = {0u, 0u}, u[2] = {0u, 0u};
+    for (int j = 0; j < 8; j++) {
+        const uint32_t lo = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu, hi = (w[2 + (j >> 2)] >> (8 * (j & 3))) & 0xFFu;
+        t[j >> 2] |= (lo ^ (eU[j] ? 0xFFu : 0u)) << (8 * (j & 3));
+        u[j >> 2] |= (hi ^ (eT[j] ? 0xFFu : 0u)) << (8 * (j & 3));
+    }
+    t0 = t[0];
+    t1 = t[1];
+    u0 = u[0];
+    u1 = u[1];
+}
+
+// Codebook values of four 4-bit indices (one per byte) through the tables above.
+__device__ __forceinline__ uint32_t nf4_xlut(uint32_t s, uint32_t t0, uint32_t t1, uint32_t u0, uint32_t u1) {
+    return __builtin_amdgcn_perm(t1, t0, s) ^ __builtin_amdgcn_perm(u1, u0, s ^ 0x08080808u);
+}
+
 // Byte mask 0xFF where bit 7 of the byte is set (v_perm selectors >= 13 give 0xFF,
 // selector 0 picks byte 0 of the zero pool).
 __device__ __forceinline__ uint32_t bit7_mask(uint32_t v) {

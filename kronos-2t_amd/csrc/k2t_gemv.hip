@@ -341,6 +341,10 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         out_p += (size_t)z * P.slot_out;
         xsrc_p += (size_t)z * P.slot_src;
     }
+    // NF4: the codebook as the two XOR tables of nf4_xlut (two v_perm and one XOR per
+    // four codes instead of two v_perm, a select and a bit-3 mask)
+    uint32_t xt0 = 0, xt1 = 0, xu0 = 0, xu1 = 0;
+    if constexpr (FMT == 1) nf4_xor_tables(cb0, cb1, cb2, cb3, xt0, xt1, xu0, xu1);
     const uint8_t *mbase = is_tail ? P.tail : pair_p + (size_t)pidx * (FMT == 0 ? (size_t)P.nc * PREC : P.ptot);
 
     auto fetch = [&](Frag<HP, NT> &fr, int c) {
@@ -466,8 +470,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
                         hi |= __builtin_rotateright32(hd[j], (e + 1u) & 31u) & 0x10101010u;
                     }
                 } else {
-                    lo = lut16(d & 0x07070707u, bit3_mask(d), cb0, cb1, cb2, cb3);
-                    hi = lut16((d >> 4) & 0x07070707u, bit7_mask(d), cb0, cb1, cb2, cb3);
+                    lo = nf4_xlut(d & 0x0F0F0F0Fu, xt0, xt1, xu0, xu1);
+                    hi = nf4_xlut((d >> 4) & 0x0F0F0F0Fu, xt0, xt1, xu0, xu1);
                 }
 #pragma unroll
                 for (int t = 0; t < NT; t++)
