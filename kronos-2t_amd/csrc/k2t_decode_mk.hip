@@ -278,8 +278,7 @@ __device__ float embed_value(const MatDev &M, int r, int c, uint32_t lane) {
         const int sub4 = w / 4;
         const uint8_t byte = d[k * 128 + g * 32 + (sub4 / 2) * 16 + j * 4 + t];
         const int idx = (sub4 & 1) == 0 ? (byte & 0x0F) : (byte >> 4);
-        const uint32_t cbw = idx < 4 ? M.cb0 : idx < 8 ? M.cb1 : idx < 12 ? M.cb2 : M.cb3;
-        const int cv = (int)(int8_t)((cbw >> (8 * (idx & 3))) & 0xFF);
+        const int cv = (int)(int8_t)(nf4_xlut((uint32_t)idx, M.cb0, M.cb1, M.cb2, M.cb3) & 0xFFu);
         const float delta = __uint_as_float((uint32_t)(sp[rl * 2] | (sp[rl * 2 + 1] << 8)) << 16);
         val = (float)cv * delta;
     }
@@ -652,6 +651,7 @@ MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg, int nwaves)
     d.cb1 = m->cb[1];
     d.cb2 = m->cb[2];
     d.cb3 = m->cb[3];
+    if (d.fmt == 1) nf4_xor_tables(m->cb[0], m->cb[1], m->cb[2], m->cb[3], d.cb0, d.cb1, d.cb2, d.cb3);
     if (pair_mode_nseg4) {  // 4 wave groups: the 4 pairs of one [gate64, up64] block
         d.smode = 0;
         d.nseg = kWaves / 4;

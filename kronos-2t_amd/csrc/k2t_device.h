@@ -132,7 +132,7 @@ __device__ __forceinline__ uint32_t lut16(uint32_t s, uint32_t m, uint32_t cb0, 
 // for n < 8 the U lookup returns a fill byte fixed by U's signs, and for n >= 8 the T
 // lookup one fixed by T's signs; T and U hold the entries XOR those fills.  The fills
 // depend on T's and U's own sign bits, an acyclic chain that every codebook satisfies.
-__device__ __forceinline__ void nf4_xor_tables(uint32_t cb0, uint32_t cb1, uint32_t cb2, uint32_t cb3, uint32_t &t0,
+__host__ __device__ __forceinline__ void nf4_xor_tables(uint32_t cb0, uint32_t cb1, uint32_t cb2, uint32_t cb3, uint32_t &t0,
                                                uint32_t &t1, uint32_t &u0, uint32_t &u1) {
     const uint32_t w[4] = {cb0, cb1, cb2, cb3};
     auto sgn = [&](int i) { return (w[i >> 2] >> (8 * (i & 3) + 7)) & 1u; };

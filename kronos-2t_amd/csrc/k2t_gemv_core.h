@@ -15,7 +15,7 @@ struct MatDev {
     size_t ptot;  // NF: bytes per pair stream
     int rows, nc, np, stripes;
     int fmt, hp, sgc;  // fmt: 0 = bit planes (hp hi planes), 1 = NF4
-    uint32_t cb0, cb1, cb2, cb3;
+    uint32_t cb0, cb1, cb2, cb3;  // NF4: the codebook's XOR tables T0 T1 U0 U1 (nf4_xor_tables)
     int smode;  // 1: a wave group owns one stripe (16 rows), 0: a stripe pair (32 rows)
     int nseg;   // waves per row block (K segments), a power of two <= 16
     int cps;    // chunks per wave
@@ -148,8 +148,9 @@ __device__ __forceinline__ void chunk_dots(const MatDev &M, const WFrag<HP> &fr,
                     hi |= __builtin_rotateright32(hd[j], (e + 1u) & 31u) & 0x10101010u;
                 }
             } else {
-                lo = lut16(d & 0x07070707u, bit3_mask(d), M.cb0, M.cb1, M.cb2, M.cb3);
-                hi = lut16((d >> 4) & 0x07070707u, bit7_mask(d), M.cb0, M.cb1, M.cb2, M.cb3);
+                // NF4: M.cb0..cb3 hold the XOR tables of the codebook (nf4_xor_tables)
+                lo = nf4_xlut(d & 0x0F0F0F0Fu, M.cb0, M.cb1, M.cb2, M.cb3);
+                hi = nf4_xlut((d >> 4) & 0x0F0F0F0Fu, M.cb0, M.cb1, M.cb2, M.cb3);
             }
             acc[j] = __builtin_amdgcn_sdot4((int)lo, (int)x[kk].x,
                                             __builtin_amdgcn_sdot4((int)hi, (int)x[kk].y, acc[j], false), false);
