@@ -93,13 +93,13 @@ def test_long_context_splits(gpu_ctx):
 
 @pytest.mark.parametrize("hd", [64, 128])
 def test_gqa_long_context_xcd_order(gpu_ctx, hd):
-    """GQA (8 q heads over 2 KV heads) with max_seq 1024: 2 KV heads x 4 splits = 8 (KV head,
-    split) tiles, so the partial-attention workgroups take the XCD-grouped order (the q
-    heads of one KV head on one XCD); 300 positions fill two splits.  Decode logits vs
-    the oracle."""
+    """GQA (8 q heads over 2 KV heads) with max_seq 2048: contexts above 1024 positions use
+    256-position spans (8 spans here), so the partial-attention workgroups take the
+    XCD-grouped order (the q heads of one KV head on one XCD), then the span merge; 300
+    positions fill two spans.  Decode logits vs the oracle."""
     print(f"gqa long context hd={hd}", flush=True)
     cfg = dict(n_layers=1, hidden=8 * hd, n_heads=8, n_kv_heads=2, head_dim=hd, intermediate=256, vocab=200,
-               max_seq=1024, rms_eps=1e-5, rope_theta=10000.0)
+               max_seq=2048, rms_eps=1e-5, rope_theta=10000.0)
     layers, head, fn = random_model(cfg, seed=11, fmt="nf4")
     ref = OracleModel(cfg, layers, head, fn)
     gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
