@@ -27,13 +27,14 @@ struct MkParams {
     int d, nq, nkv, hd, inter, vocab, max_seq, kmax;
     float eps, attn_scale;
     const float *rope;
-    const int *pos_dev;
-    const int *tokens;
-    const uint32_t *step_dev;
+    int *pos_dev;      // advanced by the kernel's last step (with step_dev)
+    int *tokens;       // input token; the kernel's last step writes the greedy next token
+    uint32_t *step_dev;
     int8_t *kq, *vq;
     float *ks, *vs;
     // hand-off vectors as {payload, epoch} words
     unsigned long long *HA, *HB, *QKV, *OACT, *GACT;
+    unsigned long long *BEST;  // [2 * grid] per-workgroup lm_head maximum {value, row} words
     float *logits;
     const uint64_t *signs;  // Hadamard sign masks of 64-blocks (bit i = element i)
     int *err;
@@ -57,6 +58,5 @@ bool decode_mk_supported(const k2t_model_config &c, int num_cus);
 // each matrix's plane count (4 or 5).
 bool decode_mk_format(const MatDev &m, int &fmt, int &hp);
 void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds);
-void launch_advance_step(hipStream_t st, int *pos, uint32_t *step, int n);
 
 }  // namespace k2t

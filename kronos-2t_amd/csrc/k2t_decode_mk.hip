@@ -623,14 +623,113 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
         }
         if (!ok) return;
     }
-}
-
-__global__ void advance_step_kernel(int *pos, uint32_t *step, int n) {
-    if (threadIdx.x == 0) {
-        pos[0] += n;
-        step[0] += 1u;
+    // Greedy choice (argmax_scalar, real_llm.rs:9914-9924: largest logit, lowest row on
+    // ties) and the position / step advance, inside the launch.  Each workgroup reduces
+    // the logits rows it wrote in the lm_head phase (its own stores, visible after the
+    // barrier) and hands {value, row} over as two words; workgroup 0 combines them, writes
+    // the next input token and advances the position and the step counter.  Every
+    // workgroup read the position and step at its start, before its words existed.
+    {
+        const MatDev &M = P.head;
+        const int nwg = (int)gridDim.x;
+        const int vb = ((int)blockIdx.x + nwg - P.head_off) % nwg;
+        const int nblocks = M.smode ? M.stripes : M.np + (M.stripes & 1);
+        const int groups = kWaves / M.nseg;
+        const int ntk = (nblocks + groups - 1) / groups;
+        const int RB = M.smode ? 16 : 32;
+        __syncthreads();
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int tk = vb; tk < ntk; tk += nwg) {
+            const int base = tk * groups;
+            for (int i = t; i < groups * RB; i += kThreads) {
+                const int g2 = i / RB, rl = i % RB, rb2 = xcd_stripe<kWaves>(M, base + g2, nblocks);
+                if (rb2 >= nblocks) continue;
+                const bool tail = !M.smode && rb2 >= M.np;
+                const int first_stripe = M.smode ? rb2 : (tail ? 2 * M.np : 2 * rb2);
+                const int row = first_stripe * 16 + rl;
+                if (rl >= (tail ? 16 : RB) || row >= M.rows) continue;
+                const float v = P.logits[row];
+                if (v > bv || (v == bv && row < bi)) {
+                    bv = v;
+                    bi = row;
+                }
+            }
+        }
+        // workgroup reduction: waves, then wave 0 over the wave results
+        for (int m2 = 1; m2 < 64; m2 <<= 1) {
+            const float ov = __shfl_xor(bv, m2, kWave);
+            const int oi = __shfl_xor(bi, m2, kWave);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) {
+            S.vec[wave] = bv;
+            S.vec[kWaves + wave] = __int_as_float(bi);
+        }
+        __syncthreads();
+        if (t == 0) {
+            for (int w = 1; w < kWaves; w++) {
+                const float ov = S.vec[w];
+                const int oi = __float_as_int(S.vec[kWaves + w]);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            ll_store(P.BEST + 2 * blockIdx.x, __float_as_uint(bv), E(nph));
+            ll_store(P.BEST + 2 * blockIdx.x + 1, (uint32_t)bi, E(nph));
+        }
+        if (blockIdx.x != 0) return;
+        bv = -INFINITY;
+        bi = 0x7fffffff;
+        bool ok = true;
+        for (int w = t; w < nwg; w += kThreads) {
+            uint32_t v = 0, r = 0;
+            if (ok && !ll_wait(P, P.BEST + 2 * w, E(nph), v)) ok = false;
+            if (ok && !ll_wait(P, P.BEST + 2 * w + 1, E(nph), r)) ok = false;
+            const float ov = __uint_as_float(v);
+            const int oi = (int)r;
+            if (ok && (ov > bv || (ov == bv && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        for (int m2 = 1; m2 < 64; m2 <<= 1) {
+            const float ov = __shfl_xor(bv, m2, kWave);
+            const int oi = __shfl_xor(bi, m2, kWave);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        __syncthreads();
+        if (lane == 0) {
+            S.vec[wave] = bv;
+            S.vec[kWaves + wave] = __int_as_float(bi);
+        }
+        if (t == 0) S.flag[0] = 0;
+        __syncthreads();
+        if (!ok) S.flag[0] = 1;
+        __syncthreads();
+        if (t == 0 && S.flag[0] == 0) {
+            for (int w = 1; w < kWaves; w++) {
+                const float ov = S.vec[w];
+                const int oi = __float_as_int(S.vec[kWaves + w]);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            P.tokens[0] = bi == 0x7fffffff ? 0 : bi;
+            P.pos_dev[0] = pos + 1;
+            P.step_dev[0] = step + 1u;
+        }
     }
 }
+
 
 }  // namespace
 
@@ -723,9 +822,5 @@ void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int nu
     hip_check(hipGetLastError(), "decode megakernel launch");
 }
 
-void launch_advance_step(hipStream_t st, int *pos, uint32_t *step, int n) {
-    hipLaunchKernelGGL(advance_step_kernel, dim3(1), dim3(64), 0, st, pos, step, n);
-    hip_check(hipGetLastError(), "advance launch");
-}
 
 }  // namespace k2t

@@ -144,7 +144,8 @@ struct k2t_model {
     size_t mk_lds = 0;
     uint32_t *step_dev = nullptr;
     int *err_dev = nullptr;
-    unsigned long long *ll_ha = nullptr, *ll_hb = nullptr, *ll_qkv = nullptr, *ll_oact = nullptr, *ll_gact = nullptr;
+    unsigned long long *ll_ha = nullptr, *ll_hb = nullptr, *ll_qkv = nullptr, *ll_oact = nullptr, *ll_gact = nullptr,
+                       *ll_best = nullptr;
     MkLayer *mk_layers = nullptr;
     int mk_head_off = 0;  // first workgroup of the persistent kernel's lm_head phase
 };
@@ -380,12 +381,13 @@ void forward_mk(k2t_model *m) {
     P.QKV = m->ll_qkv;
     P.OACT = m->ll_oact;
     P.GACT = m->ll_gact;
+    P.BEST = m->ll_best;
     P.logits = m->logits;
     P.signs = m->ctx->signs;
     P.err = m->err_dev;
     P.spin_limit = 1u << 22;
+    // the kernel also writes the greedy next token and advances the position and step
     launch_decode_mk(m->stream, P, fmt, hp, m->ctx->num_cus, m->mk_lds);
-    launch_advance_step(m->stream, m->pos_dev, m->step_dev, 1);
 }
 
 // Raises the persistent kernel's dependency-timeout flag as an error (after a sync).
@@ -493,13 +495,14 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             const uint32_t one[4] = {1u, 0u, 0u, 0u};
             hip_check(hipMemcpy(m->step_dev, one, sizeof(one), hipMemcpyHostToDevice), "step init");
             const size_t words = 2 * (size_t)c.hidden + qkv_w + (size_t)(c.n_heads * c.head_dim / 64) * 18 +
-                                 (size_t)(c.intermediate / 64) * 18;
+                                 (size_t)(c.intermediate / 64) * 18 + 2 * (size_t)ctx->num_cus;
             m->ll_ha = (unsigned long long *)dalloc(m, words * 8);
             hip_check(hipMemset(m->ll_ha, 0, words * 8), "hand-off clear");
             m->ll_hb = m->ll_ha + c.hidden;
             m->ll_qkv = m->ll_hb + c.hidden;
             m->ll_oact = m->ll_qkv + qkv_w;
             m->ll_gact = m->ll_oact + (size_t)(c.n_heads * c.head_dim / 64) * 18;
+            m->ll_best = m->ll_gact + (size_t)(c.intermediate / 64) * 18;
             m->mk_layers = (MkLayer *)dalloc(m, (size_t)c.n_layers * sizeof(MkLayer));
         } catch (...) {
             k2t_model_destroy(m);
@@ -848,10 +851,12 @@ int32_t k2t_model_generate(k2t_model *m, int32_t first_token, int32_t n_steps, i
         std::vector<int> host;
         int *dev_out = nullptr;
         if (tokens_out && n_steps > 0) dev_out = (int *)dalloc(m, (size_t)n_steps * sizeof(int));
+        const bool pk = use_persistent(m);
         for (int i = 0; i < n_steps; i++) {
             decode_step(m);
             // greedy: the next input token is argmax of these logits, written on the device
-            launch_argmax(m->stream, m->logits, m->cfg.vocab, m->tokens);
+            // (by the persistent kernel itself, or by argmax_kernel after the per-op step)
+            if (!pk) launch_argmax(m->stream, m->logits, m->cfg.vocab, m->tokens);
             if (dev_out)
                 hip_check(hipMemcpyAsync(dev_out + i, m->tokens, sizeof(int), hipMemcpyDeviceToDevice, m->stream),
                           "token copy");
