@@ -50,19 +50,36 @@ __device__ __forceinline__ int xchg1(int v) { return __builtin_amdgcn_mov_dpp(v,
 __device__ __forceinline__ int xchg2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
 __device__ __forceinline__ int xchg4(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x101F); }
 
+// Value of lane ^ m (m a power of two below 64) through the cheapest exchange that has
+// exactly that partner: DPP quad permutes for 1 and 2, the DPP row rotate by 8 (which is
+// lane ^ 8 inside a 16-lane row), ds_swizzle's bit mode for 4 and 16, ds_bpermute across
+// the two 32-lane halves.  Every wave reduction and butterfly below pairs the same lanes
+// in the same order as a __shfl_xor loop, so their results are unchanged.
+__device__ __forceinline__ int xor_lane(int v, int m) {
+    switch (m) {
+        case 1: return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+        case 2: return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+        case 4: return __builtin_amdgcn_ds_swizzle(v, 0x101F);
+        case 8: return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);
+        case 16: return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+        default: return __shfl_xor(v, m, kWave);
+    }
+}
+__device__ __forceinline__ float xor_lane(float v, int m) { return __int_as_float(xor_lane(__float_as_int(v), m)); }
+
 __device__ __forceinline__ float wave_max_f(float v) {
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+    for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, xor_lane(v, m));
     return v;
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
+    for (int m = 1; m < kWave; m <<= 1) v += xor_lane(v, m);
     return v;
 }
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
+    for (int m = 1; m < kWave; m <<= 1) v += xor_lane(v, m);
     return v;
 }
 
@@ -101,7 +118,7 @@ __device__ __forceinline__ float row_sumsq_wave(const float *xt, int K, uint32_t
 __device__ __forceinline__ float wave_butterflies64(float v, uint32_t lane) {
 #pragma unroll
     for (int h = 1; h < 64; h <<= 1) {
-        float p = __shfl_xor(v, h, kWave);
+        float p = xor_lane(v, h);
         v = (lane & h) ? (p - v) : (v + p);
     }
     return v;
