@@ -67,6 +67,13 @@ __device__ __forceinline__ int xor_lane(int v, int m) {
 }
 __device__ __forceinline__ float xor_lane(float v, int m) { return __int_as_float(xor_lane(__float_as_int(v), m)); }
 
+// Lane l's value in every lane, for a wave-uniform l (v_readlane, no LDS round trip): the
+// same value as __shfl(v, l).
+__device__ __forceinline__ int lane_val(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float lane_val(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
 __device__ __forceinline__ float wave_max_f(float v) {
 #pragma unroll
     for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, xor_lane(v, m));

@@ -68,8 +68,8 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
         }
     }
     for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = __shfl_xor(best, m, 64);
-        const int oi = __shfl_xor(idx, m, 64);
+        const float ov = xor_lane(best, m);
+        const int oi = xor_lane(idx, m);
         if (ov > best || (ov == best && oi < idx)) {
             best = ov;
             idx = oi;

@@ -569,8 +569,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             for (int i = 0; i < 2; i++) {
                 float v = f[t][i];
                 if (smode) v += __int_as_float(dpp_ror8(__float_as_int(v)));  // lane ^ 8
-                v += __shfl_xor(v, 16, kWave);
-                v += __shfl_xor(v, 32, kWave);
+                v += xor_lane(v, 16);
+                v += xor_lane(v, 32);
                 f[t][i] = v;
             }
         float *part = lds;  // [nseg][NT][RB]

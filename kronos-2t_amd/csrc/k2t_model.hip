@@ -73,8 +73,8 @@ __device__ __forceinline__ void store_q4_block(float v, uint32_t lane, uint8_t *
     float num = 0.0f, den = 0.0f;
 #pragma unroll
     for (int j = 0; j < 64; j++) {
-        num += __shfl(vc, j, kWave);
-        den += __shfl(cc, j, kWave);
+        num += lane_val(vc, j);
+        den += lane_val(cc, j);
     }
     const float s_ref = (den > 1e-12f && num > 0.0f) ? num / den : mx / 127.0f;
     const uint16_t sb = f32_to_bf16_rne(s_ref);
@@ -168,7 +168,7 @@ __device__ __forceinline__ void head_post(const float *__restrict__ h, int head,
     if (head < nq + nkv) {
         const float *row = rope + (size_t)pos * hd;
         if (nb == 1) {  // pairs (i, i+32) live in lanes lane and lane^32
-            const float other = __shfl_xor(v0, 32, kWave);
+            const float other = xor_lane(v0, 32);
             const uint32_t i = lane & 31u;
             const float c = row[i], s = row[32 + i];
             v0 = lane < 32 ? v0 * c - other * s : v0 * c + other * s;
@@ -564,8 +564,8 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 if (j0 + u >= cnt) break;
-                const float e = __shfl(em, j0 + u, kWave);
-                L = fmaf(__shfl(lm, j0 + u, kWave), e, L);
+                const float e = lane_val(em, j0 + u);
+                L = fmaf(lane_val(lm, j0 + u), e, L);
                 o0 = fmaf(v0[u], e, o0);
                 o1 = fmaf(v1[u], e, o1);
             }

@@ -113,8 +113,8 @@ static k2t_experts *make_bank(k2t_ctx *ctx, const k2t_k2tm_header &h) {
 __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = __shfl_xor(v, m, kWave);
-        const int oi = __shfl_xor(i, m, kWave);
+        const float ov = xor_lane(v, m);
+        const int oi = xor_lane(i, m);
         if (ov > v || (ov == v && oi < i)) {
             v = ov;
             i = oi;
@@ -173,22 +173,22 @@ __device__ void select_routes(float sc[4], int lane, int E, int k, int norm_topk
     }
     // Weight normalization; the sums run over the selections in selection order.
     if (scoring == K2T_MOE_TOPK_SOFTMAX) {
-        const float mz = __shfl(my_w, 0, kWave);
+        const float mz = lane_val(my_w, 0);
         const float ex = lane < k ? expf(my_w - mz) : 0.0f;
         float s = 0.0f;
-        for (int r = 0; r < k; r++) s += __shfl(ex, r, kWave);
+        for (int r = 0; r < k; r++) s += lane_val(ex, r);
         const float inv = s > 0.0f ? 1.0f / s : 1.0f / (float)k;
         my_w = ex * inv;
     } else if (norm_topk) {
         float s = 0.0f;
-        for (int r = 0; r < k; r++) s += __shfl(my_w, r, kWave);
+        for (int r = 0; r < k; r++) s += lane_val(my_w, r);
         if (s > 0.0f) my_w *= 1.0f / s;
     }
     // Ascending expert id (sparse_moe.rs:170-179): lane r's rank among the k selections
     // (ids are distinct, ties in id order are impossible).
     int rank = 0;
     for (int r = 0; r < k; r++) {
-        const int other = __shfl(my_id, r, kWave);
+        const int other = lane_val(my_id, r);
         rank += (r != lane && other < my_id) ? 1 : 0;
     }
     if (lane < k) {
