@@ -74,20 +74,23 @@ __device__ __forceinline__ float lane_val(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// Wave reductions: butterflies inside each 32-lane half, after which every lane of a half
+// holds the same bits; the last step combines the two halves' values read from lanes 0
+// and 32, which is the butterfly's own last step (max and + are commutative).
 __device__ __forceinline__ float wave_max_f(float v) {
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, xor_lane(v, m));
-    return v;
+    for (int m = 1; m < 32; m <<= 1) v = fmaxf(v, xor_lane(v, m));
+    return fmaxf(lane_val(v, 0), lane_val(v, 32));
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v += xor_lane(v, m);
-    return v;
+    for (int m = 1; m < 32; m <<= 1) v += xor_lane(v, m);
+    return lane_val(v, 0) + lane_val(v, 32);
 }
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v += xor_lane(v, m);
-    return v;
+    for (int m = 1; m < 32; m <<= 1) v += xor_lane(v, m);
+    return lane_val(v, 0) + lane_val(v, 32);
 }
 
 // Sum of squares of a K-float row (K a multiple of 64) by one wave, in a fixed order:
