@@ -462,10 +462,22 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
         const int tt = ps + i * nps;
         if (tt < seq) vacc(tt == pos ? *reinterpret_cast<const int *>(vn + cg * 4) : vpre[i], sc[tt]);
     }
-    for (int tt = ps + kVPre * nps; tt < seq; tt += nps) {
-        const int v = tt == pos ? *reinterpret_cast<const int *>(vn + cg * 4)
-                                : *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4);
-        vacc(v, sc[tt]);
+    // the rest in batches of kVB positions: all of a batch's loads are in flight before
+    // its first use (same positions, same order of accumulation)
+    constexpr int kVB = NTH == 256 ? 8 : 1;  // 512 threads: 2 measured no faster on the 1.7B model
+    for (int tb = ps + kVPre * nps; tb < seq; tb += kVB * nps) {
+        int vb[kVB];
+#pragma unroll
+        for (int u = 0; u < kVB; u++) {
+            const int tt = tb + u * nps;
+            vb[u] = tt < pos ? *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4)
+                             : *reinterpret_cast<const int *>(vn + cg * 4);
+        }
+#pragma unroll
+        for (int u = 0; u < kVB; u++) {
+            const int tt = tb + u * nps;
+            if (tt < seq) vacc(vb[u], sc[tt]);
+        }
     }
     for (int m2 = ncg; m2 < 64; m2 <<= 1) {  // lanes l and l ^ m2 hold the same columns
         a0 += __shfl_xor(a0, m2, kWave);

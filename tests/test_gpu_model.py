@@ -139,6 +139,29 @@ def test_sliding_window_ring_matches_oracle(gpu_ctx, hd, n_tok):
     assert gm.kv_window() == (0, 0) and gm.position() == 0
 
 
+@pytest.mark.parametrize("n_tok", [300, 530])
+def test_persistent_mixed_long_context_matches_oracle(gpu_ctx, n_tok):
+    """p55454 on the 256-thread persistent kernel (mode 2) past 256 positions: each thread
+    scores several positions, and the V slices beyond the first 128 positions (8 per
+    position subset, prefetched) take the batched V path, one and several batches.
+    Prefill (per-operation path), then decode steps on the persistent kernel vs the oracle."""
+    print(f"persistent mixed long context tokens={n_tok}", flush=True)
+    cfg = dict(TINY, max_seq=n_tok + 8)
+    layers, head, fn = random_model(cfg, seed=31, fmt="n4", planes=P55454)
+    ref = OracleModel(cfg, layers, head, fn)
+    gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
+    gm.set_persistent(2)
+    assert gm.persistent_active()
+    toks = np.random.default_rng(32).integers(0, cfg["vocab"], n_tok)
+    gm.prefill(toks[:-3], want_logits=False)
+    for t in toks[:-3]:
+        ref.forward_token(int(t))
+    for t in toks[-3:]:
+        a, b = gm.decode(int(t)), ref.forward_token(int(t))
+        ok, info = _close(a, b, 0.9999)
+        assert ok, info
+
+
 def test_prefill_equals_token_by_token_and_graph_equals_eager(gpu_ctx):
     """Batched prefill and token-by-token decode on the one-kernel-per-operation path run
     the same arithmetic (bit-exact); the persistent kernel sums attention and GEMV
