@@ -462,7 +462,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
         }
     }
     // the span kernel (32 positions per thread at hd 128) batches 8 deep (30B-A3B decode
-    // +1.7% over 4; 16 was slower), the whole-context kernel 4 deep (16 measured slower)
+    // +1.7% over 4; 16 was slower), the whole-context kernel 4 deep (8: decode unchanged,
+    // prefill -12%; 16 slower)
     constexpr int kVB = FINAL ? 4 : 8;
     for (; kr.bits != 4 && i + (kVB - 1) * nps < n; i += kVB * nps) {
         int vv[kVB];
