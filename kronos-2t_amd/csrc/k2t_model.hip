@@ -242,6 +242,8 @@ constexpr int kAttnSplitLen = 256;
 // over every position, and that workgroup also writes the o_proj activation (FINAL): no
 // merge kernel.
 constexpr int kAttnWhole = 1024;
+// Span merges over at most this many spans issue all their loads at once.
+constexpr int kMergeOneShot = 32;
 
 // Sum of n (a power of two) values in a fixed pairwise tree.
 __device__ __forceinline__ float tree_sum(const float *v, int n) {
@@ -544,34 +546,60 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
     const int act = active_len(kr, pos_dev[0] + tok + 1);
     const int ns = min(nsplit, (act + kAttnSplitLen - 1) / kAttnSplitLen);
     const float *pp = part + (size_t)(tok * nq + head) * nsplit * (2 + hd);
-    // Split maxima and sums one split per lane (loads in flight together), then the
-    // rescaled sums in split order.
-    float M = -INFINITY;
-    for (int s = (int)lane; s < ns; s += 64) M = fmaxf(M, pp[(size_t)s * (2 + hd)]);
-    M = wave_max_f(M);
-    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
     const int nb = hd / 64;
-    for (int s0 = 0; s0 < ns; s0 += 64) {
-        const int s = s0 + (int)lane;
-        const float em = s < ns ? expf(pp[(size_t)s * (2 + hd)] - M) : 0.0f;
-        const float lm = s < ns ? pp[(size_t)s * (2 + hd) + 1] : 0.0f;
-        const int cnt = min(64, ns - s0);
-        for (int j0 = 0; j0 < cnt; j0 += 8) {
-            float v0[8], v1[8];
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    if (ns <= kMergeOneShot) {
+        // Every load in one round trip: split s's maximum and sum in lane s, and this
+        // lane's columns of every split; then the same arithmetic, in split order, as the
+        // general path below.
+        const bool mine = (int)lane < ns;
+        const float mv = mine ? pp[(size_t)lane * (2 + hd)] : -INFINITY;
+        const float lm = mine ? pp[(size_t)lane * (2 + hd) + 1] : 0.0f;
+        float v0[kMergeOneShot], v1[kMergeOneShot];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const float *ps = pp + (size_t)(s0 + j0 + u) * (2 + hd);
-                const bool ok = j0 + u < cnt;
-                v0[u] = ok ? ps[2 + lane] : 0.0f;
-                v1[u] = ok && nb > 1 ? ps[2 + 64 + lane] : 0.0f;
-            }
+        for (int u = 0; u < kMergeOneShot; u++) {
+            const float *ps = pp + (size_t)u * (2 + hd);
+            v0[u] = u < ns ? ps[2 + lane] : 0.0f;
+            v1[u] = u < ns && nb > 1 ? ps[2 + 64 + lane] : 0.0f;
+        }
+        const float M = wave_max_f(mv);
+        const float em = mine ? expf(mv - M) : 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                if (j0 + u >= cnt) break;
-                const float e = lane_val(em, j0 + u);
-                L = fmaf(lane_val(lm, j0 + u), e, L);
-                o0 = fmaf(v0[u], e, o0);
-                o1 = fmaf(v1[u], e, o1);
+        for (int u = 0; u < kMergeOneShot; u++) {
+            if (u >= ns) break;
+            const float e = lane_val(em, u);
+            L = fmaf(lane_val(lm, u), e, L);
+            o0 = fmaf(v0[u], e, o0);
+            o1 = fmaf(v1[u], e, o1);
+        }
+    } else {
+        // Split maxima and sums one split per lane (loads in flight together), then the
+        // rescaled sums in split order.
+        float M = -INFINITY;
+        for (int s = (int)lane; s < ns; s += 64) M = fmaxf(M, pp[(size_t)s * (2 + hd)]);
+        M = wave_max_f(M);
+        for (int s0 = 0; s0 < ns; s0 += 64) {
+            const int s = s0 + (int)lane;
+            const float em = s < ns ? expf(pp[(size_t)s * (2 + hd)] - M) : 0.0f;
+            const float lm = s < ns ? pp[(size_t)s * (2 + hd) + 1] : 0.0f;
+            const int cnt = min(64, ns - s0);
+            for (int j0 = 0; j0 < cnt; j0 += 8) {
+                float v0[8], v1[8];
+    #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const float *ps = pp + (size_t)(s0 + j0 + u) * (2 + hd);
+                    const bool ok = j0 + u < cnt;
+                    v0[u] = ok ? ps[2 + lane] : 0.0f;
+                    v1[u] = ok && nb > 1 ? ps[2 + 64 + lane] : 0.0f;
+                }
+    #pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    if (j0 + u >= cnt) break;
+                    const float e = lane_val(em, j0 + u);
+                    L = fmaf(lane_val(lm, j0 + u), e, L);
+                    o0 = fmaf(v0[u], e, o0);
+                    o1 = fmaf(v1[u], e, o1);
+                }
             }
         }
     }

@@ -62,10 +62,13 @@ def _cache(rng, bits, n_kv, cap, hd, fill):
     return kq, ks, vq, vs
 
 
-# (seq above 1024: 256-position spans and the merge kernel; up to 1024 the whole-context kernel)
+# (seq above 1024: 256-position spans and the merge kernel, whose loads go out in one round
+# up to 32 spans and in batches above (8300 positions = 33 spans); up to 1024 the
+# whole-context kernel)
 @pytest.mark.parametrize("bits,hd,seq,window,sinks", [(8, 64, 300, 0, 0), (8, 128, 70, 0, 0), (4, 64, 300, 0, 0),
                                                       (4, 128, 70, 0, 0), (8, 128, 90, 24, 4), (4, 64, 90, 24, 4),
-                                                      (8, 128, 1300, 0, 0), (8, 64, 1100, 0, 0), (4, 64, 1100, 0, 0)])
+                                                      (8, 128, 1300, 0, 0), (8, 64, 1100, 0, 0), (4, 64, 1100, 0, 0),
+                                                      (8, 128, 8300, 0, 0), (4, 64, 8300, 0, 0)])
 def test_attn_decode_matches_oracle(gpu_ctx, bits, hd, seq, window, sinks):
     print(f"attn_decode bits={bits} hd={hd} seq={seq} window={window}", flush=True)
     rng = np.random.default_rng(seq + hd + bits)
