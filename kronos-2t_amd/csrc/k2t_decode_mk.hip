@@ -21,8 +21,10 @@
 //   4 gu    : RMSNorm + FWHT + int8 of hidden_mid, gate_up GEMV of one [gate64, up64]
 //             block per task, SwiGLU + FWHT (chunk ic) + int8 -> down activation chunks
 //   5 down  : down GEMV, hidden = hidden_mid + down
-// then the final norm and lm_head GEMV (logits); argmax and the position advance run as
-// ordinary kernels after it.
+// then the final norm and lm_head GEMV (logits).  For greedy generation the same launch
+// also picks the next token (argmax_kernel's tie rule: largest value, lowest row) and
+// advances the position and the step counter (workgroup 0, after every workgroup's
+// per-row maximum has arrived).
 #include <float.h>
 #include <math.h>
 
