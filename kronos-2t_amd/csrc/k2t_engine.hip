@@ -137,6 +137,7 @@ struct k2t_model {
     bool use_graph = true;
     int exact = 0;  // GEMV epilogue mode used by this model's steps
     hipGraphExec_t graph = nullptr;
+    bool graph_pk = false;  // the captured step is the persistent kernel
     std::vector<void *> allocs;
     // persistent single-launch decode step (fast epilogue, NF4 or 4-plane weights)
     int persistent = 1;  // 0 off, 1 single-format models, 2 also mixed 4/5-plane models
@@ -307,6 +308,17 @@ bool use_persistent(const k2t_model *m) {
            (hp != kHpMixed || m->persistent == 2);
 }
 
+// The persistent kernel gives each q head one workgroup, which scans the whole context:
+// beyond about 1100 attended positions the per-operation path (256-position spans over
+// many workgroups) is faster (1.7B nf4g128: 972 against 964 tok/s at 1029-1093 positions,
+// 724 against 944 at 2053-2117, 391 against 880 at 4101-4165).  A step whose context
+// exceeds this many positions runs the per-operation path.
+constexpr int kMkMaxContext = 1024;
+
+// Whether the decode step at position `pos` (attending pos + 1 positions) runs the
+// persistent kernel.
+bool persistent_at(const k2t_model *m, int pos) { return use_persistent(m) && pos + 1 <= kMkMaxContext; }
+
 // Uploads the layer table of the persistent kernel (matrix views and launch shapes).
 void upload_mk_layers(k2t_model *m) {
     int fmt, hp;
@@ -402,9 +414,13 @@ void check_mk_error(k2t_model *m) {
     }
 }
 
-void decode_step(k2t_model *m) {
+// One decode step at host position m->pos (pk = persistent_at(m, m->pos)).
+void decode_step(k2t_model *m, bool pk) {
     StreamSwap sw(m);
-    const bool pk = use_persistent(m);
+    if (m->graph && m->graph_pk != pk) {  // the context crossed kMkMaxContext: capture the other path
+        (void)hipGraphExecDestroy(m->graph);
+        m->graph = nullptr;
+    }
     if (!m->use_graph) {
         if (pk) {
             upload_mk_layers(m);
@@ -430,6 +446,7 @@ void decode_step(k2t_model *m) {
         hipError_t e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         hip_check(e, "graph instantiate");
+        m->graph_pk = pk;
     }
     hip_check(hipGraphLaunch(m->graph, m->stream), "graph launch");
 }
@@ -795,7 +812,7 @@ int32_t k2t_model_decode(k2t_model *m, int32_t token, float *logits_host) {
         arg(m->pos < m->cfg.max_seq, "context full (max_seq reached)");
         hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
         hip_check(hipMemcpyAsync(m->tokens, &token, sizeof(int), hipMemcpyHostToDevice, m->stream), "token upload");
-        decode_step(m);
+        decode_step(m, persistent_at(m, m->pos));
         m->pos += 1;
         if (logits_host) {
             hip_check(hipMemcpyAsync(logits_host, m->logits, (size_t)m->cfg.vocab * sizeof(float),
@@ -851,9 +868,9 @@ int32_t k2t_model_generate(k2t_model *m, int32_t first_token, int32_t n_steps, i
         std::vector<int> host;
         int *dev_out = nullptr;
         if (tokens_out && n_steps > 0) dev_out = (int *)dalloc(m, (size_t)n_steps * sizeof(int));
-        const bool pk = use_persistent(m);
         for (int i = 0; i < n_steps; i++) {
-            decode_step(m);
+            const bool pk = persistent_at(m, m->pos + i);
+            decode_step(m, pk);
             // greedy: the next input token is argmax of these logits, written on the device
             // (by the persistent kernel itself, or by argmax_kernel after the per-op step)
             if (!pk) launch_argmax(m->stream, m->logits, m->cfg.vocab, m->tokens);
@@ -907,7 +924,7 @@ int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable) {
 int32_t k2t_model_persistent_active(const k2t_model *m, int32_t *active) {
     return mguard([&] {
         arg(m && active, "NULL argument");
-        *active = use_persistent(m) ? 1 : 0;
+        *active = persistent_at(m, m->pos) ? 1 : 0;
     });
 }
 

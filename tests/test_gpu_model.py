@@ -213,6 +213,33 @@ def test_persistent_decode_long_run_matches_per_op(gpu_ctx):
         assert ok, (i, info)
 
 
+def test_persistent_hands_over_to_per_op_past_1024(gpu_ctx):
+    """Decode steps attending more than 1024 positions run the per-operation path even with
+    the persistent kernel enabled (the captured graph is replaced when the context crosses
+    1024); logits track a model on the per-operation path across the switch."""
+    print("persistent -> per-op handover at 1024", flush=True)
+    cfg = dict(TINY, max_seq=1040)
+    layers, head, fn = random_model(cfg, seed=41, fmt="nf4")
+    a, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
+    b, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
+    a.set_persistent(True)
+    b.set_persistent(False)
+    toks = np.random.default_rng(42).integers(0, cfg["vocab"], 1030)
+    a.prefill(toks[:1020], want_logits=False)
+    b.prefill(toks[:1020], want_logits=False)
+    for i, t in enumerate(toks[1020:1028]):
+        assert a.persistent_active() == (1020 + i + 1 <= 1024)
+        x, y = a.decode(int(t)), b.decode(int(t))
+        ok, info = _close(x, y, 0.9999)
+        assert ok, (1020 + i, info)
+    a.generate(int(toks[-1]), 2)
+    assert a.position() == 1030
+    a.reset()
+    assert a.persistent_active()
+    a.decode(int(toks[0]))  # back on the persistent kernel (the graph is captured again)
+    assert a.position() == 1
+
+
 @pytest.mark.parametrize("persistent", [False, True])
 def test_greedy_generate_matches_oracle_argmax(gpu_ctx, persistent):
     layers, head, fn = random_model(TINY, seed=6, fmt="nf4")
