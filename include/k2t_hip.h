@@ -271,8 +271,11 @@ int32_t k2t_model_set_exact(k2t_model *m, int32_t exact);
  * k2t_model_persistent_active); otherwise the per-operation path runs.  2: as 1, and
  * also for bit-plane models that mix 4- and 5-plane matrices (p55454), which then run a
  * 256-thread variant; it is slower than the per-operation path on SmolLM2-135M (one
- * attention head per workgroup), so 1 leaves such models on the per-operation path. */
+ * attention head per workgroup), so 1 leaves such models on the per-operation path.
+ * Either way, a step that attends more than 1024 positions runs the per-operation path
+ * (one workgroup per head scanning the whole context is slower there). */
 int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable);
+/* Whether the next decode step (at the current position) runs the persistent kernel. */
 int32_t k2t_model_persistent_active(const k2t_model *m, int32_t *active);
 /* reset_context: position back to 0. */
 int32_t k2t_model_reset(k2t_model *m);
