@@ -6,6 +6,15 @@
 
 namespace k2t {
 
+// Most positions one decode step of the persistent kernel attends.  Its attention phase
+// gives each q head one workgroup that scans the whole context, so past this many
+// positions the per-operation path (256-position spans over many workgroups) runs
+// instead; the kernel's LDS score buffer is sized for this bound, not for max_seq.
+// 1024 is a rounded crossover: a 1.7B nf4g128 context sweep measured the two paths
+// level at 1029-1093 positions (972 against 964 tok/s) and the persistent kernel
+// behind beyond (724 against 944 tok/s at 2053-2117, 391 against 880 at 4101-4165).
+constexpr int kMkMaxContext = 1024;
+
 struct MkLayer {
     MatDev qkv, o, gu, down;
     const float *in_norm, *post_norm, *bias;

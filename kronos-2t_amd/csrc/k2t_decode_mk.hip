@@ -317,7 +317,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     float *scal = reinterpret_cast<float *>(vn + 128);  // qas, ks_new, vs_new, m, 1/L
     float *red = scal + 8;                              // [32]
     float *opart = red + 32;                            // [16 waves][hd]
-    float *sc = opart + kMaxThreads * 4;                // [max_seq]
+    float *sc = opart + kMaxThreads * 4;                // [min(max_seq, kMkMaxContext)]
     const int t = (int)threadIdx.x;
     const int seq = pos + 1;
     const size_t base = ((size_t)layer * nkv + kvh) * P.max_seq;
@@ -791,7 +791,8 @@ size_t decode_mk_lds_bytes(const k2t_model_config &c) {
     const size_t kmax = std::max(c.hidden, c.intermediate);
     const size_t hd = c.head_dim;
     size_t b = pad16((size_t)c.hidden * 4) + pad16(kmax) + 2 * pad16((kmax / 64) * 4) + kMaxWaves * 32 * 4 + 128 * 4 + 16;
-    b += (3 * hd) * 4 + 3 * 128 + 8 * 4 + 32 * 4 + (size_t)kMaxThreads * 4 * 4 + (size_t)c.max_seq * 4;
+    b += (3 * hd) * 4 + 3 * 128 + 8 * 4 + 32 * 4 + (size_t)kMaxThreads * 4 * 4 +
+         (size_t)std::min(c.max_seq, kMkMaxContext) * 4;
     return (b + 255) / 256 * 256;
 }
 

@@ -308,12 +308,15 @@ bool use_persistent(const k2t_model *m) {
            (hp != kHpMixed || m->persistent == 2);
 }
 
-// The persistent kernel gives each q head one workgroup, which scans the whole context:
-// beyond about 1100 attended positions the per-operation path (256-position spans over
-// many workgroups) is faster (1.7B nf4g128: 972 against 964 tok/s at 1029-1093 positions,
-// 724 against 944 at 2053-2117, 391 against 880 at 4101-4165).  A step whose context
-// exceeds this many positions runs the per-operation path.
-constexpr int kMkMaxContext = 1024;
+// Destroys the captured decode graph after the stream has drained: a replay enqueued
+// earlier may still be reading the executable graph's kernel arguments.
+void drop_graph(k2t_model *m) {
+    if (!m->graph) return;
+    hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+    hip_check(hipStreamSynchronize(m->stream), "sync before graph destroy");
+    (void)hipGraphExecDestroy(m->graph);
+    m->graph = nullptr;
+}
 
 // Whether the decode step at position `pos` (attending pos + 1 positions) runs the
 // persistent kernel.
@@ -417,10 +420,9 @@ void check_mk_error(k2t_model *m) {
 // One decode step at host position m->pos (pk = persistent_at(m, m->pos)).
 void decode_step(k2t_model *m, bool pk) {
     StreamSwap sw(m);
-    if (m->graph && m->graph_pk != pk) {  // the context crossed kMkMaxContext: capture the other path
-        (void)hipGraphExecDestroy(m->graph);
-        m->graph = nullptr;
-    }
+    // the context crossed kMkMaxContext: capture the other path (an earlier step of a
+    // generate() loop may still be replaying the old graph; drop_graph waits for it)
+    if (m->graph && m->graph_pk != pk) drop_graph(m);
     if (!m->use_graph) {
         if (pk) {
             upload_mk_layers(m);
@@ -576,10 +578,7 @@ int32_t k2t_model_set_layer(k2t_model *m, int32_t layer, const k2t_mat *qkv, con
         L.gu = gate_up;
         L.down = down;
         if (gate_up) L.has_moe = false;
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
     });
 }
 
@@ -595,10 +594,7 @@ int32_t k2t_model_set_head(k2t_model *m, const k2t_mat *lm_head, const float *fi
         hip_check(hipMemcpy(m->final_norm, final_norm, m->cfg.hidden * sizeof(float), hipMemcpyHostToDevice),
                   "norm upload");
         m->head = lm_head;
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
     });
 }
 
@@ -619,10 +615,7 @@ int32_t k2t_model_set_qk_norm(k2t_model *m, int32_t layer, const float *q_norm, 
         };
         put(L.q_norm, q_norm);
         put(L.k_norm, k_norm);
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
     });
 }
 
@@ -656,10 +649,7 @@ int32_t k2t_model_set_moe(k2t_model *m, int32_t layer, const k2t_experts *bank, 
         }
         L.moe = MoeLayer{bank, shard_layer, rw, rb, top_k, norm_topk_prob ? 1 : 0, scoring};
         L.has_moe = true;
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
     });
 }
 
@@ -687,10 +677,7 @@ int32_t k2t_model_set_embedding(k2t_model *m, int32_t kind, const void *rows, co
             arg(false, "unknown embedding kind");
         }
         m->embed_kind = kind;
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
     });
 }
 
@@ -705,10 +692,7 @@ int32_t k2t_model_set_exact(k2t_model *m, int32_t exact) {
     return mguard([&] {
         arg(m != nullptr, "model is NULL");
         m->exact = exact ? 1 : 0;
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
     });
 }
 
@@ -732,10 +716,7 @@ int32_t k2t_model_set_kv_window(k2t_model *m, int32_t window, int32_t sink_token
         // set_kv_sliding_window starts a new context (real_llm.rs:1764-1790)
         hip_check(hipMemset(m->pos_dev, 0, sizeof(int)), "pos reset");
         m->pos = 0;
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
     });
 }
 
@@ -750,10 +731,7 @@ int32_t k2t_model_set_kv_bits(k2t_model *m, int32_t bits) {
         m->ring.bits = bits;
         hip_check(hipMemset(m->pos_dev, 0, sizeof(int)), "pos reset");
         m->pos = 0;
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
     });
 }
 
@@ -914,10 +892,7 @@ int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable) {
         arg(m != nullptr, "model is NULL");
         arg(enable >= 0 && enable <= 2, "persistent mode must be 0, 1 or 2");
         m->persistent = enable;
-        if (m->graph) {
-            (void)hipGraphExecDestroy(m->graph);
-            m->graph = nullptr;
-        }
+        drop_graph(m);
     });
 }
 

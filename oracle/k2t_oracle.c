@@ -181,6 +181,25 @@ float or_inv_rms(const float *x, size_t n, float eps) {
     return 1.0f / sqrtf(mean_sq + eps);
 }
 
+/* The same with the aarch64 sum of squares, dot_f32_neon_16 (real_llm.rs:929-962): four
+ * 4-lane accumulators fed by fused multiply-adds over 16-element steps, the accumulators
+ * added lane-wise as (acc0 + acc1) + (acc2 + acc3), the lanes reduced pairwise
+ * (l0 + l1) + (l2 + l3), then the remainder added sequentially (x*y rounded, then +).
+ * The reference's NEON and x86 builds differ only by this summation order. */
+float or_inv_rms_neon(const float *x, size_t n, float eps) {
+    float acc[4][4] = {{0}};
+    size_t i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int v = 0; v < 4; v++)
+            for (int l = 0; l < 4; l++) acc[v][l] = fmaf(x[i + 4 * v + l], x[i + 4 * v + l], acc[v][l]);
+    float lane[4];
+    for (int l = 0; l < 4; l++) lane[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+    float sum = (lane[0] + lane[1]) + (lane[2] + lane[3]);
+    for (; i < n; i++) sum += x[i] * x[i];
+    float mean_sq = sum / (float)n;
+    return 1.0f / sqrtf(mean_sq + eps);
+}
+
 /* ------------------------------------------------------------------ */
 /* Bipolar RTN quantizer (compiler.rs:912-1107, hessian = None)        */
 /* ------------------------------------------------------------------ */

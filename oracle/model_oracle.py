@@ -20,6 +20,17 @@ import numpy as np
 import oracle as O
 
 
+_POOLS = {}
+
+
+def _pool(n):
+    """A persistent host thread pool per width (the C calls release the GIL)."""
+    if n not in _POOLS:
+        import concurrent.futures as cf
+        _POOLS[n] = cf.ThreadPoolExecutor(max_workers=n)
+    return _POOLS[n]
+
+
 class Matrix:
     """A quantized matrix in the reference's stream layout."""
 
@@ -27,10 +38,27 @@ class Matrix:
         self.fmt, self.rows, self.cols, self.pair, self.tail = fmt, rows, cols, pair, tail
         self.hp, self.cb, self.sgc = hp, cb, sgc
 
-    def gemv(self, xq, xs, xsum):
-        if self.fmt == "n4":
-            return O.nibble4_gemv(self.pair, self.tail, self.rows, self.cols, self.hp, xq, xs, xsum)
-        return O.nf_gemv(self.pair, self.tail, self.rows, self.cols, 4, self.sgc, self.cb, xq, xs)
+    def gemv(self, xq, xs, xsum, threads=1):
+        """Integer-exact path (simd_lut.rs:3766-4091 / 6074-6364).  With threads > 1 the
+        stripe range is split over host threads; each output row is computed by exactly
+        one call, so the result does not depend on the split."""
+        def run(s0, s1):
+            if self.fmt == "n4":
+                return O.nibble4_gemv(self.pair, self.tail, self.rows, self.cols, self.hp, xq, xs, xsum, s0=s0,
+                                      s1=s1)
+            return O.nf_gemv(self.pair, self.tail, self.rows, self.cols, 4, self.sgc, self.cb, xq, xs, s0=s0, s1=s1)
+
+        stripes = (self.rows + 15) // 16
+        if threads <= 1 or stripes < 4:
+            return run(0, stripes)
+        out = np.zeros(self.rows, np.float32)
+        per = max(2, ((stripes + threads - 1) // threads + 1) & ~1)
+
+        def work(s0, s1):
+            out[s0 * 16:min(s1 * 16, self.rows)] = run(s0, s1)[s0 * 16:min(s1 * 16, self.rows)]
+
+        list(_pool(threads).map(lambda a: work(a, min(stripes, a + per)), range(0, stripes, per)))
+        return out
 
     def gemv_portable(self, xq, xs, threads=1):
         """Portable path (simd_lut.rs:3558-3581 / 5719-5748), stripe ranges over host threads
@@ -85,8 +113,13 @@ class OracleModel:
     """`gemv_threads` > 0 switches every projection to the threaded portable path (the
     timed CPU baseline); 0 keeps the NEON-semantics integer path (the parity oracle)."""
 
-    def __init__(self, cfg, layers, head, final_norm, gemv_threads=0, embed=None, window=0, sinks=0, kv_bits=8):
+    def __init__(self, cfg, layers, head, final_norm, gemv_threads=0, embed=None, window=0, sinks=0, kv_bits=8,
+                 parity_threads=1, rms_order="x86"):
         self.gemv_threads = gemv_threads
+        # sum-of-squares order of the hidden-state norms: "x86" or "neon", the reference's
+        # two builds (real_llm.rs:903-962); everything else is the same arithmetic
+        self.rms_order = rms_order
+        self.parity_threads = parity_threads  # host threads for the integer-exact GEMVs
         self.embed_fn = embed  # untied embedding: token -> f32[hidden] (embed_token_into)
         self.cfg = cfg
         self.layers = layers  # dicts: qkv, o, gu, down (Matrix), in_norm, post_norm, bias
@@ -114,7 +147,7 @@ class OracleModel:
     def _gemv(self, m, xq, xs, xsum):
         if self.gemv_threads:
             return m.gemv_portable(xq, xs, self.gemv_threads)
-        return m.gemv(xq, xs, xsum)
+        return m.gemv(xq, xs, xsum, self.parity_threads)
 
     def slot_of_pos(self, pos):
         """real_llm.rs:1116-1122"""
@@ -135,7 +168,9 @@ class OracleModel:
             return self.embed_fn(token)
         return O.ifwht64(self.head.row_rotated(token))
 
-    def forward_token(self, token):
+    def forward_token(self, token, want_logits=True):
+        """One decode step; want_logits=False stops after the last layer (a prefill
+        token whose logits nobody reads; the KV cache and position advance the same)."""
         c = self.cfg
         d, nq, nkv, hd, inter, eps = c["hidden"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["intermediate"], \
             c["rms_eps"]
@@ -145,7 +180,7 @@ class OracleModel:
         hidden = self.embed(token).astype(np.float32)
         self.last_routes = []
         for li, L in enumerate(self.layers):
-            xq, xs, xsum = O.populate_fwht(hidden, L["in_norm"], O.inv_rms(hidden, eps))
+            xq, xs, xsum = O.populate_fwht(hidden, L["in_norm"], O.inv_rms(hidden, eps, self.rms_order))
             qkv = self._gemv(L["qkv"], xq, xs, xsum).reshape(-1, hd)
             if L.get("bias") is not None:
                 qkv = (qkv + L["bias"].reshape(-1, hd)).astype(np.float32)
@@ -185,13 +220,15 @@ class OracleModel:
                 hidden, routes = moe_ffn(hidden, L["post_norm"], eps, L["moe"])
                 self.last_routes.append(routes)
                 continue
-            xq, xs, xsum = O.populate_fwht(hidden, L["post_norm"], O.inv_rms(hidden, eps))
+            xq, xs, xsum = O.populate_fwht(hidden, L["post_norm"], O.inv_rms(hidden, eps, self.rms_order))
             gu = self._gemv(L["gu"], xq, xs, xsum).reshape(-1, 128)
             sw = np.concatenate([O.swiglu(gu[ic, :64], gu[ic, 64:]) for ic in range(inter // 64)])
             iq, is_, isum = O.populate_fwht(sw)
             hidden = (hidden + self._gemv(L["down"], iq, is_, isum)).astype(np.float32)
-        xq, xs, xsum = O.populate_fwht(hidden, self.final_norm, O.inv_rms(hidden, eps))
         self.pos += 1
+        if not want_logits:
+            return None
+        xq, xs, xsum = O.populate_fwht(hidden, self.final_norm, O.inv_rms(hidden, eps, self.rms_order))
         return self._gemv(self.head, xq, xs, xsum)
 
 

@@ -44,6 +44,7 @@ def lib():
             "or_populate_fwht": (None, [F32P, VP, C.c_float, SZ, I8P, F32P, I32P]),
             "or_populate_plain": (None, [F32P, SZ, I8P, F32P, I32P]),
             "or_inv_rms": (C.c_float, [F32P, SZ, C.c_float]),
+            "or_inv_rms_neon": (C.c_float, [F32P, SZ, C.c_float]),
             "or_bipolar_rtn": (None, [F32P, SZ, SZ, C.c_int, U8P, U16P]),
             "or_pack_interleaved": (None, [U8P, SZ, SZ, C.c_int, U8P]),
             "or_nibble4_repack": (None, [U8P, U16P, SZ, SZ, C.c_int, C.c_int, U8P, U8P]),
@@ -146,9 +147,12 @@ def populate_plain(x):
     return q, s, sm
 
 
-def inv_rms(x, eps):
+def inv_rms(x, eps, order="x86"):
+    """real_llm.rs:903-926 (x86: four scalar accumulators) or, with order="neon",
+    929-962 (aarch64: 4x4 fused-multiply-add accumulators)."""
     x = _f32(x)
-    return float(lib().or_inv_rms(x, x.size, float(eps)))
+    fn = lib().or_inv_rms_neon if order == "neon" else lib().or_inv_rms
+    return float(fn(x, x.size, float(eps)))
 
 
 # --------------------------------------------------------------------------- bit-plane

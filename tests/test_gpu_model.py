@@ -262,3 +262,41 @@ def test_model_argument_errors(gpu_ctx):
     gm = k2t.Model(gpu_ctx, TINY)
     with pytest.raises(k2t.K2TError):
         gm.decode(1)  # layers not set
+
+
+def test_generate_hands_over_inside_one_call(gpu_ctx):
+    """One generate() call that starts at position 1018 and runs 12 greedy steps crosses
+    1024 attended positions inside its loop: the persistent kernel's graph is swapped for
+    the per-operation one between two enqueued steps, and the next input token passes
+    from the persistent kernel's own greedy pick to argmax_kernel.  The tokens equal those
+    of the same model run on the per-operation path throughout."""
+    print("generate across the 1024-position handover", flush=True)
+    cfg = dict(TINY, max_seq=1040)
+    layers, head, fn = random_model(cfg, seed=43, fmt="nf4")
+    a, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
+    b, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
+    a.set_persistent(True)
+    b.set_persistent(False)
+    toks = np.random.default_rng(44).integers(0, cfg["vocab"], 1019)
+    a.prefill(toks[:1018], want_logits=False)
+    b.prefill(toks[:1018], want_logits=False)
+    assert a.persistent_active()
+    ga = list(a.generate(int(toks[1018]), 12))
+    gb = list(b.generate(int(toks[1018]), 12))
+    assert a.position() == b.position() == 1030
+    assert not a.persistent_active()
+    assert ga == gb, (ga, gb)
+
+
+def test_persistent_kernel_with_large_max_seq(gpu_ctx):
+    """The persistent kernel's LDS score buffer covers at most 1024 positions, so a model
+    created with a long max_seq still runs it at short contexts (and matches the oracle)."""
+    cfg = dict(TINY, max_seq=32768)
+    layers, head, fn = random_model(cfg, seed=45, fmt="nf4")
+    ref = OracleModel(cfg, layers, head, fn)
+    gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
+    gm.set_persistent(True)
+    assert gm.persistent_active()
+    for t in (7, 123, 400):
+        ok, info = _close(gm.decode(t), ref.forward_token(t), 0.9999)
+        assert ok, info

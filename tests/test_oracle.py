@@ -445,3 +445,24 @@ def test_nf4_kv_attention_against_f64():
         want = (p / p.sum()) @ Vd
         cos = np.dot(got, want) / (np.linalg.norm(got) * np.linalg.norm(want))
         assert cos > 0.999, (hd, cos)
+
+
+def test_inv_rms_two_reference_orders():
+    """or_inv_rms (x86 portable, real_llm.rs:910-925) and or_inv_rms_neon (aarch64,
+    929-962) against the f64 closed form, equal to each other where every partial sum is
+    exact (integer squares), and different summation orders (they disagree in the last
+    bit on some random inputs)."""
+    rng = np.random.default_rng(3)
+    for n in (64, 576, 2048, 100):
+        x = rng.standard_normal(n).astype(np.float32) * 3
+        want = 1.0 / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-5)
+        for order in ("x86", "neon"):
+            assert abs(O.inv_rms(x, 1e-5, order) / want - 1) < 2e-6
+    xi = np.arange(1, 65, dtype=np.float32)  # integer squares: every partial sum exact
+    assert O.inv_rms(xi, 0.0, "x86") == O.inv_rms(xi, 0.0, "neon")
+    assert O.inv_rms(xi, 0.0) == np.float32(1.0) / np.sqrt(np.float32(np.sum(xi.astype(np.float64) ** 2) / 64))
+    diff = 0
+    for s in range(200):
+        x = np.random.default_rng(s).standard_normal(48).astype(np.float32)
+        diff += O.inv_rms(x, 1e-5, "x86") != O.inv_rms(x, 1e-5, "neon")
+    assert diff > 0
