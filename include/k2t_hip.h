@@ -312,6 +312,20 @@ int32_t k2t_attn_decode(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_
                         int32_t head_dim, const void *d_kq, const void *d_ks, const void *d_vq, const void *d_vs,
                         int32_t cap, int32_t seq, int32_t window, int32_t sink_tokens, float attn_scale,
                         float *d_out);
+/* k2t_attn_decode without any allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results as k2t_attn_decode
+ * (the same kernels), but the span partials and the position word live in a fixed 4 MiB
+ * device array inside the library (one per GPU, kept until the process ends): calls with
+ * n_heads * ceil(min(seq, window or seq) / 256) * (head_dim + 2) > 1048512 floats (for
+ * contexts above 1024 positions; at most 1024 positions use a single span) return
+ * K2T_E_ARG.  Asynchronous on the context's stream (the caller synchronizes).  Every call
+ * on one GPU shares that array: calls that overlap on one GPU (other streams, other
+ * contexts, other host threads) race. */
+int32_t k2t_attn_decode_noalloc(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_heads, int32_t n_kv_heads,
+                                int32_t head_dim, const void *d_kq, const void *d_ks, const void *d_vq,
+                                const void *d_vs, int32_t cap, int32_t seq, int32_t window, int32_t sink_tokens,
+                                float attn_scale, float *d_out);
 
 /* ---- sparse-MoE experts (.k2tm shards) ------------------------------------- */
 

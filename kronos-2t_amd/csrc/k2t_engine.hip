@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "../../include/k2t_hip.h"
@@ -99,7 +100,39 @@ void launch_argmax(hipStream_t st, const float *x, int n, int *out_idx) {
 
 }  // namespace k2t
 
+// Device scratch of k2t_attn_decode_noalloc: the span partials (n_heads * splits *
+// (head_dim + 2) floats) and the position word.  One copy per GPU, held until the process
+// ends.  Host code never passes this name to a kernel or a copy: it is a host-side
+// stand-in there; noalloc_scratch() looks up each device's own address.
+constexpr size_t kNoAllocScratchFloats = (size_t)1 << 20;  // 4 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace k2t {
+__global__ void store_int_kernel(int *dst, int v) {
+    if (threadIdx.x == 0) dst[0] = v;
+}
+}  // namespace k2t
+
 using namespace k2t;
+
+namespace {
+constexpr int kMaxNoAllocDevices = 64;
+std::mutex g_noalloc_mu;
+float *g_noalloc_ptr[kMaxNoAllocDevices] = {};
+
+// The address of `scratch` on `device` (which must be current), looked up once per
+// device with hipGetSymbolAddress.
+float *noalloc_scratch(int device) {
+    if (device < 0 || device >= kMaxNoAllocDevices) throw Error(K2T_E_ARG, "device index out of range");
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[device]) {
+        void *p = nullptr;
+        hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        g_noalloc_ptr[device] = static_cast<float *>(p);
+    }
+    return g_noalloc_ptr[device];
+}
+}  // namespace
 
 struct k2t_model {
     k2t_ctx *ctx = nullptr;
@@ -916,38 +949,77 @@ int32_t k2t_kv_store(k2t_ctx *ctx, int32_t bits, const float *d_heads, int32_t n
     });
 }
 
+namespace {
+// k2t_attn_decode's body.  noalloc: the partials and the position live in the static
+// `scratch` array (no allocation, no host-to-device copy); otherwise in the context's
+// scratch, grown on demand.
+void attn_decode_impl(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_heads, int32_t n_kv_heads,
+                      int32_t head_dim, const void *d_kq, const void *d_ks, const void *d_vq, const void *d_vs,
+                      int32_t cap, int32_t seq, int32_t window, int32_t sink_tokens, float attn_scale, float *d_out,
+                      bool noalloc) {
+    arg(ctx && d_q && d_kq && d_ks && d_vq && d_vs && d_out, "NULL argument");
+    arg(bits == 4 || bits == 8, "KV bits must be 4 or 8");
+    arg(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128");
+    arg(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
+    arg(seq >= 1 && cap >= 1 && seq <= (1 << 24), "seq / cap out of range");
+    KvRing kr{cap, 0, 0, 0, bits};
+    if (window > 0) {
+        arg(window >= 8 && sink_tokens >= 0 && sink_tokens <= window / 2, "window >= 8 and sinks <= window / 2");
+        arg(cap > window, "a windowed cache needs cap > window");
+        kr = KvRing{cap, window, sink_tokens, cap - sink_tokens, bits};
+    } else {
+        arg(seq <= cap, "seq exceeds the cache");
+    }
+    const int act = window > 0 ? std::min(seq, window) : seq;
+    const int nsplit = attn_max_splits(act);
+    hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+    const size_t part = (size_t)n_heads * nsplit * (2 + head_dim);
+    float *pp;
+    if (noalloc) {
+        if (part + 64 > kNoAllocScratchFloats)
+            throw Error(K2T_E_ARG, "k2t_attn_decode_noalloc: n_heads * ceil(positions / 256) * (head_dim + 2) = " +
+                                       std::to_string(part) + " floats exceeds its fixed scratch of " +
+                                       std::to_string(kNoAllocScratchFloats - 64) + " floats");
+        pp = noalloc_scratch(ctx->device);
+    } else {
+        ensure_scratch(ctx, part + 64);
+        pp = ctx->scratch;
+    }
+    int *pos = reinterpret_cast<int *>(pp + part);
+    const int p0 = seq - 1;
+    if (noalloc) {
+        hipLaunchKernelGGL(store_int_kernel, dim3(1), dim3(64), 0, ctx->stream, pos, p0);
+        hip_check(hipGetLastError(), "position store launch");
+    } else {
+        hip_check(hipMemcpyAsync(pos, &p0, sizeof(int), hipMemcpyHostToDevice, ctx->stream), "pos upload");
+    }
+    // read-only on the cache (no post stage: the caller's queries are final)
+    launch_attention(ctx->stream, d_q, n_heads * head_dim, (int8_t *)d_kq, (int8_t *)d_vq, (float *)d_ks,
+                     (float *)d_vs, AttnPost{}, pos, 0, n_heads, n_kv_heads, head_dim, kr, attn_scale, nsplit, 1, pp,
+                     d_out, nullptr, nullptr, nullptr);
+    // the copied position lives on this function's stack; the no-alloc variant stores it
+    // with a kernel and stays asynchronous
+    if (!noalloc) hip_check(hipStreamSynchronize(ctx->stream), "sync");
+}
+}  // namespace
+
 int32_t k2t_attn_decode(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_heads, int32_t n_kv_heads,
                         int32_t head_dim, const void *d_kq, const void *d_ks, const void *d_vq, const void *d_vs,
                         int32_t cap, int32_t seq, int32_t window, int32_t sink_tokens, float attn_scale,
                         float *d_out) {
     return mguard([&] {
-        arg(ctx && d_q && d_kq && d_ks && d_vq && d_vs && d_out, "NULL argument");
-        arg(bits == 4 || bits == 8, "KV bits must be 4 or 8");
-        arg(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128");
-        arg(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
-        arg(seq >= 1 && cap >= 1 && seq <= (1 << 24), "seq / cap out of range");
-        KvRing kr{cap, 0, 0, 0, bits};
-        if (window > 0) {
-            arg(window >= 8 && sink_tokens >= 0 && sink_tokens <= window / 2, "window >= 8 and sinks <= window / 2");
-            arg(cap > window, "a windowed cache needs cap > window");
-            kr = KvRing{cap, window, sink_tokens, cap - sink_tokens, bits};
-        } else {
-            arg(seq <= cap, "seq exceeds the cache");
-        }
-        const int act = window > 0 ? std::min(seq, window) : seq;
-        const int nsplit = attn_max_splits(act);
-        hip_check(hipSetDevice(ctx->device), "hipSetDevice");
-        const size_t part = (size_t)n_heads * nsplit * (2 + head_dim);
-        ensure_scratch(ctx, part + 64);
-        float *pp = ctx->scratch;
-        int *pos = reinterpret_cast<int *>(ctx->scratch + part);
-        const int p0 = seq - 1;
-        hip_check(hipMemcpyAsync(pos, &p0, sizeof(int), hipMemcpyHostToDevice, ctx->stream), "pos upload");
-        // read-only on the cache (no post stage: the caller's queries are final)
-        launch_attention(ctx->stream, d_q, n_heads * head_dim, (int8_t *)d_kq, (int8_t *)d_vq, (float *)d_ks,
-                         (float *)d_vs, AttnPost{}, pos, 0, n_heads, n_kv_heads, head_dim, kr, attn_scale, nsplit, 1,
-                         pp, d_out, nullptr, nullptr, nullptr);
-        hip_check(hipStreamSynchronize(ctx->stream), "sync");  // the position lives in host memory above
+        attn_decode_impl(ctx, bits, d_q, n_heads, n_kv_heads, head_dim, d_kq, d_ks, d_vq, d_vs, cap, seq, window,
+                         sink_tokens, attn_scale, d_out, false);
+    });
+}
+
+int32_t k2t_attn_decode_noalloc(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_heads, int32_t n_kv_heads,
+                                int32_t head_dim, const void *d_kq, const void *d_ks, const void *d_vq,
+                                const void *d_vs, int32_t cap, int32_t seq, int32_t window, int32_t sink_tokens,
+                                float attn_scale, float *d_out) {
+    return mguard([&] {
+        attn_decode_impl(ctx, bits, d_q, n_heads, n_kv_heads, head_dim, d_kq, d_ks, d_vq, d_vs, cap, seq, window,
+                         sink_tokens, attn_scale, d_out, true);
     });
 }
 

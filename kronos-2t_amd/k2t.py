@@ -104,6 +104,8 @@ SIGNATURES = {
     "k2t_model_kv_bits": (I32, [VP, C.POINTER(I32)]),
     "k2t_kv_store": (I32, [VP, I32, VP, I32, I32, VP, VP]),
     "k2t_attn_decode": (I32, [VP, I32, VP, I32, I32, I32, VP, VP, VP, VP, I32, I32, I32, I32, C.c_float, VP]),
+    "k2t_attn_decode_noalloc": (I32, [VP, I32, VP, I32, I32, I32, VP, VP, VP, VP, I32, I32, I32, I32, C.c_float,
+                                      VP]),
 }
 
 MOE_SOFTMAX, MOE_TOPK_SOFTMAX, MOE_SIGMOID = 0, 1, 2
@@ -269,6 +271,14 @@ class Ctx:
         """k2t_attn_decode: one token's attention over a KV cache in k2t_kv_store's layout."""
         check(lib().k2t_attn_decode(self.h, bits, _p(q), n_heads, n_kv_heads, head_dim, _p(kq), _p(ks), _p(vq),
                                     _p(vs), cap, seq, window, sink_tokens, float(attn_scale), _p(out)))
+
+    def attn_decode_noalloc(self, bits, q, n_heads, n_kv_heads, head_dim, kq, ks, vq, vs, cap, seq, attn_scale,
+                            out, window=0, sink_tokens=0):
+        """k2t_attn_decode_noalloc: attn_decode with the library's fixed device scratch
+        (allocates nothing; asynchronous on the context's stream)."""
+        check(lib().k2t_attn_decode_noalloc(self.h, bits, _p(q), n_heads, n_kv_heads, head_dim, _p(kq), _p(ks),
+                                            _p(vq), _p(vs), cap, seq, window, sink_tokens, float(attn_scale),
+                                            _p(out)))
 
     def moe_ffn(self, bank, shard_layer, router_w, hidden, post_norm, eps, top_k, norm_topk_prob=True,
                 scoring=0, router_bias=None, route_ids=None, route_weights=None):
