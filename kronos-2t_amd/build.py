@@ -54,23 +54,49 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
-def _compile(src):
-    obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+def _compile(src, objdir=None, defines=()):
+    obj = os.path.join(objdir or OBJ, os.path.basename(src) + ".o")
+    cmd = [HIPCC, *FLAGS, *[f"-D{d}" for d in defines], "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
     return obj, resource_usage(r.stderr)
 
 
-def build(verbose=False):
-    os.makedirs(OBJ, exist_ok=True)
+def check_m0(src):
+    """Sources that stage weights with inline-assembly LDS-DMA loads set M0 themselves
+    right before each load.  The compiler does not know of that, so its own code must not
+    use M0: check the generated device assembly (every M0 reference is an s_mov_b32 into
+    M0 directly followed by a global_load_lds)."""
+    asm = os.path.join(OBJ, os.path.basename(src) + ".s")
+    cmd = [HIPCC, *[f for f in FLAGS if not f.startswith("-Rpass")], "--cuda-device-only", "-S", src, "-o", asm]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for {src}:\n{r.stderr}")
+    lines = [ln.strip() for ln in open(asm) if not ln.lstrip().startswith((";", "."))]
+    for i, ln in enumerate(lines):
+        if re.search(r"\bm0\b", ln):
+            ok = (re.fullmatch(r"s_mov_b32 m0, s\d+", ln) is not None and i + 1 < len(lines)
+                  and lines[i + 1].startswith("global_load_lds"))
+            if not ok:
+                raise RuntimeError(f"{src}: compiler-generated code uses M0 ({ln!r}); the LDS-DMA loads "
+                                   "assume it does not")
+
+
+def build(verbose=False, out=None, defines=()):
+    """Builds libk2t_hip.so; `out` and `defines` make a variant elsewhere (a measurement
+    build with -DK2T_MK_TRACE, say) without touching the product library."""
+    objdir = OBJ if not defines else os.path.join(OBJ, "variant_" + "_".join(defines))
+    os.makedirs(objdir, exist_ok=True)
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        res = list(ex.map(_compile, srcs))
+        res = list(ex.map(lambda src: _compile(src, objdir, defines), srcs))
     objs = [o for o, _ in res]
+    with cf.ThreadPoolExecutor(max_workers=4) as ex:
+        list(ex.map(check_m0, [src for src in srcs if "global_load_lds" in open(src).read() or
+                               "k2t_gemv_core.h" in open(src).read()]))
     usage = [u for _, us in res for u in us]
-    with open(os.path.join(OBJ, "resource_usage.txt"), "w") as f:
+    with open(os.path.join(objdir, "resource_usage.txt"), "w") as f:
         for name, u in usage:
             f.write(f"{name} " + " ".join(f"{k}={v}" for k, v in u.items()) + "\n")
     bad = [(n, u.get("ScratchSize")) for n, u in usage if n.startswith(NO_SCRATCH) and u.get("ScratchSize", 0) != 0]
@@ -79,15 +105,21 @@ def build(verbose=False):
                            ", ".join(f"{n} ({b} B/lane)" for n, b in bad))
     if not any(n.startswith(NO_SCRATCH) for n, _ in usage):
         raise RuntimeError("no resource report for the persistent decode kernel (remark format changed?)")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", OUT, *objs]
+    out = out or OUT
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     if verbose:
-        print("built", OUT)
-    return OUT
+        print("built", out)
+    return out
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    import argparse
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--define", action="append", default=[], help="preprocessor define of a variant build")
+    ap.add_argument("--out", default=None, help="output path of a variant build")
+    a = ap.parse_args()
+    build(verbose=True, out=a.out, defines=tuple(a.define))
     sys.exit(0)

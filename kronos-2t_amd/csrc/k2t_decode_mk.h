@@ -14,6 +14,8 @@ namespace k2t {
 // level at 1029-1093 positions (972 against 964 tok/s) and the persistent kernel
 // behind beyond (724 against 944 tok/s at 2053-2117, 391 against 880 at 4101-4165).
 constexpr int kMkMaxContext = 1024;
+// Copies of the broadcast hand-off vectors (one per XCD of MI355X).
+constexpr int kMkRep = 8;
 
 struct MkLayer {
     MatDev qkv, o, gu, down;
@@ -41,20 +43,29 @@ struct MkParams {
     uint32_t *step_dev;
     int8_t *kq, *vq;
     float *ks, *vs;
-    // hand-off vectors as {payload, epoch} words
+    // hand-off vectors as {payload, epoch} words.  HA, HB, OACT and GACT, which every
+    // workgroup of the next phase reads, exist in `rep` copies ([rep][n] words); writers
+    // store every copy and a reader polls the copy of its XCD, so each line is polled by
+    // one XCD's workgroups instead of the whole grid.
     unsigned long long *HA, *HB, *QKV, *OACT, *GACT;
+    int rep;
     unsigned long long *BEST;  // [2 * grid] per-workgroup lm_head maximum {value, row} words
     float *logits;
     const uint64_t *signs;  // Hadamard sign masks of 64-blocks (bit i = element i)
     int *err;
     uint32_t spin_limit;
+    // Measurement builds only (compiled with -DK2T_MK_TRACE): per workgroup, layer and
+    // phase the wall clock at the task's start, input arrival and end.
+    unsigned long long *trace;
 };
 
 // pair_mode_nseg4: gate_up layout (4 wave groups = one [gate64, up64] block of 4 pairs).
 // max_nseg (> 0) caps the K segments per row block in stripe mode (more rows per
 // workgroup, fewer workgroups for the phase).
 // nwaves: waves per workgroup of the kernel that will run (decode_mk_threads / 64).
-MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg = 0, int nwaves = 8);
+// min_nseg (> 0) asks for at least that many K segments (fewer rows per workgroup, more
+// workgroups for the phase).
+MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg = 0, int nwaves = 8, int min_nseg = 0);
 // Workgroup tasks of a GEMV phase of the persistent kernel.
 int mk_phase_tasks(const MatDev &M, int nwaves = 8);
 // Threads per workgroup of the persistent kernel for the format decode_mk_format chose.

@@ -46,6 +46,8 @@ namespace {
 constexpr int kMaxThreads = 512;
 constexpr int kMaxWaves = kMaxThreads / 64;
 constexpr int kActWords = 18;  // per 64-element activation chunk: 16 code words, scale, sum
+constexpr int kMkFrags = 4;    // weight fragments in flight per wave (LDS slots)
+constexpr size_t kMkMaxLds = 160 * 1024;  // LDS of one gfx950 CU (one workgroup per CU)
 
 __device__ __forceinline__ void ll_store(unsigned long long *p, uint32_t v, uint32_t epoch) {
     __hip_atomic_store(p, ((unsigned long long)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -54,6 +56,12 @@ __device__ __forceinline__ void ll_store(unsigned long long *p, uint32_t v, uint
 __device__ __forceinline__ unsigned long long ll_load(const unsigned long long *p) {
     return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// Workgroup barrier for LDS data only.  __syncthreads() also waits for every global
+// store and load of the wave to complete (its release fence); hand-off words need no
+// ordering (payload and epoch travel in one word) and weight fragments are awaited
+// explicitly, so the phases use this barrier and never stall on store acknowledgements.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Polls one word until its epoch matches; false on timeout or when another workgroup
 // has raised the error flag.
@@ -83,6 +91,8 @@ struct Lds {
     float *part;     // [16][32] wave partials
     float *vec;      // [128] gate_up block / attention vectors
     float *att;      // attention scratch: q, k, v f32 [3*hd], int8 q/k/v [3*hd], opart, scores
+    uint8_t *ring;   // GEMV weight fragments staged in LDS (kMkFrags slots per wave); shares
+                     // its bytes with `att` (a workgroup runs one task at a time)
     int *flag;       // [4] workgroup flags
 };
 
@@ -105,7 +115,9 @@ __device__ Lds carve(const MkParams &P, float *base) {
     p += 128 * 4;
     L.flag = reinterpret_cast<int *>(p);
     p += 16;
+    p = reinterpret_cast<char *>(((uintptr_t)p + 255) & ~(uintptr_t)255);
     L.att = reinterpret_cast<float *>(p);
+    L.ring = reinterpret_cast<uint8_t *>(p);
     return L;
 }
 
@@ -115,21 +127,24 @@ __device__ Lds carve(const MkParams &P, float *base) {
 // vector, act == false) or are unpacked into the LDS activation (codes, scales, sums;
 // act == true).  Returns false (for the whole workgroup) on error.
 constexpr int kPoll = 8;
+// Only threads t0 .. NTH-1 poll (the others are streaming weights, and a poll of theirs
+// would return only after those loads: vector memory completes in issue order).
 template <int NTH>
 __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, const unsigned long long *src, int n,
-                                           uint32_t epoch, bool act, float *dst) {
+                                           uint32_t epoch, bool act, float *dst, int t0 = 0) {
     bool ok = true;
-    for (int i0 = (int)threadIdx.x; i0 < n; i0 += NTH * kPoll) {
+    const int np = NTH - t0;
+    for (int i0 = (int)threadIdx.x - t0; i0 >= 0 && i0 < n; i0 += np * kPoll) {
         unsigned long long w[kPoll];
 #pragma unroll
         for (int k = 0; k < kPoll; k++) {
-            const int i = i0 + k * NTH;
+            const int i = i0 + k * np;
             w[k] = i < n ? ll_load(src + i) : 0ull;
         }
         uint32_t pending = 0;
 #pragma unroll
         for (int k = 0; k < kPoll; k++)
-            if (i0 + k * NTH < n && (uint32_t)(w[k] >> 32) != epoch) pending |= 1u << k;
+            if (i0 + k * np < n && (uint32_t)(w[k] >> 32) != epoch) pending |= 1u << k;
         for (uint32_t spins = 0; pending != 0 && ok; spins++) {
             if ((spins & 31u) == 31u) {
                 if (__hip_atomic_load(P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
@@ -145,14 +160,14 @@ __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, cons
             }
 #pragma unroll
             for (int k = 0; k < kPoll; k++)
-                if (pending & (1u << k)) w[k] = ll_load(src + i0 + k * NTH);
+                if (pending & (1u << k)) w[k] = ll_load(src + i0 + k * np);
 #pragma unroll
             for (int k = 0; k < kPoll; k++)
                 if ((pending & (1u << k)) && (uint32_t)(w[k] >> 32) == epoch) pending &= ~(1u << k);
         }
 #pragma unroll
         for (int k = 0; k < kPoll; k++) {
-            const int i = i0 + k * NTH;
+            const int i = i0 + k * np;
             if (i < n && ok) {
                 const uint32_t v = (uint32_t)w[k];
                 if (!act) {
@@ -167,15 +182,16 @@ __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, cons
         }
     }
     if (threadIdx.x == 0) S.flag[0] = 0;
-    __syncthreads();
+    lds_barrier();
     if (!ok) S.flag[0] = 1;
-    __syncthreads();
+    lds_barrier();
     return S.flag[0] == 0;
 }
 
 // Quantizes the 64 rotated values held one per lane and stores the chunk as kActWords
 // LL words (simd_lut.rs:3097-3128 arithmetic, as quant_chunk_store).
-__device__ void store_act_chunk(float v, uint32_t lane, unsigned long long *dst, uint32_t epoch) {
+__device__ void store_act_chunk(float v, uint32_t lane, unsigned long long *dst, uint32_t epoch, int rep = 1,
+                                size_t copy_stride = 0) {
     const float mx = wave_max_f(fabsf(v));
     int qi = 0;
     float scale = 0.0f;
@@ -190,12 +206,21 @@ __device__ void store_act_chunk(float v, uint32_t lane, unsigned long long *dst,
     uint32_t word = byte << (8 * (lane & 3u));
     word |= __shfl_xor(word, 1, kWave);
     word |= __shfl_xor(word, 2, kWave);
-    if ((lane & 3u) == 0) ll_store(dst + lane / 4, word, epoch);
-    if (lane == 0) {
-        ll_store(dst + 16, __float_as_uint(scale), epoch);
-        ll_store(dst + 17, (uint32_t)s, epoch);
+    for (int r = 0; r < rep; r++) {
+        unsigned long long *d = dst + (size_t)r * copy_stride;
+        if ((lane & 3u) == 0) ll_store(d + lane / 4, word, epoch);
+        if (lane == 0) {
+            ll_store(d + 16, __float_as_uint(scale), epoch);
+            ll_store(d + 17, (uint32_t)s, epoch);
+        }
     }
 }
+
+// Words per copy of the replicated hand-off vectors.
+__device__ __forceinline__ size_t oact_words(const MkParams &P) { return (size_t)(P.nq * P.hd / 64) * kActWords; }
+__device__ __forceinline__ size_t gact_words(const MkParams &P) { return (size_t)(P.inter / 64) * kActWords; }
+// The copy this workgroup reads (workgroups are dispatched round-robin over the XCDs).
+__device__ __forceinline__ size_t my_copy(const MkParams &P) { return (size_t)(blockIdx.x % (unsigned)P.rep); }
 
 // RMSNorm + FWHT + int8 of S.hbuf[0..d) into the LDS activation: wave 0 computes inv_rms
 // in row_sumsq_wave order (bit-identical to rmsnorm_act_kernel); then eight lanes per
@@ -206,7 +231,7 @@ __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, 
         const float ss = row_sumsq_wave(S.hbuf, P.d, lane);
         if (lane == 0) S.vec[0] = 1.0f / sqrtf(ss / (float)P.d + P.eps);
     }
-    __syncthreads();
+    lds_barrier();
     const float inv_rms = S.vec[0];
     const uint32_t s8 = lane & 7u;
     const int nc = P.d / 64;
@@ -222,7 +247,7 @@ __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, 
                       (xb.z * inv_rms) * wb.z, (xb.w * inv_rms) * wb.w};
         rotate_quant_slice8(v, P.signs[cc], s8, cc, act, S.xl, S.xsl, S.xsuml);
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Phase kinds of the step's schedule: per layer kQkv, kAttn, kO, kGu, kDown; then kHead.
@@ -233,12 +258,16 @@ enum PhaseKind { kQkv = 0, kAttn = 1, kO = 2, kGu = 3, kDown = 4, kHead = 5 };
 // (HA after the embedding or a down phase, HB after an o phase).
 template <int NTH>
 __device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, const MkLayer &Ly, int kind,
-                                              uint32_t epoch, uint32_t lane, int wave) {
+                                              uint32_t epoch, uint32_t lane, int wave, int t0) {
     if (kind == kO || kind == kDown) {
         const int nch = kind == kO ? P.nq * P.hd / 64 : P.inter / 64;
-        return load_words<NTH>(P, S, kind == kO ? P.OACT : P.GACT, nch * kActWords, epoch, true, nullptr);
+        const unsigned long long *src = kind == kO ? P.OACT + my_copy(P) * oact_words(P)
+                                                   : P.GACT + my_copy(P) * gact_words(P);
+        return load_words<NTH>(P, S, src, nch * kActWords, epoch, true, nullptr, t0);
     }
-    if (!load_words<NTH>(P, S, kind == kGu ? P.HB : P.HA, P.d, epoch, false, S.hbuf)) return false;
+    if (!load_words<NTH>(P, S, (kind == kGu ? P.HB : P.HA) + my_copy(P) * (size_t)P.d, P.d, epoch, false, S.hbuf,
+                         t0))
+        return false;
     build_norm_act<NTH>(P, S, kind == kQkv ? Ly.in_norm : kind == kGu ? Ly.post_norm : P.final_norm, lane, wave);
     return true;
 }
@@ -362,9 +391,9 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
         qf[t] = f;  // qf, kf, vf are contiguous
     }
     if (t == 0) S.flag[0] = 0;
-    __syncthreads();
+    lds_barrier();
     if (!ok) S.flag[0] = 1;
-    __syncthreads();
+    lds_barrier();
     if (S.flag[0]) return false;
     // 2. RoPE (real_llm.rs:9328-9361) on q and k, int8 Hadamard q / k / v
     const size_t slot = ((size_t)layer * nkv + kvh) * P.max_seq + pos;
@@ -399,7 +428,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
             if (lane == 0) P.vs[slot] = vsn;
         }
     }
-    __syncthreads();
+    lds_barrier();
     // 3. scores s_t = float(q8 . k8_t) * ks_t * (qs * scale), t <= pos
     const float qas = scal[0];
     float smax = -INFINITY;
@@ -436,10 +465,10 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     }
     smax = wave_max_f(smax);
     if (lane == 0) red[wave] = smax;
-    __syncthreads();
+    lds_barrier();
     float m = red[0];
     for (int w2 = 1; w2 < (NTH / 64); w2++) m = fmaxf(m, red[w2]);
-    __syncthreads();
+    lds_barrier();
     float psum = 0.0f;
     for (int tt = t; tt < seq; tt += NTH) {
         const float p = expf(sc[tt] - m);
@@ -449,7 +478,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     }
     psum = wave_sum_f(psum);
     if (lane == 0) red[16 + wave] = psum;
-    __syncthreads();
+    lds_barrier();
     // 4. o = sum_t p_t vs_t v_t: thread = (position subset, 4-column group); the subsets
     //    of one wave are added with lane shuffles, then the waves' sums in wave order.
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
@@ -493,7 +522,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
         opart[wave * hd + cg * 4 + 2] = a2;
         opart[wave * hd + cg * 4 + 3] = a3;
     }
-    __syncthreads();
+    lds_barrier();
     if (t < hd) {
         float acc = opart[t];
         for (int w2 = 1; w2 < (NTH / 64); w2++) acc += opart[w2 * hd + t];
@@ -501,13 +530,17 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
         for (int w2 = 1; w2 < (NTH / 64); w2++) L += red[16 + w2];
         qf[t] = acc * (1.0f / L);  // reuse qf for o
     }
-    __syncthreads();
+    lds_barrier();
     // 5. ifwht64 per block, then FWHT with the o_proj chunk index + int8 (real_llm.rs:7060-7084)
     if (wave < nb) {
         const float o = ifwht_lane(qf[wave * 64 + lane], (uint64_t)wave, lane);
         const int c = h * nb + wave;
-        store_act_chunk(fwht_lane(o, (uint64_t)c, lane), lane, P.OACT + (size_t)c * kActWords, ep_out);
+        store_act_chunk(fwht_lane(o, (uint64_t)c, lane), lane, P.OACT + (size_t)c * kActWords, ep_out, P.rep,
+                        oact_words(P));
     }
+    // the next GEMV task stages weights into the LDS bytes that hold qf: every wave must
+    // be past its last read of the attention scratch first
+    lds_barrier();
     return true;
 }
 
@@ -521,6 +554,20 @@ __device__ __forceinline__ int xcd_stripe(const MatDev &M, int t, int nblocks) {
     const int a = t >> 4, s8 = (t >> 3) & 1, j = t & 7;
     return 2 * (8 * a + j) + s8;
 }
+
+#ifdef K2T_MK_TRACE
+// [workgroup][layer (L = head)][phase][start, input, first fragment, wave 0 done, computed, end]:
+// 100 MHz wall clock
+#define MK_TR(l, ph, k)                                                                              \
+    do {                                                                                             \
+        if (P.trace && threadIdx.x == 0)                                                             \
+            P.trace[(((size_t)blockIdx.x * (P.L + 1) + (l)) * 6 + (ph)) * 6 + (k)] = wall_clock64(); \
+    } while (0)
+#else
+#define MK_TR(l, ph, k) \
+    do {                \
+    } while (0)
+#endif
 
 // FMT/HP: the one weight format every projection and the head use (mixed-format models
 // run the one-kernel-per-operation path).
@@ -552,7 +599,7 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
             } else {
                 v = embed_value(P.embed, token, c, lane);
             }
-            ll_store(P.HA + c * 64 + lane, __float_as_uint(v), E(0));
+            for (int r = 0; r < P.rep; r++) ll_store(P.HA + (size_t)r * d + c * 64 + lane, __float_as_uint(v), E(0));
         }
     }
     // phases 1 .. 5L+1: a single GEMV body serves every matrix
@@ -567,8 +614,10 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
         const int off = kind == kHead ? P.head_off : P.layers[l].off[kind];
         const int vb = ((int)blockIdx.x + nwg - off) % nwg;  // this workgroup's rank in the phase
         if (kind == kAttn) {
+            if (vb < P.nq) MK_TR(l, 1, 0);
             for (int h = vb; h < P.nq; h += nwg)
                 if (!attention_head<NTH>(P, P.layers[l], S, l, h, pos, E(ph - 1), E(ph), lane, wave)) return;
+            if (vb < P.nq) MK_TR(l, 1, 5);
             continue;
         }
         const MkLayer &Ly = P.layers[kind == kHead ? 0 : l];
@@ -576,6 +625,7 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
         const int nblocks = M.smode ? M.stripes : M.np + (M.stripes & 1);
         const int groups = kWaves / M.nseg;
         if (vb * groups >= nblocks) continue;  // no task here: go on to the next phase
+        MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 0);
         // ---- GEMV rounds
         const int grp = wave / M.nseg, wseg = wave % M.nseg;
         const int RB = M.smode ? 16 : 32;
@@ -583,20 +633,27 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
         for (int base = vb * groups; base < nblocks; base += nwg * groups) {
             const int rb = xcd_stripe<kWaves>(M, base + grp, nblocks);
             const bool first = base == vb * groups;
-            // The first round requests its first weight fragments, then waits for the
-            // phase input (the weights stream in meanwhile), then computes.
-#define MK_ROUND(F, H)                                                                               \
-    {                                                                                                \
-        GemvWave<F, H> gw(M, rb, rb < nblocks, wseg, lane);                                          \
-        gw.start();                                                                                  \
-        if (first) {                                                                                 \
-            if (!mk_load_input<NTH>(P, S, Ly, kind, E(ph - 1), lane, wave)) return;                        \
-        }                                                                                            \
-        gw.finish(S.xl, S.xsl, S.xsuml, S.part + wave * 32);                                         \
-    }
-            MK_ROUND(FMT, HP)
-#undef MK_ROUND
-            __syncthreads();
+            // The whole of this wave's share (up to kMkFrags fragments) streams into its
+            // LDS slots before the input wait; the compute then reads LDS only.
+            {
+                uint8_t *slots = S.ring + (size_t)wave * kMkFrags * frag_lds_bytes<FMT, HP>();
+                GemvWaveLds<FMT, HP, kMkFrags> gw(M, rb, rb < nblocks, wseg, lane, slots);
+                gw.start();
+                if (first) {
+                    if (!mk_load_input<NTH>(P, S, Ly, kind, E(ph - 1), lane, wave, 0)) return;
+                    MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 1);
+                }
+#ifdef K2T_MK_TRACE
+                unsigned long long *tr = first && P.trace
+                    ? P.trace + (((size_t)blockIdx.x * (P.L + 1) + (kind == kHead ? P.L : l)) * 6 + (kind == kHead ? 0 : kind)) * 6
+                    : nullptr;
+                gw.finish(slots, S.xl, S.xsl, S.xsuml, S.part + wave * 32, tr);
+#else
+                gw.finish(slots, S.xl, S.xsl, S.xsuml, S.part + wave * 32);
+#endif
+            }
+            lds_barrier();
+            if (first) MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 4);
             if (t < groups * RB) {
                 const int g2 = t / RB, rl = t % RB, rb2 = xcd_stripe<kWaves>(M, base + g2, nblocks);
                 if (rb2 < nblocks) {
@@ -615,27 +672,31 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                             S.vec[t] = acc;  // the 4 groups = the 4 pairs of block ic
                         } else {
                             // residual: HB = HA + o (HA from phase ph-3), HA = HB + down (HB from ph-2)
-                            const unsigned long long *res = kind == kO ? P.HA : P.HB;
+                            const unsigned long long *res = (kind == kO ? P.HA : P.HB) + my_copy(P) * (size_t)d;
                             const uint32_t er = kind == kO ? E(ph - 3) : E(ph - 2);
                             uint32_t hv = 0;
                             if (ok && !ll_wait(P, res + row, er, hv)) ok = false;
-                            ll_store((kind == kO ? P.HB : P.HA) + row, __float_as_uint(__uint_as_float(hv) + acc), E(ph));
+                            const uint32_t nv = __float_as_uint(__uint_as_float(hv) + acc);
+                            for (int r = 0; r < P.rep; r++)
+                                ll_store((kind == kO ? P.HB : P.HA) + (size_t)r * d + row, nv, E(ph));
                         }
                     }
                 }
             }
-            __syncthreads();
+            lds_barrier();
             if (kind == kGu) {
                 if (wave == 0) {
                     const int ic = base / 4;
                     const float g = S.vec[lane], u = S.vec[64 + lane];
                     const float v = (g / (1.0f + expf(-g))) * u;  // real_llm.rs:9801-9805
-                    store_act_chunk(fwht_lane(v, (uint64_t)ic, lane), lane, P.GACT + (size_t)ic * kActWords, E(ph));
+                    store_act_chunk(fwht_lane(v, (uint64_t)ic, lane), lane, P.GACT + (size_t)ic * kActWords, E(ph),
+                                    P.rep, gact_words(P));
                 }
-                __syncthreads();
+                lds_barrier();
             }
         }
         if (!ok) return;
+        MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 5);
     }
     // Greedy choice (argmax_scalar, real_llm.rs:9914-9924: largest logit, lowest row on
     // ties) and the position / step advance, inside the launch.  Each workgroup reduces
@@ -747,7 +808,7 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
 
 }  // namespace
 
-MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg, int nwaves) {
+MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg, int nwaves, int min_nseg) {
     const int kWaves = nwaves;
     MatDev d{};
     d.pair = m->pair;
@@ -771,7 +832,7 @@ MatDev mat_dev(const k2t_mat *m, bool pair_mode_nseg4, int max_nseg, int nwaves)
     } else {
         // Stripe mode with one round of the 8 lane groups per wave where K allows.
         d.smode = 1;
-        const int want = (m->nc + 7) / 8;
+        const int want = std::max((m->nc + 7) / 8, min_nseg);
         const int cap = max_nseg > 0 ? std::min(max_nseg, kWaves) : kWaves;
         int nseg = 1;
         while (nseg < want && nseg < cap) nseg *= 2;
@@ -791,8 +852,15 @@ size_t decode_mk_lds_bytes(const k2t_model_config &c) {
     const size_t kmax = std::max(c.hidden, c.intermediate);
     const size_t hd = c.head_dim;
     size_t b = pad16((size_t)c.hidden * 4) + pad16(kmax) + 2 * pad16((kmax / 64) * 4) + kMaxWaves * 32 * 4 + 128 * 4 + 16;
-    b += (3 * hd) * 4 + 3 * 128 + 8 * 4 + 32 * 4 + (size_t)kMaxThreads * 4 * 4 +
-         (size_t)std::min(c.max_seq, kMkMaxContext) * 4;
+    b = (b + 255) / 256 * 256;
+    const size_t att = (3 * hd) * 4 + 3 * 128 + 8 * 4 + 32 * 4 + (size_t)kMaxThreads * 4 * 4 +
+                       (size_t)std::min(c.max_seq, kMkMaxContext) * 4;
+    // the largest weight ring of the three kernel variants (8 waves x NF4 / 4-plane
+    // fragments, 4 waves x mixed-plane fragments)
+    const size_t ring = std::max({(size_t)8 * kMkFrags * frag_lds_bytes<1, 0>(),
+                                  (size_t)8 * kMkFrags * frag_lds_bytes<0, 0>(),
+                                  (size_t)4 * kMkFrags * frag_lds_bytes<0, kHpMixed>()});
+    b += std::max(att, ring);
     return (b + 255) / 256 * 256;
 }
 
@@ -804,7 +872,7 @@ static bool occupancy_ok(size_t lds) {
 }
 
 bool decode_mk_supported(const k2t_model_config &c, int num_cus) {
-    if (decode_mk_lds_bytes(c) > 64 * 1024) return false;
+    if (decode_mk_lds_bytes(c) > kMkMaxLds) return false;
     if (c.hidden > 8192 || c.intermediate > 32768) return false;
     const size_t lds = decode_mk_lds_bytes(c);
     return num_cus > 0 && occupancy_ok<1, 0, 512>(lds) && occupancy_ok<0, 0, 512>(lds) &&

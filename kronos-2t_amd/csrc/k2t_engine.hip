@@ -429,13 +429,35 @@ void forward_mk(k2t_model *m) {
     P.QKV = m->ll_qkv;
     P.OACT = m->ll_oact;
     P.GACT = m->ll_gact;
+    P.rep = kMkRep;
     P.BEST = m->ll_best;
     P.logits = m->logits;
     P.signs = m->ctx->signs;
     P.err = m->err_dev;
     P.spin_limit = 1u << 22;
+#ifdef K2T_MK_TRACE
+    // measurement build: eager steps dump the phase trace to $K2T_MK_TRACE
+    static unsigned long long *trace = nullptr;
+    const size_t ntr = (size_t)m->ctx->num_cus * (c.n_layers + 1) * 6 * 6;
+    if (getenv("K2T_MK_TRACE") && !m->use_graph) {
+        if (!trace) hip_check(hipMalloc(&trace, ntr * 8), "trace");
+        hip_check(hipMemset(trace, 0, ntr * 8), "trace clear");
+        P.trace = trace;
+    }
+#endif
     // the kernel also writes the greedy next token and advances the position and step
     launch_decode_mk(m->stream, P, fmt, hp, m->ctx->num_cus, m->mk_lds);
+#ifdef K2T_MK_TRACE
+    if (P.trace) {
+        std::vector<unsigned long long> h(ntr);
+        hip_check(hipStreamSynchronize(m->stream), "sync");
+        hip_check(hipMemcpy(h.data(), trace, ntr * 8, hipMemcpyDeviceToHost), "trace copy");
+        if (FILE *f = fopen(getenv("K2T_MK_TRACE"), "wb")) {
+            fwrite(h.data(), 8, ntr, f);
+            fclose(f);
+        }
+    }
+#endif
 }
 
 // Raises the persistent kernel's dependency-timeout flag as an error (after a sync).
@@ -546,15 +568,16 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             m->err_dev = (int *)m->step_dev + 1;
             const uint32_t one[4] = {1u, 0u, 0u, 0u};
             hip_check(hipMemcpy(m->step_dev, one, sizeof(one), hipMemcpyHostToDevice), "step init");
-            const size_t words = 2 * (size_t)c.hidden + qkv_w + (size_t)(c.n_heads * c.head_dim / 64) * 18 +
-                                 (size_t)(c.intermediate / 64) * 18 + 2 * (size_t)ctx->num_cus;
+            // HA, HB, OACT and GACT in kMkRep copies (one per XCD), QKV and BEST once
+            const size_t oact = (size_t)(c.n_heads * c.head_dim / 64) * 18, gact = (size_t)(c.intermediate / 64) * 18;
+            const size_t words = kMkRep * (2 * (size_t)c.hidden + oact + gact) + qkv_w + 2 * (size_t)ctx->num_cus;
             m->ll_ha = (unsigned long long *)dalloc(m, words * 8);
             hip_check(hipMemset(m->ll_ha, 0, words * 8), "hand-off clear");
-            m->ll_hb = m->ll_ha + c.hidden;
-            m->ll_qkv = m->ll_hb + c.hidden;
-            m->ll_oact = m->ll_qkv + qkv_w;
-            m->ll_gact = m->ll_oact + (size_t)(c.n_heads * c.head_dim / 64) * 18;
-            m->ll_best = m->ll_gact + (size_t)(c.intermediate / 64) * 18;
+            m->ll_hb = m->ll_ha + kMkRep * (size_t)c.hidden;
+            m->ll_oact = m->ll_hb + kMkRep * (size_t)c.hidden;
+            m->ll_gact = m->ll_oact + kMkRep * oact;
+            m->ll_qkv = m->ll_gact + kMkRep * gact;
+            m->ll_best = m->ll_qkv + qkv_w;
             m->mk_layers = (MkLayer *)dalloc(m, (size_t)c.n_layers * sizeof(MkLayer));
         } catch (...) {
             k2t_model_destroy(m);

@@ -239,4 +239,214 @@ struct GemvWave {
     }
 };
 
+
+// ---------------------------------------------------------------------------------------
+// LDS-staged weight stream.  The weight fragments of a wave's share of a row block are
+// copied straight into LDS by the memory pipeline (global_load_lds_dwordx4: lane L's 16
+// bytes land at M0 + 16 L) instead of into registers, so a wave can have its whole share
+// of a GEMV task in flight before its input exists, without holding registers for it.
+//
+// These loads are issued from inline assembly: the compiler does not track them, and so
+// never adds the conservative "all vector memory done" wait it inserts before every LDS
+// read that follows an LDS-DMA load it knows of.  Their completion is awaited here with
+// explicit vmcnt waits.  Vector memory operations of one wave complete in issue order,
+// so a compiler-inserted wait for a later load only waits longer, never too little.
+// M0 is set inside each statement; no compiler-generated code of these kernels uses M0
+// (the build checks the generated assembly for it).
+
+// Number of 1 KB hi-plane pieces a fragment holds (bit planes with hi planes only).
+template <int FMT, int HP>
+__host__ __device__ constexpr int frag_hi_pieces() {
+    return FMT != 0 ? 0 : (HP == 0 ? 0 : (HP == 2 ? 4 : 2));
+}
+// LDS bytes of one staged fragment: 4 nibble pieces and the hi pieces (1 KB each: 16
+// bytes per lane), then the 4-byte BF16 scale pair of every lane.
+template <int FMT, int HP>
+__host__ __device__ constexpr int frag_lds_bytes() {
+    return (4 + frag_hi_pieces<FMT, HP>()) * 1024 + 256;
+}
+// Load instructions per staged fragment.
+template <int FMT, int HP>
+__host__ __device__ constexpr int frag_loads() {
+    return 4 + frag_hi_pieces<FMT, HP>() + 1;
+}
+
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// 16 bytes per lane from p (per-lane address) to LDS [m0 + 16 * lane].
+__device__ __forceinline__ void lds_dma16(const void *p, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(p), "s"(m0) : "memory");
+}
+// 4 bytes per lane from p to LDS [m0 + 4 * lane].
+__device__ __forceinline__ void lds_dma4(const void *p, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(p), "s"(m0) : "memory");
+}
+
+// Waits until at most N vector memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// GemvWave with its fragments staged in LDS: `slots` points at this wave's F fragment
+// slots.  start() requests fragments 0 .. F-1 (the whole share when it has at most F);
+// finish() computes fragment i from slot i % F and then requests fragment i + F into it,
+// so up to F fragments are in flight.  Lane groups past the wave's chunk range load a
+// valid in-range chunk whose bytes are never used: every fragment is exactly frag_loads()
+// instructions under wave-uniform control flow, which keeps the vmcnt arithmetic exact.
+template <int FMT, int HP, int F>
+struct GemvWaveLds {
+    static constexpr int NH = frag_hi_pieces<FMT, HP>();
+    static constexpr int FB = frag_lds_bytes<FMT, HP>();
+    static constexpr int L = frag_loads<FMT, HP>();
+    static_assert(F >= 1 && F <= 4 && (F - 1) * L < 64, "fragments in flight: 1 to 4 within vmcnt's range");
+    const MatDev &M;
+    Geo o;
+    int cw0, cw1, iters, G, q;
+    uint32_t lane, half, slot0;
+    bool active;
+
+    __device__ __forceinline__ GemvWaveLds(const MatDev &M_, int rb, bool active_, int wseg, uint32_t lane_,
+                                           uint8_t *slots)
+        : M(M_), lane(lane_), half(lane_ & 1u), active(active_) {
+        o = make_geo<FMT, HP>(M, active ? rb : 0, lane);
+        G = M.smode ? 8 : 4;
+        q = M.smode ? (int)(lane >> 3) : (int)(lane >> 4);
+        cw0 = wseg * M.cps;
+        cw1 = active ? min(M.nc, cw0 + M.cps) : cw0;
+        iters = cw1 > cw0 ? (cw1 - cw0 + G - 1) / G : 0;
+        slot0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(slots));
+    }
+    __device__ __forceinline__ int chunk_of(int i) const { return cw0 + i * G + q; }
+    __device__ __forceinline__ bool valid(int i) const { return i < iters && chunk_of(i) < cw1; }
+
+    // Issues fragment i (a clamped in-range chunk when i is past the share).
+    __device__ __forceinline__ void issue(int i) {
+        const int c = cw1 > cw0 ? min(chunk_of(i), cw1 - 1) : 0;
+        const uint32_t hp = (uint32_t)hp_of<HP>(M);
+        const uint8_t *rec, *scp;
+        if constexpr (FMT == 0) {
+            const uint32_t PREC = 1024 + 256 * hp + 64, TREC = 512 + 128 * hp + 32;
+            rec = o.mbase + (size_t)c * (o.is_tail ? TREC : PREC);
+            scp = rec;
+        } else {
+            const int sg = c / M.sgc, cst = sg * M.sgc, sb = c - cst;
+            const uint8_t *gb =
+                o.mbase + (o.is_tail ? (size_t)sg * 32 + (size_t)cst * 512 : (size_t)sg * 64 + (size_t)cst * 1024);
+            rec = gb + (size_t)sb * (o.is_tail ? 512 : 1024);
+            scp = gb;
+        }
+        const uint32_t base = slot0 + (uint32_t)(i % F) * (uint32_t)FB;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) lds_dma16(rec + o.nib_off + kk * 128, base + kk * 1024);
+        if constexpr (NH == 4) {
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) lds_dma16(rec + o.hi_off + kk * 64, base + (4 + kk) * 1024);
+        } else if constexpr (NH == 2) {
+            // a 4-plane matrix under the mixed variant has no hi bytes: load the nibble
+            // bytes again (in range; chunk_dots ignores them for hp 0)
+            const uint8_t *h = hp != 0 ? rec + o.hi_off : rec + o.nib_off;
+            lds_dma16(h, base + 4 * 1024);
+            lds_dma16(hp != 0 ? h + 64 : h, base + 5 * 1024);
+        }
+        lds_dma4(scp + o.sc_off, base + (4 + NH) * 1024);
+    }
+
+    __device__ __forceinline__ void start() {
+#pragma unroll
+        for (int i = 0; i < F; i++)
+            if (i < iters) issue(i);  // wave-uniform
+    }
+
+    // Waits until fragment i has landed while `after` later fragments may stay in flight.
+    __device__ __forceinline__ static void wait_frag(int after) {
+        if constexpr (F >= 4) {
+            if (after >= 3) {
+                wait_vmcnt<3 * L>();
+                return;
+            }
+        }
+        if constexpr (F >= 3) {
+            if (after == 2) {
+                wait_vmcnt<2 * L>();
+                return;
+            }
+        }
+        if constexpr (F >= 2) {
+            if (after == 1) {
+                wait_vmcnt<L>();
+                return;
+            }
+        }
+        wait_vmcnt<0>();
+    }
+
+    __device__ __forceinline__ WFrag<HP> read(int i, const uint8_t *slots) const {
+        const uint8_t *b = slots + (size_t)(i % F) * FB;
+        WFrag<HP> fr;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) fr.w[kk] = *reinterpret_cast<const uint4 *>(b + kk * 1024 + lane * 16);
+        if constexpr (NH > 0) {
+#pragma unroll
+            for (int j = 0; j < NH; j++) fr.h[j] = *reinterpret_cast<const uint4 *>(b + (4 + j) * 1024 + lane * 16);
+            if constexpr (HP == kHpMixed) {
+                if (M.hp == 0) fr.h[0] = fr.h[1] = make_uint4(0, 0, 0, 0);
+            }
+        } else {
+            fr.h[0] = make_uint4(0, 0, 0, 0);
+        }
+        fr.ws = *reinterpret_cast<const uint32_t *>(b + (4 + NH) * 1024 + lane * 4);
+        return fr;
+    }
+
+    __device__ __forceinline__ void finish(const uint8_t *slots, const int8_t *xl, const float *xsl,
+                                           const int32_t *xsuml, float *part, unsigned long long *trace = nullptr) {
+        float f0 = 0.0f, f1 = 0.0f;
+        for (int i = 0; i < iters; i++) {
+            // fragments i .. min(i + F, iters) - 1 were requested; wait for i
+            wait_frag(min(F, iters - i) - 1);
+            if (trace && i == 0 && threadIdx.x == 0) trace[2] = wall_clock64();
+            const WFrag<HP> fr = read(i, slots);
+            if (valid(i)) process(fr, chunk_of(i), xl, xsl, xsuml, f0, f1);
+            if (i + F < iters) {  // wave-uniform
+                // the slot's LDS reads must complete before the next fragment overwrites it
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                issue(i + F);
+            }
+        }
+        if (M.smode) {
+            f0 += __int_as_float(dpp_ror8(__float_as_int(f0)));
+            f1 += __int_as_float(dpp_ror8(__float_as_int(f1)));
+        }
+        f0 += __shfl_xor(f0, 16, kWave);
+        f0 += __shfl_xor(f0, 32, kWave);
+        f1 += __shfl_xor(f1, 16, kWave);
+        f1 += __shfl_xor(f1, 32, kWave);
+        const uint32_t rloc = (M.smode ? 0u : ((lane >> 3) & 1u) * 16u) + 4u * ((lane >> 1) & 3u) + 2u * half;
+        if (M.smode ? lane < 8 : lane < 16) {
+            part[rloc] = f0;
+            part[rloc + 1] = f1;
+        }
+        if (trace && threadIdx.x == 0) trace[3] = wall_clock64();
+    }
+
+    __device__ __forceinline__ void process(const WFrag<HP> &fr, int c, const int8_t *xl, const float *xsl,
+                                            const int32_t *xsuml, float &f0, float &f1) const {
+        uint2 x[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) x[kk] = *reinterpret_cast<const uint2 *>(xl + c * 64 + kk * 16 + half * 8);
+        const float sx = xsl[c];
+        const int xsum = FMT == 0 ? xsuml[c] : 0;
+        int r0, r1;
+        chunk_dots<FMT, HP>(M, fr, half, x, xsum, r0, r1);
+        const float n0 = fmaf((float)r0 * sx, bf16_lo(fr.ws), f0);
+        const float n1 = fmaf((float)r1 * sx, bf16_hi(fr.ws), f1);
+        f0 = sx != 0.0f ? n0 : f0;
+        f1 = sx != 0.0f ? n1 : f1;
+    }
+};
+
 }  // namespace k2t

@@ -14,7 +14,8 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libk2t_hip.so")
+# K2T_LIB_PATH selects another build of the library (a measurement build, for example)
+LIB_PATH = os.environ.get("K2T_LIB_PATH") or os.path.join(_HERE, "libk2t_hip.so")
 _lib = None
 _shutting_down = False
 
