@@ -335,6 +335,18 @@ __device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t
 
 // Attention of q head h for the current position (causal_gqa_group_q8,
 // real_llm.rs:8471-8594), ending with the o_proj activation chunks of this head.
+#ifdef K2T_MK_TRACE
+#define ATR(k)                                                                                      \
+    do {                                                                                            \
+        if (P.trace && threadIdx.x == 0)                                                           \
+            P.trace[(((size_t)blockIdx.x * (P.L + 1) + layer) * 6 + 1) * 6 + (k)] = wall_clock64(); \
+    } while (0)
+#else
+#define ATR(k) \
+    do {       \
+    } while (0)
+#endif
+
 template <int NTH>
 __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &S, int layer, int h, int pos,
                                uint32_t ep_in, uint32_t ep_out, uint32_t lane, int wave) {
@@ -394,6 +406,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     lds_barrier();
     if (!ok) S.flag[0] = 1;
     lds_barrier();
+    ATR(1);
     if (S.flag[0]) return false;
     // 2. RoPE (real_llm.rs:9328-9361) on q and k, int8 Hadamard q / k / v
     const size_t slot = ((size_t)layer * nkv + kvh) * P.max_seq + pos;
@@ -429,6 +442,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
         }
     }
     lds_barrier();
+    ATR(2);
     // 3. scores s_t = float(q8 . k8_t) * ks_t * (qs * scale), t <= pos
     const float qas = scal[0];
     float smax = -INFINITY;
@@ -469,6 +483,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     float m = red[0];
     for (int w2 = 1; w2 < (NTH / 64); w2++) m = fmaxf(m, red[w2]);
     lds_barrier();
+    ATR(3);
     float psum = 0.0f;
     for (int tt = t; tt < seq; tt += NTH) {
         const float p = expf(sc[tt] - m);
@@ -523,6 +538,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
         opart[wave * hd + cg * 4 + 3] = a3;
     }
     lds_barrier();
+    ATR(4);
     if (t < hd) {
         float acc = opart[t];
         for (int w2 = 1; w2 < (NTH / 64); w2++) acc += opart[w2 * hd + t];
