@@ -284,6 +284,30 @@ def copy_probe(torch, mib):
     torch.cuda.synchronize()
 
 
+def read_ceiling(ctx, torch, nbytes, steps=60):
+    """Practical single-launch HBM read rate at this byte count: k2t_stream_read_probe over
+    nbytes, rotated over enough buffers to miss the 256 MB Infinity Cache, timed back to
+    back like the GEMV cases.  Returns (GB/s, us)."""
+    nb = (nbytes + 15) // 16 * 16
+    ncopy = max(2, int(np.ceil(320e6 / nb)))
+    bufs = [torch.ones(nb // 4, dtype=torch.float32, device="cuda") for _ in range(ncopy)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    for i in range(ncopy):
+        ctx.stream_read_probe(bufs[i], nb, sink)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _busy_wait(torch, stream, 2e-3 + steps * 60e-6)
+    a.record(stream)
+    for i in range(steps):
+        ctx.stream_read_probe(bufs[i % ncopy], nb, sink)
+    b.record(stream)
+    torch.cuda.synchronize()
+    t = a.elapsed_time(b) * 1e-3 / steps
+    del bufs
+    return nb / t / 1e9, t * 1e6
+
+
 def copy_ceiling(torch, nbytes, steps=60):
     """Practical HBM rate of one launch moving this many bytes: device-to-device copies of
     nbytes/2 read + nbytes/2 written, rotated over enough buffers to miss the 256 MB
@@ -308,10 +332,22 @@ def copy_ceiling(torch, nbytes, steps=60):
     return 8 * n / t / 1e9, t * 1e6
 
 
-def cpu_decode_baseline(cfg, host, seconds=10.0, max_tokens=32):
+def cpu_model():
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_decode_baseline(cfg, host, context, seconds=10.0, max_tokens=32):
     """The reference's portable CPU decode (dequantize + fp32 dot GEMVs over stripe ranges,
     real_llm.rs:829-836 / simd_lut.rs:5719-5748; scalar q8 attention) restated in the
-    oracle, on this machine's host cores, for `ntok` tokens from an empty context."""
+    oracle, on this machine's host cores: tokens attending `context`+ positions (the KV
+    cache is seeded, as the GPU run's cache holds its prefill), at all host threads (up to
+    16, the box's CPU share) for about `seconds`, and one token on one thread."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from model_oracle import Matrix, OracleModel
     threads = min(16, os.cpu_count() or 1)
@@ -321,18 +357,50 @@ def cpu_decode_baseline(cfg, host, seconds=10.0, max_tokens=32):
     for i in range(cfg["n_layers"]):
         q, o, gu, dn = conv[4 * i:4 * i + 4]
         layers.append({"qkv": q, "o": o, "gu": gu, "down": dn, "in_norm": ones, "post_norm": ones, "bias": None})
-    om = OracleModel(dict(cfg, max_seq=max_tokens + 1), layers, conv[-1], ones, gemv_threads=threads)
-    om.forward_token(1)  # warm
-    om.pos = 0
-    t0 = time.perf_counter()
-    ntok = 0
-    while ntok < max_tokens and (ntok < 2 or time.perf_counter() - t0 < seconds):
-        om.forward_token(3 + ntok)
-        ntok += 1
-    dt = (time.perf_counter() - t0) / ntok
+
+    def run(nthreads, budget, cap):
+        om = OracleModel(dict(cfg, max_seq=context + cap + 2), layers, conv[-1], ones, gemv_threads=nthreads)
+        om.seed_kv(context, seed=1)
+        t0 = time.perf_counter()
+        ntok = 0
+        while ntok < cap and (ntok < 1 or time.perf_counter() - t0 < budget):
+            om.forward_token(3 + ntok)
+            ntok += 1
+        return ntok, (time.perf_counter() - t0) / ntok
+
+    run(threads, 0.0, 1)  # warm the page cache and thread pool
+    ntok, dt = run(threads, seconds, max_tokens)
+    _, dt1 = run(1, 0.0, 1)
     return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{ntok} decode tokens of the 1.7B nf4g128 model from an empty context on the portable "
-                      f"path (dequantize + fp32 dot, simd_lut.rs:5719-5748) restated in C, {threads} host threads"}
+            "cpu_model": cpu_model(), "one_thread": {"value": round(1.0 / dt1, 4), "unit": "tok/s", "cores": 1},
+            "sample": f"{ntok} decode tokens of the 1.7B nf4g128 model at context {context}-{context + ntok} (KV "
+                      f"cache seeded) on the portable path (dequantize + fp32 dot, simd_lut.rs:5719-5748) restated "
+                      f"in C, {threads} host threads; one_thread: 1 token on 1 thread"}
+
+
+def cpu_gemv_baseline(cases):
+    """The portable CPU GEMV (dequantize + fp32 dot, simd_lut.rs:3558-3581 / 5719-5748) on
+    the sweep's own matrices and activations, at all host threads (up to 16) and at 1:
+    GB/s of the same algorithmic bytes as the GPU line."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from model_oracle import Matrix
+    threads = min(16, os.cpu_count() or 1)
+    out = {}
+    for key, c in cases.items():
+        fmt = "n4" if c["fmt"] in ("b4", "b5", "b6") else "nf4"
+        hp = int(c["fmt"][1]) - 4 if fmt == "n4" else 0
+        m = Matrix(fmt, c["rows"], c["cols"], c["pair"], c["tail"], hp=hp, cb=c["cb"], sgc=2)
+        res = {}
+        for nt in (threads, 1):
+            m.gemv_portable(c["xq"], c["xs"], nt)  # warm
+            reps, t0 = 0, time.perf_counter()
+            while reps < 3 or (time.perf_counter() - t0 < 0.5 and reps < 200):
+                m.gemv_portable(c["xq"], c["xs"], nt)
+                reps += 1
+            dt = (time.perf_counter() - t0) / reps
+            res[f"{nt}t"] = {"us": round(dt * 1e6, 1), "GB_s": round(c["bytes"] / dt / 1e9, 3)}
+        out[key] = res
+    return {"threads": threads, "cpu_model": cpu_model(), "kind": "port", "cases": out}
 
 
 def main():
@@ -373,6 +441,7 @@ def main():
              ("nf3g128_14336x4096", "nf3", 14336, 4096), ("nf3g128_4096x14336", "nf3", 4096, 14336)]
     only = [s for s in args.only.split(",") if s]
     results = {}
+    cpu_cases = {}  # config 1 and config 4 matrices kept on the host for the CPU GEMV leg
     dom = None
     for name, fmt, r, c in specs:
         if (only and name not in only) or args.decode_only:
@@ -387,18 +456,26 @@ def main():
             log(f"# {key}: {mean_s * 1e6:.2f} us  {gbs:.1f} GB/s  {100 * gbs / HBM_PEAK_GBS:.1f}% of peak")
             if ntok == 1 and fmt == "nf4" and (dom is None or results[key]["GB_s"] < results[dom]["GB_s"]):
                 dom = key
+            if ntok == 1 and key in ("b4_1536x576_b1", "nf4g128_4096x14336_b1", "b6_4096x14336_b1"):
+                cpu_cases[key] = {"fmt": fmt, "rows": r, "cols": c, "pair": case.pair_host, "tail": case.tail_host,
+                                  "cb": case.cb, "xq": case.q[0].cpu().numpy(), "xs": case.s[0].cpu().numpy(),
+                                  "bytes": case.bytes}
             del case
-    ceiling = None
+    ceiling = rceiling = None
     if dom is not None:
         cg, cu = copy_ceiling(torch, results[dom]["bytes"])
         ceiling = {"GB_s": round(cg, 1), "us": round(cu, 3), "frac": round(cg / HBM_PEAK_GBS, 4)}
         log(f"# copy ceiling at {results[dom]['bytes']} B per launch: {cu:.2f} us  {cg:.1f} GB/s "
             f"{100 * cg / HBM_PEAK_GBS:.1f}% of peak")
+        rg, ru = read_ceiling(ctx, torch, results[dom]["bytes"])
+        rceiling = {"GB_s": round(rg, 1), "us": round(ru, 3), "frac": round(rg / HBM_PEAK_GBS, 4)}
+        log(f"# read ceiling at {results[dom]['bytes']} B per launch: {ru:.2f} us  {rg:.1f} GB/s "
+            f"{100 * rg / HBM_PEAK_GBS:.1f}% of peak")
     line = {"metric": "quant GEMV HBM GB/s (% peak) + decode tok/s, 1.7B-shape nf4g128, 1 MI355X"}
     if args.copy_probe:
         copy_probe(torch, args.copy_probe)
     if args.only:
-        line.update({"config": {"cases": results, "copy_ceiling": ceiling}})
+        line.update({"config": {"cases": results, "copy_ceiling": ceiling, "read_ceiling": rceiling}})
         print(json.dumps(line))
         return
     torch.cuda.empty_cache()
@@ -406,7 +483,12 @@ def main():
     # ---- config 3: 1.7B nf4g128 prefill 256 + greedy decode
     m17, mats17, host17, r17 = decode_bench(ctx, torch, "1.7B nf4g128", k2t.SMOLLM2_1_7B, "nf4", 256, args.steps,
                                             args.warmup, log)
-    cpu = None if args.no_cpu_baseline else cpu_decode_baseline(k2t.SMOLLM2_1_7B, host17)
+    cpu = None if args.no_cpu_baseline else cpu_decode_baseline(k2t.SMOLLM2_1_7B, host17, 256 + args.warmup)
+    if cpu is not None:
+        cpu["gemv"] = cpu_gemv_baseline(cpu_cases)
+        log(f"# CPU ({cpu['cpu_model']}): decode {cpu['value']} tok/s on {cpu['cores']} threads, "
+            f"{cpu['one_thread']['value']} tok/s on 1; GEMV " +
+            ", ".join(f"{k} {v[str(cpu['cores']) + 't']['GB_s']} GB/s" for k, v in cpu["gemv"]["cases"].items()))
     m17.close()
     for m in mats17:
         m.close()
@@ -444,7 +526,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": f"gemv_kernel ({dom})", "achieved": dr["GB_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dr["GB_s"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom),
                      "algorithmic_bytes_per_launch": dr["bytes"], "avg_launch_us": dr["us"],
-                     "copy_ceiling_same_bytes": ceiling},
+                     "copy_ceiling_same_bytes": ceiling, "read_ceiling_same_bytes": rceiling},
         "cpu_baseline": cpu,
     })
     print(json.dumps(line))

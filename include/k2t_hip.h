@@ -158,6 +158,12 @@ int32_t k2t_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq, const float
 int32_t k2t_gemv_chunk_dots(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq,
                             const int32_t *d_xsum, int32_t *d_dots);
 
+/* Measurement: one streaming read of `bytes` (16-byte aligned) from d_src, asynchronous on
+ * the context's stream; d_sink receives a word only if the data's XOR equals a marker.
+ * No reference counterpart: it gives the single-launch HBM read ceiling that the GEMV's
+ * bandwidth is read against. */
+int32_t k2t_stream_read_probe(k2t_ctx *ctx, const void *d_src, size_t bytes, uint32_t *d_sink);
+
 /* ---- offline weight compiler (host memory, multi-threaded) ------------- */
 
 /* Byte lengths of the pair / tail streams: fmt 1 = bit planes (planes 4..6),

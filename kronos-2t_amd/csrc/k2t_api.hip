@@ -420,6 +420,15 @@ int32_t k2t_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq, const float
     });
 }
 
+int32_t k2t_stream_read_probe(k2t_ctx *ctx, const void *d_src, size_t bytes, uint32_t *d_sink) {
+    return guarded([&] {
+        arg_check(ctx && d_src && d_sink, "NULL argument");
+        arg_check(bytes % 16 == 0 && ((uintptr_t)d_src & 15) == 0, "bytes and d_src must be 16-byte aligned");
+        hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+        launch_stream_read(ctx->stream, d_src, bytes, d_sink);
+    });
+}
+
 int32_t k2t_gemv_chunk_dots(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq, const int32_t *d_xsum,
                             int32_t *d_dots) {
     return guarded([&] {

@@ -60,6 +60,7 @@ struct GemvPlan {
     int rb_lo, rb_hi;  // row blocks: pairs (then the odd tail stripe), or stripes
     int nseg, cps;     // waves per workgroup (K segments) and chunks per wave
 };
+void launch_stream_read(hipStream_t st, const void *src, size_t bytes, uint32_t *sink);
 GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1);
 
 void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,

@@ -105,6 +105,7 @@ SIGNATURES = {
     "k2t_model_kv_bits": (I32, [VP, C.POINTER(I32)]),
     "k2t_kv_store": (I32, [VP, I32, VP, I32, I32, VP, VP]),
     "k2t_attn_decode": (I32, [VP, I32, VP, I32, I32, I32, VP, VP, VP, VP, I32, I32, I32, I32, C.c_float, VP]),
+    "k2t_stream_read_probe": (I32, [VP, VP, SZ, VP]),
     "k2t_attn_decode_noalloc": (I32, [VP, I32, VP, I32, I32, I32, VP, VP, VP, VP, I32, I32, I32, I32, C.c_float,
                                       VP]),
 }
@@ -272,6 +273,11 @@ class Ctx:
         """k2t_attn_decode: one token's attention over a KV cache in k2t_kv_store's layout."""
         check(lib().k2t_attn_decode(self.h, bits, _p(q), n_heads, n_kv_heads, head_dim, _p(kq), _p(ks), _p(vq),
                                     _p(vs), cap, seq, window, sink_tokens, float(attn_scale), _p(out)))
+
+    def stream_read_probe(self, src, nbytes, sink):
+        """k2t_stream_read_probe: one streaming read of nbytes of a device buffer (HBM
+        read-ceiling measurement)."""
+        check(lib().k2t_stream_read_probe(self.h, _p(src), nbytes, _p(sink)))
 
     def attn_decode_noalloc(self, bits, q, n_heads, n_kv_heads, head_dim, kq, ks, vq, vs, cap, seq, attn_scale,
                             out, window=0, sink_tokens=0):

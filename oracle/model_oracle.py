@@ -144,6 +144,19 @@ class OracleModel:
         self.vs = np.zeros((L, nkv, cap), np.float32)
         self.pos = 0
 
+    def seed_kv(self, n_pos, seed=0):
+        """Fills cache positions 0 .. n_pos-1 with seeded random int8 K/V and scales and
+        sets the position, so that a timed step attends n_pos + 1 positions without a
+        prefill (the values only matter for timing)."""
+        rng = np.random.default_rng(seed)
+        L, nkv = self.kq.shape[0], self.kq.shape[1]
+        hd = self.kq.shape[3]
+        self.kq[:, :, :n_pos] = rng.integers(-127, 128, (L, nkv, n_pos, hd), dtype=np.int8)
+        self.vq[:, :, :n_pos] = rng.integers(-127, 128, (L, nkv, n_pos, hd), dtype=np.int8)
+        self.ks[:, :, :n_pos] = rng.uniform(0.005, 0.05, (L, nkv, n_pos)).astype(np.float32)
+        self.vs[:, :, :n_pos] = rng.uniform(0.005, 0.05, (L, nkv, n_pos)).astype(np.float32)
+        self.pos = n_pos
+
     def _gemv(self, m, xq, xs, xsum):
         if self.gemv_threads:
             return m.gemv_portable(xq, xs, self.gemv_threads)
