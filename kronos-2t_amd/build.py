@@ -92,9 +92,8 @@ def build(verbose=False, out=None, defines=()):
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         res = list(ex.map(lambda src: _compile(src, objdir, defines), srcs))
     objs = [o for o, _ in res]
-    with cf.ThreadPoolExecutor(max_workers=4) as ex:
-        list(ex.map(check_m0, [src for src in srcs if "global_load_lds" in open(src).read() or
-                               "k2t_gemv_core.h" in open(src).read()]))
+    with cf.ThreadPoolExecutor(max_workers=8) as ex:
+        list(ex.map(check_m0, [src for src in srcs if src.endswith(".hip")]))
     usage = [u for _, us in res for u in us]
     with open(os.path.join(objdir, "resource_usage.txt"), "w") as f:
         for name, u in usage:

@@ -17,6 +17,31 @@ __device__ __forceinline__ uint4 load_stream16(const void *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Direct-to-LDS loads (global_load_lds): lane L's bytes land at M0 + size * L.  Issued
+// from inline assembly, so the compiler neither tracks them nor inserts its conservative
+// "all vector memory done" wait before later LDS reads; callers order them through the
+// in-issue-order completion of a wave's vector memory operations.  M0 is set inside each
+// statement: no compiler-generated code of these kernels uses M0 (the build checks).
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// 16 bytes per lane from p (per-lane address) to LDS [m0 + 16 * lane].
+__device__ __forceinline__ void lds_dma16(const void *p, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(p), "s"(m0) : "memory");
+}
+// 4 bytes per lane from p to LDS [m0 + 4 * lane].
+__device__ __forceinline__ void lds_dma4(const void *p, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(p), "s"(m0) : "memory");
+}
+
+// Waits until at most N vector memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Sign of element `i` of Hadamard block `block` (hadamard.rs:29-44): SplitMix64 state
 // seed + block*0xBF58.. advanced i+1 times, finalized, low bit.  Each lane computes its
 // own element, so no table is needed.

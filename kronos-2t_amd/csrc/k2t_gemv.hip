@@ -531,6 +531,50 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             if (valid(1)) fetch(fb, chunk_of(1));
             xb.finish(xl, xsl, xsuml);
             __builtin_amdgcn_wave_barrier();
+        } else if constexpr (XS == 5) {
+            // As XS 3, but the wave's activation codes, scales and sums are copied into LDS
+            // by direct-to-LDS loads issued before the weight loads, and every weight fetch
+            // is issued for all lanes (lane groups past the range re-read an in-range
+            // chunk), so the compiler can count them: chunk i is computed as soon as its
+            // own loads (and everything issued before them, the activation included) have
+            // landed, while chunk i + 1 is still in flight.
+            const int n = cw1 - cw0;
+            if (n > 0) {
+                const int n_u4 = n * 4;
+                const uint4 *src = reinterpret_cast<const uint4 *>(P.xq + (size_t)tok0 * P.K + (size_t)cw0 * 64);
+                const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(xl + (size_t)cw0 * 64));
+                if ((int)lane < n_u4) lds_dma16(src + lane, m0);
+                if ((int)lane + 64 < n_u4) lds_dma16(src + lane + 64, m0 + 1024);
+                if ((int)lane < n) {
+                    lds_dma4(P.xs + (size_t)tok0 * P.nc + cw0 + lane,
+                             (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(xsl + cw0)));
+                    if constexpr (FMT == 0)
+                        lds_dma4(P.xsum + (size_t)tok0 * P.nc + cw0 + lane,
+                                 (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(xsuml + cw0)));
+                }
+            }
+            // The same count of loads is outstanding at every loop entry (fa, fb), so the
+            // compiler's waits are exact; at most one fetch of a wave is wasted (iters odd).
+            auto fetchc = [&](Frag<HP, NT> &fr, int i) { fetch(fr, max(cw0, min(chunk_of(i), cw1 - 1))); };
+            if (iters > 0) {
+                fetchc(fa, 0);
+                fetchc(fb, 1);
+                // The activation copies were issued before these two fetches: once at most
+                // their loads are outstanding, the activation is in LDS.  (The compiler does
+                // not know the copies write LDS and could move the activation reads up to
+                // its own, later, wait for fa.)
+                constexpr int kFetchLoads = (FMT == 2 ? 3 : 4) + (FMT == 0 ? (HP == 0 ? 0 : HP == 1 ? 2 : 4) : 0) + 1;
+                wait_vmcnt<2 * kFetchLoads>();
+                int i = 0;
+                for (; i + 2 < iters; i += 2) {
+                    if (valid(i)) process(fa, chunk_of(i));
+                    fetchc(fa, i + 2);
+                    if (valid(i + 1)) process(fb, chunk_of(i + 1));
+                    fetchc(fb, i + 3);
+                }
+                if (valid(i)) process(fa, chunk_of(i));
+                if (valid(i + 1)) process(fb, chunk_of(i + 1));
+            }
         } else if constexpr (XS != 0) {
             // Source loads first, then the first weight loads; the wave builds its
             // activation while the weights are in flight.
@@ -543,7 +587,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         } else {
             if (valid(0)) fetch(fa, chunk_of(0));
         }
-        for (int i = 0; i < iters; i += 2) {
+        for (int i = 0; XS != 5 && i < iters; i += 2) {
             if (XS == 0 && valid(i + 1)) fetch(fb, chunk_of(i + 1));
             if (valid(i)) process(fa, chunk_of(i));
             if (valid(i + 2)) fetch(fa, chunk_of(i + 2));
@@ -680,6 +724,10 @@ static void launch_nt(int nt, int xs, dim3 grid, dim3 block, size_t lds, hipStre
         hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, false, K2T_XS_STAGED>), grid, block, lds, st, P);
         return;
     }
+    if (xs == K2T_XS_STAGED_DMA) {
+        hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, false, K2T_XS_STAGED_DMA>), grid, block, lds, st, P);
+        return;
+    }
     switch (nt) {
         case 1: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 1, DOTS, 0>), grid, block, lds, st, P); break;
         case 2: hipLaunchKernelGGL((gemv_kernel<FMT, HP, 2, false, 0>), grid, block, lds, st, P); break;
@@ -768,7 +816,10 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
     int G = (int)std::max<size_t>(1, std::min<size_t>(4, (64 * 1024) / per_tok));
     // One token from a ready int8 activation: stage it through LDS (XS 3) when each wave's
     // chunk range fits the staging registers.
-    if (xsm == 0 && ntok == 1 && !dots && !grp && plan.cps <= 32 && ctx->stage_x) xsm = K2T_XS_STAGED;
+    if (xsm == 0 && ntok == 1 && !dots && !grp && plan.cps <= 32 && ctx->stage_x)
+        // NF4: the activation copied by LDS DMA and exact load waits (measured faster on
+        // the 4096x14336 / 14336x4096 GEMVs; bit planes and NF3 measured no faster)
+        xsm = m->fmt == K2T_FMT_NF && m->bits == 4 ? K2T_XS_STAGED_DMA : K2T_XS_STAGED;
     if (xsm != 0) {  // one token; its int8 activation is built in LDS after the terms
         if (ntok != 1 || m->cols > kSignBlocks * 64 || !ctx->signs) throw Error(K2T_E_INTERNAL, "fused gemv shape");
         P.xsrc = src;

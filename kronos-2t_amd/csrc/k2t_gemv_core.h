@@ -271,25 +271,6 @@ __host__ __device__ constexpr int frag_loads() {
     return 4 + frag_hi_pieces<FMT, HP>() + 1;
 }
 
-__device__ __forceinline__ uint32_t lds_offset(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
-// 16 bytes per lane from p (per-lane address) to LDS [m0 + 16 * lane].
-__device__ __forceinline__ void lds_dma16(const void *p, uint32_t m0) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(p), "s"(m0) : "memory");
-}
-// 4 bytes per lane from p to LDS [m0 + 4 * lane].
-__device__ __forceinline__ void lds_dma4(const void *p, uint32_t m0) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(p), "s"(m0) : "memory");
-}
-
-// Waits until at most N vector memory operations of this wave are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 // GemvWave with its fragments staged in LDS: `slots` points at this wave's F fragment
 // slots.  start() requests fragments 0 .. F-1 (the whole share when it has at most F);

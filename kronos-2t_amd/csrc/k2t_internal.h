@@ -72,7 +72,8 @@ void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *
 //   K2T_XS_SWIGLU : src = interleaved gate_up[2K]      -> SwiGLU + FWHT + int8
 // Codes equal those of rmsnorm_act / swiglu_act followed by launch_gemv.
 //   K2T_XS_STAGED : a ready int8 activation (xq, xs, xsum) staged through LDS per wave
-enum { K2T_XS_GLOBAL = 0, K2T_XS_RMSNORM = 1, K2T_XS_SWIGLU = 2, K2T_XS_STAGED = 3 };
+//   K2T_XS_STAGED_DMA: as K2T_XS_STAGED, staged by direct-to-LDS loads (see gemv_kernel)
+enum { K2T_XS_GLOBAL = 0, K2T_XS_RMSNORM = 1, K2T_XS_SWIGLU = 2, K2T_XS_STAGED = 3, K2T_XS_STAGED_DMA = 5 };
 void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float *src, const float *w, float eps,
                        float *out, bool accumulate);
 uint64_t hadamard_sign_mask_host(uint64_t block);
