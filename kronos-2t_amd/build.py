@@ -107,6 +107,7 @@ def build(verbose=False, out=None, defines=()):
     if not any(n.startswith(NO_SCRATCH) for n, _ in usage):
         raise RuntimeError("no resource report for the persistent decode kernel (remark format changed?)")
     out = out or OUT
+    os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

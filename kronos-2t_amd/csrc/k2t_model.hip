@@ -536,28 +536,24 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
 // Combines the splits of one (token, q head), applies ifwht64 (real_llm.rs:8588-8592), and
 // optionally re-rotates each 64-block with its o_proj chunk index and quantizes it
 // (populate_chunk_fwht_raw(None), real_llm.rs:7060-7084) -> the o_proj activation.
-__global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ part, int nq, int hd, int nsplit,
-                                                        KvRing kr, const int *__restrict__ pos_dev,
-                                                        float *__restrict__ out_f,
-                                                        int8_t *__restrict__ aq, float *__restrict__ as,
-                                                        int32_t *__restrict__ asum) {
-    const uint32_t lane = threadIdx.x;
-    const int head = blockIdx.x, tok = blockIdx.y;
-    const int act = active_len(kr, pos_dev[0] + tok + 1);
-    const int ns = min(nsplit, (act + kAttnSplitLen - 1) / kAttnSplitLen);
-    const float *pp = part + (size_t)(tok * nq + head) * nsplit * (2 + hd);
+// One wave; pp holds the `ns` splits of this (token, head), each {max, sum, o[hd]}.
+template <int ONESHOT>
+__device__ __forceinline__ void merge_head(const float *pp, int ns, int nq, int hd, int head, int tok, uint32_t lane,
+                                           float *__restrict__ out_f, int8_t *__restrict__ aq, float *__restrict__ as,
+                                           int32_t *__restrict__ asum) {
+    static_assert(ONESHOT <= 64, "one split per lane");
     const int nb = hd / 64;
     float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-    if (ns <= kMergeOneShot) {
+    if (ns <= ONESHOT) {
         // Every load in one round trip: split s's maximum and sum in lane s, and this
         // lane's columns of every split; then the same arithmetic, in split order, as the
         // general path below.
         const bool mine = (int)lane < ns;
         const float mv = mine ? pp[(size_t)lane * (2 + hd)] : -INFINITY;
         const float lm = mine ? pp[(size_t)lane * (2 + hd) + 1] : 0.0f;
-        float v0[kMergeOneShot], v1[kMergeOneShot];
+        float v0[ONESHOT], v1[ONESHOT];
 #pragma unroll
-        for (int u = 0; u < kMergeOneShot; u++) {
+        for (int u = 0; u < ONESHOT; u++) {
             const float *ps = pp + (size_t)u * (2 + hd);
             v0[u] = u < ns ? ps[2 + lane] : 0.0f;
             v1[u] = u < ns && nb > 1 ? ps[2 + 64 + lane] : 0.0f;
@@ -565,12 +561,13 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
         const float M = wave_max_f(mv);
         const float em = mine ? expf(mv - M) : 0.0f;
 #pragma unroll
-        for (int u = 0; u < kMergeOneShot; u++) {
-            if (u >= ns) break;
-            const float e = lane_val(em, u);
-            L = fmaf(lane_val(lm, u), e, L);
-            o0 = fmaf(v0[u], e, o0);
-            o1 = fmaf(v1[u], e, o1);
+        for (int u = 0; u < ONESHOT; u++) {
+            if (u < ns) {
+                const float e = lane_val(em, u);
+                L = fmaf(lane_val(lm, u), e, L);
+                o0 = fmaf(v0[u], e, o0);
+                o1 = fmaf(v1[u], e, o1);
+            }
         }
     } else {
         // Split maxima and sums one split per lane (loads in flight together), then the
@@ -620,15 +617,408 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
     }
 }
 
+__global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ part, int nq, int hd, int nsplit,
+                                                        int span_len, KvRing kr, const int *__restrict__ pos_dev,
+                                                        float *__restrict__ out_f,
+                                                        int8_t *__restrict__ aq, float *__restrict__ as,
+                                                        int32_t *__restrict__ asum) {
+    const int head = blockIdx.x, tok = blockIdx.y;
+    const int act = active_len(kr, pos_dev[0] + tok + 1);
+    const int ns = min(nsplit, (act + span_len - 1) / span_len);
+    merge_head<kMergeOneShot>(part + (size_t)(tok * nq + head) * nsplit * (2 + hd), ns, nq, hd, head, tok, threadIdx.x,
+                              out_f, aq, as, asum);
+}
+
+// Long-context decode attention for grouped queries (int8 KV, no window), one launch.
+// Span workgroups, one per (KV head, span of kGqaSpan positions, token), score all
+// G = nq / nkv q heads of the group, so each K / V tile is read from memory once instead
+// of once per q head.  The tile is copied into LDS by direct-to-LDS loads issued first;
+// meanwhile each wave applies bias / QK-norm / RoPE and the Hadamard int8 quantization to
+// one q head (and, in the span holding the current position, waves 0 and 1 build that
+// position's K / V and store them in the cache).  Per head: s_t = float(q8 . k8_t) * ks_t *
+// (qs * scale) as causal_gqa_group_q8 (real_llm.rs:8471-8594), the span's maximum m and
+// sum of exp(s_t - m), and o = sum_t (exp(s_t - m) * vs_t) * v8_t, each V element
+// converted once for all G heads.  A span workgroup publishes its partials with a release
+// increment of its KV head's counter.  Merge workgroups, one per (KV head, q head, token),
+// come first in dispatch order and wait (bounded) for the counter to reach the number of
+// spans, then combine the spans (global maximum, exp-weighted sums), apply ifwht64
+// (real_llm.rs:8588-8592), and write the o_proj activation (populate_chunk_fwht_raw(None),
+// real_llm.rs:7060-7084).  The last merge workgroup of a KV head clears its counters.
+#ifndef K2T_GQA_SPAN
+#define K2T_GQA_SPAN 128
+#endif
+constexpr int kGqaSpan = K2T_GQA_SPAN;  // 64 or 128
+constexpr int kGqaThreads = 512;
+constexpr int kGqaMaxGroup = 8;
+
+#ifdef K2T_GQA_TRACE
+// Measurement builds only: wall-clock stamps of layer 0's workgroups, 8 per (KV head, row).
+__device__ unsigned long long g_gqa_trace[8 * 128 * 8];
+#define GQA_TR(k)                                                                                  \
+    do {                                                                                           \
+        if (layer == 0 && threadIdx.x == 0 && blockIdx.y < 128 && blockIdx.x < 8)                 \
+            g_gqa_trace[((size_t)blockIdx.x * 128 + blockIdx.y) * 8 + (k)] = wall_clock64();       \
+    } while (0)
+#else
+#define GQA_TR(k) \
+    do {          \
+    } while (0)
+#endif
+
+struct GqaArgs {
+    const float *q;
+    int q_stride;
+    int8_t *kq, *vq;
+    float *ks, *vs;
+    const int *pos_dev;
+    int layer, nq, nkv;
+    KvRing kr;
+    float attn_scale;
+    int nspan;
+    AttnPost post;
+    float *part;
+    unsigned int *cnt;  // [token][KV head] {spans done, merges started}
+    int *err;
+    unsigned int spin_limit;
+    float *out_f;
+    int8_t *aq;
+    float *as;
+    int32_t *asum;
+};
+
+template <int HD>
+__global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
+    constexpr int P = kGqaSpan, NTH = kGqaThreads, GM = kGqaMaxGroup;
+    constexpr int PW = P / 64, HW = NTH / 64 / PW;  // waves per 64 positions, heads per pass
+    static_assert(P % 64 == 0 && GM % HW == 0, "span shape");
+    // K and V tiles [position][hd] (the first half); after the o sums the whole array holds
+    // the position subsets' partial sums
+    constexpr int kTiles = 2 * P * 128 > NTH * 4 * GM * 4 ? 2 * P * 128 : NTH * 4 * GM * 4;
+    __shared__ __align__(16) int8_t tiles[kTiles];
+    __shared__ float kst[P], vst[P];
+    __shared__ __align__(16) int8_t qi[GM * 128];
+    __shared__ float qas[GM];
+    __shared__ __align__(16) float sc[P * GM];  // exp(s_t - m) * vs_t per (position, head)
+    __shared__ float red_m[GM][PW], red_l[GM][PW];
+    __shared__ __align__(16) int8_t kcur[128], vcur[128];
+    __shared__ float cur_s[2];
+    const int layer = A.layer, nq = A.nq, nkv = A.nkv;
+    constexpr int hd = HD;
+    const int G = nq / nkv;
+    constexpr int nb = HD / 64;
+    const int kvh = blockIdx.x, tok = blockIdx.z;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+    GQA_TR(0);
+    const int seq = A.pos_dev[0] + tok + 1;
+    const int nact = (seq + P - 1) / P;
+    unsigned int *cnt = A.cnt + 2 * (tok * nkv + kvh);
+    const size_t pstride = (size_t)A.nspan * (2 + hd);
+    if ((int)blockIdx.y < G) {
+        // ------------------------------------------------------------ merge workgroup
+        const int head = kvh * G + (int)blockIdx.y;
+        if (tid == 0) {
+            unsigned int it = 0;
+            while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned int)nact) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++it > A.spin_limit) {
+                    __hip_atomic_store(A.err, 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            // every merge workgroup of this KV head has seen the count: the last clears both
+            if (__hip_atomic_fetch_add(cnt + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned int)G - 1) {
+                __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cnt + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __syncthreads();
+        GQA_TR(1);
+        const float *pp = A.part + (size_t)(tok * nq + head) * pstride;
+        float *mred = reinterpret_cast<float *>(tiles);  // [NTH / 64] wave maxima, then sums
+        // global maximum of the span maxima
+        float M = -INFINITY;
+        for (int s = (int)tid; s < nact; s += NTH) M = fmaxf(M, pp[(size_t)s * (2 + hd)]);
+        M = wave_max_f(M);
+        if (lane == 0) mred[wv] = M;
+        // thread (span subset sub, 4-column group cg): spans sub, sub + nsub, ... ascending
+        constexpr int ncg = HD / 4, nsub = NTH / ncg;
+        const int cg = (int)tid % ncg, sub = (int)tid / ncg;
+        constexpr int kPre = 4;  // spans per thread loaded before the maximum is known
+        float4 ov[kPre];
+        float mv[kPre], lv[kPre];
+#pragma unroll
+        for (int j = 0; j < kPre; j++) {
+            const int s = sub + j * nsub;
+            const bool ok = s < nact;
+            const float *ps = pp + (size_t)(ok ? s : 0) * (2 + hd);
+            ov[j] = ok ? *reinterpret_cast<const float4 *>(ps + 2 + cg * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            mv[j] = ok ? ps[0] : -INFINITY;
+            lv[j] = ok ? ps[1] : 0.0f;
+        }
+        __syncthreads();
+        M = mred[0];
+        for (int w = 1; w < NTH / 64; w++) M = fmaxf(M, mred[w]);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.0f;
+        auto add_span = [&](const float4 &o, float m, float l) {
+            const float e = expf(m - M);
+            L = fmaf(l, e, L);
+            acc.x = fmaf(o.x, e, acc.x);
+            acc.y = fmaf(o.y, e, acc.y);
+            acc.z = fmaf(o.z, e, acc.z);
+            acc.w = fmaf(o.w, e, acc.w);
+        };
+#pragma unroll
+        for (int j = 0; j < kPre; j++)
+            if (sub + j * nsub < nact) add_span(ov[j], mv[j], lv[j]);
+        for (int s = sub + kPre * nsub; s < nact; s += nsub) {
+            const float *ps = pp + (size_t)s * (2 + hd);
+            add_span(*reinterpret_cast<const float4 *>(ps + 2 + cg * 4), ps[0], ps[1]);
+        }
+        // subsets added in order
+        float *osub = reinterpret_cast<float *>(tiles) + 64;  // [nsub][hd]
+        float *lsub = osub + nsub * hd;                      // [nsub]
+        *reinterpret_cast<float4 *>(osub + sub * hd + cg * 4) = acc;
+        if (cg == 0) lsub[sub] = L;
+        __syncthreads();
+        float *ofin = lsub + nsub;  // [hd]
+        if ((int)tid < hd) {
+            float Lt = lsub[0], o = osub[tid];
+            for (int u = 1; u < nsub; u++) {
+                Lt += lsub[u];
+                o += osub[u * hd + tid];
+            }
+            ofin[tid] = o * (1.0f / Lt);
+        }
+        __syncthreads();
+        if ((int)wv < nb) {
+            const int b = (int)wv;
+            const float o = ifwht_lane(ofin[b * 64 + lane], (uint64_t)b, lane);
+            const size_t hbase = (size_t)tok * nq * hd + (size_t)head * hd;
+            if (A.out_f) A.out_f[hbase + b * 64 + lane] = o;
+            if (A.aq) {
+                const size_t c = (size_t)head * nb + b, g = (size_t)tok * nq * nb + c;
+                quant_chunk_store(fwht_lane(o, c, lane), lane, A.aq + g * 64, A.as + g, A.asum + g);
+            }
+        }
+        GQA_TR(7);
+        return;
+    }
+    // ---------------------------------------------------------------- span workgroup
+    const int span = (int)blockIdx.y - G;
+    const int t0 = span * P, t1 = min(seq, t0 + P), n = t1 - t0;
+    if (n <= 0) return;  // spans past the context take no part
+    const KvRing kr = A.kr;
+    const size_t base = ((size_t)layer * nkv + kvh) * kr.cap;
+    int8_t *kt = tiles, *vt = tiles + P * 128;
+    // 1. K / V rows t0 .. t0+P-1 (rows past t1 re-read row t1-1), 16 bytes per lane; the
+    //    scales by waves 0-3 (K rows 0-63, 64-127, then V)
+    {
+        constexpr int pieces = P * HD / 16, per_row = HD / 16;
+        const uint32_t mk = lds_offset(kt), mvv = lds_offset(vt);
+        for (int j = 0; j * NTH < pieces; j++) {
+            const int i = j * NTH + (int)tid;
+            const int r = min(i / per_row, n - 1), c = i % per_row;
+            const size_t off = (base + (size_t)(t0 + r)) * hd + (size_t)c * 16;
+            const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(j * NTH + wv * 64) * 16);
+            lds_dma16(A.kq + off, mk + m0);
+            lds_dma16(A.vq + off, mvv + m0);
+        }
+        if ((int)wv < 2 * PW) {
+            const int row = (int)(wv % PW) * 64 + (int)lane;
+            const size_t sl = base + (size_t)(t0 + min(row, n - 1));
+            const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+                (int)(lds_offset((int)wv < PW ? kst : vst) + (wv % PW) * 256));
+            lds_dma4(((int)wv < PW ? A.ks : A.vs) + sl, m0);
+        }
+    }
+    // 2. q head wv (and the current position's K / V where this span holds it)
+    const AttnPost &post = A.post;
+    const int cur = seq - 1;
+    const bool covers = post.on && t0 <= cur && cur < t1;
+    if ((int)wv < G) {
+        const int h = (int)wv, head = kvh * G + h;
+        const float *qh = A.q + (size_t)tok * A.q_stride + (size_t)head * hd;
+        float qv0, qv1;
+        if (post.on) {
+            head_post(qh, head, nq, nkv, hd, post.bias, post.qn, post.kn, post.eps, post.rope, cur, lane, qv0, qv1);
+        } else {
+            qv0 = qh[lane];
+            qv1 = nb > 1 ? qh[64 + lane] : 0.0f;
+        }
+        const float r0 = fwht_lane(qv0, 0, lane);
+        const float r1 = nb > 1 ? fwht_lane(qv1, 1, lane) : 0.0f;
+        const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
+        int8_t *qd = qi + h * 128;
+        if (mx <= FLT_EPSILON) {
+            qd[lane] = 0;
+            if (nb > 1) qd[64 + lane] = 0;
+            if (lane == 0) qas[h] = 0.0f;
+        } else {
+            const float inv = 127.0f / mx;
+            qd[lane] = (int8_t)(int)rintf(r0 * inv);
+            if (nb > 1) qd[64 + lane] = (int8_t)(int)rintf(r1 * inv);
+            if (lane == 0) qas[h] = (mx / 127.0f) * A.attn_scale;
+        }
+    }
+    if (covers && wv < 2) {
+        const int hh = wv == 0 ? nq + kvh : nq + nkv + kvh;
+        float a0, a1;
+        head_post(A.q + (size_t)tok * A.q_stride + (size_t)hh * hd, hh, nq, nkv, hd, post.bias, post.qn, post.kn,
+                  post.eps, post.rope, cur, lane, a0, a1);
+        const float r0 = fwht_lane(a0, 0, lane);
+        const float r1 = nb > 1 ? fwht_lane(a1, 1, lane) : 0.0f;
+        kv_store_head(r0, r1, nb, lane, 8, hd, 0, wv == 0 ? kcur : vcur, cur_s + wv);
+        kv_store_head(r0, r1, nb, lane, 8, hd, base + (size_t)cur, wv == 0 ? A.kq : A.vq, wv == 0 ? A.ks : A.vs);
+    }
+    GQA_TR(2);
+    wait_vmcnt<0>();  // this wave's tile copies have landed
+    __syncthreads();
+    if (covers) {  // the current position's row (its tile copy read the slot before it was written)
+        const int r = cur - t0;
+        if ((int)tid < hd) {
+            kt[r * hd + tid] = kcur[tid];
+            vt[r * hd + tid] = vcur[tid];
+        }
+        if (tid == 0) {
+            kst[r] = cur_s[0];
+            vst[r] = cur_s[1];
+        }
+        __syncthreads();
+    }
+    GQA_TR(3);
+    // 3. scores: wave w takes position (w & 1) * 64 + lane for heads w / 2 and w / 2 + 4;
+    //    lane p reads its K row's 16-byte pieces starting at piece p (no bank conflicts)
+    const int p = (int)(wv % PW) * 64 + (int)lane;
+    const bool valid = p < n;
+    constexpr int KH = GM / HW;  // heads per wave
+    float s2[KH];
+    {
+        constexpr int npc = HD / 16;
+        uint4 kr4[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (i < npc) kr4[i] = reinterpret_cast<const uint4 *>(kt + p * hd)[(i + p) & (npc - 1)];
+#pragma unroll
+        for (int k = 0; k < KH; k++) {
+            const int h = (int)(wv / PW) + HW * k;
+            s2[k] = -INFINITY;
+            if (h < G) {
+                const uint4 *qr = reinterpret_cast<const uint4 *>(qi + h * 128);
+                int dot = 0;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    if (i < npc) {
+                        const uint4 a = kr4[i], b = qr[(i + p) & (npc - 1)];
+                        dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
+                        dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
+                        dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
+                        dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
+                    }
+                }
+                s2[k] = valid ? ((float)dot * kst[p]) * qas[h] : -INFINITY;
+                const float m = wave_max_f(s2[k]);
+                if (lane == 0) red_m[h][wv % PW] = m;
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < KH; k++) {
+        const int h = (int)(wv / PW) + HW * k;
+        if (h < G) {
+            float m = red_m[h][0];
+            for (int u = 1; u < PW; u++) m = fmaxf(m, red_m[h][u]);
+            const float e = valid ? expf(s2[k] - m) : 0.0f;
+            const float l = wave_sum_f(e);
+            sc[p * GM + h] = e * vst[p];
+            if (lane == 0) red_l[h][wv % PW] = l;
+        }
+    }
+    for (int i = (int)tid; i < P * GM; i += NTH)
+        if ((i & (GM - 1)) >= G) sc[i] = 0.0f;  // heads past G
+    __syncthreads();
+    GQA_TR(4);
+    // 4. o partials: thread (position subset sub, 4-column group cg) converts each V
+    //    element once and adds it into all heads; the subsets are added in order
+    constexpr int ncg = HD / 4, nsub = NTH / ncg, plen = P / nsub;
+    const int cg = (int)tid % ncg, sub = (int)tid / ncg;
+    float acc[GM][4];
+#pragma unroll
+    for (int h = 0; h < GM; h++) acc[h][0] = acc[h][1] = acc[h][2] = acc[h][3] = 0.0f;
+    {
+        const int ta = sub * plen, tb = min(n, ta + plen);
+        for (int t = ta; t < tb; t++) {
+            const int v = *reinterpret_cast<const int *>(vt + t * hd + cg * 4);
+            const float4 w0 = *reinterpret_cast<const float4 *>(sc + t * GM);
+            const float4 w1 = *reinterpret_cast<const float4 *>(sc + t * GM + 4);
+            const float x0 = (float)(int8_t)(v & 0xFF), x1 = (float)(int8_t)((v >> 8) & 0xFF);
+            const float x2 = (float)(int8_t)((v >> 16) & 0xFF), x3 = (float)(int8_t)((v >> 24) & 0xFF);
+            const float w[GM] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                acc[h][0] = fmaf(w[h], x0, acc[h][0]);
+                acc[h][1] = fmaf(w[h], x1, acc[h][1]);
+                acc[h][2] = fmaf(w[h], x2, acc[h][2]);
+                acc[h][3] = fmaf(w[h], x3, acc[h][3]);
+            }
+        }
+    }
+    __syncthreads();  // the tiles are free: they take the subsets' sums [sub][head][hd]
+    float *opart = reinterpret_cast<float *>(tiles);
+#pragma unroll
+    for (int h = 0; h < GM; h++)
+        if (h < G)
+            *reinterpret_cast<float4 *>(opart + ((size_t)sub * G + h) * hd + cg * 4) =
+                make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+    __syncthreads();
+    float *pbase = A.part + (size_t)(tok * nq + kvh * G) * pstride + (size_t)span * (2 + hd);
+    for (int i = (int)tid; i < G * hd; i += NTH) {
+        const int h = i / hd, c = i % hd;
+        float o = opart[h * hd + c];
+        for (int u = 1; u < nsub; u++) o += opart[((size_t)u * G + h) * hd + c];
+        // agent-scope stores write through to the coherence point, so publishing them
+        // needs no L2 write-back: their completion (vmcnt) before the counter increment
+        unsigned int *pp = reinterpret_cast<unsigned int *>(pbase + (size_t)h * pstride);
+        __hip_atomic_store(pp + 2 + c, __float_as_uint(o), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (c == 0) {
+            float m = red_m[h][0], l = red_l[h][0];
+            for (int u = 1; u < PW; u++) {
+                m = fmaxf(m, red_m[h][u]);
+                l += red_l[h][u];
+            }
+            __hip_atomic_store(pp, __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + 1, __float_as_uint(l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    GQA_TR(5);
+    // 5. publish: each wave's stores complete, then (after the barrier) one increment
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (tid == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    GQA_TR(6);
+}
+
+#ifdef K2T_GQA_TRACE
+extern "C" int k2t_gqa_trace_read(unsigned long long *dst) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_gqa_trace), sizeof(g_gqa_trace)) == hipSuccess ? 0 : -1;
+}
+#endif
+
 // One split (the whole-context kernel) up to kAttnWhole positions, else 256-position spans.
 int attn_max_splits(int max_seq) {
     return max_seq <= kAttnWhole ? 1 : (max_seq + kAttnSplitLen - 1) / kAttnSplitLen;
 }
 
+// Spans of the grouped-query kernel over a cache of `cap` slots.
+int gqa_spans(int cap) { return (cap + kGqaSpan - 1) / kGqaSpan; }
+
 void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale,
-                      int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum) {
+                      int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum,
+                      unsigned int *gqa_cnt, int *gqa_err) {
     if (nsplit == 1) {  // the caller sized the context within kAttnWhole (attn_max_splits)
         hipLaunchKernelGGL((attn_partial_kernel<kAttnWhole, true>), dim3(nq, 1, ntok), dim3(kAttnWhole), 0, st, q,
                            q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part, out_f,
@@ -636,12 +1026,24 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
         hip_check(hipGetLastError(), "attention launch");
         return;
     }
+    const int group = nq / nkv;
+    if (gqa_cnt && ntok == 1 && group >= 2 && group <= kGqaMaxGroup && kr.bits == 8 && kr.window == 0 &&
+        (hd == 64 || hd == 128)) {
+        GqaArgs A{q,         q_stride, kq,  vq,    ks,   vs,      pos_dev, layer,      nq, nkv, kr,
+                  attn_scale, gqa_spans(kr.cap), post, part, gqa_cnt, gqa_err, 1u << 20, out_f, aq, as, asum};
+        if (hd == 128)
+            hipLaunchKernelGGL(attn_gqa_kernel<128>, dim3(nkv, group + A.nspan, ntok), dim3(kGqaThreads), 0, st, A);
+        else
+            hipLaunchKernelGGL(attn_gqa_kernel<64>, dim3(nkv, group + A.nspan, ntok), dim3(kGqaThreads), 0, st, A);
+        hip_check(hipGetLastError(), "attn_gqa launch");
+        return;
+    }
     hipLaunchKernelGGL((attn_partial_kernel<kAttnSplitLen, false>), dim3(nq, nsplit, ntok), dim3(kAttnSplitLen), 0, st,
                        q, q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, nsplit, post, part,
                        nullptr, nullptr, nullptr, nullptr);
     hip_check(hipGetLastError(), "attn_partial launch");
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(nq, ntok), dim3(64), 0, st, part, nq, hd, nsplit, kr, pos_dev, out_f, aq, as,
-                       asum);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(nq, ntok), dim3(64), 0, st, part, nq, hd, nsplit, kAttnSplitLen, kr,
+                       pos_dev, out_f, aq, as, asum);
     hip_check(hipGetLastError(), "attn_merge launch");
 }
 
