@@ -274,12 +274,11 @@ int32_t k2t_model_set_exact(k2t_model *m, int32_t exact);
  * the shape of forward_token_sdot_megakernel (real_llm.rs:6794-7403).  0: one kernel per
  * operation.  Used only with the fast epilogue, when every matrix is NF4 or every matrix
  * has 4 bit planes, and the device and model shape allow it (see
- * k2t_model_persistent_active); otherwise the per-operation path runs.  2: as 1, and
- * also for bit-plane models that mix 4- and 5-plane matrices (p55454), which then run a
- * 256-thread variant; it is slower than the per-operation path on SmolLM2-135M (one
- * attention head per workgroup), so 1 leaves such models on the per-operation path.
- * Either way, a step that attends more than 1024 positions runs the per-operation path
- * (one workgroup per head scanning the whole context is slower there). */
+ * k2t_model_persistent_active); otherwise the per-operation path runs.  Bit-plane models
+ * that mix 4- and 5-plane matrices (p55454) run a 256-thread variant.  2: the same as 1
+ * (kept for callers of the earlier interface, where 1 left mixed-plane models on the
+ * per-operation path).  A step that attends more than 1024 positions runs the
+ * per-operation path (a few workgroups per head scanning the context are slower there). */
 int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable);
 /* Whether the next decode step (at the current position) runs the persistent kernel. */
 int32_t k2t_model_persistent_active(const k2t_model *m, int32_t *active);

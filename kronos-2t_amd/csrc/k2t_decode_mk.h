@@ -16,6 +16,10 @@ namespace k2t {
 constexpr int kMkMaxContext = 1024;
 // Copies of the broadcast hand-off vectors (one per XCD of MI355X).
 constexpr int kMkRep = 8;
+// Most spans the attention phase cuts one q head's context into, and the fewest
+// positions per span.
+constexpr int kMkSpans = 4;
+constexpr int kMkSpanMin = 128;
 
 struct MkLayer {
     MatDev qkv, o, gu, down;
@@ -49,6 +53,10 @@ struct MkParams {
     // one XCD's workgroups instead of the whole grid.
     unsigned long long *HA, *HB, *QKV, *OACT, *GACT;
     int rep;
+    // attention spans per q head (1 .. kMkSpans); APART holds the spans 1 .. nsp-1 of each
+    // head as {max, sum, o[hd]} words, [nq][nsp][2 + hd]
+    int nsp;
+    unsigned long long *APART;
     unsigned long long *BEST;  // [2 * grid] per-workgroup lm_head maximum {value, row} words
     float *logits;
     const uint64_t *signs;  // Hadamard sign masks of 64-blocks (bit i = element i)

@@ -334,7 +334,13 @@ __device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t
 }
 
 // Attention of q head h for the current position (causal_gqa_group_q8,
-// real_llm.rs:8471-8594), ending with the o_proj activation chunks of this head.
+// real_llm.rs:8471-8594) over span sp of the context: its seq = pos + 1 positions are cut
+// into P.nsp spans of ceil(seq / nsp) positions.  A task of span sp > 0 hands its span's
+// maximum score m, sum of exp(s_t - m) and o = sum_t exp(s_t - m) vs_t v8_t over as
+// 2 + hd words of APART; the span-0 task merges them with its own (global maximum,
+// exp-weighted sums in span order) and ends with the o_proj activation chunks of the
+// head.  The task whose span holds the current position builds that position's K / V
+// (and, for the first q head of its KV group, stores them in the cache).
 #ifdef K2T_MK_TRACE
 #define ATR(k)                                                                                      \
     do {                                                                                            \
@@ -348,7 +354,7 @@ __device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t
 #endif
 
 template <int NTH>
-__device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &S, int layer, int h, int pos,
+__device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &S, int layer, int h, int sp, int pos,
                                uint32_t ep_in, uint32_t ep_out, uint32_t lane, int wave) {
     const int hd = P.hd, nb = hd / 64, nq = P.nq, nkv = P.nkv;
     const int group = nq / nkv, kvh = h / group;
@@ -361,6 +367,12 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     float *sc = opart + kMaxThreads * 4;                // [min(max_seq, kMkMaxContext)]
     const int t = (int)threadIdx.x;
     const int seq = pos + 1;
+    // spans of this step: at least kMkSpanMin positions each, at most the P.nsp allotted
+    const int nsp = min(P.nsp, max(1, (seq + kMkSpanMin - 1) / kMkSpanMin));
+    if (sp >= nsp) return true;
+    const int len = (seq + nsp - 1) / nsp;
+    const int t0 = min(seq, sp * len), t1 = min(seq, t0 + len), n = t1 - t0;
+    const bool cover = t0 <= pos && pos < t1;
     const size_t base = ((size_t)layer * nkv + kvh) * P.max_seq;
     const int ncg = hd / 4, nps = NTH / ncg;
     const int cg = t % ncg, ps = t / ncg;
@@ -369,19 +381,19 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     constexpr int kVPre = 8;
     uint4 kpre[8];
     float kspre = 0.0f, vspre = 0.0f;
-    if (t < pos) {
-        const uint4 *kr = reinterpret_cast<const uint4 *>(P.kq + (base + t) * hd);
+    if (t0 + t < t1 && t0 + t < pos) {
+        const uint4 *kr = reinterpret_cast<const uint4 *>(P.kq + (base + t0 + t) * hd);
 #pragma unroll
         for (int i = 0; i < 8; i++)
             if (i < hd / 16) kpre[i] = kr[i];
-        kspre = P.ks[base + t];
-        vspre = P.vs[base + t];
+        kspre = P.ks[base + t0 + t];
+        vspre = P.vs[base + t0 + t];
     }
     int vpre[kVPre];
 #pragma unroll
     for (int i = 0; i < kVPre; i++) {
-        const int tt = ps + i * nps;
-        vpre[i] = tt < pos ? *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4) : 0;
+        const int tt = t0 + ps + i * nps;
+        vpre[i] = tt < t1 && tt < pos ? *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4) : 0;
     }
     // RoPE row of this position (waves 0 and 1 rotate q and k): requested before the wait
     float rc = 0.0f, rsn = 0.0f;
@@ -391,9 +403,9 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
         rc = rrow[ri];
         rsn = rrow[(nb == 1 ? 32u : 64u) + ri];
     }
-    // 1. this position's q, k, v (+ bias)
+    // 1. this position's q (and k, v where the span holds it) (+ bias)
     bool ok = true;
-    if (t < 3 * hd) {
+    if (t < (cover ? 3 : 1) * hd) {
         const int part = t / hd, i = t % hd;
         const int row = part == 0 ? h * hd + i : part == 1 ? (nq + kvh) * hd + i : (nq + nkv + kvh) * hd + i;
         uint32_t v = 0;
@@ -409,9 +421,9 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     ATR(1);
     if (S.flag[0]) return false;
     // 2. RoPE (real_llm.rs:9328-9361) on q and k, int8 Hadamard q / k / v
-    const size_t slot = ((size_t)layer * nkv + kvh) * P.max_seq + pos;
+    const size_t slot = base + pos;
     // waves 0, 1, 2 handle q, k, v concurrently
-    if (wave < 2) {
+    if (wave == 0 || (cover && wave == 1)) {
         const float *src = wave == 0 ? qf : kf;
         float x0 = src[lane], x1 = nb > 1 ? src[64 + lane] : 0.0f;
         if (nb == 1) {
@@ -432,7 +444,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
             if (nb > 1) P.kq[slot * hd + 64 + lane] = kn[64 + lane];
             if (lane == 0) P.ks[slot] = sc8;
         }
-    } else if (wave == 2) {
+    } else if (cover && wave == 2) {
         const float vsn = quant_head(vf[lane], nb > 1 ? vf[64 + lane] : 0.0f, nb, lane, vn);
         if (lane == 0) scal[2] = vsn;
         if (h % group == 0) {
@@ -443,14 +455,14 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     }
     lds_barrier();
     ATR(2);
-    // 3. scores s_t = float(q8 . k8_t) * ks_t * (qs * scale), t <= pos
+    // 3. scores s_t = float(q8 . k8_t) * ks_t * (qs * scale), t0 <= t < t1
     const float qas = scal[0];
     float smax = -INFINITY;
-    for (int tt = t; tt < seq; tt += NTH) {
+    for (int tt = t0 + t; tt < t1; tt += NTH) {
         const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
         int dot = 0;
         float kscale;
-        if (tt == t && tt < pos) {  // prefetched
+        if (tt == t0 + t && tt < pos) {  // prefetched
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 if (i >= hd / 16) break;
@@ -474,7 +486,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
             kscale = tt == pos ? scal[1] : P.ks[base + tt];
         }
         const float s = ((float)dot * kscale) * qas;
-        sc[tt] = s;
+        sc[tt - t0] = s;
         smax = fmaxf(smax, s);
     }
     smax = wave_max_f(smax);
@@ -485,10 +497,10 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     lds_barrier();
     ATR(3);
     float psum = 0.0f;
-    for (int tt = t; tt < seq; tt += NTH) {
-        const float p = expf(sc[tt] - m);
-        const float vsc = tt == pos ? scal[2] : (tt == t ? vspre : P.vs[base + tt]);
-        sc[tt] = p * vsc;  // p_t * vs_t
+    for (int tt = t0 + t; tt < t1; tt += NTH) {
+        const float p = expf(sc[tt - t0] - m);
+        const float vsc = tt == pos ? scal[2] : (tt == t0 + t ? vspre : P.vs[base + tt]);
+        sc[tt - t0] = p * vsc;  // p_t * vs_t
         psum += p;
     }
     psum = wave_sum_f(psum);
@@ -505,13 +517,13 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     };
 #pragma unroll
     for (int i = 0; i < kVPre; i++) {  // prefetched slices, positions in ascending order
-        const int tt = ps + i * nps;
-        if (tt < seq) vacc(tt == pos ? *reinterpret_cast<const int *>(vn + cg * 4) : vpre[i], sc[tt]);
+        const int tt = t0 + ps + i * nps;
+        if (tt < t1) vacc(tt == pos ? *reinterpret_cast<const int *>(vn + cg * 4) : vpre[i], sc[tt - t0]);
     }
     // the rest in batches of kVB positions: all of a batch's loads are in flight before
     // its first use (same positions, same order of accumulation)
     constexpr int kVB = NTH == 256 ? 8 : 1;  // 512 threads: 2 measured no faster on the 1.7B model
-    for (int tb = ps + kVPre * nps; tb < seq; tb += kVB * nps) {
+    for (int tb = t0 + ps + kVPre * nps; tb < t1; tb += kVB * nps) {
         int vb[kVB];
 #pragma unroll
         for (int u = 0; u < kVB; u++) {
@@ -522,7 +534,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
 #pragma unroll
         for (int u = 0; u < kVB; u++) {
             const int tt = tb + u * nps;
-            if (tt < seq) vacc(vb[u], sc[tt]);
+            if (tt < t1) vacc(vb[u], sc[tt - t0]);
         }
     }
     for (int m2 = ncg; m2 < 64; m2 <<= 1) {  // lanes l and l ^ m2 hold the same columns
@@ -539,14 +551,77 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
     }
     lds_barrier();
     ATR(4);
+    bool merged = true;
     if (t < hd) {
         float acc = opart[t];
         for (int w2 = 1; w2 < (NTH / 64); w2++) acc += opart[w2 * hd + t];
         float L = red[16];
         for (int w2 = 1; w2 < (NTH / 64); w2++) L += red[16 + w2];
-        qf[t] = acc * (1.0f / L);  // reuse qf for o
+        const float mm = n > 0 ? m : -INFINITY;
+        if (n == 0) L = 0.0f;
+        if (sp > 0) {  // hand the span over (an empty span: m = -inf, L = 0, o = 0)
+            unsigned long long *dst = P.APART + ((size_t)h * P.nsp + sp) * (2 + hd);
+            ll_store(dst + 2 + t, __float_as_uint(acc), ep_out);
+            if (t == 0) {
+                ll_store(dst, __float_as_uint(mm), ep_out);
+                ll_store(dst + 1, __float_as_uint(L), ep_out);
+            }
+        } else {
+            // merge the other spans' {m, L, o[t]}: all loads in flight, then re-polled
+            // together until current (attn_merge_kernel's arithmetic, span order)
+            constexpr int kSp = kMkSpans;
+            unsigned long long w[3 * (kSp - 1)];
+            const unsigned long long *src = P.APART + (size_t)h * P.nsp * (2 + hd);
+            auto addr = [&](int k) { return src + (size_t)(k / 3 + 1) * (2 + hd) + (k % 3 == 2 ? 2 + t : k % 3); };
+            uint32_t pending = 0;
+#pragma unroll
+            for (int k = 0; k < 3 * (kSp - 1); k++) {
+                w[k] = k / 3 + 1 < nsp ? ll_load(addr(k)) : 0ull;
+                if (k / 3 + 1 < nsp && (uint32_t)(w[k] >> 32) != ep_out) pending |= 1u << k;
+            }
+            for (uint32_t spins = 0; pending != 0 && merged; spins++) {
+                if ((spins & 31u) == 31u) {
+                    if (__hip_atomic_load(P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                        merged = false;
+                        break;
+                    }
+                    if (spins > P.spin_limit) {
+                        __hip_atomic_store(P.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        merged = false;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+#pragma unroll
+                for (int k = 0; k < 3 * (kSp - 1); k++)
+                    if (pending & (1u << k)) w[k] = ll_load(addr(k));
+#pragma unroll
+                for (int k = 0; k < 3 * (kSp - 1); k++)
+                    if ((pending & (1u << k)) && (uint32_t)(w[k] >> 32) == ep_out) pending &= ~(1u << k);
+            }
+            float M = mm;
+#pragma unroll
+            for (int s2 = 1; s2 < kSp; s2++)
+                if (s2 < nsp) M = fmaxf(M, __uint_as_float((uint32_t)w[3 * (s2 - 1)]));
+            const float e0 = expf(mm - M);
+            float Lt = fmaf(L, e0, 0.0f), o = fmaf(acc, e0, 0.0f);
+#pragma unroll
+            for (int s2 = 1; s2 < kSp; s2++) {
+                if (s2 < nsp) {
+                    const float e = expf(__uint_as_float((uint32_t)w[3 * (s2 - 1)]) - M);
+                    Lt = fmaf(__uint_as_float((uint32_t)w[3 * (s2 - 1) + 1]), e, Lt);
+                    o = fmaf(__uint_as_float((uint32_t)w[3 * (s2 - 1) + 2]), e, o);
+                }
+            }
+            qf[t] = o * (1.0f / Lt);  // reuse qf for o
+        }
     }
+    if (t == 0) S.flag[0] = 0;
     lds_barrier();
+    if (!merged) S.flag[0] = 1;
+    lds_barrier();
+    if (S.flag[0]) return false;
+    if (sp > 0) return true;  // (the scratch reads are done: the barriers above)
     // 5. ifwht64 per block, then FWHT with the o_proj chunk index + int8 (real_llm.rs:7060-7084)
     if (wave < nb) {
         const float o = ifwht_lane(qf[wave * 64 + lane], (uint64_t)wave, lane);
@@ -630,10 +705,13 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
         const int off = kind == kHead ? P.head_off : P.layers[l].off[kind];
         const int vb = ((int)blockIdx.x + nwg - off) % nwg;  // this workgroup's rank in the phase
         if (kind == kAttn) {
-            if (vb < P.nq) MK_TR(l, 1, 0);
-            for (int h = vb; h < P.nq; h += nwg)
-                if (!attention_head<NTH>(P, P.layers[l], S, l, h, pos, E(ph - 1), E(ph), lane, wave)) return;
-            if (vb < P.nq) MK_TR(l, 1, 5);
+            // task j = (span j / nq, head j % nq): the span-0 tasks (which merge) come first
+            const int ntask = P.nq * P.nsp;
+            if (vb < ntask) MK_TR(l, 1, 0);
+            for (int j = vb; j < ntask; j += nwg)
+                if (!attention_head<NTH>(P, P.layers[l], S, l, j % P.nq, j / P.nq, pos, E(ph - 1), E(ph), lane, wave))
+                    return;
+            if (vb < ntask) MK_TR(l, 1, 5);
             continue;
         }
         const MkLayer &Ly = P.layers[kind == kHead ? 0 : l];

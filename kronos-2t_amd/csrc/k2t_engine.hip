@@ -180,10 +180,11 @@ struct k2t_model {
     size_t mk_lds = 0;
     uint32_t *step_dev = nullptr;
     int *err_dev = nullptr;
-    unsigned long long *ll_ha = nullptr, *ll_hb = nullptr, *ll_qkv = nullptr, *ll_oact = nullptr, *ll_gact = nullptr,
+    unsigned long long *ll_ha = nullptr, *ll_hb = nullptr, *ll_qkv = nullptr, *ll_apart = nullptr, *ll_oact = nullptr, *ll_gact = nullptr,
                        *ll_best = nullptr;
     MkLayer *mk_layers = nullptr;
     int mk_head_off = 0;  // first workgroup of the persistent kernel's lm_head phase
+    int mk_nsp = 1;       // attention spans per q head in the persistent kernel
 };
 
 namespace {
@@ -340,8 +341,7 @@ bool use_persistent(const k2t_model *m) {
     if (m->ring.window > 0 || m->ring.bits != 8) return false;
     for (const auto &L : m->layers)
         if (L.has_moe || L.q_norm || L.k_norm) return false;  // these run on the per-operation path
-    return m->persistent && m->mk_ok && !m->exact && mk_format(m, fmt, hp) &&
-           (hp != kHpMixed || m->persistent == 2);
+    return m->persistent && m->mk_ok && !m->exact && mk_format(m, fmt, hp);
 }
 
 // Destroys the captured decode graph after the stream has drained: a replay enqueued
@@ -381,9 +381,17 @@ void upload_mk_layers(k2t_model *m) {
     }
     // phase task lists laid end to end over the grid (one workgroup per CU)
     const int nwg = m->ctx->num_cus;
+    // attention spans per q head (the kernel uses fewer while the context is short): 2 in
+    // the 512-thread kernel (1.7B nf4g128 decode at context 261-389: 1186 -> 1203 tok/s;
+    // 3 spans 1144-1159), 4 in the 256-thread one (135M p55454 at 512-640: 1038 -> 1259
+    // tok/s)
+    m->mk_nsp = std::max(1, std::min(nw == 8 ? 2 : kMkSpans, nwg / m->cfg.n_heads));
+#ifdef K2T_MK_SPANS
+    m->mk_nsp = K2T_MK_SPANS;
+#endif
     int cursor = 0;
     for (auto &x : h) {
-        const int tasks[5] = {mk_phase_tasks(x.qkv, nw), m->cfg.n_heads, mk_phase_tasks(x.o, nw),
+        const int tasks[5] = {mk_phase_tasks(x.qkv, nw), m->cfg.n_heads * m->mk_nsp, mk_phase_tasks(x.o, nw),
                               mk_phase_tasks(x.gu, nw), mk_phase_tasks(x.down, nw)};
         for (int k = 0; k < 5; k++) {
             x.off[k] = cursor;
@@ -431,6 +439,8 @@ void forward_mk(k2t_model *m) {
     P.HB = m->ll_hb;
     P.QKV = m->ll_qkv;
     P.OACT = m->ll_oact;
+    P.APART = m->ll_apart;
+    P.nsp = m->mk_nsp;
     P.GACT = m->ll_gact;
     P.rep = kMkRep;
     P.BEST = m->ll_best;
@@ -582,7 +592,9 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             hip_check(hipMemcpy(m->step_dev, one, sizeof(one), hipMemcpyHostToDevice), "step init");
             // HA, HB, OACT and GACT in kMkRep copies (one per XCD), QKV and BEST once
             const size_t oact = (size_t)(c.n_heads * c.head_dim / 64) * 18, gact = (size_t)(c.intermediate / 64) * 18;
-            const size_t words = kMkRep * (2 * (size_t)c.hidden + oact + gact) + qkv_w + 2 * (size_t)ctx->num_cus;
+            const size_t apart = (size_t)c.n_heads * kMkSpans * (2 + c.head_dim);
+            const size_t words =
+                kMkRep * (2 * (size_t)c.hidden + oact + gact) + qkv_w + 2 * (size_t)ctx->num_cus + apart;
             m->ll_ha = (unsigned long long *)dalloc(m, words * 8);
             hip_check(hipMemset(m->ll_ha, 0, words * 8), "hand-off clear");
             m->ll_hb = m->ll_ha + kMkRep * (size_t)c.hidden;
@@ -590,6 +602,7 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             m->ll_gact = m->ll_oact + kMkRep * oact;
             m->ll_qkv = m->ll_gact + kMkRep * gact;
             m->ll_best = m->ll_qkv + qkv_w;
+            m->ll_apart = m->ll_best + 2 * (size_t)ctx->num_cus;
             m->mk_layers = (MkLayer *)dalloc(m, (size_t)c.n_layers * sizeof(MkLayer));
         } catch (...) {
             k2t_model_destroy(m);
