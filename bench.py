@@ -342,7 +342,7 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_decode_baseline(cfg, host, context, seconds=10.0, max_tokens=32):
+def cpu_decode_baseline(cfg, host, context, seconds=10.0, max_tokens=32, name="1.7B nf4g128"):
     """The reference's portable CPU decode (dequantize + fp32 dot GEMVs over stripe ranges,
     real_llm.rs:829-836 / simd_lut.rs:5719-5748; scalar q8 attention) restated in the
     oracle, on this machine's host cores: tokens attending `context`+ positions (the KV
@@ -373,7 +373,7 @@ def cpu_decode_baseline(cfg, host, context, seconds=10.0, max_tokens=32):
     _, dt1 = run(1, 0.0, 1)
     return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
             "cpu_model": cpu_model(), "one_thread": {"value": round(1.0 / dt1, 4), "unit": "tok/s", "cores": 1},
-            "sample": f"{ntok} decode tokens of the 1.7B nf4g128 model at context {context}-{context + ntok} (KV "
+            "sample": f"{ntok} decode tokens of the {name} model at context {context}-{context + ntok} (KV "
                       f"cache seeded) on the portable path (dequantize + fp32 dot, simd_lut.rs:5719-5748) restated "
                       f"in C, {threads} host threads; one_thread: 1 token on 1 thread"}
 
@@ -497,7 +497,15 @@ def main():
     if args.decode_only:
         print(json.dumps(dict(line, value=r17["decode_tok_s"], unit="tok/s", config=r17)))
         return
-    m135, mats135, _, r135 = decode_bench(ctx, torch, "135M p55454", k2t.SMOLLM2_135M, "n4", 512, 64, 8, log)
+    m135, mats135, host135, r135 = decode_bench(ctx, torch, "135M p55454", k2t.SMOLLM2_135M, "n4", 512, 64, 8, log)
+    if cpu is not None:
+        # the same port on config 2 at the GPU run's context (512 + warmup)
+        c2 = cpu_decode_baseline(k2t.SMOLLM2_135M, host135, 512 + 8, seconds=5.0, max_tokens=64,
+                                 name="135M p55454")
+        cpu["decode_135m_p55454"] = {k: c2[k] for k in ("value", "unit", "cores", "one_thread", "sample")}
+        log(f"# CPU 135M p55454: decode {c2['value']} tok/s on {c2['cores']} threads, "
+            f"{c2['one_thread']['value']} tok/s on 1")
+    del host135
     m135.close()
     for m in mats135:
         m.close()

@@ -14,7 +14,8 @@ against the oracle on the same seeded inputs.
   and on the mixed-plane persistent kernel.
 - config 5: the Qwen3-30B-A3B shape at full width and two layers (hd 128, 32 q / 4 kv
   heads, QK-norm, 128 NF3 experts top 8, bf16 embedding, vocab 151936) at context 1100,
-  so the 256-position span kernels and the span merge run.
+  so decode runs the grouped-query attention kernel (span and merge workgroups in one
+  launch).
 
 End-to-end bar as in test_gpu_model.py: cosine > 0.9999 and max |diff| <= 2% of
 max |logit| on every step (int8 codes can move by one where inv_rms / expf round
@@ -293,7 +294,8 @@ QWEN3_30B_A3B = dict(hidden=2048, n_heads=32, n_kv_heads=4, head_dim=128, interm
 
 def test_config5_moe_full_width_matches_oracle(gpu_ctx):
     """Qwen3-30B-A3B shape at full width, two layers, context 1100 (above 1024: the
-    256-position span kernels, XCD-grouped, then the span merge), NF4g128 attention with
+    grouped-query attention kernel, 128-position spans of each KV head scoring its 8 q
+    heads, merged in the same launch), NF4g128 attention with
     QK-norm and q_dim 4096 != hidden, 128 NF3 g128 experts top-8 softmax + renorm from a
     .k2tm bank, bf16 untied embedding, NF4g128 head over 151936 rows."""
     from k2tb_writer import write_k2tm

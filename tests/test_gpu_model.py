@@ -93,10 +93,12 @@ def test_long_context_splits(gpu_ctx):
 
 @pytest.mark.parametrize("hd", [64, 128])
 def test_gqa_long_context_xcd_order(gpu_ctx, hd):
-    """GQA (8 q heads over 2 KV heads) with max_seq 2048: contexts above 1024 positions use
-    256-position spans (8 spans here), so the partial-attention workgroups take the
-    XCD-grouped order (the q heads of one KV head on one XCD), then the span merge; 300
-    positions fill two spans.  Decode logits vs the oracle."""
+    """GQA (8 q heads over 2 KV heads) with max_seq 2048: the cache is sized for the span
+    path.  The batched prefill runs the per-head 256-position span kernels in their
+    XCD-grouped order (the q heads of one KV head on one XCD) and the span merge; each
+    decode step runs the grouped-query kernel (one workgroup per KV head and 128-position
+    span scoring all 4 q heads of the group, merge workgroups in the same launch), at
+    hd 64 and 128.  Decode logits vs the oracle."""
     print(f"gqa long context hd={hd}", flush=True)
     cfg = dict(n_layers=1, hidden=8 * hd, n_heads=8, n_kv_heads=2, head_dim=hd, intermediate=256, vocab=200,
                max_seq=2048, rms_eps=1e-5, rope_theta=10000.0)
