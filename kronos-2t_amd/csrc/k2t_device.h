@@ -35,6 +35,16 @@ __device__ __forceinline__ void lds_dma4(const void *p, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(p), "s"(m0) : "memory");
 }
 
+// A 64-bit hand-off word {epoch (high half), payload (low half)}, written and read with
+// one agent-scope atomic each: coherent across XCDs, and the payload and its ready mark
+// arrive together, so neither side needs a fence.
+__device__ __forceinline__ void ll_word_store(unsigned long long *p, uint32_t v, uint32_t epoch) {
+    __hip_atomic_store(p, ((unsigned long long)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ll_word_load(const unsigned long long *p) {
+    return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Waits until at most N vector memory operations of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -27,7 +27,7 @@ void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float 
 void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale, int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as,
-                      int32_t *asum, unsigned int *gqa_cnt, int *gqa_err);
+                      int32_t *asum, const GqaWork &gqa);
 int attn_max_splits(int max_seq);
 int gqa_spans(int cap);
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums);
@@ -164,7 +164,8 @@ struct k2t_model {
     int *tokens = nullptr;
     int max_batch = 0;
     float *hidden = nullptr, *qkv = nullptr, *gu = nullptr, *logits = nullptr, *attn_part = nullptr;
-    unsigned int *attn_cnt = nullptr;  // grouped-query attention completion counters
+    unsigned long long *attn_words = nullptr;  // grouped-query attention span words
+    unsigned int *attn_cnt = nullptr;          // {its epoch, merge workgroups done}
     int8_t *xq = nullptr;
     float *xs = nullptr;
     int32_t *xsum = nullptr;
@@ -275,7 +276,7 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
         }
         launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, post, m->pos_dev, l, nq, nkv,
                          hd, m->ring, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum,
-                         m->attn_cnt, m->err_dev);
+                         GqaWork{m->attn_words, m->attn_cnt, m->err_dev});
         launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
         if (L.has_moe) {
             // one token at a time: each token has its own routes (forward_layer_single)
@@ -480,8 +481,12 @@ void check_mk_error(k2t_model *m) {
     hip_check(hipMemcpy(&e, m->err_dev, sizeof(int), hipMemcpyDeviceToHost), "error flag");
     if (e) {
         (void)hipMemset(m->err_dev, 0, sizeof(int));
-        // a timed-out wait leaves the grouped-query attention counters inconsistent
-        (void)hipMemset(m->attn_cnt, 0, 2 * (size_t)m->cfg.n_kv_heads * sizeof(unsigned int));
+        // a timed-out wait leaves the grouped-query attention's counters and words
+        // inconsistent: start its epochs over
+        (void)hipMemset(m->attn_cnt, 0, 2 * sizeof(unsigned int));
+        (void)hipMemset(m->attn_words, 0,
+                        (size_t)gqa_spans(m->cfg.max_seq) * m->cfg.n_heads * (2 + m->cfg.head_dim) *
+                            sizeof(unsigned long long));
         throw Error(K2T_E_INTERNAL, e == 2   ? "MoE route selection: router wait timed out"
                                     : e == 3 ? "grouped-query attention: span wait timed out"
                                              : "persistent decode kernel: dependency wait timed out");
@@ -571,14 +576,15 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             m->qkv = (float *)dalloc(m, (size_t)max_batch * qkv_w * sizeof(float));
             m->gu = (float *)dalloc(m, (size_t)max_batch * 2 * c.intermediate * sizeof(float));
             m->logits = (float *)dalloc(m, (size_t)c.vocab * sizeof(float));
-            // span partials: per-head 256-position spans for every token of a batch, or the
-            // grouped-query kernel's 64-position spans for one token
-            const size_t spans = std::max((size_t)max_batch * attn_max_splits(c.max_seq), (size_t)gqa_spans(c.max_seq));
-            m->attn_part = (float *)dalloc(m, spans * c.n_heads * (2 + c.head_dim) * sizeof(float));
-            // counters of the grouped-query kernel, two per KV head (each launch leaves them
-            // at zero)
-            m->attn_cnt = (unsigned int *)dalloc(m, 2 * (size_t)c.n_kv_heads * sizeof(unsigned int));
-            hip_check(hipMemset(m->attn_cnt, 0, 2 * (size_t)c.n_kv_heads * sizeof(unsigned int)), "counter clear");
+            m->attn_part = (float *)dalloc(
+                m, (size_t)max_batch * c.n_heads * attn_max_splits(c.max_seq) * (2 + c.head_dim) * sizeof(float));
+            // grouped-query attention: span words (one token) and the epoch / done counters,
+            // zeroed once (epochs only grow, so no launch clears them)
+            const size_t gw = (size_t)gqa_spans(c.max_seq) * c.n_heads * (2 + c.head_dim);
+            m->attn_words = (unsigned long long *)dalloc(m, gw * sizeof(unsigned long long));
+            hip_check(hipMemset(m->attn_words, 0, gw * sizeof(unsigned long long)), "span words clear");
+            m->attn_cnt = (unsigned int *)dalloc(m, 2 * sizeof(unsigned int));
+            hip_check(hipMemset(m->attn_cnt, 0, 2 * sizeof(unsigned int)), "counter clear");
             m->xq = (int8_t *)dalloc(m, (size_t)max_batch * kmax);
             m->xs = (float *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(float));
             m->xsum = (int32_t *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(int32_t));
@@ -1044,7 +1050,7 @@ void attn_decode_impl(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_he
     // read-only on the cache (no post stage: the caller's queries are final)
     launch_attention(ctx->stream, d_q, n_heads * head_dim, (int8_t *)d_kq, (int8_t *)d_vq, (float *)d_ks,
                      (float *)d_vs, AttnPost{}, pos, 0, n_heads, n_kv_heads, head_dim, kr, attn_scale, nsplit, 1, pp,
-                     d_out, nullptr, nullptr, nullptr, nullptr, nullptr);
+                     d_out, nullptr, nullptr, nullptr, GqaWork{});
     // the copied position lives on this function's stack; the no-alloc variant stores it
     // with a kernel and stays asynchronous
     if (!noalloc) hip_check(hipStreamSynchronize(ctx->stream), "sync");

@@ -103,6 +103,15 @@ struct KvRing {
     int cap, window, sinks, ring, bits;
 };
 
+// Workspace of the grouped-query decode attention kernel: the span words
+// ([q head][span][2 + hd] {payload, epoch}, zeroed once) and two counters {epoch of the
+// last launch, merge workgroups done} (zeroed once); err receives 3 on a wait timeout.
+struct GqaWork {
+    unsigned long long *words;
+    unsigned int *cnt;
+    int *err;
+};
+
 // One-token decode attention that also does qkv_post's work (bias, QK-norm, RoPE, K/V
 // store): q is then the raw qkv row.
 struct AttnPost {

@@ -638,12 +638,14 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
 // position's K / V and store them in the cache).  Per head: s_t = float(q8 . k8_t) * ks_t *
 // (qs * scale) as causal_gqa_group_q8 (real_llm.rs:8471-8594), the span's maximum m and
 // sum of exp(s_t - m), and o = sum_t (exp(s_t - m) * vs_t) * v8_t, each V element
-// converted once for all G heads.  A span workgroup publishes its partials with a release
-// increment of its KV head's counter.  Merge workgroups, one per (KV head, q head, token),
-// come first in dispatch order and wait (bounded) for the counter to reach the number of
-// spans, then combine the spans (global maximum, exp-weighted sums), apply ifwht64
-// (real_llm.rs:8588-8592), and write the o_proj activation (populate_chunk_fwht_raw(None),
-// real_llm.rs:7060-7084).  The last merge workgroup of a KV head clears its counters.
+// converted once for all G heads.  A span workgroup publishes its partials as
+// {payload, epoch} words (one agent-scope atomic store each).  Merge workgroups, one per
+// (KV head, q head, token), come first in dispatch order and poll (bounded) the words of
+// their head's spans until every one carries this launch's epoch, then combine the spans
+// (global maximum, exp-weighted sums in span order), apply ifwht64 (real_llm.rs:8588-8592),
+// and write the o_proj activation (populate_chunk_fwht_raw(None), real_llm.rs:7060-7084).
+// The epoch is one more than the last launch's; the last merge workgroup to finish
+// advances it, so the words never need clearing.
 #ifndef K2T_GQA_SPAN
 #define K2T_GQA_SPAN 128
 #endif
@@ -676,8 +678,8 @@ struct GqaArgs {
     float attn_scale;
     int nspan;
     AttnPost post;
-    float *part;
-    unsigned int *cnt;  // [token][KV head] {spans done, merges started}
+    unsigned long long *words;  // [token][q head][nspan][2 + hd] {payload, epoch} span words
+    unsigned int *cnt;          // {epoch of the last launch, merge workgroups done}
     int *err;
     unsigned int spin_limit;
     float *out_f;
@@ -711,70 +713,118 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
     GQA_TR(0);
     const int seq = A.pos_dev[0] + tok + 1;
     const int nact = (seq + P - 1) / P;
-    unsigned int *cnt = A.cnt + 2 * (tok * nkv + kvh);
+    // this launch's epoch: one more than the last launch's (advanced by its last merge
+    // workgroup, after every span workgroup of that launch had read it)
+    const uint32_t ep = __hip_atomic_load(A.cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     const size_t pstride = (size_t)A.nspan * (2 + hd);
     if ((int)blockIdx.y < G) {
         // ------------------------------------------------------------ merge workgroup
+        // thread (span subset sub, 4-column group cg): spans sub, sub + nsub, ... ascending;
+        // per span it polls the words {m, L, o[4 columns]} until they carry this epoch
         const int head = kvh * G + (int)blockIdx.y;
-        if (tid == 0) {
-            unsigned int it = 0;
-            while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned int)nact) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++it > A.spin_limit) {
-                    __hip_atomic_store(A.err, 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            // every merge workgroup of this KV head has seen the count: the last clears both
-            if (__hip_atomic_fetch_add(cnt + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned int)G - 1) {
-                __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(cnt + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        __syncthreads();
-        GQA_TR(1);
-        const float *pp = A.part + (size_t)(tok * nq + head) * pstride;
-        float *mred = reinterpret_cast<float *>(tiles);  // [NTH / 64] wave maxima, then sums
-        // global maximum of the span maxima
-        float M = -INFINITY;
-        for (int s = (int)tid; s < nact; s += NTH) M = fmaxf(M, pp[(size_t)s * (2 + hd)]);
-        M = wave_max_f(M);
-        if (lane == 0) mred[wv] = M;
-        // thread (span subset sub, 4-column group cg): spans sub, sub + nsub, ... ascending
+        const unsigned long long *pp = A.words + (size_t)(tok * nq + head) * pstride;
         constexpr int ncg = HD / 4, nsub = NTH / ncg;
         const int cg = (int)tid % ncg, sub = (int)tid / ncg;
-        constexpr int kPre = 4;  // spans per thread loaded before the maximum is known
-        float4 ov[kPre];
-        float mv[kPre], lv[kPre];
+        constexpr int kPre = 4;  // spans per thread polled together
+        bool ok = true;
+        auto poll = [&](int s, unsigned long long (&w)[6]) {
+            // (the caller keeps s < nact)
+            const unsigned long long *ps = pp + (size_t)s * (2 + hd);
+            w[0] = ll_word_load(ps);
+            w[1] = ll_word_load(ps + 1);
+#pragma unroll
+            for (int k = 0; k < 4; k++) w[2 + k] = ll_word_load(ps + 2 + cg * 4 + k);
+        };
+        unsigned long long wv6[kPre][6];
+        uint32_t pending = 0;
 #pragma unroll
         for (int j = 0; j < kPre; j++) {
-            const int s = sub + j * nsub;
-            const bool ok = s < nact;
-            const float *ps = pp + (size_t)(ok ? s : 0) * (2 + hd);
-            ov[j] = ok ? *reinterpret_cast<const float4 *>(ps + 2 + cg * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-            mv[j] = ok ? ps[0] : -INFINITY;
-            lv[j] = ok ? ps[1] : 0.0f;
+            if (sub + j * nsub < nact) {
+                poll(sub + j * nsub, wv6[j]);
+#pragma unroll
+                for (int k = 0; k < 6; k++)
+                    if ((uint32_t)(wv6[j][k] >> 32) != ep) pending |= 1u << (6 * j + k);
+            } else {
+                wv6[j][0] = (unsigned long long)__float_as_uint(-INFINITY);
+#pragma unroll
+                for (int k = 1; k < 6; k++) wv6[j][k] = 0ull;
+            }
         }
+        for (uint32_t spins = 0; pending != 0 && ok; spins++) {
+            if ((spins & 31u) == 31u) {
+                if (spins > A.spin_limit) {
+                    __hip_atomic_store(A.err, 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+#pragma unroll
+            for (int j = 0; j < kPre; j++) {
+                const unsigned long long *ps = pp + (size_t)(sub + j * nsub) * (2 + hd);
+#pragma unroll
+                for (int k = 0; k < 6; k++)
+                    if (pending & (1u << (6 * j + k)))
+                        wv6[j][k] = ll_word_load(ps + (k < 2 ? k : 2 + cg * 4 + (k - 2)));
+            }
+#pragma unroll
+            for (int j = 0; j < kPre; j++)
+#pragma unroll
+                for (int k = 0; k < 6; k++)
+                    if ((pending & (1u << (6 * j + k))) && (uint32_t)(wv6[j][k] >> 32) == ep)
+                        pending &= ~(1u << (6 * j + k));
+        }
+        GQA_TR(1);
+        // spans past kPre per thread (contexts above nsub * kPre * P positions): one by one
+        auto wait6 = [&](int s, unsigned long long (&w)[6]) {
+            poll(s, w);
+            for (uint32_t spins = 0; ok; spins++) {
+                bool cur = true;
+#pragma unroll
+                for (int k = 0; k < 6; k++) cur = cur && (uint32_t)(w[k] >> 32) == ep;
+                if (cur) break;
+                if (spins > A.spin_limit) {
+                    __hip_atomic_store(A.err, 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                poll(s, w);
+            }
+        };
+        auto wf = [](unsigned long long w) { return __uint_as_float((uint32_t)w); };
+        float *mred = reinterpret_cast<float *>(tiles);  // [NTH / 64] wave maxima
+        // global maximum of the span maxima
+        float M = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < kPre; j++) M = fmaxf(M, wf(wv6[j][0]));
+        for (int s = sub + kPre * nsub; s < nact; s += nsub) {
+            unsigned long long w[6];
+            wait6(s, w);
+            M = fmaxf(M, wf(w[0]));
+        }
+        M = wave_max_f(M);
+        if (lane == 0) mred[wv] = M;
         __syncthreads();
         M = mred[0];
         for (int w = 1; w < NTH / 64; w++) M = fmaxf(M, mred[w]);
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         float L = 0.0f;
-        auto add_span = [&](const float4 &o, float m, float l) {
-            const float e = expf(m - M);
-            L = fmaf(l, e, L);
-            acc.x = fmaf(o.x, e, acc.x);
-            acc.y = fmaf(o.y, e, acc.y);
-            acc.z = fmaf(o.z, e, acc.z);
-            acc.w = fmaf(o.w, e, acc.w);
+        auto add_span = [&](const unsigned long long (&w)[6]) {
+            const float e = expf(wf(w[0]) - M);
+            L = fmaf(wf(w[1]), e, L);
+            acc.x = fmaf(wf(w[2]), e, acc.x);
+            acc.y = fmaf(wf(w[3]), e, acc.y);
+            acc.z = fmaf(wf(w[4]), e, acc.z);
+            acc.w = fmaf(wf(w[5]), e, acc.w);
         };
 #pragma unroll
         for (int j = 0; j < kPre; j++)
-            if (sub + j * nsub < nact) add_span(ov[j], mv[j], lv[j]);
+            if (sub + j * nsub < nact) add_span(wv6[j]);
         for (int s = sub + kPre * nsub; s < nact; s += nsub) {
-            const float *ps = pp + (size_t)s * (2 + hd);
-            add_span(*reinterpret_cast<const float4 *>(ps + 2 + cg * 4), ps[0], ps[1]);
+            unsigned long long w[6];
+            wait6(s, w);
+            add_span(w);
         }
         // subsets added in order
         float *osub = reinterpret_cast<float *>(tiles) + 64;  // [nsub][hd]
@@ -800,6 +850,15 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
             if (A.aq) {
                 const size_t c = (size_t)head * nb + b, g = (size_t)tok * nq * nb + c;
                 quant_chunk_store(fwht_lane(o, c, lane), lane, A.aq + g * 64, A.as + g, A.asum + g);
+            }
+        }
+        // the last merge workgroup of the launch advances the epoch (every span workgroup
+        // of this launch has published, so all have read the epoch already)
+        if (tid == 0) {
+            const unsigned int total = gridDim.x * (unsigned int)G * gridDim.z;
+            if (__hip_atomic_fetch_add(A.cnt + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1u) {
+                __hip_atomic_store(A.cnt + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(A.cnt, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         GQA_TR(7);
@@ -973,31 +1032,26 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
             *reinterpret_cast<float4 *>(opart + ((size_t)sub * G + h) * hd + cg * 4) =
                 make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
     __syncthreads();
-    float *pbase = A.part + (size_t)(tok * nq + kvh * G) * pstride + (size_t)span * (2 + hd);
+    // 5. publish {m, L, o[hd]} per head as {payload, epoch} words (one agent-scope store
+    //    each: the value and its ready mark arrive together, no fence or counter)
+    unsigned long long *pbase = A.words + (size_t)(tok * nq + kvh * G) * pstride + (size_t)span * (2 + hd);
     for (int i = (int)tid; i < G * hd; i += NTH) {
         const int h = i / hd, c = i % hd;
         float o = opart[h * hd + c];
         for (int u = 1; u < nsub; u++) o += opart[((size_t)u * G + h) * hd + c];
-        // agent-scope stores write through to the coherence point, so publishing them
-        // needs no L2 write-back: their completion (vmcnt) before the counter increment
-        unsigned int *pp = reinterpret_cast<unsigned int *>(pbase + (size_t)h * pstride);
-        __hip_atomic_store(pp + 2 + c, __float_as_uint(o), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned long long *pp = pbase + (size_t)h * pstride;
+        ll_word_store(pp + 2 + c, __float_as_uint(o), ep);
         if (c == 0) {
             float m = red_m[h][0], l = red_l[h][0];
             for (int u = 1; u < PW; u++) {
                 m = fmaxf(m, red_m[h][u]);
                 l += red_l[h][u];
             }
-            __hip_atomic_store(pp, __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(pp + 1, __float_as_uint(l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ll_word_store(pp, __float_as_uint(m), ep);
+            ll_word_store(pp + 1, __float_as_uint(l), ep);
         }
     }
     GQA_TR(5);
-    // 5. publish: each wave's stores complete, then (after the barrier) one increment
-    wait_vmcnt<0>();
-    __syncthreads();
-    if (tid == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    GQA_TR(6);
 }
 
 #ifdef K2T_GQA_TRACE
@@ -1018,7 +1072,7 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale,
                       int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum,
-                      unsigned int *gqa_cnt, int *gqa_err) {
+                      const GqaWork &gqa) {
     if (nsplit == 1) {  // the caller sized the context within kAttnWhole (attn_max_splits)
         hipLaunchKernelGGL((attn_partial_kernel<kAttnWhole, true>), dim3(nq, 1, ntok), dim3(kAttnWhole), 0, st, q,
                            q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part, out_f,
@@ -1027,10 +1081,11 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
         return;
     }
     const int group = nq / nkv;
-    if (gqa_cnt && ntok == 1 && group >= 2 && group <= kGqaMaxGroup && kr.bits == 8 && kr.window == 0 &&
+    if (gqa.words && ntok == 1 && group >= 2 && group <= kGqaMaxGroup && kr.bits == 8 && kr.window == 0 &&
         (hd == 64 || hd == 128)) {
-        GqaArgs A{q,         q_stride, kq,  vq,    ks,   vs,      pos_dev, layer,      nq, nkv, kr,
-                  attn_scale, gqa_spans(kr.cap), post, part, gqa_cnt, gqa_err, 1u << 20, out_f, aq, as, asum};
+        GqaArgs A{q,          q_stride,          kq,   vq,         ks,       vs,       pos_dev, layer,
+                  nq,         nkv,               kr,   attn_scale, gqa_spans(kr.cap), post, gqa.words,
+                  gqa.cnt,    gqa.err,           1u << 20, out_f, aq, as, asum};
         if (hd == 128)
             hipLaunchKernelGGL(attn_gqa_kernel<128>, dim3(nkv, group + A.nspan, ntok), dim3(kGqaThreads), 0, st, A);
         else
