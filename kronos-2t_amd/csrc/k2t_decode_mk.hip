@@ -257,7 +257,7 @@ enum PhaseKind { kQkv = 0, kAttn = 1, kO = 2, kGu = 3, kDown = 4, kHead = 5 };
 // down_proj activation chunks as produced, or RMSNorm + FWHT + int8 of the hidden vector
 // (HA after the embedding or a down phase, HB after an o phase).
 template <int NTH>
-__device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, const MkLayer &Ly, int kind,
+__device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, const float *norm_w, int kind,
                                               uint32_t epoch, uint32_t lane, int wave, int t0) {
     if (kind == kO || kind == kDown) {
         const int nch = kind == kO ? P.nq * P.hd / 64 : P.inter / 64;
@@ -268,7 +268,7 @@ __device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, c
     if (!load_words<NTH>(P, S, (kind == kGu ? P.HB : P.HA) + my_copy(P) * (size_t)P.d, P.d, epoch, false, S.hbuf,
                          t0))
         return false;
-    build_norm_act<NTH>(P, S, kind == kQkv ? Ly.in_norm : kind == kGu ? Ly.post_norm : P.final_norm, lane, wave);
+    build_norm_act<NTH>(P, S, norm_w, lane, wave);
     return true;
 }
 
@@ -354,7 +354,7 @@ __device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t
 #endif
 
 template <int NTH>
-__device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &S, int layer, int h, int sp, int pos,
+__device__ bool attention_head(const MkParams &P, const float *bias, const Lds &S, int layer, int h, int sp, int pos,
                                uint32_t ep_in, uint32_t ep_out, uint32_t lane, int wave) {
     const int hd = P.hd, nb = hd / 64, nq = P.nq, nkv = P.nkv;
     const int group = nq / nkv, kvh = h / group;
@@ -411,7 +411,7 @@ __device__ bool attention_head(const MkParams &P, const MkLayer &Ly, const Lds &
         uint32_t v = 0;
         ok = ll_wait(P, P.QKV + row, ep_in, v);
         float f = __uint_as_float(v);
-        if (Ly.bias) f = f + Ly.bias[row];
+        if (bias) f = f + bias[row];
         qf[t] = f;  // qf, kf, vf are contiguous
     }
     if (t == 0) S.flag[0] = 0;
@@ -676,6 +676,14 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
     const uint32_t nph = 2u + 5u * (uint32_t)P.L;
     auto E = [&](int ph) { return step * nph + (uint32_t)ph + 1u; };
     const int d = P.d;
+    // The layer table is read-only for the launch: scalar loads through the constant
+    // address space (the four matrix views of a layer are consecutive).
+    using CMkLayer = const __attribute__((address_space(4))) MkLayer;
+    CMkLayer *LT = (CMkLayer *)P.layers;
+    static_assert(offsetof(MkLayer, o) == offsetof(MkLayer, qkv) + sizeof(MatDev) &&
+                      offsetof(MkLayer, gu) == offsetof(MkLayer, o) + sizeof(MatDev) &&
+                      offsetof(MkLayer, down) == offsetof(MkLayer, gu) + sizeof(MatDev),
+                  "MkLayer matrix views must be consecutive");
 
     // phase 0: embedding -> HA (one wave per 64-element chunk)
     {
@@ -702,20 +710,25 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
         // no phase's input polls queue behind weight loads that a workgroup issued on
         // finishing the previous phase.
         const int nwg = (int)gridDim.x;
-        const int off = kind == kHead ? P.head_off : P.layers[l].off[kind];
+        const int off = kind == kHead ? P.head_off : LT[l].off[kind];
         const int vb = ((int)blockIdx.x + nwg - off) % nwg;  // this workgroup's rank in the phase
         if (kind == kAttn) {
             // task j = (span j / nq, head j % nq): the span-0 tasks (which merge) come first
             const int ntask = P.nq * P.nsp;
             if (vb < ntask) MK_TR(l, 1, 0);
             for (int j = vb; j < ntask; j += nwg)
-                if (!attention_head<NTH>(P, P.layers[l], S, l, j % P.nq, j / P.nq, pos, E(ph - 1), E(ph), lane, wave))
+                if (!attention_head<NTH>(P, LT[l].bias, S, l, j % P.nq, j / P.nq, pos, E(ph - 1), E(ph), lane, wave))
                     return;
             if (vb < ntask) MK_TR(l, 1, 5);
             continue;
         }
-        const MkLayer &Ly = P.layers[kind == kHead ? 0 : l];
-        const MatDev &M = kind == kQkv ? Ly.qkv : kind == kO ? Ly.o : kind == kGu ? Ly.gu : kind == kDown ? Ly.down : P.head;
+        // the matrix view in registers, read by scalar loads (a vector load here would wait
+        // for the previous phase's hand-off stores to complete: loads return in order)
+        const int li = kind == kHead ? 0 : l;
+        MatDev Mv = P.head;
+        if (kind != kHead) Mv = *(const MatDev *)(&LT[li].qkv + (kind == kQkv ? 0 : kind - 1));
+        const MatDev &M = Mv;
+        const float *norm_w = kind == kQkv ? LT[li].in_norm : kind == kGu ? LT[li].post_norm : P.final_norm;
         const int nblocks = M.smode ? M.stripes : M.np + (M.stripes & 1);
         const int groups = kWaves / M.nseg;
         if (vb * groups >= nblocks) continue;  // no task here: go on to the next phase
@@ -734,7 +747,7 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                 GemvWaveLds<FMT, HP, kMkFrags> gw(M, rb, rb < nblocks, wseg, lane, slots);
                 gw.start();
                 if (first) {
-                    if (!mk_load_input<NTH>(P, S, Ly, kind, E(ph - 1), lane, wave, 0)) return;
+                    if (!mk_load_input<NTH>(P, S, norm_w, kind, E(ph - 1), lane, wave, 0)) return;
                     MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 1);
                 }
 #ifdef K2T_MK_TRACE
