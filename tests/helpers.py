@@ -74,3 +74,36 @@ def acts(rng, K, ntok, **kw):
         ss.append(s)
         ms.append(m)
     return np.stack(qs), np.stack(ss), np.stack(ms)
+
+
+def mix64(z):
+    z = np.uint64(z)
+    with np.errstate(over="ignore"):
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def synthetic_kv(ref, n_layers, nkv, hd, n_pos, seed):
+    """The engine's kv_synthetic fill (seeded int8 codes, scales in [0.005, 0.05]) written
+    into the oracle's cache: slot (layer*nkv + kvh, pos), hash base
+    seed*golden + slot_lin*FNV, codes (h & 0xFF) - 128 and ((h >> 8) & 0xFF) - 128 with
+    -128 clamped to -127."""
+    with np.errstate(over="ignore"):
+        lin = np.arange(n_layers * nkv * n_pos, dtype=np.uint64)
+        base = np.uint64(seed) * np.uint64(0x9E3779B97F4A7C15) + lin * np.uint64(0x100000001B3)
+        h = mix64(base[:, None] + np.arange(hd, dtype=np.uint64)[None, :])
+        hs = mix64(base ^ np.uint64(0xD1B54A32D192ED03))
+    k = (h & np.uint64(0xFF)).astype(np.int32) - 128
+    v = ((h >> np.uint64(8)) & np.uint64(0xFF)).astype(np.int32) - 128
+    k[k == -128] = -127
+    v[v == -128] = -127
+    f = np.float32
+    a = f(0.005) + (f(0.045) * (hs & np.uint64(0xFFFF)).astype(np.float32)) / f(65535.0)
+    b = f(0.005) + (f(0.045) * ((hs >> np.uint64(16)) & np.uint64(0xFFFF)).astype(np.float32)) / f(65535.0)
+    shape = (n_layers, nkv, n_pos)
+    ref.kq[:, :, :n_pos] = k.astype(np.int8).reshape(*shape, hd)
+    ref.vq[:, :, :n_pos] = v.astype(np.int8).reshape(*shape, hd)
+    ref.ks[:, :, :n_pos] = a.astype(np.float32).reshape(shape)
+    ref.vs[:, :, :n_pos] = b.astype(np.float32).reshape(shape)
+    ref.pos = n_pos

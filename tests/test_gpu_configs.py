@@ -30,6 +30,7 @@ import pytest
 
 import k2t
 import oracle as O
+from helpers import synthetic_kv
 from model_oracle import Matrix, OracleModel
 
 pytestmark = pytest.mark.gpu
@@ -57,39 +58,6 @@ def _oracle_layers(cfg, conv):
     ones = np.ones(cfg["hidden"], np.float32)
     return [{"qkv": conv[4 * i], "o": conv[4 * i + 1], "gu": conv[4 * i + 2], "down": conv[4 * i + 3],
              "in_norm": ones, "post_norm": ones, "bias": None} for i in range(cfg["n_layers"])], ones
-
-
-def _mix64(z):
-    z = np.uint64(z)
-    with np.errstate(over="ignore"):
-        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
-        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
-    return z ^ (z >> np.uint64(31))
-
-
-def _synthetic_kv(ref, n_layers, nkv, hd, n_pos, seed):
-    """The engine's kv_synthetic fill (seeded int8 codes, scales in [0.005, 0.05]) written
-    into the oracle's cache: slot (layer*nkv + kvh, pos), hash base
-    seed*golden + slot_lin*FNV, codes (h & 0xFF) - 128 and ((h >> 8) & 0xFF) - 128 with
-    -128 clamped to -127."""
-    with np.errstate(over="ignore"):
-        lin = np.arange(n_layers * nkv * n_pos, dtype=np.uint64)
-        base = np.uint64(seed) * np.uint64(0x9E3779B97F4A7C15) + lin * np.uint64(0x100000001B3)
-        h = _mix64(base[:, None] + np.arange(hd, dtype=np.uint64)[None, :])
-        hs = _mix64(base ^ np.uint64(0xD1B54A32D192ED03))
-    k = (h & np.uint64(0xFF)).astype(np.int32) - 128
-    v = ((h >> np.uint64(8)) & np.uint64(0xFF)).astype(np.int32) - 128
-    k[k == -128] = -127
-    v[v == -128] = -127
-    f = np.float32
-    a = f(0.005) + (f(0.045) * (hs & np.uint64(0xFFFF)).astype(np.float32)) / f(65535.0)
-    b = f(0.005) + (f(0.045) * ((hs >> np.uint64(16)) & np.uint64(0xFFFF)).astype(np.float32)) / f(65535.0)
-    shape = (n_layers, nkv, n_pos)
-    ref.kq[:, :, :n_pos] = k.astype(np.int8).reshape(*shape, hd)
-    ref.vq[:, :, :n_pos] = v.astype(np.int8).reshape(*shape, hd)
-    ref.ks[:, :, :n_pos] = a.astype(np.float32).reshape(shape)
-    ref.vs[:, :, :n_pos] = b.astype(np.float32).reshape(shape)
-    ref.pos = n_pos
 
 
 # ----------------------------------------------------------------------------- config 4
@@ -266,7 +234,7 @@ def test_config2_135m_p55454_ctx512_matches_oracle(gpu_ctx, n_layers):
         models.append((model, mats))
     oras = _oracles(cfg, host, n_syn + n_pre + 8, 8)
     for r in oras:
-        _synthetic_kv(r, cfg["n_layers"], cfg["n_kv_heads"], cfg["head_dim"], n_syn, SEED)
+        synthetic_kv(r, cfg["n_layers"], cfg["n_kv_heads"], cfg["head_dim"], n_syn, SEED)
     toks = np.random.default_rng(SEED + 1).integers(0, cfg["vocab"], n_pre + 2).astype(np.int32)
     for model, _ in models:
         model.kv_synthetic(n_syn, seed=SEED)
@@ -347,7 +315,7 @@ def test_config5_moe_full_width_matches_oracle(gpu_ctx):
 
     ref = OracleModel(cfg, layers, hh, fn, embed=embed, parity_threads=THREADS)
     gm.kv_synthetic(n_ctx, seed=SEED)
-    _synthetic_kv(ref, n_layers, nkv, hd, n_ctx, SEED)
+    synthetic_kv(ref, n_layers, nkv, hd, n_ctx, SEED)
     toks = np.random.default_rng(SEED + 6).integers(0, V, 3)
     for i, t in enumerate(toks):
         a, b = gm.decode(int(t)), ref.forward_token(int(t))

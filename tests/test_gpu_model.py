@@ -14,6 +14,7 @@ one; the reference itself has two such orders (NEON vs portable, real_llm.rs:903
 import numpy as np
 import pytest
 
+from helpers import synthetic_kv
 from model_oracle import OracleModel, random_model
 
 pytestmark = pytest.mark.gpu
@@ -114,6 +115,28 @@ def test_gqa_long_context_xcd_order(gpu_ctx, hd):
         a, b = gm.decode(int(t)), ref.forward_token(int(t))
         ok, info = _close(a, b)
         assert ok, info
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_gqa_attention_past_64_spans(gpu_ctx, hd):
+    """The grouped-query kernel's merge polls four spans per thread together (64 spans of
+    128 positions); a context of 8400 positions has 66 spans, so the threads of the first
+    two span subsets also take the one-span-at-a-time path.  K/V filled with the engine's
+    seeded synthetic codes (the oracle gets the same), then decode steps vs the oracle."""
+    print(f"gqa attention past 64 spans hd={hd}", flush=True)
+    n_ctx = 8400
+    cfg = dict(n_layers=1, hidden=8 * hd, n_heads=8, n_kv_heads=2, head_dim=hd, intermediate=256, vocab=200,
+               max_seq=n_ctx + 8, rms_eps=1e-5, rope_theta=10000.0)
+    layers, head, fn = random_model(cfg, seed=21, fmt="nf4")
+    ref = OracleModel(cfg, layers, head, fn)
+    gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
+    gm.kv_synthetic(n_ctx, seed=5)
+    synthetic_kv(ref, 1, 2, hd, n_ctx, 5)
+    for t in np.random.default_rng(22).integers(0, cfg["vocab"], 3):
+        a, b = gm.decode(int(t)), ref.forward_token(int(t))
+        ok, info = _close(a, b)
+        assert ok, info
+
 
 
 @pytest.mark.parametrize("hd,n_tok", [(64, 560), (128, 48)])
