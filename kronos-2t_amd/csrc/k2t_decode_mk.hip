@@ -222,11 +222,33 @@ __device__ __forceinline__ size_t gact_words(const MkParams &P) { return (size_t
 // The copy this workgroup reads (workgroups are dispatched round-robin over the XCDs).
 __device__ __forceinline__ size_t my_copy(const MkParams &P) { return (size_t)(blockIdx.x % (unsigned)P.rep); }
 
+// Norm weights and Hadamard sign mask of this lane's first slice (chunk wave*8 + lane/8,
+// elements (lane%8)*8 .. +8), requested at the start of a phase, before its weight
+// stream and its input wait, so the build after the wait does not wait for them.
+struct NormPre {
+    float4 a, b;
+    uint64_t sign;
+};
+template <int NTH>
+__device__ __forceinline__ NormPre norm_prefetch(const MkParams &P, const float *w, uint32_t lane, int wave) {
+    NormPre r{};
+    const int c = wave * 8 + (int)(lane >> 3), cc = c < P.d / 64 ? c : 0;
+    if (w && wave * 8 < P.d / 64) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(w + cc * 64 + (lane & 7u) * 8);
+        r.a = w4[0];
+        r.b = w4[1];
+        r.sign = P.signs[cc];
+    }
+    return r;
+}
+
 // RMSNorm + FWHT + int8 of S.hbuf[0..d) into the LDS activation: wave 0 computes inv_rms
 // in row_sumsq_wave order (bit-identical to rmsnorm_act_kernel); then eight lanes per
-// chunk, every chunk of the vector at once (rotate_quant_slice8).
+// chunk, every chunk of the vector at once (rotate_quant_slice8).  The first slice of
+// each lane uses the prefetched weights and sign mask.
 template <int NTH>
-__device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, uint32_t lane, int wave) {
+__device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, const NormPre &wp, uint32_t lane,
+                               int wave) {
     if (wave == 0) {
         const float ss = row_sumsq_wave(S.hbuf, P.d, lane);
         if (lane == 0) S.vec[0] = 1.0f / sqrtf(ss / (float)P.d + P.eps);
@@ -235,17 +257,22 @@ __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, 
     const float inv_rms = S.vec[0];
     const uint32_t s8 = lane & 7u;
     const int nc = P.d / 64;
-    for (int c0 = wave * 8; c0 < nc; c0 += NTH / 64 * 8) {
+    auto slice = [&](int c0, const float4 &wa, const float4 &wb, uint64_t sign) {
         const int c = c0 + (int)(lane >> 3);
         const bool act = c < nc;
         const int cc = act ? c : 0;
         const float4 *x4 = reinterpret_cast<const float4 *>(S.hbuf + cc * 64 + s8 * 8);
-        const float4 *w4 = reinterpret_cast<const float4 *>(w + cc * 64 + s8 * 8);
-        const float4 xa = x4[0], xb = x4[1], wa = w4[0], wb = w4[1];
+        const float4 xa = x4[0], xb = x4[1];
         float v[8] = {(xa.x * inv_rms) * wa.x, (xa.y * inv_rms) * wa.y, (xa.z * inv_rms) * wa.z,
                       (xa.w * inv_rms) * wa.w, (xb.x * inv_rms) * wb.x, (xb.y * inv_rms) * wb.y,
                       (xb.z * inv_rms) * wb.z, (xb.w * inv_rms) * wb.w};
-        rotate_quant_slice8(v, P.signs[cc], s8, cc, act, S.xl, S.xsl, S.xsuml);
+        rotate_quant_slice8(v, sign, s8, cc, act, S.xl, S.xsl, S.xsuml);
+    };
+    if (wave * 8 < nc) slice(wave * 8, wp.a, wp.b, wp.sign);
+    for (int c0 = wave * 8 + NTH / 64 * 8; c0 < nc; c0 += NTH / 64 * 8) {
+        const int c = c0 + (int)(lane >> 3), cc = c < nc ? c : 0;
+        const float4 *w4 = reinterpret_cast<const float4 *>(w + cc * 64 + s8 * 8);
+        slice(c0, w4[0], w4[1], P.signs[cc]);
     }
     lds_barrier();
 }
@@ -257,8 +284,9 @@ enum PhaseKind { kQkv = 0, kAttn = 1, kO = 2, kGu = 3, kDown = 4, kHead = 5 };
 // down_proj activation chunks as produced, or RMSNorm + FWHT + int8 of the hidden vector
 // (HA after the embedding or a down phase, HB after an o phase).
 template <int NTH>
-__device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, const float *norm_w, int kind,
-                                              uint32_t epoch, uint32_t lane, int wave, int t0) {
+__device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, const float *norm_w,
+                                              const NormPre &wp, int kind, uint32_t epoch, uint32_t lane, int wave,
+                                              int t0, int trace_l = -1) {
     if (kind == kO || kind == kDown) {
         const int nch = kind == kO ? P.nq * P.hd / 64 : P.inter / 64;
         const unsigned long long *src = kind == kO ? P.OACT + my_copy(P) * oact_words(P)
@@ -268,7 +296,11 @@ __device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, c
     if (!load_words<NTH>(P, S, (kind == kGu ? P.HB : P.HA) + my_copy(P) * (size_t)P.d, P.d, epoch, false, S.hbuf,
                          t0))
         return false;
-    build_norm_act<NTH>(P, S, norm_w, lane, wave);
+#ifdef K2T_MK_TRACE_IN
+    if (P.trace && threadIdx.x == 0 && trace_l >= 0)
+        P.trace[(((size_t)blockIdx.x * (P.L + 1) + trace_l) * 6 + kind) * 6 + 2] = wall_clock64();
+#endif
+    build_norm_act<NTH>(P, S, norm_w, wp, lane, wave);
     return true;
 }
 
@@ -732,6 +764,7 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
         const int nblocks = M.smode ? M.stripes : M.np + (M.stripes & 1);
         const int groups = kWaves / M.nseg;
         if (vb * groups >= nblocks) continue;  // no task here: go on to the next phase
+        const NormPre wpre = norm_prefetch<NTH>(P, kind == kO || kind == kDown ? nullptr : norm_w, lane, wave);
         MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 0);
         // ---- GEMV rounds
         const int grp = wave / M.nseg, wseg = wave % M.nseg;
@@ -747,13 +780,18 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                 GemvWaveLds<FMT, HP, kMkFrags> gw(M, rb, rb < nblocks, wseg, lane, slots);
                 gw.start();
                 if (first) {
-                    if (!mk_load_input<NTH>(P, S, norm_w, kind, E(ph - 1), lane, wave, 0)) return;
+                    if (!mk_load_input<NTH>(P, S, norm_w, wpre, kind, E(ph - 1), lane, wave, 0,
+                                            kind == kHead ? -1 : l))
+                        return;
                     MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 1);
                 }
 #ifdef K2T_MK_TRACE
                 unsigned long long *tr = first && P.trace
                     ? P.trace + (((size_t)blockIdx.x * (P.L + 1) + (kind == kHead ? P.L : l)) * 6 + (kind == kHead ? 0 : kind)) * 6
                     : nullptr;
+#ifdef K2T_MK_TRACE_IN
+                tr = nullptr;
+#endif
                 gw.finish(slots, S.xl, S.xsl, S.xsuml, S.part + wave * 32, tr);
 #else
                 gw.finish(slots, S.xl, S.xsl, S.xsuml, S.part + wave * 32);
