@@ -64,10 +64,18 @@ def _compile(src, objdir=None, defines=()):
 
 
 def check_m0(src):
-    """Sources that stage weights with inline-assembly LDS-DMA loads set M0 themselves
+    """Checks of the generated device assembly.
+
+    M0: sources that stage weights with inline-assembly LDS-DMA loads set M0 themselves
     right before each load.  The compiler does not know of that, so its own code must not
-    use M0: check the generated device assembly (every M0 reference is an s_mov_b32 into
-    M0 directly followed by a global_load_lds)."""
+    use M0 (every M0 reference is an s_mov_b32 into M0 directly followed by a
+    global_load_lds).
+
+    No flat memory instructions: a flat access is issued where the compiler cannot tell
+    whether a pointer addresses LDS or global memory (a pointer taken through an integer,
+    or a select of an LDS and a global pointer).  It counts against both the vector-memory
+    and the LDS counters, so its wait also waits for every global load and store the wave
+    has in flight, the weight prefetches included."""
     asm = os.path.join(OBJ, os.path.basename(src) + ".s")
     cmd = [HIPCC, *[f for f in FLAGS if not f.startswith("-Rpass")], "--cuda-device-only", "-S", src, "-o", asm]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -75,6 +83,9 @@ def check_m0(src):
         raise RuntimeError(f"hipcc -S failed for {src}:\n{r.stderr}")
     lines = [ln.strip() for ln in open(asm) if not ln.lstrip().startswith((";", "."))]
     for i, ln in enumerate(lines):
+        if re.match(r"flat_(load|store|atomic)", ln):
+            raise RuntimeError(f"{src}: flat memory instruction in device code ({ln!r}); state the pointer's "
+                               "address space (ld_global / ld_lds)")
         if re.search(r"\bm0\b", ln):
             ok = (re.fullmatch(r"s_mov_b32 m0, s\d+", ln) is not None and i + 1 < len(lines)
                   and lines[i + 1].startswith("global_load_lds"))

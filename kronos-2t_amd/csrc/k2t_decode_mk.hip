@@ -115,7 +115,12 @@ __device__ Lds carve(const MkParams &P, float *base) {
     p += 128 * 4;
     L.flag = reinterpret_cast<int *>(p);
     p += 16;
-    p = reinterpret_cast<char *>(((uintptr_t)p + 255) & ~(uintptr_t)255);
+    // 256-byte alignment by an offset from the base (the dynamic LDS starts at address 0):
+    // an integer round trip of the pointer would hide from the compiler that it points to
+    // LDS, and every access through it would become a flat access, which waits for the
+    // wave's outstanding global loads as well.
+    const size_t used = (size_t)(p - reinterpret_cast<char *>(base));
+    p = reinterpret_cast<char *>(base) + ((used + 255) & ~(size_t)255);
     L.att = reinterpret_cast<float *>(p);
     L.ring = reinterpret_cast<uint8_t *>(p);
     return L;
@@ -188,32 +193,30 @@ __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, cons
     return S.flag[0] == 0;
 }
 
-// Quantizes the 64 rotated values held one per lane and stores the chunk as kActWords
-// LL words (simd_lut.rs:3097-3128 arithmetic, as quant_chunk_store).
-__device__ void store_act_chunk(float v, uint32_t lane, unsigned long long *dst, uint32_t epoch, int rep = 1,
-                                size_t copy_stride = 0) {
-    const float mx = wave_max_f(fabsf(v));
-    int qi = 0;
-    float scale = 0.0f;
-    if (mx > FLT_EPSILON) {
-        const float inv = 127.0f / mx;
-        qi = (int)rintf(v * inv);
-        scale = mx / 127.0f;
-    }
-    const int s = wave_sum_i(qi);
-    // pack four lanes' codes per word: lane 4w + b -> byte b of word w
-    const uint32_t byte = (uint32_t)qi & 0xFFu;
-    uint32_t word = byte << (8 * (lane & 3u));
-    word |= __shfl_xor(word, 1, kWave);
-    word |= __shfl_xor(word, 2, kWave);
-    for (int r = 0; r < rep; r++) {
-        unsigned long long *d = dst + (size_t)r * copy_stride;
-        if ((lane & 3u) == 0) ll_store(d + lane / 4, word, epoch);
-        if (lane == 0) {
-            ll_store(d + 16, __float_as_uint(scale), epoch);
-            ll_store(d + 17, (uint32_t)s, epoch);
+// Stores a quantized chunk (simd_lut.rs:3097-3128 arithmetic) held in the slice-of-8
+// layout (every 8-lane group holds the whole chunk) as kActWords LL words: word w holds
+// the codes of elements 4w .. 4w+3 (byte b = element 4w+b), word 16 the scale, word 17
+// the code sum.  Lane group g writes copies g, g + 8, ...; lane s of a group writes words
+// 2s and 2s + 1, and its lane 0 words 16 and 17.
+__device__ __forceinline__ void store_act_chunk8(const Chunk8 &r, uint32_t lane, unsigned long long *dst,
+                                                 uint32_t epoch, int rep, size_t copy_stride) {
+    const uint32_t s = lane & 7u;
+    for (int c = (int)(lane >> 3); c < rep; c += 8) {
+        unsigned long long *d = dst + (size_t)c * copy_stride;
+        ll_store(d + 2 * s, r.lo, epoch);
+        ll_store(d + 2 * s + 1, r.hi, epoch);
+        if (s == 0) {
+            ll_store(d + 16, __float_as_uint(r.scale), epoch);
+            ll_store(d + 17, (uint32_t)r.sum, epoch);
         }
     }
+}
+
+// Hadamard sign mask of 64-block `block` (wave-uniform) by a scalar load: the table is
+// read-only, and a vector load here would also wait for the wave's earlier stores.
+__device__ __forceinline__ uint64_t sign_mask_s(const MkParams &P, int block) {
+    using CU64 = const __attribute__((address_space(4))) uint64_t;
+    return ((CU64 *)P.signs)[__builtin_amdgcn_readfirstlane(block)];
 }
 
 // Words per copy of the replicated hand-off vectors.
@@ -379,9 +382,18 @@ __device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t
         if (P.trace && threadIdx.x == 0)                                                           \
             P.trace[(((size_t)blockIdx.x * (P.L + 1) + layer) * 6 + 1) * 6 + (k)] = wall_clock64(); \
     } while (0)
+// second row of attention stamps (the phase-5 slot, unused below the head layer)
+#define ATR2(k)                                                                                     \
+    do {                                                                                            \
+        if (P.trace && threadIdx.x == 0)                                                           \
+            P.trace[(((size_t)blockIdx.x * (P.L + 1) + layer) * 6 + 5) * 6 + (k)] = wall_clock64(); \
+    } while (0)
 #else
 #define ATR(k) \
     do {       \
+    } while (0)
+#define ATR2(k) \
+    do {        \
     } while (0)
 #endif
 
@@ -506,16 +518,16 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
             }
             kscale = kspre;
         } else {
-            const uint4 *kr = tt == pos ? reinterpret_cast<const uint4 *>(kn)
-                                        : reinterpret_cast<const uint4 *>(P.kq + (base + tt) * hd);
+            const uint4 *kr = reinterpret_cast<const uint4 *>(P.kq + (base + tt) * hd);
             for (int i = 0; i < hd / 16; i++) {
-                const uint4 a = kr[i], b = qr[i];
+                const uint4 a = tt == pos ? lds_read16_now(kn + 16 * i) : ld_global(kr + i);
+                const uint4 b = qr[i];
                 dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
                 dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
                 dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
                 dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
             }
-            kscale = tt == pos ? scal[1] : P.ks[base + tt];
+            kscale = tt == pos ? ld_lds(scal + 1) : ld_global(P.ks + base + tt);
         }
         const float s = ((float)dot * kscale) * qas;
         sc[tt - t0] = s;
@@ -560,8 +572,8 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
 #pragma unroll
         for (int u = 0; u < kVB; u++) {
             const int tt = tb + u * nps;
-            vb[u] = tt < pos ? *reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4)
-                             : *reinterpret_cast<const int *>(vn + cg * 4);
+            vb[u] = tt < pos ? ld_global(reinterpret_cast<const int *>(P.vq + (base + tt) * hd + cg * 4))
+                             : ld_lds(reinterpret_cast<const int *>(vn + cg * 4));
         }
 #pragma unroll
         for (int u = 0; u < kVB; u++) {
@@ -598,6 +610,10 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
                 ll_store(dst, __float_as_uint(mm), ep_out);
                 ll_store(dst + 1, __float_as_uint(L), ep_out);
             }
+#ifdef K2T_MK_SWAIT
+            wait_vmcnt<0>();
+            ATR2(0);
+#endif
         } else {
             // merge the other spans' {m, L, o[t]}: all loads in flight, then re-polled
             // together until current (attn_merge_kernel's arithmetic, span order)
@@ -631,6 +647,7 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
                 for (int k = 0; k < 3 * (kSp - 1); k++)
                     if ((pending & (1u << k)) && (uint32_t)(w[k] >> 32) == ep_out) pending &= ~(1u << k);
             }
+            ATR2(1);
             float M = mm;
 #pragma unroll
             for (int s2 = 1; s2 < kSp; s2++)
@@ -654,13 +671,24 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
     lds_barrier();
     if (S.flag[0]) return false;
     if (sp > 0) return true;  // (the scratch reads are done: the barriers above)
+    ATR2(2);
     // 5. ifwht64 per block, then FWHT with the o_proj chunk index + int8 (real_llm.rs:7060-7084)
+    //    Eight elements per lane (slice s = lane % 8; every 8-lane group holds the block):
+    //    three in-register butterfly stages and three lane exchanges per transform.
     if (wave < nb) {
-        const float o = ifwht_lane(qf[wave * 64 + lane], (uint64_t)wave, lane);
+        const uint32_t s8 = lane & 7u;
+        const float4 *o4 = reinterpret_cast<const float4 *>(qf + wave * 64 + s8 * 8);
+        const float4 xa = o4[0], xb = o4[1];
+        float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        butterflies_slice8(v, s8);  // inverse: butterflies, then x0.125 and the block's signs
+        const uint32_t ib = (uint32_t)(sign_mask_s(P, wave) >> (8u * s8)) & 0xFFu;
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = flip_sign(v[j] * 0.125f, (ib >> j) & 1u);
         const int c = h * nb + wave;
-        store_act_chunk(fwht_lane(o, (uint64_t)c, lane), lane, P.OACT + (size_t)c * kActWords, ep_out, P.rep,
-                        oact_words(P));
+        const Chunk8 r = rotate_quant8(v, sign_mask_s(P, c), s8);
+        store_act_chunk8(r, lane, P.OACT + (size_t)c * kActWords, ep_out, P.rep, oact_words(P));
     }
+    ATR2(3);
     // the next GEMV task stages weights into the LDS bytes that hold qf: every wave must
     // be past its last read of the attention scratch first
     lds_barrier();
@@ -832,10 +860,17 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
             if (kind == kGu) {
                 if (wave == 0) {
                     const int ic = base / 4;
+                    // SwiGLU one element per lane (real_llm.rs:9801-9805), then eight
+                    // elements per lane for the rotation (one wave: its LDS accesses are
+                    // performed in program order)
                     const float g = S.vec[lane], u = S.vec[64 + lane];
-                    const float v = (g / (1.0f + expf(-g))) * u;  // real_llm.rs:9801-9805
-                    store_act_chunk(fwht_lane(v, (uint64_t)ic, lane), lane, P.GACT + (size_t)ic * kActWords, E(ph),
-                                    P.rep, gact_words(P));
+                    S.vec[lane] = (g / (1.0f + expf(-g))) * u;
+                    const uint32_t s8 = lane & 7u;
+                    const float4 *v4 = reinterpret_cast<const float4 *>(S.vec + s8 * 8);
+                    const float4 va = v4[0], vb = v4[1];
+                    float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+                    const Chunk8 r = rotate_quant8(v, sign_mask_s(P, ic), s8);
+                    store_act_chunk8(r, lane, P.GACT + (size_t)ic * kActWords, E(ph), P.rep, gact_words(P));
                 }
                 lds_barrier();
             }

@@ -17,6 +17,38 @@ __device__ __forceinline__ uint4 load_stream16(const void *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Loads with the address space stated: where one expression reads either global memory
+// or LDS (a select of the two pointers), the compiler emits a flat access, which waits
+// for the wave's outstanding global operations as well; a load from each side keeps
+// the global load a global load and the LDS read an LDS read.
+// (The host pass of a HIP source also parses these bodies; it has no such address spaces.)
+template <class T>
+__device__ __forceinline__ T ld_global(const T *p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *(const __attribute__((address_space(1))) T *)p;
+#else
+    return *p;
+#endif
+}
+template <class T>
+__device__ __forceinline__ T ld_lds(const T *p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *(const __attribute__((address_space(3))) T *)p;
+#else
+    return *p;
+#endif
+}
+
+// 16 bytes from LDS, waited for, by inline assembly: for a read that sits on one side
+// of a branch whose other side loads the same shape from global memory (the compiler
+// would otherwise merge the two into one flat load through a select of the pointers).
+__device__ __forceinline__ uint4 lds_read16_now(const void *p) {
+    uint4 r;
+    const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(a) : "memory");
+    return r;
+}
+
 // Direct-to-LDS loads (global_load_lds): lane L's bytes land at M0 + size * L.  Issued
 // from inline assembly, so the compiler neither tracks them nor inserts its conservative
 // "all vector memory done" wait before later LDS reads; callers order them through the
@@ -73,10 +105,10 @@ __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(
 
 // Exchange with lane ^ 1, ^ 2 (DPP quad permutes) and ^ 4 (ds_swizzle bit mode).
 __device__ __forceinline__ float xchg1(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float xchg2(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float xchg4(float v) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));
@@ -272,18 +304,12 @@ __device__ __forceinline__ float ifwht_lane(float v, uint64_t block, uint32_t la
     return flip_sign(v * 0.125f, hadamard_sign_bit(block, lane));
 }
 
-// Signed FWHT-64 + int8 quantization of one 64-element chunk held as eight consecutive
-// elements per lane by eight lanes (lane bits 0-2 = s, element s*8 + j): sign flip with
-// the chunk's mask bits, x0.125, butterflies h = 1, 2, 4 in registers and h = 8, 16, 32
-// across lanes (^1, ^2, ^4), then max, int8 round-half-even, scale = max/127 and the code
-// sum.  Each butterfly adds or subtracts the same operands as hadamard.rs:83-97, so the
-// result equals fwht_lane + quant_chunk_store.  All 64 lanes must call it; `act` only
-// gates the stores (codes at xl[c*64 + s*8], scale xsl[c], sum xsuml[c]).
-__device__ __forceinline__ void rotate_quant_slice8(float *v, uint64_t sign_mask, uint32_t s, int c, bool act,
-                                                    int8_t *xl, float *xsl, int32_t *xsuml) {
-    const uint32_t sb = (uint32_t)(sign_mask >> (8u * s)) & 0xFFu;
-#pragma unroll
-    for (int j = 0; j < 8; j++) v[j] = flip_sign(v[j], (sb >> j) & 1u) * 0.125f;
+// Butterflies h = 1..32 of one 64-element block held as eight consecutive elements per
+// lane by eight lanes (lane bits 0-2 = s, element s*8 + j): h = 1, 2, 4 in registers and
+// h = 8, 16, 32 across lanes (^1, ^2, ^4).  Each stage adds or subtracts the same operands
+// as hadamard.rs:83-97 (lower a+b, upper a-b), in the same stage order as
+// wave_butterflies64, so the results are bit-identical to it.
+__device__ __forceinline__ void butterflies_slice8(float *v, uint32_t s) {
 #pragma unroll
     for (int h = 1; h < 8; h <<= 1)
 #pragma unroll
@@ -293,41 +319,70 @@ __device__ __forceinline__ void rotate_quant_slice8(float *v, uint64_t sign_mask
                 v[j] = x0 + x1;
                 v[j | h] = x0 - x1;
             }
+    // across lanes: lower lane v + p, upper lane p - v, both as p + (+-v) (IEEE addition
+    // commutes and a - b is a + (-b), so the bits are those of the two-sided form)
 #pragma unroll
     for (int m = 1; m < 8; m <<= 1) {
-        const bool upper = (s & (uint32_t)m) != 0;
+        const uint32_t neg = (s & (uint32_t)m) != 0 ? 0x80000000u : 0u;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const float p = m == 1 ? xchg1(v[j]) : m == 2 ? xchg2(v[j]) : xchg4(v[j]);
-            v[j] = upper ? p - v[j] : v[j] + p;
+            v[j] = p + __uint_as_float(__float_as_uint(v[j]) ^ neg);
         }
     }
+}
+
+// One quantized 64-element chunk as eight lanes hold it: codes of elements s*8 .. s*8+3
+// (lo) and s*8+4 .. s*8+7 (hi), one byte each; scale and code sum (same in every lane).
+struct Chunk8 {
+    uint32_t lo, hi;
+    float scale;
+    int sum;
+};
+
+// Signed FWHT-64 + int8 quantization of one chunk in the slice-of-8 layout: sign flip
+// with the chunk's mask bits, x0.125, butterflies_slice8, then max, int8 round-half-even,
+// scale = max/127 and the code sum (simd_lut.rs:3097-3128 / 3172-3195).  The result
+// equals fwht_lane + quant_chunk_store.  All 64 lanes must call it.
+__device__ __forceinline__ Chunk8 rotate_quant8(float *v, uint64_t sign_mask, uint32_t s) {
+    const uint32_t sb = (uint32_t)(sign_mask >> (8u * s)) & 0xFFu;
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = flip_sign(v[j], (sb >> j) & 1u) * 0.125f;
+    butterflies_slice8(v, s);
     float mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
     mx = fmaxf(mx, xchg1(mx));
     mx = fmaxf(mx, xchg2(mx));
     mx = fmaxf(mx, xchg4(mx));
-    uint32_t lo = 0, hi = 0;
-    int sum = 0;
+    Chunk8 r{0u, 0u, 0.0f, 0};
     if (mx > FLT_EPSILON) {
         const float inv = 127.0f / mx;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int qi = (int)rintf(v[j] * inv);
-            sum += qi;
-            if (j < 4) lo |= ((uint32_t)qi & 0xFFu) << (8 * j);
-            else hi |= ((uint32_t)qi & 0xFFu) << (8 * (j - 4));
+            r.sum += qi;
+            if (j < 4) r.lo |= ((uint32_t)qi & 0xFFu) << (8 * j);
+            else r.hi |= ((uint32_t)qi & 0xFFu) << (8 * (j - 4));
         }
+        r.scale = mx / 127.0f;
     }
-    sum += xchg1(sum);
-    sum += xchg2(sum);
-    sum += xchg4(sum);
+    r.sum += xchg1(r.sum);
+    r.sum += xchg2(r.sum);
+    r.sum += xchg4(r.sum);
+    return r;
+}
+
+// rotate_quant8 into the LDS activation: `act` gates the stores (codes at
+// xl[c*64 + s*8], scale xsl[c], sum xsuml[c]).
+__device__ __forceinline__ void rotate_quant_slice8(float *v, uint64_t sign_mask, uint32_t s, int c, bool act,
+                                                    int8_t *xl, float *xsl, int32_t *xsuml) {
+    const Chunk8 r = rotate_quant8(v, sign_mask, s);
     if (act) {
-        *reinterpret_cast<uint2 *>(xl + c * 64 + s * 8) = make_uint2(lo, hi);
+        *reinterpret_cast<uint2 *>(xl + c * 64 + s * 8) = make_uint2(r.lo, r.hi);
         if (s == 0) {
-            xsl[c] = mx > FLT_EPSILON ? mx / 127.0f : 0.0f;
-            xsuml[c] = sum;
+            xsl[c] = r.scale;
+            xsuml[c] = r.sum;
         }
     }
 }

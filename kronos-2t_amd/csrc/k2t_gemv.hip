@@ -333,7 +333,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         const int z = (int)blockIdx.z;
         const uint8_t *rec = P.bank + (size_t)P.route[z] * P.bank_stride;
         pair_p = rec + P.mat_off;
-        const uint4 cbw = *reinterpret_cast<const uint4 *>(rec + P.cb_off);
+        const uint4 cbw = ld_global(reinterpret_cast<const uint4 *>(rec + P.cb_off));
         cb0 = cbw.x;
         cb1 = cbw.y;
         cb2 = cbw.z;

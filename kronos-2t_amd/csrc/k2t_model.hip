@@ -364,10 +364,10 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
             // dot of the codebook values with q, total += float(dot) * ks_g * qs
             const bool here = covers && t == cur;
             const size_t sl = base + slot_of(t);
-            const uint8_t *k4 = here ? reinterpret_cast<const uint8_t *>(kcur)
-                                     : reinterpret_cast<const uint8_t *>(kq) + sl * (size_t)(hd / 2);
-            const uint16_t *k16 = here ? reinterpret_cast<const uint16_t *>(cur_s)
-                                       : reinterpret_cast<const uint16_t *>(ks) + sl * (size_t)nb;
+            // (the current position from LDS, the others from the cache: each read states
+            // its memory, so no select of the two pointers becomes a flat access)
+            const uint8_t *k4 = reinterpret_cast<const uint8_t *>(kq) + sl * (size_t)(hd / 2);
+            const uint16_t *k16 = reinterpret_cast<const uint16_t *>(ks) + sl * (size_t)nb;
             float s = 0.0f;
             for (int g = 0; g < nb; g++) {
                 const uint4 *kp = reinterpret_cast<const uint4 *>(k4 + g * 32);
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
                 int dot = 0;
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const uint4 a = kp[h];
+                    const uint4 a = here ? lds_read16_now(kcur + g * 32 + h * 16) : ld_global(kp + h);
                     const uint32_t w4[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
@@ -387,7 +387,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
                         dot = __builtin_amdgcn_sdot4((int)hi, (int)qw[h * 8 + 4 + j], dot, false);
                     }
                 }
-                s += ((float)dot * __uint_as_float((uint32_t)k16[g] << 16)) * qas;
+                const uint16_t kb = here ? ld_lds(reinterpret_cast<const uint16_t *>(cur_s) + g) : ld_global(k16 + g);
+                s += ((float)dot * __uint_as_float((uint32_t)kb << 16)) * qas;
             }
             vscale = 1.0f;  // the V scales are per 64-block: applied in the V sum
             sc[tid] = s;
@@ -395,11 +396,11 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
         } else if (t < t1) {
             const bool here = covers && t == cur;
             const size_t sl = base + slot_of(t);
-            const uint4 *krow = here ? reinterpret_cast<const uint4 *>(kcur) : reinterpret_cast<const uint4 *>(kq + sl * hd);
+            const uint4 *krow = reinterpret_cast<const uint4 *>(kq + sl * hd);
             const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
             int dot[2] = {0, 0};
             for (int i = 0; i < hd / 16; i++) {
-                const uint4 a = krow[i], b = qr[i];
+                const uint4 a = here ? lds_read16_now(kcur + 16 * i) : ld_global(krow + i), b = qr[i];
                 int d = dot[i >> 2];
                 d = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, d, false);
                 d = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, d, false);
@@ -407,8 +408,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
                 d = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, d, false);
                 dot[i >> 2] = d;
             }
-            const float kscale = here ? cur_s[0] : ks[sl];
-            vscale = here ? cur_s[2] : vs[sl];
+            const float kscale = here ? ld_lds(cur_s) : ld_global(ks + sl);
+            vscale = here ? ld_lds(cur_s + 2) : ld_global(vs + sl);
             float s;
             if (kr.window > 0 && hd == 128)  // per-64-block terms (causal_gqa_group_q4_or_window, 8823-8868)
                 s = ((float)dot[0] * kscale) * qas + ((float)dot[1] * kscale) * qas;
@@ -451,11 +452,11 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
         for (; i < n; i += nps) {
             const bool here = covers && t0 + i == cur;
             const size_t sl = slot_of(t0 + i);
-            const uint32_t d = here ? *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint8_t *>(vcur) + off)
-                                    : *reinterpret_cast<const uint32_t *>(v4 + sl * (size_t)(hd / 2));
+            const uint32_t d = here ? ld_lds(reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint8_t *>(vcur) + off))
+                                    : ld_global(reinterpret_cast<const uint32_t *>(v4 + sl * (size_t)(hd / 2)));
             const uint32_t c = upper ? lut16((d >> 4) & 0x07070707u, bit7_mask(d), kNf4Cb0, kNf4Cb1, kNf4Cb2, kNf4Cb3)
                                      : lut16(d & 0x07070707u, bit3_mask(d), kNf4Cb0, kNf4Cb1, kNf4Cb2, kNf4Cb3);
-            const uint16_t vsb = here ? reinterpret_cast<const uint16_t *>(cur_s + 2)[g] : v16[sl * (size_t)nb];
+            const uint16_t vsb = here ? ld_lds(reinterpret_cast<const uint16_t *>(cur_s + 2) + g) : ld_global(v16 + sl * (size_t)nb);
             const float wt = sc[i] * __uint_as_float((uint32_t)vsb << 16);
             a0 = fmaf(wt, (float)(int8_t)(c & 0xFF), a0);
             a1 = fmaf(wt, (float)(int8_t)((c >> 8) & 0xFF), a1);
@@ -473,8 +474,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
 #pragma unroll
         for (int u = 0; u < kVB; u++) {
             const int idx = t0 + i + u * nps;
-            vv[u] = covers && idx == cur ? *reinterpret_cast<const int *>(vcur + cg * 4)
-                                         : *reinterpret_cast<const int *>(vcol + slot_of(idx) * hd);
+            vv[u] = covers && idx == cur ? ld_lds(reinterpret_cast<const int *>(vcur + cg * 4))
+                                         : ld_global(reinterpret_cast<const int *>(vcol + slot_of(idx) * hd));
             ww[u] = sc[i + u * nps];
         }
 #pragma unroll
@@ -486,8 +487,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
         }
     }
     for (; kr.bits != 4 && i < n; i += nps) {
-        const int v = covers && t0 + i == cur ? *reinterpret_cast<const int *>(vcur + cg * 4)
-                                              : *reinterpret_cast<const int *>(vcol + slot_of(t0 + i) * hd);
+        const int v = covers && t0 + i == cur ? ld_lds(reinterpret_cast<const int *>(vcur + cg * 4))
+                                              : ld_global(reinterpret_cast<const int *>(vcol + slot_of(t0 + i) * hd));
         const float wt = sc[i];
         a0 = fmaf(wt, (float)(int8_t)(v & 0xFF), a0);
         a1 = fmaf(wt, (float)(int8_t)((v >> 8) & 0xFF), a1);
