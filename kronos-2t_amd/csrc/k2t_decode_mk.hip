@@ -798,9 +798,25 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
         const int grp = wave / M.nseg, wseg = wave % M.nseg;
         const int RB = M.smode ? 16 : 32;
         bool ok = true;
+        // the output row of thread t in the epilogue of the round at `base` (-1: none)
+        auto out_row = [&](int base) {
+            if (t >= groups * RB) return -1;
+            const int g2 = t / RB, rl = t % RB, rb2 = xcd_stripe<kWaves>(M, base + g2, nblocks);
+            if (rb2 >= nblocks) return -1;
+            const bool tail = !M.smode && rb2 >= M.np;
+            const int first_stripe = M.smode ? rb2 : (tail ? 2 * M.np : 2 * rb2);
+            const int row = first_stripe * 16 + rl;
+            return rl < (tail ? 16 : RB) && row < M.rows ? row : -1;
+        };
+        // residual of the o / down epilogue: HB = HA + o (HA from phase ph-3), HA = HB + down
+        // (HB from ph-2)
+        const unsigned long long *res = (kind == kO ? P.HA : P.HB) + my_copy(P) * (size_t)d;
+        const uint32_t er = kind == kO ? E(ph - 3) : E(ph - 2);
         for (int base = vb * groups; base < nblocks; base += nwg * groups) {
             const int rb = xcd_stripe<kWaves>(M, base + grp, nblocks);
             const bool first = base == vb * groups;
+            const int orow = out_row(base);
+            unsigned long long rpre = 0;
             // The whole of this wave's share (up to kMkFrags fragments) streams into its
             // LDS slots before the input wait; the compute then reads LDS only.
             {
@@ -813,6 +829,10 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                         return;
                     MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 1);
                 }
+                // The residual word was written phases ago (the input's producers waited
+                // for it): request it now, so it lands during the compute.  The compute
+                // reads only LDS (no flat accesses), so nothing waits for this load early.
+                if ((kind == kO || kind == kDown) && orow >= 0) rpre = ll_load(res + orow);
 #ifdef K2T_MK_TRACE
                 unsigned long long *tr = first && P.trace
                     ? P.trace + (((size_t)blockIdx.x * (P.L + 1) + (kind == kHead ? P.L : l)) * 6 + (kind == kHead ? 0 : kind)) * 6
@@ -827,33 +847,23 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
             }
             lds_barrier();
             if (first) MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 4);
-            if (t < groups * RB) {
-                const int g2 = t / RB, rl = t % RB, rb2 = xcd_stripe<kWaves>(M, base + g2, nblocks);
-                if (rb2 < nblocks) {
-                    const bool tail = !M.smode && rb2 >= M.np;
-                    const int first_stripe = M.smode ? rb2 : (tail ? 2 * M.np : 2 * rb2);
-                    const int row = first_stripe * 16 + rl;
-                    if (rl < (tail ? 16 : RB) && row < M.rows) {
-                        const float *gp = S.part + (g2 * M.nseg) * 32;
-                        float acc = gp[rl];
-                        for (int w2 = 1; w2 < M.nseg; w2++) acc += gp[w2 * 32 + rl];
-                        if (kind == kHead) {
-                            P.logits[row] = acc;
-                        } else if (kind == kQkv) {
-                            ll_store(P.QKV + row, __float_as_uint(acc), E(ph));
-                        } else if (kind == kGu) {
-                            S.vec[t] = acc;  // the 4 groups = the 4 pairs of block ic
-                        } else {
-                            // residual: HB = HA + o (HA from phase ph-3), HA = HB + down (HB from ph-2)
-                            const unsigned long long *res = (kind == kO ? P.HA : P.HB) + my_copy(P) * (size_t)d;
-                            const uint32_t er = kind == kO ? E(ph - 3) : E(ph - 2);
-                            uint32_t hv = 0;
-                            if (ok && !ll_wait(P, res + row, er, hv)) ok = false;
-                            const uint32_t nv = __float_as_uint(__uint_as_float(hv) + acc);
-                            for (int r = 0; r < P.rep; r++)
-                                ll_store((kind == kO ? P.HB : P.HA) + (size_t)r * d + row, nv, E(ph));
-                        }
-                    }
+            if (orow >= 0) {
+                const int g2 = t / RB, rl = t % RB, row = orow;
+                const float *gp = S.part + (g2 * M.nseg) * 32;
+                float acc = gp[rl];
+                for (int w2 = 1; w2 < M.nseg; w2++) acc += gp[w2 * 32 + rl];
+                if (kind == kHead) {
+                    P.logits[row] = acc;
+                } else if (kind == kQkv) {
+                    ll_store(P.QKV + row, __float_as_uint(acc), E(ph));
+                } else if (kind == kGu) {
+                    S.vec[t] = acc;  // the 4 groups = the 4 pairs of block ic
+                } else {
+                    uint32_t hv = (uint32_t)rpre;
+                    if ((uint32_t)(rpre >> 32) != er && ok && !ll_wait(P, res + row, er, hv)) ok = false;
+                    const uint32_t nv = __float_as_uint(__uint_as_float(hv) + acc);
+                    for (int r = 0; r < P.rep; r++)
+                        ll_store((kind == kO ? P.HB : P.HA) + (size_t)r * d + row, nv, E(ph));
                 }
             }
             lds_barrier();
