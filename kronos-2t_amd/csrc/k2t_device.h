@@ -321,14 +321,16 @@ __device__ __forceinline__ void butterflies_slice8(float *v, uint32_t s) {
             }
     // across lanes: lower lane v + p, upper lane p - v, both as p + (+-v) (IEEE addition
     // commutes and a - b is a + (-b), so the bits are those of the two-sided form)
+    // (all eight exchanges of a stage are issued before the first add: the ^4 exchange
+    // is an LDS round trip, and eight of them back to back share one wait)
 #pragma unroll
     for (int m = 1; m < 8; m <<= 1) {
         const uint32_t neg = (s & (uint32_t)m) != 0 ? 0x80000000u : 0u;
+        float p[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float p = m == 1 ? xchg1(v[j]) : m == 2 ? xchg2(v[j]) : xchg4(v[j]);
-            v[j] = p + __uint_as_float(__float_as_uint(v[j]) ^ neg);
-        }
+        for (int j = 0; j < 8; j++) p[j] = m == 1 ? xchg1(v[j]) : m == 2 ? xchg2(v[j]) : xchg4(v[j]);
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = p[j] + __uint_as_float(__float_as_uint(v[j]) ^ neg);
     }
 }
 
