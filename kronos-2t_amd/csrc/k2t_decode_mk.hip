@@ -193,30 +193,29 @@ __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, cons
     return S.flag[0] == 0;
 }
 
-// Stores a quantized chunk (simd_lut.rs:3097-3128 arithmetic) held in the slice-of-8
-// layout (every 8-lane group holds the whole chunk) as kActWords LL words: word w holds
-// the codes of elements 4w .. 4w+3 (byte b = element 4w+b), word 16 the scale, word 17
-// the code sum.  Lane group g writes copies g, g + 8, ...; lane s of a group writes words
-// 2s and 2s + 1, and its lane 0 words 16 and 17.
-__device__ __forceinline__ void store_act_chunk8(const Chunk8 &r, uint32_t lane, unsigned long long *dst,
-                                                 uint32_t epoch, int rep, size_t copy_stride) {
-    const uint32_t s = lane & 7u;
-    for (int c = (int)(lane >> 3); c < rep; c += 8) {
-        unsigned long long *d = dst + (size_t)c * copy_stride;
-        ll_store(d + 2 * s, r.lo, epoch);
-        ll_store(d + 2 * s + 1, r.hi, epoch);
-        if (s == 0) {
-            ll_store(d + 16, __float_as_uint(r.scale), epoch);
-            ll_store(d + 17, (uint32_t)r.sum, epoch);
-        }
-    }
-}
-
 // Hadamard sign mask of 64-block `block` (wave-uniform) by a scalar load: the table is
 // read-only, and a vector load here would also wait for the wave's earlier stores.
 __device__ __forceinline__ uint64_t sign_mask_s(const MkParams &P, int block) {
     using CU64 = const __attribute__((address_space(4))) uint64_t;
     return ((CU64 *)P.signs)[__builtin_amdgcn_readfirstlane(block)];
+}
+
+// Stores a quantized chunk (simd_lut.rs:3097-3128 arithmetic) held in the four-element
+// layout (every 16-lane group holds the whole chunk) as kActWords LL words: word w holds
+// the codes of elements 4w .. 4w+3 (byte b = element 4w+b), word 16 the scale, word 17
+// the code sum.  Lane group g (lane / 16) writes copies g, g + 4, ...; lane s of a group
+// writes word s, and its lane 0 words 16 and 17.
+__device__ __forceinline__ void store_act_chunk4(const Chunk4 &r, uint32_t lane, unsigned long long *dst,
+                                                 uint32_t epoch, int rep, size_t copy_stride) {
+    const uint32_t s = lane & 15u;
+    for (int c = (int)(lane >> 4); c < rep; c += 4) {
+        unsigned long long *d = dst + (size_t)c * copy_stride;
+        ll_store(d + s, r.w, epoch);
+        if (s == 0) {
+            ll_store(d + 16, __float_as_uint(r.scale), epoch);
+            ll_store(d + 17, (uint32_t)r.sum, epoch);
+        }
+    }
 }
 
 // Words per copy of the replicated hand-off vectors.
@@ -353,9 +352,11 @@ __device__ float embed_value(const MatDev &M, int r, int c, uint32_t lane) {
 
 // Rotates one head (hd = 64 or 128, one or two blocks held as v0/v1 per lane) and
 // quantizes it with one scale (store_hadamard_q8_head, real_llm.rs:8282-8365).
-__device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t lane, int8_t *dst) {
-    const float r0 = fwht_lane(v0, 0, lane);
-    const float r1 = nb > 1 ? fwht_lane(v1, 1, lane) : 0.0f;
+__device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t lane, int8_t *dst,
+                                            uint64_t sm0, uint64_t sm1) {
+    // fwht_lane with the blocks' sign bits from the sign-mask table
+    const float r0 = wave_butterflies64(flip_sign(v0, (uint32_t)(sm0 >> lane) & 1u) * 0.125f, lane);
+    const float r1 = nb > 1 ? wave_butterflies64(flip_sign(v1, (uint32_t)(sm1 >> lane) & 1u) * 0.125f, lane) : 0.0f;
     const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
     if (mx <= FLT_EPSILON) {
         dst[lane] = 0;
@@ -481,7 +482,7 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
             x1 = a1 * c + a0 * sn;
         }
         int8_t *dst = wave == 0 ? qi : kn;
-        const float sc8 = quant_head(x0, x1, nb, lane, dst);
+        const float sc8 = quant_head(x0, x1, nb, lane, dst, sign_mask_s(P, 0), sign_mask_s(P, 1));
         if (lane == 0) scal[wave] = wave == 0 ? sc8 * P.attn_scale : sc8;
         if (wave == 1 && h % group == 0) {  // the first q head of the group stores this position's K
             P.kq[slot * hd + lane] = kn[lane];
@@ -489,7 +490,8 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
             if (lane == 0) P.ks[slot] = sc8;
         }
     } else if (cover && wave == 2) {
-        const float vsn = quant_head(vf[lane], nb > 1 ? vf[64 + lane] : 0.0f, nb, lane, vn);
+        const float vsn = quant_head(vf[lane], nb > 1 ? vf[64 + lane] : 0.0f, nb, lane, vn, sign_mask_s(P, 0),
+                                     sign_mask_s(P, 1));
         if (lane == 0) scal[2] = vsn;
         if (h % group == 0) {
             P.vq[slot * hd + lane] = vn[lane];
@@ -673,20 +675,19 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
     if (sp > 0) return true;  // (the scratch reads are done: the barriers above)
     ATR2(2);
     // 5. ifwht64 per block, then FWHT with the o_proj chunk index + int8 (real_llm.rs:7060-7084)
-    //    Eight elements per lane (slice s = lane % 8; every 8-lane group holds the block):
-    //    three in-register butterfly stages and three lane exchanges per transform.
+    //    Four elements per lane (slice s = lane % 16; every 16-lane group holds the block):
+    //    two in-register butterfly stages and four lane exchanges per transform.
     if (wave < nb) {
-        const uint32_t s8 = lane & 7u;
-        const float4 *o4 = reinterpret_cast<const float4 *>(qf + wave * 64 + s8 * 8);
-        const float4 xa = o4[0], xb = o4[1];
-        float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-        butterflies_slice8(v, s8);  // inverse: butterflies, then x0.125 and the block's signs
-        const uint32_t ib = (uint32_t)(sign_mask_s(P, wave) >> (8u * s8)) & 0xFFu;
+        const uint32_t s4 = lane & 15u;
+        const float4 o4 = *reinterpret_cast<const float4 *>(qf + wave * 64 + s4 * 4);
+        float v[4] = {o4.x, o4.y, o4.z, o4.w};
+        butterflies_slice4(v, s4);  // inverse: butterflies, then x0.125 and the block's signs
+        const uint32_t ib = (uint32_t)(sign_mask_s(P, wave) >> (4u * s4)) & 0xFu;
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = flip_sign(v[j] * 0.125f, (ib >> j) & 1u);
+        for (int j = 0; j < 4; j++) v[j] = flip_sign(v[j] * 0.125f, (ib >> j) & 1u);
         const int c = h * nb + wave;
-        const Chunk8 r = rotate_quant8(v, sign_mask_s(P, c), s8);
-        store_act_chunk8(r, lane, P.OACT + (size_t)c * kActWords, ep_out, P.rep, oact_words(P));
+        const Chunk4 r = rotate_quant4(v, sign_mask_s(P, c), s4);
+        store_act_chunk4(r, lane, P.OACT + (size_t)c * kActWords, ep_out, P.rep, oact_words(P));
     }
     ATR2(3);
     // the next GEMV task stages weights into the LDS bytes that hold qf: every wave must
@@ -870,17 +871,16 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
             if (kind == kGu) {
                 if (wave == 0) {
                     const int ic = base / 4;
-                    // SwiGLU one element per lane (real_llm.rs:9801-9805), then eight
+                    // SwiGLU one element per lane (real_llm.rs:9801-9805), then four
                     // elements per lane for the rotation (one wave: its LDS accesses are
                     // performed in program order)
                     const float g = S.vec[lane], u = S.vec[64 + lane];
                     S.vec[lane] = (g / (1.0f + expf(-g))) * u;
-                    const uint32_t s8 = lane & 7u;
-                    const float4 *v4 = reinterpret_cast<const float4 *>(S.vec + s8 * 8);
-                    const float4 va = v4[0], vb = v4[1];
-                    float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
-                    const Chunk8 r = rotate_quant8(v, sign_mask_s(P, ic), s8);
-                    store_act_chunk8(r, lane, P.GACT + (size_t)ic * kActWords, E(ph), P.rep, gact_words(P));
+                    const uint32_t s4 = lane & 15u;
+                    const float4 va = *reinterpret_cast<const float4 *>(S.vec + s4 * 4);
+                    float v[4] = {va.x, va.y, va.z, va.w};
+                    const Chunk4 r = rotate_quant4(v, sign_mask_s(P, ic), s4);
+                    store_act_chunk4(r, lane, P.GACT + (size_t)ic * kActWords, E(ph), P.rep, gact_words(P));
                 }
                 lds_barrier();
             }

@@ -375,6 +375,75 @@ __device__ __forceinline__ Chunk8 rotate_quant8(float *v, uint64_t sign_mask, ui
     return r;
 }
 
+// The same butterflies with four consecutive elements per lane by sixteen lanes (lane
+// bits 0-3 = s, element s*4 + j): h = 1, 2 in registers, h = 4 .. 32 across lanes (^1, ^2,
+// ^4 by ds_swizzle, ^8 by the DPP row rotate).  For a single chunk per wave this layout
+// needs about half the instructions of the eight-element one and still one LDS round
+// trip per transform.
+__device__ __forceinline__ float xchg8(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
+}
+__device__ __forceinline__ int xchg8(int v) { return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false); }
+__device__ __forceinline__ void butterflies_slice4(float *v, uint32_t s) {
+#pragma unroll
+    for (int h = 1; h < 4; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (!(j & h)) {
+                const float x0 = v[j], x1 = v[j | h];
+                v[j] = x0 + x1;
+                v[j | h] = x0 - x1;
+            }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+        const uint32_t neg = (s & (uint32_t)m) != 0 ? 0x80000000u : 0u;
+        float p[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            p[j] = m == 1 ? xchg1(v[j]) : m == 2 ? xchg2(v[j]) : m == 4 ? xchg4(v[j]) : xchg8(v[j]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = p[j] + __uint_as_float(__float_as_uint(v[j]) ^ neg);
+    }
+}
+
+// One quantized chunk as sixteen lanes hold it: the codes of elements s*4 .. s*4+3 (one
+// byte each, element s*4 + b in byte b), the scale and the code sum.
+struct Chunk4 {
+    uint32_t w;
+    float scale;
+    int sum;
+};
+
+// rotate_quant8's arithmetic in the four-element layout.
+__device__ __forceinline__ Chunk4 rotate_quant4(float *v, uint64_t sign_mask, uint32_t s) {
+    const uint32_t sb = (uint32_t)(sign_mask >> (4u * s)) & 0xFu;
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = flip_sign(v[j], (sb >> j) & 1u) * 0.125f;
+    butterflies_slice4(v, s);
+    float mx = fmaxf(fmaxf(0.0f, fabsf(v[0])), fabsf(v[1]));
+    mx = fmaxf(fmaxf(mx, fabsf(v[2])), fabsf(v[3]));
+    mx = fmaxf(mx, xchg1(mx));
+    mx = fmaxf(mx, xchg2(mx));
+    mx = fmaxf(mx, xchg4(mx));
+    mx = fmaxf(mx, xchg8(mx));
+    Chunk4 r{0u, 0.0f, 0};
+    if (mx > FLT_EPSILON) {
+        const float inv = 127.0f / mx;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int qi = (int)rintf(v[j] * inv);
+            r.sum += qi;
+            r.w |= ((uint32_t)qi & 0xFFu) << (8 * j);
+        }
+        r.scale = mx / 127.0f;
+    }
+    r.sum += xchg1(r.sum);
+    r.sum += xchg2(r.sum);
+    r.sum += xchg4(r.sum);
+    r.sum += xchg8(r.sum);
+    return r;
+}
+
 // rotate_quant8 into the LDS activation: `act` gates the stores (codes at
 // xl[c*64 + s*8], scale xsl[c], sum xsuml[c]).
 __device__ __forceinline__ void rotate_quant_slice8(float *v, uint64_t sign_mask, uint32_t s, int c, bool act,
