@@ -224,30 +224,28 @@ __device__ __forceinline__ size_t gact_words(const MkParams &P) { return (size_t
 // The copy this workgroup reads (workgroups are dispatched round-robin over the XCDs).
 __device__ __forceinline__ size_t my_copy(const MkParams &P) { return (size_t)(blockIdx.x % (unsigned)P.rep); }
 
-// Norm weights and Hadamard sign mask of this lane's first slice (chunk wave*8 + lane/8,
-// elements (lane%8)*8 .. +8), requested at the start of a phase, before its weight
+// Norm weights and Hadamard sign mask of this lane's first slice (chunk wave*4 + lane/16,
+// elements (lane%16)*4 .. +4), requested at the start of a phase, before its weight
 // stream and its input wait, so the build after the wait does not wait for them.
 struct NormPre {
-    float4 a, b;
+    float4 a;
     uint64_t sign;
 };
 template <int NTH>
 __device__ __forceinline__ NormPre norm_prefetch(const MkParams &P, const float *w, uint32_t lane, int wave) {
     NormPre r{};
-    const int c = wave * 8 + (int)(lane >> 3), cc = c < P.d / 64 ? c : 0;
-    if (w && wave * 8 < P.d / 64) {
-        const float4 *w4 = reinterpret_cast<const float4 *>(w + cc * 64 + (lane & 7u) * 8);
-        r.a = w4[0];
-        r.b = w4[1];
+    const int c = wave * 4 + (int)(lane >> 4), cc = c < P.d / 64 ? c : 0;
+    if (w && wave * 4 < P.d / 64) {
+        r.a = *reinterpret_cast<const float4 *>(w + cc * 64 + (lane & 15u) * 4);
         r.sign = P.signs[cc];
     }
     return r;
 }
 
 // RMSNorm + FWHT + int8 of S.hbuf[0..d) into the LDS activation: wave 0 computes inv_rms
-// in row_sumsq_wave order (bit-identical to rmsnorm_act_kernel); then eight lanes per
-// chunk, every chunk of the vector at once (rotate_quant_slice8).  The first slice of
-// each lane uses the prefetched weights and sign mask.
+// in row_sumsq_wave order (bit-identical to rmsnorm_act_kernel); then sixteen lanes per
+// chunk, four chunks per wave at once (rotate_quant4).  The first slice of each lane uses
+// the prefetched weights and sign mask.
 template <int NTH>
 __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, const NormPre &wp, uint32_t lane,
                                int wave) {
@@ -257,24 +255,27 @@ __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, 
     }
     lds_barrier();
     const float inv_rms = S.vec[0];
-    const uint32_t s8 = lane & 7u;
+    const uint32_t s4 = lane & 15u;
     const int nc = P.d / 64;
-    auto slice = [&](int c0, const float4 &wa, const float4 &wb, uint64_t sign) {
-        const int c = c0 + (int)(lane >> 3);
+    auto slice = [&](int c0, const float4 &wa, uint64_t sign) {
+        const int c = c0 + (int)(lane >> 4);
         const bool act = c < nc;
         const int cc = act ? c : 0;
-        const float4 *x4 = reinterpret_cast<const float4 *>(S.hbuf + cc * 64 + s8 * 8);
-        const float4 xa = x4[0], xb = x4[1];
-        float v[8] = {(xa.x * inv_rms) * wa.x, (xa.y * inv_rms) * wa.y, (xa.z * inv_rms) * wa.z,
-                      (xa.w * inv_rms) * wa.w, (xb.x * inv_rms) * wb.x, (xb.y * inv_rms) * wb.y,
-                      (xb.z * inv_rms) * wb.z, (xb.w * inv_rms) * wb.w};
-        rotate_quant_slice8(v, sign, s8, cc, act, S.xl, S.xsl, S.xsuml);
+        const float4 x = *reinterpret_cast<const float4 *>(S.hbuf + cc * 64 + s4 * 4);
+        float v[4] = {(x.x * inv_rms) * wa.x, (x.y * inv_rms) * wa.y, (x.z * inv_rms) * wa.z, (x.w * inv_rms) * wa.w};
+        const Chunk4 r = rotate_quant4(v, sign, s4);
+        if (act) {
+            *reinterpret_cast<uint32_t *>(S.xl + cc * 64 + s4 * 4) = r.w;
+            if (s4 == 0) {
+                S.xsl[cc] = r.scale;
+                S.xsuml[cc] = r.sum;
+            }
+        }
     };
-    if (wave * 8 < nc) slice(wave * 8, wp.a, wp.b, wp.sign);
-    for (int c0 = wave * 8 + NTH / 64 * 8; c0 < nc; c0 += NTH / 64 * 8) {
-        const int c = c0 + (int)(lane >> 3), cc = c < nc ? c : 0;
-        const float4 *w4 = reinterpret_cast<const float4 *>(w + cc * 64 + s8 * 8);
-        slice(c0, w4[0], w4[1], P.signs[cc]);
+    if (wave * 4 < nc) slice(wave * 4, wp.a, wp.sign);
+    for (int c0 = wave * 4 + NTH / 64 * 4; c0 < nc; c0 += NTH / 64 * 4) {
+        const int c = c0 + (int)(lane >> 4), cc = c < nc ? c : 0;
+        slice(c0, *reinterpret_cast<const float4 *>(w + cc * 64 + s4 * 4), P.signs[cc]);
     }
     lds_barrier();
 }
