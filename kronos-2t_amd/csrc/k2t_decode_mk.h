@@ -19,6 +19,11 @@ constexpr int kMkRep = 8;
 // Most spans the attention phase cuts one q head's context into, and the fewest
 // positions per span.
 constexpr int kMkSpans = 4;
+// ... and in the 512-thread kernels (the 1.7B nf4g128 decode at context 261-389: 2 spans
+// 1203 tok/s, 3 spans 1144-1159).
+constexpr int kMkSpans512 = 2;
+// Most spans per q head of the kernel with NTH threads per workgroup.
+__host__ __device__ constexpr int mk_max_spans(int nth) { return nth == 512 ? kMkSpans512 : kMkSpans; }
 constexpr int kMkSpanMin = 128;
 
 struct MkLayer {

@@ -620,16 +620,20 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
         } else {
             // merge the other spans' {m, L, o[t]}: all loads in flight, then re-polled
             // together until current (attn_merge_kernel's arithmetic, span order)
-            constexpr int kSp = kMkSpans;
+            constexpr int kSp = mk_max_spans(NTH);
             unsigned long long w[3 * (kSp - 1)];
             const unsigned long long *src = P.APART + (size_t)h * P.nsp * (2 + hd);
             auto addr = [&](int k) { return src + (size_t)(k / 3 + 1) * (2 + hd) + (k % 3 == 2 ? 2 + t : k % 3); };
+            // Every word is requested, the unused spans' too (in bounds: APART holds
+            // kMkSpans slots per head): with the load under a branch the compiler waited
+            // for each load before issuing the next (the other path's zero reuses its
+            // register).
             uint32_t pending = 0;
 #pragma unroll
-            for (int k = 0; k < 3 * (kSp - 1); k++) {
-                w[k] = k / 3 + 1 < nsp ? ll_load(addr(k)) : 0ull;
+            for (int k = 0; k < 3 * (kSp - 1); k++) w[k] = ll_load(addr(k));
+#pragma unroll
+            for (int k = 0; k < 3 * (kSp - 1); k++)
                 if (k / 3 + 1 < nsp && (uint32_t)(w[k] >> 32) != ep_out) pending |= 1u << k;
-            }
             for (uint32_t spins = 0; pending != 0 && merged; spins++) {
                 if ((spins & 31u) == 31u) {
                     if (__hip_atomic_load(P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {

@@ -386,9 +386,10 @@ void upload_mk_layers(k2t_model *m) {
     // the 512-thread kernel (1.7B nf4g128 decode at context 261-389: 1186 -> 1203 tok/s;
     // 3 spans 1144-1159), 4 in the 256-thread one (135M p55454 at 512-640: 1038 -> 1259
     // tok/s)
-    m->mk_nsp = std::max(1, std::min(nw == 8 ? 2 : kMkSpans, nwg / m->cfg.n_heads));
+    const int max_spans = mk_max_spans(nw * 64);
+    m->mk_nsp = std::max(1, std::min(max_spans, nwg / m->cfg.n_heads));
 #ifdef K2T_MK_SPANS
-    m->mk_nsp = K2T_MK_SPANS;
+    m->mk_nsp = std::min(K2T_MK_SPANS, max_spans);
 #endif
     int cursor = 0;
     for (auto &x : h) {
