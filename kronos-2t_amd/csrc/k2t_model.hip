@@ -552,12 +552,16 @@ __device__ __forceinline__ void merge_head(const float *pp, int ns, int nq, int 
         const bool mine = (int)lane < ns;
         const float mv = mine ? pp[(size_t)lane * (2 + hd)] : -INFINITY;
         const float lm = mine ? pp[(size_t)lane * (2 + hd) + 1] : 0.0f;
+        // (every load unconditional, from split min(u, ns - 1), and o1 only used when
+        // nb > 1: a load under a branch whose other path writes its register made the
+        // compiler wait for each load before the next)
+        const int off1 = nb > 1 ? 2 + 64 + (int)lane : 2 + (int)lane;
         float v0[ONESHOT], v1[ONESHOT];
 #pragma unroll
         for (int u = 0; u < ONESHOT; u++) {
-            const float *ps = pp + (size_t)u * (2 + hd);
-            v0[u] = u < ns ? ps[2 + lane] : 0.0f;
-            v1[u] = u < ns && nb > 1 ? ps[2 + 64 + lane] : 0.0f;
+            const float *ps = pp + (size_t)min(u, ns - 1) * (2 + hd);
+            v0[u] = ps[2 + lane];
+            v1[u] = ps[off1];
         }
         const float M = wave_max_f(mv);
         const float em = mine ? expf(mv - M) : 0.0f;
@@ -573,6 +577,7 @@ __device__ __forceinline__ void merge_head(const float *pp, int ns, int nq, int 
     } else {
         // Split maxima and sums one split per lane (loads in flight together), then the
         // rescaled sums in split order.
+        const int off1 = nb > 1 ? 2 + 64 + (int)lane : 2 + (int)lane;
         float M = -INFINITY;
         for (int s = (int)lane; s < ns; s += 64) M = fmaxf(M, pp[(size_t)s * (2 + hd)]);
         M = wave_max_f(M);
@@ -584,11 +589,10 @@ __device__ __forceinline__ void merge_head(const float *pp, int ns, int nq, int 
             for (int j0 = 0; j0 < cnt; j0 += 8) {
                 float v0[8], v1[8];
     #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const float *ps = pp + (size_t)(s0 + j0 + u) * (2 + hd);
-                    const bool ok = j0 + u < cnt;
-                    v0[u] = ok ? ps[2 + lane] : 0.0f;
-                    v1[u] = ok && nb > 1 ? ps[2 + 64 + lane] : 0.0f;
+                for (int u = 0; u < 8; u++) {  // (unconditional, as above)
+                    const float *ps = pp + (size_t)(s0 + min(j0 + u, cnt - 1)) * (2 + hd);
+                    v0[u] = ps[2 + lane];
+                    v1[u] = ps[off1];
                 }
     #pragma unroll
                 for (int u = 0; u < 8; u++) {
@@ -736,19 +740,21 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
 #pragma unroll
             for (int k = 0; k < 4; k++) w[2 + k] = ll_word_load(ps + 2 + cg * 4 + k);
         };
+        // Every slot's words are requested before any is examined (a slot past nact reads
+        // span nact - 1's and is then replaced by the empty span {-inf, 0, 0}): under a
+        // per-slot branch the compiler waited for each slot's loads before issuing the
+        // next slot's.
         unsigned long long wv6[kPre][6];
+#pragma unroll
+        for (int j = 0; j < kPre; j++) poll(min(sub + j * nsub, nact - 1), wv6[j]);
         uint32_t pending = 0;
 #pragma unroll
         for (int j = 0; j < kPre; j++) {
-            if (sub + j * nsub < nact) {
-                poll(sub + j * nsub, wv6[j]);
+            const bool live = sub + j * nsub < nact;
 #pragma unroll
-                for (int k = 0; k < 6; k++)
-                    if ((uint32_t)(wv6[j][k] >> 32) != ep) pending |= 1u << (6 * j + k);
-            } else {
-                wv6[j][0] = (unsigned long long)__float_as_uint(-INFINITY);
-#pragma unroll
-                for (int k = 1; k < 6; k++) wv6[j][k] = 0ull;
+            for (int k = 0; k < 6; k++) {
+                if (live && (uint32_t)(wv6[j][k] >> 32) != ep) pending |= 1u << (6 * j + k);
+                if (!live) wv6[j][k] = k == 0 ? (unsigned long long)__float_as_uint(-INFINITY) : 0ull;
             }
         }
         for (uint32_t spins = 0; pending != 0 && ok; spins++) {
