@@ -425,8 +425,8 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
     // 0. past positions' K rows, scales and V slices do not depend on this step: request
     //    this thread's first ones before waiting for q / k / v.
     // (256 threads: 12 covers the 135M model's spans at the bench contexts, 512 positions
-    // and more over 4 spans; 8 measured 1.7% slower there, 16 slower than 12.  512 threads:
-    // 8, and 12 or 16 no faster on the 1.7B model)
+    // and more over 4 spans, and measured 1.7% faster than 8 there; 16 was slower than 12.
+    // 512 threads: 8; 12 or 16 measured no faster on the 1.7B model)
     constexpr int kVPre = NTH == 256 ? 12 : 8;
     uint4 kpre[8];
     float kspre = 0.0f, vspre = 0.0f;
