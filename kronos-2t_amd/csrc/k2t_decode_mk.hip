@@ -505,6 +505,14 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
     }
     lds_barrier();
     ATR(2);
+    // The thread whose first position is the current one takes its K row from LDS into the
+    // prefetch registers (one wait for the row, not one per piece as below).
+    if (t0 + t == pos) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (i < hd / 16) kpre[i] = ld_lds(reinterpret_cast<const uint4 *>(kn) + i);
+        kspre = ld_lds(scal + 1);
+    }
     // 3. scores s_t = float(q8 . k8_t) * ks_t * (qs * scale), t0 <= t < t1
     const float qas = scal[0];
     float smax = -INFINITY;
@@ -512,7 +520,7 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
         const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
         int dot = 0;
         float kscale;
-        if (tt == t0 + t && tt < pos) {  // prefetched
+        if (tt == t0 + t && tt <= pos) {  // prefetched (or, for the current position, copied)
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 if (i >= hd / 16) break;
@@ -524,6 +532,8 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
             }
             kscale = kspre;
         } else {
+            // (the current position here only past a thread's first position: spans longer
+            // than NTH positions)
             const uint4 *kr = reinterpret_cast<const uint4 *>(P.kq + (base + tt) * hd);
             for (int i = 0; i < hd / 16; i++) {
                 const uint4 a = tt == pos ? lds_read16_now(kn + 16 * i) : ld_global(kr + i);
