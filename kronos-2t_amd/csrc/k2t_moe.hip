@@ -110,16 +110,32 @@ static k2t_experts *make_bank(k2t_ctx *ctx, const k2t_k2tm_header &h) {
 
 // ---------------------------------------------------------------- kernels
 // Largest (value, lowest index on ties) over the wave; returns the lane's view of it.
-__device__ __forceinline__ void wave_argmax(float &v, int &i) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = xor_lane(v, m);
-        const int oi = xor_lane(i, m);
-        if (ov > v || (ov == v && oi < i)) {
-            v = ov;
-            i = oi;
-        }
+// The order is total (larger value, then lower index), so any reduction tree gives the
+// same pick: rotations by 1, 2, 4 and 8 inside each 16-lane row (DPP, no LDS round trip),
+// then the four rows' results compared through v_readlane.
+__device__ __forceinline__ void take_better(float &v, int &i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
     }
+}
+template <int CTRL>
+__device__ __forceinline__ void row_rotate_argmax(float &v, int &i) {
+    const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+    const int oi = __builtin_amdgcn_mov_dpp(i, CTRL, 0xF, 0xF, false);
+    take_better(v, i, ov, oi);
+}
+__device__ __forceinline__ void wave_argmax(float &v, int &i) {
+    row_rotate_argmax<0x121>(v, i);  // row_ror:1
+    row_rotate_argmax<0x122>(v, i);  // row_ror:2
+    row_rotate_argmax<0x124>(v, i);  // row_ror:4
+    row_rotate_argmax<0x128>(v, i);  // row_ror:8
+    float bv = lane_val(v, 0);
+    int bi = lane_val(i, 0);
+#pragma unroll
+    for (int r = 1; r < 4; r++) take_better(bv, bi, lane_val(v, 16 * r), lane_val(i, 16 * r));
+    v = bv;
+    i = bi;
 }
 
 // route_sorted (sparse_moe.rs:86-182) for E <= 256 experts on one wave.  Top-k picks the
