@@ -320,11 +320,26 @@ void launch_moe_clear(hipStream_t st, const MoeWork &ws, int E) {
 
 // out.fill(0); out += w_z * expert_z in route order; hidden += out
 // (sparse_moe.rs:1001-1003, 1041-1043; real_llm.rs:6714).
+// Up to kCombineMax slots have all their loads in flight together (slot min(z, k - 1) is
+// read for z >= k and not added); a loop over a run-time k issued one load per round
+// trip.  More slots take the loop.
+constexpr int kCombineMax = 8;
 __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ hidden, const float *__restrict__ eo,
                                                           const float *__restrict__ wts, int k, int d) {
     const int r = (int)blockIdx.x * 256 + (int)threadIdx.x;
     if (r >= d) return;
     float p = 0.0f;
+    if (k <= kCombineMax) {
+        float e[kCombineMax];
+#pragma unroll
+        for (int z = 0; z < kCombineMax; z++) e[z] = eo[(size_t)min(z, k - 1) * d + r];
+        const float h = hidden[r];
+#pragma unroll
+        for (int z = 0; z < kCombineMax; z++)
+            if (z < k) p = p + wts[z] * e[z];
+        hidden[r] = h + p;
+        return;
+    }
     for (int z = 0; z < k; z++) p = p + wts[z] * eo[(size_t)z * d + r];
     hidden[r] = hidden[r] + p;
 }
