@@ -153,11 +153,11 @@ struct XBuilder {
         if constexpr (XS == 1) {
             const float4 *x4 = reinterpret_cast<const float4 *>(src);
             const int n4 = P.K / 4;
+            // (unconditional loads from a clamped index, masked in finish(): under a branch
+            // whose other side zeroed the registers the compiler waited for the first load
+            // before issuing the rest)
 #pragma unroll
-            for (int j = 0; j < kSqPre; j++) {
-                const int i = (int)lane + 64 * j;
-                sq[j] = i < n4 ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
+            for (int j = 0; j < kSqPre; j++) sq[j] = x4[min((int)lane + 64 * j, n4 - 1)];
         }
     }
 
@@ -333,7 +333,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         const int z = (int)blockIdx.z;
         const uint8_t *rec = P.bank + (size_t)P.route[z] * P.bank_stride;
         pair_p = rec + P.mat_off;
-        const uint4 cbw = ld_global(reinterpret_cast<const uint4 *>(rec + P.cb_off));
+        // The codebook as a vector load through a lane offset the compiler cannot see is
+        // zero: a uniform address made it a scalar load whose wait (scalar loads are not
+        // tracked in issue order) came before the first weight fetch, a second round trip
+        // after the route's.  The vector load completes in issue order ahead of the
+        // fragments, so its use waits for nothing they need.
+        int zoff;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zoff));
+        const uint4 cbw = ld_global(reinterpret_cast<const uint4 *>(rec + P.cb_off + zoff));
         cb0 = cbw.x;
         cb1 = cbw.y;
         cb2 = cbw.z;

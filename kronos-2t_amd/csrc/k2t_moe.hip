@@ -242,22 +242,31 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
     const uint32_t lane = threadIdx.x & 63u;
     const int wave = (int)(threadIdx.x >> 6);
     const int e = (int)blockIdx.x * 4 + wave;
-    const uint32_t epoch = *ctr + 1u;
-    if (e < E) {
-    // All loads of the wave first (NJ float4 of each vector per lane).
+    // Every load is issued before the first wait: the vectors from clamped indices (masked
+    // below; a load under a lane condition became a branch per load), the bias, and the
+    // call counter as a vector load behind them (through a lane offset the compiler cannot
+    // see is zero: as a scalar load its wait came first, one round trip before the rest).
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     const float4 *w4 = reinterpret_cast<const float4 *>(nw);
-    const float4 *r4 = reinterpret_cast<const float4 *>(W + (size_t)e * d);
+    const float4 *r4 = reinterpret_cast<const float4 *>(W + (size_t)min(e, E - 1) * d);
     const int n4 = d / 4;
     float4 xv[NJ], wv[NJ], rv[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const int i = (int)lane + 64 * j;
-        const bool ok = i < n4;
-        xv[j] = ok ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        wv[j] = ok ? w4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        rv[j] = ok ? r4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const int i = min((int)lane + 64 * j, n4 - 1);
+        xv[j] = x4[i];
+        wv[j] = w4[i];
+        rv[j] = r4[i];
     }
+    const float bv = bias ? bias[min(e, E - 1)] : 0.0f;
+    int zoff;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zoff));
+    const uint32_t epoch = ld_global(ctr + zoff) + 1u;
+    if (e < E) {
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+        if ((int)lane + 64 * j >= n4) xv[j] = wv[j] = rv[j] = zero4;
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
@@ -277,9 +286,14 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
         acc = fmaf((xv[j].w * inv_rms) * wv[j].w, rv[j].w, acc);
     }
     acc = wave_sum_f(acc);
-    if (lane == 0) word_store(words + e, __float_as_uint(bias ? acc + bias[e] : acc), epoch);
+    if (lane == 0) word_store(words + e, __float_as_uint(bias ? acc + bv : acc), epoch);
     }
     if (blockIdx.x != 0 || wave != 0) return;
+    // The E words: one load each in flight together, then a bounded wait on any not yet
+    // of this epoch.
+    unsigned long long w[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) w[j] = word_load(words + min((int)lane + 64 * j, E - 1));
     float sc[4];
     bool ok = true;
 #pragma unroll
@@ -287,17 +301,16 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
         const int ee = (int)lane + 64 * j;
         sc[j] = -INFINITY;
         if (ee >= E) continue;
-        unsigned long long w = word_load(words + ee);
-        for (uint32_t spins = 0; ok && (uint32_t)(w >> 32) != epoch; spins++) {
+        for (uint32_t spins = 0; ok && (uint32_t)(w[j] >> 32) != epoch; spins++) {
             if (spins > spin_limit) {
                 ok = false;
                 __hip_atomic_store(err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
-            w = word_load(words + ee);
+            w[j] = word_load(words + ee);
         }
-        if (ok) sc[j] = __uint_as_float((uint32_t)w);
+        if (ok) sc[j] = __uint_as_float((uint32_t)w[j]);
     }
     select_routes(sc, (int)lane, E, k, norm_topk, scoring, ids, wts);
     if (lane == 0) *ctr = epoch;
