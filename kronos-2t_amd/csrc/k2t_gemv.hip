@@ -27,6 +27,7 @@
 #include "k2t_device.h"
 #include "../../include/k2t_hip.h"
 #include "k2t_internal.h"
+#include "k2t_route.h"
 
 namespace k2t {
 
@@ -69,6 +70,21 @@ struct GemvParams {
     uint32_t mat_off, cb_off;
     size_t slot_out, slot_src;
     int gu_split;
+    // Routing in the same launch (XS 1 only, rt_w != NULL): workgroups of plane z = 0 run
+    // the router (route_logit_half on every wave, units x * waves + wave stepping by
+    // gridDim.x * waves, into rt_words [2 rt_E + 2]; then route_collect_parts on wave 0 of
+    // workgroup 0, which writes route[] / rt_wts[]
+    // and publishes sorted id r as the word rt_pub[r] = {epoch, id}); plane z >= 1 is slot
+    // z - 1, which builds its activation, then waits for its word.  epoch = *rt_ctr + 1;
+    // the counter is advanced by a later launch, when every workgroup of this one has read
+    // it.
+    const float *rt_w, *rt_b;
+    unsigned long long *rt_words, *rt_pub;
+    const uint32_t *rt_ctr;
+    int *rt_err;
+    float *rt_wts;
+    int rt_E, rt_k, rt_norm, rt_scoring;
+    uint32_t rt_spin;
 };
 
 // Output index of row r: the [gate64(ic), up64(ic)] interleave of a split gate/up matrix.
@@ -275,6 +291,30 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     extern __shared__ float lds[];
     const uint32_t lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    // Routing in this launch: the epoch of this call (a vector load through a lane offset
+    // the compiler cannot see is zero, so no scalar wait comes before the first loads).
+    constexpr bool kCanRoute = XS == 1 && NT == 1 && !DOTS;
+    const bool fused_route = kCanRoute && P.rt_w != nullptr;
+    int slot = (int)blockIdx.z;
+    uint32_t rt_epoch = 0;
+    if constexpr (kCanRoute) {
+        if (fused_route) {
+            int zoff;
+            asm volatile("v_mov_b32 %0, 0" : "=v"(zoff));
+            rt_epoch = ld_global(P.rt_ctr + zoff) + 1u;
+            if (blockIdx.z == 0) {
+                const int nw = (int)(blockDim.x >> 6);
+                for (int u = (int)blockIdx.x * nw + wave; u < 2 * P.rt_E; u += (int)gridDim.x * nw)
+                    route_logit_half(P.xsrc, P.xnorm, P.K, P.rt_w, u, lane, rt_epoch, P.rt_E, P.rt_words);
+                if (blockIdx.x == 0 && wave == 0)
+                    route_collect_parts(P.rt_words, P.rt_E, P.K, P.eps, P.rt_b, rt_epoch, P.rt_spin, P.rt_err,
+                                        lane, P.rt_k, P.rt_norm, P.rt_scoring, const_cast<int *>(P.route),
+                                        P.rt_wts, P.rt_pub);
+                return;
+            }
+            slot -= 1;
+        }
+    }
     const int tok0 = P.tok_base + (int)blockIdx.y * NT;
     const uint32_t half = lane & 1u;
     const uint32_t g = (lane >> 1) & 3u;
@@ -329,9 +369,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     uint32_t cb0 = P.cb0, cb1 = P.cb1, cb2 = P.cb2, cb3 = P.cb3;
     float *out_p = P.out;
     const float *xsrc_p = P.xsrc;
-    if (P.route) {
-        const int z = (int)blockIdx.z;
-        const uint8_t *rec = P.bank + (size_t)P.route[z] * P.bank_stride;
+    auto bind_expert = [&](int id) {
+        const uint8_t *rec = P.bank + (size_t)id * P.bank_stride;
         pair_p = rec + P.mat_off;
         // The codebook as a vector load through a lane offset the compiler cannot see is
         // zero: a uniform address made it a scalar load whose wait (scalar loads are not
@@ -345,14 +384,34 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         cb1 = cbw.y;
         cb2 = cbw.z;
         cb3 = cbw.w;
-        out_p += (size_t)z * P.slot_out;
-        xsrc_p += (size_t)z * P.slot_src;
+    };
+    if (P.route) {
+        out_p += (size_t)slot * P.slot_out;
+        xsrc_p += (size_t)slot * P.slot_src;
+        if (!fused_route) bind_expert(P.route[slot]);
     }
     // NF4: the codebook as the two XOR tables of nf4_xlut (two v_perm and one XOR per
     // four codes instead of two v_perm, a select and a bit-3 mask)
     uint32_t xt0 = 0, xt1 = 0, xu0 = 0, xu1 = 0;
     if constexpr (FMT == 1) nf4_xor_tables(cb0, cb1, cb2, cb3, xt0, xt1, xu0, xu1);
     const uint8_t *mbase = is_tail ? P.tail : pair_p + (size_t)pidx * (FMT == 0 ? (size_t)P.nc * PREC : P.ptot);
+    // Routing in this launch: the slot's expert id, once wave-uniform word rt_pub[slot]
+    // carries this epoch (bounded wait; on timeout *rt_err is raised and expert 0 is read).
+    auto await_expert = [&]() {
+        unsigned long long w = word_load(P.rt_pub + slot);
+        for (uint32_t spins = 0; (uint32_t)(w >> 32) != rt_epoch; spins++) {
+            if (spins > P.rt_spin) {
+                __hip_atomic_store(P.rt_err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                w = (unsigned long long)rt_epoch << 32;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            w = word_load(P.rt_pub + slot);
+        }
+        bind_expert(min((int)(uint32_t)w, P.rt_E - 1));
+        if constexpr (FMT == 1) nf4_xor_tables(cb0, cb1, cb2, cb3, xt0, xt1, xu0, xu1);
+        mbase = pair_p + (size_t)pidx * (FMT == 0 ? (size_t)P.nc * PREC : P.ptot);
+    };
 
     auto fetch = [&](Frag<HP, NT> &fr, int c) {
         const uint8_t *rec, *scp;
@@ -587,10 +646,19 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             // activation while the weights are in flight.
             XBuilder<XS> xb(P, xsrc_p, tok0, cw0, cw1, lane);
             xb.begin();
-            if (valid(0)) fetch(fa, chunk_of(0));
-            if (valid(1)) fetch(fb, chunk_of(1));
-            xb.finish(xl, xsl, xsuml);
-            __builtin_amdgcn_wave_barrier();
+            if (fused_route) {
+                // The expert is not known yet: the activation is built while the routing runs.
+                xb.finish(xl, xsl, xsuml);
+                __builtin_amdgcn_wave_barrier();
+                await_expert();
+                if (valid(0)) fetch(fa, chunk_of(0));
+                if (valid(1)) fetch(fb, chunk_of(1));
+            } else {
+                if (valid(0)) fetch(fa, chunk_of(0));
+                if (valid(1)) fetch(fb, chunk_of(1));
+                xb.finish(xl, xsl, xsuml);
+                __builtin_amdgcn_wave_barrier();
+            }
         } else {
             if (valid(0)) fetch(fa, chunk_of(0));
         }
@@ -847,10 +915,29 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
         P.slot_out = grp->slot_out;
         P.slot_src = grp->slot_src;
         P.gu_split = grp->gu_split;
+        int planes = grp->nslots;
+        if (grp->rt_w) {  // routing in this launch: plane 0 routes, slot z is plane z + 1
+            if (xsm != K2T_XS_RMSNORM || m->cols > 2048 || grp->rt_E < 1 || grp->rt_E > 256 || !grp->rt_words ||
+                !grp->rt_pub || !grp->rt_ctr || !grp->rt_err || !grp->rt_wts || !grp->route)
+                throw Error(K2T_E_INTERNAL, "grouped gemv: routing in the launch needs the RMSNorm source, d <= 2048");
+            P.rt_w = grp->rt_w;
+            P.rt_b = grp->rt_b;
+            P.rt_words = grp->rt_words;
+            P.rt_pub = grp->rt_pub;
+            P.rt_ctr = grp->rt_ctr;
+            P.rt_err = grp->rt_err;
+            P.rt_wts = grp->rt_wts;
+            P.rt_E = grp->rt_E;
+            P.rt_k = grp->nslots;
+            P.rt_norm = grp->rt_norm;
+            P.rt_scoring = grp->rt_scoring;
+            P.rt_spin = grp->rt_spin;
+            planes += 1;
+        }
         const dim3 block(64 * plan.nseg);
         P.lds_terms = 1;
         P.exact = ctx->exact;
-        launch_fmt<false>(m, 1, xsm, dim3(plan.rb_hi - plan.rb_lo, 1, grp->nslots), block, per_tok, ctx->stream, P);
+        launch_fmt<false>(m, 1, xsm, dim3(plan.rb_hi - plan.rb_lo, 1, planes), block, per_tok, ctx->stream, P);
         hip_check(hipGetLastError(), "grouped gemv launch");
         return;
     }

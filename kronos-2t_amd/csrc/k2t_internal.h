@@ -90,6 +90,17 @@ struct GemvGroup {
     uint32_t mat_off, cb_off;
     size_t slot_out, slot_src;
     int gu_split;
+    // Routing inside the launch (gate_up only; rt_w = NULL: route[] is ready on entry):
+    // the router rows rt_w [rt_E][d] (+ rt_b), logit words rt_words [rt_E], the published
+    // sorted ids rt_pub [nslots], the call counter rt_ctr (advanced by a later launch) and
+    // the timeout flag rt_err; ids / weights also land in route / rt_wts.
+    const float *rt_w = nullptr, *rt_b = nullptr;
+    unsigned long long *rt_words = nullptr, *rt_pub = nullptr;
+    const uint32_t *rt_ctr = nullptr;
+    int *rt_err = nullptr;
+    float *rt_wts = nullptr;
+    int rt_E = 0, rt_norm = 0, rt_scoring = 0;
+    uint32_t rt_spin = 0;
 };
 void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, int xs_mode, const float *src,
                          const float *w, float eps, float *out);

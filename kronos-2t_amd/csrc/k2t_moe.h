@@ -39,7 +39,8 @@ struct MoeLayer {
 struct MoeWork {
     float *gu;      // [top_k][2*d_ff] gate_up outputs, [gate64, up64] blocks
     float *eo;      // [top_k][d_model] expert outputs
-    unsigned long long *words;  // [E] router logits as {epoch, value} words
+    unsigned long long *words;  // [2E + 2] router logits (or partial dots and sums) as {epoch, value} words
+    unsigned long long *pub;    // [K2T_MOE_MAX_TOPK] sorted route ids as {epoch, id} words
     float *wts;                 // [top_k]
     int *ids;                   // [top_k]
     uint32_t *ctr;              // route-call counter (epoch source)

@@ -23,6 +23,7 @@
 #include "k2t_device.h"
 #include "k2t_internal.h"
 #include "k2t_moe.h"
+#include "k2t_route.h"
 
 namespace k2t {
 
@@ -109,128 +110,10 @@ static k2t_experts *make_bank(k2t_ctx *ctx, const k2t_k2tm_header &h) {
 }
 
 // ---------------------------------------------------------------- kernels
-// Largest (value, lowest index on ties) over the wave; returns the lane's view of it.
-// The order is total (larger value, then lower index), so any reduction tree gives the
-// same pick: rotations by 1, 2, 4 and 8 inside each 16-lane row (DPP, no LDS round trip),
-// then the four rows' results compared through v_readlane.
-__device__ __forceinline__ void take_better(float &v, int &i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) {
-        v = ov;
-        i = oi;
-    }
-}
-template <int CTRL>
-__device__ __forceinline__ void row_rotate_argmax(float &v, int &i) {
-    const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
-    const int oi = __builtin_amdgcn_mov_dpp(i, CTRL, 0xF, 0xF, false);
-    take_better(v, i, ov, oi);
-}
-__device__ __forceinline__ void wave_argmax(float &v, int &i) {
-    row_rotate_argmax<0x121>(v, i);  // row_ror:1
-    row_rotate_argmax<0x122>(v, i);  // row_ror:2
-    row_rotate_argmax<0x124>(v, i);  // row_ror:4
-    row_rotate_argmax<0x128>(v, i);  // row_ror:8
-    float bv = lane_val(v, 0);
-    int bi = lane_val(i, 0);
-#pragma unroll
-    for (int r = 1; r < 4; r++) take_better(bv, bi, lane_val(v, 16 * r), lane_val(i, 16 * r));
-    v = bv;
-    i = bi;
-}
-
-// route_sorted (sparse_moe.rs:86-182) for E <= 256 experts on one wave.  Top-k picks the
-// largest score with the lowest id among equals, the order select_topk_by_score's strict
-// comparisons give; the top-k sums run in selection order like the reference's loops.
-// sc[j] holds the logit of expert lane + 64 j (-inf past E) on entry.
-__device__ void select_routes(float sc[4], int lane, int E, int k, int norm_topk, int scoring, int *__restrict__ ids,
-                              float *__restrict__ wts) {
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-        if (sc[j] != sc[j]) sc[j] = -INFINITY;  // NaN never wins a comparison: rank it last
-    if (scoring == K2T_MOE_SOFTMAX) {
-        float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        m = wave_max_f(m);
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            sc[j] = lane + 64 * j < E ? expf(sc[j] - m) : 0.0f;
-            s += sc[j];
-        }
-        s = wave_sum_f(s);
-        const float inv_all = s > 0.0f ? 1.0f / s : 1.0f / (float)E;
-#pragma unroll
-        for (int j = 0; j < 4; j++) sc[j] = lane + 64 * j < E ? sc[j] * inv_all : -INFINITY;
-    } else if (scoring == K2T_MOE_SIGMOID) {
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            sc[j] = lane + 64 * j < E && sc[j] == sc[j] ? 1.0f / (1.0f + expf(-sc[j])) : -INFINITY;
-    }
-    // Selection round r leaves its (id, score) in lane r's registers.
-    int my_id = 0;
-    float my_w = 0.0f;
-    for (int r = 0; r < k; r++) {
-        float bv = sc[0];
-        int bi = lane;
-#pragma unroll
-        for (int j = 1; j < 4; j++)
-            if (sc[j] > bv) {
-                bv = sc[j];
-                bi = lane + 64 * j;
-            }
-        wave_argmax(bv, bi);
-        bi = min(bi, E - 1);  // every id indexes a record of the bank, whatever the scores
-        if (lane == r) {
-            my_id = bi;
-            my_w = bv;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (lane + 64 * j == bi) sc[j] = -INFINITY;
-    }
-    // Weight normalization; the sums run over the selections in selection order.
-    if (scoring == K2T_MOE_TOPK_SOFTMAX) {
-        const float mz = lane_val(my_w, 0);
-        const float ex = lane < k ? expf(my_w - mz) : 0.0f;
-        float s = 0.0f;
-        for (int r = 0; r < k; r++) s += lane_val(ex, r);
-        const float inv = s > 0.0f ? 1.0f / s : 1.0f / (float)k;
-        my_w = ex * inv;
-    } else if (norm_topk) {
-        float s = 0.0f;
-        for (int r = 0; r < k; r++) s += lane_val(my_w, r);
-        if (s > 0.0f) my_w *= 1.0f / s;
-    }
-    // Ascending expert id (sparse_moe.rs:170-179): lane r's rank among the k selections
-    // (ids are distinct, ties in id order are impossible).
-    int rank = 0;
-    for (int r = 0; r < k; r++) {
-        const int other = lane_val(my_id, r);
-        rank += (r != lane && other < my_id) ? 1 : 0;
-    }
-    if (lane < k) {
-        ids[rank] = my_id;
-        wts[rank] = my_w;
-    }
-}
-
-// Router logits: each wave owns one expert row; x_norm = (x * inv_rms) * w is formed on
-// the fly (rms_norm, real_llm.rs:9858-9898; the sum of squares in the order of the GEMV's
-// fused builder, so x_norm matches the expert activations' source), dot as in
-// dot_f32_moe (sparse_moe.rs:1644-1655) with a tree reduction.
-//
-// The same launch also selects the routes: every logit is published as one 64-bit word
-// {epoch, value} (a single agent-scope atomic store, so the value and its ready mark
-// arrive together, with no fence), and wave 0 of workgroup 0 waits for all E words of
-// this call's epoch, then runs the selection.  The epoch is the call counter *ctr + 1;
-// workgroup 0 advances the counter after its wait, when every workgroup has read it.
-// The wait is bounded: on timeout it raises *err and still writes in-range ids.
-__device__ __forceinline__ void word_store(unsigned long long *p, uint32_t v, uint32_t epoch) {
-    __hip_atomic_store(p, ((unsigned long long)epoch << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long word_load(const unsigned long long *p) {
-    return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
+// Router logits (route_logit, one wave per expert row) and, in the same launch, the
+// selection: wave 0 of workgroup 0 waits for all E words of this call's epoch, then runs
+// select_routes.  The epoch is the call counter *ctr + 1; workgroup 0 advances the counter
+// after its wait, when every workgroup has read it.
 template <int NJ>  // float4 per lane of each vector: d <= 256 * NJ
 __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ x, const float *__restrict__ nw,
                                                         float eps, int d, const float *__restrict__ W,
@@ -242,84 +125,22 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
     const uint32_t lane = threadIdx.x & 63u;
     const int wave = (int)(threadIdx.x >> 6);
     const int e = (int)blockIdx.x * 4 + wave;
-    // Every load is issued before the first wait: the vectors from clamped indices (masked
-    // below; a load under a lane condition became a branch per load), the bias, and the
-    // call counter as a vector load behind them (through a lane offset the compiler cannot
-    // see is zero: as a scalar load its wait came first, one round trip before the rest).
-    const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    const float4 *w4 = reinterpret_cast<const float4 *>(nw);
-    const float4 *r4 = reinterpret_cast<const float4 *>(W + (size_t)min(e, E - 1) * d);
-    const int n4 = d / 4;
-    float4 xv[NJ], wv[NJ], rv[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int i = min((int)lane + 64 * j, n4 - 1);
-        xv[j] = x4[i];
-        wv[j] = w4[i];
-        rv[j] = r4[i];
-    }
-    const float bv = bias ? bias[min(e, E - 1)] : 0.0f;
+    // The counter as a vector load through a lane offset the compiler cannot see is zero:
+    // as a scalar load its wait came first, one round trip before the vector loads.
     int zoff;
     asm volatile("v_mov_b32 %0, 0" : "=v"(zoff));
     const uint32_t epoch = ld_global(ctr + zoff) + 1u;
-    if (e < E) {
-    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-    for (int j = 0; j < NJ; j++)
-        if ((int)lane + 64 * j >= n4) xv[j] = wv[j] = rv[j] = zero4;
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        ss = fmaf(xv[j].x, xv[j].x, ss);
-        ss = fmaf(xv[j].y, xv[j].y, ss);
-        ss = fmaf(xv[j].z, xv[j].z, ss);
-        ss = fmaf(xv[j].w, xv[j].w, ss);
-    }
-    ss = wave_sum_f(ss);
-    const float inv_rms = 1.0f / sqrtf(ss / (float)d + eps);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        acc = fmaf((xv[j].x * inv_rms) * wv[j].x, rv[j].x, acc);
-        acc = fmaf((xv[j].y * inv_rms) * wv[j].y, rv[j].y, acc);
-        acc = fmaf((xv[j].z * inv_rms) * wv[j].z, rv[j].z, acc);
-        acc = fmaf((xv[j].w * inv_rms) * wv[j].w, rv[j].w, acc);
-    }
-    acc = wave_sum_f(acc);
-    if (lane == 0) word_store(words + e, __float_as_uint(bias ? acc + bv : acc), epoch);
-    }
+    if (e < E) route_logit<NJ>(x, nw, eps, d, W, bias, e, lane, epoch, words);
     if (blockIdx.x != 0 || wave != 0) return;
-    // The E words: one load each in flight together, then a bounded wait on any not yet
-    // of this epoch.
-    unsigned long long w[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) w[j] = word_load(words + min((int)lane + 64 * j, E - 1));
-    float sc[4];
-    bool ok = true;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int ee = (int)lane + 64 * j;
-        sc[j] = -INFINITY;
-        if (ee >= E) continue;
-        for (uint32_t spins = 0; ok && (uint32_t)(w[j] >> 32) != epoch; spins++) {
-            if (spins > spin_limit) {
-                ok = false;
-                __hip_atomic_store(err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-            w[j] = word_load(words + ee);
-        }
-        if (ok) sc[j] = __uint_as_float((uint32_t)w[j]);
-    }
-    select_routes(sc, (int)lane, E, k, norm_topk, scoring, ids, wts);
+    route_collect(words, E, epoch, spin_limit, err, lane, k, norm_topk, scoring, ids, wts, nullptr);
     if (lane == 0) *ctr = epoch;
 }
 
 // Clears the hand-off words and the call counter of a fresh workspace (a kernel, so that a
 // captured graph holds no memset node).
-__global__ void moe_clear_kernel(unsigned long long *words, int E, uint32_t *ctr, int *err) {
-    for (int i = (int)threadIdx.x; i < E; i += (int)blockDim.x) words[i] = 0ull;
+__global__ void moe_clear_kernel(unsigned long long *words, int E, unsigned long long *pub, uint32_t *ctr, int *err) {
+    for (int i = (int)threadIdx.x; i < 2 * E + 2; i += (int)blockDim.x) words[i] = 0ull;
+    if (threadIdx.x < K2T_MOE_MAX_TOPK) pub[threadIdx.x] = 0ull;
     if (threadIdx.x == 0) {
         *ctr = 0u;
         *err = 0;
@@ -327,7 +148,7 @@ __global__ void moe_clear_kernel(unsigned long long *words, int E, uint32_t *ctr
 }
 
 void launch_moe_clear(hipStream_t st, const MoeWork &ws, int E) {
-    hipLaunchKernelGGL(moe_clear_kernel, dim3(1), dim3(256), 0, st, ws.words, E, ws.ctr, ws.err);
+    hipLaunchKernelGGL(moe_clear_kernel, dim3(1), dim3(256), 0, st, ws.words, E, ws.pub, ws.ctr, ws.err);
     hip_check(hipGetLastError(), "moe clear launch");
 }
 
@@ -337,9 +158,13 @@ void launch_moe_clear(hipStream_t st, const MoeWork &ws, int E) {
 // read for z >= k and not added); a loop over a run-time k issued one load per round
 // trip.  More slots take the loop.
 constexpr int kCombineMax = 8;
+// With ctr set, thread 0 advances the route-call counter (routing ran inside the gate_up
+// launch, whose workgroups have all read it by now).
 __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ hidden, const float *__restrict__ eo,
-                                                          const float *__restrict__ wts, int k, int d) {
+                                                          const float *__restrict__ wts, int k, int d,
+                                                          uint32_t *__restrict__ ctr) {
     const int r = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (ctr && r == 0) *ctr = *ctr + 1u;
     if (r >= d) return;
     float p = 0.0f;
     if (k <= kCombineMax) {
@@ -362,19 +187,18 @@ void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float 
     const k2t_experts *b = L.bank;
     const int d = (int)b->hdr.d_model, dff = (int)b->hdr.d_ff_expert, E = (int)b->hdr.experts_per_layer;
     hipStream_t st = ctx->stream;
-    if (d <= 1024)
-        hipLaunchKernelGGL(moe_route_kernel<4>, dim3((E + 3) / 4), dim3(256), 0, st, hidden, post_norm, eps, d,
-                           L.router_w, L.router_b, E, L.top_k, L.norm_topk, L.scoring, ws.words, ws.ctr, ws.err,
-                           1u << 22, ws.ids, ws.wts);
-    else if (d <= 2048)
-        hipLaunchKernelGGL(moe_route_kernel<8>, dim3((E + 3) / 4), dim3(256), 0, st, hidden, post_norm, eps, d,
-                           L.router_w, L.router_b, E, L.top_k, L.norm_topk, L.scoring, ws.words, ws.ctr, ws.err,
-                           1u << 22, ws.ids, ws.wts);
-    else
-        hipLaunchKernelGGL(moe_route_kernel<16>, dim3((E + 3) / 4), dim3(256), 0, st, hidden, post_norm, eps, d,
-                           L.router_w, L.router_b, E, L.top_k, L.norm_topk, L.scoring, ws.words, ws.ctr, ws.err,
-                           1u << 22, ws.ids, ws.wts);
-    hip_check(hipGetLastError(), "moe route launch");
+    // d <= 2048: the routing runs in the gate_up launch (one launch fewer per layer);
+    // larger rows keep the route kernel.
+    const bool fused = d <= 2048;
+    if (!fused) {
+        if (d <= 4096)
+            hipLaunchKernelGGL(moe_route_kernel<16>, dim3((E + 3) / 4), dim3(256), 0, st, hidden, post_norm, eps, d,
+                               L.router_w, L.router_b, E, L.top_k, L.norm_topk, L.scoring, ws.words, ws.ctr, ws.err,
+                               1u << 22, ws.ids, ws.wts);
+        else
+            throw Error(K2T_E_ARG, "MoE router: d_model above 4096");
+        hip_check(hipGetLastError(), "moe route launch");
+    }
     const uint8_t *layer_base = b->d_bytes + kK2tmPage + (size_t)L.shard_layer * E * b->lay.aligned_bytes;
     GemvGroup g{};
     g.route = ws.ids;
@@ -386,7 +210,21 @@ void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float 
     g.slot_out = (size_t)2 * dff;
     g.slot_src = 0;
     g.gu_split = 1;
+    if (fused) {
+        g.rt_w = L.router_w;
+        g.rt_b = L.router_b;
+        g.rt_words = ws.words;
+        g.rt_pub = ws.pub;
+        g.rt_ctr = ws.ctr;
+        g.rt_err = ws.err;
+        g.rt_wts = ws.wts;
+        g.rt_E = E;
+        g.rt_norm = L.norm_topk;
+        g.rt_scoring = L.scoring;
+        g.rt_spin = 1u << 22;
+    }
     launch_gemv_grouped(ctx, &b->gu, g, K2T_XS_RMSNORM, hidden, post_norm, eps, ws.gu);
+    g.rt_w = nullptr;
     g.mat_off = (uint32_t)b->lay.dn_pair_off;
     g.cb_off = (uint32_t)b->lay.dn_cb_off;
     g.slot_out = (size_t)d;
@@ -394,13 +232,13 @@ void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float 
     g.gu_split = 0;
     launch_gemv_grouped(ctx, &b->dn, g, K2T_XS_SWIGLU, ws.gu, nullptr, 0.0f, ws.eo);
     hipLaunchKernelGGL(moe_combine_kernel, dim3((d + 255) / 256), dim3(256), 0, st, hidden, ws.eo, ws.wts, L.top_k,
-                       d);
+                       d, fused ? ws.ctr : nullptr);
     hip_check(hipGetLastError(), "moe combine launch");
 }
 
 size_t moe_work_floats(const k2t_experts *b, int top_k) {
     const size_t d = (size_t)b->hdr.d_model, dff = (size_t)b->hdr.d_ff_expert, E = (size_t)b->hdr.experts_per_layer;
-    return (size_t)top_k * 2 * dff + (size_t)top_k * d + 2 * E + 2 * (size_t)top_k + 64;
+    return (size_t)top_k * 2 * dff + (size_t)top_k * d + 4 * E + 4 + 2 * K2T_MOE_MAX_TOPK + 2 * (size_t)top_k + 64;
 }
 
 MoeWork moe_work_carve(float *base, const k2t_experts *b, int top_k) {
@@ -412,7 +250,9 @@ MoeWork moe_work_carve(float *base, const k2t_experts *b, int top_k) {
     w.eo = p;
     p += (size_t)top_k * d;
     w.words = reinterpret_cast<unsigned long long *>(p);
-    p += 2 * E;
+    p += 4 * E + 4;
+    w.pub = reinterpret_cast<unsigned long long *>(p);
+    p += 2 * K2T_MOE_MAX_TOPK;
     w.wts = p;
     p += top_k;
     w.ids = reinterpret_cast<int *>(p);

@@ -21,42 +21,52 @@ from model_oracle import Matrix, OracleModel, moe_ffn, quantize_matrix
 pytestmark = pytest.mark.gpu
 
 
-def _moe_dict(experts, router, top_k, norm, scoring):
-    return dict(router_w=router, router_b=None, top_k=top_k, norm_topk_prob=norm, scoring=scoring,
+def _moe_dict(experts, router, top_k, norm, scoring, bias=None):
+    return dict(router_w=router, router_b=bias, top_k=top_k, norm_topk_prob=norm, scoring=scoring,
                 experts=experts)
 
 
-def _well_separated(hidden, post_norm, eps, router, k):
+def _well_separated(hidden, post_norm, eps, router, k, bias=None):
     from model_oracle import rms_norm
     z = router.astype(np.float64) @ rms_norm(hidden, post_norm, eps).astype(np.float64)
+    if bias is not None:
+        z = z + bias
     s = np.sort(z)[::-1][:k + 1]
     return np.min(np.abs(np.diff(s))) > 1e-3
 
 
-@pytest.mark.parametrize("bits,E,k,scoring,norm", [(3, 16, 4, 0, True), (4, 16, 4, 0, False), (3, 64, 8, 1, True),
-                                                    (3, 32, 6, 2, True)])
-def test_moe_ffn_matches_oracle(gpu_ctx, bits, E, k, scoring, norm):
-    print(f"moe_ffn bits={bits} E={E} k={k} scoring={scoring}", flush=True)
-    d, dff = 256, 128
-    rng = np.random.default_rng(100 + E + bits)
+# d <= 2048 routes inside the gate_up launch (two waves per router row); d = 3072 takes the
+# separate route kernel; the biased case covers the bias added after the two halves.
+@pytest.mark.parametrize("bits,E,k,scoring,norm,d,biased", [(3, 16, 4, 0, True, 256, False),
+                                                           (4, 16, 4, 0, False, 256, False),
+                                                           (3, 64, 8, 1, True, 256, False),
+                                                           (3, 32, 6, 2, True, 256, False),
+                                                           (3, 48, 4, 2, True, 256, True),
+                                                           (3, 16, 4, 0, True, 3072, True)])
+def test_moe_ffn_matches_oracle(gpu_ctx, bits, E, k, scoring, norm, d, biased):
+    print(f"moe_ffn bits={bits} E={E} k={k} scoring={scoring} d={d} biased={biased}", flush=True)
+    dff = 128
+    rng = np.random.default_rng(100 + E + bits + d)
     layers = [random_moe_layer(rng, d, dff, E, bits=bits) for _ in range(2)]
+    bias = (0.3 * rng.standard_normal(E)).astype(np.float32) if biased else None
     blob = write_k2tm([l[0] for l in layers], d, dff, bits, 2)
     bank = k2t.ExpertBank.upload(gpu_ctx, blob)
     assert bank.info()["experts_per_layer"] == E
     post_norm = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
     ids = torch.zeros(k, dtype=torch.int32, device="cuda")
     wts = torch.zeros(k, dtype=torch.float32, device="cuda")
+    dbias = torch.from_numpy(bias).cuda() if biased else None
     checked = 0
     for trial in range(12):
         hidden = rng.standard_normal(d).astype(np.float32)
         layer = trial % 2
         experts, router = layers[layer]
-        if not _well_separated(hidden, post_norm, 1e-6, router, k):
+        if not _well_separated(hidden, post_norm, 1e-6, router, k, bias):
             continue
-        want, routes = moe_ffn(hidden, post_norm, 1e-6, _moe_dict(experts, router, k, norm, scoring))
+        want, routes = moe_ffn(hidden, post_norm, 1e-6, _moe_dict(experts, router, k, norm, scoring, bias))
         dh = torch.from_numpy(hidden).cuda()
         gpu_ctx.moe_ffn(bank, layer, torch.from_numpy(router).cuda(), dh, torch.from_numpy(post_norm).cuda(), 1e-6,
-                        k, norm, scoring, route_ids=ids, route_weights=wts)
+                        k, norm, scoring, router_bias=dbias, route_ids=ids, route_weights=wts)
         gpu_ctx.sync()
         got_ids = ids.cpu().numpy().tolist()
         assert got_ids == [e for e, _ in routes], f"trial {trial}: routes {got_ids} vs {routes}"
