@@ -80,6 +80,8 @@ class GemvCase:
             else:
                 self.mats.append(ctx.wrap_nf(rows, cols, self.bits, 2, self.cb, p, pair.size,
                                              t if tail.size else None, tail.size))
+                # NF3: the device's lane order (what k2t_mat_upload_nf stores), set up once
+                self.mats[-1].nf3_lane_order()
         self.pair_host, self.tail_host = pair, tail
         rng = np.random.default_rng(SEED + cols)
         x = rng.standard_normal((ntok, cols)).astype(np.float32)
@@ -208,6 +210,7 @@ def moe_decode_bench(ctx, torch, steps, warmup, context, log):
         sl.copy_(pool_d[j].unsqueeze(0).expand(sl.shape[0], rec))
     del pool_d
     bank = k2t.ExpertBank.wrap(ctx, bank_t, bank_t.numel(), page)
+    bank.nf3_lane_order()  # the device's NF3 lane order (what k2t_experts_upload stores), once
     model = k2t.Model(ctx, cfg, max_batch=1)
     mats = []
     ones_d, ones_hd = np.ones(d, np.float32), np.ones(hd, np.float32)

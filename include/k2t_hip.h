@@ -113,6 +113,12 @@ int32_t k2t_mat_wrap_nibble4(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t h
 int32_t k2t_mat_wrap_nf(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t bits, int32_t sgc,
                         const int8_t *codebook16, const void *d_pair, size_t pair_len,
                         const void *d_tail, size_t tail_len, k2t_mat **out);
+/* No counterpart in the reference: a device-layout step.  An NF3 matrix's streams
+ * rearranged IN PLACE into lane order (see k2t_experts_nf3_lane_order); k2t_mat_upload_nf
+ * stores NF3 in this order, k2t_mat_wrap_nf leaves the borrowed bytes in the reference
+ * layout until this call.  Results are unchanged; no-op for other formats and matrices
+ * already converted; synchronous. */
+int32_t k2t_mat_nf3_lane_order(k2t_mat *m);
 void k2t_mat_destroy(k2t_mat *m);
 /* rows, cols, stripes and streamed bytes (pair + tail + codebook). */
 int32_t k2t_mat_info(const k2t_mat *m, int32_t *rows, int32_t *cols, int32_t *stripes,
@@ -356,12 +362,21 @@ typedef struct k2t_k2tm_layout {
 int32_t k2t_k2tm_read_header(const uint8_t *page, size_t len, k2t_k2tm_header *out);
 int32_t k2t_k2tm_expert_layout(int64_t d_model, int64_t d_ff, int32_t bits, int32_t sgc, k2t_k2tm_layout *out);
 /* A whole shard (header page + every record) copied into HBM (MoeExpertBackend::ZeroCopyMmap,
- * sparse_moe.rs:1025-1045, with HBM in place of the mapping: no paging). */
+ * sparse_moe.rs:1025-1045, with HBM in place of the mapping: no paging).  NF3 experts are
+ * stored in lane order (k2t_experts_nf3_lane_order). */
 int32_t k2t_experts_upload(k2t_ctx *ctx, const uint8_t *k2tm, size_t len, k2t_experts **out);
 /* A shard already in device memory (borrowed; 256-byte aligned), described by its host
- * header page. */
+ * header page.  The bytes stay in the .k2tm layout until k2t_experts_nf3_lane_order. */
 int32_t k2t_experts_wrap(k2t_ctx *ctx, const uint8_t *d_k2tm, size_t len, const uint8_t *header_page,
                          k2t_experts **out);
+/* No counterpart in the reference: a device-layout step.  Rearranges every NF3 expert
+ * matrix of the bank IN PLACE (the borrowed bytes of a wrapped bank included) so that each
+ * 384-byte stripe-chunk (8 triplet blocks of 48 bytes, simd_lut.rs:4932-4960) holds 16-byte
+ * piece k of block (g, half) at 128*k + 16*(2g + half) instead of 192*half + 48*g + 16*k:
+ * the grouped GEMV then reads one 128-byte run per lane group and load.  Results are
+ * unchanged.  No-op for NF4 banks and for banks already converted; synchronous.  The bytes
+ * are no longer in the .k2tm layout afterwards (convert a shard once, not per wrap). */
+int32_t k2t_experts_nf3_lane_order(k2t_experts *bank);
 void k2t_experts_destroy(k2t_experts *b);
 int32_t k2t_experts_info(const k2t_experts *b, k2t_k2tm_header *out);
 /* One token through one MoE layer (forward_layer_single, sparse_moe.rs:961-1084, plus the

@@ -158,6 +158,20 @@ static k2t_mat *make_nibble4(k2t_ctx *ctx, int rows, int cols, int hp, const voi
     return m;
 }
 
+// NF3 streams in place into lane order (a no-op for other formats and for matrices
+// already converted); synchronous.
+static void nf3_to_lane_order(k2t_mat *m) {
+    if (m->fmt != K2T_FMT_NF || m->bits != 3 || m->nf3_lane) return;
+    hip_check(hipSetDevice(m->device), "hipSetDevice");
+    if (m->pairs)
+        launch_nf3_lane_order(m->ctx->stream, const_cast<uint8_t *>(m->pair), 0, 1, m->pair_len / m->pairs, m->pairs,
+                              m->nc, m->sgc, false);
+    if (m->has_tail)
+        launch_nf3_lane_order(m->ctx->stream, const_cast<uint8_t *>(m->tail), 0, 1, 0, 1, m->nc, m->sgc, true);
+    hip_check(hipStreamSynchronize(m->ctx->stream), "nf3 lane order");
+    m->nf3_lane = 1;
+}
+
 static k2t_mat *make_nf(k2t_ctx *ctx, int rows, int cols, int bits, int sgc, const int8_t *cb,
                         const void *pair, size_t pl, const void *tail, size_t tl, bool device_src) {
     arg_check(ctx != nullptr, "ctx is NULL");
@@ -181,8 +195,9 @@ static k2t_mat *make_nf(k2t_ctx *ctx, int rows, int cols, int bits, int sgc, con
     m->tail_len = tl;
     try {
         upload_streams(m, (const uint8_t *)pair, pl, (const uint8_t *)tail, tl, device_src);
+        if (!device_src && bits == 3) nf3_to_lane_order(m);  // our own copy: the fast layout
     } catch (...) {
-        delete m;
+        k2t_mat_destroy(m);
         throw;
     }
     return m;
@@ -341,6 +356,13 @@ int32_t k2t_mat_wrap_nf(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t bits, 
     return guarded([&] {
         arg_check(out != nullptr, "out is NULL");
         *out = make_nf(ctx, rows, cols, bits, sgc, codebook16, d_pair, pair_len, d_tail, tail_len, true);
+    });
+}
+
+int32_t k2t_mat_nf3_lane_order(k2t_mat *m) {
+    return guarded([&] {
+        arg_check(m != nullptr, "mat is NULL");
+        nf3_to_lane_order(m);
     });
 }
 

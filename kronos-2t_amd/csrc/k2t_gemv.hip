@@ -288,6 +288,7 @@ struct Frag {
 template <int FMT, int HP, int NT, bool DOTS, int XS>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     constexpr int NH = HP == 0 ? 1 : (HP == 1 ? 2 : 4);
+    constexpr bool kNF3 = FMT >= 2, kLane = FMT == 3;  // NF3; FMT 3: stripe-chunks in lane order
     extern __shared__ float lds[];
     const uint32_t lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -359,7 +360,11 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         nib_off = (is_tail ? 32u : 64u + side * 512u) + g * 32u + half * 16u;
         sc_off = is_tail ? 0u : side * 32u;
     } else {
-        nib_off = (is_tail ? 32u : 64u + side * 384u) + half * 192u + g * 48u;
+        // FMT 2: the lane's 48-byte triplet block, read as three consecutive 16-byte
+        // pieces (eight lanes of a group touch three 128-byte lines per load); FMT 3: the
+        // same pieces stored in lane order (piece k of lane 2g + half at k*128 + 16*(2g +
+        // half), nf3_lane_order_kernel), so each load reads one 128-byte run per group.
+        nib_off = (is_tail ? 32u : 64u + side * 384u) + (kLane ? (2u * g + half) * 16u : half * 192u + g * 48u);
         sc_off = is_tail ? 0u : side * 32u;
     }
     sc_off += (4u * g + 2u * half) * 2u;
@@ -426,9 +431,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             rec = gb + (size_t)sb * (is_tail ? CB : 2 * CB);
             scp = gb;
         }
-        if constexpr (FMT == 2) {
+        if constexpr (kNF3) {
 #pragma unroll
-            for (int kk = 0; kk < 3; kk++) fr.w[kk] = load_stream16(rec + nib_off + kk * 16);
+            for (int kk = 0; kk < 3; kk++) fr.w[kk] = load_stream16(rec + nib_off + kk * (kLane ? 128 : 16));
         } else {
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) fr.w[kk] = load_stream16(rec + nib_off + kk * 128);
@@ -448,7 +453,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
 #pragma unroll
             for (int kk = 0; kk < 4; kk++)
                 fr.x[t][kk] = *reinterpret_cast<const uint2 *>(P.xq + (size_t)(tok0 + t) * P.K + c * 64 +
-                                                               (FMT == 2 ? half * 32 + kk * 8 : kk * 16 + half * 8));
+                                                               (kNF3 ? half * 32 + kk * 8 : kk * 16 + half * 8));
             fr.sx[t] = P.xs[(size_t)(tok0 + t) * P.nc + c];
             if constexpr (FMT == 0) fr.sum[t] = P.xsum[(size_t)(tok0 + t) * P.nc + c];
         }
@@ -469,7 +474,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
 #pragma unroll
             for (int kk = 0; kk < 4; kk++)
                 fr.x[0][kk] = *reinterpret_cast<const uint2 *>(xl + c * 64 +
-                                                              (FMT == 2 ? half * 32 + kk * 8 : kk * 16 + half * 8));
+                                                              (kNF3 ? half * 32 + kk * 8 : kk * 16 + half * 8));
             fr.sx[0] = xsl[c];
             if constexpr (FMT == 0) fr.sum[0] = xsuml[c];
         }
@@ -478,7 +483,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         for (int t = 0; t < NT; t++)
 #pragma unroll
             for (int j = 0; j < 4; j++) acc[t][j] = 0;
-        if constexpr (FMT == 2) {
+        if constexpr (kNF3) {
             // NF3 triplets (simd_lut.rs:4932-4960): bytes (v0, v1, v2) of row j, column
             // group t hold the 3-bit codes of columns k0*16 + 4q + t (q = 0..3, codes 0-3)
             // and k1*16 + 4q + t (codes 4-7), k0 = 2*half, k1 = k0 + 1.  Four columns per
@@ -511,7 +516,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             }
         }
 #pragma unroll
-        for (int kk = 0; kk < (FMT == 2 ? 0 : 4); kk++) {
+        for (int kk = 0; kk < (kNF3 ? 0 : 4); kk++) {
             const uint32_t wd[4] = {fr.w[kk].x, fr.w[kk].y, fr.w[kk].z, fr.w[kk].w};
             uint4 hv = make_uint4(0, 0, 0, 0);
             if constexpr (HP == 2) hv = fr.h[kk];
@@ -629,7 +634,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
                 // their loads are outstanding, the activation is in LDS.  (The compiler does
                 // not know the copies write LDS and could move the activation reads up to
                 // its own, later, wait for fa.)
-                constexpr int kFetchLoads = (FMT == 2 ? 3 : 4) + (FMT == 0 ? (HP == 0 ? 0 : HP == 1 ? 2 : 4) : 0) + 1;
+                constexpr int kFetchLoads = (kNF3 ? 3 : 4) + (FMT == 0 ? (HP == 0 ? 0 : HP == 1 ? 2 : 4) : 0) + 1;
                 wait_vmcnt<2 * kFetchLoads>();
                 int i = 0;
                 for (; i + 2 < iters; i += 2) {
@@ -758,6 +763,51 @@ uint64_t hadamard_sign_mask_host(uint64_t block) {
     return mask;
 }
 
+// NF3 stripe-chunks (384 bytes: 8 triplet blocks of 48 bytes, block 4*half + g holding
+// rows 4g..4g+3 of the 32-column half `half`, simd_lut.rs:4932-4960) rearranged in place
+// into lane order: 16-byte piece k (k = 0..2) of block (g, half) moves from
+// 192*half + 48*g + 16*k to 128*k + 16*(2g + half).  One thread per stripe-chunk.  Chunk c
+// of a pair record sits at (c / sgc) * 64 + c * 768 + 64 + side * 384 (a 64-byte scale
+// header per scale group, then the groups' [side 0, side 1] chunks); of the tail stripe at
+// (c / sgc) * 32 + c * 384 + 32.  Records: nrec matrices rec_stride bytes apart.
+__global__ void nf3_lane_order_kernel(uint8_t *base, size_t rec_stride, int nrec, size_t ptot, int pairs, int nc,
+                                      int sgc, int tail) {
+    const size_t per_rec = (size_t)pairs * nc * (tail ? 1 : 2);
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= per_rec * (size_t)nrec) return;
+    const size_t r = t / per_rec, u = t % per_rec;
+    uint8_t *chunk;
+    if (tail) {
+        const int c = (int)u;
+        chunk = base + r * rec_stride + (size_t)(c / sgc) * 32 + (size_t)c * 384 + 32;
+    } else {
+        const int side = (int)(u & 1), c = (int)((u >> 1) % (size_t)nc);
+        const size_t p = (u >> 1) / (size_t)nc;
+        chunk = base + r * rec_stride + p * ptot + (size_t)(c / sgc) * 64 + (size_t)c * 768 + 64 + (size_t)side * 384;
+    }
+    uint4 *q = reinterpret_cast<uint4 *>(chunk);
+    uint4 v[24];
+#pragma unroll
+    for (int i = 0; i < 24; i++) v[i] = q[i];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int k = 0; k < 3; k++) q[k * 8 + 2 * g + h] = v[h * 12 + g * 3 + k];
+}
+
+void launch_nf3_lane_order(hipStream_t st, uint8_t *base, size_t rec_stride, int nrec, size_t ptot, int pairs,
+                           int nc, int sgc, bool tail) {
+    if ((((uintptr_t)base) | rec_stride | ptot) % 16)
+        throw Error(K2T_E_ARG, "NF3 streams must be 16-byte aligned");
+    const size_t n = (size_t)pairs * nc * (tail ? 1 : 2) * (size_t)nrec;
+    if (n == 0) return;
+    hipLaunchKernelGGL(nf3_lane_order_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, base, rec_stride,
+                       nrec, ptot, pairs, nc, sgc, tail ? 1 : 0);
+    hip_check(hipGetLastError(), "nf3 lane order launch");
+}
+
 GemvPlan plan_gemv(const k2t_ctx *ctx, const k2t_mat *m, int s0, int s1) {
     GemvPlan p;
     const int npairs = std::min(m->pairs + m->has_tail, (s1 + 1) / 2) - s0 / 2;
@@ -814,7 +864,8 @@ static void launch_nt(int nt, int xs, dim3 grid, dim3 block, size_t lds, hipStre
 template <bool DOTS>
 static void launch_fmt(const k2t_mat *m, int nt, int xs, dim3 grid, dim3 block, size_t lds, hipStream_t st,
                        const GemvParams &P) {
-    if (m->fmt == K2T_FMT_NF && m->bits == 3) launch_nt<2, 0, DOTS>(nt, xs, grid, block, lds, st, P);
+    if (m->fmt == K2T_FMT_NF && m->bits == 3 && m->nf3_lane) launch_nt<3, 0, DOTS>(nt, xs, grid, block, lds, st, P);
+    else if (m->fmt == K2T_FMT_NF && m->bits == 3) launch_nt<2, 0, DOTS>(nt, xs, grid, block, lds, st, P);
     else if (m->fmt == K2T_FMT_NF) launch_nt<1, 0, DOTS>(nt, xs, grid, block, lds, st, P);
     else if (m->hp == 0) launch_nt<0, 0, DOTS>(nt, xs, grid, block, lds, st, P);
     else if (m->hp == 1) launch_nt<0, 1, DOTS>(nt, xs, grid, block, lds, st, P);

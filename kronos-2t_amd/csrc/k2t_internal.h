@@ -40,6 +40,7 @@ struct k2t_mat {
     const uint8_t *pair = nullptr, *tail = nullptr;
     size_t pair_len = 0, tail_len = 0;
     bool owns = false;
+    int32_t nf3_lane = 0;  // NF3 stripe-chunks in lane order (launch_nf3_lane_order)
 };
 
 namespace k2t {
@@ -54,6 +55,12 @@ void set_last_error(const std::string &msg);
 
 // Grows the context's scratch buffer (synchronous allocation).
 void ensure_scratch(k2t_ctx *ctx, size_t floats);
+
+// Rearranges NF3 stripe-chunks in place into the lane order the GEMV streams fastest:
+// nrec matrices rec_stride bytes apart, each `pairs` pair records of ptot bytes (or, with
+// tail set, one tail stripe), nc chunks, scale groups of sgc chunks.
+void launch_nf3_lane_order(hipStream_t st, uint8_t *base, size_t rec_stride, int nrec, size_t ptot, int pairs,
+                           int nc, int sgc, bool tail);
 
 struct GemvPlan {
     int stripe_mode;   // 1: one workgroup per stripe, 0: per stripe pair

@@ -275,6 +275,22 @@ void check_moe_args(const k2t_experts *bank, int shard_layer, int top_k, int sco
         throw Error(K2T_E_ARG, "expert dimensions exceed the Hadamard sign table");
 }
 
+// NF3 expert matrices of every record, in place, into lane order (launch_nf3_lane_order);
+// a no-op for NF4 banks and for banks already converted; synchronous.
+static void bank_to_lane_order(k2t_experts *b) {
+    if (b->hdr.bits != 3 || b->gu.nf3_lane) return;
+    const int nrec = (int)(b->hdr.num_layers * b->hdr.experts_per_layer);
+    uint8_t *rec0 = b->d_bytes + kK2tmPage;
+    hipStream_t st = b->ctx->stream;
+    hip_check(hipSetDevice(b->ctx->device), "hipSetDevice");
+    launch_nf3_lane_order(st, rec0 + b->lay.gu_pair_off, b->lay.aligned_bytes, nrec, b->lay.gu_pair_bytes / b->gu.pairs,
+                          b->gu.pairs, b->gu.nc, b->gu.sgc, false);
+    launch_nf3_lane_order(st, rec0 + b->lay.dn_pair_off, b->lay.aligned_bytes, nrec, b->lay.dn_pair_bytes / b->dn.pairs,
+                          b->dn.pairs, b->dn.nc, b->dn.sgc, false);
+    hip_check(hipStreamSynchronize(st), "k2tm nf3 lane order");
+    b->gu.nf3_lane = b->dn.nf3_lane = 1;
+}
+
 }  // namespace k2t
 
 using namespace k2t;
@@ -346,7 +362,20 @@ int32_t k2t_experts_upload(k2t_ctx *ctx, const uint8_t *k2tm, size_t len, k2t_ex
             k2t_experts_destroy(b);
             hip_check(c, "k2tm upload");
         }
+        try {
+            bank_to_lane_order(b);  // our own copy: the fast NF3 layout
+        } catch (...) {
+            k2t_experts_destroy(b);
+            throw;
+        }
         *out = b;
+    });
+}
+
+int32_t k2t_experts_nf3_lane_order(k2t_experts *bank) {
+    return mguard([&] {
+        if (!bank) throw Error(K2T_E_ARG, "NULL argument");
+        bank_to_lane_order(bank);
     });
 }
 

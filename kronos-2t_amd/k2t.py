@@ -57,6 +57,7 @@ SIGNATURES = {
     "k2t_mat_upload_nf": (I32, [VP, I32, I32, I32, I32, VP, VP, SZ, VP, SZ, C.POINTER(VP)]),
     "k2t_mat_wrap_nibble4": (I32, [VP, I32, I32, I32, VP, SZ, VP, SZ, C.POINTER(VP)]),
     "k2t_mat_wrap_nf": (I32, [VP, I32, I32, I32, I32, VP, VP, SZ, VP, SZ, C.POINTER(VP)]),
+    "k2t_mat_nf3_lane_order": (I32, [VP]),
     "k2t_mat_destroy": (None, [VP]),
     "k2t_mat_info": (I32, [VP, C.POINTER(I32), C.POINTER(I32), C.POINTER(I32), C.POINTER(C.c_uint64)]),
     "k2t_act_quant": (I32, [VP, VP, VP, VP, I32, I32, VP, VP, VP]),
@@ -93,6 +94,7 @@ SIGNATURES = {
     "k2t_k2tm_expert_layout": (I32, [C.c_int64, C.c_int64, I32, I32, VP]),
     "k2t_experts_upload": (I32, [VP, VP, SZ, C.POINTER(VP)]),
     "k2t_experts_wrap": (I32, [VP, VP, SZ, VP, C.POINTER(VP)]),
+    "k2t_experts_nf3_lane_order": (I32, [VP]),
     "k2t_experts_destroy": (None, [VP]),
     "k2t_experts_info": (I32, [VP, VP]),
     "k2t_moe_ffn": (I32, [VP, VP, I32, VP, VP, I32, I32, I32, VP, VP, C.c_float, VP, VP]),
@@ -322,6 +324,11 @@ class ExpertBank:
         check(lib().k2t_experts_wrap(ctx.h, _p(d_tensor), nbytes, hp.ctypes.data_as(VP), C.byref(h)))
         return cls(ctx, h, keep=d_tensor)
 
+    def nf3_lane_order(self):
+        """k2t_experts_nf3_lane_order: NF3 experts rearranged in place into the GEMV's lane order
+        (a wrapped bank's borrowed bytes included)."""
+        check(lib().k2t_experts_nf3_lane_order(self.h))
+
     def info(self):
         h = K2tmHeader()
         check(lib().k2t_experts_info(self.h, C.byref(h)))
@@ -346,6 +353,10 @@ class Mat:
         self.rows = rows
         self.cols = cols
         self._keep = keep
+
+    def nf3_lane_order(self):
+        """k2t_mat_nf3_lane_order: an NF3 matrix's streams rearranged in place into lane order."""
+        check(lib().k2t_mat_nf3_lane_order(self.h))
 
     def info(self):
         r, c, s, b = I32(), I32(), I32(), C.c_uint64()

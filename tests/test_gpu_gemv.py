@@ -159,6 +159,50 @@ def test_nf3_gemv_exact(gpu_ctx, sgc, rows, cols):
     assert _close(_run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows, exact=False)[0], ref)
 
 
+@pytest.mark.parametrize("rows,cols,sgc", [(40, 256, 1), (1536, 2048, 2)])
+def test_nf3_lane_order_wrap_and_convert(gpu_ctx, rows, cols, sgc):
+    """A wrapped NF3 matrix streams the reference layout (simd_lut.rs:4932-4960) as it
+    lies; k2t_mat_nf3_lane_order rearranges it in place (16-byte piece k of triplet block
+    (g, half) from 192*half + 48*g + 16*k to 128*k + 16*(2g + half) of each 384-byte
+    stripe-chunk), and the GEMV gives the same bit-exact rows before and after, as does
+    an uploaded copy (stored in lane order at upload).  A second conversion is a no-op."""
+    import torch
+    rng = np.random.default_rng(rows + sgc + 91)
+    idx, sc, pair, tail = random_nf_streams(rng, rows, cols, sgc, bits=3)
+    cb = np.zeros(16, np.int8)
+    cb[:8] = np.sort(rng.choice(np.arange(-127, 128), 8, replace=False)).astype(np.int8)
+    dp = torch.from_numpy(pair.copy()).cuda()
+    dt = torch.from_numpy(tail.copy()).cuda() if tail.size else None
+    m = gpu_ctx.wrap_nf(rows, cols, 3, sgc, cb, dp, pair.size, dt, tail.size)
+    xq, xs, xsum = acts(rng, cols, 1, n_outliers=3, zero_chunk=1)
+    ref = O.nf_gemv(pair, tail, rows, cols, 3, sgc, cb, xq[0], xs[0])
+    before = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
+    assert np.array_equal(before.view(np.uint32), ref.view(np.uint32))
+    m.nf3_lane_order()
+    got = dp.cpu().numpy()
+    # literal positions inside the first pair record's chunk 0, side 0 (at byte 64, after
+    # the 64-byte scale header), when the matrix has pair records
+    if rows >= 32:
+        c0 = 64
+        for (g, h, k) in [(0, 0, 0), (1, 1, 2), (3, 0, 1), (2, 1, 0), (3, 1, 2)]:
+            src = c0 + 192 * h + 48 * g + 16 * k
+            dst = c0 + 128 * k + 16 * (2 * g + h)
+            assert np.array_equal(got[dst:dst + 16], pair[src:src + 16]), (g, h, k)
+        assert np.array_equal(got[:64], pair[:64])  # scale header untouched
+    assert np.array_equal(np.sort(got), np.sort(pair))
+    if dt is not None:
+        assert np.array_equal(np.sort(dt.cpu().numpy()), np.sort(tail))
+    after = _run_gemv(gpu_ctx, m, xq[0], xs[0], xsum[0], rows)[0]
+    assert np.array_equal(after.view(np.uint32), ref.view(np.uint32))
+    m.nf3_lane_order()
+    assert np.array_equal(dp.cpu().numpy(), got)
+    up = gpu_ctx.upload_nf(rows, cols, 3, sgc, cb, pair, tail)
+    assert np.array_equal(_run_gemv(gpu_ctx, up, xq[0], xs[0], xsum[0], rows)[0].view(np.uint32),
+                          ref.view(np.uint32))
+    m.close()
+    up.close()
+
+
 def test_nf3_expert_slice_pair_range_and_batch(gpu_ctx):
     """nf_sdot_pair_stream_range_slices (simd_lut.rs:6372-6540): an expert's NF3 g128
     gate_up slice (rows % 32 == 0, no tail) run over a pair sub-range writes exactly those

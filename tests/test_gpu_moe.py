@@ -81,6 +81,42 @@ def test_moe_ffn_matches_oracle(gpu_ctx, bits, E, k, scoring, norm, d, biased):
     bank.close()
 
 
+def test_moe_wrapped_bank_lane_order(gpu_ctx):
+    """A wrapped NF3 bank streams the .k2tm layout as it lies; k2t_experts_nf3_lane_order
+    rearranges it in place and the MoE output stays bit-identical, as for an uploaded
+    bank (converted at upload).  Header page and codebooks are untouched."""
+    print("moe wrapped bank lane order", flush=True)
+    d, dff, E, k = 256, 128, 16, 4
+    rng = np.random.default_rng(404)
+    layers = [random_moe_layer(rng, d, dff, E, bits=3) for _ in range(2)]
+    blob = write_k2tm([l[0] for l in layers], d, dff, 3, 2)
+    host = np.frombuffer(blob, np.uint8)
+    dev = torch.from_numpy(host.copy()).cuda()
+    wrapped = k2t.ExpertBank.wrap(gpu_ctx, dev, host.size, host[:16384])
+    uploaded = k2t.ExpertBank.upload(gpu_ctx, blob)
+    post_norm = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    router = torch.from_numpy(layers[1][1]).cuda()
+    pn = torch.from_numpy(post_norm).cuda()
+    hidden = rng.standard_normal(d).astype(np.float32)
+
+    def run(bank):
+        h = torch.from_numpy(hidden).cuda()
+        gpu_ctx.moe_ffn(bank, 1, router, h, pn, 1e-6, k, True, 0)
+        gpu_ctx.sync()
+        return h.cpu().numpy()
+
+    a = run(wrapped)
+    wrapped.nf3_lane_order()
+    got = dev.cpu().numpy()
+    assert np.array_equal(got[:16384], host[:16384])
+    assert not np.array_equal(got, host) and np.array_equal(np.sort(got), np.sort(host))
+    b, c = run(wrapped), run(uploaded)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+    wrapped.close()
+    uploaded.close()
+
+
 def test_moe_ffn_argument_errors(gpu_ctx):
     rng = np.random.default_rng(5)
     experts, router = random_moe_layer(rng, 128, 64, 4, bits=3)
