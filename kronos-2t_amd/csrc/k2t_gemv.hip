@@ -766,35 +766,41 @@ uint64_t hadamard_sign_mask_host(uint64_t block) {
 // NF3 stripe-chunks (384 bytes: 8 triplet blocks of 48 bytes, block 4*half + g holding
 // rows 4g..4g+3 of the 32-column half `half`, simd_lut.rs:4932-4960) rearranged in place
 // into lane order: 16-byte piece k (k = 0..2) of block (g, half) moves from
-// 192*half + 48*g + 16*k to 128*k + 16*(2g + half).  One thread per stripe-chunk.  Chunk c
-// of a pair record sits at (c / sgc) * 64 + c * 768 + 64 + side * 384 (a 64-byte scale
-// header per scale group, then the groups' [side 0, side 1] chunks); of the tail stripe at
-// (c / sgc) * 32 + c * 384 + 32.  Records: nrec matrices rec_stride bytes apart.
-__global__ void nf3_lane_order_kernel(uint8_t *base, size_t rec_stride, int nrec, size_t ptot, int pairs, int nc,
-                                      int sgc, int tail) {
+// 192*half + 48*g + 16*k to 128*k + 16*(2g + half).  Chunk c of a pair record sits at
+// (c / sgc) * 64 + c * 768 + 64 + side * 384 (a 64-byte scale header per scale group,
+// then the groups' [side 0, side 1] chunks); of the tail stripe at (c / sgc) * 32 + c * 384
+// + 32.  Records: nrec matrices rec_stride bytes apart.  A workgroup of 192 threads takes
+// 8 chunks, one thread per 16-byte piece: every piece is read (consecutive threads,
+// consecutive pieces) before the barrier and written to its new place after it.
+constexpr int kLaneChunksPerBlock = 8;
+__global__ __launch_bounds__(192) void nf3_lane_order_kernel(uint8_t *base, size_t rec_stride, int nrec, size_t ptot,
+                                                             int pairs, int nc, int sgc, int tail) {
     const size_t per_rec = (size_t)pairs * nc * (tail ? 1 : 2);
-    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= per_rec * (size_t)nrec) return;
-    const size_t r = t / per_rec, u = t % per_rec;
-    uint8_t *chunk;
-    if (tail) {
-        const int c = (int)u;
-        chunk = base + r * rec_stride + (size_t)(c / sgc) * 32 + (size_t)c * 384 + 32;
-    } else {
-        const int side = (int)(u & 1), c = (int)((u >> 1) % (size_t)nc);
-        const size_t p = (u >> 1) / (size_t)nc;
-        chunk = base + r * rec_stride + p * ptot + (size_t)(c / sgc) * 64 + (size_t)c * 768 + 64 + (size_t)side * 384;
+    const size_t t = (size_t)blockIdx.x * kLaneChunksPerBlock + threadIdx.x / 24;
+    const int op = (int)(threadIdx.x % 24);  // piece index in the reference order
+    const bool live = t < per_rec * (size_t)nrec;
+    uint4 *q = nullptr;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (live) {
+        const size_t r = t / per_rec, u = t % per_rec;
+        uint8_t *chunk;
+        if (tail) {
+            const int c = (int)u;
+            chunk = base + r * rec_stride + (size_t)(c / sgc) * 32 + (size_t)c * 384 + 32;
+        } else {
+            const int side = (int)(u & 1), c = (int)((u >> 1) % (size_t)nc);
+            const size_t p = (u >> 1) / (size_t)nc;
+            chunk = base + r * rec_stride + p * ptot + (size_t)(c / sgc) * 64 + (size_t)c * 768 + 64 +
+                    (size_t)side * 384;
+        }
+        q = reinterpret_cast<uint4 *>(chunk);
+        v = q[op];
     }
-    uint4 *q = reinterpret_cast<uint4 *>(chunk);
-    uint4 v[24];
-#pragma unroll
-    for (int i = 0; i < 24; i++) v[i] = q[i];
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-#pragma unroll
-            for (int k = 0; k < 3; k++) q[k * 8 + 2 * g + h] = v[h * 12 + g * 3 + k];
+    __syncthreads();
+    if (live) {
+        const int h = op / 12, g = (op % 12) / 3, k = op % 3;
+        q[k * 8 + 2 * g + h] = v;
+    }
 }
 
 void launch_nf3_lane_order(hipStream_t st, uint8_t *base, size_t rec_stride, int nrec, size_t ptot, int pairs,
@@ -803,8 +809,9 @@ void launch_nf3_lane_order(hipStream_t st, uint8_t *base, size_t rec_stride, int
         throw Error(K2T_E_ARG, "NF3 streams must be 16-byte aligned");
     const size_t n = (size_t)pairs * nc * (tail ? 1 : 2) * (size_t)nrec;
     if (n == 0) return;
-    hipLaunchKernelGGL(nf3_lane_order_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, base, rec_stride,
-                       nrec, ptot, pairs, nc, sgc, tail ? 1 : 0);
+    const size_t blocks = (n + kLaneChunksPerBlock - 1) / kLaneChunksPerBlock;
+    hipLaunchKernelGGL(nf3_lane_order_kernel, dim3((unsigned)blocks), dim3(24 * kLaneChunksPerBlock), 0, st, base,
+                       rec_stride, nrec, ptot, pairs, nc, sgc, tail ? 1 : 0);
     hip_check(hipGetLastError(), "nf3 lane order launch");
 }
 
