@@ -17,33 +17,44 @@ __device__ __forceinline__ unsigned long long word_load(const unsigned long long
     return __hip_atomic_load(const_cast<unsigned long long *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Largest (value, lowest index on ties) over the wave; returns the lane's view of it.
-// The order is total (larger value, then lower index), so any reduction tree gives the
-// same pick: rotations by 1, 2, 4 and 8 inside each 16-lane row (DPP, no LDS round trip),
-// then the four rows' results compared through v_readlane.
-__device__ __forceinline__ void take_better(float &v, int &i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) {
-        v = ov;
-        i = oi;
-    }
+// Candidate keys: the score's bits made order-preserving as an unsigned number (negative
+// values inverted, positive ones with the top bit set; -0 is added to +0 first so the two
+// zeros tie as floats do) in the high word, ~index in the low word.  The largest key is
+// the largest score with the lowest index among equals, the order of the reference's
+// strict comparisons, and it is one unsigned 64-bit comparison: no branch per step.
+__device__ __forceinline__ unsigned long long score_key(float v, int idx) {
+    uint32_t u = __float_as_uint(v + 0.0f);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
 }
+__device__ __forceinline__ float key_score(unsigned long long k) {
+    const uint32_t u = (uint32_t)(k >> 32);
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+__device__ __forceinline__ int key_index(unsigned long long k) { return (int)(0xFFFFFFFFu - (uint32_t)k); }
+
 template <int CTRL>
-__device__ __forceinline__ void row_rotate_argmax(float &v, int &i) {
-    const float ov = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
-    const int oi = __builtin_amdgcn_mov_dpp(i, CTRL, 0xF, 0xF, false);
-    take_better(v, i, ov, oi);
+__device__ __forceinline__ void row_rotate_max(unsigned long long &k) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)k, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(k >> 32), CTRL, 0xF, 0xF, false);
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    k = o > k ? o : k;
 }
-__device__ __forceinline__ void wave_argmax(float &v, int &i) {
-    row_rotate_argmax<0x121>(v, i);  // row_ror:1
-    row_rotate_argmax<0x122>(v, i);  // row_ror:2
-    row_rotate_argmax<0x124>(v, i);  // row_ror:4
-    row_rotate_argmax<0x128>(v, i);  // row_ror:8
-    float bv = lane_val(v, 0);
-    int bi = lane_val(i, 0);
+// The largest key of the wave (uniform): rotations by 1, 2, 4 and 8 inside each 16-lane
+// row (DPP), then the four rows' results read with v_readlane.
+__device__ __forceinline__ unsigned long long wave_max_key(unsigned long long k) {
+    row_rotate_max<0x121>(k);  // row_ror:1
+    row_rotate_max<0x122>(k);  // row_ror:2
+    row_rotate_max<0x124>(k);  // row_ror:4
+    row_rotate_max<0x128>(k);  // row_ror:8
+    unsigned long long b = 0;
 #pragma unroll
-    for (int r = 1; r < 4; r++) take_better(bv, bi, lane_val(v, 16 * r), lane_val(i, 16 * r));
-    v = bv;
-    i = bi;
+    for (int r = 0; r < 4; r++) {
+        const unsigned long long o = ((unsigned long long)(uint32_t)lane_val((int)(k >> 32), 16 * r) << 32) |
+                                     (uint32_t)lane_val((int)(uint32_t)k, 16 * r);
+        b = o > b ? o : b;
+    }
+    return b;
 }
 
 // route_sorted (sparse_moe.rs:86-182) for E <= 256 experts on one wave.  With `pub` set,
@@ -76,27 +87,25 @@ __device__ inline void select_routes(float sc[4], int lane, int E, int k, int no
         for (int j = 0; j < 4; j++)
             sc[j] = lane + 64 * j < E && sc[j] == sc[j] ? 1.0f / (1.0f + expf(-sc[j])) : -INFINITY;
     }
-    // Selection round r leaves its (id, score) in lane r's registers.
+    // Selection round r leaves its (id, score) in lane r's registers; a picked key is
+    // replaced by 0, below every real key (-inf's included), for the later rounds.
+    unsigned long long key[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) key[j] = score_key(sc[j], lane + 64 * j);
     int my_id = 0;
     float my_w = 0.0f;
     for (int r = 0; r < k; r++) {
-        float bv = sc[0];
-        int bi = lane;
+        unsigned long long b = key[0];
 #pragma unroll
-        for (int j = 1; j < 4; j++)
-            if (sc[j] > bv) {
-                bv = sc[j];
-                bi = lane + 64 * j;
-            }
-        wave_argmax(bv, bi);
-        bi = min(bi, E - 1);  // every id indexes a record of the bank, whatever the scores
+        for (int j = 1; j < 4; j++) b = key[j] > b ? key[j] : b;
+        b = wave_max_key(b);
+        const int bi = key_index(b);
         if (lane == r) {
-            my_id = bi;
-            my_w = bv;
+            my_id = min(bi, E - 1);  // every id indexes a record of the bank, whatever the scores
+            my_w = key_score(b);
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (lane + 64 * j == bi) sc[j] = -INFINITY;
+        for (int j = 0; j < 4; j++) key[j] = lane + 64 * j == bi ? 0ull : key[j];
     }
     // Weight normalization; the sums run over the selections in selection order.
     if (scoring == K2T_MOE_TOPK_SOFTMAX) {

@@ -81,6 +81,38 @@ def test_moe_ffn_matches_oracle(gpu_ctx, bits, E, k, scoring, norm, d, biased):
     bank.close()
 
 
+@pytest.mark.parametrize("scoring", [0, 1, 2])
+def test_moe_route_ties_pick_lowest_id(gpu_ctx, scoring):
+    """Equal router logits (duplicated router rows give bit-identical dots) rank by the
+    lower expert id, as route_sorted's strict comparisons do (sparse_moe.rs:86-182): rows
+    2 and 9 are equal and largest, rows 5, 6 and 12 equal and next, so top-3 = {2, 9, 5}."""
+    print(f"moe route ties scoring={scoring}", flush=True)
+    d, dff, E, k = 256, 128, 16, 3
+    rng = np.random.default_rng(55)
+    layers = [random_moe_layer(rng, d, dff, E, bits=3)]
+    experts, router = layers[0]
+    router = (0.01 * router).astype(np.float32)
+    hidden = rng.standard_normal(d).astype(np.float32)
+    post_norm = np.ones(d, np.float32)
+    xn = hidden / np.sqrt(np.mean(hidden.astype(np.float64) ** 2) + 1e-6)
+    top = (4.0 * xn / np.dot(xn, xn)).astype(np.float32)
+    router[2] = router[9] = top
+    router[5] = router[6] = router[12] = 0.5 * top
+    blob = write_k2tm([experts], d, dff, 3, 2)
+    bank = k2t.ExpertBank.upload(gpu_ctx, blob)
+    ids = torch.zeros(k, dtype=torch.int32, device="cuda")
+    wts = torch.zeros(k, dtype=torch.float32, device="cuda")
+    _, routes = moe_ffn(hidden, post_norm, 1e-6, _moe_dict(experts, router, k, True, scoring))
+    assert [e for e, _ in routes] == [2, 5, 9]
+    gpu_ctx.moe_ffn(bank, 0, torch.from_numpy(router).cuda(), torch.from_numpy(hidden).cuda(),
+                    torch.from_numpy(post_norm).cuda(), 1e-6, k, True, scoring, route_ids=ids, route_weights=wts)
+    gpu_ctx.sync()
+    assert ids.cpu().numpy().tolist() == [2, 5, 9]
+    w = wts.cpu().numpy()
+    assert w[0] == w[2] and np.allclose(w, [x for _, x in routes], rtol=1e-5, atol=1e-7)
+    bank.close()
+
+
 def test_moe_wrapped_bank_lane_order(gpu_ctx):
     """A wrapped NF3 bank streams the .k2tm layout as it lies; k2t_experts_nf3_lane_order
     rearranges it in place and the MoE output stays bit-identical, as for an uploaded
