@@ -117,7 +117,8 @@ int32_t k2t_mat_wrap_nf(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t bits, 
  * rearranged IN PLACE into lane order (see k2t_experts_nf3_lane_order); k2t_mat_upload_nf
  * stores NF3 in this order, k2t_mat_wrap_nf leaves the borrowed bytes in the reference
  * layout until this call.  Results are unchanged; no-op for other formats and matrices
- * already converted; synchronous. */
+ * already converted; synchronous.  A dense stream carries no mark: wrap converted bytes
+ * again only with a matrix that is then converted by no one (or re-upload them). */
 int32_t k2t_mat_nf3_lane_order(k2t_mat *m);
 void k2t_mat_destroy(k2t_mat *m);
 /* rows, cols, stripes and streamed bytes (pair + tail + codebook). */
@@ -366,7 +367,8 @@ int32_t k2t_k2tm_expert_layout(int64_t d_model, int64_t d_ff, int32_t bits, int3
  * stored in lane order (k2t_experts_nf3_lane_order). */
 int32_t k2t_experts_upload(k2t_ctx *ctx, const uint8_t *k2tm, size_t len, k2t_experts **out);
 /* A shard already in device memory (borrowed; 256-byte aligned), described by its host
- * header page.  The bytes stay in the .k2tm layout until k2t_experts_nf3_lane_order. */
+ * header page.  The bytes stay in the .k2tm layout until k2t_experts_nf3_lane_order (a
+ * shard it converted earlier is recognised by its mark and read in lane order). */
 int32_t k2t_experts_wrap(k2t_ctx *ctx, const uint8_t *d_k2tm, size_t len, const uint8_t *header_page,
                          k2t_experts **out);
 /* No counterpart in the reference: a device-layout step.  Rearranges every NF3 expert
@@ -375,7 +377,10 @@ int32_t k2t_experts_wrap(k2t_ctx *ctx, const uint8_t *d_k2tm, size_t len, const 
  * piece k of block (g, half) at 128*k + 16*(2g + half) instead of 192*half + 48*g + 16*k:
  * the grouped GEMV then reads one 128-byte run per lane group and load.  Results are
  * unchanged.  No-op for NF4 banks and for banks already converted; synchronous.  The bytes
- * are no longer in the .k2tm layout afterwards (convert a shard once, not per wrap). */
+ * are no longer in the .k2tm layout afterwards; the conversion writes a 16-byte mark into
+ * the last 16 bytes of the device header page (zero padding in the format), so a later
+ * k2t_experts_wrap of the same bytes reads them in lane order and converting again is a
+ * no-op. */
 int32_t k2t_experts_nf3_lane_order(k2t_experts *bank);
 void k2t_experts_destroy(k2t_experts *b);
 int32_t k2t_experts_info(const k2t_experts *b, k2t_k2tm_header *out);

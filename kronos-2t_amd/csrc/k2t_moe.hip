@@ -275,10 +275,25 @@ void check_moe_args(const k2t_experts *bank, int shard_layer, int top_k, int sco
         throw Error(K2T_E_ARG, "expert dimensions exceed the Hadamard sign table");
 }
 
+// A converted shard says so in the last 16 bytes of its device header page (zero padding
+// in the .k2tm header, past every field), so a later wrap of the same bytes knows their
+// order and a second conversion is a no-op.
+static const char kLaneMark[16] = {'K', '2', 'T', '-', 'N', 'F', '3', '-', 'L', 'A', 'N', 'E', '-', 'V', '1', '\0'};
+static bool bank_marked_lane(const k2t_experts *b) {
+    char got[16];
+    hip_check(hipSetDevice(b->ctx->device), "hipSetDevice");
+    hip_check(hipMemcpy(got, b->d_bytes + kK2tmPage - 16, 16, hipMemcpyDeviceToHost), "k2tm lane mark read");
+    return memcmp(got, kLaneMark, 16) == 0;
+}
+
 // NF3 expert matrices of every record, in place, into lane order (launch_nf3_lane_order);
 // a no-op for NF4 banks and for banks already converted; synchronous.
 static void bank_to_lane_order(k2t_experts *b) {
     if (b->hdr.bits != 3 || b->gu.nf3_lane) return;
+    if (bank_marked_lane(b)) {
+        b->gu.nf3_lane = b->dn.nf3_lane = 1;
+        return;
+    }
     const int nrec = (int)(b->hdr.num_layers * b->hdr.experts_per_layer);
     uint8_t *rec0 = b->d_bytes + kK2tmPage;
     hipStream_t st = b->ctx->stream;
@@ -288,6 +303,7 @@ static void bank_to_lane_order(k2t_experts *b) {
     launch_nf3_lane_order(st, rec0 + b->lay.dn_pair_off, b->lay.aligned_bytes, nrec, b->lay.dn_pair_bytes / b->dn.pairs,
                           b->dn.pairs, b->dn.nc, b->dn.sgc, false);
     hip_check(hipStreamSynchronize(st), "k2tm nf3 lane order");
+    hip_check(hipMemcpy(b->d_bytes + kK2tmPage - 16, kLaneMark, 16, hipMemcpyHostToDevice), "k2tm lane mark");
     b->gu.nf3_lane = b->dn.nf3_lane = 1;
 }
 
@@ -391,6 +407,12 @@ int32_t k2t_experts_wrap(k2t_ctx *ctx, const uint8_t *d_k2tm, size_t len, const 
         k2t_experts *b = make_bank(ctx, h);
         b->d_bytes = const_cast<uint8_t *>(d_k2tm);
         b->owns = false;
+        try {
+            if (h.bits == 3 && bank_marked_lane(b)) b->gu.nf3_lane = b->dn.nf3_lane = 1;  // converted before
+        } catch (...) {
+            delete b;
+            throw;
+        }
         *out = b;
     });
 }

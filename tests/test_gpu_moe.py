@@ -140,12 +140,21 @@ def test_moe_wrapped_bank_lane_order(gpu_ctx):
     a = run(wrapped)
     wrapped.nf3_lane_order()
     got = dev.cpu().numpy()
-    assert np.array_equal(got[:16384], host[:16384])
-    assert not np.array_equal(got, host) and np.array_equal(np.sort(got), np.sort(host))
+    mark = np.frombuffer(b"K2T-NF3-LANE-V1\0", np.uint8)
+    assert np.array_equal(got[:16384 - 16], host[:16384 - 16]) and np.array_equal(got[16384 - 16:16384], mark)
+    assert not host[16384 - 16:16384].any()
+    assert not np.array_equal(got[16384:], host[16384:])
+    assert np.array_equal(np.sort(got[16384:]), np.sort(host[16384:]))
     b, c = run(wrapped), run(uploaded)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+    # a second wrap of the converted bytes reads them in lane order; converting is a no-op
     wrapped.close()
+    again = k2t.ExpertBank.wrap(gpu_ctx, dev, host.size, host[:16384])
+    again.nf3_lane_order()
+    assert np.array_equal(dev.cpu().numpy(), got)
+    assert np.array_equal(run(again).view(np.uint32), a.view(np.uint32))
+    again.close()
     uploaded.close()
 
 
