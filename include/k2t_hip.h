@@ -169,6 +169,12 @@ int32_t k2t_gemv_chunk_dots(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq,
  * the context's stream; d_sink receives a word only if the data's XOR equals a marker.
  * No reference counterpart: it gives the single-launch HBM read ceiling that the GEMV's
  * bandwidth is read against. */
+/* Parity support (no reference counterpart): the exponential the exact-order mode uses,
+ * which returns glibc's expf result for every fp32 input (f32::exp of the x86 reference
+ * build, real_llm.rs:9595 and 9803).  k2t_expf_host runs the routine on the host;
+ * k2t_expf_device applies it on the GPU to n floats (d_x to d_y, on the context's stream). */
+float k2t_expf_host(float x);
+int32_t k2t_expf_device(k2t_ctx *ctx, const float *d_x, float *d_y, size_t n);
 int32_t k2t_stream_read_probe(k2t_ctx *ctx, const void *d_src, size_t bytes, uint32_t *d_sink);
 
 /* ---- offline weight compiler (host memory, multi-threaded) ------------- */
@@ -273,8 +279,16 @@ int32_t k2t_model_kv_window(const k2t_model *m, int32_t *window, int32_t *sink_t
 int32_t k2t_model_kv_synthetic(k2t_model *m, int32_t n_pos, uint64_t seed);
 /* 1 (default): capture the decode step once and replay it as a HIP graph. */
 int32_t k2t_model_set_graph(k2t_model *m, int32_t enable);
-/* GEMV epilogue of this model's steps (see k2t_ctx_set_exact); default 0 = fast.
- * exact = 1 also disables the persistent decode kernel (it sums per-segment chains). */
+/* Operation order of this model's steps; default 0 = fast.
+ * exact = 1 runs every step in the x86 reference build's operation order
+ * (forward_token_sdot_megakernel's portable paths, real_llm.rs:6794-7403): GEMVs with the
+ * in-order fmaf epilogue (k2t_ctx_set_exact), RMSNorm and q / k norm with the sequential
+ * four-accumulator sum of squares (dot_f32_fast, real_llm.rs:911-926), softmax and SwiGLU
+ * with glibc's expf results (k2t_expf_host), attention with sequential softmax and V sums
+ * (real_llm.rs:8533-8545, 8575-8585, 9590-9600).  Logits then equal the x86 reference's
+ * bit for bit on dense models with the int8 KV cache (MoE feed-forwards keep their own
+ * order; the NF4 KV cache is refused with K2T_E_ARG at the step).  Exact steps run the
+ * per-operation path; they are slower and meant for parity checks. */
 int32_t k2t_model_set_exact(k2t_model *m, int32_t exact);
 /* 1 (default): a decode step runs as one persistent kernel (one workgroup per CU) whose
  * phases hand vectors over through {payload, epoch} words instead of kernel boundaries:

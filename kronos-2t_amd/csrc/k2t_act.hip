@@ -8,7 +8,10 @@
 // reference's, so q / scales / sums are bit-identical given the same inputs.
 #include <float.h>
 
+#include <algorithm>
+
 #include "k2t_device.h"
+#include "k2t_expf.h"
 #include "k2t_internal.h"
 
 namespace k2t {
@@ -64,6 +67,58 @@ __global__ __launch_bounds__(256) void inv_rms_kernel(const float *__restrict__ 
         const float tot = (part[0] + part[1]) + (part[2] + part[3]);
         out[blockIdx.x] = 1.0f / sqrtf(tot / (float)K + eps);
     }
+}
+
+// inv_rms[t] = 1 / sqrt(sum(x^2)/K + eps) with the sum of squares in the reference's x86
+// order (dot_f32_fast, portable branch, real_llm.rs:911-926; rms_norm 9858-9861): four
+// accumulators, acc[k] += x[i+k]*x[i+k] over i = 0, 4, 8, ... (each product rounded, then
+// added), (acc0 + acc1) + (acc2 + acc3), then the K % 4 remainder in order.  One wave per
+// token; lanes 0-3 hold the accumulators and run their chains sequentially, eight loads
+// ahead.  Used by the exact-order decode mode.
+__global__ __launch_bounds__(64) void inv_rms_x86_kernel(const float *__restrict__ x, float eps, int K,
+                                                         float *__restrict__ out) {
+    const uint32_t lane = threadIdx.x;
+    const float *xt = x + (size_t)blockIdx.x * K;
+    const int n4 = K / 4;
+    float acc = 0.0f;
+    if (lane < 4) {
+        int j = 0;
+        for (; j + 8 <= n4; j += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = xt[4 * (j + u) + lane];
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc = acc + v[u] * v[u];
+        }
+        for (; j < n4; j++) {
+            const float v = xt[4 * j + lane];
+            acc = acc + v * v;
+        }
+    }
+    const float a0 = lane_val(acc, 0), a1 = lane_val(acc, 1), a2 = lane_val(acc, 2), a3 = lane_val(acc, 3);
+    if (lane == 0) {
+        float sum = (a0 + a1) + (a2 + a3);
+        for (int i = 4 * n4; i < K; i++) sum = sum + xt[i] * xt[i];
+        const float mean_sq = sum / (float)K;
+        out[blockIdx.x] = 1.0f / sqrtf(mean_sq + eps);
+    }
+}
+
+void launch_inv_rms_x86(hipStream_t st, const float *x, float eps, int K, int ntok, float *inv_rms) {
+    if (ntok <= 0) return;
+    hipLaunchKernelGGL(inv_rms_x86_kernel, dim3(ntok), dim3(64), 0, st, x, eps, K, inv_rms);
+    hip_check(hipGetLastError(), "inv_rms_x86 launch");
+}
+
+// y[i] = expf_rn(x[i]) (k2t_expf_device: the exact-order mode's exponential on the GPU).
+__global__ __launch_bounds__(256) void expf_map_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) y[i] = expf_rn(x[i]);
+}
+
+void launch_expf_map(hipStream_t st, const float *x, float *y, size_t n) {
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(expf_map_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, y, n);
+    hip_check(hipGetLastError(), "expf_map launch");
 }
 
 void launch_act_quant(k2t_ctx *ctx, const float *x, const float *w, const float *inv_rms, int K,

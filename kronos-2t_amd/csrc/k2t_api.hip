@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "../../include/k2t_hip.h"
+#include "k2t_expf.h"
 #include "k2t_internal.h"
 
 namespace k2t {
@@ -254,6 +255,7 @@ void k2t_ctx_destroy(k2t_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->rms_scratch) (void)hipFree(ctx->rms_scratch);
+    if (ctx->gqa_words) (void)hipFree(ctx->gqa_words);
     if (ctx->signs) (void)hipFree(ctx->signs);
     delete ctx;
 }
@@ -270,6 +272,7 @@ int32_t k2t_ctx_sync(k2t_ctx *ctx) {
         arg_check(ctx != nullptr, "ctx is NULL");
         hip_check(hipSetDevice(ctx->device), "hipSetDevice");
         hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        check_gqa_timeout(ctx);
     });
 }
 
@@ -439,6 +442,17 @@ int32_t k2t_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq, const float
         hip_check(hipSetDevice(ctx->device), "hipSetDevice");
         launch_gemv(ctx, m, d_xq, d_xs, d_xsum, ntok, s0, s1, d_out, ntok == 1 ? (size_t)m->rows : out_stride,
                     nullptr);
+    });
+}
+
+float k2t_expf_host(float x) { return expf_rn(x); }
+
+int32_t k2t_expf_device(k2t_ctx *ctx, const float *d_x, float *d_y, size_t n) {
+    return guarded([&] {
+        arg_check(ctx && d_x && d_y, "NULL argument");
+        if (n == 0) return;
+        hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+        launch_expf_map(ctx->stream, d_x, d_y, n);
     });
 }
 

@@ -25,6 +25,9 @@ constexpr int kMkSpans512 = 2;
 // Most spans per q head of the kernel with NTH threads per workgroup.
 __host__ __device__ constexpr int mk_max_spans(int nth) { return nth == 512 ? kMkSpans512 : kMkSpans; }
 constexpr int kMkSpanMin = 128;
+// Rows of one GEMV round of a workgroup (wave groups x rows per group), the most the
+// exact-order variant stages epilogue operands for.
+constexpr int kMkTermRows = 128;
 
 struct MkLayer {
     MatDev qkv, o, gu, down;
@@ -67,6 +70,9 @@ struct MkParams {
     const uint64_t *signs;  // Hadamard sign masks of 64-blocks (bit i = element i)
     int *err;
     uint32_t spin_limit;
+    // Exact-order variant only: per workgroup, the GEMV epilogue operands of one round
+    // ({term, scale} words, [row of the round][chunk]; kMkTermRows * kmax/64 words each).
+    unsigned long long *exterm;
     // Measurement builds only (compiled with -DK2T_MK_TRACE): per workgroup, layer and
     // phase the wall clock at the task's start, input arrival and end.
     unsigned long long *trace;
@@ -90,6 +96,7 @@ bool decode_mk_supported(const k2t_model_config &c, int num_cus);
 // models with any 5-plane matrix get hp = kHpMixed: the 256-thread kernel that reads
 // each matrix's plane count (4 or 5).
 bool decode_mk_format(const MatDev &m, int &fmt, int &hp);
-void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds);
+// exact: the exact-order variant (x86 reference operation order; P.exterm set, P.nsp 1).
+void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds, bool exact);
 
 }  // namespace k2t

@@ -33,6 +33,7 @@
 
 #include "../../include/k2t_hip.h"
 #include "k2t_decode_mk.h"
+#include "k2t_expf.h"
 #include "k2t_gemv_core.h"
 #include "k2t_internal.h"
 
@@ -246,14 +247,30 @@ __device__ __forceinline__ NormPre norm_prefetch(const MkParams &P, const float 
 // order (bit-identical to rmsnorm_act_kernel); then sixteen lanes per
 // chunk, four chunks per wave at once (rotate_quant4).  The first slice of each lane uses
 // the prefetched weights and sign mask.
-template <int NTH>
+// EX (exact-order variant): inv_rms from the x86 reference's sum of squares instead
+// (dot_f32_fast, real_llm.rs:911-926: four sequential accumulators over elements k, k + 4,
+// ..., then (acc0 + acc1) + (acc2 + acc3)), lanes 0-3 of wave 0 running the chains.
+template <int NTH, bool EX>
 __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, const NormPre &wp, uint32_t lane,
                                int wave) {
     // 256 threads: every wave computes inv_rms itself (the same order in each), with no
     // barrier between the sum and the slices (135M +0.8%); 512 threads: wave 0 for the
     // workgroup (eight waves reading the row measured 1.1% slower on the 1.7B model)
     float inv_rms;
-    if constexpr (NTH == 256) {
+    if constexpr (EX) {
+        if (wave == 0) {
+            float acc = 0.0f;
+            if (lane < 4)
+                for (int j = 0; j < P.d / 4; j++) {
+                    const float v = S.hbuf[4 * j + lane];
+                    acc = acc + v * v;
+                }
+            const float sum = (lane_val(acc, 0) + lane_val(acc, 1)) + (lane_val(acc, 2) + lane_val(acc, 3));
+            if (lane == 0) S.vec[0] = 1.0f / sqrtf(sum / (float)P.d + P.eps);
+        }
+        lds_barrier();
+        inv_rms = S.vec[0];
+    } else if constexpr (NTH == 256) {
         inv_rms = 1.0f / sqrtf(row_sumsq_wave(S.hbuf, P.d, lane) / (float)P.d + P.eps);
     } else {
         if (wave == 0) {
@@ -294,7 +311,7 @@ enum PhaseKind { kQkv = 0, kAttn = 1, kO = 2, kGu = 3, kDown = 4, kHead = 5 };
 // Waits for a GEMV phase's input and builds its int8 activation in LDS: the o_proj /
 // down_proj activation chunks as produced, or RMSNorm + FWHT + int8 of the hidden vector
 // (HA after the embedding or a down phase, HB after an o phase).
-template <int NTH>
+template <int NTH, bool EX>
 __device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, const float *norm_w,
                                               const NormPre &wp, int kind, uint32_t epoch, uint32_t lane, int wave,
                                               int t0, int trace_l = -1) {
@@ -311,7 +328,7 @@ __device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, c
     if (P.trace && threadIdx.x == 0 && trace_l >= 0)
         P.trace[(((size_t)blockIdx.x * (P.L + 1) + trace_l) * 6 + kind) * 6 + 2] = wall_clock64();
 #endif
-    build_norm_act<NTH>(P, S, norm_w, wp, lane, wave);
+    build_norm_act<NTH, EX>(P, S, norm_w, wp, lane, wave);
     return true;
 }
 
@@ -722,6 +739,165 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
     return true;
 }
 
+// Attention of q head h in the x86 reference's operation order (exact-order variant; one
+// task per head): causal_gqa_group_q8's portable branches (real_llm.rs:8533-8545,
+// 8575-8585) and softmax_unnorm_inplace (9590-9600).  Scores one position per thread,
+// s_t = (float(q8 . k8_t) * ks_t) * qas; p_t = exp(s_t - max) with the x86 build's exp
+// (expf_rn); sum = p_0 + p_1 + ... in position order (thread 0), inv = 1/sum; then thread
+// d accumulates o[d] += ((p_t * inv) * vs_t) * float(v8_t[d]) for t ascending (eight
+// positions' loads in flight); IFWHT, FWHT with the o_proj chunk index, int8.  The
+// position's own K / V come from LDS, as in attention_head, and are stored by the first q
+// head of each KV group.
+template <int NTH>
+__device__ bool attention_head_ex(const MkParams &P, const float *bias, const Lds &S, int layer, int h, int pos,
+                                  uint32_t ep_in, uint32_t ep_out, uint32_t lane, int wave) {
+    const int hd = P.hd, nb = hd / 64, nq = P.nq, nkv = P.nkv;
+    const int group = nq / nkv, kvh = h / group;
+    float *qf = S.att, *kf = qf + hd, *vf = kf + hd;
+    int8_t *qi = reinterpret_cast<int8_t *>(vf + hd);
+    int8_t *kn = qi + 128, *vn = kn + 128;
+    float *scal = reinterpret_cast<float *>(vn + 128);  // qas, ks_new, vs_new, inv
+    float *red = scal + 8;                              // [32]
+    float *sc = red + 32 + kMaxThreads * 4;             // [min(max_seq, kMkMaxContext)]
+    const int t = (int)threadIdx.x;
+    const int seq = pos + 1;
+    const size_t base = ((size_t)layer * nkv + kvh) * P.max_seq;
+    float rc = 0.0f, rsn = 0.0f;
+    if (wave < 2) {
+        const float *rrow = P.rope + (size_t)pos * hd;
+        const uint32_t ri = nb == 1 ? (lane & 31u) : lane;
+        rc = rrow[ri];
+        rsn = rrow[(nb == 1 ? 32u : 64u) + ri];
+    }
+    bool ok = true;
+    if (t < 3 * hd) {
+        const int part = t / hd, i = t % hd;
+        const int row = part == 0 ? h * hd + i : part == 1 ? (nq + kvh) * hd + i : (nq + nkv + kvh) * hd + i;
+        uint32_t v = 0;
+        ok = ll_wait(P, P.QKV + row, ep_in, v);
+        float f = __uint_as_float(v);
+        if (bias) f = f + bias[row];
+        qf[t] = f;
+    }
+    if (t == 0) S.flag[0] = 0;
+    lds_barrier();
+    if (!ok) S.flag[0] = 1;
+    lds_barrier();
+    if (S.flag[0]) return false;
+    const size_t slot = base + pos;
+    if (wave == 0 || wave == 1) {
+        const float *src = wave == 0 ? qf : kf;
+        float x0 = src[lane], x1 = nb > 1 ? src[64 + lane] : 0.0f;
+        if (nb == 1) {
+            const float xo = __shfl_xor(x0, 32, kWave);
+            x0 = lane < 32 ? x0 * rc - xo * rsn : x0 * rc + xo * rsn;
+        } else {
+            const float a0 = x0, a1 = x1;
+            x0 = a0 * rc - a1 * rsn;
+            x1 = a1 * rc + a0 * rsn;
+        }
+        int8_t *dst = wave == 0 ? qi : kn;
+        const float sc8 = quant_head(x0, x1, nb, lane, dst, sign_mask_s(P, 0), sign_mask_s(P, 1));
+        if (lane == 0) scal[wave] = wave == 0 ? sc8 * P.attn_scale : sc8;
+        if (wave == 1 && h % group == 0) {
+            P.kq[slot * hd + lane] = kn[lane];
+            if (nb > 1) P.kq[slot * hd + 64 + lane] = kn[64 + lane];
+            if (lane == 0) P.ks[slot] = sc8;
+        }
+    } else if (wave == 2) {
+        const float vsn = quant_head(vf[lane], nb > 1 ? vf[64 + lane] : 0.0f, nb, lane, vn, sign_mask_s(P, 0),
+                                     sign_mask_s(P, 1));
+        if (lane == 0) scal[2] = vsn;
+        if (h % group == 0) {
+            P.vq[slot * hd + lane] = vn[lane];
+            if (nb > 1) P.vq[slot * hd + 64 + lane] = vn[64 + lane];
+            if (lane == 0) P.vs[slot] = vsn;
+        }
+    }
+    lds_barrier();
+    const float qas = scal[0];
+    float smax = -INFINITY;
+    for (int tt = t; tt < seq; tt += NTH) {
+        int dot = 0;
+        float kscale;
+        const uint4 *qr = reinterpret_cast<const uint4 *>(qi);
+        if (tt == pos) {
+            for (int i = 0; i < hd / 16; i++) {
+                const uint4 a = lds_read16_now(kn + 16 * i), b = qr[i];
+                dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
+            }
+            kscale = ld_lds(scal + 1);
+        } else {
+            const uint4 *kr = reinterpret_cast<const uint4 *>(P.kq + (base + tt) * hd);
+            for (int i = 0; i < hd / 16; i++) {
+                const uint4 a = ld_global(kr + i), b = qr[i];
+                dot = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, dot, false);
+            }
+            kscale = ld_global(P.ks + base + tt);
+        }
+        const float sv = ((float)dot * kscale) * qas;
+        sc[tt] = sv;
+        smax = fmaxf(smax, sv);
+    }
+    smax = wave_max_f(smax);
+    if (lane == 0) red[wave] = smax;
+    lds_barrier();
+    float m = red[0];
+    for (int w2 = 1; w2 < (NTH / 64); w2++) m = fmaxf(m, red[w2]);
+    for (int tt = t; tt < seq; tt += NTH) sc[tt] = expf_rn(sc[tt] - m);
+    lds_barrier();
+    if (t == 0) {
+        float sum = 0.0f;
+        for (int tt = 0; tt < seq; tt++) sum = sum + sc[tt];
+        scal[3] = 1.0f / sum;
+    }
+    lds_barrier();
+    if (t < hd) {
+        const float inv = scal[3];
+        float o = 0.0f;
+        for (int tb = 0; tb < seq; tb += 8) {
+            float vsb[8];
+            int vb[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int tt = min(tb + u, seq - 1);
+                if (tt == pos) {
+                    vsb[u] = ld_lds(scal + 2);
+                    vb[u] = (int)ld_lds(vn + t);
+                } else {
+                    vsb[u] = ld_global(P.vs + base + tt);
+                    vb[u] = (int)ld_global(P.vq + (base + tt) * hd + t);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (tb + u < seq) o = o + ((sc[tb + u] * inv) * vsb[u]) * (float)vb[u];
+        }
+        qf[t] = o;
+    }
+    lds_barrier();
+    if (wave < nb) {
+        const uint32_t s4 = lane & 15u;
+        const float4 o4 = *reinterpret_cast<const float4 *>(qf + wave * 64 + s4 * 4);
+        float v[4] = {o4.x, o4.y, o4.z, o4.w};
+        butterflies_slice4(v, s4);
+        const uint32_t ib = (uint32_t)(sign_mask_s(P, wave) >> (4u * s4)) & 0xFu;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = flip_sign(v[j] * 0.125f, (ib >> j) & 1u);
+        const int c = h * nb + wave;
+        const Chunk4 r = rotate_quant4(v, sign_mask_s(P, c), s4);
+        store_act_chunk4(r, lane, P.OACT + (size_t)c * kActWords, ep_out, P.rep, oact_words(P));
+    }
+    lds_barrier();
+    return true;
+}
+
 // Stripe-mode task order with both stripes of a pair on one XCD: with one stripe per
 // workgroup, tasks t and t + 8 run on workgroups 8 apart (the same XCD), so the L2 lines
 // shared by the two halves of a record are fetched from HBM once.
@@ -749,7 +925,10 @@ __device__ __forceinline__ int xcd_stripe(const MatDev &M, int t, int nblocks) {
 
 // FMT/HP: the one weight format every projection and the head use (mixed-format models
 // run the one-kernel-per-operation path).
-template <int FMT, int HP, int NTH>
+// EX: the exact-order variant (x86 reference operation order: in-order GEMV epilogue
+// chains, sequential sums of squares, expf_rn, one attention task per head with sequential
+// softmax and V sums).
+template <int FMT, int HP, int NTH, bool EX>
 __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
     constexpr int kThreads = NTH;
     constexpr int kWaves = NTH / 64;
@@ -803,9 +982,15 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
             // task j = (span j / nq, head j % nq): the span-0 tasks (which merge) come first
             const int ntask = P.nq * P.nsp;
             if (vb < ntask) MK_TR(l, 1, 0);
-            for (int j = vb; j < ntask; j += nwg)
-                if (!attention_head<NTH>(P, LT[l].bias, S, l, j % P.nq, j / P.nq, pos, E(ph - 1), E(ph), lane, wave))
-                    return;
+            for (int j = vb; j < ntask; j += nwg) {
+                if constexpr (EX) {
+                    if (!attention_head_ex<NTH>(P, LT[l].bias, S, l, j, pos, E(ph - 1), E(ph), lane, wave)) return;
+                } else {
+                    if (!attention_head<NTH>(P, LT[l].bias, S, l, j % P.nq, j / P.nq, pos, E(ph - 1), E(ph), lane,
+                                             wave))
+                        return;
+                }
+            }
             if (vb < ntask) MK_TR(l, 1, 5);
             continue;
         }
@@ -851,7 +1036,7 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                 GemvWaveLds<FMT, HP, kMkFrags> gw(M, rb, rb < nblocks, wseg, lane, slots);
                 gw.start();
                 if (first) {
-                    if (!mk_load_input<NTH>(P, S, norm_w, wpre, kind, E(ph - 1), lane, wave, 0,
+                    if (!mk_load_input<NTH, EX>(P, S, norm_w, wpre, kind, E(ph - 1), lane, wave, 0,
                                             kind == kHead ? -1 : l))
                         return;
                     MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 1);
@@ -860,6 +1045,9 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                 // for it): request it now, so it lands during the compute.  The compute
                 // reads only LDS (no flat accesses), so nothing waits for this load early.
                 if ((kind == kO || kind == kDown) && orow >= 0) rpre = ll_load(res + orow);
+                // exact-order variant: this wave's group stages its rows' epilogue operands
+                unsigned long long *terms =
+                    EX ? P.exterm + (size_t)blockIdx.x * kMkTermRows * M.nc + (size_t)grp * RB * M.nc : nullptr;
 #ifdef K2T_MK_TRACE
                 unsigned long long *tr = first && P.trace
                     ? P.trace + (((size_t)blockIdx.x * (P.L + 1) + (kind == kHead ? P.L : l)) * 6 + (kind == kHead ? 0 : kind)) * 6
@@ -867,18 +1055,41 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
 #ifdef K2T_MK_TRACE_IN
                 tr = nullptr;
 #endif
-                gw.finish(slots, S.xl, S.xsl, S.xsuml, S.part + wave * 32, tr);
+                gw.finish(slots, S.xl, S.xsl, S.xsuml, S.part + wave * 32, tr, terms);
 #else
-                gw.finish(slots, S.xl, S.xsl, S.xsuml, S.part + wave * 32);
+                gw.finish(slots, S.xl, S.xsl, S.xsuml, S.part + wave * 32, nullptr, terms);
 #endif
+            }
+            if constexpr (EX) {
+                // the staged operands must be at the coherence point before other waves read them
+                __threadfence();
+                __syncthreads();
             }
             lds_barrier();
             if (first) MK_TR(kind == kHead ? P.L : l, kind == kHead ? 0 : kind, 4);
             if (orow >= 0) {
                 const int g2 = t / RB, rl = t % RB, row = orow;
-                const float *gp = S.part + (g2 * M.nseg) * 32;
-                float acc = gp[rl];
-                for (int w2 = 1; w2 < M.nseg; w2++) acc += gp[w2 * 32 + rl];
+                float acc = 0.0f;
+                if constexpr (EX) {
+                    // the reference's per-row chain f = fmaf(term_c, scale_c, f), c ascending
+                    // (simd_lut.rs:4030-4059, 6334-6335), sixteen operand words in flight
+                    const unsigned long long *tw =
+                        P.exterm + (size_t)blockIdx.x * kMkTermRows * M.nc + ((size_t)g2 * RB + rl) * M.nc;
+                    for (int c0 = 0; c0 < M.nc; c0 += 16) {
+                        unsigned long long wv[16];
+#pragma unroll
+                        for (int u = 0; u < 16; u++) wv[u] = ll_load(tw + min(c0 + u, M.nc - 1));
+#pragma unroll
+                        for (int u = 0; u < 16; u++)
+                            if (c0 + u < M.nc)
+                                acc = fmaf(__uint_as_float((uint32_t)wv[u]), __uint_as_float((uint32_t)(wv[u] >> 32)),
+                                           acc);
+                    }
+                } else {
+                    const float *gp = S.part + (g2 * M.nseg) * 32;
+                    acc = gp[rl];
+                    for (int w2 = 1; w2 < M.nseg; w2++) acc += gp[w2 * 32 + rl];
+                }
                 if (kind == kHead) {
                     P.logits[row] = acc;
                 } else if (kind == kQkv) {
@@ -901,7 +1112,7 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                     // elements per lane for the rotation (one wave: its LDS accesses are
                     // performed in program order)
                     const float g = S.vec[lane], u = S.vec[64 + lane];
-                    S.vec[lane] = (g / (1.0f + expf(-g))) * u;
+                    S.vec[lane] = (g / (1.0f + (EX ? expf_rn(-g) : expf(-g)))) * u;
                     const uint32_t s4 = lane & 15u;
                     const float4 va = *reinterpret_cast<const float4 *>(S.vec + s4 * 4);
                     float v[4] = {va.x, va.y, va.z, va.w};
@@ -1082,9 +1293,13 @@ size_t decode_mk_lds_bytes(const k2t_model_config &c) {
 
 template <int FMT, int HP, int NTH>
 static bool occupancy_ok(size_t lds) {
-    int nb = 0;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_mk_kernel<FMT, HP, NTH>, NTH, lds) == hipSuccess &&
-           nb >= 1;
+    int nb = 0, ne = 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_mk_kernel<FMT, HP, NTH, false>, NTH, lds) ==
+               hipSuccess &&
+           nb >= 1 &&
+           hipOccupancyMaxActiveBlocksPerMultiprocessor(&ne, decode_mk_kernel<FMT, HP, NTH, true>, NTH, lds) ==
+               hipSuccess &&
+           ne >= 1;
 }
 
 bool decode_mk_supported(const k2t_model_config &c, int num_cus) {
@@ -1112,12 +1327,22 @@ bool decode_mk_format(const MatDev &m, int &fmt, int &hp) {
     return true;
 }
 
-void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds) {
-    if (fmt == 1) hipLaunchKernelGGL((decode_mk_kernel<1, 0, 512>), dim3(num_cus), dim3(512), lds, st, P);
-    else if (hp == 0) hipLaunchKernelGGL((decode_mk_kernel<0, 0, 512>), dim3(num_cus), dim3(512), lds, st, P);
+template <bool EX>
+static void launch_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds) {
+    if (fmt == 1) hipLaunchKernelGGL((decode_mk_kernel<1, 0, 512, EX>), dim3(num_cus), dim3(512), lds, st, P);
+    else if (hp == 0) hipLaunchKernelGGL((decode_mk_kernel<0, 0, 512, EX>), dim3(num_cus), dim3(512), lds, st, P);
     else if (hp == kHpMixed)
-        hipLaunchKernelGGL((decode_mk_kernel<0, kHpMixed, 256>), dim3(num_cus), dim3(256), lds, st, P);
+        hipLaunchKernelGGL((decode_mk_kernel<0, kHpMixed, 256, EX>), dim3(num_cus), dim3(256), lds, st, P);
     else throw Error(K2T_E_INTERNAL, "persistent decode kernel: unsupported weight format");
+}
+
+void launch_decode_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int num_cus, size_t lds, bool exact) {
+    if (exact) {
+        if (!P.exterm || P.nsp != 1) throw Error(K2T_E_INTERNAL, "exact-order persistent kernel: bad parameters");
+        launch_mk<true>(st, P, fmt, hp, num_cus, lds);
+    } else {
+        launch_mk<false>(st, P, fmt, hp, num_cus, lds);
+    }
     hip_check(hipGetLastError(), "decode megakernel launch");
 }
 

@@ -23,14 +23,19 @@ void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float ep
                         float *s, int32_t *sums);
 void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
                      const float *rope, const int *pos_dev, int nq,
-                     int nkv, int hd, int ntok, int layer, KvRing kr, int8_t *kq, int8_t *vq, float *ks, float *vs);
+                     int nkv, int hd, int ntok, int layer, KvRing kr, int8_t *kq, int8_t *vq, float *ks, float *vs,
+                     bool exact);
+void launch_attention_exact(hipStream_t st, const float *q, int q_stride, const int8_t *kq, const int8_t *vq,
+                            const float *ks, const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd,
+                            KvRing kr, float attn_scale, int ntok, int max_positions, float *out_f);
 void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale, int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as,
                       int32_t *asum, const GqaWork &gqa);
 int attn_max_splits(int max_seq);
 int gqa_spans(int cap);
-void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums);
+void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
+                       bool exact);
 void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok, float *out);
 void launch_kv_synthetic(hipStream_t st, int8_t *kq, int8_t *vq, float *ks, float *vs, int layers_kv, int cap,
                          int n_pos, int hd, int bits, uint64_t seed);
@@ -102,11 +107,17 @@ void launch_argmax(hipStream_t st, const float *x, int n, int *out_idx) {
 }  // namespace k2t
 
 // Device scratch of k2t_attn_decode_noalloc: the span partials (n_heads * splits *
-// (head_dim + 2) floats) and the position word.  One copy per GPU, held until the process
-// ends.  Host code never passes this name to a kernel or a copy: it is a host-side
-// stand-in there; noalloc_scratch() looks up each device's own address.
+// (head_dim + 2) floats) and the position word in the first kNoAllocScratchFloats floats;
+// then the grouped-query kernel's span words (kNoAllocGqaWords 64-bit {payload, epoch}
+// words), its counters {epoch, merges done} and its timeout word.  Device memory starts
+// zeroed, and the words' epochs only grow, so nothing here is ever cleared (but after a
+// timeout).  One copy per GPU, held until the process ends.  Host code never passes this
+// name to a kernel or a copy: it is a host-side stand-in there; noalloc_scratch() looks up
+// each device's own address.
 constexpr size_t kNoAllocScratchFloats = (size_t)1 << 20;  // 4 MiB
-static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+constexpr size_t kNoAllocGqaWords = (size_t)1 << 19;       // 4 MiB
+constexpr size_t kNoAllocTotalFloats = kNoAllocScratchFloats + 2 * (kNoAllocGqaWords + 2);
+static __device__ __align__(256) float scratch[kNoAllocTotalFloats];
 
 namespace k2t {
 __global__ void store_int_kernel(int *dst, int v) {
@@ -133,7 +144,58 @@ float *noalloc_scratch(int device) {
     }
     return g_noalloc_ptr[device];
 }
+// The grouped-query words, counters and timeout word of one scratch region.
+GqaWork gqa_work_at(unsigned long long *words, size_t cap) {
+    return GqaWork{words, reinterpret_cast<unsigned int *>(words + cap), reinterpret_cast<int *>(words + cap + 1)};
+}
+
+GqaWork noalloc_gqa(int device) {
+    float *base = noalloc_scratch(device);
+    return gqa_work_at(reinterpret_cast<unsigned long long *>(base + kNoAllocScratchFloats), kNoAllocGqaWords);
+}
+
+// k2t_attn_decode's grouped-query workspace on the context (zeroed whenever it grows).
+GqaWork ctx_gqa(k2t_ctx *ctx, size_t words) {
+    if (words > ctx->gqa_cap) {
+        hip_check(hipStreamSynchronize(ctx->stream), "gqa workspace sync");
+        if (ctx->gqa_words) hip_check(hipFree(ctx->gqa_words), "hipFree");
+        ctx->gqa_words = nullptr;
+        ctx->gqa_cap = 0;
+        const size_t bytes = (words + 2) * sizeof(unsigned long long);
+        hipError_t e = hipMalloc((void **)&ctx->gqa_words, bytes);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            throw Error(K2T_E_NOMEM, std::string("hipMalloc failed: ") + hipGetErrorString(e));
+        }
+        hip_check(hipMemset(ctx->gqa_words, 0, bytes), "gqa workspace clear");
+        ctx->gqa_cap = words;
+    }
+    return gqa_work_at(ctx->gqa_words, ctx->gqa_cap);
+}
+
+// Reads a region's timeout word after a sync; on a timeout clears the region (its epochs
+// start over) and raises.
+void raise_gqa_timeout(const GqaWork &g, size_t cap) {
+    int e = 0;
+    hip_check(hipMemcpy(&e, g.err, sizeof(int), hipMemcpyDeviceToHost), "gqa timeout word");
+    if (!e) return;
+    hip_check(hipMemset(g.words, 0, (cap + 2) * sizeof(unsigned long long)), "gqa workspace clear");
+    throw Error(K2T_E_HIP, "grouped-query attention: span wait timed out");
+}
+
 }  // namespace
+
+namespace k2t {
+void check_gqa_timeout(k2t_ctx *ctx) {
+    if (ctx->gqa_words) raise_gqa_timeout(gqa_work_at(ctx->gqa_words, ctx->gqa_cap), ctx->gqa_cap);
+    bool seen = false;
+    {
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        seen = ctx->device >= 0 && ctx->device < kMaxNoAllocDevices && g_noalloc_ptr[ctx->device] != nullptr;
+    }
+    if (seen) raise_gqa_timeout(noalloc_gqa(ctx->device), kNoAllocGqaWords);
+}
+}  // namespace k2t
 
 struct k2t_model {
     k2t_ctx *ctx = nullptr;
@@ -171,7 +233,11 @@ struct k2t_model {
     int32_t *xsum = nullptr;
     int pos = 0;
     bool use_graph = true;
-    int exact = 0;  // GEMV epilogue mode used by this model's steps
+    // 1: exact-order steps (the x86 reference's operation order throughout: in-order GEMV
+    // epilogue, sequential sums of squares, its exp, sequential softmax and V sums)
+    int exact = 0;
+    float *rms_x86 = nullptr;  // [max_batch] inv_rms of the exact-order steps
+    float *attn_f = nullptr;   // [max_batch][n_heads * head_dim] exact-order attention output
     hipGraphExec_t graph = nullptr;
     bool graph_pk = false;  // the captured step is the persistent kernel
     std::vector<void *> allocs;
@@ -186,6 +252,7 @@ struct k2t_model {
     MkLayer *mk_layers = nullptr;
     int mk_head_off = 0;  // first workgroup of the persistent kernel's lm_head phase
     int mk_nsp = 1;       // attention spans per q head in the persistent kernel
+    unsigned long long *mk_terms = nullptr;  // exact-order variant: epilogue operands per workgroup
 };
 
 namespace {
@@ -241,9 +308,65 @@ void ensure_batch(k2t_model *m, int n) {
     throw Error(K2T_E_ARG, "token batch larger than the model's max batch");
 }
 
+// The exact-order forward pass (k2t_model_set_exact): every operation in the x86
+// reference's order (forward_token_sdot_megakernel's portable paths, real_llm.rs:6794-7403):
+// RMSNorm with the sequential four-accumulator sum of squares, GEMVs with the in-order
+// fmaf epilogue (the context's exact mode, set by the caller), q / k norm, RoPE from the
+// host table and the K / V store per head, attention with sequential softmax and V sums,
+// SwiGLU and softmax with the x86 build's exp.  Same device buffers as forward().
+void forward_exact(k2t_model *m, int ntok, bool with_logits) {
+    const k2t_model_config &c = m->cfg;
+    hipStream_t st = m->stream;
+    k2t_ctx *ctx = m->ctx;
+    const int hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, d = c.hidden, inter = c.intermediate;
+    const float attn_scale = 1.0f / sqrtf((float)hd);
+    if (m->embed_kind == K2T_EMBED_F32 || m->embed_kind == K2T_EMBED_BF16)
+        launch_embed_rows(st, m->embed_rows, m->embed_kind == K2T_EMBED_BF16, m->tokens, ntok, c.hidden, m->hidden);
+    else
+        launch_embed(st, m->embed_kind == K2T_EMBED_NF4 ? m->embed_mat : m->head, m->tokens, ntok, m->hidden);
+    auto norm_act = [&](const float *x, const float *w) {
+        launch_inv_rms_x86(st, x, c.rms_eps, d, ntok, m->rms_x86);
+        launch_act_quant(ctx, x, w, m->rms_x86, d, ntok, m->xq, m->xs, m->xsum);
+    };
+    for (int l = 0; l < c.n_layers; l++) {
+        const auto &L = m->layers[l];
+        norm_act(m->hidden, L.in_norm);
+        launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false);
+        launch_qkv_post(st, m->qkv, L.bias, L.q_norm, L.k_norm, c.rms_eps, m->rope, m->pos_dev, nq, nkv, hd, ntok, l,
+                        m->ring, m->kq, m->vq, m->ks, m->vs, true);
+        launch_attention_exact(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, m->pos_dev, l, nq, nkv, hd,
+                               m->ring, attn_scale, ntok, c.max_seq, m->attn_f);
+        launch_act_quant(ctx, m->attn_f, nullptr, nullptr, nq * hd, ntok, m->xq, m->xs, m->xsum);
+        launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
+        if (L.has_moe) {
+            // (the MoE feed-forward keeps its own order: router dot and combine as in
+            // launch_moe_ffn)
+            MoeWork ws = moe_work_carve(m->moe_ws, L.moe.bank, L.moe.top_k);
+            ws.err = m->err_dev;
+            for (int t = 0; t < ntok; t++) launch_moe_ffn(ctx, L.moe, m->hidden + (size_t)t * d, L.post_norm, c.rms_eps, ws);
+            continue;
+        }
+        norm_act(m->hidden, L.post_norm);
+        launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false);
+        launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum, true);
+        launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
+    }
+    if (with_logits) {
+        const float *last = m->hidden + (size_t)(ntok - 1) * d;
+        launch_inv_rms_x86(st, last, c.rms_eps, d, 1, m->rms_x86);
+        launch_act_quant(ctx, last, m->final_norm, m->rms_x86, d, 1, m->xq, m->xs, m->xsum);
+        launch_gemv_ex(ctx, m->head, m->xq, m->xs, m->xsum, 1, m->logits, c.vocab, false);
+    }
+    launch_advance_pos(st, m->pos_dev, ntok);
+}
+
 // One forward pass over `ntok` tokens already in m->tokens, positions pos..pos+ntok-1.
 // Logits (of the last token) go to m->logits; the device position advances by ntok.
 void forward(k2t_model *m, int ntok, bool with_logits) {
+    if (m->exact) {
+        forward_exact(m, ntok, with_logits);
+        return;
+    }
     const k2t_model_config &c = m->cfg;
     hipStream_t st = m->stream;
     k2t_ctx *ctx = m->ctx;
@@ -272,7 +395,7 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
             post = AttnPost{1, L.bias, L.q_norm, L.k_norm, m->rope, c.rms_eps};
         } else {
             launch_qkv_post(st, m->qkv, L.bias, L.q_norm, L.k_norm, c.rms_eps, m->rope, m->pos_dev, nq, nkv, hd, ntok,
-                            l, m->ring, m->kq, m->vq, m->ks, m->vs);
+                            l, m->ring, m->kq, m->vq, m->ks, m->vs, false);
         }
         launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, post, m->pos_dev, l, nq, nkv,
                          hd, m->ring, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum,
@@ -289,7 +412,7 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
         } else {
             launch_rmsnorm_act(st, m->hidden, L.post_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
             launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false);
-            launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum);
+            launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum, false);
             launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
         }
     }
@@ -342,7 +465,7 @@ bool use_persistent(const k2t_model *m) {
     if (m->ring.window > 0 || m->ring.bits != 8) return false;
     for (const auto &L : m->layers)
         if (L.has_moe || L.q_norm || L.k_norm) return false;  // these run on the per-operation path
-    return m->persistent && m->mk_ok && !m->exact && mk_format(m, fmt, hp);
+    return m->persistent && m->mk_ok && mk_format(m, fmt, hp);
 }
 
 // Destroys the captured decode graph after the stream has drained: a replay enqueued
@@ -389,8 +512,9 @@ void upload_mk_layers(k2t_model *m) {
     const int max_spans = mk_max_spans(nw * 64);
     m->mk_nsp = std::max(1, std::min(max_spans, nwg / m->cfg.n_heads));
 #ifdef K2T_MK_SPANS
-    m->mk_nsp = std::min(K2T_MK_SPANS, max_spans);
+    m->mk_nsp = std::max(1, std::min({K2T_MK_SPANS, max_spans, nwg / m->cfg.n_heads}));
 #endif
+    if (m->exact) m->mk_nsp = 1;  // one task per head: sequential softmax and V sums
     int cursor = 0;
     for (auto &x : h) {
         const int tasks[5] = {mk_phase_tasks(x.qkv, nw), m->cfg.n_heads * m->mk_nsp, mk_phase_tasks(x.o, nw),
@@ -464,7 +588,8 @@ void forward_mk(k2t_model *m) {
     }
 #endif
     // the kernel also writes the greedy next token and advances the position and step
-    launch_decode_mk(m->stream, P, fmt, hp, m->ctx->num_cus, m->mk_lds);
+    P.exterm = m->exact ? m->mk_terms : nullptr;
+    launch_decode_mk(m->stream, P, fmt, hp, m->ctx->num_cus, m->mk_lds, m->exact != 0);
 #ifdef K2T_MK_TRACE
     if (P.trace) {
         std::vector<unsigned long long> h(ntr);
@@ -589,6 +714,8 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             hip_check(hipMemset(m->attn_words, 0, gw * sizeof(unsigned long long)), "span words clear");
             m->attn_cnt = (unsigned int *)dalloc(m, 2 * sizeof(unsigned int));
             hip_check(hipMemset(m->attn_cnt, 0, 2 * sizeof(unsigned int)), "counter clear");
+            m->rms_x86 = (float *)dalloc(m, (size_t)max_batch * sizeof(float));
+            m->attn_f = (float *)dalloc(m, (size_t)max_batch * c.n_heads * c.head_dim * sizeof(float));
             m->xq = (int8_t *)dalloc(m, (size_t)max_batch * kmax);
             m->xs = (float *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(float));
             m->xsum = (int32_t *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(int32_t));
@@ -782,8 +909,17 @@ int32_t k2t_model_set_graph(k2t_model *m, int32_t enable) {
 int32_t k2t_model_set_exact(k2t_model *m, int32_t exact) {
     return mguard([&] {
         arg(m != nullptr, "model is NULL");
-        m->exact = exact ? 1 : 0;
         drop_graph(m);
+        if (exact && m->mk_ok && !m->mk_terms) {
+            // the exact-order persistent kernel's per-workgroup epilogue operands: one GEMV
+            // round (kMkTermRows rows) of the widest input
+            const k2t_model_config &c = m->cfg;
+            const size_t nc = (size_t)std::max(c.hidden, c.intermediate) / 64;
+            hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+            m->mk_terms = (unsigned long long *)dalloc(
+                m, (size_t)m->ctx->num_cus * kMkTermRows * nc * sizeof(unsigned long long));
+        }
+        m->exact = exact ? 1 : 0;
     });
 }
 
@@ -1031,6 +1167,22 @@ void attn_decode_impl(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_he
     const int act = window > 0 ? std::min(seq, window) : seq;
     const int nsplit = attn_max_splits(act);
     hip_check(hipSetDevice(ctx->device), "hipSetDevice");
+    // grouped queries at long context: the model's grouped-query kernel (each K / V tile
+    // read once for the G q heads of its KV head), with span words that persist across
+    // calls (context workspace, or the fixed no-alloc region)
+    GqaWork gq{};
+    if (gqa_eligible(nsplit, 1, n_heads, n_kv_heads, head_dim, kr)) {
+        const size_t words = gqa_words(cap, n_heads, head_dim, 1);
+        if (noalloc) {
+            if (words > kNoAllocGqaWords)
+                throw Error(K2T_E_ARG, "k2t_attn_decode_noalloc: ceil(cap / 128) * n_heads * (head_dim + 2) = " +
+                                           std::to_string(words) + " span words exceeds its fixed region of " +
+                                           std::to_string(kNoAllocGqaWords));
+            gq = noalloc_gqa(ctx->device);
+        } else {
+            gq = ctx_gqa(ctx, words);
+        }
+    }
     const size_t part = (size_t)n_heads * nsplit * (2 + head_dim);
     float *pp;
     if (noalloc) {
@@ -1054,7 +1206,7 @@ void attn_decode_impl(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_he
     // read-only on the cache (no post stage: the caller's queries are final)
     launch_attention(ctx->stream, d_q, n_heads * head_dim, (int8_t *)d_kq, (int8_t *)d_vq, (float *)d_ks,
                      (float *)d_vs, AttnPost{}, pos, 0, n_heads, n_kv_heads, head_dim, kr, attn_scale, nsplit, 1, pp,
-                     d_out, nullptr, nullptr, nullptr, GqaWork{});
+                     d_out, nullptr, nullptr, nullptr, gq);
     // the copied position lives on this function's stack; the no-alloc variant stores it
     // with a kernel and stays asynchronous
     if (!noalloc) hip_check(hipStreamSynchronize(ctx->stream), "sync");

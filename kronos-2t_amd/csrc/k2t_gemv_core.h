@@ -383,21 +383,32 @@ struct GemvWaveLds {
         return fr;
     }
 
+    // terms != nullptr (exact-order mode): instead of accumulating, each lane stores the
+    // reference's per-chunk epilogue operands of its two rows, {float(dot) * sx, bf16 scale}
+    // as one 64-bit word (low half the term), at terms[row_local * nc + c]; a neutral
+    // {-0, +0} where sx == 0 (the reference skips such chunks, and fmaf(-0, +0, f) == f).
+    // The caller replays each row's fmaf chain in chunk order from those words.
     __device__ __forceinline__ void finish(const uint8_t *slots, const int8_t *xl, const float *xsl,
-                                           const int32_t *xsuml, float *part, unsigned long long *trace = nullptr) {
+                                           const int32_t *xsuml, float *part, unsigned long long *trace = nullptr,
+                                           unsigned long long *terms = nullptr) {
         float f0 = 0.0f, f1 = 0.0f;
         for (int i = 0; i < iters; i++) {
             // fragments i .. min(i + F, iters) - 1 were requested; wait for i
             wait_frag(min(F, iters - i) - 1);
             if (trace && i == 0 && threadIdx.x == 0) trace[2] = wall_clock64();
             const WFrag<HP> fr = read(i, slots);
-            if (valid(i)) process(fr, chunk_of(i), xl, xsl, xsuml, f0, f1);
+            if (terms) {
+                if (valid(i)) store_terms(fr, chunk_of(i), xl, xsl, xsuml, terms);
+            } else if (valid(i)) {
+                process(fr, chunk_of(i), xl, xsl, xsuml, f0, f1);
+            }
             if (i + F < iters) {  // wave-uniform
                 // the slot's LDS reads must complete before the next fragment overwrites it
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 issue(i + F);
             }
         }
+        if (terms) return;
         if (M.smode) {
             f0 += __int_as_float(dpp_ror8(__float_as_int(f0)));
             f1 += __int_as_float(dpp_ror8(__float_as_int(f1)));
@@ -412,6 +423,26 @@ struct GemvWaveLds {
             part[rloc + 1] = f1;
         }
         if (trace && threadIdx.x == 0) trace[3] = wall_clock64();
+    }
+
+    __device__ __forceinline__ void store_terms(const WFrag<HP> &fr, int c, const int8_t *xl, const float *xsl,
+                                                const int32_t *xsuml, unsigned long long *terms) const {
+        uint2 x[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) x[kk] = *reinterpret_cast<const uint2 *>(xl + c * 64 + kk * 16 + half * 8);
+        const float sx = xsl[c];
+        const int xsum = FMT == 0 ? xsuml[c] : 0;
+        int r0, r1;
+        chunk_dots<FMT, HP>(M, fr, half, x, xsum, r0, r1);
+        const bool on = sx != 0.0f;
+        const float t0 = on ? (float)r0 * sx : -0.0f, w0 = on ? bf16_lo(fr.ws) : 0.0f;
+        const float t1 = on ? (float)r1 * sx : -0.0f, w1 = on ? bf16_hi(fr.ws) : 0.0f;
+        const uint32_t rloc = (M.smode ? 0u : ((lane >> 3) & 1u) * 16u) + 4u * ((lane >> 1) & 3u) + 2u * half;
+        unsigned long long *d = terms + (size_t)rloc * M.nc + c;
+        __hip_atomic_store(d, ((unsigned long long)__float_as_uint(w0) << 32) | __float_as_uint(t0), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(d + M.nc, ((unsigned long long)__float_as_uint(w1) << 32) | __float_as_uint(t1),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     __device__ __forceinline__ void process(const WFrag<HP> &fr, int c, const int8_t *xl, const float *xsl,

@@ -20,6 +20,10 @@ struct k2t_ctx {
     size_t scratch_cap = 0;  // floats
     float *rms_scratch = nullptr;
     size_t rms_cap = 0;
+    // grouped-query attention span words of k2t_attn_decode ({payload, epoch}, zeroed when
+    // allocated), then its counters {epoch, merges done} and timeout word
+    unsigned long long *gqa_words = nullptr;
+    size_t gqa_cap = 0;  // words
     // Hadamard sign masks of 64-blocks 0..kSignBlocks-1 (bit i = sign of element i),
     // uploaded at creation for the GEMV's fused activation builder.
     uint64_t *signs = nullptr;
@@ -138,11 +142,20 @@ struct AttnPost {
     float eps;
 };
 
+bool gqa_eligible(int nsplit, int ntok, int nq, int nkv, int hd, const KvRing &kr);
+size_t gqa_words(int cap, int nq, int hd, int ntok);
+// Raises (and clears) a grouped-query attention wait timeout that a k2t_attn_decode call
+// on this context left in its span-word workspace; called after a stream sync.
+void check_gqa_timeout(k2t_ctx *ctx);
+
 // The model takes ownership of `mat` (destroyed with the model).
 void model_adopt(k2t_model *m, k2t_mat *mat);
 
 void launch_act_quant(k2t_ctx *ctx, const float *x, const float *w, const float *inv_rms, int K,
                       int ntok, int8_t *q, float *scales, int32_t *sums);
 void launch_inv_rms(k2t_ctx *ctx, const float *x, float eps, int K, int ntok, float *inv_rms);
+void launch_expf_map(hipStream_t st, const float *x, float *y, size_t n);
+// inv_rms per token with the x86 reference's sum-of-squares order (exact-order mode).
+void launch_inv_rms_x86(hipStream_t st, const float *x, float eps, int K, int ntok, float *inv_rms);
 
 }  // namespace k2t

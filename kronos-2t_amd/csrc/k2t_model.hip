@@ -10,7 +10,10 @@
 #include <float.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include "k2t_device.h"
+#include "k2t_expf.h"
 #include "k2t_internal.h"
 
 namespace k2t {
@@ -148,7 +151,7 @@ void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float ep
 __device__ __forceinline__ void head_post(const float *__restrict__ h, int head, int nq, int nkv, int hd,
                                           const float *__restrict__ bias, const float *__restrict__ qn,
                                           const float *__restrict__ kn, float eps, const float *__restrict__ rope,
-                                          int pos, uint32_t lane, float &v0, float &v1) {
+                                          int pos, uint32_t lane, float &v0, float &v1, bool exact = false) {
     const int nb = hd / 64;
     v0 = h[lane];
     v1 = nb > 1 ? h[64 + lane] : 0.0f;
@@ -158,10 +161,25 @@ __device__ __forceinline__ void head_post(const float *__restrict__ h, int head,
     }
     const float *hn = head < nq ? qn : (head < nq + nkv ? kn : nullptr);
     if (hn) {
-        float ss = v0 * v0;
-        if (nb > 1) ss = fmaf(v1, v1, ss);
-        ss = wave_sum_f(ss);
-        const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)hd) + eps);
+        float inv_rms;
+        if (exact) {
+            // the x86 reference's order (dot_f32_fast, real_llm.rs:911-926): four sequential
+            // accumulators over elements k, k + 4, ...; every lane runs the same chain
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int e = 0; e < hd; e += 4)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float x = e + k < 64 ? lane_val(v0, e + k) : lane_val(v1, e + k - 64);
+                    acc[k] = acc[k] + x * x;
+                }
+            const float sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            inv_rms = 1.0f / sqrtf(sum / (float)hd + eps);
+        } else {
+            float ss = v0 * v0;
+            if (nb > 1) ss = fmaf(v1, v1, ss);
+            ss = wave_sum_f(ss);
+            inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)hd) + eps);
+        }
         v0 = (v0 * inv_rms) * hn[lane];
         if (nb > 1) v1 = (v1 * inv_rms) * hn[64 + lane];
     }
@@ -187,14 +205,14 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(float *__restrict__ qkv, c
                                                       const int *__restrict__ pos_dev, int nq, int nkv, int hd,
                                                       int row_stride, int layer, KvRing kr, int8_t *__restrict__ kq,
                                                       int8_t *__restrict__ vq, float *__restrict__ ks,
-                                                      float *__restrict__ vs) {
+                                                      float *__restrict__ vs, int exact) {
     const uint32_t lane = threadIdx.x;
     const int head = blockIdx.x, tok = blockIdx.y;
     const int pos = pos_dev[0] + tok;
     float *h = qkv + (size_t)tok * row_stride + (size_t)head * hd;
     const int nb = hd / 64;  // 1 or 2 blocks; lane holds element lane (+64)
     float v0, v1;
-    head_post(h, head, nq, nkv, hd, bias, qn, kn, eps, rope, pos, lane, v0, v1);
+    head_post(h, head, nq, nkv, hd, bias, qn, kn, eps, rope, pos, lane, v0, v1, exact != 0);
     if (head < nq) {
         h[lane] = v0;
         if (nb > 1) h[64 + lane] = v1;
@@ -226,9 +244,9 @@ void launch_kv_store(hipStream_t st, const float *heads, int n, int hd, int bits
 
 void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
                      const float *rope, const int *pos_dev, int nq, int nkv, int hd, int ntok, int layer, KvRing kr,
-                     int8_t *kq, int8_t *vq, float *ks, float *vs) {
+                     int8_t *kq, int8_t *vq, float *ks, float *vs, bool exact) {
     hipLaunchKernelGGL(qkv_post_kernel, dim3(nq + 2 * nkv, ntok), dim3(64), 0, st, qkv, bias, qn, kn, eps, rope,
-                       pos_dev, nq, nkv, hd, (nq + 2 * nkv) * hd, layer, kr, kq, vq, ks, vs);
+                       pos_dev, nq, nkv, hd, (nq + 2 * nkv) * hd, layer, kr, kq, vq, ks, vs, exact ? 1 : 0);
     hip_check(hipGetLastError(), "qkv_post launch");
 }
 
@@ -1075,6 +1093,15 @@ int attn_max_splits(int max_seq) {
 // Spans of the grouped-query kernel over a cache of `cap` slots.
 int gqa_spans(int cap) { return (cap + kGqaSpan - 1) / kGqaSpan; }
 
+// Whether launch_attention runs the grouped-query kernel (given span words), and the
+// words it then needs: [token][q head][span][2 + hd].
+bool gqa_eligible(int nsplit, int ntok, int nq, int nkv, int hd, const KvRing &kr) {
+    const int group = nq / nkv;
+    return nsplit > 1 && ntok == 1 && group >= 2 && group <= kGqaMaxGroup && kr.bits == 8 && kr.window == 0 &&
+           (hd == 64 || hd == 128);
+}
+size_t gqa_words(int cap, int nq, int hd, int ntok) { return (size_t)gqa_spans(cap) * nq * (2 + hd) * ntok; }
+
 void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale,
@@ -1109,9 +1136,115 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
     hip_check(hipGetLastError(), "attn_merge launch");
 }
 
+// ---------------------------------------------------------------- exact-order attention
+// Decode attention in the x86 reference's operation order (causal_gqa_group_q8, portable
+// branches real_llm.rs:8533-8545 and 8575-8585; softmax_unnorm_inplace 9590-9600), for the
+// exact-order mode.  One wave per (q head, token):
+//   q rotated and quantized like a KV head (store_hadamard_q8_head order), qas = qs*scale;
+//   s_t = (float(q8 . k8_t) * ks_t) * qas (with a sliding window: the sum over 64-blocks of
+//   float(dot_g) * ks_t * qas, causal_gqa_group_q4_or_window's int8 branch), one position
+//   per lane;
+//   p_t = exp(s_t - max) with the x86 build's exp (expf_rn), in parallel;
+//   sum = p_0 + p_1 + ... in position order (lane 0), inv = 1/sum;
+//   o[d] += ((p_t * inv) * vs_t) * float(v8_t[d]) for t ascending (a window skips weights of
+//   zero), lane d holding columns d and 64 + d;
+//   ifwht64 per block, written as fp32 to out_f [token][nq * hd].
+// Scores live in dynamic LDS (one float per attended position).
+__global__ __launch_bounds__(64) void attn_exact_kernel(const float *__restrict__ q, int q_stride,
+                                                        const int8_t *__restrict__ kq, const int8_t *__restrict__ vq,
+                                                        const float *__restrict__ ks, const float *__restrict__ vs,
+                                                        const int *__restrict__ pos_dev, int layer, int nq, int nkv,
+                                                        int hd, KvRing kr, float attn_scale, float *__restrict__ out_f) {
+    extern __shared__ float sc[];
+    __shared__ int8_t qi[128];
+    __shared__ float red[2];
+    const uint32_t lane = threadIdx.x;
+    const int h = blockIdx.x, tok = blockIdx.y, nb = hd / 64;
+    const int pos = pos_dev[0] + tok, seq = pos + 1;
+    const int n = active_len(kr, seq);
+    const int kvh = h / (nq / nkv);
+    const size_t base = ((size_t)layer * nkv + kvh) * kr.cap;
+    const float *qr = q + (size_t)tok * q_stride + (size_t)h * hd;
+    const float r0 = fwht_lane(qr[lane], 0, lane);
+    const float r1 = nb > 1 ? fwht_lane(qr[64 + lane], 1, lane) : 0.0f;
+    const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
+    float qscale = 0.0f;
+    if (mx <= FLT_EPSILON) {
+        qi[lane] = 0;
+        if (nb > 1) qi[64 + lane] = 0;
+    } else {
+        const float inv = 127.0f / mx;
+        qi[lane] = (int8_t)(int)rintf(r0 * inv);
+        if (nb > 1) qi[64 + lane] = (int8_t)(int)rintf(r1 * inv);
+        qscale = mx / 127.0f;
+    }
+    const float qas = qscale * attn_scale;
+    __syncthreads();
+    float smax = -INFINITY;
+    for (int idx = (int)lane; idx < n; idx += 64) {
+        const size_t slot = base + ring_slot(kr, active_pos(kr, idx, seq));
+        const int8_t *kr8 = kq + slot * hd;
+        const float kscale = ks[slot];
+        float s;
+        if (kr.window > 0) {
+            float total = 0.0f;
+            for (int g = 0; g < nb; g++) {
+                int dot = 0;
+                for (int i = 0; i < 64; i++) dot += (int)qi[g * 64 + i] * (int)kr8[g * 64 + i];
+                total = total + ((float)dot * kscale) * qas;
+            }
+            s = total;
+        } else {
+            int dot = 0;
+            for (int i = 0; i < hd; i++) dot += (int)qi[i] * (int)kr8[i];
+            s = ((float)dot * kscale) * qas;
+        }
+        sc[idx] = s;
+        smax = fmaxf(smax, s);
+    }
+    const float m = wave_max_f(smax);
+    for (int idx = (int)lane; idx < n; idx += 64) sc[idx] = expf_rn(sc[idx] - m);
+    __syncthreads();
+    if (lane == 0) {
+        float sum = 0.0f;
+        for (int idx = 0; idx < n; idx++) sum = sum + sc[idx];
+        red[0] = 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = red[0];
+    float o0 = 0.0f, o1 = 0.0f;
+    for (int idx = 0; idx < n; idx++) {
+        const size_t slot = base + ring_slot(kr, active_pos(kr, idx, seq));
+        const float w = (sc[idx] * inv) * vs[slot];
+        if (kr.window > 0 && w == 0.0f) continue;
+        const int8_t *vr = vq + slot * hd;
+        o0 = o0 + w * (float)vr[lane];
+        if (nb > 1) o1 = o1 + w * (float)vr[64 + lane];
+    }
+    float *dst = out_f + (size_t)tok * nq * hd + (size_t)h * hd;
+    dst[lane] = ifwht_lane(o0, 0, lane);
+    if (nb > 1) dst[64 + lane] = ifwht_lane(o1, 1, lane);
+}
+
+// Positions one exact-order attention launch can hold in LDS (one float each).
+constexpr int kAttnExactMaxPositions = 32768;
+
+void launch_attention_exact(hipStream_t st, const float *q, int q_stride, const int8_t *kq, const int8_t *vq,
+                            const float *ks, const float *vs, const int *pos_dev, int layer, int nq, int nkv, int hd,
+                            KvRing kr, float attn_scale, int ntok, int max_positions, float *out_f) {
+    if (kr.bits != 8) throw Error(K2T_E_ARG, "exact-order attention needs the int8 KV cache");
+    const int npos = kr.window > 0 ? std::min(max_positions, kr.window) : max_positions;
+    if (npos > kAttnExactMaxPositions) throw Error(K2T_E_ARG, "exact-order attention: context too long");
+    hipLaunchKernelGGL(attn_exact_kernel, dim3(nq, ntok), dim3(64), (size_t)npos * sizeof(float), st, q, q_stride,
+                       kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, out_f);
+    hip_check(hipGetLastError(), "attn_exact launch");
+}
+
 // ---------------------------------------------------------------- SwiGLU + FWHT + int8
 // Interleaved gate_up output: block ic = [gate64(ic), up64(ic)] (simd_lut.rs:3310-3325).
 // swiglu_activate_scalar (real_llm.rs:9801-9805), then populate_chunk_fwht_raw with chunk ic.
+// EXACT: the exponential of the x86 reference build (expf_rn) instead of the device expf.
+template <bool EXACT>
 __global__ __launch_bounds__(64) void swiglu_act_kernel(const float *__restrict__ gu, int inter, int8_t *__restrict__ q,
                                                         float *__restrict__ s, int32_t *__restrict__ sums) {
     const uint32_t lane = threadIdx.x;
@@ -1119,13 +1252,17 @@ __global__ __launch_bounds__(64) void swiglu_act_kernel(const float *__restrict_
     const int nci = inter / 64;
     const float *b = gu + (size_t)tok * 2 * inter + (size_t)ic * 128;
     const float g = b[lane], u = b[64 + lane];
-    const float v = (g / (1.0f + expf(-g))) * u;
+    const float v = (g / (1.0f + (EXACT ? expf_rn(-g) : expf(-g)))) * u;
     const size_t gc = (size_t)tok * nci + ic;
     quant_chunk_store(fwht_lane(v, (uint64_t)ic, lane), lane, q + gc * 64, s + gc, sums + gc);
 }
 
-void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums) {
-    hipLaunchKernelGGL(swiglu_act_kernel, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums);
+void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
+                       bool exact) {
+    if (exact)
+        hipLaunchKernelGGL(swiglu_act_kernel<true>, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums);
+    else
+        hipLaunchKernelGGL(swiglu_act_kernel<false>, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums);
     hip_check(hipGetLastError(), "swiglu_act launch");
 }
 

@@ -108,6 +108,8 @@ SIGNATURES = {
     "k2t_kv_store": (I32, [VP, I32, VP, I32, I32, VP, VP]),
     "k2t_attn_decode": (I32, [VP, I32, VP, I32, I32, I32, VP, VP, VP, VP, I32, I32, I32, I32, C.c_float, VP]),
     "k2t_stream_read_probe": (I32, [VP, VP, SZ, VP]),
+    "k2t_expf_host": (C.c_float, [C.c_float]),
+    "k2t_expf_device": (I32, [VP, VP, VP, SZ]),
     "k2t_attn_decode_noalloc": (I32, [VP, I32, VP, I32, I32, I32, VP, VP, VP, VP, I32, I32, I32, I32, C.c_float,
                                       VP]),
 }

@@ -29,6 +29,7 @@
  */
 #include <float.h>
 #include <math.h>
+#include <pthread.h>
 #include <stddef.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -1156,4 +1157,66 @@ void or_attn_q4_head(const float *q_head, const uint8_t *k4, const uint16_t *ks1
         }
     }
     or_ifwht64(out, hd);
+}
+
+/* ------------------------------------------------------------------ */
+/* exp of the x86 reference build                                      */
+/* ------------------------------------------------------------------ */
+
+/* The x86 reference takes f32::exp from the platform libm (softmax_unnorm_inplace,
+ * real_llm.rs:9590-9600; swiglu_activate_scalar, 9801-9805): glibc's expf, which this
+ * oracle calls directly.  Test support: counts the inputs x, over the fp32 bit patterns
+ * [lo, hi), where fn(x) and expf(x) differ in any bit, on `threads` threads; *first gets
+ * the lowest such bit pattern (0xFFFFFFFF when none). */
+typedef float (*or_f2f)(float);
+typedef struct {
+    or_f2f fn;
+    uint64_t lo, hi, bad;
+    uint32_t first;
+} or_exp_job;
+
+static void *or_exp_worker(void *p) {
+    or_exp_job *j = (or_exp_job *)p;
+    j->bad = 0;
+    j->first = 0xFFFFFFFFu;
+    for (uint64_t b = j->lo; b < j->hi; b++) {
+        const uint32_t u = (uint32_t)b;
+        float x, a, r;
+        memcpy(&x, &u, 4);
+        a = j->fn(x);
+        r = expf(x);
+        if (memcmp(&a, &r, 4) != 0) {
+            if (j->bad == 0) j->first = u;
+            j->bad++;
+        }
+    }
+    return NULL;
+}
+
+uint64_t or_expf_mismatches(or_f2f fn, uint64_t lo, uint64_t hi, int threads, uint32_t *first) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    or_exp_job jobs[64];
+    pthread_t th[64];
+    const uint64_t span = hi > lo ? hi - lo : 0;
+    for (int t = 0; t < threads; t++) {
+        jobs[t].fn = fn;
+        jobs[t].lo = lo + span * (uint64_t)t / (uint64_t)threads;
+        jobs[t].hi = lo + span * (uint64_t)(t + 1) / (uint64_t)threads;
+        pthread_create(&th[t], NULL, or_exp_worker, &jobs[t]);
+    }
+    uint64_t bad = 0;
+    uint32_t f = 0xFFFFFFFFu;
+    for (int t = 0; t < threads; t++) {
+        pthread_join(th[t], NULL);
+        bad += jobs[t].bad;
+        if (jobs[t].bad && jobs[t].first < f) f = jobs[t].first;
+    }
+    if (first) *first = f;
+    return bad;
+}
+
+/* expf over an array (test support: the libm results a device routine is compared with). */
+void or_expf_array(const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = expf(x[i]);
 }

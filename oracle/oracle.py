@@ -70,6 +70,8 @@ def lib():
             "or_rope_row": (None, [SZ, C.c_double, SZ, F32P]),
             "or_rope_apply": (None, [F32P, SZ, F32P]),
             "or_swiglu": (None, [F32P, F32P, F32P, SZ]),
+            "or_expf_mismatches": (C.c_uint64, [VP, C.c_uint64, C.c_uint64, C.c_int, C.POINTER(C.c_uint32)]),
+            "or_expf_array": (None, [F32P, F32P, SZ]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
