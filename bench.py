@@ -131,11 +131,16 @@ def time_case(ctx, torch, case, steps, warmup):
     return a.elapsed_time(b) * 1e-3 / steps
 
 
-def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log):
+def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log, planes=None):
+    """Builds the model, times a `prefill`-token prefill, then `steps` greedy decode steps
+    after `warmup` untimed ones.  The decode steps are timed twice: on the host clock
+    around generate() (decode_tok_s) and by HIP events recorded on the model's own stream
+    around the same steps (kernel_us_per_step: device time of the step's kernels, the
+    persistent decode kernel's launch when that path runs)."""
     import k2t
     t0 = time.perf_counter()
     model, mats, host = k2t.build_random_model(ctx, cfg, max_seq=prefill + warmup + steps + 8, fmt=fmt,
-                                               seed=7, max_batch=256, keep_host=True, threads=0)
+                                               planes=planes, seed=7, max_batch=256, keep_host=True, threads=0)
     t_build = time.perf_counter() - t0
     if os.environ.get("K2T_MODEL_EXACT"):
         model.set_exact(int(os.environ["K2T_MODEL_EXACT"]))
@@ -151,9 +156,17 @@ def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log):
     model.prefill(toks, want_logits=True)
     t_pre = time.perf_counter() - t0
     model.generate(int(toks[-1]), warmup, want_tokens=False)  # graph capture + warm-up
+    model.sync()
+    persistent = model.persistent_active()
+    st = torch.cuda.ExternalStream(model.stream())
+    ev_a, ev_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev_a.record(st)
     t0 = time.perf_counter()
     model.generate(int(toks[-1]), steps, want_tokens=False)
     t_dec = time.perf_counter() - t0
+    ev_b.record(st)
+    ev_b.synchronize()
+    kernel_us = ev_a.elapsed_time(ev_b) * 1e3 / steps
     kv_per_tok = cfg["n_layers"] * cfg["n_kv_heads"] * 2 * (cfg["head_dim"] + 4)
     ctx_mid = prefill + warmup + steps / 2
     tok_s = steps / t_dec
@@ -161,9 +174,13 @@ def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log):
            "prefill_tok_s": round(prefill / t_pre, 1), "prefill_tokens": prefill, "decode_steps": steps,
            "context_at_decode": [prefill + warmup, prefill + warmup + steps],
            "weight_bytes": int(wbytes), "kv_bytes_per_token": kv_per_tok,
-           "decode_GB_s": round((wbytes + kv_per_tok * ctx_mid) * tok_s / 1e9, 1), "build_s": round(t_build, 1)}
-    log(f"# {name}: decode {tok_s:.1f} tok/s ({t_dec / steps * 1e3:.3f} ms/token), prefill "
-        f"{prefill / t_pre:.0f} tok/s, weights {wbytes / 1e6:.1f} MB")
+           "decode_GB_s": round((wbytes + kv_per_tok * ctx_mid) * tok_s / 1e9, 1), "build_s": round(t_build, 1),
+           "persistent_kernel": bool(persistent), "kernel_us_per_step": round(kernel_us, 2),
+           # algorithmic HBM bytes of one decode step: every weight byte once, the K/V read
+           # at the mean context of the timed steps, and the new position's K/V written
+           "step_bytes": int(wbytes + kv_per_tok * ctx_mid + kv_per_tok)}
+    log(f"# {name}: decode {tok_s:.1f} tok/s ({t_dec / steps * 1e3:.3f} ms/token, {kernel_us:.1f} us of device "
+        f"time per step), prefill {prefill / t_pre:.0f} tok/s, weights {wbytes / 1e6:.1f} MB")
     return model, mats, host, res
 
 
@@ -264,11 +281,11 @@ def moe_decode_bench(ctx, torch, steps, warmup, context, log):
     return res
 
 
-def load_traffic(kernel_case):
-    """HBM bytes per launch of the roofline kernel, from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a
-    plain copy of known size).  None when no summary for this case is committed."""
-    path = os.path.join(ROOT, "profiles", f"gemv_{kernel_case}_hbm_traffic.txt")
+def load_traffic(name):
+    """HBM bytes per launch of a roofline kernel, from the committed rocprofv3 --pmc
+    summary profiles/<name>_hbm_traffic.txt (FETCH_SIZE + WRITE_SIZE, each scaled by the
+    same counter's reading for a plain copy of known size).  None when none is committed."""
+    path = os.path.join(ROOT, "profiles", f"{name}_hbm_traffic.txt")
     if not os.path.exists(path):
         return None
     for ln in open(path):
@@ -346,30 +363,29 @@ def cpu_model():
 
 
 def cpu_decode_baseline(cfg, host, context, seconds=10.0, max_tokens=32, name="1.7B nf4g128"):
-    """The reference's portable CPU decode (dequantize + fp32 dot GEMVs over stripe ranges,
-    real_llm.rs:829-836 / simd_lut.rs:5719-5748; scalar q8 attention) restated in the
-    oracle, on this machine's host cores: tokens attending `context`+ positions (the KV
-    cache is seeded, as the GPU run's cache holds its prefill), at all host threads (up to
-    16, the box's CPU share) for about `seconds`, and one token on one thread."""
+    """The reference's portable CPU decode step (dequantize + fp32 dot GEMVs over stripe
+    ranges, real_llm.rs:829-836 / simd_lut.rs:5719-5748; scalar q8 attention) restated in
+    the oracle's C and driven by a C decode loop over a host thread pool
+    (oracle/k2t_cpu_port.c), compiled here with -O3 -march=native: tokens attending
+    `context`+ positions (the KV cache is seeded, as the GPU run's cache holds its
+    prefill), at all host threads (up to 16, the box's CPU share) for about `seconds`, and
+    one token on one thread."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from model_oracle import Matrix, OracleModel
+    import cpu_port
+    path = cpu_port.build()
     threads = min(16, os.cpu_count() or 1)
-    conv = [Matrix(h.fmt, h.rows, h.cols, h.pair, h.tail, hp=h.hp, cb=h.cb, sgc=h.sgc) for h in host]
-    layers = []
-    ones = np.ones(cfg["hidden"], np.float32)
-    for i in range(cfg["n_layers"]):
-        q, o, gu, dn = conv[4 * i:4 * i + 4]
-        layers.append({"qkv": q, "o": o, "gu": gu, "down": dn, "in_norm": ones, "post_norm": ones, "bias": None})
 
     def run(nthreads, budget, cap):
-        om = OracleModel(dict(cfg, max_seq=context + cap + 2), layers, conv[-1], ones, gemv_threads=nthreads)
-        om.seed_kv(context, seed=1)
+        pm = cpu_port.CpuPortModel(cfg, host, nthreads, context + cap + 2, lib_path=path)
+        pm.seed_kv(context, seed=1)
         t0 = time.perf_counter()
         ntok = 0
         while ntok < cap and (ntok < 1 or time.perf_counter() - t0 < budget):
-            om.forward_token(3 + ntok)
+            pm.decode(3 + ntok)
             ntok += 1
-        return ntok, (time.perf_counter() - t0) / ntok
+        dt = (time.perf_counter() - t0) / ntok
+        pm.close()
+        return ntok, dt
 
     run(threads, 0.0, 1)  # warm the page cache and thread pool
     ntok, dt = run(threads, seconds, max_tokens)
@@ -378,7 +394,8 @@ def cpu_decode_baseline(cfg, host, context, seconds=10.0, max_tokens=32, name="1
             "cpu_model": cpu_model(), "one_thread": {"value": round(1.0 / dt1, 4), "unit": "tok/s", "cores": 1},
             "sample": f"{ntok} decode tokens of the {name} model at context {context}-{context + ntok} (KV "
                       f"cache seeded) on the portable path (dequantize + fp32 dot, simd_lut.rs:5719-5748) restated "
-                      f"in C, {threads} host threads; one_thread: 1 token on 1 thread"}
+                      f"in C with a C decode loop, gcc -O3 -march=native on this host, {threads} threads; "
+                      f"one_thread: 1 token on 1 thread"}
 
 
 def cpu_gemv_baseline(cases):
@@ -513,6 +530,14 @@ def main():
     for m in mats135:
         m.close()
     torch.cuda.empty_cache()
+    # ---- the same 135M shape with 4 bit planes everywhere (the reference's B4 tier)
+    mb4, matsb4, hostb4, rb4 = decode_bench(ctx, torch, "135M b4", k2t.SMOLLM2_135M, "n4", 512, 64, 8, log,
+                                            planes={k: 4 for k in k2t.P55454})
+    del hostb4
+    mb4.close()
+    for m in matsb4:
+        m.close()
+    torch.cuda.empty_cache()
     # ---- config 5: 30B-A3B-shaped sparse MoE, decode at context 6600
     r30 = None if args.no_moe else moe_decode_bench(ctx, torch, 32, 4, args.moe_context, log)
 
@@ -532,12 +557,23 @@ def main():
                 "random token ids; greedy decode",
         "config": {"workload": "config 3: SmolLM2-1.7B-shaped nf4g128 (24 layers, d 2048, 32 heads MHA, hd 64, "
                                "ffn 8192, vocab 49152), 256-token prefill in 4-token tiles then greedy decode",
-                   "decode_1_7b_nf4g128": r17, "decode_135m_p55454_ctx512": r135,
+                   "decode_1_7b_nf4g128": r17, "decode_135m_p55454_ctx512": r135, "decode_135m_b4_ctx512": rb4,
                    "decode_30b_a3b_moe_nf3_ctx6600": r30, "gemv_sweep": results},
-        "roofline": {"bound": "hbm", "kernel": f"gemv_kernel ({dom})", "achieved": dr["GB_s"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(dr["GB_s"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(dom),
-                     "algorithmic_bytes_per_launch": dr["bytes"], "avg_launch_us": dr["us"],
-                     "copy_ceiling_same_bytes": ceiling, "read_ceiling_same_bytes": rceiling},
+        # the kernel behind `value`: one persistent decode launch per token
+        "roofline": {"bound": "hbm",
+                     "kernel": "decode_mk_kernel<1,0,512> (one launch per 1.7B nf4g128 decode step)"
+                     if r17["persistent_kernel"] else "per-operation decode step (HIP graph)",
+                     "achieved": round(r17["step_bytes"] / r17["kernel_us_per_step"] / 1e3, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(r17["step_bytes"] / r17["kernel_us_per_step"] / 1e3 / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic("decode_1_7b_nf4g128"),
+                     "algorithmic_bytes_per_launch": r17["step_bytes"], "avg_launch_us": r17["kernel_us_per_step"],
+                     # the sweep's slowest nf4 batch-1 GEMV (config 4)
+                     "gemv": {"kernel": f"gemv_kernel ({dom})", "achieved": dr["GB_s"], "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(dr["GB_s"] / HBM_PEAK_GBS, 4),
+                              "traffic": load_traffic(f"gemv_{dom}"), "algorithmic_bytes_per_launch": dr["bytes"],
+                              "avg_launch_us": dr["us"], "copy_ceiling_same_bytes": ceiling,
+                              "read_ceiling_same_bytes": rceiling}},
         "cpu_baseline": cpu,
     })
     print(json.dumps(line))

@@ -301,6 +301,10 @@ int32_t k2t_model_set_exact(k2t_model *m, int32_t exact);
  * per-operation path).  A step that attends more than 1024 positions runs the
  * per-operation path (a few workgroups per head scanning the context are slower there). */
 int32_t k2t_model_set_persistent(k2t_model *m, int32_t enable);
+/* The hipStream_t (as void*) this model's steps are enqueued on: for the caller's own
+ * events around a step (bench timing) or waits.  Measurement support, no reference
+ * counterpart. */
+int32_t k2t_model_stream(const k2t_model *m, void **hip_stream);
 /* Whether the next decode step (at the current position) runs the persistent kernel. */
 int32_t k2t_model_persistent_active(const k2t_model *m, int32_t *active);
 /* reset_context: position back to 0. */

@@ -906,6 +906,13 @@ int32_t k2t_model_set_graph(k2t_model *m, int32_t enable) {
     });
 }
 
+int32_t k2t_model_stream(const k2t_model *m, void **hip_stream) {
+    return mguard([&] {
+        arg(m && hip_stream, "NULL argument");
+        *hip_stream = (void *)m->stream;
+    });
+}
+
 int32_t k2t_model_set_exact(k2t_model *m, int32_t exact) {
     return mguard([&] {
         arg(m != nullptr, "model is NULL");
@@ -1176,7 +1183,7 @@ void attn_decode_impl(k2t_ctx *ctx, int32_t bits, const float *d_q, int32_t n_he
         if (noalloc) {
             if (words > kNoAllocGqaWords)
                 throw Error(K2T_E_ARG, "k2t_attn_decode_noalloc: ceil(cap / 128) * n_heads * (head_dim + 2) = " +
-                                           std::to_string(words) + " span words exceeds its fixed region of " +
+                                           std::to_string(words) + " span words exceeds its fixed scratch region of " +
                                            std::to_string(kNoAllocGqaWords));
             gq = noalloc_gqa(ctx->device);
         } else {

@@ -75,6 +75,7 @@ SIGNATURES = {
     "k2t_model_set_graph": (I32, [VP, I32]),
     "k2t_model_set_exact": (I32, [VP, I32]),
     "k2t_model_set_persistent": (I32, [VP, I32]),
+    "k2t_model_stream": (I32, [VP, C.POINTER(VP)]),
     "k2t_model_persistent_active": (I32, [VP, C.POINTER(I32)]),
     "k2t_model_reset": (I32, [VP]),
     "k2t_model_position": (I32, [VP, C.POINTER(I32)]),
@@ -520,6 +521,12 @@ class Model:
 
     def set_exact(self, on):
         check(lib().k2t_model_set_exact(self.h, int(bool(on))))
+
+    def stream(self):
+        """The hipStream_t (int) the model's steps run on."""
+        s = VP()
+        check(lib().k2t_model_stream(self.h, C.byref(s)))
+        return s.value or 0
 
     def set_persistent(self, on):
         """True / 1: the persistent decode kernel where supported; 2: also for mixed 4/5-plane

@@ -98,6 +98,33 @@ def test_attn_decode_matches_oracle(gpu_ctx, bits, hd, seq, window, sinks):
         assert np.abs(got[h] - want).max() <= 1e-4 * np.abs(want).max(), (h, np.abs(got[h] - want).max())
 
 
+# Grouped queries at long context: k2t_attn_decode runs the model's grouped-query kernel
+# (span workgroups per (KV head, 128 positions) scoring all G q heads of the group, merge
+# workgroups polling the span words in the same launch).  The config-5 shape (32 q / 4 KV
+# heads, hd 128: G = 8) at the bench's context 6600 (52 spans), G = 4 at 2000 and G = 8 at
+# hd 64; two calls per case (the words' epoch advances between launches).
+@pytest.mark.parametrize("nq,nkv,hd,seq", [(32, 4, 128, 6600), (16, 4, 64, 2000), (32, 4, 64, 3000)])
+def test_attn_decode_grouped_queries_matches_oracle(gpu_ctx, nq, nkv, hd, seq):
+    print(f"attn_decode grouped queries nq={nq} nkv={nkv} hd={hd} seq={seq}", flush=True)
+    rng = np.random.default_rng(seq + nq)
+    kq, ks, vq, vs = _cache(rng, 8, nkv, seq, hd, seq)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    dk, dks, dv, dvs = dev(kq), dev(ks), dev(vq), dev(vs)
+    scale = 1.0 / np.sqrt(hd)
+    for call in range(2):
+        q = rng.standard_normal((nq, hd)).astype(np.float32)
+        out = torch.full((nq, hd), float("nan"), dtype=torch.float32, device="cuda")
+        gpu_ctx.attn_decode(8, dev(q), nq, nkv, hd, dk, dks, dv, dvs, seq, seq - call, scale, out)
+        gpu_ctx.sync()
+        got = out.cpu().numpy()
+        n = seq - call
+        for h in range(nq):
+            kv = h // (nq // nkv)
+            want = O.attn_q8_head(q[h], kq[kv, :n], ks[kv, :n], vq[kv, :n], vs[kv, :n], scale)
+            err = np.abs(got[h] - want).max()
+            assert err <= 1e-4 * np.abs(want).max(), (call, h, err, np.abs(want).max())
+
+
 @pytest.mark.parametrize("window", [0, 16])
 def test_nf4_kv_model_matches_oracle(gpu_ctx, window):
     """set_kv_bits(4): the engine stores and reads the NF4 Hadamard KV cache; decode vs the

@@ -408,14 +408,29 @@ def test_config5_moe_full_width_matches_oracle(gpu_ctx, n_ctx):
     def embed(tok):
         return (emb2[tok].astype(np.uint32) << 16).view(np.float32)
 
-    ref = OracleModel(cfg, layers, hh, fn, embed=embed, parity_threads=THREADS)
-    gm.kv_synthetic(n_ctx, seed=SEED)
-    synthetic_kv(ref, n_layers, nkv, hd, n_ctx, SEED)
     toks = np.random.default_rng(SEED + 6).integers(0, V, 3)
-    for i, t in enumerate(toks):
-        a, b = gm.decode(int(t)), ref.forward_token(int(t))
-        ok, info = _close(a, b)
-        assert ok, f"decode at context {n_ctx + i}: {info}"
+    # fast path: at 1100 the fixed bar; at 6600 the attention output is an average over
+    # 6600 random V rows, near zero, and the grouped-query kernel's span-order sums move
+    # single int8 codes of it against the oracle's sequential order (the kernel itself
+    # is within 1e-4 of the oracle at this shape: test_attn_decode_grouped_queries_*), so
+    # cosine > 0.9998 there; the exact-order run below then carries the tight bar
+    cos_min = 0.9999 if n_ctx <= 1100 else 0.9998
+    for exact in ((False,) if n_ctx <= 1100 else (False, True)):
+        gm.set_exact(exact)
+        ref = OracleModel(cfg, layers, hh, fn, embed=embed, parity_threads=THREADS)
+        gm.kv_synthetic(n_ctx, seed=SEED)
+        synthetic_kv(ref, n_layers, nkv, hd, n_ctx, SEED)
+        for i, t in enumerate(toks):
+            a, b = gm.decode(int(t)), ref.forward_token(int(t))
+            if exact:
+                # exact-order attention and norms (the MoE feed-forward keeps its order)
+                cos = float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
+                rel = float(np.abs(a - b).max() / np.abs(b).max())
+                print(f"  exact order at context {n_ctx + i}: 1-cos {1 - cos:.2e} rel {rel:.2e}", flush=True)
+                assert cos > 0.999999 and rel <= 1e-3, f"exact order, context {n_ctx + i}: {(rel, cos)}"
+            else:
+                ok, info = _close(a, b, cos_min)
+                assert ok, f"decode at context {n_ctx + i}: {info}"
     gm.close()
     for m in mats:
         m.close()
