@@ -118,7 +118,9 @@ int32_t k2t_mat_wrap_nf(k2t_ctx *ctx, int32_t rows, int32_t cols, int32_t bits, 
  * stores NF3 in this order, k2t_mat_wrap_nf leaves the borrowed bytes in the reference
  * layout until this call.  Results are unchanged; no-op for other formats and matrices
  * already converted; synchronous.  A dense stream carries no mark: wrap converted bytes
- * again only with a matrix that is then converted by no one (or re-upload them). */
+ * again only with a matrix that is then converted by no one (or re-upload them).  Every
+ * other handle that already wraps the same bytes keeps reading them in the reference
+ * order and gives wrong results afterwards: destroy such handles before converting. */
 int32_t k2t_mat_nf3_lane_order(k2t_mat *m);
 void k2t_mat_destroy(k2t_mat *m);
 /* rows, cols, stripes and streamed bytes (pair + tail + codebook). */
@@ -398,7 +400,9 @@ int32_t k2t_experts_wrap(k2t_ctx *ctx, const uint8_t *d_k2tm, size_t len, const 
  * are no longer in the .k2tm layout afterwards; the conversion writes a 16-byte mark into
  * the last 16 bytes of the device header page (zero padding in the format), so a later
  * k2t_experts_wrap of the same bytes reads them in lane order and converting again is a
- * no-op. */
+ * no-op.  A handle reads the mark when it wraps the bytes: every other handle that already
+ * wraps the same bytes keeps the reference order and gives wrong MoE outputs afterwards,
+ * so destroy such handles before converting (and wrap again). */
 int32_t k2t_experts_nf3_lane_order(k2t_experts *bank);
 void k2t_experts_destroy(k2t_experts *b);
 int32_t k2t_experts_info(const k2t_experts *b, k2t_k2tm_header *out);

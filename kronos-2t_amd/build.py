@@ -63,7 +63,7 @@ def _compile(src, objdir=None, defines=()):
     return obj, resource_usage(r.stderr)
 
 
-def check_m0(src):
+def check_m0(src, objdir=None, defines=()):
     """Checks of the generated device assembly.
 
     M0: sources that stage weights with inline-assembly LDS-DMA loads set M0 themselves
@@ -76,8 +76,9 @@ def check_m0(src):
     or a select of an LDS and a global pointer).  It counts against both the vector-memory
     and the LDS counters, so its wait also waits for every global load and store the wave
     has in flight, the weight prefetches included."""
-    asm = os.path.join(OBJ, os.path.basename(src) + ".s")
-    cmd = [HIPCC, *[f for f in FLAGS if not f.startswith("-Rpass")], "--cuda-device-only", "-S", src, "-o", asm]
+    asm = os.path.join(objdir or OBJ, os.path.basename(src) + ".s")
+    cmd = [HIPCC, *[f for f in FLAGS if not f.startswith("-Rpass")], *[f"-D{d}" for d in defines],
+           "--cuda-device-only", "-S", src, "-o", asm]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc -S failed for {src}:\n{r.stderr}")
@@ -104,7 +105,7 @@ def build(verbose=False, out=None, defines=()):
         res = list(ex.map(lambda src: _compile(src, objdir, defines), srcs))
     objs = [o for o, _ in res]
     with cf.ThreadPoolExecutor(max_workers=8) as ex:
-        list(ex.map(check_m0, [src for src in srcs if src.endswith(".hip")]))
+        list(ex.map(lambda src: check_m0(src, objdir, defines), [src for src in srcs if src.endswith(".hip")]))
     usage = [u for _, us in res for u in us]
     with open(os.path.join(objdir, "resource_usage.txt"), "w") as f:
         for name, u in usage:

@@ -579,10 +579,19 @@ void forward_mk(k2t_model *m) {
     P.spin_limit = 1u << 22;
 #ifdef K2T_MK_TRACE
     // measurement build: eager steps dump the phase trace to $K2T_MK_TRACE
+    // (one buffer for the process, regrown when a model with more layers is traced)
     static unsigned long long *trace = nullptr;
+    static size_t trace_cap = 0;
     const size_t ntr = (size_t)m->ctx->num_cus * (c.n_layers + 1) * 6 * 6;
     if (getenv("K2T_MK_TRACE") && !m->use_graph) {
-        if (!trace) hip_check(hipMalloc(&trace, ntr * 8), "trace");
+        if (ntr > trace_cap) {
+            hip_check(hipStreamSynchronize(m->stream), "sync");
+            if (trace) hip_check(hipFree(trace), "trace free");
+            trace = nullptr;
+            trace_cap = 0;
+            hip_check(hipMalloc(&trace, ntr * 8), "trace");
+            trace_cap = ntr;
+        }
         hip_check(hipMemset(trace, 0, ntr * 8), "trace clear");
         P.trace = trace;
     }
