@@ -538,6 +538,14 @@ def main():
     for m in matsb4:
         m.close()
     torch.cuda.empty_cache()
+    # ---- and with 6 bit planes everywhere (the B6 tier: the 256-thread two-hi-plane kernel)
+    mb6, matsb6, hostb6, rb6 = decode_bench(ctx, torch, "135M b6", k2t.SMOLLM2_135M, "n4", 512, 64, 8, log,
+                                            planes={k: 6 for k in k2t.P55454})
+    del hostb6
+    mb6.close()
+    for m in matsb6:
+        m.close()
+    torch.cuda.empty_cache()
     # ---- config 5: 30B-A3B-shaped sparse MoE, decode at context 6600
     r30 = None if args.no_moe else moe_decode_bench(ctx, torch, 32, 4, args.moe_context, log)
 
@@ -558,6 +566,7 @@ def main():
         "config": {"workload": "config 3: SmolLM2-1.7B-shaped nf4g128 (24 layers, d 2048, 32 heads MHA, hd 64, "
                                "ffn 8192, vocab 49152), 256-token prefill in 4-token tiles then greedy decode",
                    "decode_1_7b_nf4g128": r17, "decode_135m_p55454_ctx512": r135, "decode_135m_b4_ctx512": rb4,
+                   "decode_135m_b6_ctx512": rb6,
                    "decode_30b_a3b_moe_nf3_ctx6600": r30, "gemv_sweep": results},
         # the kernel behind `value`: one persistent decode launch per token
         "roofline": {"bound": "hbm",

@@ -479,14 +479,15 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
     }
     // 1. this position's q (and k, v where the span holds it) (+ bias)
     bool ok = true;
-    if (t < (cover ? 3 : 1) * hd) {
-        const int part = t / hd, i = t % hd;
+    // (up to 3 * 128 words: more than the 256-thread kernel's threads at hd 128)
+    for (int e = t; e < (cover ? 3 : 1) * hd && ok; e += NTH) {
+        const int part = e / hd, i = e % hd;
         const int row = part == 0 ? h * hd + i : part == 1 ? (nq + kvh) * hd + i : (nq + nkv + kvh) * hd + i;
         uint32_t v = 0;
         ok = ll_wait(P, P.QKV + row, ep_in, v);
         float f = __uint_as_float(v);
         if (bias) f = f + bias[row];
-        qf[t] = f;  // qf, kf, vf are contiguous
+        qf[e] = f;  // qf, kf, vf are contiguous
     }
     if (t == 0) S.flag[0] = 0;
     lds_barrier();
@@ -770,14 +771,14 @@ __device__ bool attention_head_ex(const MkParams &P, const float *bias, const Ld
         rsn = rrow[(nb == 1 ? 32u : 64u) + ri];
     }
     bool ok = true;
-    if (t < 3 * hd) {
-        const int part = t / hd, i = t % hd;
+    for (int e = t; e < 3 * hd && ok; e += NTH) {
+        const int part = e / hd, i = e % hd;
         const int row = part == 0 ? h * hd + i : part == 1 ? (nq + kvh) * hd + i : (nq + nkv + kvh) * hd + i;
         uint32_t v = 0;
         ok = ll_wait(P, P.QKV + row, ep_in, v);
         float f = __uint_as_float(v);
         if (bias) f = f + bias[row];
-        qf[t] = f;
+        qf[e] = f;
     }
     if (t == 0) S.flag[0] = 0;
     lds_barrier();
@@ -1286,7 +1287,8 @@ size_t decode_mk_lds_bytes(const k2t_model_config &c) {
     // fragments, 4 waves x mixed-plane fragments)
     const size_t ring = std::max({(size_t)8 * kMkFrags * frag_lds_bytes<1, 0>(),
                                   (size_t)8 * kMkFrags * frag_lds_bytes<0, 0>(),
-                                  (size_t)4 * kMkFrags * frag_lds_bytes<0, kHpMixed>()});
+                                  (size_t)4 * kMkFrags * frag_lds_bytes<0, kHpMixed>(),
+                                  (size_t)4 * kMkFrags * frag_lds_bytes<0, 2>()});
     b += std::max(att, ring);
     return (b + 255) / 256 * 256;
 }
@@ -1307,22 +1309,24 @@ bool decode_mk_supported(const k2t_model_config &c, int num_cus) {
     if (c.hidden > 8192 || c.intermediate > 32768) return false;
     const size_t lds = decode_mk_lds_bytes(c);
     return num_cus > 0 && occupancy_ok<1, 0, 512>(lds) && occupancy_ok<0, 0, 512>(lds) &&
-           occupancy_ok<0, kHpMixed, 256>(lds);
+           occupancy_ok<0, kHpMixed, 256>(lds) && occupancy_ok<0, 2, 256>(lds);
 }
 
-int decode_mk_threads(int hp) { return hp == kHpMixed ? 256 : 512; }
+int decode_mk_threads(int hp) { return hp == kHpMixed || hp == 2 ? 256 : 512; }
 
 bool decode_mk_format(const MatDev &m, int &fmt, int &hp) {
-    if (m.fmt == 0 && m.hp > 1) return false;  // b6 fragments exceed the register budget
-    if (m.fmt == 2) return false;               // NF3 runs on the per-operation path
-    // any 5-plane matrix selects the 256-thread kernel that reads each matrix's plane count
-    const int mhp = m.fmt == 0 && m.hp == 1 ? kHpMixed : 0;
+    if (m.fmt == 2) return false;  // NF3 runs on the per-operation path
+    // bit planes: any 5-plane matrix selects the 256-thread kernel that reads each matrix's
+    // plane count (4 or 5); 6-plane (b6) models run the 256-thread two-hi-plane kernel,
+    // which needs every matrix at 6 planes
+    const int mhp = m.fmt != 0 ? 0 : m.hp == 2 ? 2 : m.hp == 1 ? kHpMixed : 0;
     if (fmt < 0) {
         fmt = m.fmt;
         hp = mhp;
         return true;
     }
     if (m.fmt != fmt) return false;
+    if ((mhp == 2) != (hp == 2)) return false;
     if (mhp == kHpMixed) hp = kHpMixed;
     return true;
 }
@@ -1333,6 +1337,8 @@ static void launch_mk(hipStream_t st, const MkParams &P, int fmt, int hp, int nu
     else if (hp == 0) hipLaunchKernelGGL((decode_mk_kernel<0, 0, 512, EX>), dim3(num_cus), dim3(512), lds, st, P);
     else if (hp == kHpMixed)
         hipLaunchKernelGGL((decode_mk_kernel<0, kHpMixed, 256, EX>), dim3(num_cus), dim3(256), lds, st, P);
+    else if (hp == 2)
+        hipLaunchKernelGGL((decode_mk_kernel<0, 2, 256, EX>), dim3(num_cus), dim3(256), lds, st, P);
     else throw Error(K2T_E_INTERNAL, "persistent decode kernel: unsupported weight format");
 }
 

@@ -315,20 +315,22 @@ def test_config3_exact_order(gpu_ctx, n_layers):
             m.close()
 
 
-@pytest.mark.parametrize("n_layers", [2, 30])
-def test_config2_exact_order(gpu_ctx, n_layers):
-    """The 135M p55454 bench model at context 512 (synthetic K/V 448 + a 64-token batched
-    prefill) in exact-order mode, on the mixed-plane persistent kernel's exact-order
-    variant and on the per-operation graph: two decode steps, every logit bit-identical to
-    the x86 oracle's, at 2 layers and at the full 30."""
-    print(f"config 2: 135M p55454 ctx 512 exact order vs x86 oracle, {n_layers} layers", flush=True)
+@pytest.mark.parametrize("tier,n_layers", [("p55454", 2), ("p55454", 30), ("b6", 2)])
+def test_config2_exact_order(gpu_ctx, tier, n_layers):
+    """The 135M bench model at context 512 (synthetic K/V 448 + a 64-token batched
+    prefill) in exact-order mode, on the persistent kernel's exact-order variant (the
+    mixed-plane kernel for p55454, the two-hi-plane kernel for all-b6) and on the
+    per-operation graph: two decode steps, every logit bit-identical to the x86 oracle's;
+    p55454 at 2 layers and at the full 30, b6 at 2."""
+    print(f"config 2: 135M {tier} ctx 512 exact order vs x86 oracle, {n_layers} layers", flush=True)
     cfg = dict(k2t.SMOLLM2_135M, n_layers=n_layers)
+    planes = k2t.P55454 if tier == "p55454" else {k: 6 for k in k2t.P55454}
     n_syn, n_pre = 448, 64
     toks = np.random.default_rng(SEED + 1).integers(0, cfg["vocab"], n_pre + 2).astype(np.int32)
     runs = []
     for pk in (1, 0):
         model, mats, host = k2t.build_random_model(gpu_ctx, cfg, max_seq=n_syn + n_pre + 8, fmt="n4", seed=7,
-                                                   max_batch=64, keep_host=True)
+                                                   planes=planes, max_batch=64, keep_host=True)
         model.set_exact(True)
         model.set_persistent(pk)
         model.kv_synthetic(n_syn, seed=SEED)

@@ -54,13 +54,14 @@ def test_expf_device_matches_libm(gpu_ctx):
 CASES = [("nf4_hd64", TINY, "nf4", None, {}),
          ("p55454_hd64", TINY, "n4", P55454, {}),
          ("b6_hd128", TINY128, "n4", {k: 6 for k in P55454}, {}),
+         ("nf4_hd128", TINY128, "nf4", None, {}),
          ("nf4_bias_qknorm", TINY, "nf4", None, {"bias": True, "qk_norm": True}),
          ("nf4_window", dict(TINY, max_seq=600), "nf4", None, {"window": (16, 4)})]
 
 
 # decode steps of these run the persistent kernel's exact-order variant (one weight format
 # family, int8 KV without a window, no q / k norm); the others the per-operation path
-PERSISTENT = ("nf4_hd64", "p55454_hd64")
+PERSISTENT = ("nf4_hd64", "p55454_hd64", "b6_hd128", "nf4_hd128")
 
 
 @pytest.mark.parametrize("persistent", [1, 0])

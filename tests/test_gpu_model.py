@@ -60,11 +60,11 @@ def test_decode_matches_oracle(gpu_ctx, name, cfg, fmt, planes, exact):
     ref = OracleModel(cfg, layers, head, fn)
     gm, _ = _gpu_model(gpu_ctx, cfg, layers, head, fn)
     gm.set_exact(exact)  # exact-order steps (bit-identical: test_gpu_exact.py), or the fast path
-    # both modes run the persistent single-launch decode kernel where every matrix is NF4 or
-    # has 4 or 5 bit planes (p55454 mixes b5 and b4: mode 2 runs the 256-thread variant that
-    # reads each matrix's plane count); b6 runs the per-operation path
+    # both modes run the persistent single-launch decode kernel: NF4; 4 or 5 bit planes
+    # (p55454 mixes b5 and b4: the 256-thread variant that reads each matrix's plane
+    # count); b6 (the 256-thread two-hi-plane variant)
     gm.set_persistent(2)
-    assert gm.persistent_active() == (name in ("nf4_hd64", "p55454_hd64"))
+    assert gm.persistent_active()
     rng = np.random.default_rng(9)
     toks = rng.integers(0, cfg["vocab"], 8)
     for i, t in enumerate(toks):
