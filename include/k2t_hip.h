@@ -261,6 +261,15 @@ int32_t k2t_model_set_qk_norm(k2t_model *m, int32_t layer, const float *q_norm, 
 int32_t k2t_model_set_moe(k2t_model *m, int32_t layer, const k2t_experts *bank, int32_t shard_layer,
                           const float *router_w, const float *router_bias, int32_t top_k, int32_t norm_topk_prob,
                           int32_t scoring);
+/* The shared expert of a sparse-MoE layer (SharedMoeExpert with the NF backend,
+ * sparse_moe.rs:209-312, applied in forward_layer_single 989-1000): gate_up, an NF matrix
+ * [2 * inter][hidden] in [gate; up] row order (inter a multiple of 64), and down
+ * [hidden][inter], both borrowed; gate_weight (host [hidden], copied) or NULL.  Each
+ * token's MoE output becomes shared(x_norm) * scale + sum_k w_k expert_k(x_norm), with
+ * scale = sigmoid(gate_weight . x_norm) (1 without a gate), before the residual add.
+ * Call after k2t_model_set_moe; gate_up = NULL removes the shared expert. */
+int32_t k2t_model_set_moe_shared(k2t_model *m, int32_t layer, const k2t_mat *gate_up, const k2t_mat *down,
+                                 const float *gate_weight);
 /* set_kv_sliding_window (real_llm.rs:1764-1790): an O(1) sliding-window + attention-sink
  * ring for the int8 KV cache (QuantizedKvCache::new_with_opts, real_llm.rs:1235-1257).
  * window >= 8 with window + 512 < max_seq enables it: sinks = min(sink_tokens, window/2),

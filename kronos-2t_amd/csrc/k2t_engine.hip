@@ -880,6 +880,39 @@ int32_t k2t_model_set_moe(k2t_model *m, int32_t layer, const k2t_experts *bank, 
     });
 }
 
+int32_t k2t_model_set_moe_shared(k2t_model *m, int32_t layer, const k2t_mat *gate_up, const k2t_mat *down,
+                                 const float *gate_weight) {
+    return mguard([&] {
+        arg(m != nullptr, "model is NULL");
+        arg(layer >= 0 && layer < m->cfg.n_layers, "layer out of range");
+        auto &L = m->layers[layer];
+        arg(L.has_moe, "set the layer's MoE first (k2t_model_set_moe)");
+        drop_graph(m);
+        if (!gate_up) {
+            L.moe.sh_gu = L.moe.sh_dn = nullptr;
+            L.moe.sh_gate = nullptr;
+            return;
+        }
+        const int d = m->cfg.hidden;
+        arg(down != nullptr, "down is NULL");
+        arg(gate_up->ctx == m->ctx && down->ctx == m->ctx, "matrix of another context");
+        arg(gate_up->fmt == K2T_FMT_NF && down->fmt == K2T_FMT_NF, "the shared expert's matrices must be NF");
+        arg(gate_up->cols == d && gate_up->rows % 128 == 0, "shared gate_up must be [2*inter][hidden], inter % 64 == 0");
+        const int inter = gate_up->rows / 2;
+        arg(down->rows == d && down->cols == inter, "shared down must be [hidden][inter]");
+        hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
+        L.moe.sh_buf = (float *)dalloc(m, ((size_t)2 * inter + d + 64) * sizeof(float));
+        float *g = nullptr;
+        if (gate_weight) {
+            g = (float *)dalloc(m, (size_t)d * sizeof(float));
+            hip_check(hipMemcpy(g, gate_weight, (size_t)d * sizeof(float), hipMemcpyHostToDevice), "gate upload");
+        }
+        L.moe.sh_gu = gate_up;
+        L.moe.sh_dn = down;
+        L.moe.sh_gate = g;
+    });
+}
+
 int32_t k2t_model_set_embedding(k2t_model *m, int32_t kind, const void *rows, const k2t_mat *nf4) {
     return mguard([&] {
         arg(m != nullptr, "model is NULL");

@@ -882,7 +882,8 @@ static void launch_fmt(const k2t_mat *m, int nt, int xs, dim3 grid, dim3 block, 
 static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                              const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
                              int32_t *dots, bool accum, int xsm = 0, const float *src = nullptr,
-                             const float *w = nullptr, float eps = 0.0f, const GemvGroup *grp = nullptr);
+                             const float *w = nullptr, float eps = 0.0f, const GemvGroup *grp = nullptr,
+                             int gu_split = 0);
 
 void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                  const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
@@ -896,9 +897,9 @@ void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const floa
 }
 
 void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float *src, const float *w, float eps,
-                       float *out, bool accumulate) {
+                       float *out, bool accumulate, int gu_split) {
     launch_gemv_impl(ctx, m, nullptr, nullptr, nullptr, 1, 0, m->stripes, out, (size_t)m->rows, nullptr, accumulate,
-                     xs_mode, src, w, eps);
+                     xs_mode, src, w, eps, nullptr, gu_split);
 }
 
 void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, int xs_mode, const float *src,
@@ -912,7 +913,7 @@ void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, 
 static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                              const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
                              int32_t *dots, bool accum, int xsm, const float *src, const float *w, float eps,
-                             const GemvGroup *grp) {
+                             const GemvGroup *grp, int gu_split) {
     const int saved = ctx->max_segments;
     if (dots) ctx->max_segments = 1;
     GemvPlan plan = plan_gemv(ctx, m, s0, s1);
@@ -943,6 +944,7 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
     P.cb1 = m->cb[1];
     P.cb2 = m->cb[2];
     P.cb3 = m->cb[3];
+    P.gu_split = gu_split;  // (grouped launches set their own below)
     // Tokens per weight pass: 4, fewer when the staged terms would not fit in 64 KB of LDS.
     size_t per_tok = ctx->exact ? (size_t)m->nc * (plan.stripe_mode ? 16 : 32) * sizeof(float2)
                                 : (size_t)plan.nseg * 32 * sizeof(float);

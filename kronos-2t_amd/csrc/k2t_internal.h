@@ -85,8 +85,9 @@ void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *
 //   K2T_XS_STAGED : a ready int8 activation (xq, xs, xsum) staged through LDS per wave
 //   K2T_XS_STAGED_DMA: as K2T_XS_STAGED, staged by direct-to-LDS loads (see gemv_kernel)
 enum { K2T_XS_GLOBAL = 0, K2T_XS_RMSNORM = 1, K2T_XS_SWIGLU = 2, K2T_XS_STAGED = 3, K2T_XS_STAGED_DMA = 5 };
+// gu_split = 1: a split [gate; up] matrix whose rows are written in [gate64, up64] blocks.
 void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float *src, const float *w, float eps,
-                       float *out, bool accumulate);
+                       float *out, bool accumulate, int gu_split = 0);
 uint64_t hadamard_sign_mask_host(uint64_t block);
 
 // Grouped GEMV over sparse-MoE experts of one .k2tm bank (see GemvParams::route): slot z

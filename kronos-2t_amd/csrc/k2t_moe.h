@@ -33,6 +33,12 @@ struct MoeLayer {
     const float *router_w;  // [E][d_model]
     const float *router_b;  // [E] or NULL
     int top_k, norm_topk, scoring;
+    // Shared expert (SharedMoeExpert, sparse_moe.rs:209-312), applied to every token: an NF
+    // gate_up in [gate; up] row order and its down, an optional sigmoid gate row, and its
+    // device buffer [2 * inter gate_up | d output | 64 (gate scale)].
+    const k2t_mat *sh_gu = nullptr, *sh_dn = nullptr;
+    const float *sh_gate = nullptr;  // [d_model] or NULL (scale 1)
+    float *sh_buf = nullptr;
 };
 
 // Device workspace of one MoE forward.

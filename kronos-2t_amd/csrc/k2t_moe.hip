@@ -160,13 +160,24 @@ void launch_moe_clear(hipStream_t st, const MoeWork &ws, int E) {
 constexpr int kCombineMax = 8;
 // With ctr set, thread 0 advances the route-call counter (routing ran inside the gate_up
 // launch, whose workgroups have all read it by now).
+// With a shared expert (sh != NULL) the sum starts from its output, times the gate scale
+// when a gate is present and the scale differs from 1 by more than FLT_EPSILON
+// (forward_single then forward_layer_single, sparse_moe.rs:252-312, 989-1000).
 __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ hidden, const float *__restrict__ eo,
                                                           const float *__restrict__ wts, int k, int d,
-                                                          uint32_t *__restrict__ ctr) {
+                                                          uint32_t *__restrict__ ctr, const float *__restrict__ sh,
+                                                          const float *__restrict__ sh_scale) {
     const int r = (int)blockIdx.x * 256 + (int)threadIdx.x;
     if (ctr && r == 0) *ctr = *ctr + 1u;
     if (r >= d) return;
     float p = 0.0f;
+    if (sh) {
+        p = sh[r];
+        if (sh_scale) {
+            const float g = sh_scale[0];
+            if (fabsf(g - 1.0f) > FLT_EPSILON) p = p * g;
+        }
+    }
     if (k <= kCombineMax) {
         float e[kCombineMax];
 #pragma unroll
@@ -182,11 +193,53 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ hi
     hidden[r] = hidden[r] + p;
 }
 
+// Gate scale of the shared expert: 1 / (1 + exp(-dot(gate, x_norm))) with x_norm =
+// (hidden * inv_rms) * post_norm (gate_scale, sparse_moe.rs:241-250); inv_rms in the
+// fused activation builders' order (row_sumsq_wave), the dot as a fixed tree.  One
+// workgroup; the scale goes to out[0].
+__global__ __launch_bounds__(256) void moe_shared_gate_kernel(const float *__restrict__ hidden,
+                                                              const float *__restrict__ post_norm, float eps, int d,
+                                                              const float *__restrict__ gate, float *__restrict__ out) {
+    __shared__ float part[5];
+    const uint32_t lane = threadIdx.x & 63u;
+    const int wave = (int)(threadIdx.x >> 6);
+    if (wave == 0) {
+        const float ss = row_sumsq_wave(hidden, d, lane);
+        if (lane == 0) part[4] = 1.0f / sqrtf(ss / (float)d + eps);
+    }
+    __syncthreads();
+    const float inv = part[4];
+    float z = 0.0f;
+    for (int i = (int)threadIdx.x; i < d; i += 256) z = fmaf(gate[i], (hidden[i] * inv) * post_norm[i], z);
+    z = wave_sum_f(z);
+    if (lane == 0) part[wave] = z;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float t = (part[0] + part[1]) + (part[2] + part[3]);
+        out[0] = 1.0f / (1.0f + expf(-t));
+    }
+}
+
 void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float *post_norm, float eps,
                     const MoeWork &ws) {
     const k2t_experts *b = L.bank;
     const int d = (int)b->hdr.d_model, dff = (int)b->hdr.d_ff_expert, E = (int)b->hdr.experts_per_layer;
     hipStream_t st = ctx->stream;
+    // shared expert first (it reads the same x_norm; its output seeds the combine's sum)
+    float *sh_out = nullptr, *sh_scale = nullptr;
+    if (L.sh_gu) {
+        const int inter = L.sh_gu->rows / 2;
+        float *sh_gu = L.sh_buf;
+        sh_out = L.sh_buf + 2 * (size_t)inter;
+        if (L.sh_gate) {
+            sh_scale = sh_out + d;
+            hipLaunchKernelGGL(moe_shared_gate_kernel, dim3(1), dim3(256), 0, st, hidden, post_norm, eps, d, L.sh_gate,
+                               sh_scale);
+            hip_check(hipGetLastError(), "moe shared gate launch");
+        }
+        launch_gemv_fused(ctx, L.sh_gu, K2T_XS_RMSNORM, hidden, post_norm, eps, sh_gu, false, 1);
+        launch_gemv_fused(ctx, L.sh_dn, K2T_XS_SWIGLU, sh_gu, nullptr, 0.0f, sh_out, false);
+    }
     // d <= 2048: the routing runs in the gate_up launch (one launch fewer per layer);
     // larger rows keep the route kernel.
     const bool fused = d <= 2048;
@@ -232,7 +285,7 @@ void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float 
     g.gu_split = 0;
     launch_gemv_grouped(ctx, &b->dn, g, K2T_XS_SWIGLU, ws.gu, nullptr, 0.0f, ws.eo);
     hipLaunchKernelGGL(moe_combine_kernel, dim3((d + 255) / 256), dim3(256), 0, st, hidden, ws.eo, ws.wts, L.top_k,
-                       d, fused ? ws.ctr : nullptr);
+                       d, fused ? ws.ctr : nullptr, sh_out, sh_scale);
     hip_check(hipGetLastError(), "moe combine launch");
 }
 

@@ -101,6 +101,7 @@ SIGNATURES = {
     "k2t_moe_ffn": (I32, [VP, VP, I32, VP, VP, I32, I32, I32, VP, VP, C.c_float, VP, VP]),
     "k2t_model_set_qk_norm": (I32, [VP, I32, VP, VP]),
     "k2t_model_set_moe": (I32, [VP, I32, VP, I32, VP, VP, I32, I32, I32]),
+    "k2t_model_set_moe_shared": (I32, [VP, I32, VP, VP, VP]),
     "k2t_model_kv_synthetic": (I32, [VP, I32, C.c_uint64]),
     "k2t_model_set_kv_window": (I32, [VP, I32, I32]),
     "k2t_model_kv_window": (I32, [VP, C.POINTER(I32), C.POINTER(I32)]),
@@ -467,6 +468,17 @@ class Model:
                                       None if rb is None else rb.ctypes.data_as(VP), top_k,
                                       int(bool(norm_topk_prob)), scoring))
         self._keep.append(bank)
+
+    def set_moe_shared(self, layer, gate_up, down, gate_weight=None):
+        """k2t_model_set_moe_shared: the layer's shared expert (NF gate_up in [gate; up]
+        row order, NF down, optional sigmoid gate row); gate_up None removes it."""
+        import numpy as np
+        gw = None if gate_weight is None else np.ascontiguousarray(gate_weight, np.float32)
+        check(lib().k2t_model_set_moe_shared(self.h, layer, None if gate_up is None else gate_up.h,
+                                             None if down is None else down.h,
+                                             None if gw is None else gw.ctypes.data_as(VP)))
+        if gate_up is not None:
+            self._keep += [gate_up, down]
 
     def set_kv_window(self, window, sink_tokens=4):
         """k2t_model_set_kv_window (set_kv_sliding_window); window 0 restores the full cache."""

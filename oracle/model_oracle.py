@@ -304,11 +304,35 @@ def rms_norm(x, w, eps):
     return ((np.asarray(x, np.float32) * np.float32(O.inv_rms(x, eps))) * np.asarray(w, np.float32)).astype(np.float32)
 
 
+def shared_expert(xn, aq, as_, sh):
+    """SharedMoeExpert::forward_single, NF backend (sparse_moe.rs:252-312): gate_up GEMV on
+    the layer's int8 activation, rows [gate; up]; SwiGLU; fwht64_signed_inplace over the
+    whole inter vector then populate (= populate_fwht); down GEMV; times the gate scale
+    1 / (1 + exp(-gate . x_norm)) (241-250; dot_f32_moe, sequential on x86) when it
+    differs from 1 by more than f32::EPSILON.  sh: dict(gate_up, down: Matrix-like NF dicts
+    with pair/tail/cb/bits/sgc/rows/cols, gate_weight [d] or None)."""
+    gu, dn = sh["gate_up"], sh["down"]
+    g = O.nf_gemv(gu["pair"], gu["tail"], gu["rows"], gu["cols"], gu["bits"], gu["sgc"], gu["cb"], aq, as_)
+    inter = gu["rows"] // 2
+    sw = O.swiglu(g[:inter], g[inter:])
+    mq, ms, _ = O.populate_fwht(sw)
+    out = O.nf_gemv(dn["pair"], dn["tail"], dn["rows"], dn["cols"], dn["bits"], dn["sgc"], dn["cb"], mq, ms)
+    gw = sh.get("gate_weight")
+    if gw is not None:
+        z = np.float32(0.0)
+        for a, b in zip(np.asarray(gw, np.float32), np.asarray(xn, np.float32)):
+            z = np.float32(z + np.float32(a * b))
+        scale = np.float32(1.0) / (np.float32(1.0) + np.exp(-z, dtype=np.float32))
+        if abs(float(scale) - 1.0) > float(np.finfo(np.float32).eps):
+            out = (out * scale).astype(np.float32)
+    return out
+
+
 def moe_ffn(hidden, post_norm, eps, moe):
     """forward_layer_single (sparse_moe.rs:961-1084) + the residual add (real_llm.rs:6711-6714).
     moe: dict(router_w [E][d] f32, router_b [E] or None, top_k, norm_topk_prob, scoring,
-    experts: list of (gu Matrix-like dict, dn dict) with pair/cb/bits/sgc/rows/cols).
-    Returns (new hidden, routes)."""
+    experts: list of (gu Matrix-like dict, dn dict) with pair/cb/bits/sgc/rows/cols;
+    optional shared: see shared_expert).  Returns (new hidden, routes)."""
     xn = rms_norm(hidden, post_norm, eps)
     W = np.asarray(moe["router_w"], np.float32)
     logits = np.array([np.dot(W[e].astype(np.float64), xn.astype(np.float64)) for e in range(W.shape[0])],
@@ -318,6 +342,9 @@ def moe_ffn(hidden, post_norm, eps, moe):
     routes = route_sorted(logits, moe["top_k"], moe["norm_topk_prob"], moe["scoring"])
     aq, as_, _ = O.populate_fwht(xn)
     out = np.zeros(hidden.size, np.float32)
+    sh = moe.get("shared")
+    if sh is not None:
+        out = shared_expert(xn, aq, as_, sh)
     for e, w in routes:
         gu, dn = moe["experts"][e]
         g = O.nf_gemv(gu["pair"], np.zeros(0, np.uint8), gu["rows"], gu["cols"], gu["bits"], gu["sgc"], gu["cb"],

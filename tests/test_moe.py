@@ -89,3 +89,33 @@ def test_route_sorted_ties_pick_lower_ids():
     assert abs(r[0][1] - 0.5) < 1e-7 and abs(r[1][1] - 0.5) < 1e-7
     r = route_sorted(z, 4, False, TOPK_SOFTMAX)
     assert [e for e, _ in r] == [1, 2, 3, 4]
+
+
+@pytest.mark.parametrize("gated", [False, True])
+def test_oracle_shared_expert_against_float_math(gated):
+    """The oracle's shared expert (SharedMoeExpert::forward_single, NF backend) against the
+    same computation in float64 on the dequantized weights (gate rows first, then up;
+    SwiGLU; down; sigmoid gate scale): the int8 activations leave cosine > 0.999.  A
+    swapped gate / up split or a missing scale fails this."""
+    import oracle as O
+    from model_oracle import quantize_matrix, shared_expert
+    rng = np.random.default_rng(31 + gated)
+    d, inter = 256, 192
+    Wgu = (rng.standard_normal((2 * inter, d)) * 0.05).astype(np.float32)
+    Wdn = (rng.standard_normal((d, inter)) * 0.05).astype(np.float32)
+    gu, dn = quantize_matrix(Wgu, "nf4"), quantize_matrix(Wdn, "nf4")
+    xn = rng.standard_normal(d).astype(np.float32)
+    gate = (0.2 * rng.standard_normal(d)).astype(np.float32) if gated else None
+    as_dict = lambda m: dict(pair=m.pair, tail=m.tail, cb=m.cb, bits=4, sgc=m.sgc, rows=m.rows, cols=m.cols)  # noqa
+    aq, as_, _ = O.populate_fwht(xn)
+    got = shared_expert(xn, aq, as_, dict(gate_up=as_dict(gu), down=as_dict(dn), gate_weight=gate))
+    # float64 on the rotated-domain weights: W x = (W H^T)(H x) with H the signed FWHT
+    deq = lambda m: np.stack([O.ifwht64(m.row_rotated(r)) for r in range(m.rows)]).astype(np.float64)  # noqa
+    g = deq(gu) @ xn.astype(np.float64)
+    sw = g[:inter] / (1 + np.exp(-g[:inter])) * g[inter:]
+    want = deq(dn) @ sw
+    if gated:
+        want = want / (1 + np.exp(-float(np.dot(gate.astype(np.float64), xn))))
+    cos = float(np.dot(got, want) / (np.linalg.norm(got) * np.linalg.norm(want)))
+    assert cos > 0.999, cos
+    assert abs(np.linalg.norm(got) / np.linalg.norm(want) - 1) < 0.02
