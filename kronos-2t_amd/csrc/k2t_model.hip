@@ -675,6 +675,14 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
 constexpr int kGqaSpan = K2T_GQA_SPAN;  // 64 or 128
 constexpr int kGqaThreads = 512;
 constexpr int kGqaMaxGroup = 8;
+// q heads per span workgroup (8, or 4 in a measurement build): a group of more q heads
+// than this is split over ceil(G / heads) span workgroups of each span, which read the
+// same K / V tile.  Splitting config 5's 8 heads over two workgroups of 4 measured slower
+// (417.5 -> 391.7 tok/s: twice the span workgroups and tile reads for half the work each).
+#ifndef K2T_GQA_HEADS
+#define K2T_GQA_HEADS 8
+#endif
+constexpr int kGqaHeads = K2T_GQA_HEADS;
 
 #ifdef K2T_GQA_TRACE
 // Measurement builds only: wall-clock stamps of layer 0's workgroups, 8 per (KV head, row).
@@ -700,6 +708,7 @@ struct GqaArgs {
     KvRing kr;
     float attn_scale;
     int nspan;
+    int hsplit;  // span workgroups per span (each scores SH of the group's q heads)
     AttnPost post;
     unsigned long long *words;  // [token][q head][nspan][2 + hd] {payload, epoch} span words
     unsigned int *cnt;          // {epoch of the last launch, merge workgroups done}
@@ -711,11 +720,13 @@ struct GqaArgs {
     int32_t *asum;
 };
 
-template <int HD>
+// SH: q heads per span workgroup (the group's G heads are split over ceil(G / SH) span
+// workgroups of each span, which read the same K / V tile).
+template <int HD, int SH>
 __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
-    constexpr int P = kGqaSpan, NTH = kGqaThreads, GM = kGqaMaxGroup;
+    constexpr int P = kGqaSpan, NTH = kGqaThreads, GM = SH;
     constexpr int PW = P / 64, HW = NTH / 64 / PW;  // waves per 64 positions, heads per pass
-    static_assert(P % 64 == 0 && GM % HW == 0, "span shape");
+    static_assert(P % 64 == 0 && GM % HW == 0 && GM <= kGqaMaxGroup, "span shape");
     // K and V tiles [position][hd] (the first half); after the o sums the whole array holds
     // the position subsets' partial sums
     constexpr int kTiles = 2 * P * 128 > NTH * 4 * GM * 4 ? 2 * P * 128 : NTH * 4 * GM * 4;
@@ -890,9 +901,11 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
         return;
     }
     // ---------------------------------------------------------------- span workgroup
-    const int span = (int)blockIdx.y - G;
+    // (span, head part hs): q heads h0 .. h0 + GL - 1 of the group
+    const int span = ((int)blockIdx.y - G) / A.hsplit, hs = ((int)blockIdx.y - G) % A.hsplit;
+    const int h0 = hs * GM, GL = min(GM, G - h0);
     const int t0 = span * P, t1 = min(seq, t0 + P), n = t1 - t0;
-    if (n <= 0) return;  // spans past the context take no part
+    if (n <= 0 || GL <= 0) return;  // spans past the context take no part
     const KvRing kr = A.kr;
     const size_t base = ((size_t)layer * nkv + kvh) * kr.cap;
     int8_t *kt = tiles, *vt = tiles + P * 128;
@@ -921,8 +934,8 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
     const AttnPost &post = A.post;
     const int cur = seq - 1;
     const bool covers = post.on && t0 <= cur && cur < t1;
-    if ((int)wv < G) {
-        const int h = (int)wv, head = kvh * G + h;
+    if ((int)wv < GL) {
+        const int h = (int)wv, head = kvh * G + h0 + h;
         const float *qh = A.q + (size_t)tok * A.q_stride + (size_t)head * hd;
         float qv0, qv1;
         if (post.on) {
@@ -954,7 +967,10 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
         const float r0 = fwht_lane(a0, 0, lane);
         const float r1 = nb > 1 ? fwht_lane(a1, 1, lane) : 0.0f;
         kv_store_head(r0, r1, nb, lane, 8, hd, 0, wv == 0 ? kcur : vcur, cur_s + wv);
-        kv_store_head(r0, r1, nb, lane, 8, hd, base + (size_t)cur, wv == 0 ? A.kq : A.vq, wv == 0 ? A.ks : A.vs);
+        // (every head part builds the row for its own tile; the first stores it in the cache)
+        if (hs == 0)
+            kv_store_head(r0, r1, nb, lane, 8, hd, base + (size_t)cur, wv == 0 ? A.kq : A.vq,
+                          wv == 0 ? A.ks : A.vs);
     }
     GQA_TR(2);
     wait_vmcnt<0>();  // this wave's tile copies have landed
@@ -988,7 +1004,7 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
         for (int k = 0; k < KH; k++) {
             const int h = (int)(wv / PW) + HW * k;
             s2[k] = -INFINITY;
-            if (h < G) {
+            if (h < GL) {
                 const uint4 *qr = reinterpret_cast<const uint4 *>(qi + h * 128);
                 int dot = 0;
 #pragma unroll
@@ -1011,7 +1027,7 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
 #pragma unroll
     for (int k = 0; k < KH; k++) {
         const int h = (int)(wv / PW) + HW * k;
-        if (h < G) {
+        if (h < GL) {
             float m = red_m[h][0];
             for (int u = 1; u < PW; u++) m = fmaxf(m, red_m[h][u]);
             const float e = valid ? expf(s2[k] - m) : 0.0f;
@@ -1021,7 +1037,7 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
         }
     }
     for (int i = (int)tid; i < P * GM; i += NTH)
-        if ((i & (GM - 1)) >= G) sc[i] = 0.0f;  // heads past G
+        if ((i & (GM - 1)) >= GL) sc[i] = 0.0f;  // heads past this part
     __syncthreads();
     GQA_TR(4);
     // 4. o partials: thread (position subset sub, 4-column group cg) converts each V
@@ -1035,11 +1051,21 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
         const int ta = sub * plen, tb = min(n, ta + plen);
         for (int t = ta; t < tb; t++) {
             const int v = *reinterpret_cast<const int *>(vt + t * hd + cg * 4);
+            float w[GM];
             const float4 w0 = *reinterpret_cast<const float4 *>(sc + t * GM);
-            const float4 w1 = *reinterpret_cast<const float4 *>(sc + t * GM + 4);
+            w[0] = w0.x;
+            w[1] = w0.y;
+            w[2] = w0.z;
+            w[3] = w0.w;
+            if constexpr (GM > 4) {
+                const float4 w1 = *reinterpret_cast<const float4 *>(sc + t * GM + 4);
+                w[4] = w1.x;
+                w[5] = w1.y;
+                w[6] = w1.z;
+                w[7] = w1.w;
+            }
             const float x0 = (float)(int8_t)(v & 0xFF), x1 = (float)(int8_t)((v >> 8) & 0xFF);
             const float x2 = (float)(int8_t)((v >> 16) & 0xFF), x3 = (float)(int8_t)((v >> 24) & 0xFF);
-            const float w[GM] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
             for (int h = 0; h < GM; h++) {
                 acc[h][0] = fmaf(w[h], x0, acc[h][0]);
@@ -1053,17 +1079,18 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
     float *opart = reinterpret_cast<float *>(tiles);
 #pragma unroll
     for (int h = 0; h < GM; h++)
-        if (h < G)
-            *reinterpret_cast<float4 *>(opart + ((size_t)sub * G + h) * hd + cg * 4) =
+        if (h < GL)
+            *reinterpret_cast<float4 *>(opart + ((size_t)sub * GL + h) * hd + cg * 4) =
                 make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
     __syncthreads();
     // 5. publish {m, L, o[hd]} per head as {payload, epoch} words (one agent-scope store
     //    each: the value and its ready mark arrive together, no fence or counter)
-    unsigned long long *pbase = A.words + (size_t)(tok * nq + kvh * G) * pstride + (size_t)span * (2 + hd);
-    for (int i = (int)tid; i < G * hd; i += NTH) {
+    unsigned long long *pbase =
+        A.words + (size_t)(tok * nq + kvh * G + h0) * pstride + (size_t)span * (2 + hd);
+    for (int i = (int)tid; i < GL * hd; i += NTH) {
         const int h = i / hd, c = i % hd;
         float o = opart[h * hd + c];
-        for (int u = 1; u < nsub; u++) o += opart[((size_t)u * G + h) * hd + c];
+        for (int u = 1; u < nsub; u++) o += opart[((size_t)u * GL + h) * hd + c];
         unsigned long long *pp = pbase + (size_t)h * pstride;
         ll_word_store(pp + 2 + c, __float_as_uint(o), ep);
         if (c == 0) {
@@ -1117,13 +1144,15 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
     const int group = nq / nkv;
     if (gqa.words && ntok == 1 && group >= 2 && group <= kGqaMaxGroup && kr.bits == 8 && kr.window == 0 &&
         (hd == 64 || hd == 128)) {
+        const int hsplit = (group + kGqaHeads - 1) / kGqaHeads;
         GqaArgs A{q,          q_stride,          kq,   vq,         ks,       vs,       pos_dev, layer,
-                  nq,         nkv,               kr,   attn_scale, gqa_spans(kr.cap), post, gqa.words,
+                  nq,         nkv,               kr,   attn_scale, gqa_spans(kr.cap), hsplit, post, gqa.words,
                   gqa.cnt,    gqa.err,           1u << 20, out_f, aq, as, asum};
+        const dim3 grid(nkv, group + A.nspan * hsplit, ntok);
         if (hd == 128)
-            hipLaunchKernelGGL(attn_gqa_kernel<128>, dim3(nkv, group + A.nspan, ntok), dim3(kGqaThreads), 0, st, A);
+            hipLaunchKernelGGL((attn_gqa_kernel<128, kGqaHeads>), grid, dim3(kGqaThreads), 0, st, A);
         else
-            hipLaunchKernelGGL(attn_gqa_kernel<64>, dim3(nkv, group + A.nspan, ntok), dim3(kGqaThreads), 0, st, A);
+            hipLaunchKernelGGL((attn_gqa_kernel<64, kGqaHeads>), grid, dim3(kGqaThreads), 0, st, A);
         hip_check(hipGetLastError(), "attn_gqa launch");
         return;
     }
