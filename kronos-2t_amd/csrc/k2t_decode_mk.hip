@@ -305,6 +305,96 @@ __device__ void build_norm_act(const MkParams &P, const Lds &S, const float *w, 
     lds_barrier();
 }
 
+// The hidden-vector hand-off and the RMSNorm + FWHT + int8 build of the fast variant, with
+// two workgroup barriers instead of four: thread t polls words t, t + NTH, ... (each
+// load instruction of a wave reads 512 consecutive bytes), stores them to S.hbuf and adds
+// their squares in that order; a butterfly per wave; the waves' sums in wave order after
+// one barrier, which also carries the timeout flag (S.flag[1] set to the phase's epoch,
+// which no earlier phase had).  The slices (rotate_quant4, four elements per lane) then
+// read S.hbuf, and a second barrier ends the build.
+template <int NTH>
+__device__ __forceinline__ bool load_norm_act(const MkParams &P, const Lds &S, const unsigned long long *src,
+                                              uint32_t epoch, const float *w, const NormPre &wp, uint32_t lane,
+                                              int wave) {
+    constexpr int NW = NTH / 64;
+    const int d = P.d, nc = d / 64, t = (int)threadIdx.x;
+    bool ok = true;
+    float ss = 0.0f;
+    for (int i0 = t; i0 < d; i0 += NTH * kPoll) {
+        unsigned long long wd[kPoll];
+#pragma unroll
+        for (int k = 0; k < kPoll; k++) {
+            const int i = i0 + k * NTH;
+            wd[k] = i < d ? ll_load(src + i) : 0ull;
+        }
+        uint32_t pending = 0;
+#pragma unroll
+        for (int k = 0; k < kPoll; k++)
+            if (i0 + k * NTH < d && (uint32_t)(wd[k] >> 32) != epoch) pending |= 1u << k;
+        for (uint32_t spins = 0; pending != 0 && ok; spins++) {
+            if ((spins & 31u) == 31u) {
+                if (__hip_atomic_load(P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                    ok = false;
+                    break;
+                }
+                if (spins > P.spin_limit) {
+                    __hip_atomic_store(P.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+#pragma unroll
+            for (int k = 0; k < kPoll; k++)
+                if (pending & (1u << k)) wd[k] = ll_load(src + i0 + k * NTH);
+#pragma unroll
+            for (int k = 0; k < kPoll; k++)
+                if ((pending & (1u << k)) && (uint32_t)(wd[k] >> 32) == epoch) pending &= ~(1u << k);
+        }
+#pragma unroll
+        for (int k = 0; k < kPoll; k++) {
+            const int i = i0 + k * NTH;
+            if (i < d) {
+                const float v = __uint_as_float((uint32_t)wd[k]);
+                S.hbuf[i] = v;
+                ss = fmaf(v, v, ss);
+            }
+        }
+    }
+    ss = wave_sum_f(ss);
+    if (lane == 0) S.vec[wave] = ss;
+    if (!ok) S.flag[1] = (int)epoch;
+    lds_barrier();
+    if (S.flag[1] == (int)epoch) return false;
+    float tot = S.vec[0];
+#pragma unroll
+    for (int w2 = 1; w2 < NW; w2++) tot += S.vec[w2];
+    const float inv_rms = 1.0f / sqrtf(tot / (float)d + P.eps);
+    const uint32_t s4 = lane & 15u;
+    auto slice = [&](int c0, const float4 &wa, uint64_t sign) {
+        const int c = c0 + (int)(lane >> 4);
+        const bool act = c < nc;
+        const int cc = act ? c : 0;
+        const float4 x = *reinterpret_cast<const float4 *>(S.hbuf + cc * 64 + s4 * 4);
+        float v[4] = {(x.x * inv_rms) * wa.x, (x.y * inv_rms) * wa.y, (x.z * inv_rms) * wa.z, (x.w * inv_rms) * wa.w};
+        const Chunk4 r = rotate_quant4(v, sign, s4);
+        if (act) {
+            *reinterpret_cast<uint32_t *>(S.xl + cc * 64 + s4 * 4) = r.w;
+            if (s4 == 0) {
+                S.xsl[cc] = r.scale;
+                S.xsuml[cc] = r.sum;
+            }
+        }
+    };
+    if (wave * 4 < nc) slice(wave * 4, wp.a, wp.sign);
+    for (int c0 = wave * 4 + NW * 4; c0 < nc; c0 += NW * 4) {
+        const int c = c0 + (int)(lane >> 4), cc = c < nc ? c : 0;
+        slice(c0, *reinterpret_cast<const float4 *>(w + cc * 64 + s4 * 4), P.signs[cc]);
+    }
+    lds_barrier();
+    return true;
+}
+
 // Phase kinds of the step's schedule: per layer kQkv, kAttn, kO, kGu, kDown; then kHead.
 enum PhaseKind { kQkv = 0, kAttn = 1, kO = 2, kGu = 3, kDown = 4, kHead = 5 };
 
@@ -321,9 +411,9 @@ __device__ __forceinline__ bool mk_load_input(const MkParams &P, const Lds &S, c
                                                    : P.GACT + my_copy(P) * gact_words(P);
         return load_words<NTH>(P, S, src, nch * kActWords, epoch, true, nullptr, t0);
     }
-    if (!load_words<NTH>(P, S, (kind == kGu ? P.HB : P.HA) + my_copy(P) * (size_t)P.d, P.d, epoch, false, S.hbuf,
-                         t0))
-        return false;
+    const unsigned long long *hsrc = (kind == kGu ? P.HB : P.HA) + my_copy(P) * (size_t)P.d;
+    if (!EX) return load_norm_act<NTH>(P, S, hsrc, epoch, norm_w, wp, lane, wave);
+    if (!load_words<NTH>(P, S, hsrc, P.d, epoch, false, S.hbuf, t0)) return false;
 #ifdef K2T_MK_TRACE_IN
     if (P.trace && threadIdx.x == 0 && trace_l >= 0)
         P.trace[(((size_t)blockIdx.x * (P.L + 1) + trace_l) * 6 + kind) * 6 + 2] = wall_clock64();
@@ -943,6 +1033,7 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
     const uint32_t nph = 2u + 5u * (uint32_t)P.L;
     auto E = [&](int ph) { return step * nph + (uint32_t)ph + 1u; };
     const int d = P.d;
+    if (t == 0) S.flag[1] = 0;  // (load_norm_act's timeout flag: no phase has epoch 0)
     // The layer table is read-only for the launch: scalar loads through the constant
     // address space (the four matrix views of a layer are consecutive).
     using CMkLayer = const __attribute__((address_space(4))) MkLayer;
@@ -1106,6 +1197,9 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                 }
             }
             lds_barrier();
+#ifdef K2T_MK_TRACE_GU
+            if (kind == kGu && first) MK_TR(l, 5, 4);
+#endif
             if (kind == kGu) {
                 if (wave == 0) {
                     const int ic = base / 4;
@@ -1119,6 +1213,9 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                     float v[4] = {va.x, va.y, va.z, va.w};
                     const Chunk4 r = rotate_quant4(v, sign_mask_s(P, ic), s4);
                     store_act_chunk4(r, lane, P.GACT + (size_t)ic * kActWords, E(ph), P.rep, gact_words(P));
+#ifdef K2T_MK_TRACE_GU
+                    if (first) MK_TR(l, 5, 5);
+#endif
                 }
                 lds_barrier();
             }

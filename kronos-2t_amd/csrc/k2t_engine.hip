@@ -490,7 +490,11 @@ void upload_mk_layers(k2t_model *m) {
     std::vector<MkLayer> h(m->layers.size());
     for (size_t l = 0; l < m->layers.size(); l++) {
         const auto &L = m->layers[l];
+#ifdef K2T_MK_O_NSEG
+        h[l].o = mat_dev(L.o, false, 0, nw, K2T_MK_O_NSEG);
+#else
         h[l].o = mat_dev(L.o, false, 0, nw);
+#endif
         h[l].gu = mat_dev(L.gu, true, 0, nw);
         h[l].down = mat_dev(L.down, false, 0, nw);
         // qkv follows down: fewer, longer qkv tasks where that lets the two phases use
