@@ -187,11 +187,10 @@ __device__ __forceinline__ bool load_words(const MkParams &P, const Lds &S, cons
             }
         }
     }
-    if (threadIdx.x == 0) S.flag[0] = 0;
+    // one barrier: S.flag[1] is set to this phase's epoch on failure (no earlier phase had it)
+    if (!ok) S.flag[1] = (int)epoch;
     lds_barrier();
-    if (!ok) S.flag[0] = 1;
-    lds_barrier();
-    return S.flag[0] == 0;
+    return S.flag[1] != (int)epoch;
 }
 
 // Hadamard sign mask of 64-block `block` (wave-uniform) by a scalar load: the table is
@@ -579,12 +578,10 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
         if (bias) f = f + bias[row];
         qf[e] = f;  // qf, kf, vf are contiguous
     }
-    if (t == 0) S.flag[0] = 0;
-    lds_barrier();
-    if (!ok) S.flag[0] = 1;
+    if (!ok) S.flag[1] = (int)ep_in;
     lds_barrier();
     ATR(1);
-    if (S.flag[0]) return false;
+    if (S.flag[1] == (int)ep_in) return false;
     // 2. RoPE (real_llm.rs:9328-9361) on q and k, int8 Hadamard q / k / v
     const size_t slot = base + pos;
     // waves 0, 1, 2 handle q, k, v concurrently
@@ -801,11 +798,9 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
             qf[t] = o * (1.0f / Lt);  // reuse qf for o
         }
     }
-    if (t == 0) S.flag[0] = 0;
+    if (!merged) S.flag[1] = (int)ep_out;
     lds_barrier();
-    if (!merged) S.flag[0] = 1;
-    lds_barrier();
-    if (S.flag[0]) return false;
+    if (S.flag[1] == (int)ep_out) return false;
     if (sp > 0) return true;  // (the scratch reads are done: the barriers above)
     ATR2(2);
     // 5. ifwht64 per block, then FWHT with the o_proj chunk index + int8 (real_llm.rs:7060-7084)
@@ -1033,7 +1028,7 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
     const uint32_t nph = 2u + 5u * (uint32_t)P.L;
     auto E = [&](int ph) { return step * nph + (uint32_t)ph + 1u; };
     const int d = P.d;
-    if (t == 0) S.flag[1] = 0;  // (load_norm_act's timeout flag: no phase has epoch 0)
+    if (t == 0) S.flag[1] = 0;  // (the waits' timeout flag holds a phase epoch; none is 0)
     // The layer table is read-only for the launch: scalar loads through the constant
     // address space (the four matrix views of a layer are consecutive).
     using CMkLayer = const __attribute__((address_space(4))) MkLayer;
@@ -1189,11 +1184,17 @@ __global__ __launch_bounds__(NTH) void decode_mk_kernel(MkParams P) {
                 } else if (kind == kGu) {
                     S.vec[t] = acc;  // the 4 groups = the 4 pairs of block ic
                 } else {
+#ifdef K2T_MK_TRACE_O
+                    if (t == 0 && first) MK_TR(l, 5, kind == kO ? 2 : 4);
+#endif
                     uint32_t hv = (uint32_t)rpre;
                     if ((uint32_t)(rpre >> 32) != er && ok && !ll_wait(P, res + row, er, hv)) ok = false;
                     const uint32_t nv = __float_as_uint(__uint_as_float(hv) + acc);
                     for (int r = 0; r < P.rep; r++)
                         ll_store((kind == kO ? P.HB : P.HA) + (size_t)r * d + row, nv, E(ph));
+#ifdef K2T_MK_TRACE_O
+                    if (t == 0 && first) MK_TR(l, 5, kind == kO ? 3 : 5);
+#endif
                 }
             }
             lds_barrier();
