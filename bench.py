@@ -114,6 +114,13 @@ def _busy_wait(torch, stream, seconds):
         pass
 
 
+# Launches averaged per GEMV case (and per ceiling probe), whatever --steps says: each
+# timed batch carries a one-off start cost of about 13 us (measured: nf4 4096x14336 b1
+# averages 10.1 us over 20 launches, 9.45 us over 128), which must not be spread over
+# few launches.
+GEMV_LAUNCHES = 200
+
+
 def time_case(ctx, torch, case, steps, warmup):
     """Mean device time per GEMV: `steps` back-to-back launches between two events on
     the kernels' stream, enqueued behind a spin so the host never starves the queue."""
@@ -304,7 +311,7 @@ def copy_probe(torch, mib):
     torch.cuda.synchronize()
 
 
-def read_ceiling(ctx, torch, nbytes, steps=60):
+def read_ceiling(ctx, torch, nbytes, steps=GEMV_LAUNCHES):
     """Practical single-launch HBM read rate at this byte count: k2t_stream_read_probe over
     nbytes, rotated over enough buffers to miss the 256 MB Infinity Cache, timed back to
     back like the GEMV cases.  Returns (GB/s, us)."""
@@ -328,7 +335,7 @@ def read_ceiling(ctx, torch, nbytes, steps=60):
     return nb / t / 1e9, t * 1e6
 
 
-def copy_ceiling(torch, nbytes, steps=60):
+def copy_ceiling(torch, nbytes, steps=GEMV_LAUNCHES):
     """Practical HBM rate of one launch moving this many bytes: device-to-device copies of
     nbytes/2 read + nbytes/2 written, rotated over enough buffers to miss the 256 MB
     Infinity Cache, timed back to back like the GEMV cases.  Returns (GB/s, us)."""
@@ -468,7 +475,7 @@ def main():
             continue
         for ntok in (1, 4):
             case = GemvCase(ctx, torch, name, fmt, r, c, ntok=ntok)
-            mean_s = time_case(ctx, torch, case, max(args.steps, 20), args.warmup)
+            mean_s = time_case(ctx, torch, case, max(args.steps, GEMV_LAUNCHES), args.warmup)
             gbs = case.bytes / mean_s / 1e9
             key = f"{name}_b{ntok}"
             results[key] = {"us": round(mean_s * 1e6, 3), "GB_s": round(gbs, 1),
