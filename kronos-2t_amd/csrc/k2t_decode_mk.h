@@ -14,8 +14,11 @@ namespace k2t {
 // level at 1029-1093 positions (972 against 964 tok/s) and the persistent kernel
 // behind beyond (724 against 944 tok/s at 2053-2117, 391 against 880 at 4101-4165).
 constexpr int kMkMaxContext = 1024;
-// Copies of the broadcast hand-off vectors (one per XCD of MI355X).
-constexpr int kMkRep = 8;
+// Copies of the broadcast hand-off vectors: one per pair of MI355X's 8 XCDs (a workgroup
+// reads copy blockIdx.x mod 4).  8 copies (one per XCD) measured 1440 against 1447 tok/s
+// on the 1.7B nf4g128 decode, 1545 against 1555 on the 135M p55454 one (the writers'
+// epilogues store half as many words); 2 copies 1432 / 1547.
+constexpr int kMkRep = 4;
 // Most spans the attention phase cuts one q head's context into, and the fewest
 // positions per span.
 constexpr int kMkSpans = 4;

@@ -740,7 +740,7 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             m->err_dev = (int *)m->step_dev + 1;
             const uint32_t one[4] = {1u, 0u, 0u, 0u};
             hip_check(hipMemcpy(m->step_dev, one, sizeof(one), hipMemcpyHostToDevice), "step init");
-            // HA, HB, OACT and GACT in kMkRep copies (one per XCD), QKV and BEST once
+            // HA, HB, OACT and GACT in kMkRep copies, QKV and BEST once
             const size_t oact = (size_t)(c.n_heads * c.head_dim / 64) * 18, gact = (size_t)(c.intermediate / 64) * 18;
             const size_t apart = (size_t)c.n_heads * kMkSpans * (2 + c.head_dim);
             const size_t words =

@@ -285,6 +285,24 @@ struct Frag {
 // codebook stripes (384-byte stripe-chunks of 48-byte triplet blocks; lane bit 0 then
 // picks the 32-column half of the chunk instead of an 8-column half of each block).
 
+#ifdef K2T_GEMV_TRACE
+// Measurement builds only: wall-clock stamps of the staged batch-1 GEMV (XS 5), 8 per
+// (workgroup < 512, wave < 16).
+__device__ unsigned long long g_gemv_trace[512 * 16 * 8];
+#define GV_TR(k)                                                                                              \
+    do {                                                                                                      \
+        if (XS == 5 && lane == 0 && blockIdx.x < 512 && wave < 16)                                            \
+            g_gemv_trace[((size_t)blockIdx.x * 16 + wave) * 8 + (k)] = wall_clock64();                        \
+    } while (0)
+extern "C" int k2t_gemv_trace_read(unsigned long long *dst) {
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_gemv_trace), sizeof(g_gemv_trace)) == hipSuccess ? 0 : -1;
+}
+#else
+#define GV_TR(k) \
+    do {         \
+    } while (0)
+#endif
+
 template <int FMT, int HP, int NT, bool DOTS, int XS>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     constexpr int NH = HP == 0 ? 1 : (HP == 1 ? 2 : 4);
@@ -297,6 +315,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
     constexpr bool kCanRoute = XS == 1 && NT == 1 && !DOTS;
     const bool fused_route = kCanRoute && P.rt_w != nullptr;
     int slot = (int)blockIdx.z;
+    GV_TR(0);
     uint32_t rt_epoch = 0;
     if constexpr (kCanRoute) {
         if (fused_route) {
@@ -630,12 +649,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             if (iters > 0) {
                 fetchc(fa, 0);
                 fetchc(fb, 1);
+                GV_TR(1);
                 // The activation copies were issued before these two fetches: once at most
                 // their loads are outstanding, the activation is in LDS.  (The compiler does
                 // not know the copies write LDS and could move the activation reads up to
                 // its own, later, wait for fa.)
                 constexpr int kFetchLoads = (kNF3 ? 3 : 4) + (FMT == 0 ? (HP == 0 ? 0 : HP == 1 ? 2 : 4) : 0) + 1;
                 wait_vmcnt<2 * kFetchLoads>();
+                GV_TR(2);
                 int i = 0;
                 for (; i + 2 < iters; i += 2) {
                     if (valid(i)) process(fa, chunk_of(i));
@@ -643,8 +664,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
                     if (valid(i + 1)) process(fb, chunk_of(i + 1));
                     fetchc(fb, i + 3);
                 }
+#ifdef K2T_GEMV_TRACE
+                wait_vmcnt<kFetchLoads>();
+                GV_TR(3);
+#endif
                 if (valid(i)) process(fa, chunk_of(i));
+                GV_TR(4);
                 if (valid(i + 1)) process(fb, chunk_of(i + 1));
+                GV_TR(5);
             }
         } else if constexpr (XS != 0) {
             // Source loads first, then the first weight loads; the wave builds its
@@ -706,6 +733,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
             }
         }
         __syncthreads();
+        GV_TR(6);
         const int nrows_blk = (is_tail && !smode) ? 16 : RB;
         const int first_stripe = smode ? rb : (is_tail ? 2 * P.np : 2 * rb);
         for (int idx = (int)threadIdx.x; idx < NT * RB; idx += (int)blockDim.x) {

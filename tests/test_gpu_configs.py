@@ -176,7 +176,7 @@ def test_config3_1_7b_persistent_matches_oracle(gpu_ctx, n_layers):
     """The 1.7B nf4g128 shape (d 2048, 32 heads, ffn 8192, vocab 49152) on the default
     persistent kernel: its phase task layout over every CU, the 49152-row head and the
     cross-workgroup greedy pick.  A 12-token prefill in 4-token weight passes, 3 decode
-    steps, then 3 device-side greedy steps in one generate() call, at 2 layers and at the
+    steps, then 12 device-side greedy steps in one generate() call, at 2 layers and at the
     full 24 (the bench model, same seeds).  Logits meet _bar; greedy tokens equal the
     oracle's argmax wherever its top-2 margin exceeds twice the largest GPU-oracle logit
     difference seen (a closer call is within rounding of a tie)."""
@@ -214,7 +214,9 @@ def test_config3_1_7b_persistent_matches_oracle(gpu_ctx, n_layers):
         tok = int(np.argmax(a))
     # the persistent kernel's own cross-workgroup greedy pick, several steps in one call:
     # each device pick against the argmax of the oracle's logits for the same input token
-    got = list(model.generate(tok, 3))
+    # (twelve device steps: at 24 layers the fast path's largest logit difference, about
+    # 0.16-0.17, leaves most steps' top-2 margins of this random model too close to call)
+    got = list(model.generate(tok, 12))
     for g in got:
         b, _ = step(tok)
         top2 = np.sort(b)[-2:]
@@ -222,7 +224,7 @@ def test_config3_1_7b_persistent_matches_oracle(gpu_ctx, n_layers):
             assert g == int(np.argmax(b)), f"device greedy token {g} vs oracle {int(np.argmax(b))}"
             checked += 1
         tok = g
-    print(f"  greedy tokens checked: {checked} of 6 (margin > {2 * md:.4f})", flush=True)
+    print(f"  greedy tokens checked: {checked} of 15 (margin > {2 * md:.4f})", flush=True)
     assert checked >= 3
     model.close()
     for m in mats:
