@@ -296,9 +296,11 @@ int32_t k2t_model_set_graph(k2t_model *m, int32_t enable);
  * in-order fmaf epilogue (k2t_ctx_set_exact), RMSNorm and q / k norm with the sequential
  * four-accumulator sum of squares (dot_f32_fast, real_llm.rs:911-926), softmax and SwiGLU
  * with glibc's expf results (k2t_expf_host), attention with sequential softmax and V sums
- * (real_llm.rs:8533-8545, 8575-8585, 9590-9600).  Logits then equal the x86 reference's
- * bit for bit on dense models with the int8 KV cache (MoE feed-forwards keep their own
- * order; the NF4 KV cache is refused with K2T_E_ARG at the step).  Exact steps run the
+ * (real_llm.rs:8533-8545, 8575-8585, 9590-9600), and sparse-MoE layers with the sequential
+ * router dot, route_sorted with glibc's expf and in-order sums (sparse_moe.rs:86-206,
+ * 1644-1656).  Logits then equal the x86 reference's bit for bit with the int8 KV cache
+ * (the NF4 KV cache is refused with K2T_E_ARG at the step).  Exact steps run the
+ * persistent kernel's exact-order variant where the persistent kernel applies, else the
  * per-operation path; they are slower and meant for parity checks. */
 int32_t k2t_model_set_exact(k2t_model *m, int32_t exact);
 /* 1 (default): a decode step runs as one persistent kernel (one workgroup per CU) whose
@@ -420,7 +422,9 @@ int32_t k2t_experts_info(const k2t_experts *b, k2t_k2tm_header *out);
  *   x_norm = RMSNorm(hidden) * post_norm; routes = route_sorted(router, x_norm);
  *   hidden += sum over routes of w * down(SwiGLU(gate_up(x_norm)))
  * router_w: device f32 [E][d_model] (bias [E] or NULL).  route ids / weights (device,
- * top_k each, nullable) receive the routing.  Uses the context's scratch. */
+ * top_k each, nullable) receive the routing.  Uses the context's scratch.  With the
+ * context in exact mode (k2t_ctx_set_exact) every step follows the x86 reference's order
+ * (sequential router dot, glibc-identical expf, in-order GEMV epilogues). */
 int32_t k2t_moe_ffn(k2t_ctx *ctx, const k2t_experts *bank, int32_t shard_layer, const float *d_router_w,
                     const float *d_router_bias, int32_t top_k, int32_t norm_topk_prob, int32_t scoring,
                     float *d_hidden, const float *d_post_norm, float eps, int32_t *d_route_ids,

@@ -43,8 +43,6 @@ void launch_kv_store(hipStream_t st, const float *heads, int n, int hd, int bits
 void launch_embed_rows(hipStream_t st, const void *rows, bool bf16, const int *tokens, int ntok, int d, float *out);
 void launch_advance_pos(hipStream_t st, int *pos, int n);
 void launch_argmax(hipStream_t st, const float *x, int n, int *out_idx);
-void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum, int ntok,
-                    float *out, size_t out_stride, bool accumulate);
 
 // Greedy pick (argmax_scalar, real_llm.rs:9914-9924): largest value, lowest index on ties,
 // NaN never wins.  One workgroup.
@@ -905,7 +903,9 @@ int32_t k2t_model_set_moe_shared(k2t_model *m, int32_t layer, const k2t_mat *gat
         const int inter = gate_up->rows / 2;
         arg(down->rows == d && down->cols == inter, "shared down must be [hidden][inter]");
         hip_check(hipSetDevice(m->ctx->device), "hipSetDevice");
-        L.moe.sh_buf = (float *)dalloc(m, ((size_t)2 * inter + d + 64) * sizeof(float));
+        // [2 * inter gate_up | d output | 64 (gate scale) | exact mode: inter int8 codes,
+        //  inter / 64 scales and sums of the down activation]
+        L.moe.sh_buf = (float *)dalloc(m, ((size_t)2 * inter + d + 64 + inter / 4 + 2 * (inter / 64) + 64) * sizeof(float));
         float *g = nullptr;
         if (gate_weight) {
             g = (float *)dalloc(m, (size_t)d * sizeof(float));

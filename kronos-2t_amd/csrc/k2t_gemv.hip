@@ -70,6 +70,9 @@ struct GemvParams {
     uint32_t mat_off, cb_off;
     size_t slot_out, slot_src;
     int gu_split;
+    // Grouped mode with a ready int8 activation (XS 0): slot_act = 1 reads activation row z
+    // (xq + z * K, xs / xsum + z * nc) for slot z, 0 the same row for every slot.
+    int slot_act;
     // Routing in the same launch (XS 1 only, rt_w != NULL): workgroups of plane z = 0 run
     // the router (route_logit_half on every wave, units x * waves + wave stepping by
     // gridDim.x * waves, into rt_words [2 rt_E + 2]; then route_collect_parts on wave 0 of
@@ -336,6 +339,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         }
     }
     const int tok0 = P.tok_base + (int)blockIdx.y * NT;
+    const int xtok0 = tok0 + (P.route && P.slot_act ? slot : 0);  // activation row of a ready activation
     const uint32_t half = lane & 1u;
     const uint32_t g = (lane >> 1) & 3u;
     // Pair mode: lane bit 3 = stripe of the pair, bits 4-5 = sub-segment (4 per wave).
@@ -471,10 +475,10 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
         for (int t = 0; t < NT; t++) {
 #pragma unroll
             for (int kk = 0; kk < 4; kk++)
-                fr.x[t][kk] = *reinterpret_cast<const uint2 *>(P.xq + (size_t)(tok0 + t) * P.K + c * 64 +
+                fr.x[t][kk] = *reinterpret_cast<const uint2 *>(P.xq + (size_t)(xtok0 + t) * P.K + c * 64 +
                                                                (kNF3 ? half * 32 + kk * 8 : kk * 16 + half * 8));
-            fr.sx[t] = P.xs[(size_t)(tok0 + t) * P.nc + c];
-            if constexpr (FMT == 0) fr.sum[t] = P.xsum[(size_t)(tok0 + t) * P.nc + c];
+            fr.sx[t] = P.xs[(size_t)(xtok0 + t) * P.nc + c];
+            if constexpr (FMT == 0) fr.sum[t] = P.xsum[(size_t)(xtok0 + t) * P.nc + c];
         }
     };
 
@@ -920,8 +924,9 @@ void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *
 }
 
 void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum, int ntok,
-                    float *out, size_t out_stride, bool accumulate) {
-    launch_gemv_impl(ctx, m, xq, xs, xsum, ntok, 0, m->stripes, out, out_stride, nullptr, accumulate);
+                    float *out, size_t out_stride, bool accumulate, int gu_split) {
+    launch_gemv_impl(ctx, m, xq, xs, xsum, ntok, 0, m->stripes, out, out_stride, nullptr, accumulate, 0, nullptr,
+                     nullptr, 0.0f, nullptr, gu_split);
 }
 
 void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float *src, const float *w, float eps,
@@ -934,8 +939,10 @@ void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, 
                          const float *w, float eps, float *out) {
     if (g.nslots <= 0) return;
     if (geom->has_tail) throw Error(K2T_E_INTERNAL, "grouped gemv: expert matrices have no tail stripe");
-    launch_gemv_impl(ctx, geom, nullptr, nullptr, nullptr, 1, 0, geom->stripes, out, (size_t)geom->rows, nullptr,
-                     false, xs_mode, src, w, eps, &g);
+    if (xs_mode == 0 && (!g.xq || !g.xs || (!g.xsum && geom->fmt != K2T_FMT_NF)))
+        throw Error(K2T_E_INTERNAL, "grouped gemv: no activation");
+    launch_gemv_impl(ctx, geom, g.xq, g.xs, g.xsum, 1, 0, geom->stripes, out, (size_t)geom->rows, nullptr, false,
+                     xs_mode, src, w, eps, &g);
 }
 
 static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
@@ -994,7 +1001,6 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
         G = 1;
     }
     if (grp) {
-        if (xsm == 0) throw Error(K2T_E_INTERNAL, "grouped gemv needs a fused activation source");
         P.route = grp->route;
         P.bank = grp->bank;
         P.bank_stride = grp->stride;
@@ -1003,6 +1009,7 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
         P.slot_out = grp->slot_out;
         P.slot_src = grp->slot_src;
         P.gu_split = grp->gu_split;
+        P.slot_act = grp->slot_act;
         int planes = grp->nslots;
         if (grp->rt_w) {  // routing in this launch: plane 0 routes, slot z is plane z + 1
             if (xsm != K2T_XS_RMSNORM || m->cols > 2048 || grp->rt_E < 1 || grp->rt_E > 256 || !grp->rt_words ||

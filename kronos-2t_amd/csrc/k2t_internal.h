@@ -113,7 +113,19 @@ struct GemvGroup {
     float *rt_wts = nullptr;
     int rt_E = 0, rt_norm = 0, rt_scoring = 0;
     uint32_t rt_spin = 0;
+    // A ready int8 activation (xs_mode 0): per slot (slot_act 1: row z of xq / xs / xsum)
+    // or shared by every slot (slot_act 0).
+    const int8_t *xq = nullptr;
+    const float *xs = nullptr;
+    const int32_t *xsum = nullptr;
+    int slot_act = 0;
 };
+// GEMV of a ready int8 activation (ntok tokens); gu_split 1 writes a [gate; up] matrix's
+// rows in [gate64, up64] blocks.
+void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum, int ntok,
+                    float *out, size_t out_stride, bool accumulate, int gu_split = 0);
+void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
+                       bool exact);
 void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, int xs_mode, const float *src,
                          const float *w, float eps, float *out);
 

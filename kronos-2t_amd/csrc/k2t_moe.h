@@ -51,6 +51,12 @@ struct MoeWork {
     int *ids;                   // [top_k]
     uint32_t *ctr;              // route-call counter (epoch source)
     int *err;                   // raised when the route wait times out
+    // exact-order mode (the context's exact flag): inv_rms, the int8 activation of x_norm
+    // and the slots' down activations
+    float *rms;
+    int8_t *aq, *mq;            // [d], [top_k][d_ff]
+    float *as, *ms;             // [d / 64], [top_k][d_ff / 64]
+    int32_t *asum, *msum;
 };
 
 // Workspace size; the words and the counter must start zeroed (model: at allocation;

@@ -21,6 +21,7 @@
 
 #include "../../include/k2t_hip.h"
 #include "k2t_device.h"
+#include "k2t_expf.h"
 #include "k2t_internal.h"
 #include "k2t_moe.h"
 #include "k2t_route.h"
@@ -193,6 +194,122 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ hi
     hidden[r] = hidden[r] + p;
 }
 
+// Exact-order routing (the x86 reference's order; one workgroup): x_norm[i] = (h[i] *
+// inv_rms) * w[i] (rms_norm, real_llm.rs:9858-9898, inv_rms in the x86 order), logit e =
+// sum_i W[e][i] * x_norm[i] added in i order (dot_f32_moe's portable sum,
+// sparse_moe.rs:1644-1656) + bias, one thread per expert; then thread 0 runs route_sorted
+// (sparse_moe.rs:86-182): softmax / sigmoid with the x86 build's exp (expf_rn) and
+// sequential sums, select_topk_by_score (strict '>' insertion, 185-206), the top-k
+// renormalization, and the insertion sort by expert id.
+__global__ __launch_bounds__(256) void moe_route_exact_kernel(const float *__restrict__ hidden,
+                                                              const float *__restrict__ post_norm,
+                                                              const float *__restrict__ inv_rms, int d,
+                                                              const float *__restrict__ W, const float *__restrict__ bias,
+                                                              int E, int k, int norm_topk, int scoring,
+                                                              int *__restrict__ ids, float *__restrict__ wts) {
+    __shared__ float xn[4096];
+    __shared__ float z[256];
+    const int tid = (int)threadIdx.x;
+    const float inv = inv_rms[0];
+    for (int i = tid; i < d; i += 256) xn[i] = (hidden[i] * inv) * post_norm[i];
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) {
+        const float *row = W + (size_t)e * d;
+        float a = 0.0f;
+        for (int i = 0; i < d; i++) a = a + row[i] * xn[i];
+        if (bias) a = a + bias[e];
+        z[e] = a;
+    }
+    __syncthreads();
+    if (tid != 0) return;
+    if (scoring == K2T_MOE_SOFTMAX) {
+        float mz = -INFINITY;
+        for (int e = 0; e < E; e++) mz = fmaxf(mz, z[e]);
+        float sum = 0.0f;
+        for (int e = 0; e < E; e++) {
+            z[e] = expf_rn(z[e] - mz);
+            sum = sum + z[e];
+        }
+        const float inv_all = sum > 0.0f ? 1.0f / sum : 1.0f / (float)E;
+        for (int e = 0; e < E; e++) z[e] = z[e] * inv_all;
+    } else if (scoring == K2T_MOE_SIGMOID) {
+        for (int e = 0; e < E; e++) z[e] = 1.0f / (1.0f + expf_rn(-z[e]));
+    }
+    int oe[K2T_MOE_MAX_TOPK];
+    float ow[K2T_MOE_MAX_TOPK];
+    int len = 0;
+    for (int e = 0; e < E; e++) {
+        const float sv = z[e];
+        if (len < k) {
+            int pos = len;
+            while (pos > 0 && sv > ow[pos - 1]) {
+                oe[pos] = oe[pos - 1];
+                ow[pos] = ow[pos - 1];
+                pos--;
+            }
+            oe[pos] = e;
+            ow[pos] = sv;
+            len++;
+        } else if (sv > ow[k - 1]) {
+            int pos = k - 1;
+            while (pos > 0 && sv > ow[pos - 1]) {
+                oe[pos] = oe[pos - 1];
+                ow[pos] = ow[pos - 1];
+                pos--;
+            }
+            oe[pos] = e;
+            ow[pos] = sv;
+        }
+    }
+    if (scoring == K2T_MOE_TOPK_SOFTMAX) {
+        float mz = -INFINITY;
+        for (int i = 0; i < k; i++) mz = fmaxf(mz, ow[i]);
+        float sum = 0.0f;
+        for (int i = 0; i < k; i++) {
+            ow[i] = expf_rn(ow[i] - mz);
+            sum = sum + ow[i];
+        }
+        const float inv_k = sum > 0.0f ? 1.0f / sum : 1.0f / (float)k;
+        for (int i = 0; i < k; i++) ow[i] = ow[i] * inv_k;
+    } else if (norm_topk) {
+        float sum = 0.0f;
+        for (int i = 0; i < k; i++) sum = sum + ow[i];
+        if (sum > 0.0f) {
+            const float inv_top = 1.0f / sum;
+            for (int i = 0; i < k; i++) ow[i] = ow[i] * inv_top;
+        }
+    }
+    for (int i = 1; i < k; i++) {
+        const int ce = oe[i];
+        const float cw = ow[i];
+        int j = i;
+        while (j > 0 && oe[j - 1] > ce) {
+            oe[j] = oe[j - 1];
+            ow[j] = ow[j - 1];
+            j--;
+        }
+        oe[j] = ce;
+        ow[j] = cw;
+    }
+    for (int i = 0; i < k; i++) {
+        ids[i] = oe[i];
+        wts[i] = ow[i];
+    }
+}
+
+// Exact-order gate scale of the shared expert: 1 / (1 + exp(-z)), z = sum_i gate[i] *
+// x_norm[i] added in i order (dot_f32_moe, sparse_moe.rs:241-250), exp = expf_rn.  One
+// thread.
+__global__ void moe_shared_gate_exact_kernel(const float *__restrict__ hidden, const float *__restrict__ post_norm,
+                                             const float *__restrict__ inv_rms, int d,
+                                             const float *__restrict__ gate, float *__restrict__ out) {
+    if (threadIdx.x != 0) return;
+    const float inv = inv_rms[0];
+    float zz = 0.0f;
+    for (int i = 0; i < d; i++) zz = zz + gate[i] * ((hidden[i] * inv) * post_norm[i]);
+    out[0] = 1.0f / (1.0f + expf_rn(-zz));
+}
+
 // Gate scale of the shared expert: 1 / (1 + exp(-dot(gate, x_norm))) with x_norm =
 // (hidden * inv_rms) * post_norm (gate_scale, sparse_moe.rs:241-250); inv_rms in the
 // fused activation builders' order (row_sumsq_wave), the dot as a fixed tree.  One
@@ -220,8 +337,77 @@ __global__ __launch_bounds__(256) void moe_shared_gate_kernel(const float *__res
     }
 }
 
+// Exact-order MoE feed-forward (the context's exact mode): every step in the x86
+// reference's order.  inv_rms with the four-accumulator sum of squares, the int8
+// activation of x_norm once (populate_fwht), routing in moe_route_exact_kernel, the
+// expert GEMVs with the in-order epilogue on that activation, SwiGLU with expf_rn, and the
+// combine in route order (moe_combine_kernel's arithmetic is already the reference's).
+static void launch_moe_ffn_exact(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float *post_norm, float eps,
+                                 const MoeWork &ws) {
+    const k2t_experts *b = L.bank;
+    const int d = (int)b->hdr.d_model, dff = (int)b->hdr.d_ff_expert, E = (int)b->hdr.experts_per_layer;
+    hipStream_t st = ctx->stream;
+    launch_inv_rms_x86(st, hidden, eps, d, 1, ws.rms);
+    launch_act_quant(ctx, hidden, post_norm, ws.rms, d, 1, ws.aq, ws.as, ws.asum);
+    float *sh_out = nullptr, *sh_scale = nullptr;
+    if (L.sh_gu) {
+        const int inter = L.sh_gu->rows / 2;
+        float *sh_gu = L.sh_buf;
+        sh_out = L.sh_buf + 2 * (size_t)inter;
+        float *tail = sh_out + d + 64;  // the shared expert's down activation
+        float *s_s = tail;
+        int32_t *s_sum = reinterpret_cast<int32_t *>(tail + inter / 64);
+        int8_t *s_q = reinterpret_cast<int8_t *>(tail + 2 * (inter / 64));
+        if (L.sh_gate) {
+            sh_scale = sh_out + d;
+            hipLaunchKernelGGL(moe_shared_gate_exact_kernel, dim3(1), dim3(64), 0, st, hidden, post_norm, ws.rms, d,
+                               L.sh_gate, sh_scale);
+            hip_check(hipGetLastError(), "moe shared gate launch");
+        }
+        launch_gemv_ex(ctx, L.sh_gu, ws.aq, ws.as, ws.asum, 1, sh_gu, (size_t)L.sh_gu->rows, false, 1);
+        launch_swiglu_act(st, sh_gu, inter, 1, s_q, s_s, s_sum, true);
+        launch_gemv_ex(ctx, L.sh_dn, s_q, s_s, s_sum, 1, sh_out, (size_t)d, false);
+    }
+    hipLaunchKernelGGL(moe_route_exact_kernel, dim3(1), dim3(256), 0, st, hidden, post_norm, ws.rms, d, L.router_w,
+                       L.router_b, E, L.top_k, L.norm_topk, L.scoring, ws.ids, ws.wts);
+    hip_check(hipGetLastError(), "moe exact route launch");
+    const uint8_t *layer_base = b->d_bytes + kK2tmPage + (size_t)L.shard_layer * E * b->lay.aligned_bytes;
+    GemvGroup g{};
+    g.route = ws.ids;
+    g.nslots = L.top_k;
+    g.bank = layer_base;
+    g.stride = b->lay.aligned_bytes;
+    g.mat_off = (uint32_t)b->lay.gu_pair_off;
+    g.cb_off = (uint32_t)b->lay.gu_cb_off;
+    g.slot_out = (size_t)2 * dff;
+    g.slot_src = 0;
+    g.gu_split = 1;
+    g.xq = ws.aq;
+    g.xs = ws.as;
+    g.xsum = ws.asum;
+    g.slot_act = 0;
+    launch_gemv_grouped(ctx, &b->gu, g, 0, nullptr, nullptr, 0.0f, ws.gu);
+    launch_swiglu_act(st, ws.gu, dff, L.top_k, ws.mq, ws.ms, ws.msum, true);
+    g.mat_off = (uint32_t)b->lay.dn_pair_off;
+    g.cb_off = (uint32_t)b->lay.dn_cb_off;
+    g.slot_out = (size_t)d;
+    g.gu_split = 0;
+    g.xq = ws.mq;
+    g.xs = ws.ms;
+    g.xsum = ws.msum;
+    g.slot_act = 1;
+    launch_gemv_grouped(ctx, &b->dn, g, 0, nullptr, nullptr, 0.0f, ws.eo);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((d + 255) / 256), dim3(256), 0, st, hidden, ws.eo, ws.wts, L.top_k,
+                       d, nullptr, sh_out, sh_scale);
+    hip_check(hipGetLastError(), "moe combine launch");
+}
+
 void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float *post_norm, float eps,
                     const MoeWork &ws) {
+    if (ctx->exact) {
+        launch_moe_ffn_exact(ctx, L, hidden, post_norm, eps, ws);
+        return;
+    }
     const k2t_experts *b = L.bank;
     const int d = (int)b->hdr.d_model, dff = (int)b->hdr.d_ff_expert, E = (int)b->hdr.experts_per_layer;
     hipStream_t st = ctx->stream;
@@ -291,7 +477,8 @@ void launch_moe_ffn(k2t_ctx *ctx, const MoeLayer &L, float *hidden, const float 
 
 size_t moe_work_floats(const k2t_experts *b, int top_k) {
     const size_t d = (size_t)b->hdr.d_model, dff = (size_t)b->hdr.d_ff_expert, E = (size_t)b->hdr.experts_per_layer;
-    return (size_t)top_k * 2 * dff + (size_t)top_k * d + 4 * E + 4 + 2 * K2T_MOE_MAX_TOPK + 2 * (size_t)top_k + 64;
+    return (size_t)top_k * 2 * dff + (size_t)top_k * d + 4 * E + 4 + 2 * K2T_MOE_MAX_TOPK + 2 * (size_t)top_k + 64 +
+           64 + d / 4 + 2 * (d / 64) + (size_t)top_k * dff / 4 + 2 * ((size_t)top_k * dff / 64) + 64;
 }
 
 MoeWork moe_work_carve(float *base, const k2t_experts *b, int top_k) {
@@ -312,6 +499,20 @@ MoeWork moe_work_carve(float *base, const k2t_experts *b, int top_k) {
     p += top_k;
     w.ctr = reinterpret_cast<uint32_t *>(p);
     w.err = reinterpret_cast<int *>(p + 1);
+    p += 64;
+    w.rms = p;
+    p += 64;
+    w.as = p;
+    p += d / 64;
+    w.asum = reinterpret_cast<int32_t *>(p);
+    p += d / 64;
+    w.ms = p;
+    p += (size_t)top_k * dff / 64;
+    w.msum = reinterpret_cast<int32_t *>(p);
+    p += (size_t)top_k * dff / 64;
+    w.aq = reinterpret_cast<int8_t *>(p);
+    p += d / 4;
+    w.mq = reinterpret_cast<int8_t *>(p);
     return w;
 }
 

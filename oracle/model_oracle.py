@@ -250,9 +250,10 @@ SOFTMAX, TOPK_SOFTMAX, SIGMOID = 0, 1, 2
 
 
 def route_sorted(logits, top_k, norm_topk_prob, scoring):
-    """DenseMoeRouter::route_sorted after the logits (sparse_moe.rs:86-182) in float32:
-    scoring, select_topk_by_score (strict '>' insertion, 185-206), renormalization in
-    selection order, then sort by ascending expert id."""
+    """DenseMoeRouter::route_sorted after the logits (sparse_moe.rs:86-182) in float32, the
+    x86 build's order: scoring with the platform expf (O.expf) and sequential sums,
+    select_topk_by_score (strict '>' insertion, 185-206), renormalization in selection
+    order, then sort by ascending expert id."""
     z = np.asarray(logits, np.float32).copy()
     E = z.size
     k = min(top_k, E)
@@ -261,12 +262,12 @@ def route_sorted(logits, top_k, norm_topk_prob, scoring):
         m = z.max()
         s = f32(0.0)
         for e in range(E):
-            z[e] = np.exp(f32(z[e] - m), dtype=np.float32)
+            z[e] = O.expf(f32(z[e] - m))[0]
             s = f32(s + z[e])
         inv = f32(1.0) / s if s > 0 else f32(1.0) / f32(E)
         z = (z * inv).astype(np.float32)
     elif scoring == SIGMOID:
-        z = (f32(1.0) / (f32(1.0) + np.exp(-z, dtype=np.float32))).astype(np.float32)
+        z = (f32(1.0) / (f32(1.0) + O.expf(-z))).astype(np.float32)
     out = []
     for e in range(E):
         v = z[e]
@@ -283,7 +284,7 @@ def route_sorted(logits, top_k, norm_topk_prob, scoring):
             out.pop()
     if scoring == TOPK_SOFTMAX:
         mz = max(w for _, w in out)
-        ws = [np.exp(f32(w - mz), dtype=np.float32) for _, w in out]
+        ws = [O.expf(f32(w - mz))[0] for _, w in out]
         s = f32(0.0)
         for w in ws:
             s = f32(s + w)
@@ -322,7 +323,7 @@ def shared_expert(xn, aq, as_, sh):
         z = np.float32(0.0)
         for a, b in zip(np.asarray(gw, np.float32), np.asarray(xn, np.float32)):
             z = np.float32(z + np.float32(a * b))
-        scale = np.float32(1.0) / (np.float32(1.0) + np.exp(-z, dtype=np.float32))
+        scale = np.float32(1.0) / (np.float32(1.0) + O.expf(-z)[0])
         if abs(float(scale) - 1.0) > float(np.finfo(np.float32).eps):
             out = (out * scale).astype(np.float32)
     return out
@@ -335,8 +336,9 @@ def moe_ffn(hidden, post_norm, eps, moe):
     optional shared: see shared_expert).  Returns (new hidden, routes)."""
     xn = rms_norm(hidden, post_norm, eps)
     W = np.asarray(moe["router_w"], np.float32)
-    logits = np.array([np.dot(W[e].astype(np.float64), xn.astype(np.float64)) for e in range(W.shape[0])],
-                      np.float32)
+    # dot_f32_moe on x86 (sparse_moe.rs:1644-1656): f32 products added in index order
+    # (np.cumsum accumulates sequentially in float32)
+    logits = np.cumsum((W * xn[None, :]).astype(np.float32), axis=1, dtype=np.float32)[:, -1].astype(np.float32)
     if moe.get("router_b") is not None:
         logits = (logits + moe["router_b"]).astype(np.float32)
     routes = route_sorted(logits, moe["top_k"], moe["norm_topk_prob"], moe["scoring"])

@@ -365,6 +365,15 @@ def rope_apply(head, row):
     return h
 
 
+def expf(x):
+    """The platform libm's expf elementwise (glibc on the x86 host: the reference's x86
+    `f32::exp`, real_llm.rs:9595 / 9803, sparse_moe.rs:131, 155)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    y = np.empty_like(x)
+    lib().or_expf_array(x, y, x.size)
+    return y
+
+
 def swiglu(g, u):
     g = _f32(g)
     out = np.zeros_like(g)

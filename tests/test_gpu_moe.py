@@ -243,6 +243,16 @@ def test_moe_model_decode_matches_oracle(gpu_ctx, graph):
     for t in (3, 250, 17):
         c = gm.decode(t)
     assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+    # exact-order mode (the MoE in the x86 reference's order too): decode equals the oracle
+    # bit for bit
+    gm.set_exact(True)
+    gm.reset()
+    ref3 = OracleModel(cfg, layers, head, fn)
+    for i, t in enumerate(toks):
+        a, b = gm.decode(int(t)), ref3.forward_token(int(t))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), \
+            f"exact step {i}: rel {float(np.abs(a - b).max() / np.abs(b).max()):.2e}"
+    gm.set_exact(False)
     gm.close()
     for m in mats + [hm]:
         m.close()
@@ -252,7 +262,7 @@ def test_moe_model_decode_matches_oracle(gpu_ctx, graph):
 def test_moe_model_shared_expert_matches_oracle(gpu_ctx):
     """Qwen2-MoE-style layers with a shared expert (SharedMoeExpert, NF backend,
     sparse_moe.rs:209-312): layer 0 with a sigmoid gate row, layer 1 without, inter 192 in
-    [gate; up] row order.  Decode in exact-order mode within 1e-5 of the oracle and on the
+    [gate; up] row order.  Decode in exact-order mode bit-identical to the oracle and on the
     fast path within its bar, a 3-token prefill vs the oracle; removing the shared expert
     changes the logits."""
     print("moe model with a shared expert", flush=True)
@@ -290,10 +300,10 @@ def test_moe_model_shared_expert_matches_oracle(gpu_ctx):
     hm = up(head)
     gm.set_head(hm, fn)
     toks = np.random.default_rng(9).integers(0, cfg["vocab"], 5)
-    # exact-order steps (x86 sum-of-squares order, expf, sequential attention sums; the MoE
-    # keeps its tree-order router dot and combine) stay within 1e-5 of the oracle at every
-    # step; the fast path moves single int8 codes (1 - cos up to about 1.4e-4 here, 4e-5
-    # with no shared expert), so its bar is cosine > 0.9998
+    # exact-order steps (x86 sum-of-squares order, expf_rn, sequential attention sums, the
+    # MoE's sequential router dot, shared-expert gate and in-order GEMV epilogues) equal the
+    # oracle bit for bit at every step; the fast path moves single int8 codes (1 - cos up to
+    # about 1.4e-4 here, 4e-5 with no shared expert), so its bar is cosine > 0.9998
     last = None
     for exact in (True, False):
         gm.set_exact(exact)
@@ -304,7 +314,7 @@ def test_moe_model_shared_expert_matches_oracle(gpu_ctx):
             cos = float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b)))
             rel = float(np.abs(a - b).max() / np.abs(b).max())
             if exact:
-                assert cos > 0.999999 and rel <= 1e-5, f"exact step {i}: cos {cos} rel {rel}"
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"exact step {i}: cos {cos} rel {rel}"
             else:
                 assert cos > 0.9998 and rel <= 2e-2, f"step {i}: cos {cos} rel {rel}"
             last = a

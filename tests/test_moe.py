@@ -119,3 +119,33 @@ def test_oracle_shared_expert_against_float_math(gated):
     cos = float(np.dot(got, want) / (np.linalg.norm(got) * np.linalg.norm(want)))
     assert cos > 0.999, cos
     assert abs(np.linalg.norm(got) / np.linalg.norm(want) - 1) < 0.02
+
+
+def test_oracle_router_logits_sequential_float32():
+    """The oracle's router logits follow dot_f32_moe on x86 (sparse_moe.rs:1644-1656):
+    float32 products added in index order from 0.  Pinned against an explicit float32
+    loop (the closed form of that order), and shown to differ from a float64 dot on some
+    logit (so the order is observable and the test can fail)."""
+    import oracle as O
+    from model_oracle import moe_ffn
+    rng = np.random.default_rng(5)
+    d, E = 256, 16
+    W = (rng.standard_normal((E, d)) * 0.05).astype(np.float32)
+    h = rng.standard_normal(d).astype(np.float32)
+    pn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    xn = ((h * np.float32(O.inv_rms(h, 1e-6))) * pn).astype(np.float32)
+    loop = np.zeros(E, np.float32)
+    for e in range(E):
+        a = np.float32(0.0)
+        for i in range(d):
+            a = np.float32(a + np.float32(W[e, i] * xn[i]))
+        loop[e] = a
+    via = np.cumsum((W * xn[None, :]).astype(np.float32), axis=1, dtype=np.float32)[:, -1]
+    assert np.array_equal(loop.view(np.uint32), via.astype(np.float32).view(np.uint32))
+    f64 = np.array([np.dot(W[e].astype(np.float64), xn.astype(np.float64)) for e in range(E)], np.float32)
+    assert not np.array_equal(loop, f64)
+    # moe_ffn routes on exactly these logits: its top-1 route is argmax of the loop's softmax
+    lay, _ = random_moe_layer(rng, d, 64, E, bits=4)
+    moe = dict(router_w=W, router_b=None, top_k=2, norm_topk_prob=True, scoring=SOFTMAX, experts=lay)
+    _, routes = moe_ffn(h, pn, 1e-6, moe)
+    assert set(e for e, _ in routes) == set(np.argsort(-loop, kind="stable")[:2].tolist())
