@@ -232,10 +232,10 @@ struct GemvWave {
         const int xsum = FMT == 0 ? xsuml[c] : 0;
         int r0, r1;
         chunk_dots<FMT, HP>(M, fr, half, x, xsum, r0, r1);
-        const float n0 = fmaf((float)r0 * sx, bf16_lo(fr.ws), f0);
-        const float n1 = fmaf((float)r1 * sx, bf16_hi(fr.ws), f1);
-        f0 = sx != 0.0f ? n0 : f0;
-        f1 = sx != 0.0f ? n1 : f1;
+        // (a chunk with sx == 0 has all-zero codes: its term is +0, so the reference's skip
+        // of such chunks needs no test on this path)
+        f0 = fmaf((float)r0 * sx, bf16_lo(fr.ws), f0);
+        f1 = fmaf((float)r1 * sx, bf16_hi(fr.ws), f1);
     }
 };
 
