@@ -487,7 +487,8 @@ __device__ __forceinline__ float quant_head(float v0, float v1, int nb, uint32_t
 
 // Attention of q head h for the current position (causal_gqa_group_q8,
 // real_llm.rs:8471-8594) over span sp of the context: its seq = pos + 1 positions are cut
-// into P.nsp spans of ceil(seq / nsp) positions (two spans: 60% and 40%).  A task of span sp > 0 hands its span's
+// into P.nsp spans (span 0: 60% of two, 34% of four; the others equal).  A task of span
+// sp > 0 hands its span's
 // maximum score m, sum of exp(s_t - m) and o = sum_t exp(s_t - m) vs_t v8_t over as
 // 2 + hd words of APART; the span-0 task merges them with its own (global maximum,
 // exp-weighted sums in span order) and ends with the o_proj activation chunks of the
@@ -531,11 +532,18 @@ __device__ bool attention_head(const MkParams &P, const float *bias, const Lds &
     // spans of this step: at least kMkSpanMin positions each, at most the P.nsp allotted
     const int nsp = min(P.nsp, max(1, (seq + kMkSpanMin - 1) / kMkSpanMin));
     if (sp >= nsp) return true;
-    // Two spans: span 0, which also merges, takes the first 60% (its merge then starts
-    // about when span 1's words arrive; 1.7B nf4g128 1447 -> 1452 tok/s against halves).
-    const int len0 = nsp == 2 ? (seq * 60 + 99) / 100 : (seq + nsp - 1) / nsp;
-    const int len = nsp == 2 ? (sp == 0 ? len0 : seq - len0) : len0;
-    const int t0 = min(seq, sp * len0), t1 = min(seq, t0 + len), n = t1 - t0;
+    // Span 0, which also merges, takes a larger share: 60% of two spans, 34% of four (its
+    // merge then starts about when the other spans' words arrive; the rest is split
+    // evenly).  1.7B nf4g128 (two spans) 1447 -> 1452 tok/s against halves; 135M p55454
+    // (four spans) 1567 -> 1574 against quarters (40%: 1564, 46%: 1534).
+#ifndef K2T_MK_SPAN0_4
+#define K2T_MK_SPAN0_4 34
+#endif
+    const int pct0 = nsp == 2 ? 60 : nsp == 4 ? K2T_MK_SPAN0_4 : 100 / nsp;
+    const int len0 = nsp == 1 ? seq : (seq * pct0 + 99) / 100;
+    const int lenr = nsp == 1 ? 0 : (seq - len0 + nsp - 2) / (nsp - 1);
+    const int t0 = min(seq, sp == 0 ? 0 : len0 + (sp - 1) * lenr);
+    const int t1 = min(seq, sp == 0 ? len0 : t0 + lenr), n = t1 - t0;
     const bool cover = t0 <= pos && pos < t1;
     const size_t base = ((size_t)layer * nkv + kvh) * P.max_seq;
     const int ncg = hd / 4, nps = NTH / ncg;
