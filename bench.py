@@ -2,7 +2,7 @@
 
 Metric: quant GEMV HBM GB/s (% of peak) + decode tok/s, 1.7B-shape
 nf4g128.  `value` is decode tok/s of the SmolLM2-1.7B-shaped nf4g128 model (config 3:
-256-token prefill in 4-token GEMV tiles, then greedy decode steps; a "step" is one
+256-token prefill (NF4 GEMVs on the int8 matrix cores), then greedy decode steps; a "step" is one
 decode token).  Also reported: the config-4 GEMV sweep (nf4g128 and b6 GEMVs on
 14336x4096 and 4096x14336 at batch 1 and 4, each launch reading a different weight copy
 so the 256 MB Infinity Cache cannot serve them; HIP-event burst timing on the kernels'
@@ -153,10 +153,12 @@ def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log, planes
         model.set_exact(int(os.environ["K2T_MODEL_EXACT"]))
     if os.environ.get("K2T_PERSISTENT"):
         model.set_persistent(int(os.environ["K2T_PERSISTENT"]))
+    if os.environ.get("K2T_MFMA"):
+        ctx.set_mfma(int(os.environ["K2T_MFMA"]))
     wbytes = sum(m.info()[3] for m in mats)
     rng = np.random.default_rng(SEED)
     toks = rng.integers(0, cfg["vocab"], prefill).astype(np.int32)
-    model.prefill(toks[:8], want_logits=False)  # warm the prefill kernels
+    model.prefill(toks[:32], want_logits=False)  # warm the prefill kernels
     model.reset()
     model.sync()
     t0 = time.perf_counter()
@@ -571,7 +573,7 @@ def main():
         "data": "synthetic: random-init weights ~N(0,0.02) seeded, Hadamard RTN-quantized on the host; seeded "
                 "random token ids; greedy decode",
         "config": {"workload": "config 3: SmolLM2-1.7B-shaped nf4g128 (24 layers, d 2048, 32 heads MHA, hd 64, "
-                               "ffn 8192, vocab 49152), 256-token prefill in 4-token tiles then greedy decode",
+                               "ffn 8192, vocab 49152), 256-token prefill (int8-MFMA NF4 GEMVs) then greedy decode",
                    "decode_1_7b_nf4g128": r17, "decode_135m_p55454_ctx512": r135, "decode_135m_b4_ctx512": rb4,
                    "decode_135m_b6_ctx512": rb6,
                    "decode_30b_a3b_moe_nf3_ctx6600": r30, "gemv_sweep": results},

@@ -80,6 +80,13 @@ int32_t k2t_ctx_set_splitk(k2t_ctx *ctx, int32_t max_segments);
  * within a few ulp of the reference, and faster for long K.  Integer per-(row, chunk)
  * dots are exact in both modes. */
 int32_t k2t_ctx_set_exact(k2t_ctx *ctx, int32_t exact);
+/* Batched NF4 GEMVs (16 or more tokens of a ready activation over the whole matrix,
+ * k2t_gemv and the model's prefill): enable = 1 (default) runs them on the int8 matrix
+ * cores, one weight pass per 64 tokens, with outputs equal to the exact-order epilogue's
+ * in either mode; 0 runs the 4-token weight passes of nf_sdot_decode_neon's tile
+ * (simd_lut.rs:6074-6364).  A backend choice of this build; the reference has no
+ * counterpart. */
+int32_t k2t_ctx_set_mfma(k2t_ctx *ctx, int32_t enable);
 
 /* ---- device memory helpers (tests, benches, non-torch callers) ---------- */
 int32_t k2t_malloc(k2t_ctx *ctx, size_t bytes, void **d_out);

@@ -291,6 +291,13 @@ int32_t k2t_ctx_set_exact(k2t_ctx *ctx, int32_t exact) {
     });
 }
 
+int32_t k2t_ctx_set_mfma(k2t_ctx *ctx, int32_t enable) {
+    return guarded([&] {
+        arg_check(ctx != nullptr, "ctx is NULL");
+        ctx->mfma = enable ? 1 : 0;
+    });
+}
+
 int32_t k2t_malloc(k2t_ctx *ctx, size_t bytes, void **d_out) {
     return guarded([&] {
         arg_check(ctx && d_out, "NULL argument");

@@ -1,0 +1,174 @@
+// Batched NF4 GEMV (prefill) on the int8 matrix cores of gfx950: out[t][r] =
+// sum_c fmaf(float(dot_{r,c,t}) * sx[t][c], ws[r][c], ...) for up to 64 tokens per weight
+// pass, the chunk dots from v_mfma_i32_16x16x64_i8.
+//
+// The reference runs prefill through the same NfSdotMatrix kernels as decode, four tokens
+// per weight pass (nf_sdot_decode_neon's 4-token tile, simd_lut.rs:6074-6364).  Here one
+// wave owns one 16-row stripe and 16 to 64 tokens: per 64-column chunk it decodes the
+// stripe-chunk's NF4 codes to int8 once (the codebook as two v_perm XOR tables,
+// nf4_xlut), then runs one MFMA per 16-token block (A: 16 rows x 64 codes, B: 64
+// activation bytes x 16 tokens), so each weight byte is read once per 64 tokens instead of
+// once per 4.  The epilogue is the reference's per-row chain in chunk order (simd_lut.rs:
+// 4030-4059, 6334-6335: f = fmaf(float(dot) * sx, scale, f), chunks with sx == 0 skipped),
+// so every output equals the exact-order GEMV's (k2t_ctx_set_exact) bit for bit.
+//
+// Operand layouts of v_mfma_i32_16x16x64_i8 (checked on the GPU): lane l holds 16 bytes of
+// A row l % 16 and of B column l % 16; the products pair lane l's byte b of A with lane
+// l's byte b of B over the four lane groups l / 16, so any one assignment of the 64
+// columns to (l / 16, b) used for both operands gives the dot.  Here byte b of group g is
+// column 16g + b.  The 16 x 16 int32 result: lane l holds rows 4 (l / 16) + r, r = 0..3,
+// of column l % 16.
+//
+// NF stripe-chunk bytes (512 per stripe, NfSdotMatrix, simd_lut.rs:4796-5023): byte e of
+// dword j at kk*128 + g*32 + half*16 + 4j holds the codes of row 4g + j, columns kk*16 +
+// half*8 + e (low nibble) and kk*16 + half*8 + 4 + e (high nibble).  Row i's columns
+// 16kk .. 16kk+15 are therefore the dwords at kk*128 + (i/4)*32 + 4(i%4) and 16 bytes
+// further: low / high nibbles of the first give columns 0-3 / 4-7, of the second 8-11 /
+// 12-15.
+#include "../../include/k2t_hip.h"
+#include "k2t_device.h"
+#include "k2t_internal.h"
+
+namespace k2t {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct MfArgs {
+    const uint8_t *pair, *tail;
+    size_t ptot;  // bytes per pair stream
+    int rows, nc, np, stripes, sgc;
+    uint32_t t0, t1, u0, u1;  // NF4 codebook XOR tables (nf4_xor_tables)
+    const int8_t *xq;
+    const float *xs;
+    int K, ntok;
+    float *out;
+    size_t out_stride;
+    int accum;
+};
+
+// Everything one chunk needs, requested a chunk ahead.
+template <int NB>
+struct MfChunk {
+    uint32_t d0, d1;
+    uint2 sw;
+    int4 x[NB];
+    float sx[NB];
+};
+
+template <int NB>
+__device__ __forceinline__ void mf_fetch(const MfArgs &A, const uint8_t *mbase, bool is_tail, uint32_t nib0,
+                                         uint32_t a_off, uint32_t s_off, const int (&tok)[NB], uint32_t lg, int c,
+                                         MfChunk<NB> &f) {
+    const int sg = c / A.sgc, cst = sg * A.sgc, sb = c - cst;
+    const size_t cs = is_tail ? 512 : 1024;
+    const uint8_t *gb = mbase + (size_t)sg * (is_tail ? 32 : 64) + (size_t)cst * cs;
+    const uint8_t *rec = gb + nib0 + (size_t)sb * cs;
+    f.d0 = *reinterpret_cast<const uint32_t *>(rec + a_off);
+    f.d1 = *reinterpret_cast<const uint32_t *>(rec + a_off + 16);
+    f.sw = *reinterpret_cast<const uint2 *>(gb + s_off);
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        f.x[b] = *reinterpret_cast<const int4 *>(A.xq + (size_t)tok[b] * A.K + (size_t)c * 64 + 16 * lg);
+        f.sx[b] = A.xs[(size_t)tok[b] * A.nc + c];
+    }
+}
+
+template <int NB>
+__global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const int stripe = (int)blockIdx.x * 4 + (int)wave;
+    if (stripe >= A.stripes) return;  // whole waves; the kernel has no barrier
+    const int tokb = (int)blockIdx.y * 16 * NB;
+    const bool is_tail = stripe >= 2 * A.np;
+    const uint32_t side = is_tail ? 0u : (uint32_t)(stripe & 1);
+    const uint8_t *mbase = is_tail ? A.tail : A.pair + (size_t)(stripe >> 1) * A.ptot;
+    const uint32_t li = lane & 15u, lg = lane >> 4;
+    const uint32_t a_off = lg * 128u + (li >> 2) * 32u + 4u * (li & 3u);
+    const uint32_t s_off = (is_tail ? 0u : side * 32u) + 8u * lg;  // rows 4lg .. 4lg+3
+    const uint32_t nib0 = is_tail ? 32u : 64u + side * 512u;
+    int tok[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) tok[b] = min(tokb + 16 * b + (int)li, A.ntok - 1);
+    float acc[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[b][r] = 0.0f;
+    MfChunk<NB> cur, nxt;
+    mf_fetch<NB>(A, mbase, is_tail, nib0, a_off, s_off, tok, lg, 0, cur);
+    for (int c = 0; c < A.nc; c++) {
+        if (c + 1 < A.nc) mf_fetch<NB>(A, mbase, is_tail, nib0, a_off, s_off, tok, lg, c + 1, nxt);
+        v4i a;
+        a[0] = (int)nf4_xlut(cur.d0 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+        a[1] = (int)nf4_xlut((cur.d0 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+        a[2] = (int)nf4_xlut(cur.d1 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+        a[3] = (int)nf4_xlut((cur.d1 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+        const float ws[4] = {bf16_lo(cur.sw.x), bf16_hi(cur.sw.x), bf16_lo(cur.sw.y), bf16_hi(cur.sw.y)};
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const v4i bv = {cur.x[b].x, cur.x[b].y, cur.x[b].z, cur.x[b].w};
+            const v4i zero = {0, 0, 0, 0};
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bv, zero, 0, 0, 0);
+            const float sx = cur.sx[b];
+            const bool on = sx != 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                acc[b][r] = fmaf(on ? (float)d[r] * sx : -0.0f, on ? ws[r] : 0.0f, acc[b][r]);
+        }
+        cur = nxt;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int t = tokb + 16 * b + (int)li;
+        if (t >= A.ntok) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = stripe * 16 + 4 * (int)lg + r;
+            if (row >= A.rows) continue;
+            float *o = A.out + (size_t)t * A.out_stride + row;
+            *o = A.accum ? *o + acc[b][r] : acc[b][r];
+        }
+    }
+}
+
+}  // namespace
+
+bool gemm_nf4_mfma_supported(const k2t_mat *m, int ntok) {
+    return m->fmt == K2T_FMT_NF && m->bits == 4 && ntok >= kMfmaMinTokens && m->cols % 64 == 0;
+}
+
+void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, int ntok, float *out,
+                          size_t out_stride, bool accum) {
+    if (!gemm_nf4_mfma_supported(m, ntok)) throw Error(K2T_E_INTERNAL, "mfma gemm: unsupported matrix");
+    MfArgs A{};
+    A.pair = m->pair;
+    A.tail = m->tail;
+    A.ptot = m->pairs ? m->pair_len / m->pairs : 0;
+    A.rows = m->rows;
+    A.nc = m->nc;
+    A.np = m->pairs;
+    A.stripes = m->stripes;
+    A.sgc = m->sgc;
+    nf4_xor_tables(m->cb[0], m->cb[1], m->cb[2], m->cb[3], A.t0, A.t1, A.u0, A.u1);
+    A.xq = xq;
+    A.xs = xs;
+    A.K = m->cols;
+    A.ntok = ntok;
+    A.out = out;
+    A.out_stride = out_stride;
+    A.accum = accum ? 1 : 0;
+    const int nb = std::min(4, (ntok + 15) / 16);
+    const dim3 grid((m->stripes + 3) / 4, (ntok + 16 * nb - 1) / (16 * nb));
+    hipStream_t st = ctx->stream;
+    switch (nb) {
+        case 1: hipLaunchKernelGGL(gemm_nf4_mfma_kernel<1>, grid, dim3(256), 0, st, A); break;
+        case 2: hipLaunchKernelGGL(gemm_nf4_mfma_kernel<2>, grid, dim3(256), 0, st, A); break;
+        case 3: hipLaunchKernelGGL(gemm_nf4_mfma_kernel<3>, grid, dim3(256), 0, st, A); break;
+        default: hipLaunchKernelGGL(gemm_nf4_mfma_kernel<4>, grid, dim3(256), 0, st, A); break;
+    }
+    hip_check(hipGetLastError(), "mfma gemm launch");
+}
+
+}  // namespace k2t

@@ -949,6 +949,13 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
                              const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
                              int32_t *dots, bool accum, int xsm, const float *src, const float *w, float eps,
                              const GemvGroup *grp, int gu_split) {
+    // 16 or more tokens of a ready activation through an NF4 matrix: the matrix-core
+    // kernel (one weight pass per 64 tokens; its outputs equal the exact-order GEMV's)
+    if (!dots && !grp && xsm == 0 && gu_split == 0 && s0 == 0 && s1 == m->stripes && ctx->mfma &&
+        gemm_nf4_mfma_supported(m, ntok)) {
+        launch_gemm_nf4_mfma(ctx, m, xq, xs, ntok, out, out_stride, accum);
+        return;
+    }
     const int saved = ctx->max_segments;
     if (dots) ctx->max_segments = 1;
     GemvPlan plan = plan_gemv(ctx, m, s0, s1);

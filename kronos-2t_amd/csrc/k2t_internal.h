@@ -14,6 +14,7 @@ struct k2t_ctx {
     int max_segments = 0;  // cap on waves (K segments) per GEMV workgroup; 0 = automatic
     int exact = 0;         // 1: bit-exact fmaf-chain epilogue
     int stage_x = 1;       // 1: single-token GEMVs stage the int8 activation through LDS
+    int mfma = 1;          // 1: batched NF4 GEMVs on the matrix cores (k2t_ctx_set_mfma)
     int num_cus = 256;
     // small device scratch (debug entry points): grown on demand
     float *scratch = nullptr;
@@ -126,6 +127,12 @@ void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const floa
                     float *out, size_t out_stride, bool accumulate, int gu_split = 0);
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
                        bool exact);
+// Batched NF4 GEMV on the matrix cores (k2t_gemm_mfma.hip): kMfmaMinTokens or more tokens
+// of a ready int8 activation, outputs equal to the exact-order GEMV's.
+constexpr int kMfmaMinTokens = 16;
+bool gemm_nf4_mfma_supported(const k2t_mat *m, int ntok);
+void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, int ntok, float *out,
+                          size_t out_stride, bool accum);
 void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, int xs_mode, const float *src,
                          const float *w, float eps, float *out);
 

@@ -49,6 +49,7 @@ SIGNATURES = {
     "k2t_ctx_sync": (I32, [VP]),
     "k2t_ctx_set_splitk": (I32, [VP, I32]),
     "k2t_ctx_set_exact": (I32, [VP, I32]),
+    "k2t_ctx_set_mfma": (I32, [VP, I32]),
     "k2t_malloc": (I32, [VP, SZ, C.POINTER(VP)]),
     "k2t_free": (I32, [VP, VP]),
     "k2t_memcpy_h2d": (I32, [VP, VP, VP, SZ]),
@@ -214,6 +215,9 @@ class Ctx:
 
     def set_exact(self, on):
         check(lib().k2t_ctx_set_exact(self.h, int(bool(on))))
+
+    def set_mfma(self, on):
+        check(lib().k2t_ctx_set_mfma(self.h, int(bool(on))))
 
     def sync(self):
         check(lib().k2t_ctx_sync(self.h))

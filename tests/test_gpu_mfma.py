@@ -1,0 +1,95 @@
+"""Batched NF4 GEMV on the matrix cores (k2t_gemm_mfma.hip: 16 or more tokens per call,
+one weight pass per 64 tokens).
+
+Bar: every output bit-identical to the oracle's per-token NF4 GEMV (the reference's
+per-row fmaf chain in chunk order, simd_lut.rs:4030-4059), in the fast and the exact
+mode, for shapes with and without a tail stripe, scale groups of one and two chunks and
+token counts that leave partial 16-token blocks; with the matrix cores off, the exact
+mode's 4-token passes give the same bits.  Model level: a 40-token prefill through it
+equals exact-order token-by-token decode and the oracle bit for bit, and the fast-mode
+prefill stays within the fast path's bar.
+"""
+import numpy as np
+import pytest
+
+import k2t
+import oracle as O
+from helpers import acts, quantized_nf4
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _batch(ctx, m, xq, xs, xsum, rows, ntok, exact, mfma=True):
+    import torch
+    out = torch.full((ntok, rows), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.set_exact(exact)
+    ctx.set_mfma(mfma)
+    try:
+        ctx.gemv(m, _t(xq), _t(xs), _t(xsum), out, ntok=ntok, out_stride=rows)
+        ctx.sync()
+    finally:
+        ctx.set_exact(False)
+        ctx.set_mfma(True)
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,cols,sgc,ntok", [(1040, 2048, 2, 16), (64, 576, 1, 17), (2048, 2048, 2, 64),
+                                                (96, 1536, 2, 100), (1536, 4096, 2, 256)])
+def test_mfma_gemv_equals_reference_chain(gpu_ctx, rows, cols, sgc, ntok):
+    print(f"mfma gemv {rows}x{cols} sgc {sgc} ntok {ntok}", flush=True)
+    rng = np.random.default_rng(rows + cols + ntok)
+    _, cb, _, _, pair, tail = quantized_nf4(rng, rows, cols, sgc)
+    m = gpu_ctx.upload_nf(rows, cols, 4, sgc, cb, pair, tail)
+    xq, xs, xsum = acts(rng, cols, ntok, outlier_frac=0.001, outlier_scale=30.0)
+    xs[min(3, ntok - 1), 1] = 0.0  # a chunk with scale 0 (skipped by the reference's chain)
+    xq[min(3, ntok - 1), 64:128] = 0
+    ref = np.stack([O.nf_gemv(pair, tail, rows, cols, 4, sgc, cb, xq[t], xs[t]) for t in range(ntok)])
+    for exact in (False, True):
+        out = _batch(gpu_ctx, m, xq, xs, xsum, rows, ntok, exact)
+        bad = np.argwhere(out.view(np.uint32) != ref.view(np.uint32))
+        assert bad.size == 0, f"exact={exact}: {len(bad)} outputs differ, first {bad[:3].tolist()}"
+    if ntok <= 64:
+        four = _batch(gpu_ctx, m, xq, xs, xsum, rows, ntok, True, mfma=False)
+        assert np.array_equal(four.view(np.uint32), ref.view(np.uint32))
+    m.close()
+
+
+def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx):
+    """A 2-layer nf4 model (d 256, 4 heads of 64, ffn 768): a 40-token prefill (qkv, o
+    with the residual add, gate_up and down with the residual add on the matrix cores) in
+    exact-order mode equals the oracle bit for bit, and so does the one with the matrix
+    cores off; in fast mode it stays within the fast path's bar of the oracle."""
+    from model_oracle import OracleModel, random_model
+    from test_gpu_model import _close, _gpu_model
+    print("mfma prefill vs oracle", flush=True)
+    cfg = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, intermediate=768, vocab=520,
+               max_seq=64, rms_eps=1e-5, rope_theta=10000.0)
+    layers, head, fn = random_model(cfg, seed=41, fmt="nf4")
+    ref = OracleModel(cfg, layers, head, fn)
+    toks = np.random.default_rng(42).integers(0, cfg["vocab"], 40)
+    for t in toks[:-1]:
+        ref.forward_token(int(t), want_logits=False)
+    b = ref.forward_token(int(toks[-1]))
+    gm, mats = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
+    try:
+        gm.set_exact(True)
+        for mfma in (True, False):
+            gpu_ctx.set_mfma(mfma)
+            gm.reset()
+            pre = gm.prefill(toks, want_logits=True)
+            assert np.array_equal(pre.view(np.uint32), b.view(np.uint32)), f"mfma={mfma}"
+        gpu_ctx.set_mfma(True)
+        gm.set_exact(False)
+        gm.reset()
+        ok, info = _close(gm.prefill(toks, want_logits=True), b, 0.9999)
+        assert ok, info
+    finally:
+        gpu_ctx.set_mfma(True)
+        gm.close()
+        for m in mats:
+            m.close()
