@@ -33,6 +33,15 @@ namespace k2t {
 
 namespace {
 
+#ifndef K2T_MFMA_DEPTH
+#define K2T_MFMA_DEPTH 4
+#endif
+#ifndef K2T_MFMA_MIN_WAVES
+#define K2T_MFMA_MIN_WAVES 2048
+#endif
+constexpr int kMfmaDepth = K2T_MFMA_DEPTH;         // chunks in flight per wave
+constexpr long kMfmaMinWaves = K2T_MFMA_MIN_WAVES;  // 8 waves per CU
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct MfArgs {
@@ -40,15 +49,15 @@ struct MfArgs {
     size_t ptot;  // bytes per pair stream
     int rows, nc, np, stripes, sgc;
     uint32_t t0, t1, u0, u1;  // NF4 codebook XOR tables (nf4_xor_tables)
-    const int8_t *xq;
-    const float *xs;
-    int K, ntok;
+    const int8_t *xt;  // activations tile-major: [16-token block][chunk][64 lanes][16 bytes]
+    const float *st;   // their scales: [16-token block][chunk][16 tokens]
+    int K, ntok, nblk;  // nblk: 16-token blocks in the tiles
     float *out;
     size_t out_stride;
     int accum;
 };
 
-// Everything one chunk needs, requested a chunk ahead.
+// Everything one chunk needs (one ring stage).
 template <int NB>
 struct MfChunk {
     uint32_t d0, d1;
@@ -59,7 +68,7 @@ struct MfChunk {
 
 template <int NB>
 __device__ __forceinline__ void mf_fetch(const MfArgs &A, const uint8_t *mbase, bool is_tail, uint32_t nib0,
-                                         uint32_t a_off, uint32_t s_off, const int (&tok)[NB], uint32_t lg, int c,
+                                         uint32_t a_off, uint32_t s_off, int tb0, uint32_t lane, int c,
                                          MfChunk<NB> &f) {
     const int sg = c / A.sgc, cst = sg * A.sgc, sb = c - cst;
     const size_t cs = is_tail ? 512 : 1024;
@@ -70,12 +79,39 @@ __device__ __forceinline__ void mf_fetch(const MfArgs &A, const uint8_t *mbase, 
     f.sw = *reinterpret_cast<const uint2 *>(gb + s_off);
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-        f.x[b] = *reinterpret_cast<const int4 *>(A.xq + (size_t)tok[b] * A.K + (size_t)c * 64 + 16 * lg);
-        f.sx[b] = A.xs[(size_t)tok[b] * A.nc + c];
+        const size_t tile = (size_t)min(tb0 + b, A.nblk - 1) * A.nc + c;  // blocks past the last: never stored
+        f.x[b] = *reinterpret_cast<const int4 *>(A.xt + tile * 1024 + lane * 16);
+        f.sx[b] = A.st[tile * 16 + (lane & 15u)];
     }
 }
 
+// One chunk's decode, MFMAs and epilogue steps.  A chunk whose activation scale is 0
+// needs no select: its term float(d) * 0 * ws is +-0, and adding +-0 leaves every
+// accumulator unchanged (each starts at +0 and a round-to-nearest sum is -0 only when
+// both addends are -0, so no accumulator is ever -0).
 template <int NB>
+__device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<NB> &f, float (&acc)[NB][4]) {
+    v4i a;
+    a[0] = (int)nf4_xlut(f.d0 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+    a[1] = (int)nf4_xlut((f.d0 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+    a[2] = (int)nf4_xlut(f.d1 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+    a[3] = (int)nf4_xlut((f.d1 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+    const float ws[4] = {bf16_lo(f.sw.x), bf16_hi(f.sw.x), bf16_lo(f.sw.y), bf16_hi(f.sw.y)};
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const v4i bv = {f.x[b].x, f.x[b].y, f.x[b].z, f.x[b].w};
+        const v4i zero = {0, 0, 0, 0};
+        const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bv, zero, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[b][r] = fmaf((float)d[r] * f.sx[b], ws[r], acc[b][r]);
+    }
+}
+
+// P chunks in flight per wave: a register ring of P stages, unrolled so that each stage
+// is a fixed set of registers (no copies, so the compiler's load waits count only the
+// stages issued after the one consumed).  Stage i holds chunks i, i + P, i + 2P, ...;
+// fetches past the last chunk re-read the last chunk and are never consumed.
+template <int NB, int P>
 __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const int stripe = (int)blockIdx.x * 4 + (int)wave;
@@ -88,37 +124,27 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
     const uint32_t a_off = lg * 128u + (li >> 2) * 32u + 4u * (li & 3u);
     const uint32_t s_off = (is_tail ? 0u : side * 32u) + 8u * lg;  // rows 4lg .. 4lg+3
     const uint32_t nib0 = is_tail ? 32u : 64u + side * 512u;
-    int tok[NB];
-#pragma unroll
-    for (int b = 0; b < NB; b++) tok[b] = min(tokb + 16 * b + (int)li, A.ntok - 1);
+    const int tb0 = (int)blockIdx.y * NB;
     float acc[NB][4];
 #pragma unroll
     for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[b][r] = 0.0f;
-    MfChunk<NB> cur, nxt;
-    mf_fetch<NB>(A, mbase, is_tail, nib0, a_off, s_off, tok, lg, 0, cur);
-    for (int c = 0; c < A.nc; c++) {
-        if (c + 1 < A.nc) mf_fetch<NB>(A, mbase, is_tail, nib0, a_off, s_off, tok, lg, c + 1, nxt);
-        v4i a;
-        a[0] = (int)nf4_xlut(cur.d0 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
-        a[1] = (int)nf4_xlut((cur.d0 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
-        a[2] = (int)nf4_xlut(cur.d1 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
-        a[3] = (int)nf4_xlut((cur.d1 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
-        const float ws[4] = {bf16_lo(cur.sw.x), bf16_hi(cur.sw.x), bf16_lo(cur.sw.y), bf16_hi(cur.sw.y)};
+    const int nc = A.nc, last = nc - 1;
+    MfChunk<NB> ring[P];
 #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            const v4i bv = {cur.x[b].x, cur.x[b].y, cur.x[b].z, cur.x[b].w};
-            const v4i zero = {0, 0, 0, 0};
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bv, zero, 0, 0, 0);
-            const float sx = cur.sx[b];
-            const bool on = sx != 0.0f;
+    for (int i = 0; i < P; i++) mf_fetch<NB>(A, mbase, is_tail, nib0, a_off, s_off, tb0, lane, min(i, last), ring[i]);
+    int c0 = 0;
+    for (; c0 + P <= nc; c0 += P) {
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                acc[b][r] = fmaf(on ? (float)d[r] * sx : -0.0f, on ? ws[r] : 0.0f, acc[b][r]);
+        for (int i = 0; i < P; i++) {
+            mf_step<NB>(A, ring[i], acc);
+            mf_fetch<NB>(A, mbase, is_tail, nib0, a_off, s_off, tb0, lane, min(c0 + P + i, last), ring[i]);
         }
-        cur = nxt;
     }
+#pragma unroll
+    for (int i = 0; i < P - 1; i++)
+        if (c0 + i < nc) mf_step<NB>(A, ring[i], acc);
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         const int t = tokb + 16 * b + (int)li;
@@ -131,6 +157,22 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
             *o = A.accum ? *o + acc[b][r] : acc[b][r];
         }
     }
+}
+
+// Tile-major copy of the activations: one 16-token x 64-column tile per 1 KB, in the
+// order the MFMA's B operand is read (lane l = 16g + t holds token t's columns 16g ..
+// 16g + 15), so each B load of a wave is 1 KB contiguous.  Tokens past ntok repeat the
+// last token.  One thread per 16 bytes; blockIdx.y is the 16-token block.
+__global__ __launch_bounds__(256) void mf_tile_kernel(const int8_t *xq, const float *xs, int K, int nc, int ntok,
+                                                      int8_t *xt, float *st) {
+    const int c = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), tb = (int)blockIdx.y;
+    if (c >= nc) return;
+    const uint32_t lane = threadIdx.x & 63u, li = lane & 15u, lg = lane >> 4;
+    const int tok = min(tb * 16 + (int)li, ntok - 1);
+    const size_t tile = (size_t)tb * nc + c;
+    *reinterpret_cast<int4 *>(xt + tile * 1024 + lane * 16) =
+        *reinterpret_cast<const int4 *>(xq + (size_t)tok * K + (size_t)c * 64 + 16 * lg);
+    if (lg == 0) st[tile * 16 + li] = xs[(size_t)tok * nc + c];
 }
 
 }  // namespace
@@ -152,21 +194,33 @@ void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, cons
     A.stripes = m->stripes;
     A.sgc = m->sgc;
     nf4_xor_tables(m->cb[0], m->cb[1], m->cb[2], m->cb[3], A.t0, A.t1, A.u0, A.u1);
-    A.xq = xq;
-    A.xs = xs;
+    // The tiles live in the context's scratch: 1 KB + 64 B per tile.
+    const int blocks = (ntok + 15) / 16;
+    const size_t tiles = (size_t)blocks * m->nc;
+    ensure_scratch(ctx, tiles * (1024 + 64) / sizeof(float));
+    int8_t *xt = reinterpret_cast<int8_t *>(ctx->scratch);
+    float *stile = ctx->scratch + tiles * 256;
+    hipLaunchKernelGGL(mf_tile_kernel, dim3((m->nc + 3) / 4, blocks), dim3(256), 0, ctx->stream, xq, xs, m->cols,
+                       m->nc, ntok, xt, stile);
+    A.xt = xt;
+    A.nblk = blocks;
+    A.st = stile;
     A.K = m->cols;
     A.ntok = ntok;
     A.out = out;
     A.out_stride = out_stride;
     A.accum = accum ? 1 : 0;
-    const int nb = std::min(4, (ntok + 15) / 16);
+    // Tokens per wave: the most 16-token blocks (fewest weight passes) that still give
+    // the launch kMfmaMinWaves waves.
+    int nb = std::min(4, blocks);
+    while (nb > 1 && (long)m->stripes * ((blocks + nb - 1) / nb) < kMfmaMinWaves) nb = nb > 2 ? 2 : 1;
     const dim3 grid((m->stripes + 3) / 4, (ntok + 16 * nb - 1) / (16 * nb));
     hipStream_t st = ctx->stream;
     switch (nb) {
-        case 1: hipLaunchKernelGGL(gemm_nf4_mfma_kernel<1>, grid, dim3(256), 0, st, A); break;
-        case 2: hipLaunchKernelGGL(gemm_nf4_mfma_kernel<2>, grid, dim3(256), 0, st, A); break;
-        case 3: hipLaunchKernelGGL(gemm_nf4_mfma_kernel<3>, grid, dim3(256), 0, st, A); break;
-        default: hipLaunchKernelGGL(gemm_nf4_mfma_kernel<4>, grid, dim3(256), 0, st, A); break;
+        case 1: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<1, kMfmaDepth>), grid, dim3(256), 0, st, A); break;
+        case 2: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<2, kMfmaDepth>), grid, dim3(256), 0, st, A); break;
+        case 3: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<3, kMfmaDepth>), grid, dim3(256), 0, st, A); break;
+        default: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<4, kMfmaDepth>), grid, dim3(256), 0, st, A); break;
     }
     hip_check(hipGetLastError(), "mfma gemm launch");
 }
