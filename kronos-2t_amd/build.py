@@ -31,6 +31,10 @@ FLAGS = [
     "-Rpass-analysis=kernel-resource-usage",
 ]
 
+# Extra flags of single sources.  The MFMA kernel's results feed VALU epilogues: with
+# the VGPR form its MFMAs write ordinary VGPRs (no accumulator-register reads).
+FILE_FLAGS = {"k2t_gemm_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 # Mangled-name prefixes of kernels that must compile without scratch memory.
 NO_SCRATCH = ("_ZN3k2t12_GLOBAL__N_116decode_mk_kernel",)
 
@@ -56,7 +60,8 @@ def sources():
 
 def _compile(src, objdir=None, defines=()):
     obj = os.path.join(objdir or OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, *[f"-D{d}" for d in defines], "-c", src, "-o", obj]
+    extra = FILE_FLAGS.get(os.path.basename(src), [])
+    cmd = [HIPCC, *FLAGS, *extra, *[f"-D{d}" for d in defines], "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
@@ -77,8 +82,8 @@ def check_m0(src, objdir=None, defines=()):
     and the LDS counters, so its wait also waits for every global load and store the wave
     has in flight, the weight prefetches included."""
     asm = os.path.join(objdir or OBJ, os.path.basename(src) + ".s")
-    cmd = [HIPCC, *[f for f in FLAGS if not f.startswith("-Rpass")], *[f"-D{d}" for d in defines],
-           "--cuda-device-only", "-S", src, "-o", asm]
+    cmd = [HIPCC, *[f for f in FLAGS if not f.startswith("-Rpass")], *FILE_FLAGS.get(os.path.basename(src), []),
+           *[f"-D{d}" for d in defines], "--cuda-device-only", "-S", src, "-o", asm]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc -S failed for {src}:\n{r.stderr}")

@@ -31,7 +31,7 @@ void launch_attention_exact(hipStream_t st, const float *q, int q_stride, const 
 void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale, int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as,
-                      int32_t *asum, const GqaWork &gqa);
+                      int32_t *asum, const GqaWork &gqa, int ctx_bound = 0);
 int attn_max_splits(int max_seq);
 int gqa_spans(int cap);
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
@@ -360,7 +360,9 @@ void forward_exact(k2t_model *m, int ntok, bool with_logits) {
 
 // One forward pass over `ntok` tokens already in m->tokens, positions pos..pos+ntok-1.
 // Logits (of the last token) go to m->logits; the device position advances by ntok.
-void forward(k2t_model *m, int ntok, bool with_logits) {
+// ctx_bound: the position after the batch's last token when the host knows it (prefill;
+// never a captured step, whose position moves between replays), else 0.
+void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
     if (m->exact) {
         forward_exact(m, ntok, with_logits);
         return;
@@ -397,7 +399,7 @@ void forward(k2t_model *m, int ntok, bool with_logits) {
         }
         launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, post, m->pos_dev, l, nq, nkv,
                          hd, m->ring, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum,
-                         GqaWork{m->attn_words, m->attn_cnt, m->err_dev});
+                         GqaWork{m->attn_words, m->attn_cnt, m->err_dev}, ctx_bound);
         launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
         if (L.has_moe) {
             // one token at a time: each token has its own routes (forward_layer_single)
@@ -1099,7 +1101,7 @@ int32_t k2t_model_prefill(k2t_model *m, const int32_t *tokens, int32_t n, float 
             const int nb = std::min(chunk, n - i0);
             hip_check(hipMemcpyAsync(m->tokens, tokens + i0, nb * sizeof(int), hipMemcpyHostToDevice, m->stream),
                       "token upload");
-            forward(m, nb, i0 + nb == n);
+            forward(m, nb, i0 + nb == n, m->pos + i0 + nb);
             // the token buffer is reused by the next chunk: wait for this one
             hip_check(hipStreamSynchronize(m->stream), "sync");
         }

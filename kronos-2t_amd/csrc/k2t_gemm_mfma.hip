@@ -43,11 +43,13 @@ constexpr int kMfmaDepth = K2T_MFMA_DEPTH;         // chunks in flight per wave
 constexpr long kMfmaMinWaves = K2T_MFMA_MIN_WAVES;  // 8 waves per CU
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 struct MfArgs {
     const uint8_t *pair, *tail;
     size_t ptot;  // bytes per pair stream
-    int rows, nc, np, stripes, sgc;
+    int rows, nc, np, stripes, sgc_log2;  // scale group = 1 << sgc_log2 chunks
     uint32_t t0, t1, u0, u1;  // NF4 codebook XOR tables (nf4_xor_tables)
     const int8_t *xt;  // activations tile-major: [16-token block][chunk][64 lanes][16 bytes]
     const float *st;   // their scales: [16-token block][chunk][16 tokens]
@@ -66,22 +68,40 @@ struct MfChunk {
     float sx[NB];
 };
 
+// Buffer resource of a wave-uniform base (raw, no stride; dword 3 as gfx950 wants it).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mf_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7FFFFFFF, 0x00020000);
+}
+
+struct MfSrc {
+    __amdgpu_buffer_rsrc_t w, x, s;  // the stripe's pair stream (or the tail), the tiles, their scales
+};
+
+// Every load is a buffer load: the wave-uniform part of its offset in an SGPR, the
+// per-lane part (fixed for the wave's life) in one VGPR, so no 64-bit address adds.
 template <int NB>
-__device__ __forceinline__ void mf_fetch(const MfArgs &A, const uint8_t *mbase, bool is_tail, uint32_t nib0,
-                                         uint32_t a_off, uint32_t s_off, int tb0, uint32_t lane, int c,
-                                         MfChunk<NB> &f) {
-    const int sg = c / A.sgc, cst = sg * A.sgc, sb = c - cst;
-    const size_t cs = is_tail ? 512 : 1024;
-    const uint8_t *gb = mbase + (size_t)sg * (is_tail ? 32 : 64) + (size_t)cst * cs;
-    const uint8_t *rec = gb + nib0 + (size_t)sb * cs;
-    f.d0 = *reinterpret_cast<const uint32_t *>(rec + a_off);
-    f.d1 = *reinterpret_cast<const uint32_t *>(rec + a_off + 16);
-    f.sw = *reinterpret_cast<const uint2 *>(gb + s_off);
+__device__ __forceinline__ void mf_fetch(const MfArgs &A, const MfSrc &R, bool is_tail, uint32_t nib0,
+                                         uint32_t a_off, uint32_t s_off, uint32_t x_off, uint32_t sx_off, int tb0,
+                                         int c, MfChunk<NB> &f) {
+    const uint32_t sg = (uint32_t)c >> A.sgc_log2, sb = (uint32_t)c - (sg << A.sgc_log2);
+    const uint32_t cs = is_tail ? 512u : 1024u;
+    const uint32_t gb = sg * (is_tail ? 32u : 64u) + (sg << A.sgc_log2) * cs;  // scale-group base
+    const uint32_t rec = gb + nib0 + sb * cs;
+    f.d0 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(R.w, a_off, rec, 0);
+    f.d1 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(R.w, a_off + 16u, rec, 0);
+    const v2u sw = __builtin_amdgcn_raw_buffer_load_b64(R.w, s_off, gb, 0);
+    f.sw = make_uint2(sw[0], sw[1]);
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-        const size_t tile = (size_t)min(tb0 + b, A.nblk - 1) * A.nc + c;  // blocks past the last: never stored
-        f.x[b] = *reinterpret_cast<const int4 *>(A.xt + tile * 1024 + lane * 16);
-        f.sx[b] = A.st[tile * 16 + (lane & 15u)];
+        // blocks past the last repeat it; their outputs are never stored
+#ifdef K2T_MF_EXP_BSAME
+        const uint32_t tile = (uint32_t)min(tb0 + b, A.nblk - 1) * (uint32_t)A.nc;  // measurement only: wrong sums
+#else
+        const uint32_t tile = (uint32_t)min(tb0 + b, A.nblk - 1) * (uint32_t)A.nc + (uint32_t)c;
+#endif
+        const v4u x = __builtin_amdgcn_raw_buffer_load_b128(R.x, x_off, tile * 1024u, 0);
+        f.x[b] = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
+        f.sx[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(R.s, sx_off, tile * 64u, 0));
     }
 }
 
@@ -113,7 +133,8 @@ __device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<NB> &f, f
 // fetches past the last chunk re-read the last chunk and are never consumed.
 template <int NB, int P>
 __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: stripe math on SGPRs
     const int stripe = (int)blockIdx.x * 4 + (int)wave;
     if (stripe >= A.stripes) return;  // whole waves; the kernel has no barrier
     const int tokb = (int)blockIdx.y * 16 * NB;
@@ -124,6 +145,8 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
     const uint32_t a_off = lg * 128u + (li >> 2) * 32u + 4u * (li & 3u);
     const uint32_t s_off = (is_tail ? 0u : side * 32u) + 8u * lg;  // rows 4lg .. 4lg+3
     const uint32_t nib0 = is_tail ? 32u : 64u + side * 512u;
+    const MfSrc R{mf_rsrc(mbase), mf_rsrc(A.xt), mf_rsrc(A.st)};
+    const uint32_t x_off = lane * 16u, sx_off = li * 4u;
     const int tb0 = (int)blockIdx.y * NB;
     float acc[NB][4];
 #pragma unroll
@@ -133,13 +156,13 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
     const int nc = A.nc, last = nc - 1;
     MfChunk<NB> ring[P];
 #pragma unroll
-    for (int i = 0; i < P; i++) mf_fetch<NB>(A, mbase, is_tail, nib0, a_off, s_off, tb0, lane, min(i, last), ring[i]);
+    for (int i = 0; i < P; i++) mf_fetch<NB>(A, R, is_tail, nib0, a_off, s_off, x_off, sx_off, tb0, min(i, last), ring[i]);
     int c0 = 0;
     for (; c0 + P <= nc; c0 += P) {
 #pragma unroll
         for (int i = 0; i < P; i++) {
             mf_step<NB>(A, ring[i], acc);
-            mf_fetch<NB>(A, mbase, is_tail, nib0, a_off, s_off, tb0, lane, min(c0 + P + i, last), ring[i]);
+            mf_fetch<NB>(A, R, is_tail, nib0, a_off, s_off, x_off, sx_off, tb0, min(c0 + P + i, last), ring[i]);
         }
     }
 #pragma unroll
@@ -178,7 +201,8 @@ __global__ __launch_bounds__(256) void mf_tile_kernel(const int8_t *xq, const fl
 }  // namespace
 
 bool gemm_nf4_mfma_supported(const k2t_mat *m, int ntok) {
-    return m->fmt == K2T_FMT_NF && m->bits == 4 && ntok >= kMfmaMinTokens && m->cols % 64 == 0;
+    return m->fmt == K2T_FMT_NF && m->bits == 4 && ntok >= kMfmaMinTokens && m->cols % 64 == 0 &&
+           (m->sgc & (m->sgc - 1)) == 0;
 }
 
 void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, int ntok, float *out,
@@ -192,7 +216,7 @@ void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, cons
     A.nc = m->nc;
     A.np = m->pairs;
     A.stripes = m->stripes;
-    A.sgc = m->sgc;
+    A.sgc_log2 = __builtin_ctz((unsigned)m->sgc);
     nf4_xor_tables(m->cb[0], m->cb[1], m->cb[2], m->cb[3], A.t0, A.t1, A.u0, A.u1);
     // The tiles live in the context's scratch: 1 KB + 64 B per tile.
     const int blocks = (ntok + 15) / 16;

@@ -260,6 +260,9 @@ constexpr int kAttnSplitLen = 256;
 // over every position, and that workgroup also writes the o_proj activation (FINAL): no
 // merge kernel.
 constexpr int kAttnWhole = 1024;
+// Batches whose every token attends to at most this many positions (prefill of a short
+// prompt) run a kAttnSmall-thread version of the whole-context kernel.
+constexpr int kAttnSmall = 256;
 // Span merges over at most this many spans issue all their loads at once.
 constexpr int kMergeOneShot = 32;
 
@@ -272,7 +275,10 @@ __device__ __forceinline__ float tree_sum(const float *v, int n) {
     return t[0];
 }
 
-template <int NTH, bool FINAL>
+// VORD >= NTH: the o partial sums use the position subsets of a VORD-thread workgroup
+// (each thread then owns VORD / NTH of them), so a 256-thread launch over at most 256
+// positions gives the 1024-thread kernel's results bit for bit.
+template <int NTH, bool FINAL, int VORD = NTH>
 __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restrict__ q, int q_stride,
                                                            int8_t *__restrict__ kq, int8_t *__restrict__ vq,
                                                            float *__restrict__ ks, float *__restrict__ vs,
@@ -288,7 +294,9 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
     __shared__ float qas_s;
     __shared__ float sc[NTH];
     __shared__ float red[2 * NW];
-    __shared__ float opart[NTH * 4];  // [position subset][column]: (NTH / (hd / 4)) * hd
+    __shared__ float opart[VORD * 4];  // [position subset][column]: (VORD / (hd / 4)) * hd
+    constexpr int SUBS = VORD / NTH;   // position subsets per thread
+    static_assert(VORD % NTH == 0, "VORD must be a multiple of NTH");
     // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs by linear id,
     // so the q heads that share a KV head and a split get ids congruent mod 8 and run on
     // one XCD, where the K/V tile is fetched from HBM once and then hit in that XCD's L2.
@@ -454,11 +462,14 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
     // o partial: thread = (position subset ps, 4-column group cg); a dword of V per
     // position, loads batched 4 deep; the position subsets are added in a fixed order.
     const int n = t1 - t0;
-    const int ncg = hd / 4;           // 16 or 32 column groups
-    const int nps = NTH / ncg;        // position subsets (16 or 8 at 256 threads)
-    const int cg = (int)tid % ncg, ps = (int)tid / ncg;
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    const int ncg = hd / 4;            // 16 or 32 column groups
+    const int nps = VORD / ncg;        // position subsets
+    const int cg = (int)tid % ncg, ps0 = (int)tid / ncg;
     const int8_t *vcol = vq + base * hd + cg * 4;
+#pragma unroll
+    for (int sub = 0; sub < SUBS; sub++) {
+    const int ps = ps0 + sub * (NTH / ncg);
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     int i = ps;
     if (kr.bits == 4) {
         // NF4 V: this thread's 4 columns are one nibble half of 4 bytes of block g
@@ -518,6 +529,7 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
     op[ps * hd + cg * 4 + 1] = a1;
     op[ps * hd + cg * 4 + 2] = a2;
     op[ps * hd + cg * 4 + 3] = a3;
+    }
     __syncthreads();
     if constexpr (FINAL) {
         // One span covers every position: attn_merge_kernel's arithmetic for one split
@@ -525,8 +537,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
         // int8 of the o_proj chunk (populate_chunk_fwht_raw(None), real_llm.rs:7060-7084).
         const float inv = 1.0f / tree_sum(red + NW, NW);
         if (tid < (uint32_t)hd) {
-            float acc = op[tid];
-            for (int k = 1; k < nps; k++) acc += op[k * hd + tid];
+            float acc = opart[tid];
+            for (int k = 1; k < nps; k++) acc += opart[k * hd + tid];
             sc[tid] = acc;  // the scores are no longer needed
         }
         __syncthreads();
@@ -546,8 +558,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
         pp[1] = tree_sum(red + NW, NW);
     }
     if (tid < (uint32_t)hd) {
-        float acc = op[tid];
-        for (int k = 1; k < nps; k++) acc += op[k * hd + tid];
+        float acc = opart[tid];
+        for (int k = 1; k < nps; k++) acc += opart[k * hd + tid];
         pp[2 + tid] = acc;
     }
 }
@@ -1133,7 +1145,16 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale,
                       int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum,
-                      const GqaWork &gqa) {
+                      const GqaWork &gqa, int ctx_bound) {
+    if (nsplit == 1 && ctx_bound > 0 && ctx_bound <= kAttnSmall) {
+        // every token of the batch attends to at most kAttnSmall positions: a quarter of the
+        // threads, the whole-context kernel's sums (its V position subsets) bit for bit
+        hipLaunchKernelGGL((attn_partial_kernel<kAttnSmall, true, kAttnWhole>), dim3(nq, 1, ntok), dim3(kAttnSmall), 0,
+                           st, q, q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part,
+                           out_f, aq, as, asum);
+        hip_check(hipGetLastError(), "attention launch");
+        return;
+    }
     if (nsplit == 1) {  // the caller sized the context within kAttnWhole (attn_max_splits)
         hipLaunchKernelGGL((attn_partial_kernel<kAttnWhole, true>), dim3(nq, 1, ntok), dim3(kAttnWhole), 0, st, q,
                            q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part, out_f,
