@@ -84,8 +84,10 @@ int32_t k2t_ctx_set_exact(k2t_ctx *ctx, int32_t exact);
  * k2t_gemv and the model's prefill): enable = 1 (default) runs them on the int8 matrix
  * cores, one weight pass per 64 tokens, with outputs equal to the exact-order epilogue's
  * in either mode; 0 runs the 4-token weight passes of nf_sdot_decode_neon's tile
- * (simd_lut.rs:6074-6364).  A backend choice of this build; the reference has no
- * counterpart. */
+ * (simd_lut.rs:6074-6364).  2: matrix cores, but a model's prefill does not have the
+ * activation's producer write the tile-major copy the GEMV reads (the GEMV copies it
+ * itself); same outputs as 1, for checking.  A backend choice of this build; the
+ * reference has no counterpart.  K2T_E_ARG for other values. */
 int32_t k2t_ctx_set_mfma(k2t_ctx *ctx, int32_t enable);
 
 /* ---- device memory helpers (tests, benches, non-torch callers) ---------- */

@@ -294,7 +294,8 @@ int32_t k2t_ctx_set_exact(k2t_ctx *ctx, int32_t exact) {
 int32_t k2t_ctx_set_mfma(k2t_ctx *ctx, int32_t enable) {
     return guarded([&] {
         arg_check(ctx != nullptr, "ctx is NULL");
-        ctx->mfma = enable ? 1 : 0;
+        arg_check(enable >= 0 && enable <= 2, "mfma mode must be 0, 1 or 2");
+        ctx->mfma = enable;
     });
 }
 

@@ -20,7 +20,7 @@
 
 namespace k2t {
 void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float eps, int K, int ntok, int8_t *q,
-                        float *s, int32_t *sums);
+                        float *s, int32_t *sums, ActTiles tiles = ActTiles{});
 void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
                      const float *rope, const int *pos_dev, int nq,
                      int nkv, int hd, int ntok, int layer, KvRing kr, int8_t *kq, int8_t *vq, float *ks, float *vs,
@@ -31,11 +31,9 @@ void launch_attention_exact(hipStream_t st, const float *q, int q_stride, const 
 void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale, int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as,
-                      int32_t *asum, const GqaWork &gqa, int ctx_bound = 0);
+                      int32_t *asum, const GqaWork &gqa, int ctx_bound = 0, ActTiles tiles = ActTiles{});
 int attn_max_splits(int max_seq);
 int gqa_spans(int cap);
-void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
-                       bool exact);
 void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok, float *out);
 void launch_kv_synthetic(hipStream_t st, int8_t *kq, int8_t *vq, float *ks, float *vs, int layers_kv, int cap,
                          int n_pos, int hd, int bits, uint64_t seed);
@@ -229,6 +227,9 @@ struct k2t_model {
     int8_t *xq = nullptr;
     float *xs = nullptr;
     int32_t *xsum = nullptr;
+    // the activation's tile-major copy for matrix-core GEMVs (written by its producer)
+    int8_t *xt = nullptr;
+    float *st = nullptr;
     int pos = 0;
     bool use_graph = true;
     // 1: exact-order steps (the x86 reference's operation order throughout: in-order GEMV
@@ -358,6 +359,12 @@ void forward_exact(k2t_model *m, int ntok, bool with_logits) {
     launch_advance_pos(st, m->pos_dev, ntok);
 }
 
+// Where the producer of the activation of `w` writes the tile-major copy: the model's
+// tile buffers when that GEMV runs on the matrix cores, else nowhere.
+ActTiles act_tiles_for(const k2t_model *m, const k2t_mat *w, int ntok) {
+    return m->ctx->mfma == 1 && gemm_nf4_mfma_supported(w, ntok) ? ActTiles{m->xt, m->st} : ActTiles{};
+}
+
 // One forward pass over `ntok` tokens already in m->tokens, positions pos..pos+ntok-1.
 // Logits (of the last token) go to m->logits; the device position advances by ntok.
 // ctx_bound: the position after the batch's last token when the host knows it (prefill;
@@ -385,8 +392,10 @@ void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
         if (fused) {
             launch_gemv_fused(ctx, L.qkv, K2T_XS_RMSNORM, m->hidden, L.in_norm, c.rms_eps, m->qkv, false);
         } else {
-            launch_rmsnorm_act(st, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
-            launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false);
+            const ActTiles tq = act_tiles_for(m, L.qkv, ntok);
+            launch_rmsnorm_act(st, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum, tq);
+            launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false, 0,
+                           tq);
         }
         // One token: qkv_post's work runs inside the attention kernel.  A batch stores every
         // token's K / V first (a later token of the batch attends to them).
@@ -397,10 +406,11 @@ void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
             launch_qkv_post(st, m->qkv, L.bias, L.q_norm, L.k_norm, c.rms_eps, m->rope, m->pos_dev, nq, nkv, hd, ntok,
                             l, m->ring, m->kq, m->vq, m->ks, m->vs, false);
         }
+        const ActTiles to = act_tiles_for(m, L.o, ntok);  // (none for one token: the grouped kernel writes none)
         launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, post, m->pos_dev, l, nq, nkv,
                          hd, m->ring, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum,
-                         GqaWork{m->attn_words, m->attn_cnt, m->err_dev}, ctx_bound);
-        launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
+                         GqaWork{m->attn_words, m->attn_cnt, m->err_dev}, ctx_bound, to);
+        launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true, 0, to);
         if (L.has_moe) {
             // one token at a time: each token has its own routes (forward_layer_single)
             MoeWork ws = moe_work_carve(m->moe_ws, L.moe.bank, L.moe.top_k);
@@ -410,10 +420,11 @@ void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
             launch_gemv_fused(ctx, L.gu, K2T_XS_RMSNORM, m->hidden, L.post_norm, c.rms_eps, m->gu, false);
             launch_gemv_fused(ctx, L.down, K2T_XS_SWIGLU, m->gu, nullptr, 0.0f, m->hidden, true);
         } else {
-            launch_rmsnorm_act(st, m->hidden, L.post_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum);
-            launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false);
-            launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum, false);
-            launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
+            const ActTiles tg = act_tiles_for(m, L.gu, ntok), td = act_tiles_for(m, L.down, ntok);
+            launch_rmsnorm_act(st, m->hidden, L.post_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum, tg);
+            launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false, 0, tg);
+            launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum, false, td);
+            launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true, 0, td);
         }
     }
     if (with_logits) {
@@ -732,6 +743,9 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             m->xq = (int8_t *)dalloc(m, (size_t)max_batch * kmax);
             m->xs = (float *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(float));
             m->xsum = (int32_t *)dalloc(m, (size_t)max_batch * (kmax / 64) * sizeof(int32_t));
+            const size_t ntile = (size_t)((max_batch + 15) / 16) * (kmax / 64);
+            m->xt = (int8_t *)dalloc(m, ntile * 1024);
+            m->st = (float *)dalloc(m, ntile * 16 * sizeof(float));
             // persistent decode kernel state
             // the persistent kernel's phases assume the megakernel shape q_dim == hidden
             m->mk_ok = decode_mk_supported(c, ctx->num_cus) && c.n_heads * c.head_dim == c.hidden;

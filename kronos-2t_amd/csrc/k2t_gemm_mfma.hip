@@ -39,7 +39,7 @@ namespace {
 #ifndef K2T_MFMA_MIN_WAVES
 #define K2T_MFMA_MIN_WAVES 2048
 #endif
-constexpr int kMfmaDepth = K2T_MFMA_DEPTH;         // chunks in flight per wave
+constexpr int kMfmaDepth = K2T_MFMA_DEPTH;         // chunks in flight per wave (unshared kernels)
 constexpr long kMfmaMinWaves = K2T_MFMA_MIN_WAVES;  // 8 waves per CU
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -59,12 +59,13 @@ struct MfArgs {
     int accum;
 };
 
-// Everything one chunk needs (one ring stage).
-template <int NB>
+// Everything one chunk needs (one ring stage): the stripe-chunk's codes and scales, the
+// activation blocks this wave loads (all NB, or with sharing its own one), their scales.
+template <int NB, bool SH>
 struct MfChunk {
     uint32_t d0, d1;
     uint2 sw;
-    int4 x[NB];
+    int4 x[SH ? 1 : NB];
     float sx[NB];
 };
 
@@ -79,10 +80,10 @@ struct MfSrc {
 
 // Every load is a buffer load: the wave-uniform part of its offset in an SGPR, the
 // per-lane part (fixed for the wave's life) in one VGPR, so no 64-bit address adds.
-template <int NB>
+template <int NB, bool SH>
 __device__ __forceinline__ void mf_fetch(const MfArgs &A, const MfSrc &R, bool is_tail, uint32_t nib0,
                                          uint32_t a_off, uint32_t s_off, uint32_t x_off, uint32_t sx_off, int tb0,
-                                         int c, MfChunk<NB> &f) {
+                                         uint32_t wave, int c, MfChunk<NB, SH> &f) {
     const uint32_t sg = (uint32_t)c >> A.sgc_log2, sb = (uint32_t)c - (sg << A.sgc_log2);
     const uint32_t cs = is_tail ? 512u : 1024u;
     const uint32_t gb = sg * (is_tail ? 32u : 64u) + (sg << A.sgc_log2) * cs;  // scale-group base
@@ -99,8 +100,10 @@ __device__ __forceinline__ void mf_fetch(const MfArgs &A, const MfSrc &R, bool i
 #else
         const uint32_t tile = (uint32_t)min(tb0 + b, A.nblk - 1) * (uint32_t)A.nc + (uint32_t)c;
 #endif
-        const v4u x = __builtin_amdgcn_raw_buffer_load_b128(R.x, x_off, tile * 1024u, 0);
-        f.x[b] = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
+        if (!SH || b == (int)wave) {  // with sharing, waves >= NB load no block
+            const v4u x = __builtin_amdgcn_raw_buffer_load_b128(R.x, x_off, tile * 1024u, 0);
+            f.x[SH ? 0 : b] = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
+        }
         f.sx[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(R.s, sx_off, tile * 64u, 0));
     }
 }
@@ -109,8 +112,17 @@ __device__ __forceinline__ void mf_fetch(const MfArgs &A, const MfSrc &R, bool i
 // needs no select: its term float(d) * 0 * ws is +-0, and adding +-0 leaves every
 // accumulator unchanged (each starts at +0 and a round-to-nearest sum is -0 only when
 // both addends are -0, so no accumulator is ever -0).
-template <int NB>
-__device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<NB> &f, float (&acc)[NB][4]) {
+// With sharing, `bsh` is this chunk's LDS slot ([NB][64 lanes] of 16 bytes): the waves
+// that loaded a block store it, one barrier, then every wave reads every block.  Two
+// slots alternate: a wave stores into a slot only after the barrier that all waves
+// passed once done reading it.
+template <int NB, bool SH>
+__device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<NB, SH> &f, float (&acc)[NB][4], int4 *bsh,
+                                        uint32_t wave, uint32_t lane) {
+    if (SH) {
+        if (wave < (uint32_t)NB) bsh[wave * 64 + lane] = f.x[0];
+        __syncthreads();
+    }
     v4i a;
     a[0] = (int)nf4_xlut(f.d0 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
     a[1] = (int)nf4_xlut((f.d0 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
@@ -119,7 +131,8 @@ __device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<NB> &f, f
     const float ws[4] = {bf16_lo(f.sw.x), bf16_hi(f.sw.x), bf16_lo(f.sw.y), bf16_hi(f.sw.y)};
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-        const v4i bv = {f.x[b].x, f.x[b].y, f.x[b].z, f.x[b].w};
+        const int4 xb = SH ? bsh[b * 64 + lane] : f.x[b];
+        const v4i bv = {xb.x, xb.y, xb.z, xb.w};
         const v4i zero = {0, 0, 0, 0};
         const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bv, zero, 0, 0, 0);
 #pragma unroll
@@ -131,12 +144,21 @@ __device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<NB> &f, f
 // is a fixed set of registers (no copies, so the compiler's load waits count only the
 // stages issued after the one consumed).  Stage i holds chunks i, i + P, i + 2P, ...;
 // fetches past the last chunk re-read the last chunk and are never consumed.
-template <int NB, int P>
+//
+// SH: the waves of a workgroup share their tokens' activation blocks through LDS (wave
+// w < NB loads block w; one barrier per chunk) instead of each loading all NB.  Measured
+// (256 tokens): 16384 x 2048 at NB 4, 45.7 -> 40.4 us with P 2; 2048 x 8192 at NB 1,
+// 36.9 -> 44-49 us (one loader and a barrier per chunk for 128 chunks): on for NB 4 only.
+template <int NB, int P, bool SH>
 __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: stripe math on SGPRs
-    const int stripe = (int)blockIdx.x * 4 + (int)wave;
-    if (stripe >= A.stripes) return;  // whole waves; the kernel has no barrier
+    const int stripe_id = (int)blockIdx.x * 4 + (int)wave;
+    // With sharing every wave takes part in every barrier: a wave past the last stripe
+    // runs the last stripe's chunks and stores nothing.
+    if (!SH && stripe_id >= A.stripes) return;
+    const int stripe = min(stripe_id, A.stripes - 1);
+    __shared__ int4 bsh[2][SH ? NB * 64 : 1];
     const int tokb = (int)blockIdx.y * 16 * NB;
     const bool is_tail = stripe >= 2 * A.np;
     const uint32_t side = is_tail ? 0u : (uint32_t)(stripe & 1);
@@ -153,21 +175,23 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
     for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[b][r] = 0.0f;
+    static_assert(!SH || P % 2 == 0, "the LDS slot of chunk c0 + i is i & 1 (c0 a multiple of P)");
     const int nc = A.nc, last = nc - 1;
-    MfChunk<NB> ring[P];
+    MfChunk<NB, SH> ring[P];
 #pragma unroll
-    for (int i = 0; i < P; i++) mf_fetch<NB>(A, R, is_tail, nib0, a_off, s_off, x_off, sx_off, tb0, min(i, last), ring[i]);
+    for (int i = 0; i < P; i++) mf_fetch<NB, SH>(A, R, is_tail, nib0, a_off, s_off, x_off, sx_off, tb0, wave, min(i, last), ring[i]);
     int c0 = 0;
     for (; c0 + P <= nc; c0 += P) {
 #pragma unroll
         for (int i = 0; i < P; i++) {
-            mf_step<NB>(A, ring[i], acc);
-            mf_fetch<NB>(A, R, is_tail, nib0, a_off, s_off, x_off, sx_off, tb0, min(c0 + P + i, last), ring[i]);
+            mf_step<NB, SH>(A, ring[i], acc, bsh[i & 1], wave, lane);  // chunk c0 + i
+            mf_fetch<NB, SH>(A, R, is_tail, nib0, a_off, s_off, x_off, sx_off, tb0, wave, min(c0 + P + i, last), ring[i]);
         }
     }
 #pragma unroll
     for (int i = 0; i < P - 1; i++)
-        if (c0 + i < nc) mf_step<NB>(A, ring[i], acc);
+        if (c0 + i < nc) mf_step<NB, SH>(A, ring[i], acc, bsh[i & 1], wave, lane);
+    if (stripe_id >= A.stripes) return;
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         const int t = tokb + 16 * b + (int)li;
@@ -206,7 +230,7 @@ bool gemm_nf4_mfma_supported(const k2t_mat *m, int ntok) {
 }
 
 void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, int ntok, float *out,
-                          size_t out_stride, bool accum) {
+                          size_t out_stride, bool accum, ActTiles tiles) {
     if (!gemm_nf4_mfma_supported(m, ntok)) throw Error(K2T_E_INTERNAL, "mfma gemm: unsupported matrix");
     MfArgs A{};
     A.pair = m->pair;
@@ -218,14 +242,19 @@ void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, cons
     A.stripes = m->stripes;
     A.sgc_log2 = __builtin_ctz((unsigned)m->sgc);
     nf4_xor_tables(m->cb[0], m->cb[1], m->cb[2], m->cb[3], A.t0, A.t1, A.u0, A.u1);
-    // The tiles live in the context's scratch: 1 KB + 64 B per tile.
+    // The tile-major copy: from the activation's producer, else made here in the
+    // context's scratch (1 KB + 64 B per tile).
     const int blocks = (ntok + 15) / 16;
-    const size_t tiles = (size_t)blocks * m->nc;
-    ensure_scratch(ctx, tiles * (1024 + 64) / sizeof(float));
-    int8_t *xt = reinterpret_cast<int8_t *>(ctx->scratch);
-    float *stile = ctx->scratch + tiles * 256;
-    hipLaunchKernelGGL(mf_tile_kernel, dim3((m->nc + 3) / 4, blocks), dim3(256), 0, ctx->stream, xq, xs, m->cols,
-                       m->nc, ntok, xt, stile);
+    int8_t *xt = tiles.xt;
+    float *stile = tiles.st;
+    if (!xt) {
+        const size_t ntile = (size_t)blocks * m->nc;
+        ensure_scratch(ctx, ntile * (1024 + 64) / sizeof(float));
+        xt = reinterpret_cast<int8_t *>(ctx->scratch);
+        stile = ctx->scratch + ntile * 256;
+        hipLaunchKernelGGL(mf_tile_kernel, dim3((m->nc + 3) / 4, blocks), dim3(256), 0, ctx->stream, xq, xs, m->cols,
+                           m->nc, ntok, xt, stile);
+    }
     A.xt = xt;
     A.nblk = blocks;
     A.st = stile;
@@ -241,10 +270,10 @@ void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, cons
     const dim3 grid((m->stripes + 3) / 4, (ntok + 16 * nb - 1) / (16 * nb));
     hipStream_t st = ctx->stream;
     switch (nb) {
-        case 1: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<1, kMfmaDepth>), grid, dim3(256), 0, st, A); break;
-        case 2: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<2, kMfmaDepth>), grid, dim3(256), 0, st, A); break;
-        case 3: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<3, kMfmaDepth>), grid, dim3(256), 0, st, A); break;
-        default: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<4, kMfmaDepth>), grid, dim3(256), 0, st, A); break;
+        case 1: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<1, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
+        case 2: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<2, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
+        case 3: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<3, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
+        default: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<4, 2, true>), grid, dim3(256), 0, st, A); break;
     }
     hip_check(hipGetLastError(), "mfma gemm launch");
 }

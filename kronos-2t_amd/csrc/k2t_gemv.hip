@@ -915,7 +915,7 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
                              const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
                              int32_t *dots, bool accum, int xsm = 0, const float *src = nullptr,
                              const float *w = nullptr, float eps = 0.0f, const GemvGroup *grp = nullptr,
-                             int gu_split = 0);
+                             int gu_split = 0, ActTiles tiles = ActTiles{});
 
 void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                  const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
@@ -924,9 +924,9 @@ void launch_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *
 }
 
 void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum, int ntok,
-                    float *out, size_t out_stride, bool accumulate, int gu_split) {
+                    float *out, size_t out_stride, bool accumulate, int gu_split, ActTiles tiles) {
     launch_gemv_impl(ctx, m, xq, xs, xsum, ntok, 0, m->stripes, out, out_stride, nullptr, accumulate, 0, nullptr,
-                     nullptr, 0.0f, nullptr, gu_split);
+                     nullptr, 0.0f, nullptr, gu_split, tiles);
 }
 
 void launch_gemv_fused(k2t_ctx *ctx, const k2t_mat *m, int xs_mode, const float *src, const float *w, float eps,
@@ -948,12 +948,12 @@ void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, 
 static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs,
                              const int32_t *xsum, int ntok, int s0, int s1, float *out, size_t out_stride,
                              int32_t *dots, bool accum, int xsm, const float *src, const float *w, float eps,
-                             const GemvGroup *grp, int gu_split) {
+                             const GemvGroup *grp, int gu_split, ActTiles tiles) {
     // 16 or more tokens of a ready activation through an NF4 matrix: the matrix-core
     // kernel (one weight pass per 64 tokens; its outputs equal the exact-order GEMV's)
     if (!dots && !grp && xsm == 0 && gu_split == 0 && s0 == 0 && s1 == m->stripes && ctx->mfma &&
         gemm_nf4_mfma_supported(m, ntok)) {
-        launch_gemm_nf4_mfma(ctx, m, xq, xs, ntok, out, out_stride, accum);
+        launch_gemm_nf4_mfma(ctx, m, xq, xs, ntok, out, out_stride, accum, tiles);
         return;
     }
     const int saved = ctx->max_segments;

@@ -122,7 +122,8 @@ __device__ __forceinline__ void kv_store_head(float r0, float r1, int nb, uint32
 // runs populate_rmsnorm_fwht (simd_lut.rs:2970-2997) on its own chunk.
 __global__ __launch_bounds__(64) void rmsnorm_act_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                                          float eps, int K, int8_t *__restrict__ q,
-                                                         float *__restrict__ scales, int32_t *__restrict__ sums) {
+                                                         float *__restrict__ scales, int32_t *__restrict__ sums,
+                                                         ActTiles tiles) {
     const uint32_t lane = threadIdx.x;
     const int c = blockIdx.x, tok = blockIdx.y;
     const float *xt = x + (size_t)tok * K;
@@ -130,12 +131,13 @@ __global__ __launch_bounds__(64) void rmsnorm_act_kernel(const float *__restrict
     const float inv_rms = 1.0f / sqrtf(ss / (float)K + eps);
     const float v = (xt[c * 64 + lane] * inv_rms) * w[c * 64 + lane];
     const size_t gc = (size_t)tok * (K / 64) + c;
-    quant_chunk_store(fwht_lane(v, (uint64_t)c, lane), lane, q + gc * 64, scales + gc, sums + gc);
+    quant_chunk_store(fwht_lane(v, (uint64_t)c, lane), lane, q + gc * 64, scales + gc, sums + gc, tiles.xt, tiles.st,
+                      tok, c, K / 64);
 }
 
 void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float eps, int K, int ntok, int8_t *q,
-                        float *s, int32_t *sums) {
-    hipLaunchKernelGGL(rmsnorm_act_kernel, dim3(K / 64, ntok), dim3(64), 0, st, x, w, eps, K, q, s, sums);
+                        float *s, int32_t *sums, ActTiles tiles) {
+    hipLaunchKernelGGL(rmsnorm_act_kernel, dim3(K / 64, ntok), dim3(64), 0, st, x, w, eps, K, q, s, sums, tiles);
     hip_check(hipGetLastError(), "rmsnorm_act launch");
 }
 
@@ -286,7 +288,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
                                                            int hd, KvRing kr, float attn_scale, int nsplit,
                                                            AttnPost post, float *__restrict__ part,
                                                            float *__restrict__ out_f, int8_t *__restrict__ aq,
-                                                           float *__restrict__ as, int32_t *__restrict__ asum) {
+                                                           float *__restrict__ as, int32_t *__restrict__ asum,
+                                                           ActTiles tiles) {
     constexpr int NW = NTH / 64;  // waves
     __shared__ __align__(16) int8_t qi[128];
     __shared__ __align__(16) int8_t kcur[128], vcur[128];  // current position's K / V (post.on)
@@ -548,7 +551,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
             if (out_f) out_f[hbase + wv * 64 + lane] = o;
             if (aq) {
                 const size_t c = (size_t)head * nb + wv, g = (size_t)tok * nq * nb + c;
-                quant_chunk_store(fwht_lane(o, c, lane), lane, aq + g * 64, as + g, asum + g);
+                quant_chunk_store(fwht_lane(o, c, lane), lane, aq + g * 64, as + g, asum + g, tiles.xt, tiles.st, tok,
+                                  (int)c, nq * nb);
             }
         }
         return;
@@ -571,7 +575,7 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
 template <int ONESHOT>
 __device__ __forceinline__ void merge_head(const float *pp, int ns, int nq, int hd, int head, int tok, uint32_t lane,
                                            float *__restrict__ out_f, int8_t *__restrict__ aq, float *__restrict__ as,
-                                           int32_t *__restrict__ asum) {
+                                           int32_t *__restrict__ asum, ActTiles tiles = ActTiles{}) {
     static_assert(ONESHOT <= 64, "one split per lane");
     const int nb = hd / 64;
     float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
@@ -647,8 +651,11 @@ __device__ __forceinline__ void merge_head(const float *pp, int ns, int nq, int 
         const int nc_tok = nq * nb;  // o_proj input chunks per token
         const size_t c0 = (size_t)head * nb;
         const size_t g0 = (size_t)tok * nc_tok + c0;
-        quant_chunk_store(fwht_lane(o0, c0, lane), lane, aq + g0 * 64, as + g0, asum + g0);
-        if (nb > 1) quant_chunk_store(fwht_lane(o1, c0 + 1, lane), lane, aq + (g0 + 1) * 64, as + g0 + 1, asum + g0 + 1);
+        quant_chunk_store(fwht_lane(o0, c0, lane), lane, aq + g0 * 64, as + g0, asum + g0, tiles.xt, tiles.st, tok,
+                          (int)c0, nc_tok);
+        if (nb > 1)
+            quant_chunk_store(fwht_lane(o1, c0 + 1, lane), lane, aq + (g0 + 1) * 64, as + g0 + 1, asum + g0 + 1, tiles.xt,
+                              tiles.st, tok, (int)c0 + 1, nc_tok);
     }
 }
 
@@ -656,12 +663,12 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
                                                         int span_len, KvRing kr, const int *__restrict__ pos_dev,
                                                         float *__restrict__ out_f,
                                                         int8_t *__restrict__ aq, float *__restrict__ as,
-                                                        int32_t *__restrict__ asum) {
+                                                        int32_t *__restrict__ asum, ActTiles tiles) {
     const int head = blockIdx.x, tok = blockIdx.y;
     const int act = active_len(kr, pos_dev[0] + tok + 1);
     const int ns = min(nsplit, (act + span_len - 1) / span_len);
     merge_head<kMergeOneShot>(part + (size_t)(tok * nq + head) * nsplit * (2 + hd), ns, nq, hd, head, tok, threadIdx.x,
-                              out_f, aq, as, asum);
+                              out_f, aq, as, asum, tiles);
 }
 
 // Long-context decode attention for grouped queries (int8 KV, no window), one launch.
@@ -1145,26 +1152,27 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale,
                       int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum,
-                      const GqaWork &gqa, int ctx_bound) {
+                      const GqaWork &gqa, int ctx_bound, ActTiles tiles) {
     if (nsplit == 1 && ctx_bound > 0 && ctx_bound <= kAttnSmall) {
         // every token of the batch attends to at most kAttnSmall positions: a quarter of the
         // threads, the whole-context kernel's sums (its V position subsets) bit for bit
         hipLaunchKernelGGL((attn_partial_kernel<kAttnSmall, true, kAttnWhole>), dim3(nq, 1, ntok), dim3(kAttnSmall), 0,
                            st, q, q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part,
-                           out_f, aq, as, asum);
+                           out_f, aq, as, asum, tiles);
         hip_check(hipGetLastError(), "attention launch");
         return;
     }
     if (nsplit == 1) {  // the caller sized the context within kAttnWhole (attn_max_splits)
         hipLaunchKernelGGL((attn_partial_kernel<kAttnWhole, true>), dim3(nq, 1, ntok), dim3(kAttnWhole), 0, st, q,
                            q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part, out_f,
-                           aq, as, asum);
+                           aq, as, asum, tiles);
         hip_check(hipGetLastError(), "attention launch");
         return;
     }
     const int group = nq / nkv;
     if (gqa.words && ntok == 1 && group >= 2 && group <= kGqaMaxGroup && kr.bits == 8 && kr.window == 0 &&
         (hd == 64 || hd == 128)) {
+        if (tiles.xt) throw Error(K2T_E_INTERNAL, "grouped-query attention writes no activation tiles");
         const int hsplit = (group + kGqaHeads - 1) / kGqaHeads;
         GqaArgs A{q,          q_stride,          kq,   vq,         ks,       vs,       pos_dev, layer,
                   nq,         nkv,               kr,   attn_scale, gqa_spans(kr.cap), hsplit, post, gqa.words,
@@ -1179,10 +1187,10 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
     }
     hipLaunchKernelGGL((attn_partial_kernel<kAttnSplitLen, false>), dim3(nq, nsplit, ntok), dim3(kAttnSplitLen), 0, st,
                        q, q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, nsplit, post, part,
-                       nullptr, nullptr, nullptr, nullptr);
+                       nullptr, nullptr, nullptr, nullptr, ActTiles{});
     hip_check(hipGetLastError(), "attn_partial launch");
     hipLaunchKernelGGL(attn_merge_kernel, dim3(nq, ntok), dim3(64), 0, st, part, nq, hd, nsplit, kAttnSplitLen, kr,
-                       pos_dev, out_f, aq, as, asum);
+                       pos_dev, out_f, aq, as, asum, tiles);
     hip_check(hipGetLastError(), "attn_merge launch");
 }
 
@@ -1296,7 +1304,8 @@ void launch_attention_exact(hipStream_t st, const float *q, int q_stride, const 
 // EXACT: the exponential of the x86 reference build (expf_rn) instead of the device expf.
 template <bool EXACT>
 __global__ __launch_bounds__(64) void swiglu_act_kernel(const float *__restrict__ gu, int inter, int8_t *__restrict__ q,
-                                                        float *__restrict__ s, int32_t *__restrict__ sums) {
+                                                        float *__restrict__ s, int32_t *__restrict__ sums,
+                                                        ActTiles tiles) {
     const uint32_t lane = threadIdx.x;
     const int ic = blockIdx.x, tok = blockIdx.y;
     const int nci = inter / 64;
@@ -1304,15 +1313,18 @@ __global__ __launch_bounds__(64) void swiglu_act_kernel(const float *__restrict_
     const float g = b[lane], u = b[64 + lane];
     const float v = (g / (1.0f + (EXACT ? expf_rn(-g) : expf(-g)))) * u;
     const size_t gc = (size_t)tok * nci + ic;
-    quant_chunk_store(fwht_lane(v, (uint64_t)ic, lane), lane, q + gc * 64, s + gc, sums + gc);
+    quant_chunk_store(fwht_lane(v, (uint64_t)ic, lane), lane, q + gc * 64, s + gc, sums + gc, tiles.xt, tiles.st, tok,
+                      ic, nci);
 }
 
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
-                       bool exact) {
+                       bool exact, ActTiles tiles) {
     if (exact)
-        hipLaunchKernelGGL(swiglu_act_kernel<true>, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums);
+        hipLaunchKernelGGL(swiglu_act_kernel<true>, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums,
+                           tiles);
     else
-        hipLaunchKernelGGL(swiglu_act_kernel<false>, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums);
+        hipLaunchKernelGGL(swiglu_act_kernel<false>, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums,
+                           tiles);
     hip_check(hipGetLastError(), "swiglu_act launch");
 }
 

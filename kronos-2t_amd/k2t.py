@@ -216,8 +216,9 @@ class Ctx:
     def set_exact(self, on):
         check(lib().k2t_ctx_set_exact(self.h, int(bool(on))))
 
-    def set_mfma(self, on):
-        check(lib().k2t_ctx_set_mfma(self.h, int(bool(on))))
+    def set_mfma(self, mode):
+        """0 off, 1 on (default), 2 on with the GEMV copying the activation tiles itself."""
+        check(lib().k2t_ctx_set_mfma(self.h, int(mode)))
 
     def sync(self):
         check(lib().k2t_ctx_sync(self.h))
