@@ -279,8 +279,11 @@ __device__ __forceinline__ float tree_sum(const float *v, int n) {
 
 // VORD >= NTH: the o partial sums use the position subsets of a VORD-thread workgroup
 // (each thread then owns VORD / NTH of them), so a 256-thread launch over at most 256
-// positions gives the 1024-thread kernel's results bit for bit.
-template <int NTH, bool FINAL, int VORD = NTH>
+// positions gives the 1024-thread kernel's results bit for bit.  RING: the cache is a
+// sliding-window ring (positions map to slots through the window and ring arithmetic);
+// without it index = position = slot, and the kernel carries none of that arithmetic
+// (its modulo costs tens of instructions per position).
+template <int NTH, bool FINAL, int VORD = NTH, bool RING = true>
 __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restrict__ q, int q_stride,
                                                            int8_t *__restrict__ kq, int8_t *__restrict__ vq,
                                                            float *__restrict__ ks, float *__restrict__ vs,
@@ -320,7 +323,7 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
         }
     }
     const int seq = pos_dev[0] + tok + 1;
-    const int act = active_len(kr, seq);  // attended positions: index idx -> slot of active_pos
+    const int act = RING ? active_len(kr, seq) : seq;  // attended positions: index idx -> slot of active_pos
     const int t0 = split * NTH, t1 = min(act, t0 + NTH);
     float *pp = part + ((size_t)(tok * nq + head) * nsplit + split) * (2 + hd);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -350,7 +353,7 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
         const float r1 = nb > 1 ? fwht_lane(a1, 1, lane) : 0.0f;
         kv_store_head(r0, r1, nb, lane, kr.bits, hd, 0, wv == 1 ? kcur : vcur, wv == 1 ? cur_s : cur_s + 2);
         if (head % (nq / nkv) == 0) {
-            const size_t slot = ((size_t)layer * nkv + kvh) * kr.cap + ring_slot(kr, seq - 1);
+            const size_t slot = ((size_t)layer * nkv + kvh) * kr.cap + (RING ? ring_slot(kr, seq - 1) : seq - 1);
             kv_store_head(r0, r1, nb, lane, kr.bits, hd, slot, wv == 1 ? kq : vq, wv == 1 ? ks : vs);
         }
     }
@@ -382,7 +385,9 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
     const size_t base = ((size_t)layer * nkv + kvh) * kr.cap;
     const float qas = qas_s;
     // slot of the idx-th attended position (identity without a sliding window)
-    auto slot_of = [&](int idx) -> size_t { return (size_t)ring_slot(kr, active_pos(kr, idx, seq)); };
+    auto slot_of = [&](int idx) -> size_t {
+        return RING ? (size_t)ring_slot(kr, active_pos(kr, idx, seq)) : (size_t)idx;
+    };
     // scores: one thread per position
     float smax = -INFINITY;
     float vscale = 0.0f;
@@ -1148,6 +1153,15 @@ bool gqa_eligible(int nsplit, int ntok, int nq, int nkv, int hd, const KvRing &k
 }
 size_t gqa_words(int cap, int nq, int hd, int ntok) { return (size_t)gqa_spans(cap) * nq * (2 + hd) * ntok; }
 
+// attn_partial_kernel with or without the sliding-window ring arithmetic.
+template <int NTH, bool FINAL, int VORD, typename... Args>
+void launch_attn_partial(const KvRing &kr, dim3 grid, hipStream_t st, Args... args) {
+    if (kr.window > 0 || kr.ring > 0)
+        hipLaunchKernelGGL((attn_partial_kernel<NTH, FINAL, VORD, true>), grid, dim3(NTH), 0, st, args...);
+    else
+        hipLaunchKernelGGL((attn_partial_kernel<NTH, FINAL, VORD, false>), grid, dim3(NTH), 0, st, args...);
+}
+
 void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale,
@@ -1156,16 +1170,16 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
     if (nsplit == 1 && ctx_bound > 0 && ctx_bound <= kAttnSmall) {
         // every token of the batch attends to at most kAttnSmall positions: a quarter of the
         // threads, the whole-context kernel's sums (its V position subsets) bit for bit
-        hipLaunchKernelGGL((attn_partial_kernel<kAttnSmall, true, kAttnWhole>), dim3(nq, 1, ntok), dim3(kAttnSmall), 0,
-                           st, q, q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part,
-                           out_f, aq, as, asum, tiles);
+        launch_attn_partial<kAttnSmall, true, kAttnWhole>(kr, dim3(nq, 1, ntok), st, q, q_stride, kq, vq, ks, vs,
+                                                          pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part,
+                                                          out_f, aq, as, asum, tiles);
         hip_check(hipGetLastError(), "attention launch");
         return;
     }
     if (nsplit == 1) {  // the caller sized the context within kAttnWhole (attn_max_splits)
-        hipLaunchKernelGGL((attn_partial_kernel<kAttnWhole, true>), dim3(nq, 1, ntok), dim3(kAttnWhole), 0, st, q,
-                           q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part, out_f,
-                           aq, as, asum, tiles);
+        launch_attn_partial<kAttnWhole, true, kAttnWhole>(kr, dim3(nq, 1, ntok), st, q, q_stride, kq, vq, ks, vs,
+                                                          pos_dev, layer, nq, nkv, hd, kr, attn_scale, 1, post, part,
+                                                          out_f, aq, as, asum, tiles);
         hip_check(hipGetLastError(), "attention launch");
         return;
     }
@@ -1185,9 +1199,9 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
         hip_check(hipGetLastError(), "attn_gqa launch");
         return;
     }
-    hipLaunchKernelGGL((attn_partial_kernel<kAttnSplitLen, false>), dim3(nq, nsplit, ntok), dim3(kAttnSplitLen), 0, st,
-                       q, q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, nsplit, post, part,
-                       nullptr, nullptr, nullptr, nullptr, ActTiles{});
+    launch_attn_partial<kAttnSplitLen, false, kAttnSplitLen>(
+        kr, dim3(nq, nsplit, ntok), st, q, q_stride, kq, vq, ks, vs, pos_dev, layer, nq, nkv, hd, kr, attn_scale, nsplit,
+        post, part, (float *)nullptr, (int8_t *)nullptr, (float *)nullptr, (int32_t *)nullptr, ActTiles{});
     hip_check(hipGetLastError(), "attn_partial launch");
     hipLaunchKernelGGL(attn_merge_kernel, dim3(nq, ntok), dim3(64), 0, st, part, nq, hd, nsplit, kAttnSplitLen, kr,
                        pos_dev, out_f, aq, as, asum, tiles);
