@@ -40,6 +40,10 @@ namespace {
 #define K2T_MFMA_MIN_WAVES 2048
 #endif
 constexpr int kMfmaDepth = K2T_MFMA_DEPTH;         // chunks in flight per wave (unshared kernels)
+#ifndef K2T_MFMA_SH_DEPTH
+#define K2T_MFMA_SH_DEPTH 2
+#endif
+constexpr int kMfmaShDepth = K2T_MFMA_SH_DEPTH;    // the same, kernels sharing activation blocks
 constexpr long kMfmaMinWaves = K2T_MFMA_MIN_WAVES;  // 8 waves per CU
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -175,7 +179,6 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
     for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[b][r] = 0.0f;
-    static_assert(!SH || P % 2 == 0, "the LDS slot of chunk c0 + i is i & 1 (c0 a multiple of P)");
     const int nc = A.nc, last = nc - 1;
     MfChunk<NB, SH> ring[P];
 #pragma unroll
@@ -184,13 +187,13 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
     for (; c0 + P <= nc; c0 += P) {
 #pragma unroll
         for (int i = 0; i < P; i++) {
-            mf_step<NB, SH>(A, ring[i], acc, bsh[i & 1], wave, lane);  // chunk c0 + i
+            mf_step<NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
             mf_fetch<NB, SH>(A, R, is_tail, nib0, a_off, s_off, x_off, sx_off, tb0, wave, min(c0 + P + i, last), ring[i]);
         }
     }
 #pragma unroll
     for (int i = 0; i < P - 1; i++)
-        if (c0 + i < nc) mf_step<NB, SH>(A, ring[i], acc, bsh[i & 1], wave, lane);
+        if (c0 + i < nc) mf_step<NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
     if (stripe_id >= A.stripes) return;
 #pragma unroll
     for (int b = 0; b < NB; b++) {
@@ -273,7 +276,7 @@ void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, cons
         case 1: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<1, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
         case 2: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<2, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
         case 3: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<3, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
-        default: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<4, 2, true>), grid, dim3(256), 0, st, A); break;
+        default: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<4, kMfmaShDepth, true>), grid, dim3(256), 0, st, A); break;
     }
     hip_check(hipGetLastError(), "mfma gemm launch");
 }
