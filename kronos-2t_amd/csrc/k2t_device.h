@@ -66,6 +66,23 @@ __device__ __forceinline__ void lds_dma16(const void *p, uint32_t m0) {
 __device__ __forceinline__ void lds_dma4(const void *p, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(p), "s"(m0) : "memory");
 }
+// The same from base + voff + OFF: a wave-uniform 64-bit base (SGPRs), a per-lane 32-bit
+// offset and an immediate, so a stream that advances by a uniform stride costs its
+// waves scalar adds only.  The instruction's immediate offset moves the LDS address as
+// well (LDS [M0 + OFF + size * lane]), so M0 is set OFF lower: the bytes still land at
+// m0 + size * lane.
+template <int OFF>
+__device__ __forceinline__ void lds_dma16_sa(uint32_t voff, const void *sbase, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 offset:%3 nt" ::"v"(voff), "s"(sbase),
+                 "s"(m0 - (uint32_t)OFF), "i"(OFF)
+                 : "memory");
+}
+template <int OFF>
+__device__ __forceinline__ void lds_dma4_sa(uint32_t voff, const void *sbase, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1 offset:%3" ::"v"(voff), "s"(sbase),
+                 "s"(m0 - (uint32_t)OFF), "i"(OFF)
+                 : "memory");
+}
 
 // A 64-bit hand-off word {epoch (high half), payload (low half)}, written and read with
 // one agent-scope atomic each: coherent across XCDs, and the payload and its ready mark

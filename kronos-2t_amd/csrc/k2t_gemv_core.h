@@ -289,6 +289,12 @@ struct GemvWaveLds {
     int cw0, cw1, iters, G, q;
     uint32_t lane, half, slot0;
     bool active;
+    // Strided issue: fragment i's loads read ubase + i * dstep + (this lane's fixed offset
+    // v_nib / v_hi / v_h2 / v_sc), when the chunks of one fragment advance every lane's
+    // records by the same stride (always for bit planes; NF when sgc divides G).
+    bool strided;
+    const uint8_t *ubase;
+    uint32_t dstep, v_nib, v_hi, v_h2, v_sc;
 
     __device__ __forceinline__ GemvWaveLds(const MatDev &M_, int rb, bool active_, int wseg, uint32_t lane_,
                                            uint8_t *slots)
@@ -300,12 +306,60 @@ struct GemvWaveLds {
         cw1 = active ? min(M.nc, cw0 + M.cps) : cw0;
         iters = cw1 > cw0 ? (cw1 - cw0 + G - 1) / G : 0;
         slot0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_offset(slots));
+        const uintptr_t mb = (uintptr_t)o.mbase;
+        ubase = (const uint8_t *)(((uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)mb)) |
+                                  ((uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(mb >> 32)) << 32));
+        const uint32_t c0 = (uint32_t)(cw0 + q);  // this lane's chunk of fragment 0
+        const uint32_t hp = (uint32_t)hp_of<HP>(M);
+        uint32_t rec0, sc0;
+        if constexpr (FMT == 0) {
+            const uint32_t REC = o.is_tail ? 512u + 128u * hp + 32u : 1024u + 256u * hp + 64u;
+            rec0 = c0 * REC;
+            sc0 = rec0;
+            dstep = (uint32_t)G * REC;
+            strided = true;
+        } else {
+            const uint32_t sgc = (uint32_t)M.sgc, cs = o.is_tail ? 512u : 1024u, gsz = o.is_tail ? 32u : 64u;
+            const uint32_t sg0 = c0 / sgc;
+            rec0 = sg0 * gsz + c0 * cs;       // group base sg*gsz + (sg*sgc)*cs, plus (c - sg*sgc)*cs
+            sc0 = sg0 * (gsz + sgc * cs);     // the group base
+            dstep = ((uint32_t)G / sgc) * gsz + (uint32_t)G * cs;
+            strided = (uint32_t)G % sgc == 0;
+        }
+        v_nib = rec0 + o.nib_off;
+        v_hi = rec0 + o.hi_off;
+        v_h2 = hp != 0 ? v_hi + 64u : v_nib;  // the mixed variant's second hi piece (nibbles again for hp 0)
+        if (frag_hi_pieces<FMT, HP>() == 2 && hp == 0) v_hi = v_nib;
+        v_sc = sc0 + o.sc_off;
+        dstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)dstep);  // uniform (is_tail, G, sgc)
     }
     __device__ __forceinline__ int chunk_of(int i) const { return cw0 + i * G + q; }
     __device__ __forceinline__ bool valid(int i) const { return i < iters && chunk_of(i) < cw1; }
 
     // Issues fragment i (a clamped in-range chunk when i is past the share).
     __device__ __forceinline__ void issue(int i) {
+        const uint32_t base = slot0 + (uint32_t)(i % F) * (uint32_t)FB;
+        if (strided && cw0 + (i + 1) * G <= cw1) {  // wave-uniform: every lane's chunk is in the share
+            const uintptr_t a = (uintptr_t)(ubase + (size_t)i * dstep);  // wave-uniform: keep it in SGPRs
+            const uint8_t *sb = (const uint8_t *)(((uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a)) |
+                                                  ((uintptr_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32))
+                                                   << 32));
+            lds_dma16_sa<0>(v_nib, sb, base);
+            lds_dma16_sa<128>(v_nib, sb, base + 1024);
+            lds_dma16_sa<256>(v_nib, sb, base + 2048);
+            lds_dma16_sa<384>(v_nib, sb, base + 3072);
+            if constexpr (NH == 4) {
+                lds_dma16_sa<0>(v_hi, sb, base + 4096);
+                lds_dma16_sa<64>(v_hi, sb, base + 5120);
+                lds_dma16_sa<128>(v_hi, sb, base + 6144);
+                lds_dma16_sa<192>(v_hi, sb, base + 7168);
+            } else if constexpr (NH == 2) {
+                lds_dma16_sa<0>(v_hi, sb, base + 4096);
+                lds_dma16_sa<0>(v_h2, sb, base + 5120);
+            }
+            lds_dma4_sa<0>(v_sc, sb, base + (4 + NH) * 1024);
+            return;
+        }
         const int c = cw1 > cw0 ? min(chunk_of(i), cw1 - 1) : 0;
         const uint32_t hp = (uint32_t)hp_of<HP>(M);
         const uint8_t *rec, *scp;
@@ -320,7 +374,6 @@ struct GemvWaveLds {
             rec = gb + (size_t)sb * (o.is_tail ? 512 : 1024);
             scp = gb;
         }
-        const uint32_t base = slot0 + (uint32_t)(i % F) * (uint32_t)FB;
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) lds_dma16(rec + o.nib_off + kk * 128, base + kk * 1024);
         if constexpr (NH == 4) {
