@@ -80,11 +80,12 @@ int32_t k2t_ctx_set_splitk(k2t_ctx *ctx, int32_t max_segments);
  * within a few ulp of the reference, and faster for long K.  Integer per-(row, chunk)
  * dots are exact in both modes. */
 int32_t k2t_ctx_set_exact(k2t_ctx *ctx, int32_t exact);
-/* Batched NF4 GEMVs (16 or more tokens of a ready activation over the whole matrix,
- * k2t_gemv and the model's prefill): enable = 1 (default) runs them on the int8 matrix
- * cores, one weight pass per 64 tokens, with outputs equal to the exact-order epilogue's
- * in either mode; 0 runs the 4-token weight passes of nf_sdot_decode_neon's tile
- * (simd_lut.rs:6074-6364).  2: matrix cores, but a model's prefill does not have the
+/* Batched NF4 and bit-plane (b4 / b5 / b6) GEMVs (16 or more tokens of a ready activation
+ * over the whole matrix, k2t_gemv and the model's prefill): enable = 1 (default) runs
+ * them on the int8 matrix cores, one weight pass per 64 tokens, with outputs equal to the
+ * exact-order epilogue's in either mode; 0 runs the 4-token weight passes of the
+ * reference's tiles (nf_sdot_decode_neon, simd_lut.rs:6074-6364;
+ * nibble4_sdot_batch_stripe_range, 4101-4320).  2: matrix cores, but a model's prefill does not have the
  * activation's producer write the tile-major copy the GEMV reads (the GEMV copies it
  * itself); same outputs as 1, for checking.  A backend choice of this build; the
  * reference has no counterpart.  K2T_E_ARG for other values. */

@@ -289,22 +289,26 @@ __device__ __forceinline__ uint32_t bit3_mask(uint32_t v) {
     return __builtin_amdgcn_perm(0u, 0x8000u, v & 0x08080808u);
 }
 
-// Lane `lane`'s byte (column lane of chunk c, token tok) and the chunk's scale in the
-// tile-major copy the matrix-core GEMV reads: per (16-token block, chunk) 1 KB in its B
-// operand's lane order (16 bytes per MFMA lane 16 * (col / 16) + tok % 16) and 16 scales.
-__device__ __forceinline__ void act_tile_store(int8_t *xt, float *st, int tok, int c, int nc, uint32_t lane,
-                                               int8_t qv, float scale) {
+// Lane `lane`'s byte (column lane of chunk c, token tok), the chunk's scale and its code
+// sum in the tile-major copy the matrix-core GEMV reads: per (16-token block, chunk) 1 KB
+// in its B operand's lane order (16 bytes per MFMA lane 16 * (col / 16) + tok % 16), 16
+// scales and 16 sums.
+__device__ __forceinline__ void act_tile_store(int8_t *xt, float *st, int32_t *ut, int tok, int c, int nc,
+                                               uint32_t lane, int8_t qv, float scale, int32_t sum) {
     const size_t tile = (size_t)(tok >> 4) * nc + c;
     xt[tile * 1024 + (((lane >> 4) * 16u + (uint32_t)(tok & 15)) * 16u) + (lane & 15u)] = qv;
-    if (lane == 0) st[tile * 16 + (tok & 15)] = scale;
+    if (lane == 0) {
+        st[tile * 16 + (tok & 15)] = scale;
+        ut[tile * 16 + (tok & 15)] = sum;
+    }
 }
 
 // Quantizes the 64 values held one per lane (already rotated) to int8 with one scale
 // (simd_lut.rs:3097-3128 / 3172-3195).  With xt, also into the tile-major copy (chunk c
-// of nc, token tok).
+// of nc, token tok; st and ut receive the scale and the code sum).
 __device__ __forceinline__ void quant_chunk_store(float v, uint32_t lane, int8_t *q, float *scale,
                                                   int32_t *sum, int8_t *xt = nullptr, float *st = nullptr,
-                                                  int tok = 0, int c = 0, int nc = 0) {
+                                                  int32_t *ut = nullptr, int tok = 0, int c = 0, int nc = 0) {
     const float mx = wave_max_f(fabsf(v));
     if (mx <= FLT_EPSILON) {
         q[lane] = 0;
@@ -312,7 +316,7 @@ __device__ __forceinline__ void quant_chunk_store(float v, uint32_t lane, int8_t
             *scale = 0.0f;
             *sum = 0;
         }
-        if (xt) act_tile_store(xt, st, tok, c, nc, lane, 0, 0.0f);
+        if (xt) act_tile_store(xt, st, ut, tok, c, nc, lane, 0, 0.0f, 0);
         return;
     }
     const float inv = 127.0f / mx;
@@ -323,7 +327,7 @@ __device__ __forceinline__ void quant_chunk_store(float v, uint32_t lane, int8_t
         *scale = mx / 127.0f;
         *sum = s;
     }
-    if (xt) act_tile_store(xt, st, tok, c, nc, lane, (int8_t)qi, mx / 127.0f);
+    if (xt) act_tile_store(xt, st, ut, tok, c, nc, lane, (int8_t)qi, mx / 127.0f, s);
 }
 
 __device__ __forceinline__ float fwht_lane(float v, uint64_t block, uint32_t lane) {

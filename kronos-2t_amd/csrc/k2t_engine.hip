@@ -230,6 +230,7 @@ struct k2t_model {
     // the activation's tile-major copy for matrix-core GEMVs (written by its producer)
     int8_t *xt = nullptr;
     float *st = nullptr;
+    int32_t *ut = nullptr;
     int pos = 0;
     bool use_graph = true;
     // 1: exact-order steps (the x86 reference's operation order throughout: in-order GEMV
@@ -362,7 +363,7 @@ void forward_exact(k2t_model *m, int ntok, bool with_logits) {
 // Where the producer of the activation of `w` writes the tile-major copy: the model's
 // tile buffers when that GEMV runs on the matrix cores, else nowhere.
 ActTiles act_tiles_for(const k2t_model *m, const k2t_mat *w, int ntok) {
-    return m->ctx->mfma == 1 && gemm_nf4_mfma_supported(w, ntok) ? ActTiles{m->xt, m->st} : ActTiles{};
+    return m->ctx->mfma == 1 && gemm_mfma_supported(w, ntok) ? ActTiles{m->xt, m->st, m->ut} : ActTiles{};
 }
 
 // One forward pass over `ntok` tokens already in m->tokens, positions pos..pos+ntok-1.
@@ -746,6 +747,7 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             const size_t ntile = (size_t)((max_batch + 15) / 16) * (kmax / 64);
             m->xt = (int8_t *)dalloc(m, ntile * 1024);
             m->st = (float *)dalloc(m, ntile * 16 * sizeof(float));
+            m->ut = (int32_t *)dalloc(m, ntile * 16 * sizeof(int32_t));
             // persistent decode kernel state
             // the persistent kernel's phases assume the megakernel shape q_dim == hidden
             m->mk_ok = decode_mk_supported(c, ctx->num_cus) && c.n_heads * c.head_dim == c.hidden;

@@ -1,16 +1,23 @@
-// Batched NF4 GEMV (prefill) on the int8 matrix cores of gfx950: out[t][r] =
+// Batched quantized GEMV (prefill) on the int8 matrix cores of gfx950: out[t][r] =
 // sum_c fmaf(float(dot_{r,c,t}) * sx[t][c], ws[r][c], ...) for up to 64 tokens per weight
-// pass, the chunk dots from v_mfma_i32_16x16x64_i8.
+// pass, the chunk dots from v_mfma_i32_16x16x64_i8.  NF4 (NfSdotMatrix) and the bit-plane
+// formats b4 / b5 / b6 (Nibble4SdotMatrix) share the kernel.
 //
-// The reference runs prefill through the same NfSdotMatrix kernels as decode, four tokens
-// per weight pass (nf_sdot_decode_neon's 4-token tile, simd_lut.rs:6074-6364).  Here one
-// wave owns one 16-row stripe and 16 to 64 tokens: per 64-column chunk it decodes the
-// stripe-chunk's NF4 codes to int8 once (the codebook as two v_perm XOR tables,
-// nf4_xlut), then runs one MFMA per 16-token block (A: 16 rows x 64 codes, B: 64
-// activation bytes x 16 tokens), so each weight byte is read once per 64 tokens instead of
-// once per 4.  The epilogue is the reference's per-row chain in chunk order (simd_lut.rs:
-// 4030-4059, 6334-6335: f = fmaf(float(dot) * sx, scale, f), chunks with sx == 0 skipped),
-// so every output equals the exact-order GEMV's (k2t_ctx_set_exact) bit for bit.
+// The reference runs prefill through the same kernels as decode, four tokens per weight
+// pass (nf_sdot_decode_neon's 4-token tile, simd_lut.rs:6074-6364, and the Nibble4 tile
+// nibble4_sdot_batch_stripe_range, 4101-4320).  Here one wave owns one 16-row stripe and 16 to 64 tokens: per 64-column
+// chunk it decodes the stripe-chunk's codes to int8 once, then runs one MFMA per 16-token
+// block (A: 16 rows x 64 codes, B: 64 activation bytes x 16 tokens), so each weight byte
+// is read once per 64 tokens instead of once per 4.
+//  - NF4: the codebook value of each code (the codebook as two v_perm XOR tables,
+//    nf4_xlut); the MFMA gives the chunk dot.
+//  - bit planes: the unsigned code u (4 + hp bits: the nibble and the hi-plane bits); the
+//    MFMA gives sum(u * x), and the chunk dot of the odd weights 2u - (2^(4+hp) - 1) is
+//    2 * sum(u * x) - (2^(4+hp) - 1) * sum(x), as the reference computes it (simd_lut.rs:
+//    4030-4045 and 4304-4309: the sdot of the codes acc, then 2 * acc - max_odd * xsum).
+// The epilogue is the reference's per-row chain in chunk order (simd_lut.rs:4030-4059,
+// 6334-6335: f = fmaf(float(dot) * sx, scale, f), chunks with sx == 0 skipped), so every
+// output equals the exact-order GEMV's (k2t_ctx_set_exact) bit for bit.
 //
 // Operand layouts of v_mfma_i32_16x16x64_i8 (checked on the GPU): lane l holds 16 bytes of
 // A row l % 16 and of B column l % 16; the products pair lane l's byte b of A with lane
@@ -19,12 +26,16 @@
 // column 16g + b.  The 16 x 16 int32 result: lane l holds rows 4 (l / 16) + r, r = 0..3,
 // of column l % 16.
 //
-// NF stripe-chunk bytes (512 per stripe, NfSdotMatrix, simd_lut.rs:4796-5023): byte e of
-// dword j at kk*128 + g*32 + half*16 + 4j holds the codes of row 4g + j, columns kk*16 +
-// half*8 + e (low nibble) and kk*16 + half*8 + 4 + e (high nibble).  Row i's columns
-// 16kk .. 16kk+15 are therefore the dwords at kk*128 + (i/4)*32 + 4(i%4) and 16 bytes
-// further: low / high nibbles of the first give columns 0-3 / 4-7, of the second 8-11 /
-// 12-15.
+// Nibble bytes of a stripe-chunk (512 per stripe, the same order in both formats:
+// NfSdotMatrix, simd_lut.rs:4796-5023; Nibble4SdotMatrix, 3331-3385): byte e of dword j at
+// kk*128 + g*32 + half*16 + 4j holds the codes of row 4g + j, columns kk*16 + half*8 + e
+// (low nibble) and kk*16 + half*8 + 4 + e (high nibble).  Row i's columns 16kk .. 16kk+15
+// are therefore the dwords at kk*128 + (i/4)*32 + 4(i%4) and 16 bytes further: low / high
+// nibbles of the first give columns 0-3 / 4-7, of the second 8-11 / 12-15.  Bit-plane hi
+// planes: for 16-byte piece p of a stripe's hi bytes (64 bytes apart), dword j of row
+// group g (g*16 + 4j) holds the bits of row 4g + j for columns kk*16 .. kk*16+15, kk = 2p
+// and 2p + 1 (one hi plane) or kk = p (two), in the bit positions the decode kernels'
+// rotations select (chunk_dots in k2t_gemv_core.h).
 #include "../../include/k2t_hip.h"
 #include "k2t_device.h"
 #include "k2t_internal.h"
@@ -53,10 +64,11 @@ typedef unsigned v2u __attribute__((ext_vector_type(2)));
 struct MfArgs {
     const uint8_t *pair, *tail;
     size_t ptot;  // bytes per pair stream
-    int rows, nc, np, stripes, sgc_log2;  // scale group = 1 << sgc_log2 chunks
+    int rows, nc, np, stripes, sgc_log2;  // NF scale group = 1 << sgc_log2 chunks
     uint32_t t0, t1, u0, u1;  // NF4 codebook XOR tables (nf4_xor_tables)
     const int8_t *xt;  // activations tile-major: [16-token block][chunk][64 lanes][16 bytes]
     const float *st;   // their scales: [16-token block][chunk][16 tokens]
+    const int32_t *ut;  // their code sums (bit planes): [16-token block][chunk][16 tokens]
     int K, ntok, nblk;  // nblk: 16-token blocks in the tiles
     float *out;
     size_t out_stride;
@@ -65,12 +77,14 @@ struct MfArgs {
 
 // Everything one chunk needs (one ring stage): the stripe-chunk's codes and scales, the
 // activation blocks this wave loads (all NB, or with sharing its own one), their scales.
-template <int NB, bool SH>
+template <int FMT, int NB, bool SH>
 struct MfChunk {
     uint32_t d0, d1;
+    uint32_t hv;  // bit planes with hi planes: this lane's hi-plane dword
     uint2 sw;
     int4 x[SH ? 1 : NB];
     float sx[NB];
+    int32_t su[FMT == 0 ? NB : 1];  // bit planes: the tokens' code sums
 };
 
 // Buffer resource of a wave-uniform base (raw, no stride; dword 3 as gfx950 wants it).
@@ -79,36 +93,52 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t mf_rsrc(const void *base) {
 }
 
 struct MfSrc {
-    __amdgpu_buffer_rsrc_t w, x, s;  // the stripe's pair stream (or the tail), the tiles, their scales
+    __amdgpu_buffer_rsrc_t w, x, s, u;  // the stripe's stream (pair or tail), the tiles, scales, sums
+};
+
+// Per-lane offsets of a stripe-chunk record, fixed for the wave's life.
+struct MfLane {
+    uint32_t a_off;  // the lane's first nibble dword (the second is 16 bytes further)
+    uint32_t h_off;  // its hi-plane dword (bit planes)
+    uint32_t s_off;  // its rows' BF16 scale pair
+    uint32_t x_off, sx_off;
 };
 
 // Every load is a buffer load: the wave-uniform part of its offset in an SGPR, the
 // per-lane part (fixed for the wave's life) in one VGPR, so no 64-bit address adds.
-template <int NB, bool SH>
-__device__ __forceinline__ void mf_fetch(const MfArgs &A, const MfSrc &R, bool is_tail, uint32_t nib0,
-                                         uint32_t a_off, uint32_t s_off, uint32_t x_off, uint32_t sx_off, int tb0,
-                                         uint32_t wave, int c, MfChunk<NB, SH> &f) {
-    const uint32_t sg = (uint32_t)c >> A.sgc_log2, sb = (uint32_t)c - (sg << A.sgc_log2);
-    const uint32_t cs = is_tail ? 512u : 1024u;
-    const uint32_t gb = sg * (is_tail ? 32u : 64u) + (sg << A.sgc_log2) * cs;  // scale-group base
-    const uint32_t rec = gb + nib0 + sb * cs;
-    f.d0 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(R.w, a_off, rec, 0);
-    f.d1 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(R.w, a_off + 16u, rec, 0);
-    const v2u sw = __builtin_amdgcn_raw_buffer_load_b64(R.w, s_off, gb, 0);
+//  - NF: group sg = c / sgc starts at sg * gsz + sg * sgc * cs (gsz = 64 bytes of scales,
+//    32 in the tail; cs = 1024 bytes of codes per chunk, 512 in the tail), the chunk's
+//    codes at that + gsz + (c - sg * sgc) * cs.
+//  - bit planes: chunk c's record at c * REC (REC = 1024 + 256 hp + 64, the tail's
+//    512 + 128 hp + 32): codes, hi bytes, scales; the lane offsets point inside it.
+template <int FMT, int HP, int NB, bool SH>
+__device__ __forceinline__ void mf_fetch(const MfArgs &A, const MfSrc &R, const MfLane &L, bool is_tail, int tb0,
+                                         uint32_t wave, int c, MfChunk<FMT, NB, SH> &f) {
+    uint32_t rec, sgb;
+    if constexpr (FMT == 0) {
+        rec = (uint32_t)c * (is_tail ? 512u + 128u * HP + 32u : 1024u + 256u * HP + 64u);
+        sgb = rec;
+    } else {
+        const uint32_t sg = (uint32_t)c >> A.sgc_log2, sb = (uint32_t)c - (sg << A.sgc_log2);
+        const uint32_t cs = is_tail ? 512u : 1024u, gsz = is_tail ? 32u : 64u;
+        sgb = sg * gsz + (sg << A.sgc_log2) * cs;  // scale-group base
+        rec = sgb + gsz + sb * cs;
+    }
+    f.d0 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(R.w, L.a_off, rec, 0);
+    f.d1 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(R.w, L.a_off + 16u, rec, 0);
+    if constexpr (FMT == 0 && HP > 0) f.hv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(R.w, L.h_off, rec, 0);
+    const v2u sw = __builtin_amdgcn_raw_buffer_load_b64(R.w, L.s_off, sgb, 0);
     f.sw = make_uint2(sw[0], sw[1]);
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         // blocks past the last repeat it; their outputs are never stored
-#ifdef K2T_MF_EXP_BSAME
-        const uint32_t tile = (uint32_t)min(tb0 + b, A.nblk - 1) * (uint32_t)A.nc;  // measurement only: wrong sums
-#else
         const uint32_t tile = (uint32_t)min(tb0 + b, A.nblk - 1) * (uint32_t)A.nc + (uint32_t)c;
-#endif
         if (!SH || b == (int)wave) {  // with sharing, waves >= NB load no block
-            const v4u x = __builtin_amdgcn_raw_buffer_load_b128(R.x, x_off, tile * 1024u, 0);
+            const v4u x = __builtin_amdgcn_raw_buffer_load_b128(R.x, L.x_off, tile * 1024u, 0);
             f.x[SH ? 0 : b] = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
         }
-        f.sx[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(R.s, sx_off, tile * 64u, 0));
+        f.sx[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(R.s, L.sx_off, tile * 64u, 0));
+        if constexpr (FMT == 0) f.su[b] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(R.u, L.sx_off, tile * 64u, 0);
     }
 }
 
@@ -120,18 +150,41 @@ __device__ __forceinline__ void mf_fetch(const MfArgs &A, const MfSrc &R, bool i
 // that loaded a block store it, one barrier, then every wave reads every block.  Two
 // slots alternate: a wave stores into a slot only after the barrier that all waves
 // passed once done reading it.
-template <int NB, bool SH>
-__device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<NB, SH> &f, float (&acc)[NB][4], int4 *bsh,
-                                        uint32_t wave, uint32_t lane) {
+template <int FMT, int HP, int NB, bool SH>
+__device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<FMT, NB, SH> &f, float (&acc)[NB][4],
+                                        int4 *bsh, uint32_t wave, uint32_t lane) {
     if (SH) {
         if (wave < (uint32_t)NB) bsh[wave * 64 + lane] = f.x[0];
         __syncthreads();
     }
     v4i a;
-    a[0] = (int)nf4_xlut(f.d0 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
-    a[1] = (int)nf4_xlut((f.d0 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
-    a[2] = (int)nf4_xlut(f.d1 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
-    a[3] = (int)nf4_xlut((f.d1 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+    if constexpr (FMT == 0) {
+        // the unsigned codes: nibble, then the hi-plane bits (as chunk_dots places them for
+        // kk = lane group, half 0 for the first dword and half 1 for the second)
+        uint32_t lo0 = f.d0 & 0x0F0F0F0Fu, hi0 = (f.d0 >> 4) & 0x0F0F0F0Fu;
+        uint32_t lo1 = f.d1 & 0x0F0F0F0Fu, hi1 = (f.d1 >> 4) & 0x0F0F0F0Fu;
+        if constexpr (HP == 2) {
+            lo0 |= f.hv & 0x30303030u;
+            hi0 |= __builtin_rotateright32(f.hv, 2u) & 0x30303030u;
+            lo1 |= __builtin_rotateright32(f.hv, 30u) & 0x30303030u;
+            hi1 |= __builtin_rotateright32(f.hv, 28u) & 0x30303030u;
+        } else if constexpr (HP == 1) {
+            const uint32_t e = (lane & 16u) ? 28u : 0u;  // odd lane group: the piece's upper bits
+            lo0 |= __builtin_rotateright32(f.hv, e) & 0x10101010u;
+            hi0 |= __builtin_rotateright32(f.hv, e + 1u) & 0x10101010u;
+            lo1 |= __builtin_rotateright32(f.hv, e + 2u) & 0x10101010u;
+            hi1 |= __builtin_rotateright32(f.hv, e + 3u) & 0x10101010u;
+        }
+        a[0] = (int)lo0;
+        a[1] = (int)hi0;
+        a[2] = (int)lo1;
+        a[3] = (int)hi1;
+    } else {
+        a[0] = (int)nf4_xlut(f.d0 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+        a[1] = (int)nf4_xlut((f.d0 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+        a[2] = (int)nf4_xlut(f.d1 & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+        a[3] = (int)nf4_xlut((f.d1 >> 4) & 0x0F0F0F0Fu, A.t0, A.t1, A.u0, A.u1);
+    }
     const float ws[4] = {bf16_lo(f.sw.x), bf16_hi(f.sw.x), bf16_lo(f.sw.y), bf16_hi(f.sw.y)};
 #pragma unroll
     for (int b = 0; b < NB; b++) {
@@ -140,7 +193,11 @@ __device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<NB, SH> &
         const v4i zero = {0, 0, 0, 0};
         const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bv, zero, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[b][r] = fmaf((float)d[r] * f.sx[b], ws[r], acc[b][r]);
+        for (int r = 0; r < 4; r++) {
+            int dot = d[r];
+            if constexpr (FMT == 0) dot = 2 * dot - ((1 << (4 + HP)) - 1) * f.su[b];
+            acc[b][r] = fmaf((float)dot * f.sx[b], ws[r], acc[b][r]);
+        }
     }
 }
 
@@ -153,8 +210,8 @@ __device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<NB, SH> &
 // w < NB loads block w; one barrier per chunk) instead of each loading all NB.  Measured
 // (256 tokens): 16384 x 2048 at NB 4, 45.7 -> 40.4 us with P 2; 2048 x 8192 at NB 1,
 // 36.9 -> 44-49 us (one loader and a barrier per chunk for 128 chunks): on for NB 4 only.
-template <int NB, int P, bool SH>
-__global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
+template <int FMT, int HP, int NB, int P, bool SH>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(MfArgs A) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: stripe math on SGPRs
     const int stripe_id = (int)blockIdx.x * 4 + (int)wave;
@@ -168,11 +225,19 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
     const uint32_t side = is_tail ? 0u : (uint32_t)(stripe & 1);
     const uint8_t *mbase = is_tail ? A.tail : A.pair + (size_t)(stripe >> 1) * A.ptot;
     const uint32_t li = lane & 15u, lg = lane >> 4;
-    const uint32_t a_off = lg * 128u + (li >> 2) * 32u + 4u * (li & 3u);
-    const uint32_t s_off = (is_tail ? 0u : side * 32u) + 8u * lg;  // rows 4lg .. 4lg+3
-    const uint32_t nib0 = is_tail ? 32u : 64u + side * 512u;
-    const MfSrc R{mf_rsrc(mbase), mf_rsrc(A.xt), mf_rsrc(A.st)};
-    const uint32_t x_off = lane * 16u, sx_off = li * 4u;
+    MfLane L;
+    L.a_off = (is_tail ? 0u : side * 512u) + lg * 128u + (li >> 2) * 32u + 4u * (li & 3u);
+    if constexpr (FMT == 0) {
+        const uint32_t hib = is_tail ? 512u : 1024u + side * 128u * HP;  // the stripe's hi bytes
+        L.h_off = hib + (HP == 2 ? lg : lg >> 1) * 64u + (li >> 2) * 16u + 4u * (li & 3u);
+        L.s_off = (is_tail ? 512u + 128u * HP : 1024u + 256u * HP + side * 32u) + 8u * lg;  // rows 4lg .. 4lg+3
+    } else {
+        L.h_off = 0;
+        L.s_off = (is_tail ? 0u : side * 32u) + 8u * lg;
+    }
+    L.x_off = lane * 16u;
+    L.sx_off = li * 4u;
+    const MfSrc R{mf_rsrc(mbase), mf_rsrc(A.xt), mf_rsrc(A.st), mf_rsrc(FMT == 0 ? (const void *)A.ut : A.st)};
     const int tb0 = (int)blockIdx.y * NB;
     float acc[NB][4];
 #pragma unroll
@@ -180,20 +245,20 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[b][r] = 0.0f;
     const int nc = A.nc, last = nc - 1;
-    MfChunk<NB, SH> ring[P];
+    MfChunk<FMT, NB, SH> ring[P];
 #pragma unroll
-    for (int i = 0; i < P; i++) mf_fetch<NB, SH>(A, R, is_tail, nib0, a_off, s_off, x_off, sx_off, tb0, wave, min(i, last), ring[i]);
+    for (int i = 0; i < P; i++) mf_fetch<FMT, HP, NB, SH>(A, R, L, is_tail, tb0, wave, min(i, last), ring[i]);
     int c0 = 0;
     for (; c0 + P <= nc; c0 += P) {
 #pragma unroll
         for (int i = 0; i < P; i++) {
-            mf_step<NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
-            mf_fetch<NB, SH>(A, R, is_tail, nib0, a_off, s_off, x_off, sx_off, tb0, wave, min(c0 + P + i, last), ring[i]);
+            mf_step<FMT, HP, NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
+            mf_fetch<FMT, HP, NB, SH>(A, R, L, is_tail, tb0, wave, min(c0 + P + i, last), ring[i]);
         }
     }
 #pragma unroll
     for (int i = 0; i < P - 1; i++)
-        if (c0 + i < nc) mf_step<NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
+        if (c0 + i < nc) mf_step<FMT, HP, NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
     if (stripe_id >= A.stripes) return;
 #pragma unroll
     for (int b = 0; b < NB; b++) {
@@ -211,10 +276,11 @@ __global__ __launch_bounds__(256) void gemm_nf4_mfma_kernel(MfArgs A) {
 
 // Tile-major copy of the activations: one 16-token x 64-column tile per 1 KB, in the
 // order the MFMA's B operand is read (lane l = 16g + t holds token t's columns 16g ..
-// 16g + 15), so each B load of a wave is 1 KB contiguous.  Tokens past ntok repeat the
-// last token.  One thread per 16 bytes; blockIdx.y is the 16-token block.
-__global__ __launch_bounds__(256) void mf_tile_kernel(const int8_t *xq, const float *xs, int K, int nc, int ntok,
-                                                      int8_t *xt, float *st) {
+// 16g + 15), so each B load of a wave is 1 KB contiguous, with the chunk scales (and
+// code sums, for bit planes) in 16-token groups.  Tokens past ntok repeat the last token.
+// One thread per 16 bytes; blockIdx.y is the 16-token block.
+__global__ __launch_bounds__(256) void mf_tile_kernel(const int8_t *xq, const float *xs, const int32_t *xsum, int K,
+                                                      int nc, int ntok, int8_t *xt, float *st, int32_t *ut) {
     const int c = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), tb = (int)blockIdx.y;
     if (c >= nc) return;
     const uint32_t lane = threadIdx.x & 63u, li = lane & 15u, lg = lane >> 4;
@@ -223,18 +289,31 @@ __global__ __launch_bounds__(256) void mf_tile_kernel(const int8_t *xq, const fl
     *reinterpret_cast<int4 *>(xt + tile * 1024 + lane * 16) =
         *reinterpret_cast<const int4 *>(xq + (size_t)tok * K + (size_t)c * 64 + 16 * lg);
     if (lg == 0) st[tile * 16 + li] = xs[(size_t)tok * nc + c];
+    if (lg == 1 && ut) ut[tile * 16 + li] = xsum[(size_t)tok * nc + c];
 }
 
 }  // namespace
 
-bool gemm_nf4_mfma_supported(const k2t_mat *m, int ntok) {
-    return m->fmt == K2T_FMT_NF && m->bits == 4 && ntok >= kMfmaMinTokens && m->cols % 64 == 0 &&
-           (m->sgc & (m->sgc - 1)) == 0;
+bool gemm_mfma_supported(const k2t_mat *m, int ntok) {
+    if (ntok < kMfmaMinTokens || m->cols % 64 != 0) return false;
+    if (m->fmt == K2T_FMT_NF) return m->bits == 4 && (m->sgc & (m->sgc - 1)) == 0;
+    return m->fmt == K2T_FMT_NIBBLE4 && m->hp >= 0 && m->hp <= 2;
 }
 
-void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, int ntok, float *out,
-                          size_t out_stride, bool accum, ActTiles tiles) {
-    if (!gemm_nf4_mfma_supported(m, ntok)) throw Error(K2T_E_INTERNAL, "mfma gemm: unsupported matrix");
+template <int FMT, int HP>
+static void launch_gemm_mfma_fmt(hipStream_t st, int nb, dim3 grid, const MfArgs &A) {
+    switch (nb) {
+        case 1: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 1, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
+        case 2: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 2, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
+        case 3: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 3, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
+        default: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 4, kMfmaShDepth, true>), grid, dim3(256), 0, st, A); break;
+    }
+}
+
+void launch_gemm_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum,
+                      int ntok, float *out, size_t out_stride, bool accum, ActTiles tiles) {
+    if (!gemm_mfma_supported(m, ntok)) throw Error(K2T_E_INTERNAL, "mfma gemm: unsupported matrix");
+    const bool planes = m->fmt == K2T_FMT_NIBBLE4;
     MfArgs A{};
     A.pair = m->pair;
     A.tail = m->tail;
@@ -243,24 +322,27 @@ void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, cons
     A.nc = m->nc;
     A.np = m->pairs;
     A.stripes = m->stripes;
-    A.sgc_log2 = __builtin_ctz((unsigned)m->sgc);
-    nf4_xor_tables(m->cb[0], m->cb[1], m->cb[2], m->cb[3], A.t0, A.t1, A.u0, A.u1);
+    A.sgc_log2 = planes ? 0 : __builtin_ctz((unsigned)m->sgc);
+    if (!planes) nf4_xor_tables(m->cb[0], m->cb[1], m->cb[2], m->cb[3], A.t0, A.t1, A.u0, A.u1);
     // The tile-major copy: from the activation's producer, else made here in the
-    // context's scratch (1 KB + 64 B per tile).
+    // context's scratch (1 KB + 64 B of scales + 64 B of code sums per tile).
     const int blocks = (ntok + 15) / 16;
     int8_t *xt = tiles.xt;
     float *stile = tiles.st;
-    if (!xt) {
+    int32_t *utile = tiles.ut;
+    if (!xt || (planes && !utile)) {
         const size_t ntile = (size_t)blocks * m->nc;
-        ensure_scratch(ctx, ntile * (1024 + 64) / sizeof(float));
+        ensure_scratch(ctx, ntile * (1024 + 64 + 64) / sizeof(float));
         xt = reinterpret_cast<int8_t *>(ctx->scratch);
         stile = ctx->scratch + ntile * 256;
-        hipLaunchKernelGGL(mf_tile_kernel, dim3((m->nc + 3) / 4, blocks), dim3(256), 0, ctx->stream, xq, xs, m->cols,
-                           m->nc, ntok, xt, stile);
+        utile = reinterpret_cast<int32_t *>(ctx->scratch + ntile * 272);
+        hipLaunchKernelGGL(mf_tile_kernel, dim3((m->nc + 3) / 4, blocks), dim3(256), 0, ctx->stream, xq, xs, xsum,
+                           m->cols, m->nc, ntok, xt, stile, planes ? utile : nullptr);
     }
     A.xt = xt;
     A.nblk = blocks;
     A.st = stile;
+    A.ut = utile;
     A.K = m->cols;
     A.ntok = ntok;
     A.out = out;
@@ -272,12 +354,10 @@ void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, cons
     while (nb > 1 && (long)m->stripes * ((blocks + nb - 1) / nb) < kMfmaMinWaves) nb = nb > 2 ? 2 : 1;
     const dim3 grid((m->stripes + 3) / 4, (ntok + 16 * nb - 1) / (16 * nb));
     hipStream_t st = ctx->stream;
-    switch (nb) {
-        case 1: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<1, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
-        case 2: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<2, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
-        case 3: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<3, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
-        default: hipLaunchKernelGGL((gemm_nf4_mfma_kernel<4, kMfmaShDepth, true>), grid, dim3(256), 0, st, A); break;
-    }
+    if (!planes) launch_gemm_mfma_fmt<1, 0>(st, nb, grid, A);
+    else if (m->hp == 0) launch_gemm_mfma_fmt<0, 0>(st, nb, grid, A);
+    else if (m->hp == 1) launch_gemm_mfma_fmt<0, 1>(st, nb, grid, A);
+    else launch_gemm_mfma_fmt<0, 2>(st, nb, grid, A);
     hip_check(hipGetLastError(), "mfma gemm launch");
 }
 

@@ -952,8 +952,8 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
     // 16 or more tokens of a ready activation through an NF4 matrix: the matrix-core
     // kernel (one weight pass per 64 tokens; its outputs equal the exact-order GEMV's)
     if (!dots && !grp && xsm == 0 && gu_split == 0 && s0 == 0 && s1 == m->stripes && ctx->mfma &&
-        gemm_nf4_mfma_supported(m, ntok)) {
-        launch_gemm_nf4_mfma(ctx, m, xq, xs, ntok, out, out_stride, accum, tiles);
+        gemm_mfma_supported(m, ntok)) {
+        launch_gemm_mfma(ctx, m, xq, xs, xsum, ntok, out, out_stride, accum, tiles);
         return;
     }
     const int saved = ctx->max_segments;

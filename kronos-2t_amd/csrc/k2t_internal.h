@@ -128,17 +128,18 @@ struct GemvGroup {
 struct ActTiles {
     int8_t *xt = nullptr;
     float *st = nullptr;
+    int32_t *ut = nullptr;  // the chunks' code sums (read by bit-plane matrices)
 };
 void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum, int ntok,
                     float *out, size_t out_stride, bool accumulate, int gu_split = 0, ActTiles tiles = ActTiles{});
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
                        bool exact, ActTiles tiles = ActTiles{});
-// Batched NF4 GEMV on the matrix cores (k2t_gemm_mfma.hip): kMfmaMinTokens or more tokens
-// of a ready int8 activation, outputs equal to the exact-order GEMV's.
+// Batched NF4 / bit-plane GEMV on the matrix cores (k2t_gemm_mfma.hip): kMfmaMinTokens or
+// more tokens of a ready int8 activation, outputs equal to the exact-order GEMV's.
 constexpr int kMfmaMinTokens = 16;
-bool gemm_nf4_mfma_supported(const k2t_mat *m, int ntok);
-void launch_gemm_nf4_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, int ntok, float *out,
-                          size_t out_stride, bool accum, ActTiles tiles = ActTiles{});
+bool gemm_mfma_supported(const k2t_mat *m, int ntok);
+void launch_gemm_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum,
+                      int ntok, float *out, size_t out_stride, bool accum, ActTiles tiles = ActTiles{});
 void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, int xs_mode, const float *src,
                          const float *w, float eps, float *out);
 

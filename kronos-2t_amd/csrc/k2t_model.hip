@@ -132,7 +132,7 @@ __global__ __launch_bounds__(64) void rmsnorm_act_kernel(const float *__restrict
     const float v = (xt[c * 64 + lane] * inv_rms) * w[c * 64 + lane];
     const size_t gc = (size_t)tok * (K / 64) + c;
     quant_chunk_store(fwht_lane(v, (uint64_t)c, lane), lane, q + gc * 64, scales + gc, sums + gc, tiles.xt, tiles.st,
-                      tok, c, K / 64);
+                      tiles.ut, tok, c, K / 64);
 }
 
 void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float eps, int K, int ntok, int8_t *q,
@@ -556,8 +556,8 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
             if (out_f) out_f[hbase + wv * 64 + lane] = o;
             if (aq) {
                 const size_t c = (size_t)head * nb + wv, g = (size_t)tok * nq * nb + c;
-                quant_chunk_store(fwht_lane(o, c, lane), lane, aq + g * 64, as + g, asum + g, tiles.xt, tiles.st, tok,
-                                  (int)c, nq * nb);
+                quant_chunk_store(fwht_lane(o, c, lane), lane, aq + g * 64, as + g, asum + g, tiles.xt, tiles.st,
+                                  tiles.ut, tok, (int)c, nq * nb);
             }
         }
         return;
@@ -656,11 +656,11 @@ __device__ __forceinline__ void merge_head(const float *pp, int ns, int nq, int 
         const int nc_tok = nq * nb;  // o_proj input chunks per token
         const size_t c0 = (size_t)head * nb;
         const size_t g0 = (size_t)tok * nc_tok + c0;
-        quant_chunk_store(fwht_lane(o0, c0, lane), lane, aq + g0 * 64, as + g0, asum + g0, tiles.xt, tiles.st, tok,
-                          (int)c0, nc_tok);
+        quant_chunk_store(fwht_lane(o0, c0, lane), lane, aq + g0 * 64, as + g0, asum + g0, tiles.xt, tiles.st,
+                          tiles.ut, tok, (int)c0, nc_tok);
         if (nb > 1)
             quant_chunk_store(fwht_lane(o1, c0 + 1, lane), lane, aq + (g0 + 1) * 64, as + g0 + 1, asum + g0 + 1, tiles.xt,
-                              tiles.st, tok, (int)c0 + 1, nc_tok);
+                              tiles.st, tiles.ut, tok, (int)c0 + 1, nc_tok);
     }
 }
 
@@ -1327,8 +1327,8 @@ __global__ __launch_bounds__(64) void swiglu_act_kernel(const float *__restrict_
     const float g = b[lane], u = b[64 + lane];
     const float v = (g / (1.0f + (EXACT ? expf_rn(-g) : expf(-g)))) * u;
     const size_t gc = (size_t)tok * nci + ic;
-    quant_chunk_store(fwht_lane(v, (uint64_t)ic, lane), lane, q + gc * 64, s + gc, sums + gc, tiles.xt, tiles.st, tok,
-                      ic, nci);
+    quant_chunk_store(fwht_lane(v, (uint64_t)ic, lane), lane, q + gc * 64, s + gc, sums + gc, tiles.xt, tiles.st,
+                      tiles.ut, tok, ic, nci);
 }
 
 void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,

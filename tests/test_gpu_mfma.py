@@ -14,7 +14,7 @@ import pytest
 
 import k2t
 import oracle as O
-from helpers import acts, quantized_nf4
+from helpers import acts, quantized_nf4, quantized_nibble4
 
 pytestmark = pytest.mark.gpu
 
@@ -59,21 +59,47 @@ def test_mfma_gemv_equals_reference_chain(gpu_ctx, rows, cols, sgc, ntok):
     m.close()
 
 
-@pytest.mark.parametrize("max_seq", [64, 1100])
-def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, max_seq):
-    """A 2-layer nf4 model (d 256, 4 heads of 64, ffn 768): a 40-token prefill (qkv, o
-    with the residual add, gate_up and down with the residual add on the matrix cores) in
+@pytest.mark.parametrize("planes,rows,cols,ntok", [(4, 1040, 2048, 16), (5, 96, 1536, 100), (6, 2048, 576, 64),
+                                                   (4, 1536, 4096, 256), (6, 1040, 1536, 33)])
+def test_mfma_bitplane_gemv_equals_reference_chain(gpu_ctx, planes, rows, cols, ntok):
+    """Bit-plane matrices (b4 / b5 / b6, Nibble4SdotMatrix; rows % 32 == 16 has a tail
+    stripe): every output bit-identical to the oracle's per-token chain of the odd-weight
+    dots 2 * sum(u x) - max_odd * sum(x) (simd_lut.rs:4030-4045, 4304-4309), in both modes."""
+    print(f"mfma bit-plane gemv b{planes} {rows}x{cols} ntok {ntok}", flush=True)
+    rng = np.random.default_rng(planes * 1000 + rows + ntok)
+    _, _, _, pair, tail = quantized_nibble4(rng, rows, cols, planes)
+    hp = planes - 4
+    m = gpu_ctx.upload_nibble4(rows, cols, hp, pair, tail)
+    xq, xs, xsum = acts(rng, cols, ntok, outlier_frac=0.001, outlier_scale=30.0)
+    xs[min(3, ntok - 1), 1] = 0.0
+    xq[min(3, ntok - 1), 64:128] = 0
+    xsum[min(3, ntok - 1), 1] = 0
+    ref = np.stack([O.nibble4_gemv(pair, tail, rows, cols, hp, xq[t], xs[t], xsum[t]) for t in range(ntok)])
+    for exact in (False, True):
+        out = _batch(gpu_ctx, m, xq, xs, xsum, rows, ntok, exact)
+        bad = np.argwhere(out.view(np.uint32) != ref.view(np.uint32))
+        assert bad.size == 0, f"exact={exact}: {len(bad)} outputs differ, first {bad[:3].tolist()}"
+    m.close()
+
+
+@pytest.mark.parametrize("fmt,planes,max_seq", [("nf4", None, 64), ("nf4", None, 1100), ("n4", "p55454", 64),
+                                                ("n4", "b6", 64)])
+def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_seq):
+    """A 2-layer model (d 256, 4 heads of 64, ffn 768; nf4, p55454 and b6 weights): a
+    40-token prefill (qkv, o with the residual add, gate_up and down with the residual
+    add on the matrix cores) in
     exact-order mode equals the oracle bit for bit, and so does the one with the matrix
     cores off; in fast mode the activation tiles written by their producers (RMSNorm,
     attention, SwiGLU) give the same logits as tiles copied by the GEMV, within the fast
     path's bar of the oracle.  max_seq 1100 takes the split attention and its merge
     kernel (the activation's producer for o_proj there)."""
     from model_oracle import OracleModel, random_model
-    from test_gpu_model import _close, _gpu_model
-    print(f"mfma prefill vs oracle, max_seq {max_seq}", flush=True)
+    from test_gpu_model import P55454, _close, _gpu_model
+    print(f"mfma prefill vs oracle, {fmt} {planes} max_seq {max_seq}", flush=True)
+    plane_map = {"p55454": P55454, "b6": {k: 6 for k in P55454}, None: None}[planes]
     cfg = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, intermediate=768, vocab=520,
                max_seq=max_seq, rms_eps=1e-5, rope_theta=10000.0)
-    layers, head, fn = random_model(cfg, seed=41, fmt="nf4")
+    layers, head, fn = random_model(cfg, seed=41, fmt=fmt, planes=plane_map)
     ref = OracleModel(cfg, layers, head, fn)
     toks = np.random.default_rng(42).integers(0, cfg["vocab"], 40)
     for t in toks[:-1]:
