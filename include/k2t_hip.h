@@ -165,7 +165,12 @@ int32_t k2t_act_quant_rmsnorm(k2t_ctx *ctx, const float *d_x, const float *d_nor
  * Weights are read once per 4 tokens.  d_xsum is required for bit-plane
  * matrices and ignored for NF ones.  Per-(row, chunk) integer dots are exact;
  * with split-K disabled the fp32 result is bit-identical to the reference's
- * in-order fmaf epilogue. */
+ * in-order fmaf epilogue.  16 or more tokens over the whole matrix (NF4 or bit
+ * planes, k2t_ctx_set_mfma): one weight pass per 64 tokens on the matrix
+ * cores, outputs bit-identical to that epilogue in either mode; such a call
+ * copies the activation into the context's scratch, which it grows first if it
+ * is too small (a synchronous allocation, so the first such call of a size
+ * must not be inside a stream capture). */
 int32_t k2t_gemv(k2t_ctx *ctx, const k2t_mat *m, const int8_t *d_xq, const float *d_xs,
                  const int32_t *d_xsum, int32_t ntok, int32_t s0, int32_t s1, float *d_out,
                  size_t out_stride);
