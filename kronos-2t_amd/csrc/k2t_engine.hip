@@ -31,7 +31,8 @@ void launch_attention_exact(hipStream_t st, const float *q, int q_stride, const 
 void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, int8_t *vq, float *ks, float *vs,
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale, int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as,
-                      int32_t *asum, const GqaWork &gqa, int ctx_bound = 0, ActTiles tiles = ActTiles{});
+                      int32_t *asum, const GqaWork &gqa, int ctx_bound = 0, ActTiles tiles = ActTiles{},
+                      bool mfma = false);
 int attn_max_splits(int max_seq);
 int gqa_spans(int cap);
 void launch_embed(hipStream_t st, const k2t_mat *m, const int *tokens, int ntok, float *out);
@@ -410,7 +411,7 @@ void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
         const ActTiles to = act_tiles_for(m, L.o, ntok);  // (none for one token: the grouped kernel writes none)
         launch_attention(st, m->qkv, (nq + 2 * nkv) * hd, m->kq, m->vq, m->ks, m->vs, post, m->pos_dev, l, nq, nkv,
                          hd, m->ring, attn_scale, nsplit, ntok, m->attn_part, nullptr, m->xq, m->xs, m->xsum,
-                         GqaWork{m->attn_words, m->attn_cnt, m->err_dev}, ctx_bound, to);
+                         GqaWork{m->attn_words, m->attn_cnt, m->err_dev}, ctx_bound, to, ctx->mfma != 0);
         launch_gemv_ex(ctx, L.o, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true, 0, to);
         if (L.has_moe) {
             // one token at a time: each token has its own routes (forward_layer_single)

@@ -573,6 +573,177 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
     }
 }
 
+// ---------------------------------------------------------------- prefill attention on the matrix cores
+// A batch of 16 or more tokens over the int8 cache without a window (fast mode).  One
+// workgroup per (q head, 16-token query block), 4 waves; wave w takes the 16-position
+// tiles w, w + 4, ... of the positions the block attends to, with an online softmax,
+// and the workgroup merges its waves' (max, sum, o) in wave order at the end.  Per tile:
+//  - scores: v_mfma_i32_16x16x64_i8 with A = K (16 positions x 64 dims, lane l row l%16)
+//    and B = the block's int8 q heads (64 dims x 16 tokens): exact integer dots, lane l
+//    holding positions 4(l/16) + r of token l%16; s = (float(dot) * ks) * (qs * scale) as
+//    causal_gqa_group_q8 (real_llm.rs:8471-8594);
+//  - o: four v_mfma_f32_16x16x4f32 per 16 dims, the r-th over positions r, 4 + r, 8 + r,
+//    12 + r, with A = V^T (lane l: dim l%16, position 4(l/16) + r) and B = (p * vs)^T
+//    (lane l: position 4(l/16) + r, token l%16), which is the score tile's own layout,
+//    so no lane exchange is needed; o^T accumulates in fp32 (lane l: dims 4(l/16) + r
+//    of token l%16).  (fp16 weights in a 16x16x16 MFMA cost a quarter of the MFMAs but
+//    left 2-layer logits at cosine 0.99989 against the oracle, under the fast path's
+//    0.9999.)
+// The sums run in tile order: the outputs are close to, not bit-equal with, the one-token
+// kernel's, which a batch of fewer than 16 tokens still uses.  q quantization and the
+// closing ifwht64 / FWHT + int8 of the o_proj chunk are the whole-context kernel's.
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__restrict__ q, int q_stride,
+                                                                const int8_t *__restrict__ kq,
+                                                                const int8_t *__restrict__ vq,
+                                                                const float *__restrict__ ks,
+                                                                const float *__restrict__ vs,
+                                                                const int *__restrict__ pos_dev, int layer, int nq,
+                                                                int nkv, int cap, float attn_scale, int ntok,
+                                                                float *__restrict__ out_f, int8_t *__restrict__ aq,
+                                                                float *__restrict__ as, int32_t *__restrict__ asum,
+                                                                ActTiles tiles) {
+    constexpr int NB = HD / 64;  // 64-dim blocks
+    constexpr int DB = HD / 16;  // 16-dim output blocks
+    __shared__ __align__(16) int8_t qi[16][HD];
+    __shared__ float qas_s[16];
+    __shared__ float wm[4][16], wl[4][16];  // per wave and token: running max and sum
+    __shared__ float wo[4][16][HD + 1];     // per wave: o[token][dim] (padded rows)
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int head = blockIdx.x, tb = blockIdx.y, t0 = tb * 16;
+    const int kvh = head / (nq / nkv);
+    const int pos0 = pos_dev[0];
+    // 1. the block's q heads rotated and quantized (as the whole-context kernel): wave w
+    //    takes tokens w, w + 4, w + 8, w + 12 (tokens past the batch repeat the last one)
+    for (int j = (int)wave; j < 16; j += 4) {
+        const int tok = min(t0 + j, ntok - 1);
+        const float *qh = q + (size_t)tok * q_stride + (size_t)head * HD;
+        const float r0 = fwht_lane(qh[lane], 0, lane);
+        const float r1 = NB > 1 ? fwht_lane(qh[64 + lane], 1, lane) : 0.0f;
+        const float mx = wave_max_f(fmaxf(fabsf(r0), fabsf(r1)));
+        float qs = 0.0f;
+        if (mx <= FLT_EPSILON) {
+            qi[j][lane] = 0;
+            if (NB > 1) qi[j][64 + lane] = 0;
+        } else {
+            const float inv = 127.0f / mx;
+            qi[j][lane] = (int8_t)(int)rintf(r0 * inv);
+            if (NB > 1) qi[j][64 + lane] = (int8_t)(int)rintf(r1 * inv);
+            qs = mx / 127.0f;
+        }
+        if (lane == 0) qas_s[j] = qs * attn_scale;
+    }
+    __syncthreads();
+    const uint32_t li = lane & 15u, lg = lane >> 4;
+    // B operand of the score MFMA: token li's dims 64k + 16 lg .. + 15
+    v4i_t qb[NB];
+#pragma unroll
+    for (int k = 0; k < NB; k++) {
+        const int4 v = *reinterpret_cast<const int4 *>(&qi[li][64 * k + 16 * lg]);
+        qb[k] = v4i_t{v.x, v.y, v.z, v.w};
+    }
+    const float qas = qas_s[li];
+    const int my_tok = t0 + (int)li;          // this lane's token (column of every tile)
+    const int my_last = pos0 + my_tok;        // the last position it attends to
+    const int n_att = pos0 + min(t0 + 16, ntok);  // positions any token of the block attends to
+    const size_t base = ((size_t)layer * nkv + kvh) * cap;
+    float m = -INFINITY, l = 0.0f;
+    v4f o[DB];
+#pragma unroll
+    for (int b = 0; b < DB; b++) o[b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int p0 = 16 * (int)wave; p0 < n_att; p0 += 64) {
+        // scores of positions p0 + 4 lg + r for token li
+        v4i_t acc = {0, 0, 0, 0};
+        const int prow = min(p0 + (int)li, n_att - 1);  // K row of this lane (A operand)
+#pragma unroll
+        for (int k = 0; k < NB; k++) {
+            const int4 kv = *reinterpret_cast<const int4 *>(kq + (base + prow) * HD + 64 * k + 16 * lg);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i_t{kv.x, kv.y, kv.z, kv.w}, qb[k], acc, 0, 0, 0);
+        }
+        const int pr = p0 + 4 * (int)lg;  // this lane's first position
+        float sc[4], vsc[4];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int p = pr + r;
+            const bool live = p <= my_last && p < n_att;
+            const int pc = min(p, n_att - 1);
+            sc[r] = live ? ((float)acc[r] * ks[base + pc]) * qas : -INFINITY;
+            vsc[r] = vs[base + pc];
+            tmax = fmaxf(tmax, sc[r]);
+        }
+        tmax = fmaxf(tmax, xor_lane(tmax, 16));
+        tmax = fmaxf(tmax, xor_lane(tmax, 32));
+        const float mn = fmaxf(m, tmax);
+        // (mn = -inf: every position so far masked; nothing accumulated yet)
+        const float corr = mn == -INFINITY ? 1.0f : expf(m - mn);
+        float psum = 0.0f, w[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float pw = sc[r] == -INFINITY ? 0.0f : expf(sc[r] - mn);
+            psum += pw;
+            w[r] = pw * vsc[r];
+        }
+        psum += xor_lane(psum, 16);
+        psum += xor_lane(psum, 32);
+        l = l * corr + psum;
+        m = mn;
+        // o^T += V^T * (p vs)^T: A lane l = dim 16 b + li, position pr + r
+#pragma unroll
+        for (int b = 0; b < DB; b++) {
+            o[b] = o[b] * corr;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int pc = min(pr + r, n_att - 1);
+                const float a = (float)vq[(base + pc) * HD + 16 * b + li];
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, w[r], o[b], 0, 0, 0);
+            }
+        }
+    }
+    // 2. merge the waves in order: per token the largest max, then the rescaled sums
+    if (lg == 0) {
+        wm[wave][li] = m;
+        wl[wave][li] = l;
+    }
+#pragma unroll
+    for (int b = 0; b < DB; b++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) wo[wave][li][16 * b + 4 * lg + r] = o[b][r];
+    __syncthreads();
+    for (int j = (int)wave; j < 16; j += 4) {
+        const int tok = t0 + j;
+        if (tok >= ntok) break;  // wave-uniform
+        float M = -INFINITY;
+#pragma unroll
+        for (int w2 = 0; w2 < 4; w2++) M = fmaxf(M, wm[w2][j]);
+        float L = 0.0f, e[4];
+#pragma unroll
+        for (int w2 = 0; w2 < 4; w2++) {
+            e[w2] = wm[w2][j] == -INFINITY ? 0.0f : expf(wm[w2][j] - M);
+            L = fmaf(wl[w2][j], e[w2], L);
+        }
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int blk = 0; blk < NB; blk++) {
+            float acc_o = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < 4; w2++) acc_o = fmaf(wo[w2][j][64 * blk + lane], e[w2], acc_o);
+            const float ov = ifwht_lane(acc_o * inv, (uint64_t)blk, lane);
+            const size_t hbase = (size_t)tok * nq * HD + (size_t)head * HD;
+            if (out_f) out_f[hbase + 64 * blk + lane] = ov;
+            if (aq) {
+                const size_t c = (size_t)head * NB + blk, g = (size_t)tok * nq * NB + c;
+                quant_chunk_store(fwht_lane(ov, c, lane), lane, aq + g * 64, as + g, asum + g, tiles.xt, tiles.st,
+                                  tiles.ut, tok, (int)c, nq * NB);
+            }
+        }
+    }
+}
+
 // Combines the splits of one (token, q head), applies ifwht64 (real_llm.rs:8588-8592), and
 // optionally re-rotates each 64-block with its o_proj chunk index and quantizes it
 // (populate_chunk_fwht_raw(None), real_llm.rs:7060-7084) -> the o_proj activation.
@@ -1166,7 +1337,18 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
                       const AttnPost &post, const int *pos_dev, int layer, int nq, int nkv, int hd, KvRing kr,
                       float attn_scale,
                       int nsplit, int ntok, float *part, float *out_f, int8_t *aq, float *as, int32_t *asum,
-                      const GqaWork &gqa, int ctx_bound, ActTiles tiles) {
+                      const GqaWork &gqa, int ctx_bound, ActTiles tiles, bool mfma) {
+    if (mfma && ntok >= 16 && !post.on && kr.bits == 8 && kr.window == 0 && kr.ring == 0 && (hd == 64 || hd == 128)) {
+        const dim3 grid(nq, (ntok + 15) / 16);
+        if (hd == 128)
+            hipLaunchKernelGGL(attn_prefill_mfma_kernel<128>, grid, dim3(256), 0, st, q, q_stride, kq, vq, ks, vs,
+                               pos_dev, layer, nq, nkv, kr.cap, attn_scale, ntok, out_f, aq, as, asum, tiles);
+        else
+            hipLaunchKernelGGL(attn_prefill_mfma_kernel<64>, grid, dim3(256), 0, st, q, q_stride, kq, vq, ks, vs,
+                               pos_dev, layer, nq, nkv, kr.cap, attn_scale, ntok, out_f, aq, as, asum, tiles);
+        hip_check(hipGetLastError(), "prefill attention launch");
+        return;
+    }
     if (nsplit == 1 && ctx_bound > 0 && ctx_bound <= kAttnSmall) {
         // every token of the batch attends to at most kAttnSmall positions: a quarter of the
         // threads, the whole-context kernel's sums (its V position subsets) bit for bit
