@@ -56,6 +56,12 @@ constexpr int kMfmaDepth = K2T_MFMA_DEPTH;         // chunks in flight per wave 
 #endif
 constexpr int kMfmaShDepth = K2T_MFMA_SH_DEPTH;    // the same, kernels sharing activation blocks
 constexpr long kMfmaMinWaves = K2T_MFMA_MIN_WAVES;  // 8 waves per CU
+#ifndef K2T_MFMA_MAX_BLOCKS
+#define K2T_MFMA_MAX_BLOCKS 4
+#endif
+// 16-token blocks per wave: 4, or 8 in a measurement build (16384 x 2048 at 256 tokens:
+// 40.0 -> 41.0 us at 188 VGPRs; 1.7B prefill unchanged)
+constexpr int kMfmaMaxBlocks = K2T_MFMA_MAX_BLOCKS;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -82,7 +88,7 @@ struct MfChunk {
     uint32_t d0, d1;
     uint32_t hv;  // bit planes with hi planes: this lane's hi-plane dword
     uint2 sw;
-    int4 x[SH ? 1 : NB];
+    int4 x[SH ? (NB + 3) / 4 : NB];  // with sharing: blocks wave, wave + 4
     float sx[NB];
     int32_t su[FMT == 0 ? NB : 1];  // bit planes: the tokens' code sums
 };
@@ -133,9 +139,9 @@ __device__ __forceinline__ void mf_fetch(const MfArgs &A, const MfSrc &R, const 
     for (int b = 0; b < NB; b++) {
         // blocks past the last repeat it; their outputs are never stored
         const uint32_t tile = (uint32_t)min(tb0 + b, A.nblk - 1) * (uint32_t)A.nc + (uint32_t)c;
-        if (!SH || b == (int)wave) {  // with sharing, waves >= NB load no block
+        if (!SH || b % 4 == (int)wave) {  // with sharing, wave w loads blocks w, w + 4
             const v4u x = __builtin_amdgcn_raw_buffer_load_b128(R.x, L.x_off, tile * 1024u, 0);
-            f.x[SH ? 0 : b] = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
+            f.x[SH ? b / 4 : b] = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
         }
         f.sx[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(R.s, L.sx_off, tile * 64u, 0));
         if constexpr (FMT == 0) f.su[b] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(R.u, L.sx_off, tile * 64u, 0);
@@ -154,7 +160,9 @@ template <int FMT, int HP, int NB, bool SH>
 __device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<FMT, NB, SH> &f, float (&acc)[NB][4],
                                         int4 *bsh, uint32_t wave, uint32_t lane) {
     if (SH) {
-        if (wave < (uint32_t)NB) bsh[wave * 64 + lane] = f.x[0];
+#pragma unroll
+        for (int k = 0; k < (NB + 3) / 4; k++)
+            if ((int)wave + 4 * k < NB) bsh[(wave + 4 * k) * 64 + lane] = f.x[k];
         __syncthreads();
     }
     v4i a;
@@ -306,7 +314,11 @@ static void launch_gemm_mfma_fmt(hipStream_t st, int nb, dim3 grid, const MfArgs
         case 1: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 1, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
         case 2: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 2, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
         case 3: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 3, kMfmaDepth, false>), grid, dim3(256), 0, st, A); break;
-        default: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 4, kMfmaShDepth, true>), grid, dim3(256), 0, st, A); break;
+        case 4: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 4, kMfmaShDepth, true>), grid, dim3(256), 0, st, A); break;
+        default:
+            if constexpr (kMfmaMaxBlocks >= 8)
+                hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 8, kMfmaShDepth, true>), grid, dim3(256), 0, st, A);
+            break;
     }
 }
 
@@ -350,8 +362,9 @@ void launch_gemm_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const fl
     A.accum = accum ? 1 : 0;
     // Tokens per wave: the most 16-token blocks (fewest weight passes) that still give
     // the launch kMfmaMinWaves waves.
-    int nb = std::min(4, blocks);
-    while (nb > 1 && (long)m->stripes * ((blocks + nb - 1) / nb) < kMfmaMinWaves) nb = nb > 2 ? 2 : 1;
+    int nb = std::min(kMfmaMaxBlocks, blocks);
+    if (nb > 4 && nb < 8) nb = 4;
+    while (nb > 1 && (long)m->stripes * ((blocks + nb - 1) / nb) < kMfmaMinWaves) nb = nb > 4 ? 4 : nb > 2 ? 2 : 1;
     const dim3 grid((m->stripes + 3) / 4, (ntok + 16 * nb - 1) / (16 * nb));
     hipStream_t st = ctx->stream;
     if (!planes) launch_gemm_mfma_fmt<1, 0>(st, nb, grid, A);
