@@ -59,6 +59,37 @@ def test_mfma_gemv_equals_reference_chain(gpu_ctx, rows, cols, sgc, ntok):
     m.close()
 
 
+def test_mfma_gemv_strided_output_scale_groups_and_modes(gpu_ctx):
+    """Output rows wider than the matrix (out_stride > rows: the gap stays untouched), NF4
+    with 4-chunk scale groups (matrix cores) and 3-chunk groups (not a power of two: the
+    4-token passes), both bit-identical to the oracle's chain in exact mode; an invalid
+    k2t_ctx_set_mfma mode is refused."""
+    import torch
+    import k2t
+    rng = np.random.default_rng(77)
+    ntok = 20
+    for rows, cols, sgc in [(64, 1024, 4), (48, 576, 3)]:
+        _, cb, _, _, pair, tail = quantized_nf4(rng, rows, cols, sgc)
+        m = gpu_ctx.upload_nf(rows, cols, 4, sgc, cb, pair, tail)
+        xq, xs, xsum = acts(rng, cols, ntok)
+        ref = np.stack([O.nf_gemv(pair, tail, rows, cols, 4, sgc, cb, xq[t], xs[t]) for t in range(ntok)])
+        stride = rows + 13
+        out = torch.full((ntok, stride), 7.0, dtype=torch.float32, device="cuda")
+        gpu_ctx.set_exact(True)
+        try:
+            gpu_ctx.gemv(m, _t(xq), _t(xs), _t(xsum), out, ntok=ntok, out_stride=stride)
+            gpu_ctx.sync()
+        finally:
+            gpu_ctx.set_exact(False)
+        o = out.cpu().numpy()
+        assert np.array_equal(o[:, :rows].view(np.uint32), ref.view(np.uint32)), (rows, cols, sgc)
+        assert np.all(o[:, rows:] == 7.0)
+        m.close()
+    with pytest.raises(k2t.K2TError):
+        gpu_ctx.set_mfma(3)
+    gpu_ctx.set_mfma(1)
+
+
 @pytest.mark.parametrize("planes,rows,cols,ntok", [(4, 1040, 2048, 16), (5, 96, 1536, 100), (6, 2048, 576, 64),
                                                    (4, 1536, 4096, 256), (6, 1040, 1536, 33)])
 def test_mfma_bitplane_gemv_equals_reference_chain(gpu_ctx, planes, rows, cols, ntok):
