@@ -117,15 +117,14 @@ def test_mfma_bitplane_gemv_equals_reference_chain(gpu_ctx, planes, rows, cols, 
                                                    ("n4", "p55454", 64, 64), ("n4", "b6", 64, 64),
                                                    ("nf4", None, 300, 128)])
 def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_seq, hd):
-    """A 2-layer model (d 256, 4 heads of 64, ffn 768; nf4, p55454 and b6 weights): a
-    40-token prefill (qkv, o with the residual add, gate_up and down with the residual
-    add on the matrix cores) in
-    exact-order mode equals the oracle bit for bit, and so does the one with the matrix
-    cores off; in fast mode the activation tiles written by their producers (RMSNorm,
-    attention, SwiGLU) give the same logits as tiles copied by the GEMV, within the fast
-    path's bar of the oracle.  In fast mode the batch's attention runs on the matrix
-    cores (attn_prefill_mfma_kernel, hd 64 and 128); with the matrix cores off, max_seq
-    1100 takes the split attention and its merge kernel in exact mode."""
+    """A 2-layer model (d 256, 256 / hd heads of hd 64 or 128, ffn 768; nf4, p55454 and b6
+    weights): a 40-token prefill (qkv, o with the residual add, gate_up and down with the
+    residual add on the matrix cores) in exact-order mode equals the oracle bit for bit,
+    and so does the one with the matrix cores off, and one of 20 + 20 tokens (the second
+    batch appended at position 20).  In fast mode the batch's attention also runs on the
+    matrix cores (attn_prefill_mfma_kernel), and the activation tiles written by their
+    producers (RMSNorm, attention, SwiGLU) give the same logits as tiles copied by the
+    GEMV, within the fast path's bar of the oracle, for one batch and for 20 + 20."""
     from model_oracle import OracleModel, random_model
     from test_gpu_model import P55454, _close, _gpu_model
     print(f"mfma prefill vs oracle, {fmt} {planes} max_seq {max_seq} hd {hd}", flush=True)
@@ -146,6 +145,10 @@ def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_
             gm.reset()
             pre = gm.prefill(toks, want_logits=True)
             assert np.array_equal(pre.view(np.uint32), b.view(np.uint32)), f"mfma={mfma}"
+        gm.reset()
+        gm.prefill(toks[:20], want_logits=False)
+        pre = gm.prefill(toks[20:], want_logits=True)
+        assert np.array_equal(pre.view(np.uint32), b.view(np.uint32)), "20 + 20"
         gm.set_exact(False)
         fast = {}
         for mode in (1, 2):  # tiles written by the activations' producers / copied by the GEMV
@@ -155,6 +158,11 @@ def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_
         assert np.array_equal(fast[1].view(np.uint32), fast[2].view(np.uint32))
         ok, info = _close(fast[1], b, 0.9999)
         assert ok, info
+        gpu_ctx.set_mfma(1)
+        gm.reset()
+        gm.prefill(toks[:20], want_logits=False)
+        ok, info = _close(gm.prefill(toks[20:], want_logits=True), b, 0.9999)
+        assert ok, ("20 + 20", info)
     finally:
         gpu_ctx.set_mfma(True)
         gm.close()
