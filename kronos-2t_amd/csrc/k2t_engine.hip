@@ -232,6 +232,7 @@ struct k2t_model {
     int8_t *xt = nullptr;
     float *st = nullptr;
     int32_t *ut = nullptr;
+    ActTiles dtiles;  // the down input's tiles when gate_up's epilogue writes them (apart from xt)
     int pos = 0;
     bool use_graph = true;
     // 1: exact-order steps (the x86 reference's operation order throughout: in-order GEMV
@@ -424,9 +425,16 @@ void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
         } else {
             const ActTiles tg = act_tiles_for(m, L.gu, ntok), td = act_tiles_for(m, L.down, ntok);
             launch_rmsnorm_act(st, m->hidden, L.post_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum, tg);
-            launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false, 0, tg);
-            launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum, false, td);
-            launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true, 0, td);
+            // gate_up with the SwiGLU epilogue when both GEMVs take producer tiles (the
+            // gate_up kernel reads only tg, so it may overwrite xq; its tiles go apart)
+            if (tg.xt && td.xt &&
+                launch_gemm_mfma_swiglu(ctx, L.gu, tg, ntok, m->xq, m->xs, m->xsum, m->dtiles)) {
+                launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true, 0, m->dtiles);
+            } else {
+                launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false, 0, tg);
+                launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum, false, td);
+                launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true, 0, td);
+            }
         }
     }
     if (with_logits) {
@@ -749,6 +757,9 @@ int32_t k2t_model_create(k2t_ctx *ctx, const k2t_model_config *cfg, int32_t max_
             m->xt = (int8_t *)dalloc(m, ntile * 1024);
             m->st = (float *)dalloc(m, ntile * 16 * sizeof(float));
             m->ut = (int32_t *)dalloc(m, ntile * 16 * sizeof(int32_t));
+            m->dtiles.xt = (int8_t *)dalloc(m, ntile * 1024);
+            m->dtiles.st = (float *)dalloc(m, ntile * 16 * sizeof(float));
+            m->dtiles.ut = (int32_t *)dalloc(m, ntile * 16 * sizeof(int32_t));
             // persistent decode kernel state
             // the persistent kernel's phases assume the megakernel shape q_dim == hidden
             m->mk_ok = decode_mk_supported(c, ctx->num_cus) && c.n_heads * c.head_dim == c.hidden;

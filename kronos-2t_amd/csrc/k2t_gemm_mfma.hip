@@ -79,6 +79,13 @@ struct MfArgs {
     float *out;
     size_t out_stride;
     int accum;
+    // SwiGLU epilogue (gate_up with interleaved [gate64, up64] blocks): the down input as
+    // int8 chunks, scales and sums ([token][nci]) and its tile-major copy
+    int8_t *sq;
+    float *ss;
+    int32_t *ssum;
+    ActTiles stiles;
+    int nci;
 };
 
 // Everything one chunk needs (one ring stage): the stripe-chunk's codes and scales, the
@@ -218,11 +225,20 @@ __device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<FMT, NB, 
 // w < NB loads block w; one barrier per chunk) instead of each loading all NB.  Measured
 // (256 tokens): 16384 x 2048 at NB 4, 45.7 -> 40.4 us with P 2; 2048 x 8192 at NB 1,
 // 36.9 -> 44-49 us (one loader and a barrier per chunk for 128 chunks): on for NB 4 only.
-template <int FMT, int HP, int NB, int P, bool SH>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(MfArgs A) {
+//
+// SW (gate_up only): 8 waves per workgroup, so a workgroup holds one interleaved block ic
+// of 128 rows ([gate64(ic), up64(ic)], simd_lut.rs:3310-3325) for its 64 tokens, and its
+// epilogue is swiglu_act_kernel's instead of a store: per token, v = (g / (1 + exp(-g)))
+// * u (swiglu_activate_scalar, real_llm.rs:9801-9805), the FWHT of chunk ic and the int8
+// quantization (populate_chunk_fwht_raw) of the down input, with its tile-major copy.
+// The same arithmetic in the same order as that kernel, so the outputs are the same.
+template <int FMT, int HP, int NB, int P, bool SH, bool SW = false>
+__global__ __launch_bounds__(SW ? 512 : 256) void gemm_mfma_kernel(MfArgs A) {
+    constexpr int W = SW ? 8 : 4;  // waves (stripes) per workgroup
+    static_assert(!SW || (SH && NB == 4), "the SwiGLU epilogue runs on 64-token workgroups");
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: stripe math on SGPRs
-    const int stripe_id = (int)blockIdx.x * 4 + (int)wave;
+    const int stripe_id = (int)blockIdx.x * W + (int)wave;
     // With sharing every wave takes part in every barrier: a wave past the last stripe
     // runs the last stripe's chunks and stores nothing.
     if (!SH && stripe_id >= A.stripes) return;
@@ -267,6 +283,25 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MfArgs A) {
 #pragma unroll
     for (int i = 0; i < P - 1; i++)
         if (c0 + i < nc) mf_step<FMT, HP, NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
+    if constexpr (SW) {
+        __shared__ float ep[64][129];  // [token][row of the block]
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) ep[16 * b + li][wave * 16 + 4 * lg + r] = acc[b][r];
+        __syncthreads();
+        const int ic = (int)blockIdx.x;
+        for (int tl = (int)wave; tl < 16 * NB; tl += W) {
+            const int t = tokb + tl;
+            if (t >= A.ntok) break;  // wave-uniform
+            const float g = ep[tl][lane], u = ep[tl][64 + lane];
+            const float v = (g / (1.0f + expf(-g))) * u;
+            const size_t gc = (size_t)t * A.nci + ic;
+            quant_chunk_store(fwht_lane(v, (uint64_t)ic, lane), lane, A.sq + gc * 64, A.ss + gc, A.ssum + gc,
+                              A.stiles.xt, A.stiles.st, A.stiles.ut, t, ic, A.nci);
+        }
+        return;
+    }
     if (stripe_id >= A.stripes) return;
 #pragma unroll
     for (int b = 0; b < NB; b++) {
@@ -322,11 +357,13 @@ static void launch_gemm_mfma_fmt(hipStream_t st, int nb, dim3 grid, const MfArgs
     }
 }
 
-void launch_gemm_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum,
-                      int ntok, float *out, size_t out_stride, bool accum, ActTiles tiles) {
-    if (!gemm_mfma_supported(m, ntok)) throw Error(K2T_E_INTERNAL, "mfma gemm: unsupported matrix");
+// Arguments of one launch over all of m's stripes, and the tile-major activation (the
+// producer's, else copied here into the context's scratch: 1 KB + 64 B of scales + 64 B
+// of code sums per tile).  Returns the 16-token blocks per wave the launch will use.
+static int mfma_args(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum,
+                     int ntok, ActTiles tiles, MfArgs &A) {
     const bool planes = m->fmt == K2T_FMT_NIBBLE4;
-    MfArgs A{};
+    A = MfArgs{};
     A.pair = m->pair;
     A.tail = m->tail;
     A.ptot = m->pairs ? m->pair_len / m->pairs : 0;
@@ -336,8 +373,6 @@ void launch_gemm_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const fl
     A.stripes = m->stripes;
     A.sgc_log2 = planes ? 0 : __builtin_ctz((unsigned)m->sgc);
     if (!planes) nf4_xor_tables(m->cb[0], m->cb[1], m->cb[2], m->cb[3], A.t0, A.t1, A.u0, A.u1);
-    // The tile-major copy: from the activation's producer, else made here in the
-    // context's scratch (1 KB + 64 B of scales + 64 B of code sums per tile).
     const int blocks = (ntok + 15) / 16;
     int8_t *xt = tiles.xt;
     float *stile = tiles.st;
@@ -357,21 +392,58 @@ void launch_gemm_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const fl
     A.ut = utile;
     A.K = m->cols;
     A.ntok = ntok;
-    A.out = out;
-    A.out_stride = out_stride;
-    A.accum = accum ? 1 : 0;
     // Tokens per wave: the most 16-token blocks (fewest weight passes) that still give
     // the launch kMfmaMinWaves waves.
     int nb = std::min(kMfmaMaxBlocks, blocks);
     if (nb > 4 && nb < 8) nb = 4;
     while (nb > 1 && (long)m->stripes * ((blocks + nb - 1) / nb) < kMfmaMinWaves) nb = nb > 4 ? 4 : nb > 2 ? 2 : 1;
+    return nb;
+}
+
+void launch_gemm_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum,
+                      int ntok, float *out, size_t out_stride, bool accum, ActTiles tiles) {
+    if (!gemm_mfma_supported(m, ntok)) throw Error(K2T_E_INTERNAL, "mfma gemm: unsupported matrix");
+    MfArgs A;
+    const int nb = mfma_args(ctx, m, xq, xs, xsum, ntok, tiles, A);
+    A.out = out;
+    A.out_stride = out_stride;
+    A.accum = accum ? 1 : 0;
     const dim3 grid((m->stripes + 3) / 4, (ntok + 16 * nb - 1) / (16 * nb));
     hipStream_t st = ctx->stream;
-    if (!planes) launch_gemm_mfma_fmt<1, 0>(st, nb, grid, A);
+    if (m->fmt == K2T_FMT_NF) launch_gemm_mfma_fmt<1, 0>(st, nb, grid, A);
     else if (m->hp == 0) launch_gemm_mfma_fmt<0, 0>(st, nb, grid, A);
     else if (m->hp == 1) launch_gemm_mfma_fmt<0, 1>(st, nb, grid, A);
     else launch_gemm_mfma_fmt<0, 2>(st, nb, grid, A);
     hip_check(hipGetLastError(), "mfma gemm launch");
+}
+
+template <int FMT, int HP>
+static void launch_swiglu_fmt(hipStream_t st, dim3 grid, const MfArgs &A) {
+    hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 4, kMfmaShDepth, true, true>), grid, dim3(512), 0, st, A);
+}
+
+bool launch_gemm_mfma_swiglu(k2t_ctx *ctx, const k2t_mat *gu, ActTiles tiles, int ntok, int8_t *q, float *s,
+                             int32_t *sums, ActTiles out_tiles) {
+    if (!gemm_mfma_supported(gu, ntok) || !tiles.xt || !out_tiles.xt || gu->rows % 128 != 0) return false;
+    if (gu->fmt == K2T_FMT_NIBBLE4 && !tiles.ut) return false;
+    // Only where the plain GEMV would take 64-token workgroups anyway: forcing them on a
+    // small gate_up (135M: 3072 rows, 768 waves at 256 tokens) cost more than the launch
+    // the fusion saves (135M prefill 130k -> 123k tok/s).
+    MfArgs A;
+    if (mfma_args(ctx, gu, nullptr, nullptr, nullptr, ntok, tiles, A) != 4) return false;
+    A.sq = q;
+    A.ss = s;
+    A.ssum = sums;
+    A.stiles = out_tiles;
+    A.nci = gu->rows / 128;
+    const dim3 grid(gu->rows / 128, (ntok + 63) / 64);
+    hipStream_t st = ctx->stream;
+    if (gu->fmt == K2T_FMT_NF) launch_swiglu_fmt<1, 0>(st, grid, A);
+    else if (gu->hp == 0) launch_swiglu_fmt<0, 0>(st, grid, A);
+    else if (gu->hp == 1) launch_swiglu_fmt<0, 1>(st, grid, A);
+    else launch_swiglu_fmt<0, 2>(st, grid, A);
+    hip_check(hipGetLastError(), "mfma gate_up + swiglu launch");
+    return true;
 }
 
 }  // namespace k2t

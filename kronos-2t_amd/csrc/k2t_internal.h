@@ -140,6 +140,12 @@ constexpr int kMfmaMinTokens = 16;
 bool gemm_mfma_supported(const k2t_mat *m, int ntok);
 void launch_gemm_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum,
                       int ntok, float *out, size_t out_stride, bool accum, ActTiles tiles = ActTiles{});
+// gate_up (interleaved [gate64, up64] blocks) from producer tiles with the SwiGLU + FWHT +
+// int8 of the down input (q / s / sums [token][rows / 128], its tiles into out_tiles,
+// which must not be `tiles`) as the epilogue; false (nothing launched) when the plain
+// launch would not take 64-token workgroups, or for other shapes.
+bool launch_gemm_mfma_swiglu(k2t_ctx *ctx, const k2t_mat *gu, ActTiles tiles, int ntok, int8_t *q, float *s,
+                             int32_t *sums, ActTiles out_tiles);
 void launch_gemv_grouped(k2t_ctx *ctx, const k2t_mat *geom, const GemvGroup &g, int xs_mode, const float *src,
                          const float *w, float eps, float *out);
 

@@ -113,27 +113,32 @@ def test_mfma_bitplane_gemv_equals_reference_chain(gpu_ctx, planes, rows, cols, 
     m.close()
 
 
-@pytest.mark.parametrize("fmt,planes,max_seq,hd", [("nf4", None, 64, 64), ("nf4", None, 1100, 64),
-                                                   ("n4", "p55454", 64, 64), ("n4", "b6", 64, 64),
-                                                   ("nf4", None, 300, 128)])
-def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_seq, hd):
-    """A 2-layer model (d 256, 256 / hd heads of hd 64 or 128, ffn 768; nf4, p55454 and b6
-    weights): a 40-token prefill (qkv, o with the residual add, gate_up and down with the
+@pytest.mark.parametrize("fmt,planes,max_seq,hd,n,ffn", [("nf4", None, 64, 64, 40, 768),
+                                                         ("nf4", None, 1100, 64, 40, 768),
+                                                         ("n4", "p55454", 64, 64, 40, 768),
+                                                         ("n4", "b6", 64, 64, 40, 768),
+                                                         ("nf4", None, 300, 128, 40, 768),
+                                                         ("nf4", None, 160, 64, 100, 8192),
+                                                         ("n4", "p55454", 160, 64, 100, 8192)])
+def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_seq, hd, n, ffn):
+    """A 2-layer model (d 256, 256 / hd heads of hd 64 or 128, ffn 768 or 8192; nf4, p55454
+    and b6 weights): an n-token prefill (qkv, o with the residual add, gate_up and down with the
     residual add on the matrix cores) in exact-order mode equals the oracle bit for bit,
-    and so does the one with the matrix cores off, and one of 20 + 20 tokens (the second
-    batch appended at position 20).  In fast mode the batch's attention also runs on the
-    matrix cores (attn_prefill_mfma_kernel), and the activation tiles written by their
-    producers (RMSNorm, attention, SwiGLU) give the same logits as tiles copied by the
-    GEMV, within the fast path's bar of the oracle, for one batch and for 20 + 20."""
+    and so does the one with the matrix cores off, and one of 20 + (n - 20) tokens (the
+    second batch appended at position 20).  In fast mode the batch's attention also runs
+    on the matrix cores (attn_prefill_mfma_kernel), and the activation tiles written by
+    their producers (RMSNorm, attention, SwiGLU or, with ffn 8192 and 100 tokens, gate_up's
+    SwiGLU epilogue) give the same logits as tiles copied by the GEMV (mode 2: separate SwiGLU),
+    within the fast path's bar of the oracle, for one batch and for 20 + (n - 20)."""
     from model_oracle import OracleModel, random_model
     from test_gpu_model import P55454, _close, _gpu_model
-    print(f"mfma prefill vs oracle, {fmt} {planes} max_seq {max_seq} hd {hd}", flush=True)
+    print(f"mfma prefill vs oracle, {fmt} {planes} max_seq {max_seq} hd {hd} n {n}", flush=True)
     plane_map = {"p55454": P55454, "b6": {k: 6 for k in P55454}, None: None}[planes]
-    cfg = dict(n_layers=2, hidden=256, n_heads=256 // hd, n_kv_heads=128 // hd, head_dim=hd, intermediate=768,
+    cfg = dict(n_layers=2, hidden=256, n_heads=256 // hd, n_kv_heads=128 // hd, head_dim=hd, intermediate=ffn,
                vocab=520, max_seq=max_seq, rms_eps=1e-5, rope_theta=10000.0)
     layers, head, fn = random_model(cfg, seed=41, fmt=fmt, planes=plane_map)
     ref = OracleModel(cfg, layers, head, fn)
-    toks = np.random.default_rng(42).integers(0, cfg["vocab"], 40)
+    toks = np.random.default_rng(42).integers(0, cfg["vocab"], n)
     for t in toks[:-1]:
         ref.forward_token(int(t), want_logits=False)
     b = ref.forward_token(int(toks[-1]))
