@@ -392,20 +392,27 @@ void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
     const bool fused = ntok == 1;
     for (int l = 0; l < c.n_layers; l++) {
         const auto &L = m->layers[l];
+        bool qkv_posted = false;
         if (fused) {
             launch_gemv_fused(ctx, L.qkv, K2T_XS_RMSNORM, m->hidden, L.in_norm, c.rms_eps, m->qkv, false);
         } else {
             const ActTiles tq = act_tiles_for(m, L.qkv, ntok);
             launch_rmsnorm_act(st, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum, tq);
-            launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false, 0,
-                           tq);
+            // head size 64 with producer tiles: qkv_post's work as the GEMV's epilogue
+            qkv_posted = hd == 64 && tq.xt &&
+                         launch_gemm_mfma_qkv(ctx, L.qkv, tq, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd,
+                                              QkvPostDev{L.bias, L.q_norm, L.k_norm, m->rope, c.rms_eps, m->pos_dev,
+                                                         nq, nkv, l, m->ring, m->kq, m->vq, m->ks, m->vs});
+            if (!qkv_posted)
+                launch_gemv_ex(ctx, L.qkv, m->xq, m->xs, m->xsum, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd, false,
+                               0, tq);
         }
         // One token: qkv_post's work runs inside the attention kernel.  A batch stores every
         // token's K / V first (a later token of the batch attends to them).
         AttnPost post{};
         if (ntok == 1) {
             post = AttnPost{1, L.bias, L.q_norm, L.k_norm, m->rope, c.rms_eps};
-        } else {
+        } else if (!qkv_posted) {
             launch_qkv_post(st, m->qkv, L.bias, L.q_norm, L.k_norm, c.rms_eps, m->rope, m->pos_dev, nq, nkv, hd, ntok,
                             l, m->ring, m->kq, m->vq, m->ks, m->vs, false);
         }

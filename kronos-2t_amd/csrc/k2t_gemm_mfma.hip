@@ -39,6 +39,7 @@
 #include "../../include/k2t_hip.h"
 #include "k2t_device.h"
 #include "k2t_internal.h"
+#include "k2t_kv_dev.h"
 
 namespace k2t {
 
@@ -86,6 +87,7 @@ struct MfArgs {
     int32_t *ssum;
     ActTiles stiles;
     int nci;
+    QkvPostDev qp;  // q / k / v epilogue (the qkv projection at head size 64)
 };
 
 // Everything one chunk needs (one ring stage): the stripe-chunk's codes and scales, the
@@ -232,7 +234,13 @@ __device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<FMT, NB, 
 // * u (swiglu_activate_scalar, real_llm.rs:9801-9805), the FWHT of chunk ic and the int8
 // quantization (populate_chunk_fwht_raw) of the down input, with its tile-major copy.
 // The same arithmetic in the same order as that kernel, so the outputs are the same.
-template <int FMT, int HP, int NB, int P, bool SH, bool SW = false>
+//
+// QP (qkv, head size 64): a workgroup's 4 stripes are one head's 64 rows, and its epilogue
+// is qkv_post_kernel's for each of its tokens: bias, q / k RMSNorm and RoPE
+// (head_post_vals), then q back into the qkv rows, k and v rotated and stored in the
+// cache slot of their position.  The same arithmetic on the same values, so the cache
+// and q equal the separate kernel's.
+template <int FMT, int HP, int NB, int P, bool SH, bool SW = false, bool QP = false>
 __global__ __launch_bounds__(SW ? 512 : 256) void gemm_mfma_kernel(MfArgs A) {
     constexpr int W = SW ? 8 : 4;  // waves (stripes) per workgroup
     static_assert(!SW || (SH && NB == 4), "the SwiGLU epilogue runs on 64-token workgroups");
@@ -283,6 +291,32 @@ __global__ __launch_bounds__(SW ? 512 : 256) void gemm_mfma_kernel(MfArgs A) {
 #pragma unroll
     for (int i = 0; i < P - 1; i++)
         if (c0 + i < nc) mf_step<FMT, HP, NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
+    if constexpr (QP) {
+        __shared__ float eq[16 * NB][65];  // [token][row of the head]
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) eq[16 * b + li][wave * 16 + 4 * lg + r] = acc[b][r];
+        __syncthreads();
+        const QkvPostDev &Q = A.qp;
+        const int head = (int)blockIdx.x, pos0 = Q.pos_dev[0];
+        for (int tl = (int)wave; tl < 16 * NB; tl += W) {
+            const int t = tokb + tl;
+            if (t >= A.ntok) break;  // wave-uniform
+            float v0 = eq[tl][lane], v1 = 0.0f;
+            head_post_vals(head, Q.nq, Q.nkv, 64, Q.bias, Q.qn, Q.kn, Q.eps, Q.rope, pos0 + t, lane, v0, v1);
+            if (head < Q.nq) {
+                A.out[(size_t)t * A.out_stride + (size_t)head * 64 + lane] = v0;
+                continue;
+            }
+            const bool is_k = head < Q.nq + Q.nkv;
+            const int kvh = is_k ? head - Q.nq : head - Q.nq - Q.nkv;
+            const size_t slot = ((size_t)Q.layer * Q.nkv + kvh) * Q.kr.cap + ring_slot(Q.kr, pos0 + t);
+            kv_store_head(fwht_lane(v0, 0, lane), 0.0f, 1, lane, Q.kr.bits, 64, slot, is_k ? Q.kq : Q.vq,
+                          is_k ? Q.ks : Q.vs);
+        }
+        return;
+    }
     if constexpr (SW) {
         __shared__ float ep[64][129];  // [token][row of the block]
 #pragma unroll
@@ -415,6 +449,36 @@ void launch_gemm_mfma(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const fl
     else if (m->hp == 1) launch_gemm_mfma_fmt<0, 1>(st, nb, grid, A);
     else launch_gemm_mfma_fmt<0, 2>(st, nb, grid, A);
     hip_check(hipGetLastError(), "mfma gemm launch");
+}
+
+template <int FMT, int HP>
+static void launch_qkv_fmt(hipStream_t st, int nb, dim3 grid, const MfArgs &A) {
+    const dim3 blk(256);
+    switch (nb) {
+        case 1: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 1, kMfmaDepth, false, false, true>), grid, blk, 0, st, A); break;
+        case 2: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 2, kMfmaDepth, false, false, true>), grid, blk, 0, st, A); break;
+        case 3: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 3, kMfmaDepth, false, false, true>), grid, blk, 0, st, A); break;
+        default: hipLaunchKernelGGL((gemm_mfma_kernel<FMT, HP, 4, kMfmaShDepth, true, false, true>), grid, blk, 0, st, A);
+    }
+}
+
+bool launch_gemm_mfma_qkv(k2t_ctx *ctx, const k2t_mat *qkv, ActTiles tiles, int ntok, float *out, size_t out_stride,
+                          const QkvPostDev &qp) {
+    if (!gemm_mfma_supported(qkv, ntok) || !tiles.xt || qkv->rows % 64 != 0) return false;
+    if (qkv->fmt == K2T_FMT_NIBBLE4 && !tiles.ut) return false;
+    MfArgs A;
+    const int nb = std::min(4, mfma_args(ctx, qkv, nullptr, nullptr, nullptr, ntok, tiles, A));
+    A.out = out;
+    A.out_stride = out_stride;
+    A.qp = qp;
+    const dim3 grid(qkv->rows / 64, (ntok + 16 * nb - 1) / (16 * nb));
+    hipStream_t st = ctx->stream;
+    if (qkv->fmt == K2T_FMT_NF) launch_qkv_fmt<1, 0>(st, nb, grid, A);
+    else if (qkv->hp == 0) launch_qkv_fmt<0, 0>(st, nb, grid, A);
+    else if (qkv->hp == 1) launch_qkv_fmt<0, 1>(st, nb, grid, A);
+    else launch_qkv_fmt<0, 2>(st, nb, grid, A);
+    hip_check(hipGetLastError(), "mfma qkv launch");
+    return true;
 }
 
 template <int FMT, int HP>

@@ -158,6 +158,23 @@ struct KvRing {
     int cap, window, sinks, ring, bits;
 };
 
+// The post-processing of a qkv row's heads (qkv_post_kernel's arguments): bias, q / k
+// RMSNorm weights, the RoPE table, the positions, and the K / V cache it stores into.
+struct QkvPostDev {
+    const float *bias, *qn, *kn, *rope;
+    float eps;
+    const int *pos_dev;
+    int nq, nkv, layer;
+    KvRing kr;
+    int8_t *kq, *vq;
+    float *ks, *vs;
+};
+// The qkv projection (head size 64) on the matrix cores from producer tiles, with
+// qkv_post_kernel's work as the epilogue: q heads into out, K / V into the cache; false
+// (nothing launched) where it does not apply.
+bool launch_gemm_mfma_qkv(k2t_ctx *ctx, const k2t_mat *qkv, ActTiles tiles, int ntok, float *out, size_t out_stride,
+                          const QkvPostDev &qp);
+
 // Workspace of the grouped-query decode attention kernel: the span words
 // ([q head][span][2 + hd] {payload, epoch}, zeroed once) and two counters {epoch of the
 // last launch, merge workgroups done} (zeroed once); err receives 3 on a wait timeout.

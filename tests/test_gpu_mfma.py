@@ -113,14 +113,15 @@ def test_mfma_bitplane_gemv_equals_reference_chain(gpu_ctx, planes, rows, cols, 
     m.close()
 
 
-@pytest.mark.parametrize("fmt,planes,max_seq,hd,n,ffn", [("nf4", None, 64, 64, 40, 768),
-                                                         ("nf4", None, 1100, 64, 40, 768),
-                                                         ("n4", "p55454", 64, 64, 40, 768),
-                                                         ("n4", "b6", 64, 64, 40, 768),
-                                                         ("nf4", None, 300, 128, 40, 768),
-                                                         ("nf4", None, 160, 64, 100, 8192),
-                                                         ("n4", "p55454", 160, 64, 100, 8192)])
-def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_seq, hd, n, ffn):
+@pytest.mark.parametrize("fmt,planes,max_seq,hd,n,ffn,qk", [("nf4", None, 64, 64, 40, 768, False),
+                                                            ("nf4", None, 1100, 64, 40, 768, False),
+                                                            ("n4", "p55454", 64, 64, 40, 768, False),
+                                                            ("n4", "b6", 64, 64, 40, 768, False),
+                                                            ("nf4", None, 300, 128, 40, 768, False),
+                                                            ("nf4", None, 160, 64, 100, 8192, False),
+                                                            ("n4", "p55454", 160, 64, 100, 8192, False),
+                                                            ("nf4", None, 64, 64, 40, 768, True)])
+def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_seq, hd, n, ffn, qk):
     """A 2-layer model (d 256, 256 / hd heads of hd 64 or 128, ffn 768 or 8192; nf4, p55454
     and b6 weights): an n-token prefill (qkv, o with the residual add, gate_up and down with the
     residual add on the matrix cores) in exact-order mode equals the oracle bit for bit,
@@ -128,7 +129,8 @@ def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_
     second batch appended at position 20).  In fast mode the batch's attention also runs
     on the matrix cores (attn_prefill_mfma_kernel), and the activation tiles written by
     their producers (RMSNorm, attention, SwiGLU or, with ffn 8192 and 100 tokens, gate_up's
-    SwiGLU epilogue) give the same logits as tiles copied by the GEMV (mode 2: separate SwiGLU),
+    SwiGLU epilogue), with the qkv GEMV's q / k / v epilogue at head size 64 (also with a
+    qkv bias and q / k norms), give the same logits as tiles copied by the GEMV (mode 2: separate SwiGLU),
     within the fast path's bar of the oracle, for one batch and for 20 + (n - 20)."""
     from model_oracle import OracleModel, random_model
     from test_gpu_model import P55454, _close, _gpu_model
@@ -137,12 +139,22 @@ def test_mfma_prefill_matches_exact_decode_and_oracle(gpu_ctx, fmt, planes, max_
     cfg = dict(n_layers=2, hidden=256, n_heads=256 // hd, n_kv_heads=128 // hd, head_dim=hd, intermediate=ffn,
                vocab=520, max_seq=max_seq, rms_eps=1e-5, rope_theta=10000.0)
     layers, head, fn = random_model(cfg, seed=41, fmt=fmt, planes=plane_map)
+    if qk:  # a qkv bias and Qwen3 q / k norms (the q / k / v epilogue of the qkv GEMV applies them)
+        rng = np.random.default_rng(5)
+        nqkv = (cfg["n_heads"] + 2 * cfg["n_kv_heads"]) * hd
+        for L in layers:
+            L["bias"] = (0.05 * rng.standard_normal(nqkv)).astype(np.float32)
+            L["q_norm"] = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+            L["k_norm"] = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
     ref = OracleModel(cfg, layers, head, fn)
     toks = np.random.default_rng(42).integers(0, cfg["vocab"], n)
     for t in toks[:-1]:
         ref.forward_token(int(t), want_logits=False)
     b = ref.forward_token(int(toks[-1]))
-    gm, mats = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=64)
+    gm, mats = _gpu_model(gpu_ctx, cfg, layers, head, fn, max_batch=128)
+    if qk:
+        for i, L in enumerate(layers):
+            gm.set_qk_norm(i, L["q_norm"], L["k_norm"])
     try:
         gm.set_exact(True)
         for mfma in (True, False):
