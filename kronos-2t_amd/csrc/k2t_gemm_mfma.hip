@@ -144,13 +144,27 @@ __device__ __forceinline__ void mf_fetch(const MfArgs &A, const MfSrc &R, const 
     if constexpr (FMT == 0 && HP > 0) f.hv = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(R.w, L.h_off, rec, 0);
     const v2u sw = __builtin_amdgcn_raw_buffer_load_b64(R.w, L.s_off, sgb, 0);
     f.sw = make_uint2(sw[0], sw[1]);
+    if constexpr (SH) {
+        // With sharing, wave w loads blocks w, w + 4, ...  The load is unconditional (a
+        // wave past the blocks re-reads the last one and stores nothing), so the ring
+        // stage's registers hold only the new value: a conditional load kept the old one
+        // alive, which cost copies, and a wait for nearly every load, at the loop's back
+        // edge.
+#pragma unroll
+        for (int k = 0; k < (NB + 3) / 4; k++) {
+            const int b = min((int)wave + 4 * k, NB - 1);
+            const uint32_t tile = (uint32_t)min(tb0 + b, A.nblk - 1) * (uint32_t)A.nc + (uint32_t)c;
+            const v4u x = __builtin_amdgcn_raw_buffer_load_b128(R.x, L.x_off, tile * 1024u, 0);
+            f.x[k] = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
+        }
+    }
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         // blocks past the last repeat it; their outputs are never stored
         const uint32_t tile = (uint32_t)min(tb0 + b, A.nblk - 1) * (uint32_t)A.nc + (uint32_t)c;
-        if (!SH || b % 4 == (int)wave) {  // with sharing, wave w loads blocks w, w + 4
+        if constexpr (!SH) {
             const v4u x = __builtin_amdgcn_raw_buffer_load_b128(R.x, L.x_off, tile * 1024u, 0);
-            f.x[SH ? b / 4 : b] = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
+            f.x[b] = make_int4((int)x[0], (int)x[1], (int)x[2], (int)x[3]);
         }
         f.sx[b] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(R.s, L.sx_off, tile * 64u, 0));
         if constexpr (FMT == 0) f.su[b] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(R.u, L.sx_off, tile * 64u, 0);
@@ -221,7 +235,13 @@ __device__ __forceinline__ void mf_step(const MfArgs &A, const MfChunk<FMT, NB, 
 // P chunks in flight per wave: a register ring of P stages, unrolled so that each stage
 // is a fixed set of registers (no copies, so the compiler's load waits count only the
 // stages issued after the one consumed).  Stage i holds chunks i, i + P, i + 2P, ...;
-// fetches past the last chunk re-read the last chunk and are never consumed.
+// fetches past the last chunk re-read the last chunk and are never consumed.  Scheduling
+// barriers keep each refill right after the step that frees its stage: left to itself,
+// the compiler sank every load of a round below the round's last MFMA and a wait for all
+// loads, so no load was in flight during compute (256-token 1.7B prefill: o / down 24.8
+// -> 22.9 us, gate_up 40.7 -> 39.6 us).  A software-pipelined form (chunk c's MFMAs
+// issued before chunk c - 1's epilogue) measured slower (25.3 / 41.5 us): the register
+// allocator then copied ring registers at the loop head, which drained the ring.
 //
 // SH: the waves of a workgroup share their tokens' activation blocks through LDS (wave
 // w < NB loads block w; one barrier per chunk) instead of each loading all NB.  Measured
@@ -285,7 +305,9 @@ __global__ __launch_bounds__(SW ? 512 : 256) void gemm_mfma_kernel(MfArgs A) {
 #pragma unroll
         for (int i = 0; i < P; i++) {
             mf_step<FMT, HP, NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
+            __builtin_amdgcn_sched_barrier(0);
             mf_fetch<FMT, HP, NB, SH>(A, R, L, is_tail, tb0, wave, min(c0 + P + i, last), ring[i]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
