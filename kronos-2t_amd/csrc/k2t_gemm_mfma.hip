@@ -340,21 +340,41 @@ __global__ __launch_bounds__(SW ? 512 : 256) void gemm_mfma_kernel(MfArgs A) {
         return;
     }
     if constexpr (SW) {
-        __shared__ float ep[64][129];  // [token][row of the block]
+        __shared__ float4 ep4[64][33];  // [token][row of the block / 4] (+1 float4 of padding)
+        float *ep = reinterpret_cast<float *>(ep4);
 #pragma unroll
         for (int b = 0; b < NB; b++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) ep[16 * b + li][wave * 16 + 4 * lg + r] = acc[b][r];
+            for (int r = 0; r < 4; r++) ep[(16 * b + li) * 132 + wave * 16 + 4 * lg + r] = acc[b][r];
         __syncthreads();
         const int ic = (int)blockIdx.x;
-        for (int tl = (int)wave; tl < 16 * NB; tl += W) {
-            const int t = tokb + tl;
-            if (t >= A.ntok) break;  // wave-uniform
-            const float g = ep[tl][lane], u = ep[tl][64 + lane];
-            const float v = (g / (1.0f + expf(-g))) * u;
-            const size_t gc = (size_t)t * A.nci + ic;
-            quant_chunk_store(fwht_lane(v, (uint64_t)ic, lane), lane, A.sq + gc * 64, A.ss + gc, A.ssum + gc,
-                              A.stiles.xt, A.stiles.st, A.stiles.ut, t, ic, A.nci);
+        // Four tokens per wave at a time: lanes 16k .. 16k + 15 hold token tl0 + k, four
+        // consecutive elements each (rotate_quant4: the arithmetic of fwht_lane +
+        // quant_chunk_store in that layout, so the codes, scales and sums are the same).
+        const uint64_t smask = __ballot(hadamard_sign_bit((uint64_t)ic, lane) != 0u);
+        const uint32_t sl = lane & 15u;
+        for (int tl0 = 4 * (int)wave; tl0 < 16 * NB; tl0 += 4 * W) {
+            if (tokb + tl0 >= A.ntok) break;  // wave-uniform
+            const int tl = tl0 + (int)(lane >> 4), t = tokb + tl;
+            const float4 g4 = ep4[tl][sl], u4 = ep4[tl][16 + sl];
+            const float gs[4] = {g4.x, g4.y, g4.z, g4.w}, us[4] = {u4.x, u4.y, u4.z, u4.w};
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = (gs[j] / (1.0f + expf(-gs[j]))) * us[j];
+            const Chunk4 r = rotate_quant4(v, smask, sl);
+            if (t < A.ntok) {
+                const size_t gc = (size_t)t * A.nci + ic;
+                *reinterpret_cast<uint32_t *>(A.sq + gc * 64 + 4 * sl) = r.w;
+                const size_t tile = (size_t)(t >> 4) * A.nci + ic;
+                *reinterpret_cast<uint32_t *>(A.stiles.xt + tile * 1024 + ((sl >> 2) * 16u + (uint32_t)(t & 15)) * 16u +
+                                              (sl & 3u) * 4u) = r.w;
+                if (sl == 0) {
+                    A.ss[gc] = r.scale;
+                    A.ssum[gc] = r.sum;
+                    A.stiles.st[tile * 16 + (t & 15)] = r.scale;
+                    A.stiles.ut[tile * 16 + (t & 15)] = r.sum;
+                }
+            }
         }
         return;
     }
