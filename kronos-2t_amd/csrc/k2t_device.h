@@ -481,6 +481,29 @@ __device__ __forceinline__ Chunk4 rotate_quant4(float *v, uint64_t sign_mask, ui
     return r;
 }
 
+// A Chunk4 (sixteen lanes, slice sl) of chunk c, token tok, stored as quant_chunk_store
+// stores the one-element-per-lane form: codes q[tok * nc + c][4 sl .. 4 sl + 3] as one
+// word, the scale and the code sum; with xt, also into the tile-major copy (the four
+// codes are consecutive bytes there too).
+__device__ __forceinline__ void chunk4_store(const Chunk4 &r, uint32_t sl, int tok, int c, int nc, int8_t *q,
+                                             float *scale, int32_t *sum, int8_t *xt, float *st, int32_t *ut) {
+    const size_t gc = (size_t)tok * nc + c;
+    *reinterpret_cast<uint32_t *>(q + gc * 64 + 4 * sl) = r.w;
+    if (sl == 0) {
+        scale[gc] = r.scale;
+        sum[gc] = r.sum;
+    }
+    if (xt) {
+        const size_t tile = (size_t)(tok >> 4) * nc + c;
+        *reinterpret_cast<uint32_t *>(xt + tile * 1024 + ((sl >> 2) * 16u + (uint32_t)(tok & 15)) * 16u + (sl & 3u) * 4u) =
+            r.w;
+        if (sl == 0) {
+            st[tile * 16 + (tok & 15)] = r.scale;
+            ut[tile * 16 + (tok & 15)] = r.sum;
+        }
+    }
+}
+
 // rotate_quant8 into the LDS activation: `act` gates the stores (codes at
 // xl[c*64 + s*8], scale xsl[c], sum xsuml[c]).
 __device__ __forceinline__ void rotate_quant_slice8(float *v, uint64_t sign_mask, uint32_t s, int c, bool act,

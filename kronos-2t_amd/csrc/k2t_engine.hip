@@ -19,8 +19,8 @@
 #include "k2t_moe.h"
 
 namespace k2t {
-void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float eps, int K, int ntok, int8_t *q,
-                        float *s, int32_t *sums, ActTiles tiles = ActTiles{});
+void launch_rmsnorm_act(hipStream_t st, const uint64_t *signs, const float *x, const float *w, float eps, int K,
+                        int ntok, int8_t *q, float *s, int32_t *sums, ActTiles tiles = ActTiles{});
 void launch_qkv_post(hipStream_t st, float *qkv, const float *bias, const float *qn, const float *kn, float eps,
                      const float *rope, const int *pos_dev, int nq,
                      int nkv, int hd, int ntok, int layer, KvRing kr, int8_t *kq, int8_t *vq, float *ks, float *vs,
@@ -350,7 +350,7 @@ void forward_exact(k2t_model *m, int ntok, bool with_logits) {
         }
         norm_act(m->hidden, L.post_norm);
         launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false);
-        launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum, true);
+        launch_swiglu_act(st, ctx->signs, m->gu, inter, ntok, m->xq, m->xs, m->xsum, true);
         launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true);
     }
     if (with_logits) {
@@ -397,7 +397,7 @@ void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
             launch_gemv_fused(ctx, L.qkv, K2T_XS_RMSNORM, m->hidden, L.in_norm, c.rms_eps, m->qkv, false);
         } else {
             const ActTiles tq = act_tiles_for(m, L.qkv, ntok);
-            launch_rmsnorm_act(st, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum, tq);
+            launch_rmsnorm_act(st, ctx->signs, m->hidden, L.in_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum, tq);
             // head size 64 with producer tiles: qkv_post's work as the GEMV's epilogue
             qkv_posted = hd == 64 && tq.xt &&
                          launch_gemm_mfma_qkv(ctx, L.qkv, tq, ntok, m->qkv, (size_t)(nq + 2 * nkv) * hd,
@@ -431,7 +431,7 @@ void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
             launch_gemv_fused(ctx, L.down, K2T_XS_SWIGLU, m->gu, nullptr, 0.0f, m->hidden, true);
         } else {
             const ActTiles tg = act_tiles_for(m, L.gu, ntok), td = act_tiles_for(m, L.down, ntok);
-            launch_rmsnorm_act(st, m->hidden, L.post_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum, tg);
+            launch_rmsnorm_act(st, ctx->signs, m->hidden, L.post_norm, c.rms_eps, d, ntok, m->xq, m->xs, m->xsum, tg);
             // gate_up with the SwiGLU epilogue when both GEMVs take producer tiles (the
             // gate_up kernel reads only tg, so it may overwrite xq; its tiles go apart)
             if (tg.xt && td.xt &&
@@ -439,7 +439,7 @@ void forward(k2t_model *m, int ntok, bool with_logits, int ctx_bound = 0) {
                 launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true, 0, m->dtiles);
             } else {
                 launch_gemv_ex(ctx, L.gu, m->xq, m->xs, m->xsum, ntok, m->gu, (size_t)2 * inter, false, 0, tg);
-                launch_swiglu_act(st, m->gu, inter, ntok, m->xq, m->xs, m->xsum, false, td);
+                launch_swiglu_act(st, ctx->signs, m->gu, inter, ntok, m->xq, m->xs, m->xsum, false, td);
                 launch_gemv_ex(ctx, L.down, m->xq, m->xs, m->xsum, ntok, m->hidden, d, true, 0, td);
             }
         }

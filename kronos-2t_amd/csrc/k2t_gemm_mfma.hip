@@ -362,19 +362,8 @@ __global__ __launch_bounds__(SW ? 512 : 256) void gemm_mfma_kernel(MfArgs A) {
 #pragma unroll
             for (int j = 0; j < 4; j++) v[j] = (gs[j] / (1.0f + expf(-gs[j]))) * us[j];
             const Chunk4 r = rotate_quant4(v, smask, sl);
-            if (t < A.ntok) {
-                const size_t gc = (size_t)t * A.nci + ic;
-                *reinterpret_cast<uint32_t *>(A.sq + gc * 64 + 4 * sl) = r.w;
-                const size_t tile = (size_t)(t >> 4) * A.nci + ic;
-                *reinterpret_cast<uint32_t *>(A.stiles.xt + tile * 1024 + ((sl >> 2) * 16u + (uint32_t)(t & 15)) * 16u +
-                                              (sl & 3u) * 4u) = r.w;
-                if (sl == 0) {
-                    A.ss[gc] = r.scale;
-                    A.ssum[gc] = r.sum;
-                    A.stiles.st[tile * 16 + (t & 15)] = r.scale;
-                    A.stiles.ut[tile * 16 + (t & 15)] = r.sum;
-                }
-            }
+            if (t < A.ntok)
+                chunk4_store(r, sl, t, ic, A.nci, A.sq, A.ss, A.ssum, A.stiles.xt, A.stiles.st, A.stiles.ut);
         }
         return;
     }

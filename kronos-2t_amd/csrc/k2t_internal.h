@@ -132,8 +132,8 @@ struct ActTiles {
 };
 void launch_gemv_ex(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, const float *xs, const int32_t *xsum, int ntok,
                     float *out, size_t out_stride, bool accumulate, int gu_split = 0, ActTiles tiles = ActTiles{});
-void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
-                       bool exact, ActTiles tiles = ActTiles{});
+void launch_swiglu_act(hipStream_t st, const uint64_t *signs, const float *gu, int inter, int ntok, int8_t *q,
+                       float *s, int32_t *sums, bool exact, ActTiles tiles = ActTiles{});
 // Batched NF4 / bit-plane GEMV on the matrix cores (k2t_gemm_mfma.hip): kMfmaMinTokens or
 // more tokens of a ready int8 activation, outputs equal to the exact-order GEMV's.
 constexpr int kMfmaMinTokens = 16;

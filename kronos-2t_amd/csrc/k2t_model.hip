@@ -20,27 +20,35 @@
 namespace k2t {
 
 // ---------------------------------------------------------------- RMSNorm + FWHT + int8
-// One wave per (chunk, token): every wave recomputes inv_rms = 1/sqrt(mean(x^2) + eps)
+// One wave per (token, four chunks): the wave computes inv_rms = 1/sqrt(mean(x^2) + eps)
 // (real_llm.rs:6929) from the whole row (L2-resident, a few KB) in a fixed order, then
-// runs populate_rmsnorm_fwht (simd_lut.rs:2970-2997) on its own chunk.
+// runs populate_rmsnorm_fwht (simd_lut.rs:2970-2997) on its four chunks at once: lanes
+// 16k .. 16k + 15 hold chunk 4 blockIdx.x + k, four consecutive elements each
+// (rotate_quant4, the arithmetic of fwht_lane + quant_chunk_store in that layout).  A
+// group past the last chunk repeats it and stores nothing.
 __global__ __launch_bounds__(64) void rmsnorm_act_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                                          float eps, int K, int8_t *__restrict__ q,
                                                          float *__restrict__ scales, int32_t *__restrict__ sums,
-                                                         ActTiles tiles) {
-    const uint32_t lane = threadIdx.x;
-    const int c = blockIdx.x, tok = blockIdx.y;
+                                                         ActTiles tiles, const uint64_t *__restrict__ signs) {
+    const uint32_t lane = threadIdx.x, sl = lane & 15u;
+    const int nc = K / 64, tok = blockIdx.y;
+    const int cg = 4 * (int)blockIdx.x + (int)(lane >> 4), c = min(cg, nc - 1);
     const float *xt = x + (size_t)tok * K;
+    const float4 xv = *reinterpret_cast<const float4 *>(xt + c * 64 + 4 * sl);
+    const float4 wv = *reinterpret_cast<const float4 *>(w + c * 64 + 4 * sl);
+    const uint64_t mask = signs[c];
     const float ss = row_sumsq_wave(xt, K, lane);
     const float inv_rms = 1.0f / sqrtf(ss / (float)K + eps);
-    const float v = (xt[c * 64 + lane] * inv_rms) * w[c * 64 + lane];
-    const size_t gc = (size_t)tok * (K / 64) + c;
-    quant_chunk_store(fwht_lane(v, (uint64_t)c, lane), lane, q + gc * 64, scales + gc, sums + gc, tiles.xt, tiles.st,
-                      tiles.ut, tok, c, K / 64);
+    float v[4] = {(xv.x * inv_rms) * wv.x, (xv.y * inv_rms) * wv.y, (xv.z * inv_rms) * wv.z, (xv.w * inv_rms) * wv.w};
+    const Chunk4 r = rotate_quant4(v, mask, sl);
+    if (cg < nc) chunk4_store(r, sl, tok, c, nc, q, scales, sums, tiles.xt, tiles.st, tiles.ut);
 }
 
-void launch_rmsnorm_act(hipStream_t st, const float *x, const float *w, float eps, int K, int ntok, int8_t *q,
-                        float *s, int32_t *sums, ActTiles tiles) {
-    hipLaunchKernelGGL(rmsnorm_act_kernel, dim3(K / 64, ntok), dim3(64), 0, st, x, w, eps, K, q, s, sums, tiles);
+void launch_rmsnorm_act(hipStream_t st, const uint64_t *signs, const float *x, const float *w, float eps, int K,
+                        int ntok, int8_t *q, float *s, int32_t *sums, ActTiles tiles) {
+    if (K % 64 != 0 || K / 64 > kSignBlocks || !signs) throw Error(K2T_E_INTERNAL, "rmsnorm_act shape");
+    hipLaunchKernelGGL(rmsnorm_act_kernel, dim3((K / 64 + 3) / 4, ntok), dim3(64), 0, st, x, w, eps, K, q, s, sums,
+                       tiles, signs);
     hip_check(hipGetLastError(), "rmsnorm_act launch");
 }
 
@@ -1346,29 +1354,33 @@ void launch_attention_exact(hipStream_t st, const float *q, int q_stride, const 
 // Interleaved gate_up output: block ic = [gate64(ic), up64(ic)] (simd_lut.rs:3310-3325).
 // swiglu_activate_scalar (real_llm.rs:9801-9805), then populate_chunk_fwht_raw with chunk ic.
 // EXACT: the exponential of the x86 reference build (expf_rn) instead of the device expf.
+// One wave per (token, four chunks), in rmsnorm_act_kernel's four-element layout.
 template <bool EXACT>
 __global__ __launch_bounds__(64) void swiglu_act_kernel(const float *__restrict__ gu, int inter, int8_t *__restrict__ q,
                                                         float *__restrict__ s, int32_t *__restrict__ sums,
-                                                        ActTiles tiles) {
-    const uint32_t lane = threadIdx.x;
-    const int ic = blockIdx.x, tok = blockIdx.y;
-    const int nci = inter / 64;
+                                                        ActTiles tiles, const uint64_t *__restrict__ signs) {
+    const uint32_t lane = threadIdx.x, sl = lane & 15u;
+    const int nci = inter / 64, tok = blockIdx.y;
+    const int cg = 4 * (int)blockIdx.x + (int)(lane >> 4), ic = min(cg, nci - 1);
     const float *b = gu + (size_t)tok * 2 * inter + (size_t)ic * 128;
-    const float g = b[lane], u = b[64 + lane];
-    const float v = (g / (1.0f + (EXACT ? expf_rn(-g) : expf(-g)))) * u;
-    const size_t gc = (size_t)tok * nci + ic;
-    quant_chunk_store(fwht_lane(v, (uint64_t)ic, lane), lane, q + gc * 64, s + gc, sums + gc, tiles.xt, tiles.st,
-                      tiles.ut, tok, ic, nci);
+    const float4 g4 = *reinterpret_cast<const float4 *>(b + 4 * sl);
+    const float4 u4 = *reinterpret_cast<const float4 *>(b + 64 + 4 * sl);
+    const float gs[4] = {g4.x, g4.y, g4.z, g4.w}, us[4] = {u4.x, u4.y, u4.z, u4.w};
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = (gs[j] / (1.0f + (EXACT ? expf_rn(-gs[j]) : expf(-gs[j])))) * us[j];
+    const Chunk4 r = rotate_quant4(v, signs[ic], sl);
+    if (cg < nci) chunk4_store(r, sl, tok, ic, nci, q, s, sums, tiles.xt, tiles.st, tiles.ut);
 }
 
-void launch_swiglu_act(hipStream_t st, const float *gu, int inter, int ntok, int8_t *q, float *s, int32_t *sums,
-                       bool exact, ActTiles tiles) {
+void launch_swiglu_act(hipStream_t st, const uint64_t *signs, const float *gu, int inter, int ntok, int8_t *q,
+                       float *s, int32_t *sums, bool exact, ActTiles tiles) {
+    if (inter % 64 != 0 || inter / 64 > kSignBlocks || !signs) throw Error(K2T_E_INTERNAL, "swiglu_act shape");
+    const dim3 grid((inter / 64 + 3) / 4, ntok);
     if (exact)
-        hipLaunchKernelGGL(swiglu_act_kernel<true>, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums,
-                           tiles);
+        hipLaunchKernelGGL(swiglu_act_kernel<true>, grid, dim3(64), 0, st, gu, inter, q, s, sums, tiles, signs);
     else
-        hipLaunchKernelGGL(swiglu_act_kernel<false>, dim3(inter / 64, ntok), dim3(64), 0, st, gu, inter, q, s, sums,
-                           tiles);
+        hipLaunchKernelGGL(swiglu_act_kernel<false>, grid, dim3(64), 0, st, gu, inter, q, s, sums, tiles, signs);
     hip_check(hipGetLastError(), "swiglu_act launch");
 }
 

@@ -365,7 +365,7 @@ static void launch_moe_ffn_exact(k2t_ctx *ctx, const MoeLayer &L, float *hidden,
             hip_check(hipGetLastError(), "moe shared gate launch");
         }
         launch_gemv_ex(ctx, L.sh_gu, ws.aq, ws.as, ws.asum, 1, sh_gu, (size_t)L.sh_gu->rows, false, 1);
-        launch_swiglu_act(st, sh_gu, inter, 1, s_q, s_s, s_sum, true);
+        launch_swiglu_act(st, ctx->signs, sh_gu, inter, 1, s_q, s_s, s_sum, true);
         launch_gemv_ex(ctx, L.sh_dn, s_q, s_s, s_sum, 1, sh_out, (size_t)d, false);
     }
     hipLaunchKernelGGL(moe_route_exact_kernel, dim3(1), dim3(256), 0, st, hidden, post_norm, ws.rms, d, L.router_w,
@@ -387,7 +387,7 @@ static void launch_moe_ffn_exact(k2t_ctx *ctx, const MoeLayer &L, float *hidden,
     g.xsum = ws.asum;
     g.slot_act = 0;
     launch_gemv_grouped(ctx, &b->gu, g, 0, nullptr, nullptr, 0.0f, ws.gu);
-    launch_swiglu_act(st, ws.gu, dff, L.top_k, ws.mq, ws.ms, ws.msum, true);
+    launch_swiglu_act(st, ctx->signs, ws.gu, dff, L.top_k, ws.mq, ws.ms, ws.msum, true);
     g.mat_off = (uint32_t)b->lay.dn_pair_off;
     g.cb_off = (uint32_t)b->lay.dn_cb_off;
     g.slot_out = (size_t)d;
