@@ -734,6 +734,12 @@ constexpr int kGqaMaxGroup = 8;
 #define K2T_GQA_HEADS 8
 #endif
 constexpr int kGqaHeads = K2T_GQA_HEADS;
+// Scores and o sums on the matrix cores (needs one 16-position tile per wave: 128-position
+// spans, 8 waves); 0 in a measurement build keeps the dot-product form.
+#ifndef K2T_GQA_MFMA
+#define K2T_GQA_MFMA 1
+#endif
+constexpr bool kGqaMfma = K2T_GQA_MFMA != 0 && kGqaSpan == 16 * (kGqaThreads / 64);
 
 #ifdef K2T_GQA_TRACE
 // Measurement builds only: wall-clock stamps of layer 0's workgroups, 8 per (KV head, row).
@@ -773,7 +779,8 @@ struct GqaArgs {
 
 // SH: q heads per span workgroup (the group's G heads are split over ceil(G / SH) span
 // workgroups of each span, which read the same K / V tile).
-template <int HD, int SH>
+// MF: steps 3-5 on the matrix cores (see below).
+template <int HD, int SH, bool MF>
 __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
     constexpr int P = kGqaSpan, NTH = kGqaThreads, GM = SH;
     constexpr int PW = P / 64, HW = NTH / 64 / PW;  // waves per 64 positions, heads per pass
@@ -786,7 +793,7 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
     __shared__ __align__(16) int8_t qi[GM * 128];
     __shared__ float qas[GM];
     __shared__ __align__(16) float sc[P * GM];  // exp(s_t - m) * vs_t per (position, head)
-    __shared__ float red_m[GM][PW], red_l[GM][PW];
+    __shared__ float red_m[GM][MF ? NTH / 64 : PW], red_l[GM][MF ? NTH / 64 : PW];
     __shared__ __align__(16) int8_t kcur[128], vcur[128];
     __shared__ float cur_s[2];
     const int layer = A.layer, nq = A.nq, nkv = A.nkv;
@@ -1039,6 +1046,98 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
         __syncthreads();
     }
     GQA_TR(3);
+    if constexpr (MF) {
+        // 3-5 on the matrix cores (the layout of attn_prefill_mfma_kernel with the group's q
+        // heads in place of its tokens).  Wave w takes positions 16w .. 16w + 15 of the span:
+        //  - scores: v_mfma_i32_16x16x64_i8 with A = K (lane l: position 16w + l%16) and
+        //    B = the int8 q heads (lane l: head l%16; heads past the part are zero): exact
+        //    integer dots, lane l holding positions 16w + 4(l/16) + r of head l%16;
+        //    s = (float(dot) * ks) * qas as before;
+        //  - the span's maximum and sum per head: each wave's over its positions, then the
+        //    waves' in wave order;
+        //  - o^T += V^T (p vs)^T: four v_mfma_f32_16x16x4f32 per 16 dims, the r-th over the
+        //    wave's positions 4g + r (g = 0..3), whose weights are the score tile's own
+        //    registers; the waves' partial o are added in wave order.
+        static_assert(P == 16 * (NTH / 64), "one 16-position tile per wave");
+        constexpr int NW = NTH / 64, DB = HD / 16;
+        const uint32_t li = lane & 15u, lg = lane >> 4;
+        const int pw0 = 16 * (int)wv;
+        const bool hl = (int)li < GL;
+        v4i_t acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < nb; k++) {
+            const int4 kv = *reinterpret_cast<const int4 *>(kt + (pw0 + (int)li) * HD + 64 * k + 16 * (int)lg);
+            const int4 qv = hl ? *reinterpret_cast<const int4 *>(qi + li * 128 + 64 * k + 16 * lg) : make_int4(0, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i_t{kv.x, kv.y, kv.z, kv.w}, v4i_t{qv.x, qv.y, qv.z, qv.w}, acc,
+                                                         0, 0, 0);
+        }
+        const float qs = hl ? qas[li] : 0.0f;
+        const int pr = pw0 + 4 * (int)lg;  // this lane's first position
+        float sc4[4];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            sc4[r] = hl && pr + r < n ? ((float)acc[r] * kst[pr + r]) * qs : -INFINITY;
+            tmax = fmaxf(tmax, sc4[r]);
+        }
+        tmax = fmaxf(tmax, xor_lane(tmax, 16));
+        tmax = fmaxf(tmax, xor_lane(tmax, 32));
+        if (lg == 0 && hl) red_m[li][wv] = tmax;
+        __syncthreads();
+        float m = -INFINITY;
+        if (hl) {
+            m = red_m[li][0];
+#pragma unroll
+            for (int u = 1; u < NW; u++) m = fmaxf(m, red_m[li][u]);
+        }
+        float psum = 0.0f, w[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float pe = sc4[r] == -INFINITY ? 0.0f : expf(sc4[r] - m);
+            psum += pe;
+            w[r] = pe * vst[pr + r];
+        }
+        psum += xor_lane(psum, 16);
+        psum += xor_lane(psum, 32);
+        if (lg == 0 && hl) red_l[li][wv] = psum;
+        v4f o[DB];
+#pragma unroll
+        for (int b = 0; b < DB; b++) {
+            o[b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float a = (float)vt[(pr + r) * HD + 16 * b + (int)li];
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, w[r], o[b], 0, 0, 0);
+            }
+        }
+        // the waves' partial o [wave][head][dim] after the K / V tiles (still being read)
+        float *opw = reinterpret_cast<float *>(tiles + 2 * P * 128);
+        if (hl) {
+#pragma unroll
+            for (int b = 0; b < DB; b++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) opw[((int)wv * GM + (int)li) * HD + 16 * b + 4 * (int)lg + r] = o[b][r];
+        }
+        __syncthreads();
+        unsigned long long *pbase =
+            A.words + (size_t)(tok * nq + kvh * G + h0) * pstride + (size_t)span * (2 + hd);
+        for (int i = (int)tid; i < GL * hd; i += NTH) {
+            const int h = i / hd, c = i % hd;
+            float ov = opw[h * HD + c];
+            for (int u = 1; u < NW; u++) ov += opw[(u * GM + h) * HD + c];
+            unsigned long long *pp = pbase + (size_t)h * pstride;
+            ll_word_store(pp + 2 + c, __float_as_uint(ov), ep);
+            if (c == 0) {
+                float mm = red_m[h][0], l = red_l[h][0];
+                for (int u = 1; u < NW; u++) {
+                    mm = fmaxf(mm, red_m[h][u]);
+                    l += red_l[h][u];
+                }
+                ll_word_store(pp, __float_as_uint(mm), ep);
+                ll_word_store(pp + 1, __float_as_uint(l), ep);
+            }
+        }
+    } else {
     // 3. scores: wave w takes position (w & 1) * 64 + lane for heads w / 2 and w / 2 + 4;
     //    lane p reads its K row's 16-byte pieces starting at piece p (no bank conflicts)
     const int p = (int)(wv % PW) * 64 + (int)lane;
@@ -1154,6 +1253,7 @@ __global__ __launch_bounds__(kGqaThreads) void attn_gqa_kernel(GqaArgs A) {
             ll_word_store(pp + 1, __float_as_uint(l), ep);
         }
     }
+    }
     GQA_TR(5);
 }
 
@@ -1231,9 +1331,9 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
                   gqa.cnt,    gqa.err,           1u << 20, out_f, aq, as, asum};
         const dim3 grid(nkv, group + A.nspan * hsplit, ntok);
         if (hd == 128)
-            hipLaunchKernelGGL((attn_gqa_kernel<128, kGqaHeads>), grid, dim3(kGqaThreads), 0, st, A);
+            hipLaunchKernelGGL((attn_gqa_kernel<128, kGqaHeads, kGqaMfma>), grid, dim3(kGqaThreads), 0, st, A);
         else
-            hipLaunchKernelGGL((attn_gqa_kernel<64, kGqaHeads>), grid, dim3(kGqaThreads), 0, st, A);
+            hipLaunchKernelGGL((attn_gqa_kernel<64, kGqaHeads, kGqaMfma>), grid, dim3(kGqaThreads), 0, st, A);
         hip_check(hipGetLastError(), "attn_gqa launch");
         return;
     }
