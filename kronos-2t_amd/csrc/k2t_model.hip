@@ -467,7 +467,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
     __shared__ __align__(16) int8_t qi[16][HD];
     __shared__ float qas_s[16];
     __shared__ float wm[4][16], wl[4][16];  // per wave and token: running max and sum
-    __shared__ float wo[4][16][HD + 1];     // per wave: o[token][dim] (padded rows)
+    __shared__ __align__(16) float wo[4][16][HD + 4];  // per wave: o[token][dim] (padded rows)
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int head = blockIdx.x, tb = blockIdx.y, t0 = tb * 16;
@@ -548,16 +548,29 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
         psum += xor_lane(psum, 32);
         l = l * corr + psum;
         m = mn;
-        // o^T += V^T * (p vs)^T: A lane l = dim 16 b + li, position pr + r
+        // o^T += V^T * (p vs)^T: dim block b holds dims DB m + b (m = 0..15), so A lane l =
+        // dim DB li + b, position pr + r, and the lane's DB dims of a position are one load
+        float va[4][DB];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int pc = min(pr + r, n_att - 1);
+            const int8_t *vrow = vq + (base + pc) * HD + DB * li;
+            uint32_t vw[DB / 4];
+            if constexpr (DB == 8) {
+                const uint2 d2 = *reinterpret_cast<const uint2 *>(vrow);
+                vw[0] = d2.x;
+                vw[1] = d2.y;
+            } else {
+                vw[0] = *reinterpret_cast<const uint32_t *>(vrow);
+            }
+#pragma unroll
+            for (int b = 0; b < DB; b++) va[r][b] = (float)(int8_t)((vw[b >> 2] >> (8 * (b & 3))) & 0xFFu);
+        }
 #pragma unroll
         for (int b = 0; b < DB; b++) {
             o[b] = o[b] * corr;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int pc = min(pr + r, n_att - 1);
-                const float a = (float)vq[(base + pc) * HD + 16 * b + li];
-                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, w[r], o[b], 0, 0, 0);
-            }
+            for (int r = 0; r < 4; r++) o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[r][b], w[r], o[b], 0, 0, 0);
         }
     }
     // 2. merge the waves in order: per token the largest max, then the rescaled sums
@@ -568,11 +581,21 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
 #pragma unroll
     for (int b = 0; b < DB; b++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) wo[wave][li][16 * b + 4 * lg + r] = o[b][r];
+        for (int r = 0; r < 4; r++) wo[wave][li][DB * (4 * lg + r) + b] = o[b][r];
+    // Hadamard sign masks: ifwht64 of blocks 0 .. NB-1, and the o_proj chunks' rotations
+    uint64_t mi[NB], mc[NB];
+#pragma unroll
+    for (int blk = 0; blk < NB; blk++) {
+        mi[blk] = __ballot(hadamard_sign_bit((uint64_t)blk, lane) != 0u);
+        mc[blk] = __ballot(hadamard_sign_bit((uint64_t)(head * NB + blk), lane) != 0u);
+    }
     __syncthreads();
-    for (int j = (int)wave; j < 16; j += 4) {
-        const int tok = t0 + j;
-        if (tok >= ntok) break;  // wave-uniform
+    // Four tokens per wave: lanes 16k .. 16k + 15 hold token 4w + k, four consecutive
+    // elements each (butterflies_slice4 / rotate_quant4: the one-element-per-lane
+    // ifwht_lane, fwht_lane and quant_chunk_store arithmetic in that layout).
+    {
+        const uint32_t sl = lane & 15u;
+        const int j = 4 * (int)wave + (int)lg, tok = t0 + j;
         float M = -INFINITY;
 #pragma unroll
         for (int w2 = 0; w2 < 4; w2++) M = fmaxf(M, wm[w2][j]);
@@ -583,18 +606,31 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
             L = fmaf(wl[w2][j], e[w2], L);
         }
         const float inv = 1.0f / L;
+        const bool live = tok < ntok;
+        const size_t hbase = (size_t)tok * nq * HD + (size_t)head * HD;
 #pragma unroll
         for (int blk = 0; blk < NB; blk++) {
-            float acc_o = 0.0f;
+            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int w2 = 0; w2 < 4; w2++) acc_o = fmaf(wo[w2][j][64 * blk + lane], e[w2], acc_o);
-            const float ov = ifwht_lane(acc_o * inv, (uint64_t)blk, lane);
-            const size_t hbase = (size_t)tok * nq * HD + (size_t)head * HD;
-            if (out_f) out_f[hbase + 64 * blk + lane] = ov;
+            for (int w2 = 0; w2 < 4; w2++) {
+                const float4 wq = *reinterpret_cast<const float4 *>(&wo[w2][j][64 * blk + 4 * sl]);
+                v[0] = fmaf(wq.x, e[w2], v[0]);
+                v[1] = fmaf(wq.y, e[w2], v[1]);
+                v[2] = fmaf(wq.z, e[w2], v[2]);
+                v[3] = fmaf(wq.w, e[w2], v[3]);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) v[jj] = v[jj] * inv;
+            butterflies_slice4(v, sl);
+            const uint32_t sb = (uint32_t)(mi[blk] >> (4u * sl)) & 0xFu;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) v[jj] = flip_sign(v[jj] * 0.125f, (sb >> jj) & 1u);
+            if (out_f && live)
+                *reinterpret_cast<float4 *>(out_f + hbase + 64 * blk + 4 * sl) = make_float4(v[0], v[1], v[2], v[3]);
             if (aq) {
-                const size_t c = (size_t)head * NB + blk, g = (size_t)tok * nq * NB + c;
-                quant_chunk_store(fwht_lane(ov, c, lane), lane, aq + g * 64, as + g, asum + g, tiles.xt, tiles.st,
-                                  tiles.ut, tok, (int)c, nq * NB);
+                const int c = head * NB + blk;
+                const Chunk4 r = rotate_quant4(v, mc[blk], sl);
+                if (live) chunk4_store(r, sl, tok, c, nq * NB, aq, as, asum, tiles.xt, tiles.st, tiles.ut);
             }
         }
     }
