@@ -314,7 +314,7 @@ __global__ __launch_bounds__(SW ? 512 : 256) void gemm_mfma_kernel(MfArgs A) {
     for (int i = 0; i < P - 1; i++)
         if (c0 + i < nc) mf_step<FMT, HP, NB, SH>(A, ring[i], acc, bsh[(c0 + i) & 1], wave, lane);
     if constexpr (QP) {
-        __shared__ float eq[16 * NB][65];  // [token][row of the head]
+        __shared__ __align__(16) float eq[16 * NB][68];  // [token][row of the head] (padded rows)
 #pragma unroll
         for (int b = 0; b < NB; b++)
 #pragma unroll
@@ -322,6 +322,36 @@ __global__ __launch_bounds__(SW ? 512 : 256) void gemm_mfma_kernel(MfArgs A) {
         __syncthreads();
         const QkvPostDev &Q = A.qp;
         const int head = (int)blockIdx.x, pos0 = Q.pos_dev[0];
+        if (Q.kr.bits == 8) {
+            // Four tokens per wave pass: lanes 16k .. 16k + 15 hold token 4 (pass * W + w) + k,
+            // four consecutive elements each (head_post4; the K / V rotation and int8 by
+            // rotate_quant4 with block 0's signs: fwht_lane + kv_store_head's int8 branch).
+            const uint32_t sl = lane & 15u;
+            const uint64_t m0 = __ballot(hadamard_sign_bit(0, lane) != 0u);
+            for (int tl0 = 4 * (int)wave; tl0 < 16 * NB; tl0 += 4 * W) {
+                if (tokb + tl0 >= A.ntok) break;  // wave-uniform
+                const int t = tokb + tl0 + (int)lg;
+                const bool live = t < A.ntok;
+                const float4 e4 = *reinterpret_cast<const float4 *>(&eq[tl0 + (int)lg][4 * sl]);
+                float v[4] = {e4.x, e4.y, e4.z, e4.w};
+                head_post4(head, Q.nq, Q.nkv, Q.bias, Q.qn, Q.kn, Q.eps, Q.rope, pos0 + min(t, A.ntok - 1), sl, v);
+                if (head < Q.nq) {
+                    if (live)
+                        *reinterpret_cast<float4 *>(A.out + (size_t)t * A.out_stride + (size_t)head * 64 + 4 * sl) =
+                            make_float4(v[0], v[1], v[2], v[3]);
+                    continue;
+                }
+                const Chunk4 r = rotate_quant4(v, m0, sl);
+                if (live) {
+                    const bool is_k = head < Q.nq + Q.nkv;
+                    const int kvh = is_k ? head - Q.nq : head - Q.nq - Q.nkv;
+                    const size_t slot = ((size_t)Q.layer * Q.nkv + kvh) * Q.kr.cap + ring_slot(Q.kr, pos0 + t);
+                    *reinterpret_cast<uint32_t *>((is_k ? Q.kq : Q.vq) + slot * 64 + 4 * sl) = r.w;
+                    if (sl == 0) (is_k ? Q.ks : Q.vs)[slot] = r.scale;
+                }
+            }
+            return;
+        }
         for (int tl = (int)wave; tl < 16 * NB; tl += W) {
             const int t = tokb + tl;
             if (t >= A.ntok) break;  // wave-uniform

@@ -163,6 +163,50 @@ __device__ __forceinline__ void head_post_vals(int head, int nq, int nkv, int hd
     }
 }
 
+// head_post_vals at head size 64 (fast path) with sixteen lanes per head, lane slice sl
+// holding elements 4 sl .. 4 sl + 3: the same operations on the same operands.  The
+// q / k RMSNorm's sum of squares follows wave_sum_f's pairs (elements i, i ^ 1 and i ^ 2 in
+// registers, i ^ 4 .. i ^ 16 by slice exchanges ^1 .. ^4, the halves by ^8; IEEE addition
+// commutes, so the bits are the same), RoPE's partner i ^ 32 is slice sl ^ 8.
+__device__ __forceinline__ void head_post4(int head, int nq, int nkv, const float *__restrict__ bias,
+                                           const float *__restrict__ qn, const float *__restrict__ kn, float eps,
+                                           const float *__restrict__ rope, int pos, uint32_t sl, float (&v)[4]) {
+    if (bias) {
+        const float4 b4 = *reinterpret_cast<const float4 *>(bias + head * 64 + 4 * sl);
+        v[0] = v[0] + b4.x;
+        v[1] = v[1] + b4.y;
+        v[2] = v[2] + b4.z;
+        v[3] = v[3] + b4.w;
+    }
+    const float *hn = head < nq ? qn : (head < nq + nkv ? kn : nullptr);
+    if (hn) {
+        float ss = (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+        ss += xchg1(ss);
+        ss += xchg2(ss);
+        ss += xchg4(ss);
+        ss += xchg8(ss);
+        const float inv_rms = 1.0f / sqrtf(ss * (1.0f / 64.0f) + eps);
+        const float4 w4 = *reinterpret_cast<const float4 *>(hn + 4 * sl);
+        v[0] = (v[0] * inv_rms) * w4.x;
+        v[1] = (v[1] * inv_rms) * w4.y;
+        v[2] = (v[2] * inv_rms) * w4.z;
+        v[3] = (v[3] * inv_rms) * w4.w;
+    }
+    if (head < nq + nkv) {
+        const float *row = rope + (size_t)pos * 64;
+        const uint32_t i0 = (4u * sl) & 31u;  // element index mod 32 of v[0]
+        const float4 c4 = *reinterpret_cast<const float4 *>(row + i0);
+        const float4 s4 = *reinterpret_cast<const float4 *>(row + 32 + i0);
+        const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+        float other[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) other[j] = xchg8(v[j]);
+        const bool lower = sl < 8u;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = lower ? v[j] * cs[j] - other[j] * sn[j] : v[j] * cs[j] + other[j] * sn[j];
+    }
+}
+
 __device__ __forceinline__ void head_post(const float *__restrict__ h, int head, int nq, int nkv, int hd,
                                           const float *__restrict__ bias, const float *__restrict__ qn,
                                           const float *__restrict__ kn, float eps, const float *__restrict__ rope,
