@@ -1,4 +1,4 @@
-"""Parity at the BASELINE configurations' own shapes (configs 2-5), through the C ABI,
+"""Parity at the benchmark configurations' own shapes (configs 2-5 of BASELINE.json), through the C ABI,
 against the oracle on the same seeded inputs.
 
 - config 4: nf4g128 / nf3g128 / b6 GEMVs at 14336x4096 and 4096x14336, batch 1 and 4,
