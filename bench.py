@@ -158,7 +158,9 @@ def decode_bench(ctx, torch, name, cfg, fmt, prefill, steps, warmup, log, planes
     wbytes = sum(m.info()[3] for m in mats)
     rng = np.random.default_rng(SEED)
     toks = rng.integers(0, cfg["vocab"], prefill).astype(np.int32)
-    model.prefill(toks[:32], want_logits=False)  # warm the prefill kernels
+    # Warm-up: the same prefill once, untimed (the first launch of each kernel variant a
+    # batch of this size uses loads its code object), then back to position 0.
+    model.prefill(toks, want_logits=True)
     model.reset()
     model.sync()
     t0 = time.perf_counter()
