@@ -317,6 +317,39 @@ def test_config3_exact_order(gpu_ctx, n_layers):
             m.close()
 
 
+def test_config3_prefill_256_matrix_cores(gpu_ctx):
+    """The bench's 256-token prefill at the 1.7B nf4g128 shape (2 layers): qkv with the
+    q / k / v epilogue (two 16-token blocks per wave), gate_up with the SwiGLU epilogue
+    (64-token workgroups), o and down at one block per wave, attention on the matrix cores.
+    The last token's logits meet the two-layer fast bar against the oracle, and with the
+    tiles copied by the GEMVs (mode 2: the separate q / k / v post and SwiGLU kernels) the
+    logits are the same bit for bit."""
+    print("config 3: 1.7B nf4g128 256-token matrix-core prefill vs oracle, 2 layers", flush=True)
+    cfg = dict(k2t.SMOLLM2_1_7B, n_layers=2)
+    n = 256
+    model, mats, host = k2t.build_random_model(gpu_ctx, cfg, max_seq=n + 8, fmt="nf4", seed=7, max_batch=n,
+                                               keep_host=True)
+    try:
+        toks = np.random.default_rng(SEED).integers(0, cfg["vocab"], n).astype(np.int32)
+        pre = {}
+        for mode in (1, 2):
+            gpu_ctx.set_mfma(mode)
+            model.reset()
+            pre[mode] = model.prefill(toks, want_logits=True)
+        assert np.array_equal(pre[1].view(np.uint32), pre[2].view(np.uint32)), "mode 1 / mode 2"
+        ref = _oracles(cfg, host, n + 8, THREADS)[0]
+        for t in toks[:-1]:
+            ref.forward_token(int(t), want_logits=False)
+        b = ref.forward_token(int(toks[-1]))
+        ok, info = _close(pre[1], b, FAST_COS_2L)
+        assert ok, f"prefill logits {info}"
+    finally:
+        gpu_ctx.set_mfma(1)
+        model.close()
+        for m in mats:
+            m.close()
+
+
 @pytest.mark.parametrize("tier,n_layers", [("p55454", 2), ("p55454", 30), ("b6", 2)])
 def test_config2_exact_order(gpu_ctx, tier, n_layers):
     """The 135M bench model at context 512 (synthetic K/V 448 + a 64-token batched
