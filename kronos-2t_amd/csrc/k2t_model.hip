@@ -511,25 +511,50 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
     v4f o[DB];
 #pragma unroll
     for (int b = 0; b < DB; b++) o[b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int p0 = 16 * (int)wave; p0 < n_att; p0 += 64) {
-        // scores of positions p0 + 4 lg + r for token li
-        v4i_t acc = {0, 0, 0, 0};
+    // A tile's loads (K rows, scales, V words; rows past n_att re-read the last one) are
+    // issued a tile ahead: two register sets alternate, so the next tile's loads are in
+    // flight while this one computes.
+    struct Tile {
+        int4 kv[NB];
+        float ksc[4], vsc[4];
+        uint32_t vw[4][DB / 4];
+    };
+    auto load_tile = [&](int p0, Tile &T) {
         const int prow = min(p0 + (int)li, n_att - 1);  // K row of this lane (A operand)
 #pragma unroll
-        for (int k = 0; k < NB; k++) {
-            const int4 kv = *reinterpret_cast<const int4 *>(kq + (base + prow) * HD + 64 * k + 16 * lg);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i_t{kv.x, kv.y, kv.z, kv.w}, qb[k], acc, 0, 0, 0);
+        for (int k = 0; k < NB; k++)
+            T.kv[k] = *reinterpret_cast<const int4 *>(kq + (base + prow) * HD + 64 * k + 16 * lg);
+        const int pr = p0 + 4 * (int)lg;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int pc = min(pr + r, n_att - 1);
+            T.ksc[r] = ks[base + pc];
+            T.vsc[r] = vs[base + pc];
+            const int8_t *vrow = vq + (base + pc) * HD + DB * li;
+            if constexpr (DB == 8) {
+                const uint2 d2 = *reinterpret_cast<const uint2 *>(vrow);
+                T.vw[r][0] = d2.x;
+                T.vw[r][DB / 4 - 1] = d2.y;
+            } else {
+                T.vw[r][0] = *reinterpret_cast<const uint32_t *>(vrow);
+            }
         }
+    };
+    auto tile_step = [&](int p0, const Tile &T) {
+        // scores of positions p0 + 4 lg + r for token li
+        v4i_t acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < NB; k++)
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i_t{T.kv[k].x, T.kv[k].y, T.kv[k].z, T.kv[k].w}, qb[k], acc,
+                                                         0, 0, 0);
         const int pr = p0 + 4 * (int)lg;  // this lane's first position
-        float sc[4], vsc[4];
+        float sc[4];
         float tmax = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int p = pr + r;
             const bool live = p <= my_last && p < n_att;
-            const int pc = min(p, n_att - 1);
-            sc[r] = live ? ((float)acc[r] * ks[base + pc]) * qas : -INFINITY;
-            vsc[r] = vs[base + pc];
+            sc[r] = live ? ((float)acc[r] * T.ksc[r]) * qas : -INFINITY;
             tmax = fmaxf(tmax, sc[r]);
         }
         tmax = fmaxf(tmax, xor_lane(tmax, 16));
@@ -542,7 +567,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
         for (int r = 0; r < 4; r++) {
             const float pw = sc[r] == -INFINITY ? 0.0f : expf(sc[r] - mn);
             psum += pw;
-            w[r] = pw * vsc[r];
+            w[r] = pw * T.vsc[r];
         }
         psum += xor_lane(psum, 16);
         psum += xor_lane(psum, 32);
@@ -550,28 +575,25 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
         m = mn;
         // o^T += V^T * (p vs)^T: dim block b holds dims DB m + b (m = 0..15), so A lane l =
         // dim DB li + b, position pr + r, and the lane's DB dims of a position are one load
-        float va[4][DB];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int pc = min(pr + r, n_att - 1);
-            const int8_t *vrow = vq + (base + pc) * HD + DB * li;
-            uint32_t vw[DB / 4];
-            if constexpr (DB == 8) {
-                const uint2 d2 = *reinterpret_cast<const uint2 *>(vrow);
-                vw[0] = d2.x;
-                vw[1] = d2.y;
-            } else {
-                vw[0] = *reinterpret_cast<const uint32_t *>(vrow);
-            }
-#pragma unroll
-            for (int b = 0; b < DB; b++) va[r][b] = (float)(int8_t)((vw[b >> 2] >> (8 * (b & 3))) & 0xFFu);
-        }
 #pragma unroll
         for (int b = 0; b < DB; b++) {
             o[b] = o[b] * corr;
 #pragma unroll
-            for (int r = 0; r < 4; r++) o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[r][b], w[r], o[b], 0, 0, 0);
+            for (int r = 0; r < 4; r++) {
+                const float va = (float)(int8_t)((T.vw[r][b >> 2] >> (8 * (b & 3))) & 0xFFu);
+                o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, w[r], o[b], 0, 0, 0);
+            }
         }
+    };
+    Tile tile_a, tile_b;
+    int p0 = 16 * (int)wave;
+    load_tile(p0, tile_a);
+    for (; p0 < n_att; p0 += 128) {
+        load_tile(p0 + 64, tile_b);
+        tile_step(p0, tile_a);
+        if (p0 + 64 >= n_att) break;
+        load_tile(p0 + 128, tile_a);
+        tile_step(p0 + 64, tile_b);
     }
     // 2. merge the waves in order: per token the largest max, then the rescaled sums
     if (lg == 0) {
