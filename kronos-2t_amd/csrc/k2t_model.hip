@@ -451,8 +451,13 @@ __global__ __launch_bounds__(NTH) void attn_partial_kernel(const float *__restri
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
+#ifndef K2T_PATT_WAVES
+#define K2T_PATT_WAVES 4
+#endif
+constexpr int kPattWaves = K2T_PATT_WAVES;  // waves per (q head, 16-token block) workgroup
+
 template <int HD>
-__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__restrict__ q, int q_stride,
+__global__ __launch_bounds__(64 * kPattWaves) void attn_prefill_mfma_kernel(const float *__restrict__ q, int q_stride,
                                                                 const int8_t *__restrict__ kq,
                                                                 const int8_t *__restrict__ vq,
                                                                 const float *__restrict__ ks,
@@ -466,8 +471,9 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
     constexpr int DB = HD / 16;  // 16-dim output blocks
     __shared__ __align__(16) int8_t qi[16][HD];
     __shared__ float qas_s[16];
-    __shared__ float wm[4][16], wl[4][16];  // per wave and token: running max and sum
-    __shared__ __align__(16) float wo[4][16][HD + 4];  // per wave: o[token][dim] (padded rows)
+    constexpr int AW = kPattWaves;
+    __shared__ float wm[AW][16], wl[AW][16];  // per wave and token: running max and sum
+    __shared__ __align__(16) float wo[AW][16][HD + 4];  // per wave: o[token][dim] (padded rows)
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int head = blockIdx.x, tb = blockIdx.y, t0 = tb * 16;
@@ -475,7 +481,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
     const int pos0 = pos_dev[0];
     // 1. the block's q heads rotated and quantized (as the whole-context kernel): wave w
     //    takes tokens w, w + 4, w + 8, w + 12 (tokens past the batch repeat the last one)
-    for (int j = (int)wave; j < 16; j += 4) {
+    for (int j = (int)wave; j < 16; j += AW) {
         const int tok = min(t0 + j, ntok - 1);
         const float *qh = q + (size_t)tok * q_stride + (size_t)head * HD;
         const float r0 = fwht_lane(qh[lane], 0, lane);
@@ -586,14 +592,15 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
         }
     };
     Tile tile_a, tile_b;
+    constexpr int TS = 16 * AW;  // a wave's tile stride
     int p0 = 16 * (int)wave;
     load_tile(p0, tile_a);
-    for (; p0 < n_att; p0 += 128) {
-        load_tile(p0 + 64, tile_b);
+    for (; p0 < n_att; p0 += 2 * TS) {
+        load_tile(p0 + TS, tile_b);
         tile_step(p0, tile_a);
-        if (p0 + 64 >= n_att) break;
-        load_tile(p0 + 128, tile_a);
-        tile_step(p0 + 64, tile_b);
+        if (p0 + TS >= n_att) break;
+        load_tile(p0 + 2 * TS, tile_a);
+        tile_step(p0 + TS, tile_b);
     }
     // 2. merge the waves in order: per token the largest max, then the rescaled sums
     if (lg == 0) {
@@ -612,18 +619,19 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
         mc[blk] = __ballot(hadamard_sign_bit((uint64_t)(head * NB + blk), lane) != 0u);
     }
     __syncthreads();
-    // Four tokens per wave: lanes 16k .. 16k + 15 hold token 4w + k, four consecutive
-    // elements each (butterflies_slice4 / rotate_quant4: the one-element-per-lane
-    // ifwht_lane, fwht_lane and quant_chunk_store arithmetic in that layout).
-    {
+    // Four tokens per wave (the first four waves): lanes 16k .. 16k + 15 hold token 4w + k,
+    // four consecutive elements each (butterflies_slice4 / rotate_quant4: the
+    // one-element-per-lane ifwht_lane, fwht_lane and quant_chunk_store arithmetic in that
+    // layout).
+    if (wave < 4) {
         const uint32_t sl = lane & 15u;
         const int j = 4 * (int)wave + (int)lg, tok = t0 + j;
         float M = -INFINITY;
 #pragma unroll
-        for (int w2 = 0; w2 < 4; w2++) M = fmaxf(M, wm[w2][j]);
-        float L = 0.0f, e[4];
+        for (int w2 = 0; w2 < AW; w2++) M = fmaxf(M, wm[w2][j]);
+        float L = 0.0f, e[AW];
 #pragma unroll
-        for (int w2 = 0; w2 < 4; w2++) {
+        for (int w2 = 0; w2 < AW; w2++) {
             e[w2] = wm[w2][j] == -INFINITY ? 0.0f : expf(wm[w2][j] - M);
             L = fmaf(wl[w2][j], e[w2], L);
         }
@@ -634,7 +642,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const float *__r
         for (int blk = 0; blk < NB; blk++) {
             float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int w2 = 0; w2 < 4; w2++) {
+            for (int w2 = 0; w2 < AW; w2++) {
                 const float4 wq = *reinterpret_cast<const float4 *>(&wo[w2][j][64 * blk + 4 * sl]);
                 v[0] = fmaf(wq.x, e[w2], v[0]);
                 v[1] = fmaf(wq.y, e[w2], v[1]);
@@ -1355,10 +1363,10 @@ void launch_attention(hipStream_t st, const float *q, int q_stride, int8_t *kq, 
     if (mfma && ntok >= 16 && !post.on && kr.bits == 8 && kr.window == 0 && kr.ring == 0 && (hd == 64 || hd == 128)) {
         const dim3 grid(nq, (ntok + 15) / 16);
         if (hd == 128)
-            hipLaunchKernelGGL(attn_prefill_mfma_kernel<128>, grid, dim3(256), 0, st, q, q_stride, kq, vq, ks, vs,
+            hipLaunchKernelGGL(attn_prefill_mfma_kernel<128>, grid, dim3(64 * kPattWaves), 0, st, q, q_stride, kq, vq, ks, vs,
                                pos_dev, layer, nq, nkv, kr.cap, attn_scale, ntok, out_f, aq, as, asum, tiles);
         else
-            hipLaunchKernelGGL(attn_prefill_mfma_kernel<64>, grid, dim3(256), 0, st, q, q_stride, kq, vq, ks, vs,
+            hipLaunchKernelGGL(attn_prefill_mfma_kernel<64>, grid, dim3(64 * kPattWaves), 0, st, q, q_stride, kq, vq, ks, vs,
                                pos_dev, layer, nq, nkv, kr.cap, attn_scale, ntok, out_f, aq, as, asum, tiles);
         hip_check(hipGetLastError(), "prefill attention launch");
         return;
