@@ -306,8 +306,13 @@ extern "C" int k2t_gemv_trace_read(unsigned long long *dst) {
     } while (0)
 #endif
 
+// The two-hi-plane kernel with the fused RMSNorm builder needs more registers than a
+// 1024-thread workgroup leaves a lane; its launches are held to kB6NormThreads threads.
+constexpr int kB6NormThreads = 512;
+
 template <int FMT, int HP, int NT, bool DOTS, int XS>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvParams P) {
+__global__ __launch_bounds__(FMT == 0 && HP == 2 && XS == K2T_XS_RMSNORM ? kB6NormThreads : 1024) void gemv_kernel(
+    GemvParams P) {
     constexpr int NH = HP == 0 ? 1 : (HP == 1 ? 2 : 4);
     constexpr bool kNF3 = FMT >= 2, kLane = FMT == 3;  // NF3; FMT 3: stripe-chunks in lane order
     extern __shared__ float lds[];
@@ -959,6 +964,11 @@ static void launch_gemv_impl(k2t_ctx *ctx, const k2t_mat *m, const int8_t *xq, c
     const int saved = ctx->max_segments;
     if (dots) ctx->max_segments = 1;
     GemvPlan plan = plan_gemv(ctx, m, s0, s1);
+    if (xsm == K2T_XS_RMSNORM && m->fmt == K2T_FMT_NIBBLE4 && m->hp == 2 && 64 * plan.nseg > kB6NormThreads) {
+        constexpr int kSeg = kB6NormThreads / 64;
+        plan.cps = (m->nc + kSeg - 1) / kSeg;
+        plan.nseg = (m->nc + plan.cps - 1) / plan.cps;
+    }
     ctx->max_segments = saved;
     if (plan.rb_hi <= plan.rb_lo || ntok <= 0) return;
     GemvParams P{};
